@@ -1,0 +1,322 @@
+"""Python host side of the gfx950 camera-path library.
+
+Thin ctypes mirror of the C ABI in ``include/bf_cuda_ops.h``,
+``include/bf_cuda_swin.h`` and ``include/bf_cuda_camera.h`` (the reference's
+operator/plugin interface for this path).  PyTorch supplies device memory and
+the current HIP stream; every computation runs in ``lib/libbfhip.so``.  There
+is no fallback: if the library is missing, importing an entry point raises.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import pathlib
+
+PKG = pathlib.Path(__file__).resolve().parent.parent
+LIB_DIR = PKG / "lib"
+HIP_LIB = LIB_DIR / "libbfhip.so"
+MODEL_LIB = LIB_DIR / "libbfmodel.so"
+
+_vp, _sz, _i = C.c_void_p, C.c_size_t, C.c_int
+
+
+class BfHipError(RuntimeError):
+    pass
+
+
+class ConvDesc(C.Structure):
+    """``bf_cuda_conv2d_desc`` (include/bf_cuda_ops.h)."""
+    _fields_ = [(n, C.c_int) for n in (
+        "batches", "input_channels", "output_channels", "input_height", "input_width",
+        "kernel_height", "kernel_width", "stride_height", "stride_width", "padding_height",
+        "padding_width", "output_height", "output_width", "transpose", "relu")]
+
+
+# Every symbol declared by include/*.h, with its ctypes signature.
+SIGNATURES = {
+    "bf_cuda_conv2d_f32": (_i, [C.POINTER(ConvDesc), _vp, _vp, _vp, _vp, _vp, C.c_char_p, _sz]),
+    "bf_cuda_gemm_f32": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, C.c_char_p, _sz]),
+    "bf_cuda_swin_create": (_i, [_vp, _sz, _sz, _sz, C.POINTER(_vp), C.c_char_p, _sz]),
+    "bf_cuda_swin_destroy": (None, [_vp]),
+    "bf_cuda_swin_resident_bytes": (_sz, [_vp]),
+    "bf_cuda_swin_forward": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, C.c_char_p, _sz]),
+    "bf_cuda_camera_neck_create": (_i, [_vp, _sz, _sz, _sz, _sz, _sz, C.POINTER(_vp),
+                                        C.c_char_p, _sz]),
+    "bf_cuda_camera_neck_destroy": (None, [_vp]),
+    "bf_cuda_camera_neck_resident_bytes": (_sz, [_vp]),
+    "bf_cuda_camera_fpn_forward": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, C.c_char_p, _sz]),
+    "bf_cuda_camera_depth_forward": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, C.c_char_p, _sz]),
+    "bf_cuda_camera_neck_forward": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                         C.c_char_p, _sz]),
+    "bf_cuda_camera_downsample_forward": (_i, [_vp, _vp, _vp, _vp, C.c_char_p, _sz]),
+}
+
+MODEL_SIGNATURES = {
+    "bf_model_open": (_i, [C.c_char_p, C.POINTER(_vp), C.c_char_p, _sz]),
+    "bf_model_close": (None, [_vp]),
+    "bf_model_tensor_count": (_sz, [_vp]),
+    "bf_model_file_bytes": (C.c_uint64, [_vp]),
+    "bf_model_tensor_at": (_vp, [_vp, _sz]),
+    "bf_model_find": (_vp, [_vp, C.c_char_p]),
+    "bf_model_validate_tensor": (_i, [_vp, _vp, C.c_char_p, _sz]),
+    "bf_model_validate_all": (_i, [_vp, C.c_char_p, _sz]),
+    "bf_dtype_name": (C.c_char_p, [C.c_uint32]),
+}
+
+_model_lib = None
+_hip_lib = None
+
+
+def _bind(lib, table):
+    """Attach signatures; a symbol the library lacks raises when first used."""
+    for name, (res, args) in table.items():
+        if hasattr(lib, name):
+            fn = getattr(lib, name)
+            fn.restype, fn.argtypes = res, args
+    return lib
+
+
+def missing_symbols():
+    """Entry points declared in include/*.h that libbfhip.so does not export."""
+    lib = hip_lib()
+    return [n for n in SIGNATURES if not hasattr(lib, n)]
+
+
+def model_lib():
+    global _model_lib
+    if _model_lib is None:
+        if not MODEL_LIB.exists():
+            raise BfHipError(f"{MODEL_LIB} is not built (run __graft_entry__.build())")
+        _model_lib = _bind(C.CDLL(str(MODEL_LIB), mode=C.RTLD_GLOBAL), MODEL_SIGNATURES)
+    return _model_lib
+
+
+def hip_lib():
+    """Load libbfhip.so; raises BfHipError if it is missing (no CPU fallback)."""
+    global _hip_lib
+    if _hip_lib is None:
+        model_lib()
+        if not HIP_LIB.exists():
+            raise BfHipError(f"{HIP_LIB} is not built (run __graft_entry__.build())")
+        _hip_lib = _bind(C.CDLL(str(HIP_LIB)), SIGNATURES)
+    return _hip_lib
+
+
+def _err():
+    return C.create_string_buffer(512)
+
+
+def _check(ok, err, what):
+    if not ok:
+        raise BfHipError(f"{what}: {err.value.decode(errors='replace')}")
+
+
+class Model:
+    """A BFW container opened through libbfmodel.so."""
+
+    def __init__(self, path):
+        lib = model_lib()
+        self.handle, err = _vp(), _err()
+        _check(lib.bf_model_open(str(path).encode(), C.byref(self.handle), err, 512), err,
+               f"open {path}")
+
+    def close(self):
+        if self.handle:
+            model_lib().bf_model_close(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# ---------------------------------------------------------------- torch glue
+def _torch():
+    import torch
+    return torch
+
+
+def _ptr(t):
+    if t is None:
+        return None
+    torch = _torch()
+    if not t.is_cuda or t.dtype != torch.float32 or not t.is_contiguous():
+        raise BfHipError("expected a contiguous float32 device tensor")
+    return _vp(t.data_ptr())
+
+
+def _stream(stream=None):
+    torch = _torch()
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return _vp(s.cuda_stream)
+
+
+def gemm_f32(x, w, b=None, relu=False, out=None, stream=None):
+    """out[M,N] = x[M,K] @ w[N,K]^T + b (bf_cuda_gemm_f32)."""
+    torch = _torch()
+    M, K = x.shape
+    N = w.shape[0]
+    out = out if out is not None else torch.empty((M, N), device=x.device, dtype=torch.float32)
+    err = _err()
+    _check(hip_lib().bf_cuda_gemm_f32(_ptr(x), _ptr(w), _ptr(b), _ptr(out), M, K, N, int(relu),
+                                      _stream(stream), err, 512), err, "bf_cuda_gemm_f32")
+    return out
+
+
+def conv_desc(x_shape, w_shape, stride=(1, 1), padding=(0, 0), transpose=False, relu=False,
+              out_hw=None, output_channels=None):
+    n, ci, ih, iw = x_shape
+    if transpose:
+        co = output_channels or w_shape[1]
+        kh, kw = w_shape[2], w_shape[3]
+        oh = (ih - 1) * stride[0] - 2 * padding[0] + kh
+        ow = (iw - 1) * stride[1] - 2 * padding[1] + kw
+    else:
+        co, kh, kw = w_shape[0], w_shape[2], w_shape[3]
+        oh = (ih + 2 * padding[0] - kh) // stride[0] + 1
+        ow = (iw + 2 * padding[1] - kw) // stride[1] + 1
+    if out_hw is not None:
+        oh, ow = out_hw
+    return ConvDesc(n, ci, co, ih, iw, kh, kw, stride[0], stride[1], padding[0], padding[1],
+                    oh, ow, int(transpose), int(relu))
+
+
+def conv2d_f32(x, w, b=None, stride=(1, 1), padding=(0, 0), transpose=False, relu=False,
+               out_hw=None, out=None, stream=None):
+    """NCHW convolution (bf_cuda_conv2d_f32); weights OIHW or IOHW if transpose."""
+    torch = _torch()
+    d = conv_desc(tuple(x.shape), tuple(w.shape), stride, padding, transpose, relu, out_hw)
+    shape = (d.batches, d.output_channels, d.output_height, d.output_width)
+    out = out if out is not None else torch.empty(shape, device=x.device, dtype=torch.float32)
+    err = _err()
+    _check(hip_lib().bf_cuda_conv2d_f32(C.byref(d), _ptr(x), _ptr(w), _ptr(b), _ptr(out),
+                                        _stream(stream), err, 512), err, "bf_cuda_conv2d_f32")
+    return out
+
+
+def conv2d_raw(desc, x, w, b, out, stream=None):
+    """Call bf_cuda_conv2d_f32 with an explicit descriptor; returns (ok, message)."""
+    err = _err()
+    ok = hip_lib().bf_cuda_conv2d_f32(C.byref(desc), x, w, b, out, _stream(stream), err, 512)
+    return bool(ok), err.value.decode(errors="replace")
+
+
+class Swin:
+    """bf_cuda_swin context (include/bf_cuda_swin.h)."""
+
+    def __init__(self, model: Model, batches: int, height: int, width: int):
+        self.lib = hip_lib()
+        self.batches, self.height, self.width = batches, height, width
+        self.handle, err = _vp(), _err()
+        _check(self.lib.bf_cuda_swin_create(model.handle, batches, height, width,
+                                            C.byref(self.handle), err, 512), err,
+               "bf_cuda_swin_create")
+
+    def output_shapes(self):
+        b, h, w = self.batches, self.height, self.width
+        return [(b, c, -(-h // d), -(-w // d)) for c, d in ((192, 8), (384, 16), (768, 32))]
+
+    def resident_bytes(self) -> int:
+        return self.lib.bf_cuda_swin_resident_bytes(self.handle)
+
+    def forward(self, images, outs=None, stream=None):
+        torch = _torch()
+        if outs is None:
+            outs = [torch.empty(s, device=images.device, dtype=torch.float32)
+                    for s in self.output_shapes()]
+        err = _err()
+        _check(self.lib.bf_cuda_swin_forward(self.handle, _ptr(images), *map(_ptr, outs),
+                                             _stream(stream), err, 512), err,
+               "bf_cuda_swin_forward")
+        return outs
+
+    def close(self):
+        if self.handle:
+            self.lib.bf_cuda_swin_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class CameraNeck:
+    """bf_cuda_camera_neck context (include/bf_cuda_camera.h)."""
+
+    def __init__(self, model: Model, batches: int, feature_h: int, feature_w: int,
+                 bev_h: int, bev_w: int):
+        self.lib = hip_lib()
+        self.batches, self.h, self.w = batches, feature_h, feature_w
+        self.bev_h, self.bev_w = bev_h, bev_w
+        self.handle, err = _vp(), _err()
+        _check(self.lib.bf_cuda_camera_neck_create(model.handle, batches, feature_h, feature_w,
+                                                   bev_h, bev_w, C.byref(self.handle), err, 512),
+               err, "bf_cuda_camera_neck_create")
+
+    def resident_bytes(self) -> int:
+        return self.lib.bf_cuda_camera_neck_resident_bytes(self.handle)
+
+    def _empty(self, shape, like):
+        torch = _torch()
+        return torch.empty(shape, device=like.device, dtype=torch.float32)
+
+    def fpn_forward(self, s0, s1, s2, stream=None):
+        b, h, w = self.batches, self.h, self.w
+        f0 = self._empty((b, 256, h, w), s0)
+        f1 = self._empty((b, 256, (h + 1) // 2, (w + 1) // 2), s0)
+        err = _err()
+        _check(self.lib.bf_cuda_camera_fpn_forward(self.handle, _ptr(s0), _ptr(s1), _ptr(s2),
+                                                   _ptr(f0), _ptr(f1), _stream(stream), err, 512),
+               err, "bf_cuda_camera_fpn_forward")
+        return f0, f1
+
+    def depth_forward(self, fpn0, depth, stream=None):
+        b, h, w = self.batches, self.h, self.w
+        logits = self._empty((b, 118, h, w), fpn0)
+        ctx = self._empty((b, 80, h, w), fpn0)
+        err = _err()
+        _check(self.lib.bf_cuda_camera_depth_forward(self.handle, _ptr(fpn0), _ptr(depth),
+                                                     _ptr(logits), _ptr(ctx), _stream(stream),
+                                                     err, 512), err,
+               "bf_cuda_camera_depth_forward")
+        return logits, ctx
+
+    def neck_forward(self, s0, s1, s2, depth, logits=None, ctx=None, stream=None):
+        b, h, w = self.batches, self.h, self.w
+        logits = logits if logits is not None else self._empty((b, 118, h, w), s0)
+        ctx = ctx if ctx is not None else self._empty((b, 80, h, w), s0)
+        err = _err()
+        _check(self.lib.bf_cuda_camera_neck_forward(self.handle, _ptr(s0), _ptr(s1), _ptr(s2),
+                                                    _ptr(depth), _ptr(logits), _ptr(ctx),
+                                                    _stream(stream), err, 512), err,
+               "bf_cuda_camera_neck_forward")
+        return logits, ctx
+
+    def downsample_forward(self, bev, stream=None):
+        out = self._empty((1, 80, self.bev_w // 2, self.bev_h // 2), bev)
+        err = _err()
+        _check(self.lib.bf_cuda_camera_downsample_forward(self.handle, _ptr(bev), _ptr(out),
+                                                          _stream(stream), err, 512), err,
+               "bf_cuda_camera_downsample_forward")
+        return out
+
+    def close(self):
+        if self.handle:
+            self.lib.bf_cuda_camera_neck_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

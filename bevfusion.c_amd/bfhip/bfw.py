@@ -1,0 +1,265 @@
+"""BFW container writer and synthetic camera-branch checkpoints.
+
+The writer emits the layout read by ``csrc/bfw_model.c`` (and by the
+reference's ``src/model.c``): a 64-byte header, 160-byte directory entries and
+64-byte aligned little-endian payloads, as produced by the reference exporter
+``tools/export_checkpoint.py:12-17,49-80``.
+
+``camera_branch_tensors`` builds random-init weights under the exact tensor
+names and shapes that the Swin-T context (reference src/cuda_swin.cu:290-317)
+and the camera-neck context (src/cuda_camera.cu:301-318) bind.  There is no
+network access for the real checkpoint, so every benchmark and parity test
+runs on these synthetic weights.
+"""
+
+from __future__ import annotations
+
+import pathlib
+import struct
+import zlib
+
+import numpy as np
+
+MAGIC = b"BFW0001\0"
+HEADER = struct.Struct("<8sIIQQQQII8s")
+ENTRY = struct.Struct("<96sII8IQQII")
+ALIGN = 64
+F32, I64 = 1, 2
+
+SWIN_CHANNELS = (96, 192, 384, 768)
+SWIN_HEADS = (3, 6, 12, 24)
+SWIN_DEPTHS = (2, 2, 6, 2)
+
+
+# --------------------------------------------------------------------------
+# Counter-based RNG: splitmix64 over (stream, index) + Box-Muller.  Every
+# value depends only on (seed, name, index), so a tensor regenerates
+# bit-identically regardless of the order tensors are produced in.
+# --------------------------------------------------------------------------
+_M64 = np.uint64(0xFFFFFFFFFFFFFFFF)
+
+
+def _splitmix64(x: np.ndarray) -> np.ndarray:
+    with np.errstate(over="ignore"):
+        z = x + np.uint64(0x9E3779B97F4A7C15)
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+        return z ^ (z >> np.uint64(31))
+
+
+def stream_key(seed: int, name: str) -> int:
+    return ((seed & 0xFFFFFFFF) << 32) ^ zlib.crc32(name.encode("utf-8"))
+
+
+def uniform(key: int, count: int, offset: int = 0) -> np.ndarray:
+    """Uniform float64 in (0, 1), 53-bit, from counter ``offset + i``."""
+    idx = np.arange(offset, offset + count, dtype=np.uint64)
+    with np.errstate(over="ignore"):
+        base = _splitmix64(np.uint64(key) * np.uint64(0xD1B54A32D192ED03) + idx)
+    bits = _splitmix64(base) >> np.uint64(11)
+    return (bits.astype(np.float64) + 0.5) * (1.0 / 9007199254740992.0)
+
+
+def normal(key: int, count: int) -> np.ndarray:
+    """Standard normal float64 via Box-Muller on paired uniforms."""
+    pairs = (count + 1) // 2
+    u1 = uniform(key, pairs, 0)
+    u2 = uniform(key, pairs, 1 << 40)
+    r = np.sqrt(-2.0 * np.log(u1))
+    z = np.concatenate([r * np.cos(2.0 * np.pi * u2), r * np.sin(2.0 * np.pi * u2)])
+    return z[:count]
+
+
+def randn(seed: int, name: str, shape, std=1.0, mean=0.0) -> np.ndarray:
+    n = int(np.prod(shape)) if len(shape) else 1
+    return (normal(stream_key(seed, name), n) * std + mean).astype(np.float32).reshape(shape)
+
+
+def randu(seed: int, name: str, shape, low=0.0, high=1.0) -> np.ndarray:
+    n = int(np.prod(shape)) if len(shape) else 1
+    u = uniform(stream_key(seed, name), n)
+    return (low + (high - low) * u).astype(np.float32).reshape(shape)
+
+
+# --------------------------------------------------------------------------
+# Writer
+# --------------------------------------------------------------------------
+def _align(v: int) -> int:
+    return (v + ALIGN - 1) & -ALIGN
+
+
+def write_bfw(tensors, path) -> int:
+    """Write [(name, ndarray)] (float32 or int64) to ``path``; returns bytes."""
+    path = pathlib.Path(path)
+    entries, payloads = [], []
+    data_offset = _align(HEADER.size + len(tensors) * ENTRY.size)
+    cursor = data_offset
+    seen = set()
+    for name, arr in tensors:
+        if name in seen:
+            raise ValueError(f"duplicate tensor {name}")
+        seen.add(name)
+        arr = np.ascontiguousarray(arr)
+        if arr.dtype == np.float32:
+            dtype = F32
+        elif arr.dtype == np.int64:
+            dtype = I64
+        else:
+            raise TypeError(f"{name}: unsupported dtype {arr.dtype}")
+        enc = name.encode("utf-8")
+        if len(enc) >= 96 or arr.ndim > 8 or any(d <= 0 for d in arr.shape):
+            raise ValueError(f"{name}: unsupported name or shape {arr.shape}")
+        raw = arr.astype(arr.dtype.newbyteorder("<"), copy=False).tobytes()
+        cursor = _align(cursor)
+        dims = list(arr.shape) + [0] * (8 - arr.ndim)
+        entries.append(ENTRY.pack(enc, dtype, arr.ndim, *dims, cursor, len(raw),
+                                  zlib.crc32(raw) & 0xFFFFFFFF, 0))
+        payloads.append((cursor, raw))
+        cursor += len(raw)
+    directory = b"".join(entries)
+    header = HEADER.pack(MAGIC, 1, HEADER.size, len(tensors), HEADER.size,
+                         data_offset, cursor, zlib.crc32(directory) & 0xFFFFFFFF,
+                         0, b"\0" * 8)
+    path.parent.mkdir(parents=True, exist_ok=True)
+    tmp = path.with_name(path.name + ".tmp")
+    with tmp.open("wb") as f:
+        f.write(header)
+        f.write(directory)
+        for off, raw in payloads:
+            f.write(b"\0" * (off - f.tell()))
+            f.write(raw)
+    tmp.replace(path)
+    return cursor
+
+
+# --------------------------------------------------------------------------
+# Synthetic camera-branch checkpoint
+# --------------------------------------------------------------------------
+def relative_position_index(window: int = 7) -> np.ndarray:
+    """Swin relative index, closed form (qy-ky+w-1)*(2w-1) + (qx-kx+w-1)."""
+    t = np.arange(window * window)
+    qy, qx = (t // window)[:, None], (t % window)[:, None]
+    ky, kx = (t // window)[None, :], (t % window)[None, :]
+    return ((qy - ky + window - 1) * (2 * window - 1) + (qx - kx + window - 1)).astype(np.int64)
+
+
+class _Init:
+    """Weight initialisation policy.
+
+    ``mode="baseline"``: every weight ~N(0, 0.02), as BASELINE.json configs
+    2-4 state.  ``mode="fan_in"``: weights ~N(0, gain/sqrt(fan_in)) so every
+    residual branch contributes O(1) to its output; the parity tests use it
+    so that a wrong branch cannot hide under the residual stream.
+    """
+
+    def __init__(self, seed: int, mode: str = "baseline", gain: float = 1.0):
+        if mode not in ("baseline", "fan_in"):
+            raise ValueError(mode)
+        self.seed, self.mode, self.gain = seed, mode, gain
+
+    def weight(self, name, shape, fan_in):
+        std = 0.02 if self.mode == "baseline" else self.gain / np.sqrt(fan_in)
+        return randn(self.seed, name, shape, std)
+
+    def bias(self, name, shape):
+        return randn(self.seed, name, shape, 0.02)
+
+    def norm(self, prefix, c):
+        return [(prefix + ".weight", randn(self.seed, prefix + ".weight", (c,), 0.02, 1.0)),
+                (prefix + ".bias", randn(self.seed, prefix + ".bias", (c,), 0.02))]
+
+    def bn(self, prefix, c):
+        return [(prefix + ".weight", randn(self.seed, prefix + ".weight", (c,), 0.1, 1.0)),
+                (prefix + ".bias", randn(self.seed, prefix + ".bias", (c,), 0.1)),
+                (prefix + ".running_mean", randn(self.seed, prefix + ".running_mean", (c,), 0.1)),
+                (prefix + ".running_var", randu(self.seed, prefix + ".running_var", (c,), 0.5, 1.5))]
+
+
+def swin_tensors(init: _Init):
+    out = []
+    p = "image_backbone."
+    out.append((p + "patch_embed.projection.weight",
+                init.weight(p + "patch_embed.projection.weight", (96, 3, 4, 4), 48)))
+    out.append((p + "patch_embed.projection.bias", init.bias(p + "patch_embed.projection.bias", (96,))))
+    out += init.norm(p + "patch_embed.norm", 96)
+    rel_index = relative_position_index(7)
+    for s, (c, h, d) in enumerate(zip(SWIN_CHANNELS, SWIN_HEADS, SWIN_DEPTHS)):
+        for b in range(d):
+            q = f"{p}stages.{s}.blocks.{b}."
+            out += init.norm(q + "norm1", c)
+            out.append((q + "attn.w_msa.relative_position_bias_table",
+                        randn(init.seed, q + "attn.w_msa.relative_position_bias_table", (169, h),
+                              0.02 if init.mode == "baseline" else 0.5)))
+            out.append((q + "attn.w_msa.relative_position_index", rel_index.copy()))
+            out.append((q + "attn.w_msa.qkv.weight", init.weight(q + "attn.w_msa.qkv.weight", (3 * c, c), c)))
+            out.append((q + "attn.w_msa.qkv.bias", init.bias(q + "attn.w_msa.qkv.bias", (3 * c,))))
+            out.append((q + "attn.w_msa.proj.weight", init.weight(q + "attn.w_msa.proj.weight", (c, c), c)))
+            out.append((q + "attn.w_msa.proj.bias", init.bias(q + "attn.w_msa.proj.bias", (c,))))
+            out += init.norm(q + "norm2", c)
+            out.append((q + "ffn.layers.0.0.weight", init.weight(q + "ffn.layers.0.0.weight", (4 * c, c), c)))
+            out.append((q + "ffn.layers.0.0.bias", init.bias(q + "ffn.layers.0.0.bias", (4 * c,))))
+            out.append((q + "ffn.layers.1.weight", init.weight(q + "ffn.layers.1.weight", (c, 4 * c), 4 * c)))
+            out.append((q + "ffn.layers.1.bias", init.bias(q + "ffn.layers.1.bias", (c,))))
+        if s < 3:
+            q = f"{p}stages.{s}.downsample."
+            out += init.norm(q + "norm", 4 * c)
+            out.append((q + "reduction.weight", init.weight(q + "reduction.weight", (2 * c, 4 * c), 4 * c)))
+    for i in range(1, 4):
+        out += init.norm(f"{p}norm{i}", SWIN_CHANNELS[i])
+    return out
+
+
+def neck_tensors(init: _Init):
+    out = []
+    for level, cin in ((0, 448), (1, 1152)):
+        for kind, ci, k in (("lateral_convs", cin, 1), ("fpn_convs", 256, 3)):
+            q = f"neck.{kind}.{level}."
+            out.append((q + "conv.weight", init.weight(q + "conv.weight", (256, ci, k, k), ci * k * k)))
+            out += init.bn(q + "bn", 256)
+    v = "vtransform."
+    for conv, bn, co, ci, k in ((0, 1, 8, 1, 1), (3, 4, 32, 8, 5), (6, 7, 64, 32, 5)):
+        q = f"{v}dtransform.{conv}."
+        out.append((q + "weight", init.weight(q + "weight", (co, ci, k, k), ci * k * k)))
+        out.append((q + "bias", init.bias(q + "bias", (co,))))
+        out += init.bn(f"{v}dtransform.{bn}", co)
+    for conv, bn, co, ci, k in ((0, 1, 256, 320, 3), (3, 4, 256, 256, 3)):
+        q = f"{v}depthnet.{conv}."
+        out.append((q + "weight", init.weight(q + "weight", (co, ci, k, k), ci * k * k)))
+        out.append((q + "bias", init.bias(q + "bias", (co,))))
+        out += init.bn(f"{v}depthnet.{bn}", co)
+    out.append((v + "depthnet.6.weight", init.weight(v + "depthnet.6.weight", (198, 256, 1, 1), 256)))
+    out.append((v + "depthnet.6.bias", init.bias(v + "depthnet.6.bias", (198,))))
+    for conv, bn in ((0, 1), (3, 4), (6, 7)):
+        q = f"{v}downsample.{conv}."
+        out.append((q + "weight", init.weight(q + "weight", (80, 80, 3, 3), 720)))
+        out += init.bn(f"{v}downsample.{bn}", 80)
+    return out
+
+
+def camera_branch_tensors(seed: int = 0, mode: str = "baseline", gain: float = 1.0):
+    init = _Init(seed, mode, gain)
+    return swin_tensors(init) + neck_tensors(init)
+
+
+def write_camera_branch(path, seed: int = 0, mode: str = "baseline", gain: float = 1.0) -> pathlib.Path:
+    path = pathlib.Path(path)
+    write_bfw(camera_branch_tensors(seed, mode, gain), path)
+    return path
+
+
+# --------------------------------------------------------------------------
+# Synthetic frame inputs
+# --------------------------------------------------------------------------
+IMAGENET_MEAN = np.array([0.485, 0.456, 0.406], dtype=np.float32)
+IMAGENET_STD = np.array([0.229, 0.224, 0.225], dtype=np.float32)
+
+
+def synthetic_images(seed: int, batches=6, height=256, width=704) -> np.ndarray:
+    """U[0,1] pixels, ImageNet-normalised, NCHW float32."""
+    img = randu(seed, "images", (batches, 3, height, width))
+    return ((img - IMAGENET_MEAN[None, :, None, None]) / IMAGENET_STD[None, :, None, None]).astype(np.float32)
+
+
+def synthetic_depth(seed: int, batches=6, height=256, width=704) -> np.ndarray:
+    """Dense depth |N(0,1)|, [B,1,H,W] float32."""
+    return np.abs(randn(seed, "dense_depth", (batches, 1, height, width)))

@@ -1,0 +1,350 @@
+"""ctypes binding of the CPU oracle (TEST INFRASTRUCTURE ONLY).
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline
+leg may import this package, and only as the checker.  The same wrapper drives
+four interchangeable libraries with identical C signatures:
+
+  ``port``        oracle/_build/liboracle.so         restatement, OpenMP dispatch
+  ``port_scalar`` oracle/_build/liboracle_scalar.so  restatement, no OpenMP
+  ``ref``         oracle/_ref/libbfref.so            reference C compiled from its sources
+  ``ref_scalar``  oracle/_ref/libbfref_scalar.so     same, no OpenMP
+
+Each library carries its own BFW reader, so models are opened through the
+library that consumes them.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import os
+import pathlib
+
+import numpy as np
+
+HERE = pathlib.Path(__file__).resolve().parent
+LIBS = {
+    "port": HERE / "_build" / "liboracle.so",
+    "port_scalar": HERE / "_build" / "liboracle_scalar.so",
+    "ref": HERE / "_ref" / "libbfref.so",
+    "ref_scalar": HERE / "_ref" / "libbfref_scalar.so",
+}
+
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_i64p = np.ctypeslib.ndpointer(dtype=np.int64, flags="C_CONTIGUOUS")
+_sz = C.c_size_t
+
+
+class ConvDesc(C.Structure):
+    _fields_ = [(n, _sz) for n in (
+        "n", "in_channels", "in_height", "in_width", "out_channels", "kernel_height",
+        "kernel_width", "stride_height", "stride_width", "pad_height", "pad_width",
+        "dilation_height", "dilation_width", "groups")]
+
+
+class ConvTransposeDesc(C.Structure):
+    _fields_ = [(n, _sz) for n in (
+        "n", "in_channels", "in_height", "in_width", "out_channels", "kernel_height",
+        "kernel_width", "stride_height", "stride_width", "pad_height", "pad_width",
+        "output_pad_height", "output_pad_width", "dilation_height", "dilation_width",
+        "groups")]
+
+
+class WindowDesc(C.Structure):
+    _fields_ = [(n, _sz) for n in (
+        "batches", "height", "width", "channels", "heads", "window_size", "shift_size")]
+
+
+class OracleError(RuntimeError):
+    pass
+
+
+def available(flavour: str) -> bool:
+    return LIBS[flavour].exists()
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+class Oracle:
+    def __init__(self, flavour: str = "port"):
+        path = LIBS[flavour]
+        if not path.exists():
+            raise OracleError(f"oracle library {path} is not built")
+        self.flavour = flavour
+        self.lib = C.CDLL(str(path))
+        L = self.lib
+        L.bf_model_open.argtypes = [C.c_char_p, C.POINTER(C.c_void_p), C.c_char_p, _sz]
+        L.bf_model_close.argtypes = [C.c_void_p]
+        L.bf_cpu_kernel_backend.restype = C.c_char_p
+        L.bf_conv2d_f32.argtypes = [_f32p, _f32p, C.c_void_p, _f32p, C.POINTER(ConvDesc)]
+        L.bf_conv2d_f32_ref.argtypes = L.bf_conv2d_f32.argtypes
+        L.bf_conv2d_output_shape.argtypes = [C.POINTER(ConvDesc), C.POINTER(_sz), C.POINTER(_sz)]
+        L.bf_conv_transpose2d_f32_ref.argtypes = [_f32p, _f32p, C.c_void_p, _f32p,
+                                                  C.POINTER(ConvTransposeDesc)]
+        L.bf_conv_transpose2d_output_shape.argtypes = [C.POINTER(ConvTransposeDesc),
+                                                       C.POINTER(_sz), C.POINTER(_sz)]
+        for n in ("bf_linear_f32", "bf_linear_f32_ref"):
+            getattr(L, n).argtypes = [_f32p, _f32p, C.c_void_p, _f32p, _sz, _sz, _sz]
+            getattr(L, n).restype = None
+        for n in ("bf_layer_norm_f32", "bf_layer_norm_f32_ref"):
+            getattr(L, n).argtypes = [_f32p, _f32p, _f32p, C.c_float, _f32p, _sz, _sz]
+            getattr(L, n).restype = None
+        for n in ("bf_batch_norm_2d_f32", "bf_batch_norm_2d_f32_ref"):
+            getattr(L, n).argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, C.c_float, _f32p,
+                                      _sz, _sz, _sz, _sz]
+            getattr(L, n).restype = None
+        L.bf_softmax_f32_ref.argtypes = [_f32p, _f32p, _sz, _sz]
+        L.bf_softmax_f32_ref.restype = None
+        for n in ("bf_gelu_f32", "bf_gelu_f32_ref", "bf_relu_f32", "bf_relu_f32_ref"):
+            getattr(L, n).argtypes = [_f32p, _f32p, _sz]
+            getattr(L, n).restype = None
+        L.bf_swin_shifted_window_f32_ref.argtypes = [
+            _f32p, _f32p, _f32p, _f32p, _i64p, _f32p, _f32p, _f32p, C.POINTER(WindowDesc)]
+        L.bf_swin_shifted_window_workspace_bytes.argtypes = [C.POINTER(WindowDesc)]
+        L.bf_swin_shifted_window_workspace_bytes.restype = _sz
+        L.bf_swin_shifted_window_f32_workspace_ref.argtypes = [
+            _f32p, _f32p, _f32p, _f32p, _i64p, _f32p, _f32p, _f32p, C.POINTER(WindowDesc),
+            C.c_void_p, _sz]
+        L.bf_swin_window_attention_f32_ref.argtypes = [
+            _f32p, _f32p, _f32p, _f32p, _i64p, C.c_void_p, _sz, _f32p, _f32p, _f32p,
+            _sz, _sz, _sz, _sz, _sz]
+        for mod in ("swin_backbone", "image_fpn", "depth_head", "lss_downsample"):
+            getattr(L, f"bf_{mod}_create").argtypes = [C.c_void_p, C.POINTER(C.c_void_p),
+                                                       C.c_char_p, _sz]
+            getattr(L, f"bf_{mod}_destroy").argtypes = [C.c_void_p]
+            getattr(L, f"bf_{mod}_destroy").restype = None
+        L.bf_swin_backbone_workspace_bytes.argtypes = [_sz, _sz, _sz]
+        L.bf_swin_backbone_workspace_bytes.restype = _sz
+        L.bf_swin_backbone_forward_ref.argtypes = [
+            C.c_void_p, _f32p, _sz, _sz, _sz, _f32p, _f32p, _f32p, C.c_void_p, _sz,
+            C.c_char_p, _sz]
+        for mod in ("image_fpn", "depth_head", "lss_downsample"):
+            getattr(L, f"bf_{mod}_workspace_bytes").argtypes = [_sz, _sz]
+            getattr(L, f"bf_{mod}_workspace_bytes").restype = _sz
+        L.bf_image_fpn_forward_ref.argtypes = [
+            C.c_void_p, _f32p, _f32p, _f32p, _sz, _sz, _sz, _f32p, _f32p, C.c_void_p, _sz,
+            C.c_char_p, _sz]
+        L.bf_depth_head_forward_ref.argtypes = [
+            C.c_void_p, _f32p, _f32p, _sz, _sz, _sz, _f32p, _f32p, C.c_void_p, _sz,
+            C.c_char_p, _sz]
+        L.bf_lss_downsample_forward_ref.argtypes = [
+            C.c_void_p, _f32p, _sz, _sz, _sz, _f32p, C.c_void_p, _sz, C.c_char_p, _sz]
+
+    # ---- utilities -------------------------------------------------------
+    def backend(self) -> str:
+        return self.lib.bf_cpu_kernel_backend().decode()
+
+    def open_model(self, path):
+        handle, err = C.c_void_p(), C.create_string_buffer(256)
+        if not self.lib.bf_model_open(str(path).encode(), C.byref(handle), err, 256):
+            raise OracleError(err.value.decode())
+        return _Model(self.lib, handle)
+
+    # ---- operators -------------------------------------------------------
+    def conv2d(self, x, w, b, stride=(1, 1), pad=(0, 0), dilation=(1, 1), groups=1,
+               scalar=False):
+        x, w = _f32(x), _f32(w)
+        n, ci, ih, iw = x.shape
+        co, _, kh, kw = w.shape
+        d = ConvDesc(n, ci, ih, iw, co, kh, kw, stride[0], stride[1], pad[0], pad[1],
+                     dilation[0], dilation[1], groups)
+        oh, ow = _sz(), _sz()
+        if not self.lib.bf_conv2d_output_shape(C.byref(d), C.byref(oh), C.byref(ow)):
+            raise OracleError("invalid convolution")
+        y = np.empty((n, co, oh.value, ow.value), np.float32)
+        bb = None if b is None else _f32(b)
+        fn = self.lib.bf_conv2d_f32_ref if scalar else self.lib.bf_conv2d_f32
+        if not fn(x, w, None if bb is None else bb.ctypes.data, y, C.byref(d)):
+            raise OracleError("convolution failed")
+        return y
+
+    def conv_transpose2d(self, x, w_iohw, b, stride=(1, 1), pad=(0, 0), output_pad=(0, 0),
+                         dilation=(1, 1), groups=1):
+        x, w = _f32(x), _f32(w_iohw)
+        n, ci, ih, iw = x.shape
+        co = w.shape[1] * groups
+        d = ConvTransposeDesc(n, ci, ih, iw, co, w.shape[2], w.shape[3], stride[0], stride[1],
+                              pad[0], pad[1], output_pad[0], output_pad[1], dilation[0],
+                              dilation[1], groups)
+        oh, ow = _sz(), _sz()
+        if not self.lib.bf_conv_transpose2d_output_shape(C.byref(d), C.byref(oh), C.byref(ow)):
+            raise OracleError("invalid transposed convolution")
+        y = np.empty((n, co, oh.value, ow.value), np.float32)
+        bb = None if b is None else _f32(b)
+        if not self.lib.bf_conv_transpose2d_f32_ref(x, w, None if bb is None else bb.ctypes.data,
+                                                    y, C.byref(d)):
+            raise OracleError("transposed convolution failed")
+        return y
+
+    def linear(self, x, w, b, scalar=False):
+        x, w = _f32(x), _f32(w)
+        rows, k = x.shape
+        y = np.empty((rows, w.shape[0]), np.float32)
+        bb = None if b is None else _f32(b)
+        fn = self.lib.bf_linear_f32_ref if scalar else self.lib.bf_linear_f32
+        fn(x, w, None if bb is None else bb.ctypes.data, y, rows, k, w.shape[0])
+        return y
+
+    def layer_norm(self, x, g, b, eps=1e-5, scalar=False):
+        x = _f32(x)
+        y = np.empty_like(x)
+        fn = self.lib.bf_layer_norm_f32_ref if scalar else self.lib.bf_layer_norm_f32
+        fn(x, _f32(g), _f32(b), eps, y, x.size // x.shape[-1], x.shape[-1])
+        return y
+
+    def batch_norm(self, x, g, b, mean, var, eps=1e-5, scalar=False):
+        x = _f32(x)
+        y = np.empty_like(x)
+        fn = self.lib.bf_batch_norm_2d_f32_ref if scalar else self.lib.bf_batch_norm_2d_f32
+        fn(x, _f32(g), _f32(b), _f32(mean), _f32(var), eps, y, *x.shape)
+        return y
+
+    def softmax(self, x):
+        x = _f32(x)
+        y = np.empty_like(x)
+        self.lib.bf_softmax_f32_ref(x, y, x.size // x.shape[-1], x.shape[-1])
+        return y
+
+    def gelu(self, x, scalar=False):
+        x = _f32(x)
+        y = np.empty_like(x)
+        (self.lib.bf_gelu_f32_ref if scalar else self.lib.bf_gelu_f32)(x, y, x.size)
+        return y
+
+    def relu(self, x):
+        x = _f32(x)
+        y = np.empty_like(x)
+        self.lib.bf_relu_f32(x, y, x.size)
+        return y
+
+    def swin_window(self, query, qkv_w, qkv_b, rel_bias, rel_index, proj_w, proj_b,
+                    heads, window, shift, streamed=True):
+        """One W-MSA / SW-MSA branch on [B,H,W,C] tokens (swin.c:119-311)."""
+        q = _f32(query)
+        b, h, w, c = q.shape
+        d = WindowDesc(b, h, w, c, heads, window, shift)
+        out = np.zeros_like(q)
+        args = (q, _f32(qkv_w), _f32(qkv_b), _f32(rel_bias),
+                np.ascontiguousarray(rel_index, np.int64), _f32(proj_w), _f32(proj_b), out,
+                C.byref(d))
+        if streamed:
+            nbytes = self.lib.bf_swin_shifted_window_workspace_bytes(C.byref(d))
+            ws = np.empty(nbytes // 4 + 1, np.float32)
+            ok = self.lib.bf_swin_shifted_window_f32_workspace_ref(*args, ws.ctypes.data, nbytes)
+        else:
+            ok = self.lib.bf_swin_shifted_window_f32_ref(*args)
+        if not ok:
+            raise OracleError("window attention failed")
+        return out
+
+    # ---- modules -----------------------------------------------------------
+    def swin_backbone(self, model, images):
+        x = _f32(images)
+        b, _, ih, iw = x.shape
+        net = model.create("swin_backbone")
+        try:
+            outs = [np.empty((b, c, -(-ih // d), -(-iw // d)), np.float32)
+                    for c, d in ((192, 8), (384, 16), (768, 32))]
+            nbytes = self.lib.bf_swin_backbone_workspace_bytes(b, ih, iw)
+            ws = np.empty(nbytes // 4 + 1, np.float32)
+            err = C.create_string_buffer(256)
+            if not self.lib.bf_swin_backbone_forward_ref(net, x, b, ih, iw, *outs, ws.ctypes.data,
+                                                         nbytes, err, 256):
+                raise OracleError(err.value.decode())
+            return tuple(outs)
+        finally:
+            self.lib.bf_swin_backbone_destroy(net)
+
+    def image_fpn(self, model, s0, s1, s2):
+        s0, s1, s2 = _f32(s0), _f32(s1), _f32(s2)
+        b, _, h, w = s0.shape
+        net = model.create("image_fpn")
+        try:
+            o0 = np.empty((b, 256, h, w), np.float32)
+            o1 = np.empty((b, 256, (h + 1) // 2, (w + 1) // 2), np.float32)
+            nbytes = self.lib.bf_image_fpn_workspace_bytes(h, w)
+            ws = np.empty(nbytes // 4 + 1, np.float32)
+            err = C.create_string_buffer(256)
+            if not self.lib.bf_image_fpn_forward_ref(net, s0, s1, s2, b, h, w, o0, o1,
+                                                     ws.ctypes.data, nbytes, err, 256):
+                raise OracleError(err.value.decode())
+            return o0, o1
+        finally:
+            self.lib.bf_image_fpn_destroy(net)
+
+    def depth_head(self, model, features, depth):
+        f, d = _f32(features), _f32(depth)
+        b, _, h, w = f.shape
+        net = model.create("depth_head")
+        try:
+            logits = np.empty((b, 118, h, w), np.float32)
+            ctx = np.empty((b, 80, h, w), np.float32)
+            nbytes = self.lib.bf_depth_head_workspace_bytes(h, w)
+            ws = np.empty(nbytes // 4 + 1, np.float32)
+            err = C.create_string_buffer(256)
+            if not self.lib.bf_depth_head_forward_ref(net, f, d, b, h, w, logits, ctx,
+                                                      ws.ctypes.data, nbytes, err, 256):
+                raise OracleError(err.value.decode())
+            return logits, ctx
+        finally:
+            self.lib.bf_depth_head_destroy(net)
+
+    def lss_downsample(self, model, bev):
+        x = _f32(bev)
+        b, _, h, w = x.shape
+        net = model.create("lss_downsample")
+        try:
+            out = np.empty((b, 80, w // 2, h // 2), np.float32)
+            nbytes = self.lib.bf_lss_downsample_workspace_bytes(h, w)
+            ws = np.empty(nbytes // 4 + 1, np.float32)
+            err = C.create_string_buffer(256)
+            if not self.lib.bf_lss_downsample_forward_ref(net, x, b, h, w, out, ws.ctypes.data,
+                                                          nbytes, err, 256):
+                raise OracleError(err.value.decode())
+            return out
+        finally:
+            self.lib.bf_lss_downsample_destroy(net)
+
+
+class _Model:
+    def __init__(self, lib, handle):
+        self.lib, self.handle = lib, handle
+
+    def create(self, module: str):
+        out, err = C.c_void_p(), C.create_string_buffer(256)
+        if not getattr(self.lib, f"bf_{module}_create")(self.handle, C.byref(out), err, 256):
+            raise OracleError(err.value.decode())
+        return out
+
+    def close(self):
+        if self.handle:
+            self.lib.bf_model_close(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def scalar_env():
+    """Context manager forcing BF_CPU_SCALAR=1 (the reference's scalar switch)."""
+    class _Env:
+        def __enter__(self):
+            self.prev = os.environ.get("BF_CPU_SCALAR")
+            os.environ["BF_CPU_SCALAR"] = "1"
+
+        def __exit__(self, *exc):
+            if self.prev is None:
+                os.environ.pop("BF_CPU_SCALAR", None)
+            else:
+                os.environ["BF_CPU_SCALAR"] = self.prev
+    return _Env()

@@ -1,0 +1,173 @@
+/*
+ * CPU oracle: a C11 restatement of the reference's scalar CPU path for the
+ * camera dense-contraction hot path. TEST INFRASTRUCTURE ONLY: it is the
+ * checker that tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg
+ * compare the HIP library against; no product code links or calls it.
+ *
+ * Function names, argument meaning, workspace sizes and error behaviour follow
+ * the reference headers they restate:
+ *   bf_kernels.h        -> reference include/bf_kernels.h:11-87, src/kernels_ref.c:16-475
+ *   bf_swin.h           -> reference include/bf_swin.h:7-46,     src/swin.c:16-311
+ *   bf_swin_backbone.h  -> reference include/bf_swin_backbone.h, src/swin_backbone.c:38-352
+ *   bf_image_fpn.h      -> reference include/bf_image_fpn.h,     src/image_fpn.c:73-197
+ *   bf_depth_head.h     -> reference include/bf_depth_head.h,    src/depth_head.c:96-190
+ *   bf_lss_downsample.h -> reference include/bf_lss_downsample.h, src/lss_downsample.c:70-148
+ * Floating-point operation order matches the reference per output element, so
+ * the scalar build (no OpenMP, BF_CPU_SCALAR=1) is bit-identical to the
+ * reference compiled from its own sources (oracle/_ref).
+ */
+#ifndef BF_ORACLE_H
+#define BF_ORACLE_H
+
+#include "bf_model.h"
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- operator library (bf_kernels.h) ---------------------------------- */
+typedef struct {
+    size_t n, in_channels, in_height, in_width;
+    size_t out_channels, kernel_height, kernel_width;
+    size_t stride_height, stride_width;
+    size_t pad_height, pad_width;
+    size_t dilation_height, dilation_width;
+    size_t groups;
+} bf_conv2d_desc;
+
+typedef struct {
+    size_t n, in_channels, in_height, in_width;
+    size_t out_channels, kernel_height, kernel_width;
+    size_t stride_height, stride_width;
+    size_t pad_height, pad_width;
+    size_t output_pad_height, output_pad_width;
+    size_t dilation_height, dilation_width;
+    size_t groups;
+} bf_conv_transpose2d_desc;
+
+const char *bf_cpu_kernel_backend(void);
+int bf_conv2d_output_shape(const bf_conv2d_desc *d, size_t *oh, size_t *ow);
+int bf_conv2d_f32_ref(const float *input, const float *weight, const float *bias,
+                      float *output, const bf_conv2d_desc *d);
+int bf_conv2d_f32(const float *input, const float *weight, const float *bias,
+                  float *output, const bf_conv2d_desc *d);
+int bf_conv_transpose2d_output_shape(const bf_conv_transpose2d_desc *d,
+                                     size_t *oh, size_t *ow);
+int bf_conv_transpose2d_f32_ref(const float *input, const float *weight_iohw,
+                                const float *bias, float *output,
+                                const bf_conv_transpose2d_desc *d);
+void bf_linear_f32_ref(const float *input, const float *weight, const float *bias,
+                       float *output, size_t rows, size_t in_f, size_t out_f);
+void bf_linear_f32(const float *input, const float *weight, const float *bias,
+                   float *output, size_t rows, size_t in_f, size_t out_f);
+void bf_batch_norm_2d_f32_ref(const float *input, const float *scale,
+                              const float *bias, const float *mean,
+                              const float *variance, float epsilon, float *output,
+                              size_t n, size_t channels, size_t height, size_t width);
+void bf_batch_norm_2d_f32(const float *input, const float *scale,
+                          const float *bias, const float *mean,
+                          const float *variance, float epsilon, float *output,
+                          size_t n, size_t channels, size_t height, size_t width);
+void bf_layer_norm_f32_ref(const float *input, const float *scale, const float *bias,
+                           float epsilon, float *output, size_t rows, size_t channels);
+void bf_layer_norm_f32(const float *input, const float *scale, const float *bias,
+                       float epsilon, float *output, size_t rows, size_t channels);
+void bf_softmax_f32_ref(const float *input, float *output, size_t rows, size_t columns);
+void bf_gelu_f32_ref(const float *input, float *output, size_t count);
+void bf_gelu_f32(const float *input, float *output, size_t count);
+void bf_relu_f32_ref(const float *input, float *output, size_t count);
+void bf_relu_f32(const float *input, float *output, size_t count);
+
+/* ---- shifted-window attention (bf_swin.h) ----------------------------- */
+typedef struct {
+    size_t batches, height, width, channels, heads, window_size, shift_size;
+} bf_swin_window_desc;
+
+int bf_swin_window_attention_f32_ref(
+    const float *windows, const float *qkv_weight, const float *qkv_bias,
+    const float *relative_bias, const int64_t *relative_index,
+    const float *mask, size_t mask_windows,
+    const float *projection_weight, const float *projection_bias,
+    float *output, size_t total_windows, size_t tokens, size_t channels,
+    size_t heads, size_t relative_bias_rows);
+int bf_swin_shifted_window_f32_ref(
+    const float *query, const float *qkv_weight, const float *qkv_bias,
+    const float *relative_bias, const int64_t *relative_index,
+    const float *projection_weight, const float *projection_bias,
+    float *output, const bf_swin_window_desc *desc);
+size_t bf_swin_shifted_window_workspace_bytes(const bf_swin_window_desc *desc);
+int bf_swin_shifted_window_f32_workspace_ref(
+    const float *query, const float *qkv_weight, const float *qkv_bias,
+    const float *relative_bias, const int64_t *relative_index,
+    const float *projection_weight, const float *projection_bias,
+    float *output, const bf_swin_window_desc *desc,
+    void *workspace, size_t workspace_bytes);
+
+/* ---- Swin-T backbone (bf_swin_backbone.h) ----------------------------- */
+typedef struct bf_swin_backbone bf_swin_backbone;
+typedef struct {
+    size_t height[3], width[3], channels[3];
+} bf_swin_backbone_shapes;
+int bf_swin_backbone_create(const bf_model *model, bf_swin_backbone **out,
+                            char *error, size_t cap);
+void bf_swin_backbone_destroy(bf_swin_backbone *net);
+int bf_swin_backbone_output_shapes(size_t input_height, size_t input_width,
+                                   bf_swin_backbone_shapes *shapes);
+size_t bf_swin_backbone_workspace_bytes(size_t batches, size_t input_height,
+                                        size_t input_width);
+int bf_swin_backbone_forward_ref(const bf_swin_backbone *net, const float *input,
+                                 size_t batches, size_t input_height,
+                                 size_t input_width, float *out1, float *out2,
+                                 float *out3, void *workspace,
+                                 size_t workspace_bytes, char *error, size_t cap);
+
+/* ---- image FPN (bf_image_fpn.h) --------------------------------------- */
+typedef struct bf_image_fpn bf_image_fpn;
+int bf_image_fpn_create(const bf_model *model, bf_image_fpn **out,
+                        char *error, size_t cap);
+void bf_image_fpn_destroy(bf_image_fpn *fpn);
+size_t bf_image_fpn_workspace_bytes(size_t height, size_t width);
+int bf_image_fpn_forward_ref(const bf_image_fpn *fpn, const float *input0,
+                             const float *input1, const float *input2,
+                             size_t batches, size_t h0, size_t w0,
+                             float *output0, float *output1, void *workspace,
+                             size_t workspace_bytes, char *error, size_t cap);
+
+/* ---- DepthLSS head (bf_depth_head.h) ---------------------------------- */
+typedef struct bf_depth_head bf_depth_head;
+int bf_depth_head_create(const bf_model *model, bf_depth_head **out,
+                         char *error, size_t cap);
+void bf_depth_head_destroy(bf_depth_head *head);
+size_t bf_depth_head_workspace_bytes(size_t height, size_t width);
+int bf_depth_head_forward_ref(const bf_depth_head *head, const float *features,
+                              const float *depth, size_t camera_batches,
+                              size_t height, size_t width, float *logits,
+                              float *context, void *workspace,
+                              size_t workspace_bytes, char *error, size_t cap);
+
+/* ---- post-LSS downsample (bf_lss_downsample.h) ------------------------ */
+typedef struct bf_lss_downsample bf_lss_downsample;
+int bf_lss_downsample_create(const bf_model *model, bf_lss_downsample **out,
+                             char *error, size_t cap);
+void bf_lss_downsample_destroy(bf_lss_downsample *down);
+size_t bf_lss_downsample_workspace_bytes(size_t height, size_t width);
+int bf_lss_downsample_forward_ref(const bf_lss_downsample *down, const float *input,
+                                  size_t batches, size_t height, size_t width,
+                                  float *output, void *workspace,
+                                  size_t workspace_bytes, char *error, size_t cap);
+
+/* ---- shared helpers (internal to the oracle) --------------------------- */
+int bf_oracle_fail(char *error, size_t cap, const char *fmt, ...);
+int bf_oracle_mul(size_t a, size_t b, size_t *out);
+const void *bf_oracle_bind(const bf_model *model, const char *name, uint32_t dtype,
+                           uint32_t rank, const uint32_t *dims,
+                           char *error, size_t cap);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif
