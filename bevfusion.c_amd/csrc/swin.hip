@@ -1,0 +1,344 @@
+// Swin-T camera backbone context (drop-in for reference src/cuda_swin.cu).
+//
+// Data layout in HBM:
+//   x    fp32 [tokens, C]   residual stream, NHWC token order, in place
+//   xn   bf16 [tokens, C]   LayerNorm output -> QKV input; reused for the
+//                           attention output and for the 2x2 merge rows
+//   big  bf16 [tokens, 4C]  QKV [tokens, 3C], later the GELU hidden [tokens, 4C]
+// Window partitioning never materialises: the attention kernel gathers its 49
+// (padded, cyclically shifted) tokens straight from the token-major QKV rows
+// and scatters its output back the same way, so QKV and proj run as plain
+// token GEMMs over B*H*W rows instead of windows*49 rows.
+//
+// Per block (7 launches): LN1 -> QKV GEMM(+bias, bf16) -> window attention ->
+// proj GEMM(+bias, += into x) -> LN2 -> fc1 GEMM(+bias, GELU, bf16) ->
+// fc2 GEMM(+bias, += into x).
+#include "bf_cuda_swin.h"
+#include "conv_core.h"
+#include "host_util.h"
+#include "linear.h"
+#include "swin_kernels.h"
+
+#include <algorithm>
+#include <climits>
+#include <cstdlib>
+#include <vector>
+
+using namespace bfhip;
+
+namespace {
+
+constexpr int kC[4] = {96, 192, 384, 768};
+constexpr int kHeads[4] = {3, 6, 12, 24};
+constexpr int kDepth[4] = {2, 2, 6, 2};
+
+struct BlockW {
+    const float *n1s, *n1b, *n2s, *n2b, *qkv_b, *proj_b, *fc1_b, *fc2_b, *bias_mat;
+    const bf16 *qkv_w, *proj_w, *fc1_w, *fc2_w;
+};
+
+struct BlockOff {
+    size_t n1s, n1b, n2s, n2b, qkv_b, proj_b, fc1_b, fc2_b, bias_mat, qkv_w, proj_w, fc1_w, fc2_w;
+};
+
+}  // namespace
+
+struct bf_cuda_swin {
+    size_t batches, input_h, input_w, resident_bytes;
+    int h[4], w[4];
+    unsigned char *params, *acts;
+    const bf16 *patch_w;
+    const float *patch_b, *patch_ns, *patch_nb;
+    BlockW blocks[4][6];
+    const float *merge_s[3], *merge_b[3], *out_s[3], *out_b[3];
+    const bf16 *merge_w[3];
+    float *x;
+    bf16 *xn, *big;
+};
+
+namespace {
+
+template <typename OutT>
+void launch_ln(int C, const float *x, OutT *y, const float *g, const float *b, int rows,
+               hipStream_t s) {
+#define BF_LN(CC)                                                                            \
+    case CC: {                                                                               \
+        const int per_block = RowLayout<CC>::RPW * 4;                                        \
+        hipLaunchKernelGGL((ln_rows_kernel<CC, OutT>), dim3((rows + per_block - 1) / per_block), \
+                           dim3(256), 0, s, x, y, g, b, rows);                               \
+        break;                                                                               \
+    }
+    switch (C) { BF_LN(96) BF_LN(192) BF_LN(384) BF_LN(768) default: break; }
+#undef BF_LN
+}
+
+void launch_merge(int C, const float *x, bf16 *y, const float *g, const float *b, int batches,
+                  int H, int W, hipStream_t s) {
+    const int rows = batches * ((H + 1) / 2) * ((W + 1) / 2);
+#define BF_MERGE(CC)                                                                         \
+    case CC: {                                                                               \
+        const int per_block = (64 / ((CC % 64 == 0) ? 64 : 32)) * 4;                         \
+        hipLaunchKernelGGL((merge_ln_kernel<CC>), dim3((rows + per_block - 1) / per_block),  \
+                           dim3(256), 0, s, x, y, g, b, batches, H, W);                      \
+        break;                                                                               \
+    }
+    switch (C) { BF_MERGE(96) BF_MERGE(192) BF_MERGE(384) default: break; }
+#undef BF_MERGE
+}
+
+void launch_out_ln(int C, const float *x, float *out, const float *g, const float *b, int rows,
+                   int hw, hipStream_t s) {
+    const dim3 grid((rows + 15) / 16);
+    switch (C) {
+        case 192: hipLaunchKernelGGL((out_ln_kernel<192>), grid, dim3(256), 0, s, x, out, g, b, rows, hw); break;
+        case 384: hipLaunchKernelGGL((out_ln_kernel<384>), grid, dim3(256), 0, s, x, out, g, b, rows, hw); break;
+        case 768: hipLaunchKernelGGL((out_ln_kernel<768>), grid, dim3(256), 0, s, x, out, g, b, rows, hw); break;
+        default: break;
+    }
+}
+
+}  // namespace
+
+extern "C" void bf_cuda_swin_destroy(bf_cuda_swin *s) {
+    if (!s) return;
+    if (s->params) (void)hipFree(s->params);
+    if (s->acts) (void)hipFree(s->acts);
+    std::free(s);
+}
+
+extern "C" size_t bf_cuda_swin_resident_bytes(const bf_cuda_swin *s) {
+    return s ? s->resident_bytes : 0;
+}
+
+static int swin_build(bf_cuda_swin *s, const bf_model *model, size_t batches, size_t input_h,
+                      size_t input_w, char *error, size_t cap) {
+    s->batches = batches;
+    s->input_h = input_h;
+    s->input_w = input_w;
+    s->h[0] = (int)(input_h / 4);
+    s->w[0] = (int)(input_w / 4);
+    for (int i = 1; i < 4; ++i) {
+        s->h[i] = (s->h[i - 1] + 1) / 2;
+        s->w[i] = (s->w[i - 1] + 1) / 2;
+    }
+
+    ParamArena arena;
+    char name[224];
+    size_t o_patch_w, o_patch_b, o_patch_ns, o_patch_nb;
+    BlockOff off[4][6];
+    size_t o_ms[3], o_mb[3], o_mw[3], o_os[3], o_ob[3];
+    {
+        const float *pw = bind_f32(model, "image_backbone.patch_embed.projection.weight",
+                                   {96, 3, 4, 4}, error, cap);
+        const float *pb = bind_f32(model, "image_backbone.patch_embed.projection.bias", {96},
+                                   error, cap);
+        const float *ns = bind_f32(model, "image_backbone.patch_embed.norm.weight", {96}, error,
+                                   cap);
+        const float *nb = bind_f32(model, "image_backbone.patch_embed.norm.bias", {96}, error,
+                                   cap);
+        if (!pw || !pb || !ns || !nb) return 0;
+        o_patch_w = arena.add_bf16(pw, 96 * 48);
+        o_patch_b = arena.add_f32(pb, 96);
+        o_patch_ns = arena.add_f32(ns, 96);
+        o_patch_nb = arena.add_f32(nb, 96);
+    }
+    for (int st = 0; st < 4; ++st) {
+        const uint32_t c = (uint32_t)kC[st], hd = (uint32_t)kHeads[st];
+        for (int b = 0; b < kDepth[st]; ++b) {
+            BlockOff &o = off[st][b];
+#define BF_F32(SUFFIX, ...)                                                                  \
+    (std::snprintf(name, sizeof(name), "image_backbone.stages.%d.blocks.%d.%s", st, b, SUFFIX), \
+     bind_f32(model, name, {__VA_ARGS__}, error, cap))
+            const float *n1s = BF_F32("norm1.weight", c), *n1b = BF_F32("norm1.bias", c);
+            const float *table = BF_F32("attn.w_msa.relative_position_bias_table", 169, hd);
+            std::snprintf(name, sizeof(name),
+                          "image_backbone.stages.%d.blocks.%d.attn.w_msa.relative_position_index",
+                          st, b);
+            const uint32_t idims[2] = {49, 49};
+            const int64_t *index =
+                (const int64_t *)bind_tensor(model, name, BF_DTYPE_I64, 2, idims, error, cap);
+            const float *qkv_w = BF_F32("attn.w_msa.qkv.weight", 3 * c, c);
+            const float *qkv_b = BF_F32("attn.w_msa.qkv.bias", 3 * c);
+            const float *proj_w = BF_F32("attn.w_msa.proj.weight", c, c);
+            const float *proj_b = BF_F32("attn.w_msa.proj.bias", c);
+            const float *n2s = BF_F32("norm2.weight", c), *n2b = BF_F32("norm2.bias", c);
+            const float *fc1_w = BF_F32("ffn.layers.0.0.weight", 4 * c, c);
+            const float *fc1_b = BF_F32("ffn.layers.0.0.bias", 4 * c);
+            const float *fc2_w = BF_F32("ffn.layers.1.weight", c, 4 * c);
+            const float *fc2_b = BF_F32("ffn.layers.1.bias", c);
+#undef BF_F32
+            if (!n1s || !n1b || !table || !index || !qkv_w || !qkv_b || !proj_w || !proj_b ||
+                !n2s || !n2b || !fc1_w || !fc1_b || !fc2_w || !fc2_b)
+                return 0;
+            // Dense per-head bias matrix [heads][49][49] gathered through the
+            // checkpoint's index table (bounds as reference swin.c:34-37).
+            std::vector<float> bias((size_t)hd * 49 * 49);
+            for (int q = 0; q < 49 * 49; ++q) {
+                const int64_t r = index[q];
+                if (r < 0 || r >= 169) {
+                    fail(error, cap, "stage %d block %d: relative_position_index out of range",
+                         st, b);
+                    return 0;
+                }
+                for (uint32_t hh = 0; hh < hd; ++hh) bias[(size_t)hh * 2401 + q] = table[r * hd + hh];
+            }
+            o.n1s = arena.add_f32(n1s, c); o.n1b = arena.add_f32(n1b, c);
+            o.n2s = arena.add_f32(n2s, c); o.n2b = arena.add_f32(n2b, c);
+            o.qkv_b = arena.add_f32(qkv_b, 3 * c); o.proj_b = arena.add_f32(proj_b, c);
+            o.fc1_b = arena.add_f32(fc1_b, 4 * c); o.fc2_b = arena.add_f32(fc2_b, c);
+            o.bias_mat = arena.add_f32(bias);
+            o.qkv_w = arena.add_bf16(qkv_w, (size_t)3 * c * c);
+            o.proj_w = arena.add_bf16(proj_w, (size_t)c * c);
+            o.fc1_w = arena.add_bf16(fc1_w, (size_t)4 * c * c);
+            o.fc2_w = arena.add_bf16(fc2_w, (size_t)4 * c * c);
+        }
+    }
+    for (int st = 0; st < 3; ++st) {
+        const uint32_t c = (uint32_t)kC[st];
+        std::snprintf(name, sizeof(name), "image_backbone.stages.%d.downsample.norm.weight", st);
+        const float *ms = bind_f32(model, name, {4 * c}, error, cap);
+        std::snprintf(name, sizeof(name), "image_backbone.stages.%d.downsample.norm.bias", st);
+        const float *mb = bind_f32(model, name, {4 * c}, error, cap);
+        std::snprintf(name, sizeof(name), "image_backbone.stages.%d.downsample.reduction.weight", st);
+        const float *mw = bind_f32(model, name, {2 * c, 4 * c}, error, cap);
+        std::snprintf(name, sizeof(name), "image_backbone.norm%d.weight", st + 1);
+        const float *os = bind_f32(model, name, {(uint32_t)kC[st + 1]}, error, cap);
+        std::snprintf(name, sizeof(name), "image_backbone.norm%d.bias", st + 1);
+        const float *ob = bind_f32(model, name, {(uint32_t)kC[st + 1]}, error, cap);
+        if (!ms || !mb || !mw || !os || !ob) return 0;
+        o_ms[st] = arena.add_f32(ms, 4 * c);
+        o_mb[st] = arena.add_f32(mb, 4 * c);
+        o_mw[st] = arena.add_bf16(mw, (size_t)8 * c * c);
+        o_os[st] = arena.add_f32(os, kC[st + 1]);
+        o_ob[st] = arena.add_f32(ob, kC[st + 1]);
+    }
+    {
+        if (!hip_ok(hipMalloc(&s->params, arena.host.size()), error, cap, "allocate Swin parameters") ||
+            !hip_ok(hipMemcpy(s->params, arena.host.data(), arena.host.size(), hipMemcpyHostToDevice),
+                    error, cap, "upload Swin parameters"))
+            return 0;
+        s->resident_bytes += arena.host.size();
+        unsigned char *p = s->params;
+        auto F = [p](size_t o) { return (const float *)(p + o); };
+        auto H = [p](size_t o) { return (const bf16 *)(p + o); };
+        s->patch_w = H(o_patch_w); s->patch_b = F(o_patch_b);
+        s->patch_ns = F(o_patch_ns); s->patch_nb = F(o_patch_nb);
+        for (int st = 0; st < 4; ++st)
+            for (int b = 0; b < kDepth[st]; ++b) {
+                const BlockOff &o = off[st][b];
+                BlockW &w = s->blocks[st][b];
+                w.n1s = F(o.n1s); w.n1b = F(o.n1b); w.n2s = F(o.n2s); w.n2b = F(o.n2b);
+                w.qkv_b = F(o.qkv_b); w.proj_b = F(o.proj_b); w.fc1_b = F(o.fc1_b);
+                w.fc2_b = F(o.fc2_b); w.bias_mat = F(o.bias_mat);
+                w.qkv_w = H(o.qkv_w); w.proj_w = H(o.proj_w); w.fc1_w = H(o.fc1_w);
+                w.fc2_w = H(o.fc2_w);
+            }
+        for (int st = 0; st < 3; ++st) {
+            s->merge_s[st] = F(o_ms[st]); s->merge_b[st] = F(o_mb[st]);
+            s->merge_w[st] = H(o_mw[st]); s->out_s[st] = F(o_os[st]); s->out_b[st] = F(o_ob[st]);
+        }
+    }
+    {
+        size_t x_elems = 0, xn_elems = 0, big_elems = 0;
+        for (int st = 0; st < 4; ++st) {
+            const size_t t = batches * (size_t)s->h[st] * s->w[st];
+            x_elems = std::max(x_elems, t * kC[st]);
+            xn_elems = std::max(xn_elems, t * kC[st]);
+            big_elems = std::max(big_elems, t * 4 * kC[st]);
+            if (st < 3) {
+                const size_t t2 = batches * (size_t)s->h[st + 1] * s->w[st + 1];
+                xn_elems = std::max(xn_elems, t2 * 4 * kC[st]);
+                x_elems = std::max(x_elems, t2 * 2 * kC[st]);
+            }
+        }
+        const size_t x_bytes = (x_elems * 4 + 255) & ~size_t(255);
+        const size_t xn_bytes = (xn_elems * 2 + 255) & ~size_t(255);
+        const size_t big_bytes = (big_elems * 2 + 255) & ~size_t(255);
+        if (!hip_ok(hipMalloc(&s->acts, x_bytes + xn_bytes + big_bytes), error, cap,
+                    "allocate Swin activations"))
+            return 0;
+        s->x = (float *)s->acts;
+        s->xn = (bf16 *)(s->acts + x_bytes);
+        s->big = (bf16 *)(s->acts + x_bytes + xn_bytes);
+        s->resident_bytes += x_bytes + xn_bytes + big_bytes;
+    }
+    return 1;
+}
+
+extern "C" int bf_cuda_swin_create(const bf_model *model, size_t batches, size_t input_h,
+                                   size_t input_w, bf_cuda_swin **out, char *error, size_t cap) {
+    if (out) *out = nullptr;
+    if (!model || !out || !batches || !input_h || !input_w || (input_h % 4) || (input_w % 4) ||
+        batches > INT_MAX || input_h > INT_MAX || input_w > INT_MAX)
+        return fail(error, cap, "invalid HIP Swin contract");
+    // Stage-0 hidden activations ([tokens, 384]) must index within int range.
+    if ((unsigned long long)batches * (input_h / 4) * (input_w / 4) * 384ull > (unsigned long long)INT_MAX)
+        return fail(error, cap, "HIP Swin input is too large");
+    bf_cuda_swin *s = (bf_cuda_swin *)std::calloc(1, sizeof(*s));
+    if (!s) return fail(error, cap, "Swin host allocation failed");
+    if (!swin_build(s, model, batches, input_h, input_w, error, cap)) {
+        bf_cuda_swin_destroy(s);
+        return 0;
+    }
+    *out = s;
+    return 1;
+}
+
+extern "C" int bf_cuda_swin_forward(bf_cuda_swin *s, const float *images, float *out1,
+                                    float *out2, float *out3, void *stream_value, char *error,
+                                    size_t cap) {
+    if (!s || !images || !out1 || !out2 || !out3)
+        return fail(error, cap, "invalid HIP Swin buffers");
+    hipStream_t stream = reinterpret_cast<hipStream_t>(stream_value);
+    const int B = (int)s->batches;
+    float *outputs[3] = {out1, out2, out3};
+
+    // Patch embedding: 4x4/s4 conv 3->96 straight from NCHW images into NHWC
+    // tokens, then LayerNorm in place.
+    {
+        using T = Tile<128, 96, 32, 2, 2>;
+        ConvGeom g{};
+        g.N = B; g.Ci = 3; g.IH = (int)s->input_h; g.IW = (int)s->input_w;
+        g.OH = s->h[0]; g.OW = s->w[0]; g.KH = 4; g.KW = 4; g.SH = 4; g.SW = 4;
+        g.PH = 0; g.PW = 0; g.transpose = 0;
+        g.M = B * s->h[0] * s->w[0]; g.K = 48;
+        LoadConvA<T::BM, T::BK, T::kThreads, 4, 4, SrcNCHW> al{};
+        al.src = SrcNCHW{images, 3, g.IH, g.IW};
+        al.g = g;
+        LoadRowsBf16<T::BN, T::BK, T::kThreads> bl{s->patch_w, 48, 96, 48};
+        EpiRowsF32 epi{s->x, s->patch_b, 96, g.M, 96, 0};
+        launch_gemm<T>(al, bl, epi, g.M, 96, 48, stream);
+        launch_ln<float>(96, s->x, s->x, s->patch_ns, s->patch_nb, g.M, stream);
+    }
+
+    for (int st = 0; st < 4; ++st) {
+        const int C = kC[st], heads = kHeads[st], H = s->h[st], W = s->w[st];
+        const int T = B * H * W;
+        const int wy_n = (H + 6) / 7, wx_n = (W + 6) / 7;
+        const int items = B * wy_n * wx_n * heads;
+        for (int b = 0; b < kDepth[st]; ++b) {
+            const BlockW &w = s->blocks[st][b];
+            const int shift = (b & 1) ? 3 : 0;
+            launch_ln<bf16>(C, s->x, s->xn, w.n1s, w.n1b, T, stream);
+            linear_bf16(s->xn, w.qkv_w, T, 3 * C, C,
+                        EpiRowsBf16<false>{s->big, w.qkv_b, 3 * C, T, 3 * C}, stream);
+            hipLaunchKernelGGL(window_attention_kernel, dim3((items + kAttnWaves - 1) / kAttnWaves),
+                               dim3(64 * kAttnWaves), 0, stream, s->big, w.qkv_b, w.bias_mat,
+                               s->xn, H, W, C, heads, wy_n, wx_n, shift, items);
+            linear_bf16(s->xn, w.proj_w, T, C, C, EpiResidualF32{s->x, w.proj_b, C, T, C}, stream);
+            launch_ln<bf16>(C, s->x, s->xn, w.n2s, w.n2b, T, stream);
+            linear_bf16(s->xn, w.fc1_w, T, 4 * C, C,
+                        EpiRowsBf16<true>{s->big, w.fc1_b, 4 * C, T, 4 * C}, stream);
+            linear_bf16(s->big, w.fc2_w, T, C, 4 * C, EpiResidualF32{s->x, w.fc2_b, C, T, C},
+                        stream);
+        }
+        if (st > 0) launch_out_ln(C, s->x, outputs[st - 1], s->out_s[st - 1], s->out_b[st - 1], T, H * W, stream);
+        if (st < 3) {
+            const int T2 = B * s->h[st + 1] * s->w[st + 1];
+            launch_merge(C, s->x, s->xn, s->merge_s[st], s->merge_b[st], B, H, W, stream);
+            linear_bf16(s->xn, s->merge_w[st], T2, 2 * C, 4 * C,
+                        EpiRowsF32{s->x, nullptr, 2 * C, T2, 2 * C, 0}, stream);
+        }
+    }
+    return launch_ok(error, cap, "launch HIP Swin graph");
+}

@@ -1,0 +1,360 @@
+// Swin-T building blocks on gfx950: row LayerNorms, the patch-merge gather,
+// the stage-output LayerNorm with NHWC->NCHW store, and batched shifted-
+// window attention on MFMA.
+#pragma once
+
+#include "hip_common.h"
+
+namespace bfhip {
+
+// ------------------------------------------------------------ LayerNorm rows
+// Row layout of a C-channel LayerNorm across a wave: LPR lanes per row
+// (largest power of two <= 64 dividing C/4), PER float4 per lane.
+template <int C>
+struct RowLayout {
+    static constexpr int V4 = C / 4;
+    static constexpr int LPR = (V4 % 64 == 0) ? 64 : (V4 % 32 == 0) ? 32 : (V4 % 16 == 0) ? 16
+                             : (V4 % 8 == 0) ? 8 : (V4 % 4 == 0) ? 4 : (V4 % 2 == 0) ? 2 : 1;
+    static constexpr int PER = V4 / LPR;
+    static constexpr int RPW = kWave / LPR;
+    static_assert(C % 4 == 0, "channels must be a multiple of 4");
+};
+
+__device__ __forceinline__ void store4(float *p, float a, float b, float c, float d) {
+    *reinterpret_cast<float4 *>(p) = make_float4(a, b, c, d);
+}
+__device__ __forceinline__ void store4(bf16 *p, float a, float b, float c, float d) {
+    bf16x4 v;
+    v[0] = to_bf16(a); v[1] = to_bf16(b); v[2] = to_bf16(c); v[3] = to_bf16(d);
+    *reinterpret_cast<bf16x4 *>(p) = v;
+}
+
+// y = LN(x) * g + b over rows of C (eps 1e-5, two-pass statistics held in
+// registers).  In-place (y == x) is safe: a row is fully read before written.
+template <int C, typename OutT>
+__global__ __launch_bounds__(256) void ln_rows_kernel(const float *x, OutT *y, const float *g,
+                                                      const float *b, int rows) {
+    using L = RowLayout<C>;
+    const int lane = threadIdx.x & 63;
+    const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int sub = lane / L::LPR, li = lane % L::LPR;
+    const int row = wave * L::RPW + sub;
+    const bool ok = row < rows;
+    float4 v[L::PER];
+    float s = 0.0f;
+#pragma unroll
+    for (int p = 0; p < L::PER; ++p) {
+        v[p] = ok ? reinterpret_cast<const float4 *>(x + (size_t)row * C)[li + p * L::LPR]
+                  : make_float4(0.f, 0.f, 0.f, 0.f);
+        s += (v[p].x + v[p].y) + (v[p].z + v[p].w);
+    }
+    const float mean = group_sum<L::LPR>(s) * (1.0f / C);
+    float q = 0.0f;
+#pragma unroll
+    for (int p = 0; p < L::PER; ++p) {
+        const float a = v[p].x - mean, bb = v[p].y - mean, c = v[p].z - mean, d = v[p].w - mean;
+        q += (a * a + bb * bb) + (c * c + d * d);
+    }
+    const float rstd = rsqrtf(group_sum<L::LPR>(q) * (1.0f / C) + 1e-5f);
+    if (!ok) return;
+#pragma unroll
+    for (int p = 0; p < L::PER; ++p) {
+        const int c4 = (li + p * L::LPR) * 4;
+        const float4 gg = *reinterpret_cast<const float4 *>(g + c4);
+        const float4 bb = *reinterpret_cast<const float4 *>(b + c4);
+        store4(y + (size_t)row * C + c4, (v[p].x - mean) * rstd * gg.x + bb.x,
+               (v[p].y - mean) * rstd * gg.y + bb.y, (v[p].z - mean) * rstd * gg.z + bb.z,
+               (v[p].w - mean) * rstd * gg.w + bb.w);
+    }
+}
+
+// Patch merging: output row (n, oy, ox) is the 2x2 nn.Unfold of x[n,H,W,C]
+// with element order c*4 + ky*2 + kx (zero beyond odd edges; reference
+// swin_backbone.c:278-302, cuda_swin.cu:218-225), LayerNorm over 4C, bf16.
+template <int C>
+__global__ __launch_bounds__(256) void merge_ln_kernel(const float *x, bf16 *y, const float *g,
+                                                       const float *b, int batches, int H,
+                                                       int W) {
+    constexpr int LPR = (C % 64 == 0) ? 64 : 32;
+    constexpr int PER = C / LPR;  // channels per lane
+    constexpr int RPW = kWave / LPR;
+    const int lane = threadIdx.x & 63;
+    const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int sub = lane / LPR, li = lane % LPR;
+    const int H2 = (H + 1) / 2, W2 = (W + 1) / 2, rows = batches * H2 * W2;
+    const int row = wave * RPW + sub;
+    const bool ok = row < rows;
+    const int rr = ok ? row : 0;
+    const int n = rr / (H2 * W2), p2 = rr - n * H2 * W2, oy = p2 / W2, ox = p2 - oy * W2;
+    float v[PER][4];
+    float s = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int sy = 2 * oy + (q >> 1), sx = 2 * ox + (q & 1);
+        const bool in = ok && sy < H && sx < W;
+        const float *src = x + (((size_t)n * H + sy) * W + sx) * C;
+#pragma unroll
+        for (int p = 0; p < PER; ++p) {
+            v[p][q] = in ? src[li + p * LPR] : 0.0f;
+            s += v[p][q];
+        }
+    }
+    const float mean = group_sum<LPR>(s) * (1.0f / (4 * C));
+    float sq = 0.0f;
+#pragma unroll
+    for (int p = 0; p < PER; ++p)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) sq += (v[p][q] - mean) * (v[p][q] - mean);
+    const float rstd = rsqrtf(group_sum<LPR>(sq) * (1.0f / (4 * C)) + 1e-5f);
+    if (!ok) return;
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+        const int e = (li + p * LPR) * 4;
+        const float4 gg = *reinterpret_cast<const float4 *>(g + e);
+        const float4 bb = *reinterpret_cast<const float4 *>(b + e);
+        store4(y + (size_t)row * 4 * C + e, (v[p][0] - mean) * rstd * gg.x + bb.x,
+               (v[p][1] - mean) * rstd * gg.y + bb.y, (v[p][2] - mean) * rstd * gg.z + bb.z,
+               (v[p][3] - mean) * rstd * gg.w + bb.w);
+    }
+}
+
+// Stage output: LayerNorm over C of tokens [n, HW, C], stored NCHW.  A block
+// normalises 16 consecutive tokens into LDS, then writes 16-token runs of each
+// channel plane (reference store_output, swin_backbone.c:265-276).
+template <int C>
+__global__ __launch_bounds__(256) void out_ln_kernel(const float *x, float *out, const float *g,
+                                                     const float *b, int rows, int hw) {
+    using L = RowLayout<C>;
+    constexpr int kRows = 16;
+    __shared__ float tile[C * (kRows + 1)];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sub = lane / L::LPR, li = lane % L::LPR;
+    const int row0 = blockIdx.x * kRows;
+    // `base` is uniform across the wave, so every lane group runs the same
+    // number of iterations and its shuffles see only active lanes.
+    for (int base = wave * L::RPW; base < kRows; base += 4 * L::RPW) {
+        const int r = base + sub, row = row0 + r;
+        const bool ok = row < rows && r < kRows;
+        float4 v[L::PER];
+        float s = 0.0f;
+#pragma unroll
+        for (int p = 0; p < L::PER; ++p) {
+            v[p] = ok ? reinterpret_cast<const float4 *>(x + (size_t)row * C)[li + p * L::LPR]
+                      : make_float4(0.f, 0.f, 0.f, 0.f);
+            s += (v[p].x + v[p].y) + (v[p].z + v[p].w);
+        }
+        const float mean = group_sum<L::LPR>(s) * (1.0f / C);
+        float q = 0.0f;
+#pragma unroll
+        for (int p = 0; p < L::PER; ++p) {
+            const float a = v[p].x - mean, bb = v[p].y - mean, c = v[p].z - mean,
+                        d = v[p].w - mean;
+            q += (a * a + bb * bb) + (c * c + d * d);
+        }
+        const float rstd = rsqrtf(group_sum<L::LPR>(q) * (1.0f / C) + 1e-5f);
+        if (r < kRows) {
+#pragma unroll
+            for (int p = 0; p < L::PER; ++p) {
+                const int c4 = (li + p * L::LPR) * 4;
+                tile[(c4 + 0) * (kRows + 1) + r] = (v[p].x - mean) * rstd * g[c4 + 0] + b[c4 + 0];
+                tile[(c4 + 1) * (kRows + 1) + r] = (v[p].y - mean) * rstd * g[c4 + 1] + b[c4 + 1];
+                tile[(c4 + 2) * (kRows + 1) + r] = (v[p].z - mean) * rstd * g[c4 + 2] + b[c4 + 2];
+                tile[(c4 + 3) * (kRows + 1) + r] = (v[p].w - mean) * rstd * g[c4 + 3] + b[c4 + 3];
+            }
+        }
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < C * kRows; e += blockDim.x) {
+        const int c = e / kRows, r = e - c * kRows, row = row0 + r;
+        if (row >= rows) continue;
+        const int n = row / hw, p = row - n * hw;
+        out[((size_t)n * C + c) * hw + p] = tile[c * (kRows + 1) + r];
+    }
+}
+
+// ------------------------------------------------------- window attention
+// Window token t of window (n, wy, wx) reads padded, cyclically shifted source
+// ((wy*7 + t/7 + shift) mod Hp, (wx*7 + t%7 + shift) mod Wp) (reference
+// gather_windows_kernel cuda_swin.cu:120-131, cyclic_source swin.c:106-110).
+// Returns the token row, -1 for a zero-padded source (q/k/v = qkv bias), -2
+// for the MFMA padding rows t >= 49.
+__device__ __forceinline__ int window_token(int t, int n, int wy, int wx, int H, int W, int Hp,
+                                            int Wp, int shift) {
+    if (t >= 49) return -2;
+    const int py = wy * 7 + t / 7, px = wx * 7 + t % 7;
+    const int sy = shift ? (py + shift) % Hp : py, sx = shift ? (px + shift) % Wp : px;
+    return (sy < H && sx < W) ? (n * H + sy) * W + sx : -1;
+}
+
+// Shifted-window region label 3*ry + rx of padded position (py, px)
+// (reference mask_region, swin.c:112-117; cuda_swin.cu:132-134).
+__device__ __forceinline__ int window_label(int t, int wy, int wx, int Hp, int Wp, int shift) {
+    const int py = wy * 7 + t / 7, px = wx * 7 + t % 7;
+    const int ry = py < Hp - 7 ? 0 : (py < Hp - shift ? 1 : 2);
+    const int rx = px < Wp - 7 ? 0 : (px < Wp - shift ? 1 : 2);
+    return 3 * ry + rx;
+}
+
+// One wave64 per (window, head) with head dim 32: Q, K (rows) and V^T are
+// staged in LDS as bf16 with the 49 tokens padded to 64; S^T = K Q^T is 16
+// MFMAs, the fp32 softmax over keys runs on the accumulator registers (the
+// 64 keys of a query sit in 16 registers x 4 lanes), and O^T = V^T P^T takes
+// P straight from those registers as the B operand (the key order of the
+// k-slots is a permutation shared by both operands).  Scores are
+// q.k/sqrt(32) + rel_bias[h][i][j] (- 100 across shifted regions); keys
+// t >= 49 are excluded.  Outputs go back to the token rows they came from.
+constexpr int kAttnWaves = 4;
+
+__global__ __launch_bounds__(256) void window_attention_kernel(
+    const bf16 *__restrict__ qkv, const float *__restrict__ qkv_bias,
+    const float *__restrict__ bias_mat, bf16 *__restrict__ out, int H, int W, int C, int heads,
+    int wy_n, int wx_n, int shift, int items) {
+    constexpr int QS = 40;  // LDS row stride of Q/K (bf16)
+    constexpr int VS = 72;  // LDS row stride of V^T (bf16)
+    __shared__ __attribute__((aligned(16))) bf16 sQ[kAttnWaves][64 * QS];
+    __shared__ __attribute__((aligned(16))) bf16 sK[kAttnWaves][64 * QS];
+    __shared__ __attribute__((aligned(16))) bf16 sV[kAttnWaves][32 * VS];
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int item = blockIdx.x * kAttnWaves + wave;
+    const bool active = item < items;
+    const int it = active ? item : 0;
+    const int h = it % heads, win = it / heads;
+    const int wx = win % wx_n, t1 = win / wx_n, wy = t1 % wy_n, n = t1 / wy_n;
+    const int Hp = wy_n * 7, Wp = wx_n * 7;
+    const size_t ld = 3 * (size_t)C;
+
+    bf16 *Q = sQ[wave], *K = sK[wave], *Vt = sV[wave];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int slot = lane + 64 * i, row = slot >> 2, ch = slot & 3;
+        const int tok = active ? window_token(row, n, wy, wx, H, W, Hp, Wp, shift) : -2;
+        bf16x8 q = {}, k = {}, v = {};
+        if (tok >= 0) {
+            const bf16 *src = qkv + (size_t)tok * ld + h * 32 + ch * 8;
+            q = *reinterpret_cast<const bf16x8 *>(src);
+            k = *reinterpret_cast<const bf16x8 *>(src + C);
+            v = *reinterpret_cast<const bf16x8 *>(src + 2 * C);
+        } else if (tok == -1) {
+            const float *bq = qkv_bias + h * 32 + ch * 8;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                q[e] = to_bf16(bq[e]);
+                k[e] = to_bf16(bq[C + e]);
+                v[e] = to_bf16(bq[2 * C + e]);
+            }
+        }
+        *reinterpret_cast<bf16x8 *>(Q + row * QS + ch * 8) = q;
+        *reinterpret_cast<bf16x8 *>(K + row * QS + ch * 8) = k;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) Vt[(ch * 8 + e) * VS + row] = v[e];
+    }
+    __syncthreads();
+    if (!active) return;
+
+    const int l16 = lane & 15, g = lane >> 4;
+    // S^T[j][i] blocks: s[jb][ib][e] = S[i = 16ib + l16][j = 16jb + 4g + e].
+    f32x4 s[4][4];
+    {
+        bf16x8 kf[4], qf[4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            kf[b] = *reinterpret_cast<const bf16x8 *>(K + (16 * b + l16) * QS + 8 * g);
+            qf[b] = *reinterpret_cast<const bf16x8 *>(Q + (16 * b + l16) * QS + 8 * g);
+        }
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+            for (int ib = 0; ib < 4; ++ib) s[jb][ib] = mfma16(kf[jb], qf[ib], f32x4{0, 0, 0, 0});
+    }
+
+    const float scale = 0.17677669529663687f;  // 1/sqrt(32)
+    const float *bm = bias_mat + (size_t)h * 49 * 49;
+    int lab_j[4][4];
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int j = 16 * jb + 4 * g + e;
+            lab_j[jb][e] = shift && j < 49 ? window_label(j, wy, wx, Hp, Wp, shift) : 0;
+        }
+    float inv[4];
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib) {
+        const int i = 16 * ib + l16;
+        const int lab_i = shift && i < 49 ? window_label(i, wy, wx, Hp, Wp, shift) : 0;
+        float m = -INFINITY;
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int j = 16 * jb + 4 * g + e;
+                float v = -INFINITY;
+                if (j < 49) {
+                    v = s[jb][ib][e] * scale + (i < 49 ? bm[i * 49 + j] : 0.0f);
+                    if (lab_i != lab_j[jb][e]) v -= 100.0f;
+                }
+                s[jb][ib][e] = v;
+                m = fmaxf(m, v);
+            }
+        m = fmaxf(m, __shfl_xor(m, 16));
+        m = fmaxf(m, __shfl_xor(m, 32));
+        float sum = 0.0f;
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float p = __expf(s[jb][ib][e] - m);
+                s[jb][ib][e] = p;
+                sum += p;
+            }
+        sum += __shfl_xor(sum, 16);
+        sum += __shfl_xor(sum, 32);
+        inv[ib] = 1.0f / sum;
+    }
+
+    // O^T = V^T P^T over two 32-key chunks; k-slot e of lane group g is key
+    // 32c + 16*(e>>2) + 4g + (e&3) in both operands.
+    f32x4 o[2][4];
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int ib = 0; ib < 4; ++ib) o[db][ib] = f32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        bf16x8 pf[4], vf[2];
+#pragma unroll
+        for (int ib = 0; ib < 4; ++ib)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) pf[ib][e] = to_bf16(s[2 * c + (e >> 2)][ib][e & 3]);
+#pragma unroll
+        for (int db = 0; db < 2; ++db) {
+            const bf16 *r = Vt + (16 * db + l16) * VS + 32 * c + 4 * g;
+            const bf16x4 lo = *reinterpret_cast<const bf16x4 *>(r);
+            const bf16x4 hi = *reinterpret_cast<const bf16x4 *>(r + 16);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                vf[db][e] = lo[e];
+                vf[db][4 + e] = hi[e];
+            }
+        }
+#pragma unroll
+        for (int db = 0; db < 2; ++db)
+#pragma unroll
+            for (int ib = 0; ib < 4; ++ib) o[db][ib] = mfma16(vf[db], pf[ib], o[db][ib]);
+    }
+    // o[db][ib][e] = O[i = 16ib + l16][d = 16db + 4g + e] (unnormalised).
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib) {
+        const int i = 16 * ib + l16;
+        const int tok = window_token(i, n, wy, wx, H, W, Hp, Wp, shift);
+        if (tok < 0) continue;
+        bf16 *dst = out + (size_t)tok * C + h * 32 + 4 * g;
+#pragma unroll
+        for (int db = 0; db < 2; ++db)
+            store4(dst + 16 * db, o[db][ib][0] * inv[ib], o[db][ib][1] * inv[ib],
+                   o[db][ib][2] * inv[ib], o[db][ib][3] * inv[ib]);
+    }
+}
+
+}  // namespace bfhip
