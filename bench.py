@@ -1,0 +1,306 @@
+#!/usr/bin/env python3
+"""Benchmark: 6-camera 256x704 Swin-T + FPN + depth-head forward on one MI355X.
+
+Workload (the config the metric is quoted on):
+images [6,3,256,704] U[0,1] ImageNet-normalised and dense depth [6,1,256,704]
+|N(0,1)|, 20 distinct frames (seeds 0-19) resident in HBM; random-init
+weights ~N(0,0.02) under the checkpoint's tensor names (no network for the
+real checkpoint).  One step = bf_cuda_swin_forward + bf_cuda_camera_neck_forward
+(the reference runtime's camera calls, src/cuda_runtime.cu:74), replayed from
+a HIP graph.  The timed region is bracketed by torch.cuda.synchronize().
+
+Prints one JSON line with ms/frame, achieved TFLOP/s (304.4 GFLOP/frame), the
+dominant kernel's roofline (timed live with HIP events) and the CPU baseline
+(the reference's own CPU path, OpenMP, on this host's cores).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import pathlib
+import sys
+import tempfile
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "bevfusion.c_amd"))
+
+# Algorithmic work per frame (6 cameras): GEMM flops 2*M*N*K with window rows
+# including padding tokens; see DESIGN.md "Measurement".
+GFLOP_FRAME = 304.4
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_HBM_GBS = 8000.0
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--no-graph", action="store_true", help="launch eagerly instead of a HIP graph")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--cpu-cameras", type=int, default=2,
+                   help="cameras in the bounded CPU-baseline sample")
+    p.add_argument("--no-roofline", action="store_true", help="skip per-kernel timing")
+    p.add_argument("--kernel-reps", type=int, default=20,
+                   help="HIP-event timed launches per kernel in the roofline leg")
+    return p.parse_args()
+
+
+def frame_flops():
+    """Algorithmic FLOPs of one frame, recomputed from the graph shapes."""
+    b = 6
+    total = 0.0
+    dims = [(64, 176), (32, 88), (16, 44), (8, 22)]
+    for s, (c, d, heads) in enumerate(zip((96, 192, 384, 768), (2, 2, 6, 2), (3, 6, 12, 24))):
+        h, w = dims[s]
+        tok = b * h * w
+        win_rows = b * ((h + 6) // 7) * ((w + 6) // 7) * 49
+        per_block = (2 * win_rows * c * 3 * c + 2 * win_rows * c * c          # qkv, proj
+                     + 2 * 2 * win_rows * 49 * c                              # QK^T, AV
+                     + 2 * 2 * tok * c * 4 * c)                               # fc1, fc2
+        total += d * per_block
+        if s < 3:
+            h2, w2 = dims[s + 1]
+            total += 2 * b * h2 * w2 * 4 * c * 2 * c                         # merge
+    total += 2 * b * 64 * 176 * 96 * 48                                      # patch embed
+    h, w = 32, 88
+    convs = [(16, 44, 1152, 256, 1), (16, 44, 256, 256, 3), (h, w, 448, 256, 1),
+             (h, w, 256, 256, 3), (256, 704, 1, 8, 1), (64, 176, 8, 32, 5), (h, w, 32, 64, 5),
+             (h, w, 320, 256, 3), (h, w, 256, 256, 3), (h, w, 256, 198, 1)]
+    for oh, ow, ci, co, k in convs:
+        total += 2 * b * oh * ow * co * ci * k * k
+    return total
+
+
+SWIN_STAGES = [(64, 176, 96, 3, 2), (32, 88, 192, 6, 2), (16, 44, 384, 12, 6),
+               (8, 22, 768, 24, 2)]
+NECK_LAYERS = {  # layer index: (name, M pixels, Ci, Co, k, input pixels)
+    0: ("fpn.lateral1", 6 * 16 * 44, 1152, 256, 1, 6 * 16 * 44),
+    1: ("fpn.output1", 6 * 16 * 44, 256, 256, 3, 6 * 16 * 44),
+    2: ("fpn.lateral0", 6 * 32 * 88, 448, 256, 1, 6 * 32 * 88),
+    3: ("fpn.output0", 6 * 32 * 88, 256, 256, 3, 6 * 32 * 88),
+    5: ("depth.dtransform6", 6 * 32 * 88, 32, 64, 5, 6 * 64 * 176),
+    6: ("depth.depthnet0", 6 * 32 * 88, 320, 256, 3, 6 * 32 * 88),
+    7: ("depth.depthnet3", 6 * 32 * 88, 256, 256, 3, 6 * 32 * 88),
+}
+
+
+def swin_op_cost(stage, op, b=6):
+    """Algorithmic FLOPs and HBM bytes of one launch of a Swin op: GEMM flops
+    2*M*N*K over the tokens the kernel computes; bytes = every operand read
+    once and every result written once at its stored width (bf16 activations
+    and weights, fp32 residual stream)."""
+    h, w, c, heads, _ = SWIN_STAGES[stage]
+    t = b * h * w
+    win = b * ((h + 6) // 7) * ((w + 6) // 7)
+    if op in ("ln1", "ln2"):
+        return 8.0 * t * c, t * c * 4 + t * c * 2 + 8 * c
+    if op == "qkv":
+        return 2.0 * t * c * 3 * c, t * c * 2 + 3 * c * c * 2 + t * 3 * c * 2
+    if op == "attention":
+        return 4.0 * win * 49 * 49 * c, t * 3 * c * 2 + t * c * 2 + heads * 49 * 49 * 4
+    if op == "proj":
+        return 2.0 * t * c * c, t * c * 2 + c * c * 2 + 2 * t * c * 4
+    if op == "fc1":
+        return 2.0 * t * c * 4 * c, t * c * 2 + 4 * c * c * 2 + t * 4 * c * 2
+    if op == "fc2":
+        return 2.0 * t * 4 * c * c, t * 4 * c * 2 + 4 * c * c * 2 + 2 * t * c * 4
+    if op == "merge":
+        h2, w2 = SWIN_STAGES[stage + 1][:2]
+        t2 = b * h2 * w2
+        return 2.0 * t2 * 4 * c * 2 * c, t * c * 4 + 2 * t2 * 4 * c * 2 + 8 * c * c * 2 + t2 * 2 * c * 4
+    raise ValueError(op)
+
+
+def neck_layer_cost(layer):
+    name, m, ci, co, k, m_in = NECK_LAYERS[layer]
+    return 2.0 * m * co * ci * k * k, m_in * ci * 2 + co * ci * k * k * 2 + m * co * 2
+
+
+def roofline_entry(name, avg_s, per_frame, flops, nbytes):
+    ai = flops / nbytes
+    ridge = PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
+    if ai >= ridge:
+        achieved, peak, unit, bound = flops / avg_s / 1e12, PEAK_BF16_TFLOPS, "TFLOP/s", "mfma"
+    else:
+        achieved, peak, unit, bound = nbytes / avg_s / 1e9, PEAK_HBM_GBS, "GB/s", "hbm"
+    return {"kernel": name, "bound": bound, "achieved": round(achieved, 1), "peak": peak,
+            "unit": unit, "frac": round(achieved / peak, 4), "traffic": None,
+            "avg_us": round(avg_s * 1e6, 2), "launches_per_frame": per_frame,
+            "us_per_frame": round(avg_s * 1e6 * per_frame, 1),
+            "flops_per_launch": flops, "bytes_per_launch": nbytes,
+            "tflops": round(flops / avg_s / 1e12, 1), "gbs": round(nbytes / avg_s / 1e9, 1)}
+
+
+def time_kernels(swin, neck, stream, reps=20):
+    """Time single ops of the path with HIP events on the stream they are
+    launched on; returns roofline entries sorted by time per frame."""
+    import torch
+    cands = []
+    for st in range(4):
+        depth = SWIN_STAGES[st][4]
+        for op in ("ln1", "qkv", "attention", "proj", "ln2", "fc1", "fc2"):
+            cands.append((f"swin.s{st}.{op}", lambda st=st, op=op: swin.profile_op(st, 0, op, stream),
+                          depth, swin_op_cost(st, op)))
+        if st < 3:
+            cands.append((f"swin.s{st}.merge", lambda st=st: swin.profile_op(st, 0, "merge", stream),
+                          1, swin_op_cost(st, "merge")))
+    for layer, (name, *_rest) in NECK_LAYERS.items():
+        cands.append((f"neck.{name}", lambda layer=layer: neck.profile_layer(layer, stream), 1,
+                      neck_layer_cost(layer)))
+    out = []
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for name, fn, per_frame, (flops, nbytes) in cands:
+        for _ in range(3):
+            fn()
+        start.record(stream)
+        for _ in range(reps):
+            fn()
+        stop.record(stream)
+        stop.synchronize()
+        avg_s = start.elapsed_time(stop) / 1e3 / reps
+        out.append(roofline_entry(name, avg_s, per_frame, flops, nbytes))
+    out.sort(key=lambda e: -e["us_per_frame"])
+    return out
+
+
+def cpu_baseline(model_path, cameras):
+    """Reference CPU path (oracle/_ref, the reference's C compiled from its own
+    sources, OpenMP) on a bounded sample of `cameras` cameras, scaled to a
+    6-camera frame.  Falls back to the restatement if _ref is absent."""
+    import numpy as np
+    import oracle
+    from bfhip import bfw
+    kind = "reference" if oracle.available("ref") else "port"
+    o = oracle.Oracle("ref" if kind == "reference" else "port")
+    images = bfw.synthetic_images(0, cameras, 256, 704)
+    depth = bfw.synthetic_depth(0, cameras, 256, 704)
+    with o.open_model(model_path) as m:
+        t0 = time.perf_counter()
+        s0, s1, s2 = o.swin_backbone(m, images)
+        t1 = time.perf_counter()
+        f0, _ = o.image_fpn(m, s0, s1, s2)
+        o.depth_head(m, f0, depth)
+        t2 = time.perf_counter()
+    per_frame_ms = (t2 - t0) * 1e3 * 6 / cameras
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or os.cpu_count()
+    return {"value": round(per_frame_ms, 1), "unit": "ms/frame", "cores": threads,
+            "kind": kind, "backend": o.backend(),
+            "sample": f"{cameras} of 6 cameras, Swin-T + FPN + depth head at 256x704 "
+                      f"(swin {1e3 * (t1 - t0):.0f} ms, neck {1e3 * (t2 - t1):.0f} ms), "
+                      f"scaled x{6 / cameras:g}",
+            "cpu_model": _cpu_model()}
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; the path shards per camera "
+                                   "across GPUs by design (DESIGN.md) but no multi-GPU run is "
+                                   "part of it", "n_gpus": args.gpus}))
+        sys.exit(2)
+    import numpy as np
+    import torch
+    import bfhip
+    from bfhip import bfw
+
+    dev = torch.device("cuda:0")
+    tmp = pathlib.Path(tempfile.mkdtemp(prefix="bench_"))
+    model_path = bfw.write_camera_branch(tmp / "camera_branch.bfw", seed=0, mode="baseline")
+    with bfhip.Model(model_path) as m:
+        swin = bfhip.Swin(m, 6, 256, 704)
+        neck = bfhip.CameraNeck(m, 6, 32, 88, 360, 360)
+
+    frames = 20
+    imgs = [torch.from_numpy(bfw.synthetic_images(s, 6, 256, 704)).to(dev) for s in range(frames)]
+    deps = [torch.from_numpy(bfw.synthetic_depth(s, 6, 256, 704)).to(dev) for s in range(frames)]
+    img_in = torch.empty_like(imgs[0])
+    dep_in = torch.empty_like(deps[0])
+    outs = [torch.empty(s, device=dev) for s in swin.output_shapes()]
+    logits = torch.empty((6, 118, 32, 88), device=dev)
+    ctx = torch.empty((6, 80, 32, 88), device=dev)
+
+    def step():
+        swin.forward(img_in, outs)
+        neck.neck_forward(*outs, dep_in, logits, ctx)
+
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        img_in.copy_(imgs[0]); dep_in.copy_(deps[0])
+        step()
+        torch.cuda.synchronize()
+        eager = (logits.clone(), ctx.clone())
+        graph = None
+        if not args.no_graph:
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                step()
+            graph.replay()
+            torch.cuda.synchronize()
+            if not (torch.equal(eager[0], logits) and torch.equal(eager[1], ctx)):
+                raise SystemExit("graph replay differs from eager forward")
+        run = graph.replay if graph is not None else step
+
+        for i in range(args.warmup):
+            img_in.copy_(imgs[i % frames]); dep_in.copy_(deps[i % frames])
+            run()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(args.steps):
+            img_in.copy_(imgs[i % frames]); dep_in.copy_(deps[i % frames])
+            run()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+    ms = (t1 - t0) * 1e3 / args.steps
+    gflop = frame_flops() / 1e9
+    tflops = gflop / ms
+
+    result = {
+        "metric": "GEMM TFLOP/s (% bf16 MFMA peak); 6-cam Swin-T+FPN+depth ms/frame",
+        "value": round(ms, 4),
+        "unit": "ms/frame",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (images U[0,1] ImageNet-normalised, dense depth |N(0,1)|, "
+                "random-init weights N(0,0.02), seeds 0-19)",
+        "config": {"workload": "BASELINE config 5: 6x3x256x704 images -> Swin-T -> FPN -> "
+                               "depth head (118 bins + 80 ctx), one frame per step",
+                   "cameras": 6, "image_hw": [256, 704], "graph": graph is not None},
+        "tflops": round(tflops, 2),
+        "gflop_per_frame": round(gflop, 1),
+        "frac_bf16_peak": round(tflops / PEAK_BF16_TFLOPS, 4),
+        "frames_per_s": round(1e3 / ms, 1),
+    }
+    if not args.no_roofline:
+        with torch.cuda.stream(stream):
+            kernels = time_kernels(swin, neck, stream, args.kernel_reps)
+        result["roofline"] = kernels[0]
+        result["kernels"] = [{k: e[k] for k in ("kernel", "bound", "frac", "avg_us",
+                                                  "us_per_frame", "tflops", "gbs")}
+                             for e in kernels[:12]]
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(model_path, args.cpu_cameras)
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

@@ -49,7 +49,11 @@ SIGNATURES = {
     "bf_cuda_camera_neck_forward": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                          C.c_char_p, _sz]),
     "bf_cuda_camera_downsample_forward": (_i, [_vp, _vp, _vp, _vp, C.c_char_p, _sz]),
+    "bfhip_swin_profile_op": (_i, [_vp, _i, _i, _i, _vp, C.c_char_p, _sz]),
+    "bfhip_camera_profile_layer": (_i, [_vp, _i, _vp, C.c_char_p, _sz]),
 }
+
+SWIN_OPS = ("ln1", "qkv", "attention", "proj", "ln2", "fc1", "fc2", "merge")
 
 MODEL_SIGNATURES = {
     "bf_model_open": (_i, [C.c_char_p, C.POINTER(_vp), C.c_char_p, _sz]),
@@ -238,6 +242,13 @@ class Swin:
                "bf_cuda_swin_forward")
         return outs
 
+    def profile_op(self, stage, block, op, stream=None):
+        """Enqueue one op's kernels (include/bfhip_profile.h)."""
+        err = _err()
+        _check(self.lib.bfhip_swin_profile_op(self.handle, stage, block, SWIN_OPS.index(op),
+                                              _stream(stream), err, 512), err,
+               "bfhip_swin_profile_op")
+
     def close(self):
         if self.handle:
             self.lib.bf_cuda_swin_destroy(self.handle)
@@ -309,6 +320,12 @@ class CameraNeck:
                                                           _stream(stream), err, 512), err,
                "bf_cuda_camera_downsample_forward")
         return out
+
+    def profile_layer(self, layer, stream=None):
+        """Enqueue one convolution layer (include/bfhip_profile.h)."""
+        err = _err()
+        _check(self.lib.bfhip_camera_profile_layer(self.handle, layer, _stream(stream), err, 512),
+               err, "bfhip_camera_profile_layer")
 
     def close(self):
         if self.handle:

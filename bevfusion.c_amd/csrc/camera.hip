@@ -1,16 +1,19 @@
 // Camera neck context: GeneralizedLSSFPN + DepthLSS head + post-LSS
 // downsample (drop-in for reference src/cuda_camera.cu).
 //
-// Every convolution is an implicit GEMM on the bf16 MFMA core with BN folded
-// into bf16 weights and an fp32 bias at create.  The reference's glue passes
-// become operand gathers or epilogues, so no concat / upsample / split /
-// transpose buffer exists:
+// Every convolution is a channels-last implicit GEMM on the bf16 MFMA core with
+// BN folded into bf16 [Co][KH][KW][Ci] weights and an fp32 bias at create.
+// Boundary maps (NCHW fp32 by the ABI) are packed to NHWC bf16 once; every
+// intermediate stays NHWC bf16.  The reference's glue passes become operand
+// gathers or epilogues, so no concat / upsample / split / transpose buffer
+// exists:
 //   lateral 1x1 convs read concat(lower, bilinear-up(upper)) taps directly;
 //   dtransform.0 (1x1, 1->8) is evaluated inside dtransform.3's gather;
 //   depthnet.0 reads concat(dtransform out, fpn0) taps directly;
 //   depthnet.6 stores logits / context from its epilogue;
 //   the last downsample conv stores the x/y-transposed map.
 #include "bf_cuda_camera.h"
+#include "bfhip_profile.h"
 #include "conv_core.h"
 #include "host_util.h"
 
@@ -40,13 +43,16 @@ struct bf_cuda_camera_neck {
     unsigned char *params, *acts;
     ConvLayer L[kLayers];
     const float *dt0_w, *dt0_b;  // dtransform.0 folded, fused into dtransform.3
-    float *t1, *fpn1, *t0, *fpn0, *e1, *e2, *d0, *d1, *bev0, *bev1;
+    // Channels-last bf16 maps: packed Swin levels, FPN laterals / outputs,
+    // depth encoder, depth trunk, packed BEV and downsample intermediates.
+    bf16 *p0, *p1, *p2, *t1, *f1, *t0, *f0, *e1, *e2, *d0, *d1, *bp, *b0, *b1;
 };
 
 namespace {
 
 // Binds conv (+ optional bias, + optional BN), folds BN in fp32 exactly as the
-// reference (cuda_camera.cu:116-122), and returns folded weight/bias on host.
+// reference (cuda_camera.cu:116-122) and returns the folded weights permuted
+// to [Co][KH][KW][Ci] (channels-last reduction order) plus the fp32 bias.
 int fold_conv(const bf_model *m, const char *wname, const char *bname, const char *bn,
               int ci, int co, int k, std::vector<float> &w, std::vector<float> &b,
               char *error, size_t cap) {
@@ -54,7 +60,7 @@ int fold_conv(const bf_model *m, const char *wname, const char *bname, const cha
     const float *src = bind_f32(m, wname, {uco, uci, uk, uk}, error, cap);
     if (!src) return 0;
     const size_t span = (size_t)ci * k * k;
-    w.assign(src, src + span * co);
+    std::vector<float> folded(src, src + span * co);
     b.assign(co, 0.0f);
     if (bname) {
         const float *sb = bind_f32(m, bname, {uco}, error, cap);
@@ -72,9 +78,14 @@ int fold_conv(const bf_model *m, const char *wname, const char *bname, const cha
         for (int o = 0; o < co; ++o) {
             const float f = p[0][o] / std::sqrt(p[3][o] + 1e-5f);
             b[o] = (b[o] - p[2][o]) * f + p[1][o];
-            for (size_t i = 0; i < span; ++i) w[(size_t)o * span + i] *= f;
+            for (size_t i = 0; i < span; ++i) folded[(size_t)o * span + i] *= f;
         }
     }
+    w.resize(span * co);
+    for (int o = 0; o < co; ++o)
+        for (int c = 0; c < ci; ++c)
+            for (int t = 0; t < k * k; ++t)
+                w[((size_t)o * k * k + t) * ci + c] = folded[((size_t)o * ci + c) * k * k + t];
     return 1;
 }
 
@@ -91,53 +102,63 @@ ConvGeom geom_of(const ConvLayer &l) {
 template <class T, int KH, int KW, class Src, class Epi>
 void run_conv(const ConvLayer &l, const Src &src, const Epi &epi, hipStream_t s) {
     const ConvGeom g = geom_of(l);
-    LoadConvA<T::BM, T::BK, T::kThreads, KH, KW, Src> al{};
+    LoadConvNHWC<T::BM, T::BK, T::kThreads, KH, KW, Src> al{};
     al.src = src;
     al.g = g;
     LoadRowsBf16<T::BN, T::BK, T::kThreads> bl{l.w, g.K, l.co, g.K};
     launch_gemm<T>(al, bl, epi, g.M, l.co, g.K, s);
 }
 
-using T256 = Tile<64, 128, 64, 2, 2>;   // 256 / 198 output channels
+// Tiles from a sweep of the GEMM core on these shapes (MI355X): 128 x 128 for
+// the 256-channel maps at 32x88, 64 x 64 where M is small (level 1, 16x44,
+// and dtransform.6), narrow tiles for the 32 / 80-channel layers.
+using T256 = Tile<128, 128, 64, 2, 2>;  // 256 / 198 output channels at level 0
+using T64 = Tile<64, 64, 64, 2, 2>;     // level-1 convs and dtransform.6
 using T32 = Tile<128, 32, 32, 4, 1>;    // dtransform.3: 32 channels
-using T64 = Tile<64, 64, 64, 2, 2>;     // dtransform.6: 64 channels
 using T80 = Tile<64, 80, 64, 2, 1>;     // downsample: 80 channels
 
-EpiNCHW nchw(const ConvLayer &l, float *out, int relu = 1) {
-    return EpiNCHW{out, l.b, l.n * l.oh * l.ow, l.co, l.oh * l.ow, relu};
+EpiConvOut out_to(const ConvLayer &l, bf16 *nhwc, float *nchw = nullptr) {
+    return EpiConvOut{nhwc, nchw, l.b, l.n * l.oh * l.ow, l.co, l.oh * l.ow, 1};
 }
 
+// FPN from NCHW fp32 Swin levels; FPN levels land channels-last in f0/f1 and,
+// when requested, also NCHW fp32 in out0/out1.
 void fpn_impl(bf_cuda_camera_neck *n, const float *s0, const float *s1, const float *s2,
               float *out0, float *out1, hipStream_t s) {
     const int B = (int)n->batches;
     const int h = (int)n->h, w = (int)n->w, h1 = (int)n->h1, w1 = (int)n->w1;
     const int h2 = (int)n->h2, w2 = (int)n->w2;
-    SrcUpConcat up1{s1, s2, 384, 768, h1, w1, h2, w2};
-    run_conv<T256, 1, 1>(n->L[kLat1], up1, nchw(n->L[kLat1], n->t1), s);
-    run_conv<T256, 3, 3>(n->L[kFpn1], SrcNCHW{n->t1, 256, h1, w1}, nchw(n->L[kFpn1], out1), s);
-    SrcUpConcat up0{s0, out1, 192, 256, h, w, h1, w1};
-    run_conv<T256, 1, 1>(n->L[kLat0], up0, nchw(n->L[kLat0], n->t0), s);
-    run_conv<T256, 3, 3>(n->L[kFpn0], SrcNCHW{n->t0, 256, h, w}, nchw(n->L[kFpn0], out0), s);
-    (void)B;
+    pack_nhwc(s0, n->p0, B, 192, h * w, s);
+    pack_nhwc(s1, n->p1, B, 384, h1 * w1, s);
+    pack_nhwc(s2, n->p2, B, 768, h2 * w2, s);
+    run_conv<T64, 1, 1>(n->L[kLat1], SrcNHWCUpConcat{n->p1, n->p2, 384, 768, h1, w1, h2, w2},
+                        out_to(n->L[kLat1], n->t1), s);
+    run_conv<T64, 3, 3>(n->L[kFpn1], SrcNHWC{n->t1, 256, h1, w1},
+                        out_to(n->L[kFpn1], n->f1, out1), s);
+    run_conv<T256, 1, 1>(n->L[kLat0], SrcNHWCUpConcat{n->p0, n->f1, 192, 256, h, w, h1, w1},
+                         out_to(n->L[kLat0], n->t0), s);
+    run_conv<T256, 3, 3>(n->L[kFpn0], SrcNHWC{n->t0, 256, h, w},
+                         out_to(n->L[kFpn0], n->f0, out0), s);
 }
 
-void depth_impl(bf_cuda_camera_neck *n, const float *fpn0, const float *depth, float *logits,
-                float *context, hipStream_t s) {
+// Depth head from the channels-last fpn0 in n->f0.
+void depth_impl(bf_cuda_camera_neck *n, const float *depth, float *logits, float *context,
+                hipStream_t s) {
     const int h = (int)n->h, w = (int)n->w;
-    SrcDepthAffine dsrc{depth, n->dt0_w, n->dt0_b, 8 * h, 8 * w};
-    run_conv<T32, 5, 5>(n->L[kDt1], dsrc, nchw(n->L[kDt1], n->e1), s);
-    run_conv<T64, 5, 5>(n->L[kDt2], SrcNCHW{n->e1, 32, 2 * h, 2 * w}, nchw(n->L[kDt2], n->e2), s);
-    run_conv<T256, 3, 3>(n->L[kDn0], SrcConcat2{n->e2, fpn0, 64, 256, h, w},
-                         nchw(n->L[kDn0], n->d0), s);
-    run_conv<T256, 3, 3>(n->L[kDn3], SrcNCHW{n->d0, 256, h, w}, nchw(n->L[kDn3], n->d1), s);
+    run_conv<T32, 5, 5>(n->L[kDt1], SrcNHWCDepthAffine{depth, n->dt0_w, n->dt0_b, 8 * h, 8 * w},
+                        out_to(n->L[kDt1], n->e1), s);
+    run_conv<T64, 5, 5>(n->L[kDt2], SrcNHWC{n->e1, 32, 2 * h, 2 * w}, out_to(n->L[kDt2], n->e2), s);
+    run_conv<T256, 3, 3>(n->L[kDn0], SrcNHWCConcat{n->e2, n->f0, 64, 256, h, w},
+                         out_to(n->L[kDn0], n->d0), s);
+    run_conv<T256, 3, 3>(n->L[kDn3], SrcNHWC{n->d0, 256, h, w}, out_to(n->L[kDn3], n->d1), s);
     const ConvLayer &l = n->L[kDn6];
-    run_conv<T256, 1, 1>(l, SrcNCHW{n->d1, 256, h, w},
+    run_conv<T256, 1, 1>(l, SrcNHWC{n->d1, 256, h, w},
                          EpiSplitDepth{logits, context, l.b, l.n * h * w, h * w, 118, 80}, s);
 }
 
 int build(bf_cuda_camera_neck *n, const bf_model *model, char *error, size_t cap) {
     const int B = (int)n->batches, h = (int)n->h, w = (int)n->w;
-    const int h1 = (int)n->h1, w1 = (int)n->w1;
+    const int h1 = (int)n->h1, w1 = (int)n->w1, h2 = (int)n->h2, w2 = (int)n->w2;
     const int bh = (int)n->bev_h, bw = (int)n->bev_w;
     struct Spec {
         const char *w, *b, *bn;
@@ -188,23 +209,22 @@ int build(bf_cuda_camera_neck *n, const bf_model *model, char *error, size_t cap
     n->dt0_w = (const float *)(n->params + dt0w);
     n->dt0_b = (const float *)(n->params + dt0b);
 
-    // Activations (fp32 NCHW): level-1 lateral / output, level-0 lateral /
-    // output, depth encoder maps, trunk maps, downsample intermediates.
-    const size_t hw = (size_t)h * w, hw1 = (size_t)h1 * w1;
-    const size_t sizes[10] = {
-        (size_t)B * 256 * hw1, (size_t)B * 256 * hw1, (size_t)B * 256 * hw, (size_t)B * 256 * hw,
-        (size_t)B * 32 * 4 * hw, (size_t)B * 64 * hw, (size_t)B * 256 * hw, (size_t)B * 256 * hw,
-        (size_t)80 * bh * bw, (size_t)80 * (bh / 2) * (bw / 2)};
-    size_t total = 0, offs[10];
-    for (int i = 0; i < 10; ++i) {
+    const size_t hw = (size_t)h * w, hw1 = (size_t)h1 * w1, hw2 = (size_t)h2 * w2;
+    const size_t bev = (size_t)bh * bw;
+    const size_t elems[14] = {
+        B * 192 * hw, B * 384 * hw1, B * 768 * hw2, B * 256 * hw1, B * 256 * hw1, B * 256 * hw,
+        B * 256 * hw, B * 32 * 4 * hw, B * 64 * hw, B * 256 * hw, B * 256 * hw, 80 * bev,
+        80 * bev, 80 * (bev / 4)};
+    bf16 **slots[14] = {&n->p0, &n->p1, &n->p2, &n->t1, &n->f1, &n->t0, &n->f0,
+                        &n->e1, &n->e2, &n->d0, &n->d1, &n->bp, &n->b0, &n->b1};
+    size_t total = 0, offs[14];
+    for (int i = 0; i < 14; ++i) {
         offs[i] = total;
-        total += (sizes[i] * 4 + 255) & ~size_t(255);
+        total += (elems[i] * 2 + 255) & ~size_t(255);
     }
     if (!hip_ok(hipMalloc(&n->acts, total), error, cap, "allocate camera activations")) return 0;
     n->resident_bytes += total;
-    float **slots[10] = {&n->t1, &n->fpn1, &n->t0, &n->fpn0, &n->e1,
-                         &n->e2, &n->d0,   &n->d1, &n->bev0, &n->bev1};
-    for (int i = 0; i < 10; ++i) *slots[i] = (float *)(n->acts + offs[i]);
+    for (int i = 0; i < 14; ++i) *slots[i] = (bf16 *)(n->acts + offs[i]);
     return 1;
 }
 
@@ -262,7 +282,9 @@ extern "C" int bf_cuda_camera_depth_forward(bf_cuda_camera_neck *n, const float 
                                             void *stream, char *error, size_t cap) {
     if (!n || !fpn0 || !depth || !logits || !context)
         return fail(error, cap, "invalid HIP depth buffers");
-    depth_impl(n, fpn0, depth, logits, context, reinterpret_cast<hipStream_t>(stream));
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    pack_nhwc(fpn0, n->f0, (int)n->batches, 256, (int)(n->h * n->w), s);
+    depth_impl(n, depth, logits, context, s);
     return launch_ok(error, cap, "HIP depth launch");
 }
 
@@ -273,8 +295,8 @@ extern "C" int bf_cuda_camera_neck_forward(bf_cuda_camera_neck *n, const float *
     if (!n || !s0 || !s1 || !s2 || !depth || !logits || !context)
         return fail(error, cap, "invalid HIP camera-neck buffers");
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    fpn_impl(n, s0, s1, s2, n->fpn0, n->fpn1, s);
-    depth_impl(n, n->fpn0, depth, logits, context, s);
+    fpn_impl(n, s0, s1, s2, nullptr, nullptr, s);
+    depth_impl(n, depth, logits, context, s);
     return launch_ok(error, cap, "HIP camera-neck launch");
 }
 
@@ -284,10 +306,38 @@ extern "C" int bf_cuda_camera_downsample_forward(bf_cuda_camera_neck *n, const f
     if (!n || !input || !output) return fail(error, cap, "invalid HIP downsample buffers");
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int bh = (int)n->bev_h, bw = (int)n->bev_w;
-    run_conv<T80, 3, 3>(n->L[kDs0], SrcNCHW{input, 80, bh, bw}, nchw(n->L[kDs0], n->bev0), s);
-    run_conv<T80, 3, 3>(n->L[kDs1], SrcNCHW{n->bev0, 80, bh, bw}, nchw(n->L[kDs1], n->bev1), s);
+    pack_nhwc(input, n->bp, 1, 80, bh * bw, s);
+    run_conv<T80, 3, 3>(n->L[kDs0], SrcNHWC{n->bp, 80, bh, bw}, out_to(n->L[kDs0], n->b0), s);
+    run_conv<T80, 3, 3>(n->L[kDs1], SrcNHWC{n->b0, 80, bh, bw}, out_to(n->L[kDs1], n->b1), s);
     const ConvLayer &l = n->L[kDs2];
-    run_conv<T80, 3, 3>(l, SrcNCHW{n->bev1, 80, bh / 2, bw / 2},
+    run_conv<T80, 3, 3>(l, SrcNHWC{n->b1, 80, bh / 2, bw / 2},
                         EpiTransposeXY{output, l.b, l.oh * l.ow, 80, l.oh, l.ow}, s);
     return launch_ok(error, cap, "HIP downsample launch");
+}
+
+extern "C" int bfhip_camera_profile_layer(bf_cuda_camera_neck *n, int layer, void *stream,
+                                          char *error, size_t cap) {
+    if (!n || layer < 0 || layer >= kLayers) return fail(error, cap, "invalid HIP camera layer");
+    if (layer == kDt1 || layer == kDn6)
+        return fail(error, cap, "camera layer %d reads or writes caller buffers; time it through "
+                    "bf_cuda_camera_depth_forward", layer);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const int h = (int)n->h, w = (int)n->w, h1 = (int)n->h1, w1 = (int)n->w1;
+    const int h2 = (int)n->h2, w2 = (int)n->w2, bh = (int)n->bev_h, bw = (int)n->bev_w;
+    const ConvLayer &l = n->L[layer];
+    // Same kernels and shapes as the forward entry points, on context buffers.
+    switch (layer) {
+        case kLat1: run_conv<T64, 1, 1>(l, SrcNHWCUpConcat{n->p1, n->p2, 384, 768, h1, w1, h2, w2}, out_to(l, n->t1), s); break;
+        case kFpn1: run_conv<T64, 3, 3>(l, SrcNHWC{n->t1, 256, h1, w1}, out_to(l, n->f1), s); break;
+        case kLat0: run_conv<T256, 1, 1>(l, SrcNHWCUpConcat{n->p0, n->f1, 192, 256, h, w, h1, w1}, out_to(l, n->t0), s); break;
+        case kFpn0: run_conv<T256, 3, 3>(l, SrcNHWC{n->t0, 256, h, w}, out_to(l, n->f0), s); break;
+        case kDt2: run_conv<T64, 5, 5>(l, SrcNHWC{n->e1, 32, 2 * h, 2 * w}, out_to(l, n->e2), s); break;
+        case kDn0: run_conv<T256, 3, 3>(l, SrcNHWCConcat{n->e2, n->f0, 64, 256, h, w}, out_to(l, n->d0), s); break;
+        case kDn3: run_conv<T256, 3, 3>(l, SrcNHWC{n->d0, 256, h, w}, out_to(l, n->d1), s); break;
+        case kDs0: run_conv<T80, 3, 3>(l, SrcNHWC{n->bp, 80, bh, bw}, out_to(l, n->b0), s); break;
+        case kDs1: run_conv<T80, 3, 3>(l, SrcNHWC{n->b0, 80, bh, bw}, out_to(l, n->b1), s); break;
+        case kDs2: run_conv<T80, 3, 3>(l, SrcNHWC{n->b1, 80, bh / 2, bw / 2}, out_to(l, n->b0), s); break;
+        default: break;
+    }
+    return launch_ok(error, cap, "launch HIP camera profiling layer");
 }

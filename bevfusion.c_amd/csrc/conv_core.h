@@ -24,70 +24,15 @@ struct ConvGeom {
 
 // ----------------------------------------------------------------- sources
 // A source returns input value (n, c, iy, ix) for an in-bounds tap; prepare()
-// sees the output pixel a thread owns before any load.
+// sees the output pixel a thread owns before any load.  The NCHW gather below
+// serves the stateless fp32 ABI; the contexts use the channels-last path at
+// the end of this file.
 struct SrcNCHW {
     const float *x;
     int C, H, W;
     __device__ void prepare(int, int, int) {}
     __device__ float operator()(int n, int c, int iy, int ix) const {
         return x[(((size_t)n * C + c) * H + iy) * W + ix];
-    }
-};
-
-// Channel concat of two NCHW maps of equal size: [0,C0) from a, [C0,C0+C1)
-// from b (reference depth_concat_kernel, src/cuda_camera.cu:246-253).
-struct SrcConcat2 {
-    const float *a, *b;
-    int C0, C1, H, W;
-    __device__ void prepare(int, int, int) {}
-    __device__ float operator()(int n, int c, int iy, int ix) const {
-        const size_t hw = (size_t)iy * W + ix;
-        return c < C0 ? a[((size_t)n * C0 + c) * H * W + hw]
-                      : b[((size_t)n * C1 + (c - C0)) * H * W + hw];
-    }
-};
-
-// Concat of a lower map with the bilinear (align_corners=False) upsample of an
-// upper map, consumed by a 1x1 stride-1 convolution, so the tap position is
-// the output pixel itself (reference fpn_concat_kernel, cuda_camera.cu:219-244;
-// CPU bilinear_channel, image_fpn.c:123-142).
-struct SrcUpConcat {
-    const float *lower, *upper;
-    int Cl, Cu, H, W, h, w;
-    int y0, y1, x0, x1;
-    float fy, fx;
-    __device__ void prepare(int, int oy, int ox) {
-        float sy = ((float)oy + 0.5f) * (float)h / (float)H - 0.5f;
-        float sx = ((float)ox + 0.5f) * (float)w / (float)W - 0.5f;
-        sy = fmaxf(sy, 0.0f);
-        sx = fmaxf(sx, 0.0f);
-        y0 = (int)floorf(sy);
-        x0 = (int)floorf(sx);
-        y1 = min(y0 + 1, h - 1);
-        x1 = min(x0 + 1, w - 1);
-        fy = sy - (float)y0;
-        fx = sx - (float)x0;
-    }
-    __device__ float operator()(int n, int c, int iy, int ix) const {
-        if (c < Cl) return lower[(((size_t)n * Cl + c) * H + iy) * W + ix];
-        const float *p = upper + ((size_t)n * Cu + (c - Cl)) * h * w;
-        const float top = p[y0 * w + x0] * (1.0f - fx) + p[y0 * w + x1] * fx;
-        const float bot = p[y1 * w + x0] * (1.0f - fx) + p[y1 * w + x1] * fx;
-        return top * (1.0f - fy) + bot * fy;
-    }
-};
-
-// dtransform.0 (1x1 conv 1->C on dense depth, BN folded, ReLU) evaluated on
-// the fly: channel c of tap (iy, ix) is relu(d*w[c] + b[c]).  Padding taps
-// stay zero because the consumer's zero padding applies to this map.
-struct SrcDepthAffine {
-    const float *depth;
-    const float *w, *b;
-    int H, W;
-    __device__ void prepare(int, int, int) {}
-    __device__ float operator()(int n, int c, int iy, int ix) const {
-        const float v = fmaf(depth[((size_t)n * H + iy) * W + ix], w[c], 0.0f) + b[c];
-        return v > 0.0f ? v : 0.0f;
     }
 };
 
@@ -213,6 +158,7 @@ struct LoadWeightIOHW {
 // Final 1x1 of the depth head: channels [0,118) are depth logits, [118,198)
 // context, both NCHW (reference split_depth_kernel, cuda_camera.cu:255-263).
 struct EpiSplitDepth {
+    static constexpr bool kRowVector = false;
     float *logits, *context;
     const float *bias;
     int M, ohw, bins, ctx;
@@ -235,6 +181,7 @@ struct EpiSplitDepth {
 // permute out[c][x][y] = y(c, y, x) on a [C, H, W] map (reference
 // transpose_xy_kernel, cuda_camera.cu:265-271; lss_downsample.c:142-146).
 struct EpiTransposeXY {
+    static constexpr bool kRowVector = false;
     float *out;
     const float *bias;
     int M, C, H, W;
@@ -251,5 +198,223 @@ struct EpiTransposeXY {
         }
     }
 };
+
+}  // namespace bfhip
+
+namespace bfhip {
+
+// ======================================================================
+// Channels-last implicit GEMM.  Reduction order is k = (ky*KW + kx)*Ci + ci,
+// so eight consecutive k are eight channels of one input pixel: one 16-byte
+// load per chunk instead of eight scalar gathers.  Every source below keeps
+// its channel count a multiple of 8.  Weights are stored [Co][KH][KW][Ci].
+// ======================================================================
+
+// Plain NHWC bf16 map x[n][iy][ix][C].
+struct SrcNHWC {
+    const bf16 *x;
+    int C, H, W;
+    struct Row {};
+    __device__ Row row(int, int, int) const { return {}; }
+    __device__ bf16x8 load(const Row &, int n, int iy, int ix, int c0) const {
+        return *reinterpret_cast<const bf16x8 *>(x + (((size_t)n * H + iy) * W + ix) * C + c0);
+    }
+};
+
+// Channel concat of two NHWC maps of the same size: [0,C0) from a, rest from b.
+struct SrcNHWCConcat {
+    const bf16 *a, *b;
+    int C0, C1, H, W;
+    struct Row {};
+    __device__ Row row(int, int, int) const { return {}; }
+    __device__ bf16x8 load(const Row &, int n, int iy, int ix, int c0) const {
+        const size_t pix = ((size_t)n * H + iy) * W + ix;
+        return c0 < C0 ? *reinterpret_cast<const bf16x8 *>(a + pix * C0 + c0)
+                       : *reinterpret_cast<const bf16x8 *>(b + pix * C1 + (c0 - C0));
+    }
+};
+
+// concat(lower, bilinear-up(upper)) read by a 1x1/s1 convolution; bilinear
+// coordinates follow the reference's fpn_concat_kernel (cuda_camera.cu:234-242)
+// and are computed once per output pixel.
+struct SrcNHWCUpConcat {
+    const bf16 *lower, *upper;
+    int Cl, Cu, H, W, h, w;
+    struct Row { int y0, y1, x0, x1; float fy, fx; };
+    __device__ Row row(int, int oy, int ox) const {
+        Row r;
+        float sy = ((float)oy + 0.5f) * (float)h / (float)H - 0.5f;
+        float sx = ((float)ox + 0.5f) * (float)w / (float)W - 0.5f;
+        sy = fmaxf(sy, 0.0f);
+        sx = fmaxf(sx, 0.0f);
+        r.y0 = (int)floorf(sy);
+        r.x0 = (int)floorf(sx);
+        r.y1 = min(r.y0 + 1, h - 1);
+        r.x1 = min(r.x0 + 1, w - 1);
+        r.fy = sy - (float)r.y0;
+        r.fx = sx - (float)r.x0;
+        return r;
+    }
+    __device__ bf16x8 load(const Row &r, int n, int iy, int ix, int c0) const {
+        if (c0 < Cl)
+            return *reinterpret_cast<const bf16x8 *>(lower + (((size_t)n * H + iy) * W + ix) * Cl + c0);
+        const bf16 *p = upper + (size_t)n * h * w * Cu + (c0 - Cl);
+        const bf16x8 a = *reinterpret_cast<const bf16x8 *>(p + ((size_t)r.y0 * w + r.x0) * Cu);
+        const bf16x8 b = *reinterpret_cast<const bf16x8 *>(p + ((size_t)r.y0 * w + r.x1) * Cu);
+        const bf16x8 c = *reinterpret_cast<const bf16x8 *>(p + ((size_t)r.y1 * w + r.x0) * Cu);
+        const bf16x8 d = *reinterpret_cast<const bf16x8 *>(p + ((size_t)r.y1 * w + r.x1) * Cu);
+        bf16x8 o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float top = to_f32(a[e]) * (1.0f - r.fx) + to_f32(b[e]) * r.fx;
+            const float bot = to_f32(c[e]) * (1.0f - r.fx) + to_f32(d[e]) * r.fx;
+            o[e] = to_bf16(top * (1.0f - r.fy) + bot * r.fy);
+        }
+        return o;
+    }
+};
+
+// dtransform.0 fused into dtransform.3's gather: the 8 virtual channels of tap
+// (iy, ix) are relu(depth*w[c] + b[c]) from one fp32 depth value.
+struct SrcNHWCDepthAffine {
+    const float *depth;
+    const float *w, *b;
+    int H, W;
+    struct Row {};
+    __device__ Row row(int, int, int) const { return {}; }
+    __device__ bf16x8 load(const Row &, int n, int iy, int ix, int) const {
+        const float d = depth[((size_t)n * H + iy) * W + ix];
+        bf16x8 o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float v = fmaf(d, w[e], 0.0f) + b[e];
+            o[e] = to_bf16(v > 0.0f ? v : 0.0f);
+        }
+        return o;
+    }
+};
+
+template <int BM, int BK, int THREADS, int KH, int KW, class Src>
+struct LoadConvNHWC {
+    static constexpr int kPerRow = BK / 8;
+    static constexpr int kChunks = BM * kPerRow;
+    static constexpr int kPer = kChunks / THREADS;
+    static constexpr int kRowStep = THREADS / kPerRow;
+    static_assert(kChunks % THREADS == 0 && THREADS % kPerRow == 0, "tile/thread mismatch");
+    Src src;
+    ConvGeom g;
+    int tid, cc;
+    int n[kPer], iy0[kPer], ix0[kPer];
+    bool ok[kPer];
+    typename Src::Row rs[kPer];
+    bf16x8 st[kPer];
+
+    __device__ void setup(int m0, int t) {
+        tid = t;
+        cc = t % kPerRow;
+        const int ohw = g.OH * g.OW;
+#pragma unroll
+        for (int p = 0; p < kPer; ++p) {
+            const int m = m0 + t / kPerRow + p * kRowStep;
+            ok[p] = m < g.M;
+            const int mm = ok[p] ? m : 0;
+            n[p] = mm / ohw;
+            const int q = mm - n[p] * ohw, oy = q / g.OW, ox = q - oy * g.OW;
+            iy0[p] = oy * g.SH - g.PH;
+            ix0[p] = ox * g.SW - g.PW;
+            rs[p] = src.row(n[p], oy, ox);
+        }
+    }
+    __device__ void load(int k0) {
+        const int k = k0 + cc * 8;
+        const bool kin = k < g.K;
+        const int tap = kin ? k / g.Ci : 0, c0 = k - tap * g.Ci;
+        const int ky = tap / KW, kx = tap - ky * KW;
+#pragma unroll
+        for (int p = 0; p < kPer; ++p) {
+            const int iy = iy0[p] + ky, ix = ix0[p] + kx;
+            bf16x8 v = {};
+            if (kin && ok[p] && (unsigned)iy < (unsigned)g.IH && (unsigned)ix < (unsigned)g.IW)
+                v = src.load(rs[p], n[p], iy, ix, c0);
+            st[p] = v;
+        }
+    }
+    __device__ void store(bf16 *lds) const {
+#pragma unroll
+        for (int p = 0; p < kPer; ++p)
+            *reinterpret_cast<bf16x8 *>(lds + (tid / kPerRow + p * kRowStep) * (BK + 8) + cc * 8) = st[p];
+    }
+};
+
+// Conv epilogue writing bias+ReLU results as NHWC bf16 (internal maps) and/or
+// NCHW fp32 (boundary outputs); either pointer may be null.
+struct EpiConvOut {
+    static constexpr bool kRowVector = false;
+    bf16 *nhwc;
+    float *nchw;
+    const float *bias;
+    int M, Co, ohw, relu;
+    __device__ void operator()(int row, int col, f32x4 v) const {
+        if (col >= Co) return;
+        const float b = bias[col];
+        f32x4 y;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            y[r] = v[r] + b;
+            if (relu && y[r] < 0.0f) y[r] = 0.0f;
+        }
+        if (nhwc)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                if (row + r < M) nhwc[(size_t)(row + r) * Co + col] = to_bf16(y[r]);
+        if (nchw) {
+            const int n = row / ohw, p = row - n * ohw;
+            if ((ohw & 3) == 0 && row + 3 < M) {
+                *reinterpret_cast<f32x4 *>(nchw + ((size_t)n * Co + col) * ohw + p) = y;
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int rr = row + r;
+                    if (rr >= M) break;
+                    const int nn = rr / ohw, pp = rr - nn * ohw;
+                    nchw[((size_t)nn * Co + col) * ohw + pp] = y[r];
+                }
+            }
+        }
+    }
+};
+
+// NCHW fp32 [N][C][HW] -> NHWC bf16 [N][HW][C] through a 64-pixel x 64-channel
+// LDS tile (coalesced reads along pixels, 16-byte writes along channels).
+// C must be a multiple of 8.
+static __global__ __launch_bounds__(256) void pack_nhwc_kernel(const float *x, bf16 *y, int C, int HW) {
+    __shared__ float tile[64][65];
+    const int n = blockIdx.z, c0 = blockIdx.y * 64, p0 = blockIdx.x * 64;
+    const int t = threadIdx.x;
+    const float *src = x + (size_t)n * C * HW;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int cl = (t >> 6) + 4 * i, pl = t & 63;
+        const int c = c0 + cl, p = p0 + pl;
+        tile[cl][pl] = (c < C && p < HW) ? src[(size_t)c * HW + p] : 0.0f;
+    }
+    __syncthreads();
+    bf16 *dst = y + (size_t)n * HW * C;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int q = t + 256 * i, pl = q >> 3, ch = (q & 7) * 8;
+        const int p = p0 + pl, c = c0 + ch;
+        if (p >= HW || c >= C) continue;
+        bf16x8 v;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = to_bf16(tile[ch + e][pl]);
+        *reinterpret_cast<bf16x8 *>(dst + (size_t)p * C + c) = v;
+    }
+}
+
+inline void pack_nhwc(const float *x, bf16 *y, int N, int C, int HW, hipStream_t s) {
+    hipLaunchKernelGGL(pack_nhwc_kernel, dim3((HW + 63) / 64, (C + 63) / 64, N), dim3(256), 0, s,
+                       x, y, C, HW);
+}
 
 }  // namespace bfhip

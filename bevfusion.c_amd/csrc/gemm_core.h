@@ -119,8 +119,15 @@ struct LoadRowsF32 {
 template <class T, class ALoad, class BLoad, class Epi>
 __global__ __launch_bounds__(T::kThreads) void gemm_kernel(ALoad al, BLoad bl, Epi epi,
                                                            int M, int N, int K, int tiles_n) {
-    __shared__ __attribute__((aligned(16))) bf16 sA[2][T::BM * T::kStride];
-    __shared__ __attribute__((aligned(16))) bf16 sB[2][T::BN * T::kStride];
+    // One LDS arena: double-buffered A/B tiles in the main loop, then (for
+    // row-vector epilogues) the fp32 output tile.
+    constexpr int kCStride = T::BN + 4;  // floats; staggers rows across banks
+    constexpr size_t kABBytes = (size_t)2 * (T::BM + T::BN) * T::kStride * sizeof(bf16);
+    constexpr size_t kCBytes = Epi::kRowVector ? (size_t)T::BM * kCStride * sizeof(float) : 0;
+    __shared__ __attribute__((aligned(16))) unsigned char smem[kABBytes > kCBytes ? kABBytes : kCBytes];
+    bf16(*sA)[T::BM * T::kStride] = reinterpret_cast<bf16(*)[T::BM * T::kStride]>(smem);
+    bf16(*sB)[T::BN * T::kStride] =
+        reinterpret_cast<bf16(*)[T::BN * T::kStride]>(smem + (size_t)2 * T::BM * T::kStride * sizeof(bf16));
 
     const int pid = xcd_swizzle((int)blockIdx.x, (int)gridDim.x);
     const int m0 = (pid / tiles_n) * T::BM, n0 = (pid % tiles_n) * T::BN;
@@ -176,12 +183,33 @@ __global__ __launch_bounds__(T::kThreads) void gemm_kernel(ALoad al, BLoad bl, E
         __syncthreads();
     }
 
-    const int row_base = m0 + wm * T::kWaveRows + 4 * (lane >> 4);
-    const int col_base = n0 + wn * T::kWaveCols + (lane & 15);
+    if constexpr (Epi::kRowVector) {
+        // Stage the tile through LDS (the loop's final barrier freed it) so
+        // the epilogue writes whole rows with 16-byte vectors instead of one
+        // scalar per lane per row.
+        float *sC = reinterpret_cast<float *>(smem);
+        const int r0 = wm * T::kWaveRows + 4 * (lane >> 4), c0 = wn * T::kWaveCols + (lane & 15);
 #pragma unroll
-    for (int i = 0; i < T::kFragM; ++i)
+        for (int i = 0; i < T::kFragM; ++i)
 #pragma unroll
-        for (int j = 0; j < T::kFragN; ++j) epi(row_base + i * 16, col_base + j * 16, acc[i][j]);
+            for (int j = 0; j < T::kFragN; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    sC[(r0 + i * 16 + r) * kCStride + c0 + j * 16] = acc[i][j][r];
+        __syncthreads();
+        constexpr int kQuads = T::BN / 4;
+        for (int c = tid; c < T::BM * kQuads; c += T::kThreads) {
+            const int r = c / kQuads, q = c - r * kQuads;
+            epi.row4(m0 + r, n0 + 4 * q, *reinterpret_cast<const float4 *>(sC + r * kCStride + 4 * q));
+        }
+    } else {
+        const int row_base = m0 + wm * T::kWaveRows + 4 * (lane >> 4);
+        const int col_base = n0 + wn * T::kWaveCols + (lane & 15);
+#pragma unroll
+        for (int i = 0; i < T::kFragM; ++i)
+#pragma unroll
+            for (int j = 0; j < T::kFragN; ++j) epi(row_base + i * 16, col_base + j * 16, acc[i][j]);
+    }
 }
 
 // Host launcher: one workgroup per output tile.
@@ -197,10 +225,31 @@ inline void launch_gemm(const ALoad &al, const BLoad &bl, const Epi &epi, int M,
 // Each is called with the fragment origin (row, col) of four consecutive rows
 // row..row+3 in one column; bounds are the epilogue's responsibility.
 
+// Row-vector epilogues (kRowVector) receive four consecutive columns of one
+// row through row4(); vector stores need ld % 4 == 0 and an aligned base,
+// otherwise they fall back to scalars.
 struct EpiRowsF32 {  // out[row*ld + col] = v (+bias) (ReLU)
+    static constexpr bool kRowVector = true;
     float *out;
     const float *bias;
     int ld, M, N, relu;
+    __device__ void row4(int row, int col, float4 v) const {
+        if (row >= M || col >= N) return;
+        float y[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            if (bias && col + e < N) y[e] += bias[col + e];
+            if (relu && y[e] < 0.0f) y[e] = 0.0f;
+        }
+        float *p = out + (size_t)row * ld + col;
+        if (col + 3 < N && (ld & 3) == 0 && ((uintptr_t)out & 15) == 0) {
+            *reinterpret_cast<float4 *>(p) = make_float4(y[0], y[1], y[2], y[3]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (col + e < N) p[e] = y[e];
+        }
+    }
     __device__ void operator()(int row, int col, f32x4 v) const {
         if (col >= N) return;
         const float b = bias ? bias[col] : 0.0f;
@@ -215,10 +264,30 @@ struct EpiRowsF32 {  // out[row*ld + col] = v (+bias) (ReLU)
 };
 
 template <bool GELU>
-struct EpiRowsBf16 {  // out[row*ld + col] = bf16(act(v + bias))
+struct EpiRowsBf16 {  // out[row*ld + col] = bf16(act(v + bias)); ld % 4 == 0
+    static constexpr bool kRowVector = true;
     bf16 *out;
     const float *bias;
     int ld, M, N;
+    __device__ void row4(int row, int col, float4 v) const {
+        if (row >= M || col >= N) return;
+        float y[4] = {v.x, v.y, v.z, v.w};
+        bf16x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float t = y[e] + (bias && col + e < N ? bias[col + e] : 0.0f);
+            if (GELU) t = gelu_erf(t);
+            o[e] = to_bf16(t);
+        }
+        bf16 *p = out + (size_t)row * ld + col;
+        if (col + 3 < N) {
+            *reinterpret_cast<bf16x4 *>(p) = o;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (col + e < N) p[e] = o[e];
+        }
+    }
     __device__ void operator()(int row, int col, f32x4 v) const {
         if (col >= N) return;
         const float b = bias ? bias[col] : 0.0f;
@@ -232,10 +301,24 @@ struct EpiRowsBf16 {  // out[row*ld + col] = bf16(act(v + bias))
     }
 };
 
-struct EpiResidualF32 {  // x[row*ld + col] += v + bias
+struct EpiResidualF32 {  // x[row*ld + col] += v + bias; ld % 4 == 0
+    static constexpr bool kRowVector = true;
     float *x;
     const float *bias;
     int ld, M, N;
+    __device__ void row4(int row, int col, float4 v) const {
+        if (row >= M || col >= N) return;
+        float *p = x + (size_t)row * ld + col;
+        if (col + 3 < N) {
+            float4 a = *reinterpret_cast<const float4 *>(p);
+            const float4 b = bias ? *reinterpret_cast<const float4 *>(bias + col) : make_float4(0, 0, 0, 0);
+            a.x += v.x + b.x; a.y += v.y + b.y; a.z += v.z + b.z; a.w += v.w + b.w;
+            *reinterpret_cast<float4 *>(p) = a;
+        } else {
+            const float y[4] = {v.x, v.y, v.z, v.w};
+            for (int e = 0; e < 4 && col + e < N; ++e) p[e] = p[e] + (y[e] + (bias ? bias[col + e] : 0.0f));
+        }
+    }
     __device__ void operator()(int row, int col, f32x4 v) const {
         if (col >= N) return;
         const float b = bias ? bias[col] : 0.0f;
@@ -251,6 +334,7 @@ struct EpiResidualF32 {  // x[row*ld + col] += v + bias
 // Implicit-GEMM convolution output: row = n*OHW + p, col = output channel,
 // stored NCHW.  Four consecutive rows of one image are one float4 when aligned.
 struct EpiNCHW {
+    static constexpr bool kRowVector = false;
     float *out;
     const float *bias;
     int M, Co, ohw, relu;

@@ -14,6 +14,7 @@
 // proj GEMM(+bias, += into x) -> LN2 -> fc1 GEMM(+bias, GELU, bf16) ->
 // fc2 GEMM(+bias, += into x).
 #include "bf_cuda_swin.h"
+#include "bfhip_profile.h"
 #include "conv_core.h"
 #include "host_util.h"
 #include "linear.h"
@@ -284,61 +285,102 @@ extern "C" int bf_cuda_swin_create(const bf_model *model, size_t batches, size_t
     return 1;
 }
 
+namespace {
+
+// The launches of one frame, factored per op so that the forward and the
+// profiling hook (bfhip_swin_profile_op) run exactly the same kernels.
+void patch_embed(bf_cuda_swin *s, const float *images, hipStream_t stream) {
+    // 4x4/s4 conv 3->96 straight from NCHW images into NHWC tokens, then
+    // LayerNorm in place.
+    using T = Tile<128, 96, 32, 2, 2>;
+    const int B = (int)s->batches;
+    ConvGeom g{};
+    g.N = B; g.Ci = 3; g.IH = (int)s->input_h; g.IW = (int)s->input_w;
+    g.OH = s->h[0]; g.OW = s->w[0]; g.KH = 4; g.KW = 4; g.SH = 4; g.SW = 4;
+    g.PH = 0; g.PW = 0; g.transpose = 0;
+    g.M = B * s->h[0] * s->w[0]; g.K = 48;
+    LoadConvA<T::BM, T::BK, T::kThreads, 4, 4, SrcNCHW> al{};
+    al.src = SrcNCHW{images, 3, g.IH, g.IW};
+    al.g = g;
+    LoadRowsBf16<T::BN, T::BK, T::kThreads> bl{s->patch_w, 48, 96, 48};
+    EpiRowsF32 epi{s->x, s->patch_b, 96, g.M, 96, 0};
+    launch_gemm<T>(al, bl, epi, g.M, 96, 48, stream);
+    launch_ln<float>(96, s->x, s->x, s->patch_ns, s->patch_nb, g.M, stream);
+}
+
+void block_op(bf_cuda_swin *s, int st, int b, int op, hipStream_t stream) {
+    const int B = (int)s->batches, C = kC[st], heads = kHeads[st], H = s->h[st], W = s->w[st];
+    const int T = B * H * W, wy_n = (H + 6) / 7, wx_n = (W + 6) / 7;
+    const int items = B * wy_n * wx_n * heads;
+    const BlockW &w = s->blocks[st][b];
+    switch (op) {
+        case BFHIP_SWIN_LN1:
+            launch_ln<bf16>(C, s->x, s->xn, w.n1s, w.n1b, T, stream);
+            break;
+        case BFHIP_SWIN_QKV:
+            linear_bf16(s->xn, w.qkv_w, T, 3 * C, C,
+                        EpiRowsBf16<false>{s->big, w.qkv_b, 3 * C, T, 3 * C}, stream);
+            break;
+        case BFHIP_SWIN_ATTENTION:
+            hipLaunchKernelGGL(window_attention_kernel, dim3((items + kAttnWaves - 1) / kAttnWaves),
+                               dim3(64 * kAttnWaves), 0, stream, s->big, w.qkv_b, w.bias_mat,
+                               s->xn, H, W, C, heads, wy_n, wx_n, (b & 1) ? 3 : 0, items);
+            break;
+        case BFHIP_SWIN_PROJ:
+            linear_bf16(s->xn, w.proj_w, T, C, C, EpiResidualF32{s->x, w.proj_b, C, T, C}, stream);
+            break;
+        case BFHIP_SWIN_LN2:
+            launch_ln<bf16>(C, s->x, s->xn, w.n2s, w.n2b, T, stream);
+            break;
+        case BFHIP_SWIN_FC1:
+            linear_bf16(s->xn, w.fc1_w, T, 4 * C, C,
+                        EpiRowsBf16<true>{s->big, w.fc1_b, 4 * C, T, 4 * C}, stream);
+            break;
+        case BFHIP_SWIN_FC2:
+            linear_bf16(s->big, w.fc2_w, T, C, 4 * C, EpiResidualF32{s->x, w.fc2_b, C, T, C}, stream);
+            break;
+        default:
+            break;
+    }
+}
+
+void merge_op(bf_cuda_swin *s, int st, hipStream_t stream) {
+    const int B = (int)s->batches, C = kC[st];
+    const int T2 = B * s->h[st + 1] * s->w[st + 1];
+    launch_merge(C, s->x, s->xn, s->merge_s[st], s->merge_b[st], B, s->h[st], s->w[st], stream);
+    linear_bf16(s->xn, s->merge_w[st], T2, 2 * C, 4 * C,
+                EpiRowsF32{s->x, nullptr, 2 * C, T2, 2 * C, 0}, stream);
+}
+
+}  // namespace
+
 extern "C" int bf_cuda_swin_forward(bf_cuda_swin *s, const float *images, float *out1,
                                     float *out2, float *out3, void *stream_value, char *error,
                                     size_t cap) {
     if (!s || !images || !out1 || !out2 || !out3)
         return fail(error, cap, "invalid HIP Swin buffers");
     hipStream_t stream = reinterpret_cast<hipStream_t>(stream_value);
-    const int B = (int)s->batches;
     float *outputs[3] = {out1, out2, out3};
-
-    // Patch embedding: 4x4/s4 conv 3->96 straight from NCHW images into NHWC
-    // tokens, then LayerNorm in place.
-    {
-        using T = Tile<128, 96, 32, 2, 2>;
-        ConvGeom g{};
-        g.N = B; g.Ci = 3; g.IH = (int)s->input_h; g.IW = (int)s->input_w;
-        g.OH = s->h[0]; g.OW = s->w[0]; g.KH = 4; g.KW = 4; g.SH = 4; g.SW = 4;
-        g.PH = 0; g.PW = 0; g.transpose = 0;
-        g.M = B * s->h[0] * s->w[0]; g.K = 48;
-        LoadConvA<T::BM, T::BK, T::kThreads, 4, 4, SrcNCHW> al{};
-        al.src = SrcNCHW{images, 3, g.IH, g.IW};
-        al.g = g;
-        LoadRowsBf16<T::BN, T::BK, T::kThreads> bl{s->patch_w, 48, 96, 48};
-        EpiRowsF32 epi{s->x, s->patch_b, 96, g.M, 96, 0};
-        launch_gemm<T>(al, bl, epi, g.M, 96, 48, stream);
-        launch_ln<float>(96, s->x, s->x, s->patch_ns, s->patch_nb, g.M, stream);
-    }
-
+    patch_embed(s, images, stream);
     for (int st = 0; st < 4; ++st) {
-        const int C = kC[st], heads = kHeads[st], H = s->h[st], W = s->w[st];
-        const int T = B * H * W;
-        const int wy_n = (H + 6) / 7, wx_n = (W + 6) / 7;
-        const int items = B * wy_n * wx_n * heads;
-        for (int b = 0; b < kDepth[st]; ++b) {
-            const BlockW &w = s->blocks[st][b];
-            const int shift = (b & 1) ? 3 : 0;
-            launch_ln<bf16>(C, s->x, s->xn, w.n1s, w.n1b, T, stream);
-            linear_bf16(s->xn, w.qkv_w, T, 3 * C, C,
-                        EpiRowsBf16<false>{s->big, w.qkv_b, 3 * C, T, 3 * C}, stream);
-            hipLaunchKernelGGL(window_attention_kernel, dim3((items + kAttnWaves - 1) / kAttnWaves),
-                               dim3(64 * kAttnWaves), 0, stream, s->big, w.qkv_b, w.bias_mat,
-                               s->xn, H, W, C, heads, wy_n, wx_n, shift, items);
-            linear_bf16(s->xn, w.proj_w, T, C, C, EpiResidualF32{s->x, w.proj_b, C, T, C}, stream);
-            launch_ln<bf16>(C, s->x, s->xn, w.n2s, w.n2b, T, stream);
-            linear_bf16(s->xn, w.fc1_w, T, 4 * C, C,
-                        EpiRowsBf16<true>{s->big, w.fc1_b, 4 * C, T, 4 * C}, stream);
-            linear_bf16(s->big, w.fc2_w, T, C, 4 * C, EpiResidualF32{s->x, w.fc2_b, C, T, C},
-                        stream);
-        }
-        if (st > 0) launch_out_ln(C, s->x, outputs[st - 1], s->out_s[st - 1], s->out_b[st - 1], T, H * W, stream);
-        if (st < 3) {
-            const int T2 = B * s->h[st + 1] * s->w[st + 1];
-            launch_merge(C, s->x, s->xn, s->merge_s[st], s->merge_b[st], B, H, W, stream);
-            linear_bf16(s->xn, s->merge_w[st], T2, 2 * C, 4 * C,
-                        EpiRowsF32{s->x, nullptr, 2 * C, T2, 2 * C, 0}, stream);
-        }
+        for (int b = 0; b < kDepth[st]; ++b)
+            for (int op = BFHIP_SWIN_LN1; op <= BFHIP_SWIN_FC2; ++op) block_op(s, st, b, op, stream);
+        const int T = (int)s->batches * s->h[st] * s->w[st];
+        if (st > 0)
+            launch_out_ln(kC[st], s->x, outputs[st - 1], s->out_s[st - 1], s->out_b[st - 1], T,
+                          s->h[st] * s->w[st], stream);
+        if (st < 3) merge_op(s, st, stream);
     }
     return launch_ok(error, cap, "launch HIP Swin graph");
+}
+
+extern "C" int bfhip_swin_profile_op(bf_cuda_swin *s, int stage, int block, int op, void *stream,
+                                     char *error, size_t cap) {
+    if (!s || stage < 0 || stage > 3 || block < 0 || block >= kDepth[stage] ||
+        op < BFHIP_SWIN_LN1 || op > BFHIP_SWIN_MERGE || (op == BFHIP_SWIN_MERGE && stage > 2))
+        return fail(error, cap, "invalid HIP Swin profiling op");
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (op == BFHIP_SWIN_MERGE) merge_op(s, stage, st);
+    else block_op(s, stage, block, op, st);
+    return launch_ok(error, cap, "launch HIP Swin profiling op");
 }

@@ -205,7 +205,7 @@ __device__ __forceinline__ int window_label(int t, int wy, int wx, int Hp, int W
 // t >= 49 are excluded.  Outputs go back to the token rows they came from.
 constexpr int kAttnWaves = 4;
 
-__global__ __launch_bounds__(256) void window_attention_kernel(
+static __global__ __launch_bounds__(256) void window_attention_kernel(
     const bf16 *__restrict__ qkv, const float *__restrict__ qkv_bias,
     const float *__restrict__ bias_mat, bf16 *__restrict__ out, int H, int W, int C, int heads,
     int wy_n, int wx_n, int shift, int items) {

@@ -1,0 +1,90 @@
+"""C-ABI boundary checks that need no GPU.
+
+libbfhip.so must load, export every entry point declared in include/*.h, and
+reject invalid contracts before launching anything (reference
+src/cuda_ops.cu:150-170,192-196; cuda_swin.cu:272-273; cuda_camera.cu:288-290;
+tests/test_cuda_ops.cu:164-174).
+"""
+
+import ctypes as C
+import pathlib
+import re
+
+import bfhip
+
+ROOT = pathlib.Path(__file__).resolve().parent.parent
+HEADERS = ["bf_cuda_ops.h", "bf_cuda_swin.h", "bf_cuda_camera.h", "bfhip_profile.h"]
+
+
+def declared(header):
+    text = (ROOT / "include" / header).read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b((?:bf|bfhip)_[a-z0-9_]+)\s*\(", text))
+
+
+def test_every_declared_entry_point_is_exported():
+    lib = bfhip.hip_lib()
+    names = set().union(*(declared(h) for h in HEADERS))
+    assert len(names) == 15
+    assert names == set(bfhip.SIGNATURES)
+    missing = [n for n in sorted(names) if not hasattr(lib, n)]
+    assert not missing, missing
+    model = bfhip.model_lib()
+    assert all(hasattr(model, n) for n in declared("bf_model.h"))
+
+
+def _err():
+    return C.create_string_buffer(256)
+
+
+def test_conv_rejects_invalid_and_oversized():
+    lib = bfhip.hip_lib()
+    e = _err()
+    zero = bfhip.ConvDesc()
+    assert lib.bf_cuda_conv2d_f32(C.byref(zero), None, None, None, None, None, e, 256) == 0
+    assert b"invalid" in e.value
+    big = 2147483647
+    over = bfhip.ConvDesc(big, 1, 1, big, big, 1, 1, 1, 1, 0, 0, big, big, 0, 0)
+    s = C.c_void_p(1)
+    assert lib.bf_cuda_conv2d_f32(C.byref(over), s, s, None, s, None, e, 256) == 0
+    assert b"too large" in e.value
+    bad_relu = bfhip.ConvDesc(1, 1, 1, 4, 4, 1, 1, 1, 1, 0, 0, 4, 4, 0, 2)
+    assert lib.bf_cuda_conv2d_f32(C.byref(bad_relu), s, s, None, s, None, e, 256) == 0
+    # NULL / zero-capacity error buffers are allowed.
+    assert lib.bf_cuda_conv2d_f32(C.byref(zero), None, None, None, None, None, None, 0) == 0
+
+
+def test_gemm_rejects_invalid():
+    lib = bfhip.hip_lib()
+    e = _err()
+    s = C.c_void_p(1)
+    assert lib.bf_cuda_gemm_f32(s, s, None, s, 0, 4, 4, 0, None, e, 256) == 0
+    assert lib.bf_cuda_gemm_f32(s, s, None, s, 4, 4, 4, 2, None, e, 256) == 0
+    assert lib.bf_cuda_gemm_f32(None, s, None, s, 4, 4, 4, 0, None, e, 256) == 0
+    assert b"invalid" in e.value
+
+
+def test_contexts_reject_invalid_contracts(tmp_path):
+    from bfhip import bfw
+    lib = bfhip.hip_lib()
+    e = _err()
+    out = C.c_void_p()
+    assert not lib.bf_cuda_swin_create(None, 6, 256, 704, C.byref(out), e, 256)
+    path = tmp_path / "x.bfw"
+    bfw.write_bfw([("x", bfw.randn(0, "x", (4,)))], path)
+    with bfhip.Model(path) as m:
+        assert not lib.bf_cuda_swin_create(m.handle, 6, 258, 704, C.byref(out), e, 256)
+        assert b"invalid" in e.value
+        assert not lib.bf_cuda_swin_create(m.handle, 0, 256, 704, C.byref(out), e, 256)
+        assert not lib.bf_cuda_camera_neck_create(m.handle, 6, 32, 88, 361, 360, C.byref(out),
+                                                  e, 256)
+        assert b"invalid" in e.value
+    assert out.value is None
+    assert lib.bf_cuda_swin_resident_bytes(None) == 0
+    assert lib.bf_cuda_camera_neck_resident_bytes(None) == 0
+    lib.bf_cuda_swin_destroy(None)
+    lib.bf_cuda_camera_neck_destroy(None)
+    s = C.c_void_p(1)
+    assert not lib.bf_cuda_swin_forward(None, s, s, s, s, None, e, 256)
+    assert not lib.bf_cuda_camera_downsample_forward(None, s, s, None, e, 256)
+    assert not lib.bf_cuda_camera_neck_forward(None, s, s, s, s, s, s, None, e, 256)
