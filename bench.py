@@ -46,6 +46,8 @@ def parse():
     p.add_argument("--no-roofline", action="store_true", help="skip per-kernel timing")
     p.add_argument("--kernel-reps", type=int, default=20,
                    help="HIP-event timed launches per kernel in the roofline leg")
+    p.add_argument("--kernels", default="",
+                   help="comma-separated op names to time in the roofline leg (default: all)")
     return p.parse_args()
 
 
@@ -135,7 +137,7 @@ def roofline_entry(name, avg_s, per_frame, flops, nbytes):
             "tflops": round(flops / avg_s / 1e12, 1), "gbs": round(nbytes / avg_s / 1e9, 1)}
 
 
-def time_kernels(swin, neck, stream, reps=20):
+def time_kernels(swin, neck, stream, reps=20, only=()):
     """Time single ops of the path with HIP events on the stream they are
     launched on; returns roofline entries sorted by time per frame."""
     import torch
@@ -151,6 +153,8 @@ def time_kernels(swin, neck, stream, reps=20):
     for layer, (name, *_rest) in NECK_LAYERS.items():
         cands.append((f"neck.{name}", lambda layer=layer: neck.profile_layer(layer, stream), 1,
                       neck_layer_cost(layer)))
+    if only:
+        cands = [c for c in cands if c[0] in only]
     out = []
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     for name, fn, per_frame, (flops, nbytes) in cands:
@@ -292,7 +296,8 @@ def main():
     }
     if not args.no_roofline:
         with torch.cuda.stream(stream):
-            kernels = time_kernels(swin, neck, stream, args.kernel_reps)
+            only = tuple(k for k in args.kernels.split(",") if k)
+            kernels = time_kernels(swin, neck, stream, args.kernel_reps, only)
         result["roofline"] = kernels[0]
         result["kernels"] = [{k: e[k] for k in ("kernel", "bound", "frac", "avg_us",
                                                   "us_per_frame", "tflops", "gbs")}

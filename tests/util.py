@@ -48,6 +48,7 @@ def assert_close(actual, expected, name="", rel_l2=REL_L2, max_abs_rms=MAX_ABS_R
     assert np.array_equal(a[inf_e], e[inf_e]), f"{name}: Inf signs differ"
     fin = np.isfinite(e)
     rl2, mabs, rms = errors(a[fin], e[fin])
+    print(f"[parity] {name}: rel_l2={rl2:.3e} max_abs/rms={mabs / max(rms, 1e-30):.3e}")
     assert rl2 <= rel_l2, f"{name}: rel L2 {rl2:.3e} > {rel_l2:.1e}"
     assert mabs <= max_abs_rms * rms, f"{name}: max abs {mabs:.3e} > {max_abs_rms} x rms {rms:.3e}"
     return rl2, mabs / max(rms, 1e-30)
