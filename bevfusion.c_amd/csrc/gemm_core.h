@@ -115,15 +115,71 @@ struct LoadRowsF32 {
     }
 };
 
+// ------------------------------------------------------------------ epilogue
+// Hands the accumulators of one BM x BN tile to the epilogue policy.  Row-vector
+// epilogues get the tile staged through LDS (the caller has synchronised the
+// arena) so that whole rows leave as 16-byte vectors; column-fragment
+// epilogues take the four rows of each MFMA fragment directly.
+template <class T, class Epi>
+__device__ __forceinline__ void store_tile(const f32x4 (&acc)[T::kFragM][T::kFragN], const Epi &epi,
+                                           unsigned char *smem, int m0, int n0, int tid) {
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / T::WN, wn = wave % T::WN;
+    if constexpr (Epi::kRowVector) {
+        constexpr int kCStride = T::BN + 4;  // floats; staggers rows across banks
+        float *sC = reinterpret_cast<float *>(smem);
+        const int r0 = wm * T::kWaveRows + 4 * (lane >> 4), c0 = wn * T::kWaveCols + (lane & 15);
+#pragma unroll
+        for (int i = 0; i < T::kFragM; ++i)
+#pragma unroll
+            for (int j = 0; j < T::kFragN; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    sC[(r0 + i * 16 + r) * kCStride + c0 + j * 16] = acc[i][j][r];
+        __syncthreads();
+        constexpr int kQuads = T::BN / 4;
+        if constexpr (T::kThreads % kQuads == 0 && T::BM % (T::kThreads / kQuads) == 0) {
+            // Each thread owns one column quad for the whole tile: the
+            // epilogue's per-column state (bias) is fetched once, and all of
+            // the thread's rows are handed over together so that their
+            // global reads (residual) can be in flight at once.
+            constexpr int kStep = T::kThreads / kQuads, kRows = T::BM / kStep;
+            const int q = tid % kQuads, r = tid / kQuads;
+            float4 v[kRows];
+#pragma unroll
+            for (int i = 0; i < kRows; ++i)
+                v[i] = *reinterpret_cast<const float4 *>(sC + (r + i * kStep) * kCStride + 4 * q);
+            epi.template rows<kRows>(m0 + r, kStep, epi.column(n0 + 4 * q), v);
+        } else {
+            for (int c = tid; c < T::BM * kQuads; c += T::kThreads) {
+                const int r = c / kQuads, q = c - r * kQuads;
+                const float4 v[1] = {*reinterpret_cast<const float4 *>(sC + r * kCStride + 4 * q)};
+                epi.template rows<1>(m0 + r, 0, epi.column(n0 + 4 * q), v);
+            }
+        }
+    } else {
+        const int row_base = m0 + wm * T::kWaveRows + 4 * (lane >> 4);
+        const int col_base = n0 + wn * T::kWaveCols + (lane & 15);
+#pragma unroll
+        for (int i = 0; i < T::kFragM; ++i)
+#pragma unroll
+            for (int j = 0; j < T::kFragN; ++j) epi(row_base + i * 16, col_base + j * 16, acc[i][j]);
+    }
+}
+
+template <class T, class Epi>
+constexpr size_t epilogue_bytes() {
+    return Epi::kRowVector ? (size_t)T::BM * (T::BN + 4) * sizeof(float) : 0;
+}
+
 // ------------------------------------------------------------------ main loop
 template <class T, class ALoad, class BLoad, class Epi>
 __global__ __launch_bounds__(T::kThreads) void gemm_kernel(ALoad al, BLoad bl, Epi epi,
                                                            int M, int N, int K, int tiles_n) {
     // One LDS arena: double-buffered A/B tiles in the main loop, then (for
     // row-vector epilogues) the fp32 output tile.
-    constexpr int kCStride = T::BN + 4;  // floats; staggers rows across banks
     constexpr size_t kABBytes = (size_t)2 * (T::BM + T::BN) * T::kStride * sizeof(bf16);
-    constexpr size_t kCBytes = Epi::kRowVector ? (size_t)T::BM * kCStride * sizeof(float) : 0;
+    constexpr size_t kCBytes = epilogue_bytes<T, Epi>();
     __shared__ __attribute__((aligned(16))) unsigned char smem[kABBytes > kCBytes ? kABBytes : kCBytes];
     bf16(*sA)[T::BM * T::kStride] = reinterpret_cast<bf16(*)[T::BM * T::kStride]>(smem);
     bf16(*sB)[T::BN * T::kStride] =
@@ -183,33 +239,7 @@ __global__ __launch_bounds__(T::kThreads) void gemm_kernel(ALoad al, BLoad bl, E
         __syncthreads();
     }
 
-    if constexpr (Epi::kRowVector) {
-        // Stage the tile through LDS (the loop's final barrier freed it) so
-        // the epilogue writes whole rows with 16-byte vectors instead of one
-        // scalar per lane per row.
-        float *sC = reinterpret_cast<float *>(smem);
-        const int r0 = wm * T::kWaveRows + 4 * (lane >> 4), c0 = wn * T::kWaveCols + (lane & 15);
-#pragma unroll
-        for (int i = 0; i < T::kFragM; ++i)
-#pragma unroll
-            for (int j = 0; j < T::kFragN; ++j)
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    sC[(r0 + i * 16 + r) * kCStride + c0 + j * 16] = acc[i][j][r];
-        __syncthreads();
-        constexpr int kQuads = T::BN / 4;
-        for (int c = tid; c < T::BM * kQuads; c += T::kThreads) {
-            const int r = c / kQuads, q = c - r * kQuads;
-            epi.row4(m0 + r, n0 + 4 * q, *reinterpret_cast<const float4 *>(sC + r * kCStride + 4 * q));
-        }
-    } else {
-        const int row_base = m0 + wm * T::kWaveRows + 4 * (lane >> 4);
-        const int col_base = n0 + wn * T::kWaveCols + (lane & 15);
-#pragma unroll
-        for (int i = 0; i < T::kFragM; ++i)
-#pragma unroll
-            for (int j = 0; j < T::kFragN; ++j) epi(row_base + i * 16, col_base + j * 16, acc[i][j]);
-    }
+    store_tile<T>(acc, epi, smem, m0, n0, tid);
 }
 
 // Host launcher: one workgroup per output tile.
@@ -221,45 +251,253 @@ inline void launch_gemm(const ALoad &al, const BLoad &bl, const Epi &epi, int M,
                        dim3(T::kThreads), 0, stream, al, bl, epi, M, N, K, tiles_n);
 }
 
+// ====================================================== LDS-DMA pipelined core
+// Operands that are plain bf16 rows (or 16-byte gathers of them) skip the
+// register round trip: buffer_load_dwordx4 ... lds writes each lane's 16 bytes
+// straight into LDS at M0 + 16 * lane, so a wave instruction fills 1 KiB of
+// the tile.  With registers out of the way, STAGES-1 k-tiles are in flight
+// while the matrix cores work on the current one, which is what the short
+// reductions of this path (K = 96 ... 3072, a handful of k-tiles per output
+// tile) need: one k-tile of look-ahead leaves the loop bound by memory latency.
+//
+// LDS rows hold BK bf16 with no padding.  To keep the 16-byte fragment reads
+// of 8 consecutive rows on distinct banks, chunk c of row r is stored in slot
+// c ^ swz(r); the DMA side applies the same permutation to the global chunk
+// each lane fetches, so the stored image is already swizzled.
+template <int BM_, int BN_, int BK_, int WM_, int WN_, int STAGES_>
+struct DmaTile {
+    static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_, kStages = STAGES_;
+    static constexpr int kThreads = WM * WN * kWave;
+    static constexpr int kWaveRows = BM / WM, kWaveCols = BN / WN;
+    static constexpr int kFragM = kWaveRows / 16, kFragN = kWaveCols / 16;
+    static_assert(BK == 32 || BK == 64 || BK == 128, "swizzle covers BK of 32, 64 or 128");
+    static_assert(kWaveRows % 16 == 0 && kWaveCols % 16 == 0, "wave tile must be 16-aligned");
+    static_assert(kStages >= 2 && kStages <= 4, "2 to 4 stages");
+};
+
+template <int BK>
+__device__ __forceinline__ int dma_swizzle(int r) {
+    return BK == 32 ? (r >> 1) & 3 : r & 7;
+}
+
+// s_waitcnt vmcnt(n) leaving lgkmcnt/expcnt alone (gfx9 encoding: vmcnt in
+// bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Workgroup barrier without the release/acquire fences of __syncthreads (which
+// would drain every outstanding DMA); the empty asm statements keep the
+// compiler from moving LDS accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, uint32_t bytes) {
+    // Raw buffer, 32-bit data format: offsets at or past `bytes` read as zero.
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)bytes, 0x00020000);
+}
+
+constexpr uint32_t kDmaOutOfRange = 0x80000000u;  // >= any num_records used here
+
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, bf16 *lds, uint32_t voffset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        rsrc, (__attribute__((address_space(3))) void *)(lds), 16, voffset, 0, 0, 0);
+}
+
+// Row-major bf16 operand X[R, K] (leading dimension ld elements, K % 8 == 0,
+// 16-byte aligned rows, R * ld * 2 < 2^31 bytes).  Rows past R and k past K
+// read as zero.
+template <int ROWS, int BK, int THREADS>
+struct DmaRowsBf16 {
+    static constexpr int kCpr = BK / 8, kWaves = THREADS / kWave;
+    static constexpr int kChunks = ROWS * kCpr;
+    static_assert(kChunks % (kWave * kWaves) == 0, "tile must split evenly over the waves");
+    static constexpr int kIssue = kChunks / (kWave * kWaves);  // DMA instructions per wave per stage
+    const bf16 *base;
+    int ld, rows, K;
+    int wave;
+    uint32_t row_off[kIssue];  // byte offset of the lane's row, or kDmaOutOfRange
+    int kcol[kIssue];          // first k of the lane's chunk within the tile
+
+    __device__ void setup(int r0, int tid) {
+        wave = tid / kWave;
+        const int lane = tid % kWave;
+#pragma unroll
+        for (int j = 0; j < kIssue; ++j) {
+            const int q = (j * kWaves + wave) * kWave + lane;
+            const int r = q / kCpr, slot = q % kCpr;
+            row_off[j] = r0 + r < rows ? (uint32_t)(r0 + r) * (uint32_t)ld * 2u : kDmaOutOfRange;
+            kcol[j] = 8 * (slot ^ dma_swizzle<BK>(r));
+        }
+    }
+    __device__ void issue(bf16 *lds, int k0) const {
+        const __amdgpu_buffer_rsrc_t rsrc = buffer_rsrc(base, (uint32_t)rows * (uint32_t)ld * 2u);
+#pragma unroll
+        for (int j = 0; j < kIssue; ++j) {
+            const int k = k0 + kcol[j];
+            const uint32_t off = (row_off[j] != kDmaOutOfRange && k < K) ? row_off[j] + 2u * k : kDmaOutOfRange;
+            dma16(rsrc, lds + (j * kWaves + wave) * kWave * 8, off);
+        }
+    }
+};
+
+template <int N>
+struct DmaWait {  // wait until at most n stages of P instructions are outstanding
+    template <int P>
+    __device__ static void stages(int n) {
+        if constexpr (N > 0) {
+            if (n >= N) { wait_vmcnt<N * P>(); return; }
+            DmaWait<N - 1>::template stages<P>(n);
+        } else {
+            wait_vmcnt<0>();
+        }
+    }
+};
+
+template <class T, class ALoad, class BLoad, class Epi>
+__global__ __launch_bounds__(T::kThreads) void gemm_dma_kernel(ALoad al, BLoad bl, Epi epi,
+                                                               int M, int N, int K, int tiles_n) {
+    constexpr int S = T::kStages;
+    constexpr int kA = T::BM * T::BK, kB = T::BN * T::BK;  // elements per stage
+    constexpr size_t kABBytes = (size_t)S * (kA + kB) * sizeof(bf16);
+    constexpr size_t kCBytes = epilogue_bytes<T, Epi>();
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[kABBytes > kCBytes ? kABBytes : kCBytes];
+    bf16 *sA = reinterpret_cast<bf16 *>(smem);
+    bf16 *sB = sA + S * kA;
+
+    const int pid = xcd_swizzle((int)blockIdx.x, (int)gridDim.x);
+    const int m0 = (pid / tiles_n) * T::BM, n0 = (pid % tiles_n) * T::BN;
+    const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / T::WN, wn = wave % T::WN;
+
+    al.setup(m0, tid);
+    bl.setup(n0, tid);
+
+    f32x4 acc[T::kFragM][T::kFragN];
+#pragma unroll
+    for (int i = 0; i < T::kFragM; ++i)
+#pragma unroll
+        for (int j = 0; j < T::kFragN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int nk = (K + T::BK - 1) / T::BK;
+#pragma unroll
+    for (int st = 0; st < S - 1; ++st)
+        if (st < nk) {
+            al.issue(sA + st * kA, st * T::BK);
+            bl.issue(sB + st * kB, st * T::BK);
+        }
+
+    // Fragment origins: row (lane & 15) of the wave's sub-tile; the 16-byte
+    // chunk for MFMA step kk is (kk / 8 + lane / 16) ^ swz(row), and swz only
+    // depends on row % 16, i.e. on the lane.
+    const int swz = dma_swizzle<T::BK>(lane & 15);
+    const int a_row = (wm * T::kWaveRows + (lane & 15)) * T::BK;
+    const int b_row = (wn * T::kWaveCols + (lane & 15)) * T::BK;
+    constexpr int kSteps = T::BK / 32;
+    int koff[kSteps];
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) koff[s] = 8 * ((4 * s + (lane >> 4)) ^ swz);
+
+    constexpr int P = ALoad::kIssue + BLoad::kIssue;
+    for (int kt = 0; kt < nk; ++kt) {
+        const int ahead = nk - 1 - kt;  // stages issued after this one
+        DmaWait<S - 2>::template stages<P>(ahead < S - 2 ? ahead : S - 2);
+        lds_barrier();
+        const int nxt = kt + S - 1;
+        if (nxt < nk) {
+            al.issue(sA + (nxt % S) * kA, nxt * T::BK);
+            bl.issue(sB + (nxt % S) * kB, nxt * T::BK);
+        }
+        const bf16 *a = sA + (kt % S) * kA + a_row;
+        const bf16 *b = sB + (kt % S) * kB + b_row;
+#pragma unroll
+        for (int s = 0; s < kSteps; ++s) {
+            bf16x8 af[T::kFragM], bfr[T::kFragN];
+#pragma unroll
+            for (int i = 0; i < T::kFragM; ++i)
+                af[i] = *reinterpret_cast<const bf16x8 *>(a + i * 16 * T::BK + koff[s]);
+#pragma unroll
+            for (int j = 0; j < T::kFragN; ++j)
+                bfr[j] = *reinterpret_cast<const bf16x8 *>(b + j * 16 * T::BK + koff[s]);
+#pragma unroll
+            for (int i = 0; i < T::kFragM; ++i)
+#pragma unroll
+                for (int j = 0; j < T::kFragN; ++j) acc[i][j] = mfma16(af[i], bfr[j], acc[i][j]);
+        }
+    }
+    __syncthreads();  // every wave is done with the stage buffers
+    store_tile<T>(acc, epi, smem, m0, n0, tid);
+}
+
+template <class T, class ALoad, class BLoad, class Epi>
+inline void launch_gemm_dma(const ALoad &al, const BLoad &bl, const Epi &epi, int M, int N, int K,
+                            hipStream_t stream) {
+    const int tiles_m = (M + T::BM - 1) / T::BM, tiles_n = (N + T::BN - 1) / T::BN;
+    hipLaunchKernelGGL((gemm_dma_kernel<T, ALoad, BLoad, Epi>), dim3(tiles_m * tiles_n),
+                       dim3(T::kThreads), 0, stream, al, bl, epi, M, N, K, tiles_n);
+}
+
 // ---------------------------------------------------------------- epilogues
 // Each is called with the fragment origin (row, col) of four consecutive rows
 // row..row+3 in one column; bounds are the epilogue's responsibility.
 
-// Row-vector epilogues (kRowVector) receive four consecutive columns of one
-// row through row4(); vector stores need ld % 4 == 0 and an aligned base,
-// otherwise they fall back to scalars.
+// Row-vector epilogues (kRowVector) work on quads of four consecutive columns:
+// column(col) gathers the per-column state once, rows<R>(row0, step, c, v)
+// then receives R rows row0 + i * step of that quad (rows ascending; bounds
+// are the epilogue's responsibility).  Vector accesses need ld % 4 == 0 and
+// 16-byte aligned bases, otherwise they fall back to scalars.
+struct ColQuad {
+    int col;
+    float4 b;
+};
+
+__device__ __forceinline__ float4 load_quad(const float *p, int col, int n) {
+    float4 r = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (!p || col >= n) return r;
+    if (col + 3 < n && ((uintptr_t)(p + col) & 15) == 0) return *reinterpret_cast<const float4 *>(p + col);
+    r.x = p[col];
+    if (col + 1 < n) r.y = p[col + 1];
+    if (col + 2 < n) r.z = p[col + 2];
+    if (col + 3 < n) r.w = p[col + 3];
+    return r;
+}
+
+__device__ __forceinline__ float4 add4(float4 a, float4 b) {
+    return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+}
+
 struct EpiRowsF32 {  // out[row*ld + col] = v (+bias) (ReLU)
     static constexpr bool kRowVector = true;
     float *out;
     const float *bias;
     int ld, M, N, relu;
-    __device__ void row4(int row, int col, float4 v) const {
-        if (row >= M || col >= N) return;
-        float y[4] = {v.x, v.y, v.z, v.w};
+    __device__ ColQuad column(int col) const { return ColQuad{col, load_quad(bias, col, N)}; }
+    template <int R>
+    __device__ void rows(int row0, int step, const ColQuad &c, const float4 (&v)[R]) const {
+        if (c.col >= N) return;
+        const bool vec = c.col + 3 < N && (ld & 3) == 0 && ((uintptr_t)out & 15) == 0;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            if (bias && col + e < N) y[e] += bias[col + e];
-            if (relu && y[e] < 0.0f) y[e] = 0.0f;
-        }
-        float *p = out + (size_t)row * ld + col;
-        if (col + 3 < N && (ld & 3) == 0 && ((uintptr_t)out & 15) == 0) {
-            *reinterpret_cast<float4 *>(p) = make_float4(y[0], y[1], y[2], y[3]);
-        } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                if (col + e < N) p[e] = y[e];
-        }
-    }
-    __device__ void operator()(int row, int col, f32x4 v) const {
-        if (col >= N) return;
-        const float b = bias ? bias[col] : 0.0f;
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-            if (row + r < M) {
-                float y = v[r] + b;
-                if (relu && y < 0.0f) y = 0.0f;
-                out[(size_t)(row + r) * ld + col] = y;
+        for (int i = 0; i < R; ++i) {
+            const int row = row0 + i * step;
+            if (row >= M) break;
+            float4 y = add4(v[i], c.b);
+            if (relu) {  // NaN passes through, as in the reference's ReLU
+                y.x = y.x < 0.f ? 0.f : y.x; y.y = y.y < 0.f ? 0.f : y.y;
+                y.z = y.z < 0.f ? 0.f : y.z; y.w = y.w < 0.f ? 0.f : y.w;
             }
+            float *p = out + (size_t)row * ld + c.col;
+            if (vec) {
+                *reinterpret_cast<float4 *>(p) = y;
+            } else {
+                const float t[4] = {y.x, y.y, y.z, y.w};
+                for (int e = 0; e < 4 && c.col + e < N; ++e) p[e] = t[e];
+            }
+        }
     }
 };
 
@@ -269,65 +507,61 @@ struct EpiRowsBf16 {  // out[row*ld + col] = bf16(act(v + bias)); ld % 4 == 0
     bf16 *out;
     const float *bias;
     int ld, M, N;
-    __device__ void row4(int row, int col, float4 v) const {
-        if (row >= M || col >= N) return;
-        float y[4] = {v.x, v.y, v.z, v.w};
-        bf16x4 o;
+    __device__ ColQuad column(int col) const { return ColQuad{col, load_quad(bias, col, N)}; }
+    template <int R>
+    __device__ void rows(int row0, int step, const ColQuad &c, const float4 (&v)[R]) const {
+        if (c.col >= N) return;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            float t = y[e] + (bias && col + e < N ? bias[col + e] : 0.0f);
-            if (GELU) t = gelu_erf(t);
-            o[e] = to_bf16(t);
-        }
-        bf16 *p = out + (size_t)row * ld + col;
-        if (col + 3 < N) {
-            *reinterpret_cast<bf16x4 *>(p) = o;
-        } else {
+        for (int i = 0; i < R; ++i) {
+            const int row = row0 + i * step;
+            if (row >= M) break;
+            const float4 y = add4(v[i], c.b);
+            const float t[4] = {y.x, y.y, y.z, y.w};
+            bf16x4 o;
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                if (col + e < N) p[e] = o[e];
-        }
-    }
-    __device__ void operator()(int row, int col, f32x4 v) const {
-        if (col >= N) return;
-        const float b = bias ? bias[col] : 0.0f;
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-            if (row + r < M) {
-                float y = v[r] + b;
-                if (GELU) y = gelu_erf(y);
-                out[(size_t)(row + r) * ld + col] = to_bf16(y);
+            for (int e = 0; e < 4; ++e) o[e] = to_bf16(GELU ? gelu_erf(t[e]) : t[e]);
+            bf16 *p = out + (size_t)row * ld + c.col;
+            if (c.col + 3 < N) {
+                *reinterpret_cast<bf16x4 *>(p) = o;
+            } else {
+                for (int e = 0; e < 4 && c.col + e < N; ++e) p[e] = o[e];
             }
+        }
     }
 };
 
-struct EpiResidualF32 {  // x[row*ld + col] += v + bias; ld % 4 == 0
+struct EpiResidualF32 {  // x[row*ld + col] += v + bias; ld % 4 == 0, x 16-byte aligned
     static constexpr bool kRowVector = true;
     float *x;
     const float *bias;
     int ld, M, N;
-    __device__ void row4(int row, int col, float4 v) const {
-        if (row >= M || col >= N) return;
-        float *p = x + (size_t)row * ld + col;
-        if (col + 3 < N) {
-            float4 a = *reinterpret_cast<const float4 *>(p);
-            const float4 b = bias ? *reinterpret_cast<const float4 *>(bias + col) : make_float4(0, 0, 0, 0);
-            a.x += v.x + b.x; a.y += v.y + b.y; a.z += v.z + b.z; a.w += v.w + b.w;
-            *reinterpret_cast<float4 *>(p) = a;
-        } else {
-            const float y[4] = {v.x, v.y, v.z, v.w};
-            for (int e = 0; e < 4 && col + e < N; ++e) p[e] = p[e] + (y[e] + (bias ? bias[col + e] : 0.0f));
-        }
-    }
-    __device__ void operator()(int row, int col, f32x4 v) const {
-        if (col >= N) return;
-        const float b = bias ? bias[col] : 0.0f;
+    __device__ ColQuad column(int col) const { return ColQuad{col, load_quad(bias, col, N)}; }
+    template <int R>
+    __device__ void rows(int row0, int step, const ColQuad &c, const float4 (&v)[R]) const {
+        if (c.col >= N) return;
+        if (c.col + 3 < N) {
+            float4 a[R];
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-            if (row + r < M) {
-                float *p = x + (size_t)(row + r) * ld + col;
-                *p = *p + (v[r] + b);
+            for (int i = 0; i < R; ++i) {
+                const int row = row0 + i * step;
+                a[i] = row < M ? *reinterpret_cast<const float4 *>(x + (size_t)row * ld + c.col)
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
             }
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                const int row = row0 + i * step;
+                if (row < M) *reinterpret_cast<float4 *>(x + (size_t)row * ld + c.col) = add4(a[i], add4(v[i], c.b));
+            }
+        } else {
+            const float b[4] = {c.b.x, c.b.y, c.b.z, c.b.w};
+            for (int i = 0; i < R; ++i) {
+                const int row = row0 + i * step;
+                if (row >= M) break;
+                const float t[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+                float *p = x + (size_t)row * ld + c.col;
+                for (int e = 0; e < 4 && c.col + e < N; ++e) p[e] = p[e] + (t[e] + b[e]);
+            }
+        }
     }
 };
 

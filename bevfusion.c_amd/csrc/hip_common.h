@@ -58,13 +58,14 @@ __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 acc) {
 // output it feeds.
 __device__ __forceinline__ float gelu_erf(float x) {
     const float z = fabsf(x) * 0.7071067811865475244f;
-    const float t = __frcp_rn(fmaf(0.3275911f, z, 1.0f));
+    const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, z, 1.0f));  // v_rcp_f32, 1 ulp
     float poly = fmaf(1.061405429f, t, -1.453152027f);
     poly = fmaf(poly, t, 1.421413741f);
     poly = fmaf(poly, t, -0.284496736f);
     poly = fmaf(poly, t, 0.254829592f);
     poly *= t;
-    const float e = exp2f(-z * z * 1.4426950408889634f);
+    // v_exp_f32 directly: an argument below -126 flushes to 0, where erf is 1.
+    const float e = __builtin_amdgcn_exp2f(-z * z * 1.4426950408889634f);
     const float erf_abs = fmaf(-poly, e, 1.0f);
     const float erf_x = x < 0.0f ? -erf_abs : erf_abs;
     return 0.5f * x * (1.0f + erf_x);

@@ -252,6 +252,12 @@ static int swin_build(bf_cuda_swin *s, const bf_model *model, size_t batches, si
                 x_elems = std::max(x_elems, t2 * 2 * kC[st]);
             }
         }
+        // The linears address their bf16 operands through 32-bit buffer offsets.
+        if (std::max(xn_elems, big_elems) * 2 >= (size_t(1) << 31)) {
+            fail(error, cap, "Swin batch too large: %zu images exceed the 2 GiB activation limit",
+                 batches);
+            return 0;
+        }
         const size_t x_bytes = (x_elems * 4 + 255) & ~size_t(255);
         const size_t xn_bytes = (xn_elems * 2 + 255) & ~size_t(255);
         const size_t big_bytes = (big_elems * 2 + 255) & ~size_t(255);
