@@ -109,16 +109,47 @@ void run_conv(const ConvLayer &l, const Src &src, const Epi &epi, hipStream_t s)
     launch_gemm<T>(al, bl, epi, g.M, l.co, g.K, s);
 }
 
-// Tiles from a sweep of the GEMM core on these shapes (MI355X): 128 x 128 for
-// the 256-channel maps at 32x88, 64 x 64 where M is small (level 1, 16x44,
-// and dtransform.6), narrow tiles for the 32 / 80-channel layers.
-using T256 = Tile<128, 128, 64, 2, 2>;  // 256 / 198 output channels at level 0
-using T64 = Tile<64, 64, 64, 2, 2>;     // level-1 convs and dtransform.6
-using T32 = Tile<128, 32, 32, 4, 1>;    // dtransform.3: 32 channels
-using T80 = Tile<64, 80, 64, 2, 1>;     // downsample: 80 channels
+// LDS-DMA pipeline for convs over plain or concatenated channels-last maps
+// whose channel counts are multiples of the k-tile (every 3x3 / 1x1 conv of
+// the FPN outputs and the depth trunk, and dtransform.6).
+template <class T, int K, class Epi>
+void run_conv_dma(const ConvLayer &l, const bf16 *a, int c0, const bf16 *b, int c1, const Epi &epi,
+                  hipStream_t s) {
+    const ConvGeom g = geom_of(l);
+    DmaConvNHWC<T::BM, T::BK, T::kThreads, K, K> al{a, b, c0, c1, g};
+    DmaRowsBf16<T::BN, T::BK, T::kThreads> bl{l.w, g.K, l.co, g.K};
+    launch_gemm_dma<T>(al, bl, epi, g.M, l.co, g.K, s);
+}
+
+// Tiles from sweeps of both cores on these shapes (MI355X).  DMA-fed: 64 x 128
+// for the 256-channel 3x3 convs at 32x88 and the depthnet.6 1x1, 64 x 64 at
+// level 1 (16x44), a two-wave 32 x 64 tile over 32-deep k-steps for
+// dtransform.6 (32 input channels).  Register-fed gathers (bilinear / depth
+// affine sources, 80-channel BEV maps): 128 x 128 / 64 x 64 for the lateral
+// 1x1s, narrow tiles for the 32 / 80-channel layers.
+using D256 = DmaTile<64, 128, 64, 2, 2, 2>;  // 3x3 256-channel convs and depthnet.6 at level 0
+using D64 = DmaTile<64, 64, 64, 2, 2, 2>;    // fpn_convs.1 at level 1
+using D32 = DmaTile<32, 64, 32, 1, 2, 4>;    // dtransform.6: 32 input channels
+using T256 = Tile<128, 128, 64, 2, 2>;       // lateral_convs.0
+using T64 = Tile<64, 64, 64, 2, 2>;          // lateral_convs.1
+using T32 = Tile<128, 32, 32, 4, 1>;         // dtransform.3: 32 output channels
+using T80 = Tile<64, 80, 64, 2, 1>;          // downsample: 80 channels
 
 EpiConvOut out_to(const ConvLayer &l, bf16 *nhwc, float *nchw = nullptr) {
     return EpiConvOut{nhwc, nchw, l.b, l.n * l.oh * l.ow, l.co, l.oh * l.ow, 1};
+}
+
+EpiConvNHWC nhwc_to(const ConvLayer &l, bf16 *nhwc) {
+    return EpiConvNHWC{nhwc, l.b, l.n * l.oh * l.ow, l.co};
+}
+
+// FPN output conv: channels-last only, or also NCHW fp32 for the boundary.
+template <class T>
+void fpn_conv(const ConvLayer &l, const bf16 *in, bf16 *nhwc, float *nchw, hipStream_t s) {
+    if (nchw)
+        run_conv_dma<T, 3>(l, in, 256, nullptr, 0, out_to(l, nhwc, nchw), s);
+    else
+        run_conv_dma<T, 3>(l, in, 256, nullptr, 0, nhwc_to(l, nhwc), s);
 }
 
 // FPN from NCHW fp32 Swin levels; FPN levels land channels-last in f0/f1 and,
@@ -132,13 +163,11 @@ void fpn_impl(bf_cuda_camera_neck *n, const float *s0, const float *s1, const fl
     pack_nhwc(s1, n->p1, B, 384, h1 * w1, s);
     pack_nhwc(s2, n->p2, B, 768, h2 * w2, s);
     run_conv<T64, 1, 1>(n->L[kLat1], SrcNHWCUpConcat{n->p1, n->p2, 384, 768, h1, w1, h2, w2},
-                        out_to(n->L[kLat1], n->t1), s);
-    run_conv<T64, 3, 3>(n->L[kFpn1], SrcNHWC{n->t1, 256, h1, w1},
-                        out_to(n->L[kFpn1], n->f1, out1), s);
+                        nhwc_to(n->L[kLat1], n->t1), s);
+    fpn_conv<D64>(n->L[kFpn1], n->t1, n->f1, out1, s);
     run_conv<T256, 1, 1>(n->L[kLat0], SrcNHWCUpConcat{n->p0, n->f1, 192, 256, h, w, h1, w1},
-                         out_to(n->L[kLat0], n->t0), s);
-    run_conv<T256, 3, 3>(n->L[kFpn0], SrcNHWC{n->t0, 256, h, w},
-                         out_to(n->L[kFpn0], n->f0, out0), s);
+                         nhwc_to(n->L[kLat0], n->t0), s);
+    fpn_conv<D256>(n->L[kFpn0], n->t0, n->f0, out0, s);
 }
 
 // Depth head from the channels-last fpn0 in n->f0.
@@ -146,14 +175,13 @@ void depth_impl(bf_cuda_camera_neck *n, const float *depth, float *logits, float
                 hipStream_t s) {
     const int h = (int)n->h, w = (int)n->w;
     run_conv<T32, 5, 5>(n->L[kDt1], SrcNHWCDepthAffine{depth, n->dt0_w, n->dt0_b, 8 * h, 8 * w},
-                        out_to(n->L[kDt1], n->e1), s);
-    run_conv<T64, 5, 5>(n->L[kDt2], SrcNHWC{n->e1, 32, 2 * h, 2 * w}, out_to(n->L[kDt2], n->e2), s);
-    run_conv<T256, 3, 3>(n->L[kDn0], SrcNHWCConcat{n->e2, n->f0, 64, 256, h, w},
-                         out_to(n->L[kDn0], n->d0), s);
-    run_conv<T256, 3, 3>(n->L[kDn3], SrcNHWC{n->d0, 256, h, w}, out_to(n->L[kDn3], n->d1), s);
+                        nhwc_to(n->L[kDt1], n->e1), s);
+    run_conv_dma<D32, 5>(n->L[kDt2], n->e1, 32, nullptr, 0, nhwc_to(n->L[kDt2], n->e2), s);
+    run_conv_dma<D256, 3>(n->L[kDn0], n->e2, 64, n->f0, 256, nhwc_to(n->L[kDn0], n->d0), s);
+    run_conv_dma<D256, 3>(n->L[kDn3], n->d0, 256, nullptr, 0, nhwc_to(n->L[kDn3], n->d1), s);
     const ConvLayer &l = n->L[kDn6];
-    run_conv<T256, 1, 1>(l, SrcNHWC{n->d1, 256, h, w},
-                         EpiSplitDepth{logits, context, l.b, l.n * h * w, h * w, 118, 80}, s);
+    run_conv_dma<D256, 1>(l, n->d1, 256, nullptr, 0,
+                          EpiSplitDepth{logits, context, l.b, l.n * h * w, h * w, 118, 80}, s);
 }
 
 int build(bf_cuda_camera_neck *n, const bf_model *model, char *error, size_t cap) {
@@ -307,8 +335,8 @@ extern "C" int bf_cuda_camera_downsample_forward(bf_cuda_camera_neck *n, const f
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int bh = (int)n->bev_h, bw = (int)n->bev_w;
     pack_nhwc(input, n->bp, 1, 80, bh * bw, s);
-    run_conv<T80, 3, 3>(n->L[kDs0], SrcNHWC{n->bp, 80, bh, bw}, out_to(n->L[kDs0], n->b0), s);
-    run_conv<T80, 3, 3>(n->L[kDs1], SrcNHWC{n->b0, 80, bh, bw}, out_to(n->L[kDs1], n->b1), s);
+    run_conv<T80, 3, 3>(n->L[kDs0], SrcNHWC{n->bp, 80, bh, bw}, nhwc_to(n->L[kDs0], n->b0), s);
+    run_conv<T80, 3, 3>(n->L[kDs1], SrcNHWC{n->b0, 80, bh, bw}, nhwc_to(n->L[kDs1], n->b1), s);
     const ConvLayer &l = n->L[kDs2];
     run_conv<T80, 3, 3>(l, SrcNHWC{n->b1, 80, bh / 2, bw / 2},
                         EpiTransposeXY{output, l.b, l.oh * l.ow, 80, l.oh, l.ow}, s);
@@ -327,16 +355,16 @@ extern "C" int bfhip_camera_profile_layer(bf_cuda_camera_neck *n, int layer, voi
     const ConvLayer &l = n->L[layer];
     // Same kernels and shapes as the forward entry points, on context buffers.
     switch (layer) {
-        case kLat1: run_conv<T64, 1, 1>(l, SrcNHWCUpConcat{n->p1, n->p2, 384, 768, h1, w1, h2, w2}, out_to(l, n->t1), s); break;
-        case kFpn1: run_conv<T64, 3, 3>(l, SrcNHWC{n->t1, 256, h1, w1}, out_to(l, n->f1), s); break;
-        case kLat0: run_conv<T256, 1, 1>(l, SrcNHWCUpConcat{n->p0, n->f1, 192, 256, h, w, h1, w1}, out_to(l, n->t0), s); break;
-        case kFpn0: run_conv<T256, 3, 3>(l, SrcNHWC{n->t0, 256, h, w}, out_to(l, n->f0), s); break;
-        case kDt2: run_conv<T64, 5, 5>(l, SrcNHWC{n->e1, 32, 2 * h, 2 * w}, out_to(l, n->e2), s); break;
-        case kDn0: run_conv<T256, 3, 3>(l, SrcNHWCConcat{n->e2, n->f0, 64, 256, h, w}, out_to(l, n->d0), s); break;
-        case kDn3: run_conv<T256, 3, 3>(l, SrcNHWC{n->d0, 256, h, w}, out_to(l, n->d1), s); break;
-        case kDs0: run_conv<T80, 3, 3>(l, SrcNHWC{n->bp, 80, bh, bw}, out_to(l, n->b0), s); break;
-        case kDs1: run_conv<T80, 3, 3>(l, SrcNHWC{n->b0, 80, bh, bw}, out_to(l, n->b1), s); break;
-        case kDs2: run_conv<T80, 3, 3>(l, SrcNHWC{n->b1, 80, bh / 2, bw / 2}, out_to(l, n->b0), s); break;
+        case kLat1: run_conv<T64, 1, 1>(l, SrcNHWCUpConcat{n->p1, n->p2, 384, 768, h1, w1, h2, w2}, nhwc_to(l, n->t1), s); break;
+        case kFpn1: fpn_conv<D64>(l, n->t1, n->f1, nullptr, s); break;
+        case kLat0: run_conv<T256, 1, 1>(l, SrcNHWCUpConcat{n->p0, n->f1, 192, 256, h, w, h1, w1}, nhwc_to(l, n->t0), s); break;
+        case kFpn0: fpn_conv<D256>(l, n->t0, n->f0, nullptr, s); break;
+        case kDt2: run_conv_dma<D32, 5>(l, n->e1, 32, nullptr, 0, nhwc_to(l, n->e2), s); break;
+        case kDn0: run_conv_dma<D256, 3>(l, n->e2, 64, n->f0, 256, nhwc_to(l, n->d0), s); break;
+        case kDn3: run_conv_dma<D256, 3>(l, n->d0, 256, nullptr, 0, nhwc_to(l, n->d1), s); break;
+        case kDs0: run_conv<T80, 3, 3>(l, SrcNHWC{n->bp, 80, bh, bw}, nhwc_to(l, n->b0), s); break;
+        case kDs1: run_conv<T80, 3, 3>(l, SrcNHWC{n->b0, 80, bh, bw}, nhwc_to(l, n->b1), s); break;
+        case kDs2: run_conv<T80, 3, 3>(l, SrcNHWC{n->b1, 80, bh / 2, bw / 2}, nhwc_to(l, n->b0), s); break;
         default: break;
     }
     return launch_ok(error, cap, "launch HIP camera profiling layer");

@@ -346,6 +346,86 @@ struct LoadConvNHWC {
     }
 };
 
+// LDS-DMA gather of channels-last taps for DmaTile pipelines: the A operand of
+// a conv over one NHWC map, or over the channel concat of two maps of the same
+// size (channels [0, C0) from a, [C0, C0 + C1) from b).  C0 and C1 are
+// multiples of BK, so one k-tile lies inside one tap of one source: the tap
+// and the source are uniform per stage and each lane moves one 16-byte chunk
+// of 8 channels.  Taps outside the map read as zero through an out-of-range
+// buffer offset.  Each source must span < 2 GiB.
+template <int ROWS, int BK, int THREADS, int KH, int KW>
+struct DmaConvNHWC {
+    static constexpr int kCpr = BK / 8, kWaves = THREADS / kWave;
+    static constexpr int kChunks = ROWS * kCpr;
+    static_assert(kChunks % (kWave * kWaves) == 0, "tile must split evenly over the waves");
+    static constexpr int kIssue = kChunks / (kWave * kWaves);
+    const bf16 *a, *b;
+    int C0, C1;
+    ConvGeom g;
+    int wave;
+    int pix[kIssue];  // n * IH * IW of the lane's output pixel, or -1 past M
+    int iy0[kIssue], ix0[kIssue];
+    int cofs[kIssue];  // channel offset of the lane's chunk within the k-tile
+
+    __device__ void setup(int m0, int tid) {
+        wave = tid / kWave;
+        const int lane = tid % kWave, ohw = g.OH * g.OW;
+#pragma unroll
+        for (int j = 0; j < kIssue; ++j) {
+            const int q = (j * kWaves + wave) * kWave + lane;
+            const int r = q / kCpr, slot = q % kCpr, m = m0 + r;
+            const int mm = m < g.M ? m : 0;
+            const int n = mm / ohw, p = mm - n * ohw, oy = p / g.OW, ox = p - oy * g.OW;
+            pix[j] = m < g.M ? n * g.IH * g.IW : -1;
+            iy0[j] = oy * g.SH - g.PH;
+            ix0[j] = ox * g.SW - g.PW;
+            cofs[j] = 8 * (slot ^ dma_swizzle<BK>(r));
+        }
+    }
+    __device__ void issue(bf16 *lds, int k0) const {
+        const int ci = C0 + C1, tap = k0 / ci, cb = k0 - tap * ci;
+        const int ky = tap / KW, kx = tap - ky * KW;
+        const bool hi = cb >= C0;
+        const int cs = hi ? C1 : C0, c0 = hi ? cb - C0 : cb;
+        const uint32_t pixels = (uint32_t)g.N * g.IH * g.IW;
+        const __amdgpu_buffer_rsrc_t rsrc = buffer_rsrc(hi ? b : a, pixels * (uint32_t)cs * 2u);
+#pragma unroll
+        for (int j = 0; j < kIssue; ++j) {
+            const int iy = iy0[j] + ky, ix = ix0[j] + kx;
+            const bool in = pix[j] >= 0 && (unsigned)iy < (unsigned)g.IH && (unsigned)ix < (unsigned)g.IW;
+            const uint32_t off = in ? (uint32_t)(((pix[j] + iy * g.IW + ix) * cs + c0 + cofs[j]) * 2)
+                                    : kDmaOutOfRange;
+            dma16(rsrc, lds + (j * kWaves + wave) * kWave * 8, off);
+        }
+    }
+};
+
+// Row-vector conv epilogue for channels-last bf16 maps: out[row][col] =
+// bf16(relu(v + bias)), Co % 4 == 0.
+struct EpiConvNHWC {
+    static constexpr bool kRowVector = true;
+    bf16 *out;
+    const float *bias;
+    int M, Co;
+    __device__ ColQuad column(int col) const { return ColQuad{col, load_quad(bias, col, Co)}; }
+    template <int R>
+    __device__ void rows(int row0, int step, const ColQuad &c, const float4 (&v)[R]) const {
+        if (c.col >= Co) return;
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            const int row = row0 + i * step;
+            if (row >= M) break;
+            const float4 y = add4(v[i], c.b);
+            bf16x4 o;
+            o[0] = to_bf16(y.x < 0.f ? 0.f : y.x);
+            o[1] = to_bf16(y.y < 0.f ? 0.f : y.y);
+            o[2] = to_bf16(y.z < 0.f ? 0.f : y.z);
+            o[3] = to_bf16(y.w < 0.f ? 0.f : y.w);
+            *reinterpret_cast<bf16x4 *>(out + (size_t)row * Co + c.col) = o;
+        }
+    }
+};
+
 // Conv epilogue writing bias+ReLU results as NHWC bf16 (internal maps) and/or
 // NCHW fp32 (boundary outputs); either pointer may be null.
 struct EpiConvOut {
