@@ -51,6 +51,9 @@ SIGNATURES = {
     "bf_cuda_camera_downsample_forward": (_i, [_vp, _vp, _vp, _vp, C.c_char_p, _sz]),
     "bfhip_swin_profile_op": (_i, [_vp, _i, _i, _i, _vp, C.c_char_p, _sz]),
     "bfhip_camera_profile_layer": (_i, [_vp, _i, _vp, C.c_char_p, _sz]),
+    "bfhip_debug_window_map": (_i, [_i, _i, _i, _i, _vp, _vp, _vp, C.c_char_p, _sz]),
+    "bfhip_debug_window_attention": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp,
+                                          C.c_char_p, _sz]),
 }
 
 SWIN_OPS = ("ln1", "qkv", "attention", "proj", "ln2", "fc1", "fc2", "merge")
@@ -211,6 +214,43 @@ def conv2d_raw(desc, x, w, b, out, stream=None):
     err = _err()
     ok = hip_lib().bf_cuda_conv2d_f32(C.byref(desc), x, w, b, out, _stream(stream), err, 512)
     return bool(ok), err.value.decode(errors="replace")
+
+
+def window_map(batches, height, width, shift, device, stream=None):
+    """Device window partition (include/bfhip_debug.h): (token, label) int32."""
+    torch = _torch()
+    n = batches * (-(-height // 7)) * (-(-width // 7)) * 49
+    token = torch.empty(n, dtype=torch.int32, device=device)
+    label = torch.empty(n, dtype=torch.int32, device=device)
+    err = _err()
+    _check(hip_lib().bfhip_debug_window_map(batches, height, width, shift,
+                                            _vp(token.data_ptr()), _vp(label.data_ptr()),
+                                            _stream(stream), err, 512), err,
+           "bfhip_debug_window_map")
+    return token, label
+
+
+def window_attention(qkv, qkv_bias, bias_mat, batches, height, width, heads, shift, out=None,
+                     stream=None):
+    """Production window-attention kernel on caller buffers (include/bfhip_debug.h):
+    qkv bf16 [tokens, 96*heads], qkv_bias fp32 [96*heads], bias_mat fp32
+    [heads, 49, 49]; returns out bf16 [tokens, 32*heads]."""
+    torch = _torch()
+    c = 32 * heads
+    tokens = batches * height * width
+    if (qkv.dtype != torch.bfloat16 or tuple(qkv.shape) != (tokens, 3 * c)
+            or not qkv.is_contiguous()):
+        raise BfHipError("qkv must be a contiguous bf16 [tokens, 3C] tensor")
+    if tuple(qkv_bias.shape) != (3 * c,) or tuple(bias_mat.shape) != (heads, 49, 49):
+        raise BfHipError("qkv_bias must be [3C] and bias_mat [heads, 49, 49]")
+    out = out if out is not None else torch.zeros((tokens, c), dtype=torch.bfloat16,
+                                                  device=qkv.device)
+    err = _err()
+    _check(hip_lib().bfhip_debug_window_attention(
+        _vp(qkv.data_ptr()), _ptr(qkv_bias), _ptr(bias_mat), _vp(out.data_ptr()), batches,
+        height, width, c, heads, shift, _stream(stream), err, 512), err,
+        "bfhip_debug_window_attention")
+    return out
 
 
 class Swin:

@@ -14,6 +14,7 @@
 // proj GEMM(+bias, += into x) -> LN2 -> fc1 GEMM(+bias, GELU, bf16) ->
 // fc2 GEMM(+bias, += into x).
 #include "bf_cuda_swin.h"
+#include "bfhip_debug.h"
 #include "bfhip_profile.h"
 #include "conv_core.h"
 #include "host_util.h"
@@ -389,4 +390,36 @@ extern "C" int bfhip_swin_profile_op(bf_cuda_swin *s, int stage, int block, int 
     if (op == BFHIP_SWIN_MERGE) merge_op(s, stage, st);
     else block_op(s, stage, block, op, st);
     return launch_ok(error, cap, "launch HIP Swin profiling op");
+}
+
+extern "C" int bfhip_debug_window_map(int batches, int height, int width, int shift, int *token,
+                                      int *label, void *stream, char *error, size_t cap) {
+    if (!token || !label || batches <= 0 || height <= 0 || width <= 0 || shift < 0 || shift >= 7)
+        return fail(error, cap, "invalid window-map probe");
+    const long long wy_n = (height + 6) / 7, wx_n = (width + 6) / 7;
+    const long long total = (long long)batches * wy_n * wx_n * 49;
+    if (total > INT_MAX || (long long)batches * height * width > INT_MAX)
+        return fail(error, cap, "window-map probe is too large");
+    hipLaunchKernelGGL(window_map_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                       reinterpret_cast<hipStream_t>(stream), token, label, batches, height, width,
+                       (int)wy_n, (int)wx_n, shift);
+    return launch_ok(error, cap, "launch window-map probe");
+}
+
+extern "C" int bfhip_debug_window_attention(const void *qkv, const float *qkv_bias,
+                                            const float *bias_mat, void *out, int batches,
+                                            int height, int width, int channels, int heads,
+                                            int shift, void *stream, char *error, size_t cap) {
+    if (!qkv || !qkv_bias || !bias_mat || !out || batches <= 0 || height <= 0 || width <= 0 ||
+        heads <= 0 || channels != 32 * heads || shift < 0 || shift >= 7)
+        return fail(error, cap, "invalid window-attention probe");
+    const long long wy_n = (height + 6) / 7, wx_n = (width + 6) / 7;
+    const long long items = (long long)batches * wy_n * wx_n * heads;
+    if (items > INT_MAX || (long long)batches * height * width * 3 * channels > INT_MAX)
+        return fail(error, cap, "window-attention probe is too large");
+    hipLaunchKernelGGL(window_attention_kernel, dim3((unsigned)((items + kAttnWaves - 1) / kAttnWaves)),
+                       dim3(64 * kAttnWaves), 0, reinterpret_cast<hipStream_t>(stream),
+                       static_cast<const bf16 *>(qkv), qkv_bias, bias_mat, static_cast<bf16 *>(out),
+                       height, width, channels, heads, (int)wy_n, (int)wx_n, shift, (int)items);
+    return launch_ok(error, cap, "launch window-attention probe");
 }

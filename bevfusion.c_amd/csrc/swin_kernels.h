@@ -195,6 +195,19 @@ __device__ __forceinline__ int window_label(int t, int wy, int wx, int Hp, int W
     return 3 * ry + rx;
 }
 
+// Index-map probe: the window_token / window_label values of every window
+// token, as the attention kernel computes them.
+static __global__ __launch_bounds__(256) void window_map_kernel(int *token, int *label, int batches,
+                                                              int H, int W, int wy_n, int wx_n,
+                                                              int shift) {
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= batches * wy_n * wx_n * 49) return;
+    const int t = idx % 49, win = idx / 49;
+    const int wx = win % wx_n, t1 = win / wx_n, wy = t1 % wy_n, n = t1 / wy_n;
+    token[idx] = window_token(t, n, wy, wx, H, W, wy_n * 7, wx_n * 7, shift);
+    label[idx] = window_label(t, wy, wx, wy_n * 7, wx_n * 7, shift);
+}
+
 // One wave64 per (window, head) with head dim 32: Q, K (rows) and V^T are
 // staged in LDS as bf16 with the 49 tokens padded to 64; S^T = K Q^T is 16
 // MFMAs, the fp32 softmax over keys runs on the accumulator registers (the

@@ -1,0 +1,48 @@
+/*
+ * Index-map probes of libbfhip.so.  These have no counterpart in the
+ * reference: they let a test compare the integer work of the Swin window path
+ * bit for bit against the CPU oracle, on the device code the forward uses.
+ *
+ *   bfhip_debug_window_map
+ *       For every window (n, wy, wx) of a [batches, height, width] token grid
+ *       (padded up to multiples of 7, cyclic shift `shift`) and window token
+ *       t < 49, writes at [((n*wy_n + wy)*wx_n + wx)*49 + t]:
+ *         token[] = the source token row n*H*W + sy*W + sx, or -1 when the
+ *                   padded source lies outside the map (a zero row);
+ *         label[] = the shifted-window region label 3*ry + rx.
+ *       Same device functions as the attention kernel (reference
+ *       gather_windows_kernel / mask_region_device, src/cuda_swin.cu:120-134;
+ *       cyclic_source / mask_region, src/swin.c:106-117).
+ *
+ *   bfhip_debug_window_attention
+ *       Launches the production window-attention kernel on caller buffers:
+ *       qkv bf16 [tokens, 3C] (token-major, tokens = batches*height*width),
+ *       qkv_bias fp32 [3C], bias_mat fp32 [heads, 49, 49] (relative-position
+ *       bias already gathered), out bf16 [tokens, C].  C = 32 * heads.
+ *
+ * All pointers are device pointers; stream is a hipStream_t.  Returns 1 on
+ * success, 0 with a message in error[0..error_cap).
+ */
+#ifndef BFHIP_DEBUG_H
+#define BFHIP_DEBUG_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+int bfhip_debug_window_map(int batches, int height, int width, int shift,
+                           int *token_device, int *label_device, void *stream,
+                           char *error, size_t error_cap);
+
+int bfhip_debug_window_attention(const void *qkv_bf16_device, const float *qkv_bias_device,
+                                 const float *bias_mat_device, void *out_bf16_device,
+                                 int batches, int height, int width, int channels, int heads,
+                                 int shift, void *stream, char *error, size_t error_cap);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

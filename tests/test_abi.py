@@ -13,7 +13,8 @@ import re
 import bfhip
 
 ROOT = pathlib.Path(__file__).resolve().parent.parent
-HEADERS = ["bf_cuda_ops.h", "bf_cuda_swin.h", "bf_cuda_camera.h", "bfhip_profile.h"]
+HEADERS = ["bf_cuda_ops.h", "bf_cuda_swin.h", "bf_cuda_camera.h", "bfhip_profile.h",
+           "bfhip_debug.h"]
 
 
 def declared(header):
@@ -25,7 +26,7 @@ def declared(header):
 def test_every_declared_entry_point_is_exported():
     lib = bfhip.hip_lib()
     names = set().union(*(declared(h) for h in HEADERS))
-    assert len(names) == 15
+    assert len(names) == 17
     assert names == set(bfhip.SIGNATURES)
     missing = [n for n in sorted(names) if not hasattr(lib, n)]
     assert not missing, missing
@@ -88,3 +89,20 @@ def test_contexts_reject_invalid_contracts(tmp_path):
     assert not lib.bf_cuda_swin_forward(None, s, s, s, s, None, e, 256)
     assert not lib.bf_cuda_camera_downsample_forward(None, s, s, None, e, 256)
     assert not lib.bf_cuda_camera_neck_forward(None, s, s, s, s, s, s, None, e, 256)
+
+
+def test_index_probes_reject_invalid():
+    lib = bfhip.hip_lib()
+    e = _err()
+    s = C.c_void_p(1)
+    assert lib.bfhip_debug_window_map(1, 7, 7, 7, s, s, None, e, 256) == 0
+    assert b"invalid" in e.value
+    assert lib.bfhip_debug_window_map(0, 7, 7, 3, s, s, None, e, 256) == 0
+    assert lib.bfhip_debug_window_map(1, 7, 7, 3, None, s, None, e, 256) == 0
+    # channels must be 32 per head
+    assert lib.bfhip_debug_window_attention(s, s, s, s, 1, 7, 7, 64, 3, 0, None, e, 256) == 0
+    assert b"invalid" in e.value
+    assert lib.bfhip_debug_window_attention(s, s, s, s, 1, 7, 7, 96, 3, 7, None, e, 256) == 0
+    assert lib.bfhip_debug_window_attention(s, s, s, s, 70000, 7000, 7000, 96, 3, 3, None, e,
+                                            256) == 0
+    assert b"too large" in e.value
