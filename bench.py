@@ -110,6 +110,8 @@ def swin_op_cost(stage, op, b=6):
         return 2.0 * t * c * 4 * c, t * c * 2 + 4 * c * c * 2 + t * 4 * c * 2
     if op == "fc2":
         return 2.0 * t * 4 * c * c, t * 4 * c * 2 + 4 * c * c * 2 + 2 * t * c * 4
+    if op == "mlp":  # fused LN2 -> fc1 -> GELU -> fc2 -> residual (+ next LN1)
+        return 4.0 * t * c * 4 * c, t * c * 4 * 2 + t * c * 2 + 8 * c * c * 2
     if op == "merge":
         h2, w2 = SWIN_STAGES[stage + 1][:2]
         t2 = b * h2 * w2
@@ -137,16 +139,39 @@ def roofline_entry(name, avg_s, per_frame, flops, nbytes):
             "tflops": round(flops / avg_s / 1e12, 1), "gbs": round(nbytes / avg_s / 1e9, 1)}
 
 
+def fused_stages(swin, stream):
+    """Stages whose blocks run the fused MLP kernel (the library refuses
+    their separate fc1 op)."""
+    import bfhip
+    out = []
+    for st in range(4):
+        try:
+            swin.profile_op(st, 0, "mlp", stream)
+            out.append(st)
+        except bfhip.BfHipError:
+            pass
+    return out
+
+
 def time_kernels(swin, neck, stream, reps=20, only=()):
     """Time single ops of the path with HIP events on the stream they are
     launched on; returns roofline entries sorted by time per frame."""
     import torch
+    import bfhip
     cands = []
+    fused = fused_stages(swin, stream)
     for st in range(4):
         depth = SWIN_STAGES[st][4]
-        for op in ("ln1", "qkv", "attention", "proj", "ln2", "fc1", "fc2"):
+        for op in ("ln1", "qkv", "attention", "proj", "ln2", "fc1", "fc2", "mlp"):
+            try:  # ops a stage does not launch are refused by the library
+                swin.profile_op(st, 0, op, stream)
+            except bfhip.BfHipError:
+                continue
+            # LN1 runs once per stage when the previous block's fused MLP
+            # already produced it.
+            per_frame = 1 if (op == "ln1" and st in fused) else depth
             cands.append((f"swin.s{st}.{op}", lambda st=st, op=op: swin.profile_op(st, 0, op, stream),
-                          depth, swin_op_cost(st, op)))
+                          per_frame, swin_op_cost(st, op)))
         if st < 3:
             cands.append((f"swin.s{st}.merge", lambda st=st: swin.profile_op(st, 0, "merge", stream),
                           1, swin_op_cost(st, "merge")))

@@ -56,7 +56,7 @@ SIGNATURES = {
                                           C.c_char_p, _sz]),
 }
 
-SWIN_OPS = ("ln1", "qkv", "attention", "proj", "ln2", "fc1", "fc2", "merge")
+SWIN_OPS = ("ln1", "qkv", "attention", "proj", "ln2", "fc1", "fc2", "merge", "mlp")
 
 MODEL_SIGNATURES = {
     "bf_model_open": (_i, [C.c_char_p, C.POINTER(_vp), C.c_char_p, _sz]),

@@ -51,24 +51,21 @@ __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 acc) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
 }
 
-// Exact-erf GELU 0.5*x*(1 + erf(x/sqrt(2))) with erf from Abramowitz & Stegun,
-// Handbook of Mathematical Functions, formula 7.1.26 (|error| <= 1.5e-7 for
-// all x; odd symmetry for x < 0): one reciprocal, one exp2 and five FMAs
-// instead of a full-precision erff, well inside the bf16 rounding of the
-// output it feeds.
-__device__ __forceinline__ float gelu_erf(float x) {
-    const float z = fabsf(x) * 0.7071067811865475244f;
-    const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, z, 1.0f));  // v_rcp_f32, 1 ulp
-    float poly = fmaf(1.061405429f, t, -1.453152027f);
-    poly = fmaf(poly, t, 1.421413741f);
-    poly = fmaf(poly, t, -0.284496736f);
-    poly = fmaf(poly, t, 0.254829592f);
-    poly *= t;
-    // v_exp_f32 directly: an argument below -126 flushes to 0, where erf is 1.
-    const float e = __builtin_amdgcn_exp2f(-z * z * 1.4426950408889634f);
-    const float erf_abs = fmaf(-poly, e, 1.0f);
-    const float erf_x = x < 0.0f ? -erf_abs : erf_abs;
-    return 0.5f * x * (1.0f + erf_x);
+// GELU 0.5*x*(1 + erf(x/sqrt(2))) (the reference's exact-erf form,
+// kernels_ref.c:448-452) evaluated as x * sigmoid(x*(a + b*x^2 + c*x^4)), with
+// (a, b, c) a minimax fit to the exact-erf GELU over [-10, 10] (x clamped
+// there, so the quartic cannot change sign).  Evaluated in fp32 as below the
+// absolute error is <= 2.6e-5 for every x, and the relative error <= 1.2e-3
+// wherever |GELU(x)| > 0.01: below the half-ulp (2^-9) of the bf16 value it
+// feeds.  Cost: 7 VALU + v_exp_f32 + v_rcp_f32 (vs 16 + 2 for a rational erf).
+// The constants carry the -log2(e) of sigmoid(u) = 1 / (1 + 2^(-u*log2 e)).
+__device__ __forceinline__ float gelu(float x) {
+    const float xc = __builtin_amdgcn_fmed3f(x, -10.0f, 10.0f);
+    const float t = xc * xc;
+    float p = fmaf(t, 1.014263055e-03f, -1.067757240e-01f);
+    p = fmaf(t, p, -2.301121339e+00f);
+    const float e = __builtin_amdgcn_exp2f(xc * p);  // in [2^-29, 2^29]: no overflow
+    return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
 // Rows of the same LayerNorm live in a power-of-two group of lanes.

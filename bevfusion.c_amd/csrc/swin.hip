@@ -10,9 +10,12 @@
 // and scatters its output back the same way, so QKV and proj run as plain
 // token GEMMs over B*H*W rows instead of windows*49 rows.
 //
-// Per block (7 launches): LN1 -> QKV GEMM(+bias, bf16) -> window attention ->
+// Per block: LN1 -> QKV GEMM(+bias, bf16) -> window attention ->
 // proj GEMM(+bias, += into x) -> LN2 -> fc1 GEMM(+bias, GELU, bf16) ->
-// fc2 GEMM(+bias, += into x).
+// fc2 GEMM(+bias, += into x).  Stage 0 (C = 96) runs LN2 -> fc1 -> GELU ->
+// fc2 -> residual as one fused kernel whose hidden layer stays on chip
+// (swin_mlp.h); it also writes the next block's LN1 output, so only the first
+// block of the stage launches LN1.
 #include "bf_cuda_swin.h"
 #include "bfhip_debug.h"
 #include "bfhip_profile.h"
@@ -20,6 +23,7 @@
 #include "host_util.h"
 #include "linear.h"
 #include "swin_kernels.h"
+#include "swin_mlp.h"
 
 #include <algorithm>
 #include <climits>
@@ -34,13 +38,20 @@ constexpr int kC[4] = {96, 192, 384, 768};
 constexpr int kHeads[4] = {3, 6, 12, 24};
 constexpr int kDepth[4] = {2, 2, 6, 2};
 
+// Fused-MLP configuration of stage 0: one 16-token fragment per wave, four
+// waves, three weight chunks in flight (measured best on MI355X at 6x256x704).
+using MlpS0 = MlpCfg<96, 1, 4, 3>;
+constexpr bool kFusedMlp[4] = {true, false, false, false};
+
 struct BlockW {
     const float *n1s, *n1b, *n2s, *n2b, *qkv_b, *proj_b, *fc1_b, *fc2_b, *bias_mat;
     const bf16 *qkv_w, *proj_w, *fc1_w, *fc2_w;
+    const bf16 *mlp_w;  // fc1/fc2 packed for the fused MLP (fused stages only)
 };
 
 struct BlockOff {
     size_t n1s, n1b, n2s, n2b, qkv_b, proj_b, fc1_b, fc2_b, bias_mat, qkv_w, proj_w, fc1_w, fc2_w;
+    size_t mlp_w;
 };
 
 }  // namespace
@@ -193,6 +204,12 @@ static int swin_build(bf_cuda_swin *s, const bf_model *model, size_t batches, si
             o.proj_w = arena.add_bf16(proj_w, (size_t)c * c);
             o.fc1_w = arena.add_bf16(fc1_w, (size_t)4 * c * c);
             o.fc2_w = arena.add_bf16(fc2_w, (size_t)4 * c * c);
+            o.mlp_w = 0;
+            if (kFusedMlp[st]) {
+                std::vector<uint16_t> packed((size_t)8 * c * c);
+                pack_mlp_weights<MlpS0>(fc1_w, fc2_w, packed.data(), bf16_bits);
+                o.mlp_w = arena.add(packed.data(), packed.size() * 2);
+            }
         }
     }
     for (int st = 0; st < 3; ++st) {
@@ -234,6 +251,7 @@ static int swin_build(bf_cuda_swin *s, const bf_model *model, size_t batches, si
                 w.fc2_b = F(o.fc2_b); w.bias_mat = F(o.bias_mat);
                 w.qkv_w = H(o.qkv_w); w.proj_w = H(o.proj_w); w.fc1_w = H(o.fc1_w);
                 w.fc2_w = H(o.fc2_w);
+                w.mlp_w = kFusedMlp[st] ? H(o.mlp_w) : nullptr;
             }
         for (int st = 0; st < 3; ++st) {
             s->merge_s[st] = F(o_ms[st]); s->merge_b[st] = F(o_mb[st]);
@@ -346,9 +364,36 @@ void block_op(bf_cuda_swin *s, int st, int b, int op, hipStream_t stream) {
         case BFHIP_SWIN_FC2:
             linear_bf16(s->big, w.fc2_w, T, C, 4 * C, EpiResidualF32{s->x, w.fc2_b, C, T, C}, stream);
             break;
+        case BFHIP_SWIN_MLP: {
+            // The next block's LN1 is fused into the epilogue; the last block
+            // of the stage feeds the merge / stage output, which read x.
+            const bool next = b + 1 < kDepth[st];
+            const BlockW *nw = next ? &s->blocks[st][b + 1] : nullptr;
+            launch_swin_mlp<MlpS0>(s->x, w.n2s, w.n2b, w.mlp_w, w.fc1_b, w.fc2_b,
+                                   nw ? nw->n1s : nullptr, nw ? nw->n1b : nullptr,
+                                   next ? s->xn : nullptr, T, stream);
+            break;
+        }
         default:
             break;
     }
+}
+
+// The ops one block launches, in order.
+int block_ops(int st, int b, int *ops) {
+    int n = 0;
+    if (!kFusedMlp[st] || b == 0) ops[n++] = BFHIP_SWIN_LN1;
+    ops[n++] = BFHIP_SWIN_QKV;
+    ops[n++] = BFHIP_SWIN_ATTENTION;
+    ops[n++] = BFHIP_SWIN_PROJ;
+    if (kFusedMlp[st]) {
+        ops[n++] = BFHIP_SWIN_MLP;
+    } else {
+        ops[n++] = BFHIP_SWIN_LN2;
+        ops[n++] = BFHIP_SWIN_FC1;
+        ops[n++] = BFHIP_SWIN_FC2;
+    }
+    return n;
 }
 
 void merge_op(bf_cuda_swin *s, int st, hipStream_t stream) {
@@ -370,8 +415,11 @@ extern "C" int bf_cuda_swin_forward(bf_cuda_swin *s, const float *images, float 
     float *outputs[3] = {out1, out2, out3};
     patch_embed(s, images, stream);
     for (int st = 0; st < 4; ++st) {
-        for (int b = 0; b < kDepth[st]; ++b)
-            for (int op = BFHIP_SWIN_LN1; op <= BFHIP_SWIN_FC2; ++op) block_op(s, st, b, op, stream);
+        for (int b = 0; b < kDepth[st]; ++b) {
+            int ops[8];
+            const int n = block_ops(st, b, ops);
+            for (int i = 0; i < n; ++i) block_op(s, st, b, ops[i], stream);
+        }
         const int T = (int)s->batches * s->h[st] * s->w[st];
         if (st > 0)
             launch_out_ln(kC[st], s->x, outputs[st - 1], s->out_s[st - 1], s->out_b[st - 1], T,
@@ -384,11 +432,18 @@ extern "C" int bf_cuda_swin_forward(bf_cuda_swin *s, const float *images, float 
 extern "C" int bfhip_swin_profile_op(bf_cuda_swin *s, int stage, int block, int op, void *stream,
                                      char *error, size_t cap) {
     if (!s || stage < 0 || stage > 3 || block < 0 || block >= kDepth[stage] ||
-        op < BFHIP_SWIN_LN1 || op > BFHIP_SWIN_MERGE || (op == BFHIP_SWIN_MERGE && stage > 2))
+        op < BFHIP_SWIN_LN1 || op > BFHIP_SWIN_MLP || (op == BFHIP_SWIN_MERGE && stage > 2))
         return fail(error, cap, "invalid HIP Swin profiling op");
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    if (op == BFHIP_SWIN_MERGE) merge_op(s, stage, st);
-    else block_op(s, stage, block, op, st);
+    if (op == BFHIP_SWIN_MERGE) {
+        merge_op(s, stage, st);
+    } else {
+        int ops[8];
+        const int n = block_ops(stage, block, ops);
+        if (std::find(ops, ops + n, op) == ops + n)
+            return fail(error, cap, "stage %d block %d does not launch op %d", stage, block, op);
+        block_op(s, stage, block, op, st);
+    }
     return launch_ok(error, cap, "launch HIP Swin profiling op");
 }
 

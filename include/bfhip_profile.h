@@ -23,7 +23,10 @@ extern "C" {
 #endif
 
 /* Ops of one Swin block, in forward order; MERGE is the patch merge that
- * follows stage `stage` (0..2; `block` is ignored). */
+ * follows stage `stage` (0..2; `block` is ignored).  MLP is the fused
+ * LN2 -> fc1 -> GELU -> fc2 -> residual (+ next block's LN1) kernel of the
+ * stages that run it (stage 0); those stages launch LN1 only in block 0 and
+ * refuse LN2 / FC1 / FC2, the other stages refuse MLP. */
 enum {
     BFHIP_SWIN_LN1 = 0,
     BFHIP_SWIN_QKV = 1,
@@ -32,7 +35,8 @@ enum {
     BFHIP_SWIN_LN2 = 4,
     BFHIP_SWIN_FC1 = 5,
     BFHIP_SWIN_FC2 = 6,
-    BFHIP_SWIN_MERGE = 7
+    BFHIP_SWIN_MERGE = 7,
+    BFHIP_SWIN_MLP = 8
 };
 
 int bfhip_swin_profile_op(bf_cuda_swin *swin, int stage, int block, int op,
