@@ -46,12 +46,13 @@ constexpr bool kFusedMlp[4] = {true, false, false, false};
 struct BlockW {
     const float *n1s, *n1b, *n2s, *n2b, *qkv_b, *proj_b, *fc1_b, *fc2_b, *bias_mat;
     const bf16 *qkv_w, *proj_w, *fc1_w, *fc2_w;
-    const bf16 *mlp_w;  // fc1/fc2 packed for the fused MLP (fused stages only)
+    const bf16 *mlp_w;      // fc1/fc2 packed for the fused MLP (fused stages only)
+    const bf16 *attn_term;  // relative bias + shift mask per window type (attn_term_kernel)
 };
 
 struct BlockOff {
     size_t n1s, n1b, n2s, n2b, qkv_b, proj_b, fc1_b, fc2_b, bias_mat, qkv_w, proj_w, fc1_w, fc2_w;
-    size_t mlp_w;
+    size_t mlp_w, attn_term;
 };
 
 }  // namespace
@@ -200,6 +201,7 @@ static int swin_build(bf_cuda_swin *s, const bf_model *model, size_t batches, si
             o.qkv_b = arena.add_f32(qkv_b, 3 * c); o.proj_b = arena.add_f32(proj_b, c);
             o.fc1_b = arena.add_f32(fc1_b, 4 * c); o.fc2_b = arena.add_f32(fc2_b, c);
             o.bias_mat = arena.add_f32(bias);
+            o.attn_term = arena.add(nullptr, attn_term_elems((int)hd, (b & 1) ? 3 : 0) * 2);
             o.qkv_w = arena.add_bf16(qkv_w, (size_t)3 * c * c);
             o.proj_w = arena.add_bf16(proj_w, (size_t)c * c);
             o.fc1_w = arena.add_bf16(fc1_w, (size_t)4 * c * c);
@@ -252,11 +254,26 @@ static int swin_build(bf_cuda_swin *s, const bf_model *model, size_t batches, si
                 w.qkv_w = H(o.qkv_w); w.proj_w = H(o.proj_w); w.fc1_w = H(o.fc1_w);
                 w.fc2_w = H(o.fc2_w);
                 w.mlp_w = kFusedMlp[st] ? H(o.mlp_w) : nullptr;
+                w.attn_term = H(o.attn_term);
             }
         for (int st = 0; st < 3; ++st) {
             s->merge_s[st] = F(o_ms[st]); s->merge_b[st] = F(o_mb[st]);
             s->merge_w[st] = H(o_mw[st]); s->out_s[st] = F(o_os[st]); s->out_b[st] = F(o_ob[st]);
         }
+        // Attention score terms (relative bias + shift mask, in the kernel's
+        // accumulator order) from the uploaded bias matrices.
+        for (int st = 0; st < 4; ++st)
+            for (int b = 0; b < kDepth[st]; ++b) {
+                const int shift = (b & 1) ? 3 : 0, heads = kHeads[st];
+                const int wy_n = (s->h[st] + 6) / 7, wx_n = (s->w[st] + 6) / 7;
+                hipLaunchKernelGGL(attn_term_kernel, dim3(window_types(shift) * heads * 8), dim3(64), 0,
+                                   nullptr, s->blocks[st][b].bias_mat,
+                                   const_cast<bf16 *>(s->blocks[st][b].attn_term), heads, wy_n, wx_n,
+                                   shift);
+            }
+        if (!launch_ok(error, cap, "build attention terms") ||
+            !hip_ok(hipDeviceSynchronize(), error, cap, "build attention terms"))
+            return 0;
     }
     {
         size_t x_elems = 0, xn_elems = 0, big_elems = 0;
@@ -348,7 +365,7 @@ void block_op(bf_cuda_swin *s, int st, int b, int op, hipStream_t stream) {
             break;
         case BFHIP_SWIN_ATTENTION:
             hipLaunchKernelGGL(window_attention_kernel, dim3((items + kAttnWaves - 1) / kAttnWaves),
-                               dim3(64 * kAttnWaves), 0, stream, s->big, w.qkv_b, w.bias_mat,
+                               dim3(64 * kAttnWaves), 0, stream, s->big, w.qkv_b, w.attn_term,
                                s->xn, H, W, C, heads, wy_n, wx_n, (b & 1) ? 3 : 0, items);
             break;
         case BFHIP_SWIN_PROJ:
@@ -472,9 +489,21 @@ extern "C" int bfhip_debug_window_attention(const void *qkv, const float *qkv_bi
     const long long items = (long long)batches * wy_n * wx_n * heads;
     if (items > INT_MAX || (long long)batches * height * width * 3 * channels > INT_MAX)
         return fail(error, cap, "window-attention probe is too large");
+    // The probe builds the score terms with the context's builder into its own
+    // buffer (test path only: it allocates and synchronises).
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    bf16 *term = nullptr;
+    if (!hip_ok(hipMalloc(&term, attn_term_elems(heads, shift) * 2), error, cap,
+                "allocate probe attention terms"))
+        return 0;
+    hipLaunchKernelGGL(attn_term_kernel, dim3(window_types(shift) * heads * 8), dim3(64), 0, s,
+                       bias_mat, term, heads, (int)wy_n, (int)wx_n, shift);
     hipLaunchKernelGGL(window_attention_kernel, dim3((unsigned)((items + kAttnWaves - 1) / kAttnWaves)),
-                       dim3(64 * kAttnWaves), 0, reinterpret_cast<hipStream_t>(stream),
-                       static_cast<const bf16 *>(qkv), qkv_bias, bias_mat, static_cast<bf16 *>(out),
-                       height, width, channels, heads, (int)wy_n, (int)wx_n, shift, (int)items);
-    return launch_ok(error, cap, "launch window-attention probe");
+                       dim3(64 * kAttnWaves), 0, s, static_cast<const bf16 *>(qkv), qkv_bias, term,
+                       static_cast<bf16 *>(out), height, width, channels, heads, (int)wy_n, (int)wx_n,
+                       shift, (int)items);
+    const int ok = launch_ok(error, cap, "launch window-attention probe") &&
+                   hip_ok(hipStreamSynchronize(s), error, cap, "window-attention probe");
+    (void)hipFree(term);
+    return ok;
 }

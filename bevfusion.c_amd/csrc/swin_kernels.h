@@ -177,18 +177,22 @@ __global__ __launch_bounds__(256) void out_ln_kernel(const float *x, float *out,
 // ((wy*7 + t/7 + shift) mod Hp, (wx*7 + t%7 + shift) mod Wp) (reference
 // gather_windows_kernel cuda_swin.cu:120-131, cyclic_source swin.c:106-110).
 // Returns the token row, -1 for a zero-padded source (q/k/v = qkv bias), -2
-// for the MFMA padding rows t >= 49.
+// for the MFMA padding rows t >= 49.  shift < 7 <= Hp, Wp, so one conditional
+// subtraction is the modulo.
 __device__ __forceinline__ int window_token(int t, int n, int wy, int wx, int H, int W, int Hp,
                                             int Wp, int shift) {
     if (t >= 49) return -2;
-    const int py = wy * 7 + t / 7, px = wx * 7 + t % 7;
-    const int sy = shift ? (py + shift) % Hp : py, sx = shift ? (px + shift) % Wp : px;
+    const int ty = t / 7;
+    int sy = wy * 7 + ty + shift, sx = wx * 7 + (t - 7 * ty) + shift;
+    sy -= sy >= Hp ? Hp : 0;
+    sx -= sx >= Wp ? Wp : 0;
     return (sy < H && sx < W) ? (n * H + sy) * W + sx : -1;
 }
 
 // Shifted-window region label 3*ry + rx of padded position (py, px)
 // (reference mask_region, swin.c:112-117; cuda_swin.cu:132-134).
-__device__ __forceinline__ int window_label(int t, int wy, int wx, int Hp, int Wp, int shift) {
+__host__ __device__ __forceinline__ int window_label(int t, int wy, int wx, int Hp, int Wp,
+                                                     int shift) {
     const int py = wy * 7 + t / 7, px = wx * 7 + t % 7;
     const int ry = py < Hp - 7 ? 0 : (py < Hp - shift ? 1 : 2);
     const int rx = px < Wp - 7 ? 0 : (px < Wp - shift ? 1 : 2);
@@ -208,48 +212,106 @@ static __global__ __launch_bounds__(256) void window_map_kernel(int *token, int 
     label[idx] = window_label(t, wy, wx, wy_n * 7, wx_n * 7, shift);
 }
 
-// One wave64 per (window, head) with head dim 32: Q, K (rows) and V^T are
-// staged in LDS as bf16 with the 49 tokens padded to 64; S^T = K Q^T is 16
-// MFMAs, the fp32 softmax over keys runs on the accumulator registers (the
-// 64 keys of a query sit in 16 registers x 4 lanes), and O^T = V^T P^T takes
-// P straight from those registers as the B operand (the key order of the
-// k-slots is a permutation shared by both operands).  Scores are
-// q.k/sqrt(32) + rel_bias[h][i][j] (- 100 across shifted regions); keys
-// t >= 49 are excluded.  Outputs go back to the token rows they came from.
+// The region labels of a window depend only on whether it is in the last
+// window row and/or column: type = 2*(wy == wy_n-1) + (wx == wx_n-1).  An
+// unshifted block has a single type (no mask).
+__host__ __device__ __forceinline__ int window_type(int wy, int wx, int wy_n, int wx_n, int shift) {
+    return shift ? 2 * (wy == wy_n - 1) + (wx == wx_n - 1) : 0;
+}
+__host__ __device__ constexpr int window_types(int shift) { return shift ? 4 : 1; }
+
+// Additive score term of the attention kernel, in the order its accumulators
+// hold scores, pre-multiplied by log2(e) (softmax runs on exp2):
+//   lane l, value v = 16*jb + 4*ib + e  ->  query i = 16*ib + (l & 15),
+//                                           key   j = 16*jb + 4*(l >> 4) + e
+//   term = rel_bias[h][i][j] - 100 * (label(i) != label(j))  for i, j < 49,
+//          0 for padded queries (i >= 49), -inf for padded keys (j >= 49).
+// Stored per (type, head) as 8 chunks of [64 lanes][8] bf16, so chunk c is one
+// coalesced 16-byte load per lane.  A representative window of each type
+// supplies the labels (bias_mat is [heads][49][49] fp32).
+static __global__ __launch_bounds__(64) void attn_term_kernel(const float *__restrict__ bias_mat,
+                                                              bf16 *__restrict__ term, int heads,
+                                                              int wy_n, int wx_n, int shift) {
+    const int lane = threadIdx.x, c = blockIdx.x & 7, th = blockIdx.x >> 3;
+    const int h = th % heads, type = th / heads;
+    const int wy = (type & 2) ? wy_n - 1 : 0, wx = (type & 1) ? wx_n - 1 : 0;
+    const int Hp = wy_n * 7, Wp = wx_n * 7;
+    constexpr float kLog2e = 1.4426950408889634f;
+    bf16x8 o;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int v = 8 * c + k, jb = v >> 4, ib = (v >> 2) & 3, e = v & 3;
+        const int i = 16 * ib + (lane & 15), j = 16 * jb + 4 * (lane >> 4) + e;
+        float t;
+        if (j >= 49) {
+            t = -INFINITY;
+        } else if (i >= 49) {
+            t = 0.0f;
+        } else {
+            t = bias_mat[((size_t)h * 49 + i) * 49 + j];
+            if (shift && window_label(i, wy, wx, Hp, Wp, shift) != window_label(j, wy, wx, Hp, Wp, shift))
+                t -= 100.0f;
+            t *= kLog2e;
+        }
+        o[k] = to_bf16(t);
+    }
+    *reinterpret_cast<bf16x8 *>(term + ((size_t)(th * 8 + c) * 64 + lane) * 8) = o;
+}
+
+inline size_t attn_term_elems(int heads, int shift) {
+    return (size_t)window_types(shift) * heads * 8 * 64 * 8;
+}
+
+// One wave64 per (window, head) with head dim 32.  Window slot r = 16b + (l&15)
+// (b = 0..3, 49 tokens padded to 64) is lane l's row in every operand: the
+// S^T = K Q^T MFMAs take K and Q fragments (8 channels 8*(l>>4).. of that row)
+// straight from global memory, V goes through LDS once to become V^T, and the
+// output row of slot r is stored by the same lane.  The fp32 softmax over keys
+// runs on the accumulator registers (the 64 keys of a query sit in 16
+// registers x 4 lanes), and O^T = V^T P^T takes P straight from those
+// registers as the B operand (the key order of the k-slots is a permutation
+// shared by both operands).  Scores are q.k/sqrt(32) + rel_bias[h][i][j]
+// (- 100 across shifted regions), the latter read as one precomputed bf16 term
+// per accumulator (attn_term_kernel); keys t >= 49 get -inf.  Each wave works
+// on its own LDS slice, so waves never synchronise.
 constexpr int kAttnWaves = 4;
 
 static __global__ __launch_bounds__(256) void window_attention_kernel(
     const bf16 *__restrict__ qkv, const float *__restrict__ qkv_bias,
-    const float *__restrict__ bias_mat, bf16 *__restrict__ out, int H, int W, int C, int heads,
+    const bf16 *__restrict__ term, bf16 *__restrict__ out, int H, int W, int C, int heads,
     int wy_n, int wx_n, int shift, int items) {
-    constexpr int QS = 40;  // LDS row stride of Q/K (bf16)
     constexpr int VS = 72;  // LDS row stride of V^T (bf16)
-    __shared__ __attribute__((aligned(16))) bf16 sQ[kAttnWaves][64 * QS];
-    __shared__ __attribute__((aligned(16))) bf16 sK[kAttnWaves][64 * QS];
     __shared__ __attribute__((aligned(16))) bf16 sV[kAttnWaves][32 * VS];
 
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int item = blockIdx.x * kAttnWaves + wave;
-    const bool active = item < items;
-    const int it = active ? item : 0;
-    const int h = it % heads, win = it / heads;
+    if (item >= items) return;  // no workgroup barrier follows
+    const int h = item % heads, win = item / heads;
     const int wx = win % wx_n, t1 = win / wx_n, wy = t1 % wy_n, n = t1 / wy_n;
     const int Hp = wy_n * 7, Wp = wx_n * 7;
     const size_t ld = 3 * (size_t)C;
+    const int l16 = lane & 15, g = lane >> 4;
 
-    bf16 *Q = sQ[wave], *K = sK[wave], *Vt = sV[wave];
+    // This window type's score terms: 8 coalesced 16-byte loads per lane.
+    const bf16 *tp = term + ((size_t)(window_type(wy, wx, wy_n, wx_n, shift) * heads + h) * 512 + lane) * 8;
+    bf16x8 add[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int slot = lane + 64 * i, row = slot >> 2, ch = slot & 3;
-        const int tok = active ? window_token(row, n, wy, wx, H, W, Hp, Wp, shift) : -2;
+    for (int c = 0; c < 8; ++c) add[c] = *reinterpret_cast<const bf16x8 *>(tp + c * 512);
+
+    int tok[4];
+    bf16x8 qf[4], kf[4];
+    bf16 *Vt = sV[wave];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        tok[b] = window_token(16 * b + l16, n, wy, wx, H, W, Hp, Wp, shift);
         bf16x8 q = {}, k = {}, v = {};
-        if (tok >= 0) {
-            const bf16 *src = qkv + (size_t)tok * ld + h * 32 + ch * 8;
+        if (tok[b] >= 0) {
+            const bf16 *src = qkv + (size_t)tok[b] * ld + h * 32 + 8 * g;
             q = *reinterpret_cast<const bf16x8 *>(src);
             k = *reinterpret_cast<const bf16x8 *>(src + C);
             v = *reinterpret_cast<const bf16x8 *>(src + 2 * C);
-        } else if (tok == -1) {
-            const float *bq = qkv_bias + h * 32 + ch * 8;
+        } else if (tok[b] == -1) {  // zero-padded source: q/k/v are the qkv bias
+            const float *bq = qkv_bias + h * 32 + 8 * g;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 q[e] = to_bf16(bq[e]);
@@ -257,58 +319,33 @@ static __global__ __launch_bounds__(256) void window_attention_kernel(
                 v[e] = to_bf16(bq[2 * C + e]);
             }
         }
-        *reinterpret_cast<bf16x8 *>(Q + row * QS + ch * 8) = q;
-        *reinterpret_cast<bf16x8 *>(K + row * QS + ch * 8) = k;
+        qf[b] = q;
+        kf[b] = k;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) Vt[(ch * 8 + e) * VS + row] = v[e];
+        for (int e = 0; e < 8; ++e) Vt[(8 * g + e) * VS + 16 * b + l16] = v[e];
     }
-    __syncthreads();
-    if (!active) return;
 
-    const int l16 = lane & 15, g = lane >> 4;
     // S^T[j][i] blocks: s[jb][ib][e] = S[i = 16ib + l16][j = 16jb + 4g + e].
     f32x4 s[4][4];
-    {
-        bf16x8 kf[4], qf[4];
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            kf[b] = *reinterpret_cast<const bf16x8 *>(K + (16 * b + l16) * QS + 8 * g);
-            qf[b] = *reinterpret_cast<const bf16x8 *>(Q + (16 * b + l16) * QS + 8 * g);
-        }
-#pragma unroll
-        for (int jb = 0; jb < 4; ++jb)
-#pragma unroll
-            for (int ib = 0; ib < 4; ++ib) s[jb][ib] = mfma16(kf[jb], qf[ib], f32x4{0, 0, 0, 0});
-    }
-
-    const float scale = 0.17677669529663687f;  // 1/sqrt(32)
-    const float *bm = bias_mat + (size_t)h * 49 * 49;
-    int lab_j[4][4];
 #pragma unroll
     for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int j = 16 * jb + 4 * g + e;
-            lab_j[jb][e] = shift && j < 49 ? window_label(j, wy, wx, Hp, Wp, shift) : 0;
-        }
+        for (int ib = 0; ib < 4; ++ib) s[jb][ib] = mfma16(kf[jb], qf[ib], f32x4{0, 0, 0, 0});
+
+    // Softmax in base 2: scores and terms carry log2(e).
+    const float scale = 0.17677669529663687f * 1.4426950408889634f;  // log2(e) / sqrt(32)
     float inv[4];
 #pragma unroll
     for (int ib = 0; ib < 4; ++ib) {
-        const int i = 16 * ib + l16;
-        const int lab_i = shift && i < 49 ? window_label(i, wy, wx, Hp, Wp, shift) : 0;
         float m = -INFINITY;
 #pragma unroll
         for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const int j = 16 * jb + 4 * g + e;
-                float v = -INFINITY;
-                if (j < 49) {
-                    v = s[jb][ib][e] * scale + (i < 49 ? bm[i * 49 + j] : 0.0f);
-                    if (lab_i != lab_j[jb][e]) v -= 100.0f;
-                }
-                s[jb][ib][e] = v;
-                m = fmaxf(m, v);
+                const int v = 16 * jb + 4 * ib + e;
+                const float x = fmaf(s[jb][ib][e], scale, to_f32(add[v >> 3][v & 7]));
+                s[jb][ib][e] = x;
+                m = fmaxf(m, x);
             }
         m = fmaxf(m, __shfl_xor(m, 16));
         m = fmaxf(m, __shfl_xor(m, 32));
@@ -317,7 +354,7 @@ static __global__ __launch_bounds__(256) void window_attention_kernel(
         for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const float p = __expf(s[jb][ib][e] - m);
+                const float p = __builtin_amdgcn_exp2f(s[jb][ib][e] - m);  // -inf -> 0
                 s[jb][ib][e] = p;
                 sum += p;
             }
@@ -325,6 +362,12 @@ static __global__ __launch_bounds__(256) void window_attention_kernel(
         sum += __shfl_xor(sum, 32);
         inv[ib] = 1.0f / sum;
     }
+
+    // V^T was written by this wave only; LDS accesses of one wave complete in
+    // order, so a compiler-level fence is all the reads below need.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
     // O^T = V^T P^T over two 32-key chunks; k-slot e of lane group g is key
     // 32c + 16*(e>>2) + 4g + (e&3) in both operands.
@@ -359,10 +402,8 @@ static __global__ __launch_bounds__(256) void window_attention_kernel(
     // o[db][ib][e] = O[i = 16ib + l16][d = 16db + 4g + e] (unnormalised).
 #pragma unroll
     for (int ib = 0; ib < 4; ++ib) {
-        const int i = 16 * ib + l16;
-        const int tok = window_token(i, n, wy, wx, H, W, Hp, Wp, shift);
-        if (tok < 0) continue;
-        bf16 *dst = out + (size_t)tok * C + h * 32 + 4 * g;
+        if (tok[ib] < 0) continue;
+        bf16 *dst = out + (size_t)tok[ib] * C + h * 32 + 4 * g;
 #pragma unroll
         for (int db = 0; db < 2; ++db)
             store4(dst + 16 * db, o[db][ib][0] * inv[ib], o[db][ib][1] * inv[ib],
