@@ -48,6 +48,10 @@ def parse():
                    help="HIP-event timed launches per kernel in the roofline leg")
     p.add_argument("--kernels", default="",
                    help="comma-separated op names to time in the roofline leg (default: all)")
+    p.add_argument("--no-traffic", action="store_true",
+                   help="skip the rocprofv3 FETCH_SIZE / WRITE_SIZE passes on the dominant kernel")
+    p.add_argument("--pmc-child", default="",
+                   help=argparse.SUPPRESS)  # internal: the program rocprofv3 profiles
     return p.parse_args()
 
 
@@ -153,12 +157,11 @@ def fused_stages(swin, stream):
     return out
 
 
-def time_kernels(swin, neck, stream, reps=20, only=()):
-    """Time single ops of the path with HIP events on the stream they are
-    launched on; returns roofline entries sorted by time per frame."""
-    import torch
+def op_table(swin, neck, stream):
+    """name -> (launch fn, launches per frame, (flops, bytes) per launch) for
+    every op the forward launches (profiling hooks of include/bfhip_profile.h)."""
     import bfhip
-    cands = []
+    table = {}
     fused = fused_stages(swin, stream)
     for st in range(4):
         depth = SWIN_STAGES[st][4]
@@ -170,19 +173,26 @@ def time_kernels(swin, neck, stream, reps=20, only=()):
             # LN1 runs once per stage when the previous block's fused MLP
             # already produced it.
             per_frame = 1 if (op == "ln1" and st in fused) else depth
-            cands.append((f"swin.s{st}.{op}", lambda st=st, op=op: swin.profile_op(st, 0, op, stream),
-                          per_frame, swin_op_cost(st, op)))
+            table[f"swin.s{st}.{op}"] = (lambda st=st, op=op: swin.profile_op(st, 0, op, stream),
+                                         per_frame, swin_op_cost(st, op))
         if st < 3:
-            cands.append((f"swin.s{st}.merge", lambda st=st: swin.profile_op(st, 0, "merge", stream),
-                          1, swin_op_cost(st, "merge")))
+            table[f"swin.s{st}.merge"] = (lambda st=st: swin.profile_op(st, 0, "merge", stream),
+                                          1, swin_op_cost(st, "merge"))
     for layer, (name, *_rest) in NECK_LAYERS.items():
-        cands.append((f"neck.{name}", lambda layer=layer: neck.profile_layer(layer, stream), 1,
-                      neck_layer_cost(layer)))
-    if only:
-        cands = [c for c in cands if c[0] in only]
+        table[f"neck.{name}"] = (lambda layer=layer: neck.profile_layer(layer, stream), 1,
+                                 neck_layer_cost(layer))
+    return table
+
+
+def time_kernels(swin, neck, stream, reps=20, only=()):
+    """Time single ops of the path with HIP events on the stream they are
+    launched on; returns roofline entries sorted by time per frame."""
+    import torch
     out = []
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    for name, fn, per_frame, (flops, nbytes) in cands:
+    for name, (fn, per_frame, (flops, nbytes)) in op_table(swin, neck, stream).items():
+        if only and name not in only:
+            continue
         for _ in range(3):
             fn()
         start.record(stream)
@@ -194,6 +204,87 @@ def time_kernels(swin, neck, stream, reps=20, only=()):
         out.append(roofline_entry(name, avg_s, per_frame, flops, nbytes))
     out.sort(key=lambda e: -e["us_per_frame"])
     return out
+
+
+# HBM traffic of one op, from two rocprofv3 counter passes over a child run of
+# this script (--pmc-child): FETCH_SIZE and WRITE_SIZE (KiB per dispatch) of
+# the op's kernels, each scaled by what the same counter reads for a plain
+# device copy of known size in the same run.
+PMC_OP_REPS, PMC_COPY_REPS, PMC_COPY_BYTES = 23, 29, 64 << 20
+
+
+def pmc_child(op):
+    """Body of the profiled child: a 64 MiB device-to-device copy
+    PMC_COPY_REPS times (the calibration kernel), then the op PMC_OP_REPS
+    times; every dispatch after the last copy belongs to the op."""
+    import torch
+    import bfhip
+    from bfhip import bfw
+    dev = torch.device("cuda:0")
+    tmp = pathlib.Path(tempfile.mkdtemp(prefix="pmc_"))
+    model_path = bfw.write_camera_branch(tmp / "camera_branch.bfw", seed=0, mode="baseline")
+    with bfhip.Model(model_path) as m:
+        swin = bfhip.Swin(m, 6, 256, 704)
+        neck = bfhip.CameraNeck(m, 6, 32, 88, 360, 360)
+    img = torch.from_numpy(bfw.synthetic_images(0, 6, 256, 704)).to(dev)
+    dep = torch.from_numpy(bfw.synthetic_depth(0, 6, 256, 704)).to(dev)
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        outs = swin.forward(img, stream=stream)
+        neck.neck_forward(*outs, dep, stream=stream)
+        fn = op_table(swin, neck, stream)[op][0]
+        src = torch.zeros(PMC_COPY_BYTES // 4, device=dev)
+        dst = torch.empty_like(src)
+        stream.synchronize()
+        for _ in range(PMC_COPY_REPS):
+            dst.copy_(src)
+        stream.synchronize()
+        for _ in range(PMC_OP_REPS):
+            fn()
+        stream.synchronize()
+
+
+def measure_traffic(op, timeout_s=120):
+    """Scaled HBM bytes per launch of `op`, or (None, reason)."""
+    import csv
+    import shutil
+    import statistics
+    import subprocess
+    prof = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    if not os.path.exists(prof):
+        return None, "rocprofv3 not found"
+    per = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        out = pathlib.Path(tempfile.mkdtemp(prefix=f"pmc_{counter}_", dir="/tmp"))
+        cmd = ["timeout", "-s", "KILL", str(timeout_s), prof, "--pmc", counter,
+               "--output-format", "csv", "-d", str(out), "-o", "p", "--",
+               os.path.realpath(sys.executable), str(ROOT / "bench.py"), "--pmc-child", op]
+        env = dict(os.environ, TMPDIR="/tmp")
+        proc = subprocess.run(cmd, cwd="/tmp", env=env, capture_output=True, text=True)
+        files = list(out.rglob("*counter_collection.csv"))
+        if not files:
+            return None, f"{counter} pass produced no counters (exit {proc.returncode})"
+        rows = [r for r in csv.DictReader(open(files[0])) if r.get("Counter_Name") == counter]
+        rows.sort(key=lambda r: int(r["Dispatch_Id"]))
+        groups = {}
+        for r in rows:
+            groups.setdefault((r["Kernel_Name"], r["Grid_Size"]), []).append(r)
+        copy = [g for g in groups.values() if len(g) == PMC_COPY_REPS]
+        if len(copy) != 1:
+            return None, f"{counter}: calibration copy not identified in the counter dump"
+        last_copy = max(int(r["Dispatch_Id"]) for r in copy[0])
+        after = [r for r in rows if int(r["Dispatch_Id"]) > last_copy]
+        if not after or len(after) % PMC_OP_REPS:
+            return None, f"{counter}: {len(after)} op dispatches, expected a multiple of {PMC_OP_REPS}"
+        op_kib = sum(float(r["Counter_Value"]) for r in after) / PMC_OP_REPS
+        copy_kib = statistics.median(float(r["Counter_Value"]) for r in copy[0])
+        per[counter] = (op_kib, (PMC_COPY_BYTES / 1024) / copy_kib)
+    fetch = per["FETCH_SIZE"][0] * per["FETCH_SIZE"][1] * 1024
+    write = per["WRITE_SIZE"][0] * per["WRITE_SIZE"][1] * 1024
+    return {"bytes": round(fetch + write), "fetch_bytes": round(fetch), "write_bytes": round(write),
+            "fetch_kib_raw": round(per["FETCH_SIZE"][0], 1), "write_kib_raw": round(per["WRITE_SIZE"][0], 1),
+            "fetch_scale": round(per["FETCH_SIZE"][1], 4), "write_scale": round(per["WRITE_SIZE"][1], 4),
+            "calibration": f"{PMC_COPY_BYTES >> 20} MiB device copy"}, None
 
 
 def cpu_baseline(model_path, cameras):
@@ -236,6 +327,9 @@ def _cpu_model():
 
 def main():
     args = parse()
+    if args.pmc_child:
+        pmc_child(args.pmc_child)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; the path shards per camera "
                                    "across GPUs by design (DESIGN.md) but no multi-GPU run is "
@@ -327,6 +421,14 @@ def main():
         result["kernels"] = [{k: e[k] for k in ("kernel", "bound", "frac", "avg_us",
                                                   "us_per_frame", "tflops", "gbs")}
                              for e in kernels[:12]]
+        if not args.no_traffic:
+            torch.cuda.synchronize()
+            traffic, why = measure_traffic(kernels[0]["kernel"])
+            if traffic:
+                result["roofline"]["traffic"] = traffic["bytes"]
+                result["roofline"]["traffic_detail"] = traffic
+            else:
+                result["roofline"]["traffic_error"] = why
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(model_path, args.cpu_cameras)
     print(json.dumps(result))
