@@ -114,8 +114,9 @@ def swin_op_cost(stage, op, b=6):
         return 2.0 * t * c * 4 * c, t * c * 2 + 4 * c * c * 2 + t * 4 * c * 2
     if op == "fc2":
         return 2.0 * t * 4 * c * c, t * 4 * c * 2 + 4 * c * c * 2 + 2 * t * c * 4
-    if op == "mlp":  # fused LN2 -> fc1 -> GELU -> fc2 -> residual (+ next LN1)
-        return 4.0 * t * c * 4 * c, t * c * 4 * 2 + t * c * 2 + 8 * c * c * 2
+    if op == "mlp":  # fused proj -> LN2 -> fc1 -> GELU -> fc2 -> residual (+ next LN1)
+        return (2.0 * t * c * c + 4.0 * t * c * 4 * c,
+                t * c * 4 * 2 + t * c * 2 * 2 + 9 * c * c * 2)
     if op == "merge":
         h2, w2 = SWIN_STAGES[stage + 1][:2]
         t2 = b * h2 * w2

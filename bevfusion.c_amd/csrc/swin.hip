@@ -14,8 +14,9 @@
 // proj GEMM(+bias, += into x) -> LN2 -> fc1 GEMM(+bias, GELU, bf16) ->
 // fc2 GEMM(+bias, += into x).  Stage 0 (C = 96) runs LN2 -> fc1 -> GELU ->
 // fc2 -> residual as one fused kernel whose hidden layer stays on chip
-// (swin_mlp.h); it also writes the next block's LN1 output, so only the first
-// block of the stage launches LN1.
+// (swin_mlp.h), with the proj GEMM and its residual fused in front; it also
+// writes the next block's LN1 output, so only the first block of the stage
+// launches LN1.
 #include "bf_cuda_swin.h"
 #include "bfhip_debug.h"
 #include "bfhip_profile.h"
@@ -38,21 +39,23 @@ constexpr int kC[4] = {96, 192, 384, 768};
 constexpr int kHeads[4] = {3, 6, 12, 24};
 constexpr int kDepth[4] = {2, 2, 6, 2};
 
-// Fused-MLP configuration of stage 0: one 16-token fragment per wave, four
-// waves, three weight chunks in flight (measured best on MI355X at 6x256x704).
-using MlpS0 = MlpCfg<96, 1, 4, 3>;
+// Fused proj + MLP configuration of stage 0: one 16-token fragment per wave,
+// four waves, three weight chunks in flight (measured best on MI355X at
+// 6x256x704).
+using MlpS0 = MlpCfg<96, 1, 4, 3, true>;
 constexpr bool kFusedMlp[4] = {true, false, false, false};
 
 struct BlockW {
     const float *n1s, *n1b, *n2s, *n2b, *qkv_b, *proj_b, *fc1_b, *fc2_b, *bias_mat;
     const bf16 *qkv_w, *proj_w, *fc1_w, *fc2_w;
     const bf16 *mlp_w;      // fc1/fc2 packed for the fused MLP (fused stages only)
+    const bf16 *mlp_proj;   // proj packed for the fused MLP (fused stages only)
     const bf16 *attn_term;  // relative bias + shift mask per window type (attn_term_kernel)
 };
 
 struct BlockOff {
     size_t n1s, n1b, n2s, n2b, qkv_b, proj_b, fc1_b, fc2_b, bias_mat, qkv_w, proj_w, fc1_w, fc2_w;
-    size_t mlp_w, attn_term;
+    size_t mlp_w, mlp_proj, attn_term;
 };
 
 }  // namespace
@@ -206,11 +209,14 @@ static int swin_build(bf_cuda_swin *s, const bf_model *model, size_t batches, si
             o.proj_w = arena.add_bf16(proj_w, (size_t)c * c);
             o.fc1_w = arena.add_bf16(fc1_w, (size_t)4 * c * c);
             o.fc2_w = arena.add_bf16(fc2_w, (size_t)4 * c * c);
-            o.mlp_w = 0;
+            o.mlp_w = o.mlp_proj = 0;
             if (kFusedMlp[st]) {
                 std::vector<uint16_t> packed((size_t)8 * c * c);
                 pack_mlp_weights<MlpS0>(fc1_w, fc2_w, packed.data(), bf16_bits);
                 o.mlp_w = arena.add(packed.data(), packed.size() * 2);
+                std::vector<uint16_t> proj((size_t)c * c);
+                pack_proj_weights<MlpS0>(proj_w, proj.data(), bf16_bits);
+                o.mlp_proj = arena.add(proj.data(), proj.size() * 2);
             }
         }
     }
@@ -254,6 +260,7 @@ static int swin_build(bf_cuda_swin *s, const bf_model *model, size_t batches, si
                 w.qkv_w = H(o.qkv_w); w.proj_w = H(o.proj_w); w.fc1_w = H(o.fc1_w);
                 w.fc2_w = H(o.fc2_w);
                 w.mlp_w = kFusedMlp[st] ? H(o.mlp_w) : nullptr;
+                w.mlp_proj = kFusedMlp[st] ? H(o.mlp_proj) : nullptr;
                 w.attn_term = H(o.attn_term);
             }
         for (int st = 0; st < 3; ++st) {
@@ -386,9 +393,10 @@ void block_op(bf_cuda_swin *s, int st, int b, int op, hipStream_t stream) {
             // of the stage feeds the merge / stage output, which read x.
             const bool next = b + 1 < kDepth[st];
             const BlockW *nw = next ? &s->blocks[st][b + 1] : nullptr;
-            launch_swin_mlp<MlpS0>(s->x, w.n2s, w.n2b, w.mlp_w, w.fc1_b, w.fc2_b,
-                                   nw ? nw->n1s : nullptr, nw ? nw->n1b : nullptr,
-                                   next ? s->xn : nullptr, T, stream);
+            // proj reads the attention output in xn; LN1' overwrites it row by row.
+            launch_swin_mlp<MlpS0>(s->x, s->xn, w.mlp_proj, w.proj_b, w.n2s, w.n2b, w.mlp_w,
+                                   w.fc1_b, w.fc2_b, nw ? nw->n1s : nullptr,
+                                   nw ? nw->n1b : nullptr, next ? s->xn : nullptr, T, stream);
             break;
         }
         default:
@@ -402,10 +410,10 @@ int block_ops(int st, int b, int *ops) {
     if (!kFusedMlp[st] || b == 0) ops[n++] = BFHIP_SWIN_LN1;
     ops[n++] = BFHIP_SWIN_QKV;
     ops[n++] = BFHIP_SWIN_ATTENTION;
-    ops[n++] = BFHIP_SWIN_PROJ;
     if (kFusedMlp[st]) {
-        ops[n++] = BFHIP_SWIN_MLP;
+        ops[n++] = BFHIP_SWIN_MLP;  // proj + residual + LN2 + fc1 + fc2 + residual (+ LN1')
     } else {
+        ops[n++] = BFHIP_SWIN_PROJ;
         ops[n++] = BFHIP_SWIN_LN2;
         ops[n++] = BFHIP_SWIN_FC1;
         ops[n++] = BFHIP_SWIN_FC2;

@@ -1,40 +1,51 @@
-// Fused Swin MLP for the wide, shallow stages (C = 96, 192):
-//   x += fc2(GELU(fc1(LN2(x))))          and optionally  xn = LN1'(x)
-// in one launch, with the 4C-wide hidden layer never leaving the chip.
+// Fused Swin block tail for the wide, shallow stage 0 (C = 96):
+//   [x += proj(a) + b_proj]                      (PROJ: a = attention output)
+//   x += fc2(GELU(fc1(LN2(x)) + b1)) + b2
+//   xn = LN1'(x)                                  (optional: next block's LN1)
+// in one launch: x is read and written once, the 4C-wide hidden layer never
+// leaves the chip.
 //
-// Transposed formulation on v_mfma_f32_16x16x32_bf16 (A = weights, B = tokens):
-//   fc1:  H^T[hid, tok] = W1[hid, c] . LN2(x)^T[c, tok]
-//   fc2:  y^T[c, tok]   = W2[c, hid] . GELU(H^T + b1)[hid, tok]
-// The fc1 accumulator of lane l holds hidden rows 4*(l>>4)+r of token l&15,
-// which is exactly the k-slot set the fc2 B operand wants from that lane if the
-// hidden index of k-slot e is 16*(e>>2) + 4*(l>>4) + (e&3): GELU(H) feeds fc2
-// straight from registers.  W2's columns are packed in that order at create.
+// Transposed formulation on v_mfma_f32_16x16x32_bf16 (A = weights, B = tokens).
+// Every lane owns token (l & 15) of its 16-token fragment and, in the fp32
+// accumulator ("C") layout, channels 16j + 4(l>>4) + e (j < C/16, e < 4): the
+// residual row, the proj output, LN2, the fc2 output and LN1' all live in
+// that layout, so x is loaded and stored as float4s and never shuffled.
+//   proj:  y^T[c, tok]   = Wp[c, k] . a^T[k, tok]       (a rows as B operand)
+//   fc1:   H^T[hid, tok] = W1[hid, c] . LN2(x)^T[c, tok]
+//   fc2:   y^T[c, tok]   = W2[c, hid] . GELU(H^T + b1)[hid, tok]
+// An operand that comes out of an accumulator is used in place: k-slot e of
+// lane group g stands for index 16(e>>2) + 4g + (e&3) of the 32-wide k-step,
+// so LN2(x) feeds fc1 and GELU(H) feeds fc2 straight from registers; W1 and
+// W2 columns are packed in that order at create.
 //
-// Weights are packed per 32-wide hidden chunk in MFMA-fragment order: a 1 KiB
-// fragment is the 64 lanes' 16-byte operands, lane-major, so one LDS-DMA
-// instruction per fragment fills LDS and each fragment read is one
-// conflict-free ds_read_b128.  Chunk q of the packed buffer holds
-//   W1 fragments (f = 0,1; s = 0..C/32-1): lane l, element e ->
-//       W1[32q + 16f + (l&15)][32s + 8(l>>4) + e]
-//   W2 fragments (j = 0..C/16-1): lane l, element e ->
+// Weights are packed in MFMA-fragment order: a 1 KiB fragment is the 64 lanes'
+// 16-byte operands, lane-major, so one LDS-DMA instruction per fragment fills
+// LDS and each fragment read is one conflict-free ds_read_b128.  Chunk q (32
+// hidden units) of the packed MLP buffer holds
+//   W1 fragments (f = 0,1; s < C/32): lane l, element e ->
+//       W1[32q + 16f + (l&15)][32s + 16(e>>2) + 4(l>>4) + (e&3)]
+//   W2 fragments (j < C/16): lane l, element e ->
 //       W2[16j + (l&15)][32q + 16(e>>2) + 4(l>>4) + (e&3)]
-// Chunks stream through NBUF LDS buffers (one barrier per chunk) while every
-// wave keeps its tokens' LN2 rows (the fc1 B operand) and fc2 accumulators in
-// registers.  Each wave owns 16*TF tokens; LayerNorm statistics are fp32 over
-// the 4 lanes that share a token (two-pass, eps 1e-5).
+// and the proj buffer holds fragments (j < C/16, s < C/32): lane l, element e
+//   -> Wp[16j + (l&15)][32s + 8(l>>4) + e].
+// Chunks stream through NBUF LDS buffers (one barrier per chunk); proj
+// fragments are read once per wave straight from global memory (L1/L2).
+// LayerNorm statistics are fp32 over the 4 lanes that share a token (two-pass,
+// eps 1e-5).
 #pragma once
 
 #include "gemm_core.h"
 
 namespace bfhip {
 
-template <int C_, int TF_, int WAVES_, int NBUF_>
+template <int C_, int TF_, int WAVES_, int NBUF_, bool PROJ_>
 struct MlpCfg {
     static constexpr int C = C_, TF = TF_, kWaves = WAVES_, kBufs = NBUF_;
+    static constexpr bool kProj = PROJ_;
     static constexpr int kHid = 4 * C;
     static constexpr int kChunks = kHid / 32;
-    static constexpr int kKs = C / 32;          // fc1 k-steps
-    static constexpr int kCf = C / 16;          // fc2 output-channel fragments
+    static constexpr int kKs = C / 32;            // k-steps over channels
+    static constexpr int kCf = C / 16;            // output-channel fragments
     static constexpr int kFrags = 2 * kKs + kCf;  // 1 KiB fragments per chunk
     static constexpr int kChunkBytes = kFrags * 1024;
     static constexpr int kTokens = kWaves * TF * 16;
@@ -44,6 +55,9 @@ struct MlpCfg {
     static_assert(kFrags % kWaves == 0, "chunk fragments must split evenly over the waves");
     static_assert(kBufs >= 2 && kBufs <= kChunks, "2 .. kChunks chunk buffers");
 };
+
+// Hidden / channel index of k-slot e of lane group g within a 32-wide k-step.
+constexpr int kslot(int g, int e) { return 16 * (e >> 2) + 4 * g + (e & 3); }
 
 // Host-side packing of W1 [4C][C] and W2 [C][4C] (fp32, PyTorch [out, in])
 // into the chunked fragment order above, as bf16 bit patterns.
@@ -56,23 +70,37 @@ void pack_mlp_weights(const float *w1, const float *w2, uint16_t *dst, ToBf16 to
             for (int s = 0; s < Cfg::kKs; ++s)
                 for (int l = 0; l < 64; ++l)
                     for (int e = 0; e < 8; ++e)
-                        dst[o++] = to_bf16_bits(w1[(size_t)(32 * q + 16 * f + (l & 15)) * C + 32 * s + 8 * (l >> 4) + e]);
+                        dst[o++] = to_bf16_bits(w1[(size_t)(32 * q + 16 * f + (l & 15)) * C + 32 * s + kslot(l >> 4, e)]);
         for (int j = 0; j < Cfg::kCf; ++j)
             for (int l = 0; l < 64; ++l)
                 for (int e = 0; e < 8; ++e)
-                    dst[o++] = to_bf16_bits(
-                        w2[(size_t)(16 * j + (l & 15)) * H + 32 * q + 16 * (e >> 2) + 4 * (l >> 4) + (e & 3)]);
+                    dst[o++] = to_bf16_bits(w2[(size_t)(16 * j + (l & 15)) * H + 32 * q + kslot(l >> 4, e)]);
     }
 }
 
+// Host-side packing of the proj weight Wp [C][C] (fragment (j, s) order).
+template <class Cfg, class ToBf16>
+void pack_proj_weights(const float *wp, uint16_t *dst, ToBf16 to_bf16_bits) {
+    constexpr int C = Cfg::C;
+    size_t o = 0;
+    for (int j = 0; j < Cfg::kCf; ++j)
+        for (int s = 0; s < Cfg::kKs; ++s)
+            for (int l = 0; l < 64; ++l)
+                for (int e = 0; e < 8; ++e)
+                    dst[o++] = to_bf16_bits(wp[(size_t)(16 * j + (l & 15)) * C + 32 * s + 8 * (l >> 4) + e]);
+}
+
 template <class Cfg>
-__global__ __launch_bounds__(Cfg::kThreads) void swin_mlp_kernel(
-    float *__restrict__ x, const float *__restrict__ ln_g, const float *__restrict__ ln_b,
+__global__ __launch_bounds__(Cfg::kThreads) __attribute__((amdgpu_waves_per_eu(4))) void swin_mlp_kernel(
+    float *__restrict__ x, const bf16 *attn, const bf16 *__restrict__ wproj,
+    const float *__restrict__ bproj, const float *__restrict__ ln_g, const float *__restrict__ ln_b,
     const bf16 *__restrict__ wpk, const float *__restrict__ b1, const float *__restrict__ b2,
-    const float *__restrict__ next_g, const float *__restrict__ next_b, bf16 *__restrict__ xn,
-    int T) {
+    const float *__restrict__ next_g, const float *__restrict__ next_b, bf16 *xn, int T) {
+    // attn and xn may be the same buffer: each row is read (prologue) by the
+    // lane group that later writes it (epilogue), so neither is __restrict__.
     constexpr int C = Cfg::C, TF = Cfg::TF, KS = Cfg::kKs, CF = Cfg::kCf;
     constexpr int NB = Cfg::kBufs, P = Cfg::kPerWave;
+    constexpr int kBiasPer = (Cfg::kHid + Cfg::kThreads - 1) / Cfg::kThreads;
     __shared__ __attribute__((aligned(1024))) bf16 sw[NB][Cfg::kChunkBytes / 2];
     __shared__ float sb1[Cfg::kHid];
 
@@ -90,79 +118,99 @@ __global__ __launch_bounds__(Cfg::kThreads) void swin_mlp_kernel(
         }
     };
 
-    // LN2 of this wave's tokens into fc1 B operands: lane holds token
-    // tok0 + 16i + l16, channels 32s + 8g + e.
-    // x rows first, then the first NB-1 weight chunks, so that waiting for
-    // x (in-order vmcnt) does not also wait for the weight stream.
-    float4 xv[TF][KS][2];
+    // Global loads first (x rows in the C layout, attention rows, proj
+    // fragments, b1), then the first NB-1 weight chunks, so that waiting for
+    // the former (in-order vmcnt) never waits for the weight stream.
+    float4 xr[TF][CF];
+    bf16x8 af[TF][KS];
 #pragma unroll
     for (int i = 0; i < TF; ++i) {
         const int t = tok0 + 16 * i + l16;
         const bool ok = t < T;
+        const size_t row = (size_t)(ok ? t : 0) * C;
 #pragma unroll
-        for (int k = 0; k < KS; ++k) {
-            const float *src = x + (size_t)(ok ? t : 0) * C + 32 * k + 8 * g;
-            xv[i][k][0] = ok ? *reinterpret_cast<const float4 *>(src) : make_float4(0.f, 0.f, 0.f, 0.f);
-            xv[i][k][1] = ok ? *reinterpret_cast<const float4 *>(src + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
+        for (int j = 0; j < CF; ++j)
+            xr[i][j] = ok ? *reinterpret_cast<const float4 *>(x + row + 16 * j + 4 * g)
+                          : make_float4(0.f, 0.f, 0.f, 0.f);
+        if constexpr (Cfg::kProj)
+#pragma unroll
+            for (int k = 0; k < KS; ++k)
+                af[i][k] = ok ? *reinterpret_cast<const bf16x8 *>(attn + row + 32 * k + 8 * g) : bf16x8{};
     }
-    float bias1[(Cfg::kHid + Cfg::kThreads - 1) / Cfg::kThreads];
+    float bias1[kBiasPer];
 #pragma unroll
-    for (int r = 0; r < (Cfg::kHid + Cfg::kThreads - 1) / Cfg::kThreads; ++r) {
+    for (int r = 0; r < kBiasPer; ++r) {
         const int i = threadIdx.x + r * Cfg::kThreads;
         bias1[r] = i < Cfg::kHid ? b1[i] : 0.0f;
+    }
+    if constexpr (Cfg::kProj) {
+        // x += proj(a) + b_proj, accumulated in the C layout.
+#pragma unroll
+        for (int j = 0; j < CF; ++j) {
+            const float4 bp = *reinterpret_cast<const float4 *>(bproj + 16 * j + 4 * g);
+            f32x4 pa[TF];
+#pragma unroll
+            for (int i = 0; i < TF; ++i) pa[i] = f32x4{bp.x, bp.y, bp.z, bp.w};
+#pragma unroll
+            for (int k = 0; k < KS; ++k) {
+                const bf16x8 w = *reinterpret_cast<const bf16x8 *>(wproj + ((j * KS + k) * 64 + lane) * 8);
+#pragma unroll
+                for (int i = 0; i < TF; ++i) pa[i] = mfma16(w, af[i][k], pa[i]);
+            }
+#pragma unroll
+            for (int i = 0; i < TF; ++i) {
+                xr[i][j].x += pa[i][0]; xr[i][j].y += pa[i][1];
+                xr[i][j].z += pa[i][2]; xr[i][j].w += pa[i][3];
+            }
+        }
     }
 #pragma unroll
     for (int q = 0; q < NB - 1; ++q) issue(q);
 #pragma unroll
-    for (int r = 0; r < (Cfg::kHid + Cfg::kThreads - 1) / Cfg::kThreads; ++r) {
+    for (int r = 0; r < kBiasPer; ++r) {
         const int i = threadIdx.x + r * Cfg::kThreads;
         if (i < Cfg::kHid) sb1[i] = bias1[r];
     }
 
+    // LN2 in the C layout, then into fc1 B operands (k-slot order).
     bf16x8 xf[TF][KS];
 #pragma unroll
     for (int i = 0; i < TF; ++i) {
-        float v[KS][8];
         float s = 0.0f;
 #pragma unroll
-        for (int k = 0; k < KS; ++k) {
-            const float4 a = xv[i][k][0], b = xv[i][k][1];
-            v[k][0] = a.x; v[k][1] = a.y; v[k][2] = a.z; v[k][3] = a.w;
-            v[k][4] = b.x; v[k][5] = b.y; v[k][6] = b.z; v[k][7] = b.w;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) s += v[k][e];
-        }
+        for (int j = 0; j < CF; ++j) s += (xr[i][j].x + xr[i][j].y) + (xr[i][j].z + xr[i][j].w);
         s += __shfl_xor(s, 16);
         s += __shfl_xor(s, 32);
         const float mean = s * (1.0f / C);
         float q = 0.0f;
 #pragma unroll
-        for (int k = 0; k < KS; ++k)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) q += (v[k][e] - mean) * (v[k][e] - mean);
+        for (int j = 0; j < CF; ++j) {
+            const float a = xr[i][j].x - mean, b = xr[i][j].y - mean, c = xr[i][j].z - mean,
+                        d = xr[i][j].w - mean;
+            q += (a * a + b * b) + (c * c + d * d);
+        }
         q += __shfl_xor(q, 16);
         q += __shfl_xor(q, 32);
         const float rstd = rsqrtf(q * (1.0f / C) + 1e-5f);
 #pragma unroll
-        for (int k = 0; k < KS; ++k) {
-            const int c = 32 * k + 8 * g;
-            const float4 ga = *reinterpret_cast<const float4 *>(ln_g + c);
-            const float4 gb = *reinterpret_cast<const float4 *>(ln_g + c + 4);
-            const float4 ba = *reinterpret_cast<const float4 *>(ln_b + c);
-            const float4 bb = *reinterpret_cast<const float4 *>(ln_b + c + 4);
-            const float gg[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
-            const float bbv[8] = {ba.x, ba.y, ba.z, ba.w, bb.x, bb.y, bb.z, bb.w};
-#pragma unroll
-            for (int e = 0; e < 8; ++e) xf[i][k][e] = to_bf16((v[k][e] - mean) * rstd * gg[e] + bbv[e]);
+        for (int j = 0; j < CF; ++j) {
+            const float4 gg = *reinterpret_cast<const float4 *>(ln_g + 16 * j + 4 * g);
+            const float4 bb = *reinterpret_cast<const float4 *>(ln_b + 16 * j + 4 * g);
+            const int k = j >> 1, e0 = 4 * (j & 1);
+            xf[i][k][e0 + 0] = to_bf16((xr[i][j].x - mean) * rstd * gg.x + bb.x);
+            xf[i][k][e0 + 1] = to_bf16((xr[i][j].y - mean) * rstd * gg.y + bb.y);
+            xf[i][k][e0 + 2] = to_bf16((xr[i][j].z - mean) * rstd * gg.z + bb.z);
+            xf[i][k][e0 + 3] = to_bf16((xr[i][j].w - mean) * rstd * gg.w + bb.w);
         }
     }
 
     f32x4 acc[CF][TF];
 #pragma unroll
-    for (int j = 0; j < CF; ++j)
+    for (int j = 0; j < CF; ++j) {
+        const float4 bj = *reinterpret_cast<const float4 *>(b2 + 16 * j + 4 * g);
 #pragma unroll
-        for (int i = 0; i < TF; ++i) acc[j][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < TF; ++i) acc[j][i] = f32x4{bj.x, bj.y, bj.z, bj.w};
+    }
 
     for (int q = 0; q < Cfg::kChunks; ++q) {
         // Chunks issued after q: min(NB - 2, kChunks - 1 - q); wait for q only.
@@ -189,7 +237,7 @@ __global__ __launch_bounds__(Cfg::kThreads) void swin_mlp_kernel(
 #pragma unroll
                 for (int i = 0; i < TF; ++i) h[f][i] = mfma16(a, xf[i][k], h[f][i]);
             }
-        // GELU(H + b1) -> fc2 B operands (k-slot e = hidden 16(e>>2) + 4g + (e&3)).
+        // GELU(H + b1) -> fc2 B operands (k-slot order).
         bf16x8 hb[TF];
 #pragma unroll
         for (int i = 0; i < TF; ++i)
@@ -203,26 +251,21 @@ __global__ __launch_bounds__(Cfg::kThreads) void swin_mlp_kernel(
         }
     }
 
-    // Residual: acc[j][i][e] is y[token tok0 + 16i + l16][channel 16j + 4g + e].
+    // Residual (+ LN1' of the next block): acc[j][i][e] is channel 16j + 4g + e.
 #pragma unroll
     for (int i = 0; i < TF; ++i) {
         const int t = tok0 + 16 * i + l16;
         const bool ok = t < T;
         float *row = x + (size_t)(ok ? t : 0) * C + 4 * g;
-        float4 y[CF];
-#pragma unroll
-        for (int j = 0; j < CF; ++j)
-            y[j] = ok ? *reinterpret_cast<const float4 *>(row + 16 * j) : make_float4(0.f, 0.f, 0.f, 0.f);
         float s = 0.0f;
 #pragma unroll
         for (int j = 0; j < CF; ++j) {
-            const float4 bj = *reinterpret_cast<const float4 *>(b2 + 16 * j + 4 * g);
-            y[j].x += acc[j][i][0] + bj.x;
-            y[j].y += acc[j][i][1] + bj.y;
-            y[j].z += acc[j][i][2] + bj.z;
-            y[j].w += acc[j][i][3] + bj.w;
-            if (ok) *reinterpret_cast<float4 *>(row + 16 * j) = y[j];
-            s += (y[j].x + y[j].y) + (y[j].z + y[j].w);
+            xr[i][j].x += acc[j][i][0];
+            xr[i][j].y += acc[j][i][1];
+            xr[i][j].z += acc[j][i][2];
+            xr[i][j].w += acc[j][i][3];
+            if (ok) *reinterpret_cast<float4 *>(row + 16 * j) = xr[i][j];
+            s += (xr[i][j].x + xr[i][j].y) + (xr[i][j].z + xr[i][j].w);
         }
         if (!xn) continue;  // uniform: the next LayerNorm is fused or not for the whole launch
         s += __shfl_xor(s, 16);
@@ -231,7 +274,8 @@ __global__ __launch_bounds__(Cfg::kThreads) void swin_mlp_kernel(
         float qs = 0.0f;
 #pragma unroll
         for (int j = 0; j < CF; ++j) {
-            const float a = y[j].x - mean, b = y[j].y - mean, c = y[j].z - mean, d = y[j].w - mean;
+            const float a = xr[i][j].x - mean, b = xr[i][j].y - mean, c = xr[i][j].z - mean,
+                        d = xr[i][j].w - mean;
             qs += (a * a + b * b) + (c * c + d * d);
         }
         qs += __shfl_xor(qs, 16);
@@ -244,21 +288,23 @@ __global__ __launch_bounds__(Cfg::kThreads) void swin_mlp_kernel(
             const float4 gg = *reinterpret_cast<const float4 *>(next_g + c);
             const float4 bb = *reinterpret_cast<const float4 *>(next_b + c);
             bf16x4 o;
-            o[0] = to_bf16((y[j].x - mean) * rstd * gg.x + bb.x);
-            o[1] = to_bf16((y[j].y - mean) * rstd * gg.y + bb.y);
-            o[2] = to_bf16((y[j].z - mean) * rstd * gg.z + bb.z);
-            o[3] = to_bf16((y[j].w - mean) * rstd * gg.w + bb.w);
+            o[0] = to_bf16((xr[i][j].x - mean) * rstd * gg.x + bb.x);
+            o[1] = to_bf16((xr[i][j].y - mean) * rstd * gg.y + bb.y);
+            o[2] = to_bf16((xr[i][j].z - mean) * rstd * gg.z + bb.z);
+            o[3] = to_bf16((xr[i][j].w - mean) * rstd * gg.w + bb.w);
             *reinterpret_cast<bf16x4 *>(xn + (size_t)t * C + c) = o;
         }
     }
 }
 
 template <class Cfg>
-inline void launch_swin_mlp(float *x, const float *ln_g, const float *ln_b, const bf16 *wpk,
+inline void launch_swin_mlp(float *x, const bf16 *attn, const bf16 *wproj, const float *bproj,
+                            const float *ln_g, const float *ln_b, const bf16 *wpk,
                             const float *b1, const float *b2, const float *next_g,
                             const float *next_b, bf16 *xn, int T, hipStream_t s) {
     hipLaunchKernelGGL((swin_mlp_kernel<Cfg>), dim3((T + Cfg::kTokens - 1) / Cfg::kTokens),
-                       dim3(Cfg::kThreads), 0, s, x, ln_g, ln_b, wpk, b1, b2, next_g, next_b, xn, T);
+                       dim3(Cfg::kThreads), 0, s, x, attn, wproj, bproj, ln_g, ln_b, wpk, b1, b2,
+                       next_g, next_b, xn, T);
 }
 
 }  // namespace bfhip

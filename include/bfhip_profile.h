@@ -24,9 +24,10 @@ extern "C" {
 
 /* Ops of one Swin block, in forward order; MERGE is the patch merge that
  * follows stage `stage` (0..2; `block` is ignored).  MLP is the fused
- * LN2 -> fc1 -> GELU -> fc2 -> residual (+ next block's LN1) kernel of the
- * stages that run it (stage 0); those stages launch LN1 only in block 0 and
- * refuse LN2 / FC1 / FC2, the other stages refuse MLP. */
+ * proj -> residual -> LN2 -> fc1 -> GELU -> fc2 -> residual (+ next block's
+ * LN1) kernel of the stages that run it (stage 0); those stages launch LN1
+ * only in block 0 and refuse PROJ / LN2 / FC1 / FC2, the other stages refuse
+ * MLP. */
 enum {
     BFHIP_SWIN_LN1 = 0,
     BFHIP_SWIN_QKV = 1,
