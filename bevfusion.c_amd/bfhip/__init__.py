@@ -1,8 +1,9 @@
 """Python host side of the gfx950 camera-path library.
 
 Thin ctypes mirror of the C ABI in ``include/bf_cuda_ops.h``,
-``include/bf_cuda_swin.h`` and ``include/bf_cuda_camera.h`` (the reference's
-operator/plugin interface for this path).  PyTorch supplies device memory and
+``include/bf_cuda_swin.h``, ``include/bf_cuda_camera.h`` and
+``include/bf_cuda.h`` (the reference's operator/plugin interface for this
+path and for the lift-splat pooling that consumes it).  PyTorch supplies device memory and
 the current HIP stream; every computation runs in ``lib/libbfhip.so``.  There
 is no fallback: if the library is missing, importing an entry point raises.
 """
@@ -32,6 +33,21 @@ class ConvDesc(C.Structure):
         "padding_width", "output_height", "output_width", "transpose", "relu")]
 
 
+class LssDesc(C.Structure):
+    """``bf_lss_desc`` (include/bf_lss.h)."""
+    _fields_ = [("batches", _sz), ("cameras", _sz), ("depth_bins", _sz),
+                ("feature_height", _sz), ("feature_width", _sz), ("channels", _sz),
+                ("grid_minimum", C.c_float * 3), ("grid_step", C.c_float * 3),
+                ("grid_cells", _sz * 3)]
+
+
+def lss_desc(batches, cameras, depth_bins, height, width, channels, minimum, step, cells):
+    return LssDesc(batches, cameras, depth_bins, height, width, channels,
+                   (C.c_float * 3)(*minimum), (C.c_float * 3)(*step), (_sz * 3)(*cells))
+
+
+_lssp = C.POINTER(LssDesc)
+
 # Every symbol declared by include/*.h, with its ctypes signature.
 SIGNATURES = {
     "bf_cuda_conv2d_f32": (_i, [C.POINTER(ConvDesc), _vp, _vp, _vp, _vp, _vp, C.c_char_p, _sz]),
@@ -54,6 +70,17 @@ SIGNATURES = {
     "bfhip_debug_window_map": (_i, [_i, _i, _i, _i, _vp, _vp, _vp, C.c_char_p, _sz]),
     "bfhip_debug_window_attention": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp,
                                           C.c_char_p, _sz]),
+    "bf_cuda_available": (_i, [C.c_char_p, _sz]),
+    "bf_cuda_lss_lift_pool_f32": (_i, [_vp, _vp, _vp, _vp, _lssp, _vp, C.c_char_p, _sz]),
+    "bf_cuda_lss_geometry_to_ranks_f32": (_i, [_vp, _vp, _lssp, _vp, C.c_char_p, _sz]),
+    "bf_cuda_lss_lift_pool_ranks_f32": (_i, [_vp, _vp, _vp, _vp, _lssp, _vp, C.c_char_p, _sz]),
+    "bf_cuda_lss_plan_create": (_i, [_lssp, C.POINTER(_vp), C.c_char_p, _sz]),
+    "bf_cuda_lss_plan_destroy": (None, [_vp]),
+    "bf_cuda_lss_plan_resident_bytes": (_sz, [_vp]),
+    "bf_cuda_lss_plan_prepare_geometry_f32": (_i, [_vp, _vp, _vp, C.c_char_p, _sz]),
+    "bf_cuda_lss_plan_prepare_calibration_f32": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                                      _vp, _vp, C.c_char_p, _sz]),
+    "bf_cuda_lss_plan_forward_f32": (_i, [_vp, _vp, _vp, _vp, _vp, C.c_char_p, _sz]),
 }
 
 SWIN_OPS = ("ln1", "qkv", "attention", "proj", "ln2", "fc1", "fc2", "merge", "mlp")
@@ -157,6 +184,13 @@ def _ptr(t):
     torch = _torch()
     if not t.is_cuda or t.dtype != torch.float32 or not t.is_contiguous():
         raise BfHipError("expected a contiguous float32 device tensor")
+    return _vp(t.data_ptr())
+
+
+def _iptr(t):
+    torch = _torch()
+    if not t.is_cuda or t.dtype != torch.int32 or not t.is_contiguous():
+        raise BfHipError("expected a contiguous int32 device tensor")
     return _vp(t.data_ptr())
 
 
@@ -371,6 +405,101 @@ class CameraNeck:
         if self.handle:
             self.lib.bf_cuda_camera_neck_destroy(self.handle)
             self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# ------------------------------------------------------ lift-splat pooling
+def _lss_shapes(desc):
+    d = desc
+    return ((d.batches, d.cameras, d.depth_bins, d.feature_height, d.feature_width),
+            (d.batches, d.channels * d.grid_cells[2], d.grid_cells[0], d.grid_cells[1]))
+
+
+def lss_lift_pool(logits, context, geometry, desc, out=None, stream=None):
+    """Stateless lift + pool with float atomics (bf_cuda_lss_lift_pool_f32)."""
+    lib, err = hip_lib(), _err()
+    out = out if out is not None else _torch().empty(_lss_shapes(desc)[1], device=logits.device)
+    _check(lib.bf_cuda_lss_lift_pool_f32(_ptr(logits), _ptr(context), _ptr(geometry), _ptr(out),
+                                         C.byref(desc), _stream(stream), err, 512),
+           err, "bf_cuda_lss_lift_pool_f32")
+    return out
+
+
+def lss_geometry_to_ranks(geometry, desc, out=None, stream=None):
+    """[B,N,D,H,W,3] -> int32 cell ranks within each batch, -1 outside."""
+    lib, err = hip_lib(), _err()
+    torch = _torch()
+    out = out if out is not None else torch.empty(_lss_shapes(desc)[0], device=geometry.device,
+                                                  dtype=torch.int32)
+    _check(lib.bf_cuda_lss_geometry_to_ranks_f32(_ptr(geometry), _iptr(out), C.byref(desc),
+                                                 _stream(stream), err, 512),
+           err, "bf_cuda_lss_geometry_to_ranks_f32")
+    return out
+
+
+def lss_lift_pool_ranks(logits, context, ranks, desc, out=None, stream=None):
+    """Stateless lift + pool from precomputed ranks (float atomics)."""
+    lib, err = hip_lib(), _err()
+    out = out if out is not None else _torch().empty(_lss_shapes(desc)[1], device=logits.device)
+    _check(lib.bf_cuda_lss_lift_pool_ranks_f32(_ptr(logits), _ptr(context), _iptr(ranks),
+                                               _ptr(out), C.byref(desc), _stream(stream), err,
+                                               512),
+           err, "bf_cuda_lss_lift_pool_ranks_f32")
+    return out
+
+
+class LssPlan:
+    """bf_cuda_lss_plan: deterministic lift-splat pooling (include/bf_cuda.h)."""
+
+    def __init__(self, desc: LssDesc):
+        self.lib, self.desc = hip_lib(), desc
+        self.handle, err = _vp(), _err()
+        _check(self.lib.bf_cuda_lss_plan_create(C.byref(desc), C.byref(self.handle), err, 512),
+               err, "bf_cuda_lss_plan_create")
+
+    def resident_bytes(self) -> int:
+        return self.lib.bf_cuda_lss_plan_resident_bytes(self.handle)
+
+    def prepare_geometry(self, geometry, stream=None):
+        err = _err()
+        _check(self.lib.bf_cuda_lss_plan_prepare_geometry_f32(self.handle, _ptr(geometry),
+                                                              _stream(stream), err, 512),
+               err, "bf_cuda_lss_plan_prepare_geometry_f32")
+
+    def prepare_calibration(self, frustum, camera_rotation, camera_translation, intrinsics,
+                            post_rotation, post_translation, extra_rotation=None,
+                            extra_translation=None, stream=None):
+        err = _err()
+        _check(self.lib.bf_cuda_lss_plan_prepare_calibration_f32(
+            self.handle, _ptr(frustum), _ptr(camera_rotation), _ptr(camera_translation),
+            _ptr(intrinsics), _ptr(post_rotation), _ptr(post_translation), _ptr(extra_rotation),
+            _ptr(extra_translation), _stream(stream), err, 512),
+            err, "bf_cuda_lss_plan_prepare_calibration_f32")
+
+    def forward(self, logits, context, out=None, stream=None):
+        out = out if out is not None else _torch().empty(_lss_shapes(self.desc)[1],
+                                                         device=logits.device)
+        err = _err()
+        _check(self.lib.bf_cuda_lss_plan_forward_f32(self.handle, _ptr(logits), _ptr(context),
+                                                     _ptr(out), _stream(stream), err, 512),
+               err, "bf_cuda_lss_plan_forward_f32")
+        return out
+
+    def close(self):
+        if self.handle:
+            self.lib.bf_cuda_lss_plan_destroy(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
 
     def __del__(self):
         try:

@@ -54,6 +54,19 @@ class WindowDesc(C.Structure):
         "batches", "height", "width", "channels", "heads", "window_size", "shift_size")]
 
 
+class LssDesc(C.Structure):
+    """bf_lss_desc (include/bf_lss.h)."""
+    _fields_ = [("batches", _sz), ("cameras", _sz), ("depth_bins", _sz),
+                ("feature_height", _sz), ("feature_width", _sz), ("channels", _sz),
+                ("grid_minimum", C.c_float * 3), ("grid_step", C.c_float * 3),
+                ("grid_cells", _sz * 3)]
+
+
+def lss_desc(batches, cameras, depth_bins, height, width, channels, minimum, step, cells):
+    return LssDesc(batches, cameras, depth_bins, height, width, channels,
+                   (C.c_float * 3)(*minimum), (C.c_float * 3)(*step), (_sz * 3)(*cells))
+
+
 class OracleError(RuntimeError):
     pass
 
@@ -130,6 +143,14 @@ class Oracle:
             C.c_char_p, _sz]
         L.bf_lss_downsample_forward_ref.argtypes = [
             C.c_void_p, _f32p, _sz, _sz, _sz, _f32p, C.c_void_p, _sz, C.c_char_p, _sz]
+        L.bf_lss_geometry_f32_ref.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p,
+                                              C.c_void_p, C.c_void_p, _f32p, _sz, _sz, _sz,
+                                              _sz, _sz]
+        L.bf_lss_lift_f32_ref.argtypes = [_f32p, _f32p, _f32p, C.POINTER(LssDesc)]
+        L.bf_lss_bev_pool_f32_ref.argtypes = [_f32p, _f32p, _f32p, C.POINTER(LssDesc)]
+        L.bf_lss_lift_pool_f32_ref.argtypes = [_f32p, _f32p, _f32p, _f32p, C.POINTER(LssDesc)]
+        if hasattr(L, "bf_oracle_lss_ranks"):
+            L.bf_oracle_lss_ranks.argtypes = [_f32p, C.c_void_p, C.POINTER(LssDesc)]
 
     # ---- utilities -------------------------------------------------------
     def backend(self) -> str:
@@ -305,6 +326,57 @@ class Oracle:
             return out
         finally:
             self.lib.bf_lss_downsample_destroy(net)
+
+
+    # ---- lift-splat pooling (bf_lss.h) ------------------------------------
+    def lss_geometry(self, frustum, cam_rot, cam_trans, intrinsics, post_rot, post_trans,
+                     extra_rot=None, extra_trans=None):
+        """frustum [D,H,W,3]; per-camera matrices [B,N,3,3] / [B,N,3]; optional
+        per-batch extra [B,3,3] / [B,3].  Returns geometry [B,N,D,H,W,3]."""
+        fr = _f32(frustum)
+        b, n = cam_rot.shape[:2]
+        d, h, w = fr.shape[:3]
+        out = np.empty((b, n, d, h, w, 3), np.float32)
+        er = None if extra_rot is None else _f32(extra_rot)
+        et = None if extra_trans is None else _f32(extra_trans)
+        if not self.lib.bf_lss_geometry_f32_ref(
+                fr, _f32(cam_rot), _f32(cam_trans), _f32(intrinsics), _f32(post_rot),
+                _f32(post_trans), None if er is None else er.ctypes.data,
+                None if et is None else et.ctypes.data, out, b, n, d, h, w):
+            raise OracleError("LSS geometry failed (singular matrix)")
+        return out
+
+    def lss_lift(self, logits, context, desc):
+        out = np.empty(tuple(logits.shape) + (desc.channels,), np.float32)
+        if not self.lib.bf_lss_lift_f32_ref(_f32(logits), _f32(context), out, C.byref(desc)):
+            raise OracleError("LSS lift failed")
+        return out
+
+    @staticmethod
+    def _bev_shape(desc):
+        return (desc.batches, desc.channels * desc.grid_cells[2], desc.grid_cells[0],
+                desc.grid_cells[1])
+
+    def lss_bev_pool(self, lifted, geometry, desc):
+        out = np.empty(self._bev_shape(desc), np.float32)
+        if not self.lib.bf_lss_bev_pool_f32_ref(_f32(lifted), _f32(geometry), out, C.byref(desc)):
+            raise OracleError("LSS pool failed")
+        return out
+
+    def lss_ranks(self, geometry, desc):
+        """Per-sample cell rank within its batch, -1 outside (int32)."""
+        g = _f32(geometry)
+        out = np.empty(g.shape[:-1], np.int32)
+        if not self.lib.bf_oracle_lss_ranks(g, out.ctypes.data, C.byref(desc)):
+            raise OracleError("LSS ranks failed")
+        return out
+
+    def lss_lift_pool(self, logits, context, geometry, desc):
+        out = np.empty(self._bev_shape(desc), np.float32)
+        if not self.lib.bf_lss_lift_pool_f32_ref(_f32(logits), _f32(context), _f32(geometry),
+                                                 out, C.byref(desc)):
+            raise OracleError("LSS lift-pool failed")
+        return out
 
 
 class _Model:

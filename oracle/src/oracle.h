@@ -12,6 +12,7 @@
  *   bf_image_fpn.h      -> reference include/bf_image_fpn.h,     src/image_fpn.c:73-197
  *   bf_depth_head.h     -> reference include/bf_depth_head.h,    src/depth_head.c:96-190
  *   bf_lss_downsample.h -> reference include/bf_lss_downsample.h, src/lss_downsample.c:70-148
+ *   bf_lss.h            -> reference include/bf_lss.h:18-46,     src/lss.c:8-241
  * Floating-point operation order matches the reference per output element, so
  * the scalar build (no OpenMP, BF_CPU_SCALAR=1) is bit-identical to the
  * reference compiled from its own sources (oracle/_ref).
@@ -19,6 +20,7 @@
 #ifndef BF_ORACLE_H
 #define BF_ORACLE_H
 
+#include "bf_lss.h"
 #include "bf_model.h"
 
 #include <stddef.h>
@@ -165,6 +167,24 @@ int bf_oracle_mul(size_t a, size_t b, size_t *out);
 const void *bf_oracle_bind(const bf_model *model, const char *name, uint32_t dtype,
                            uint32_t rank, const uint32_t *dims,
                            char *error, size_t cap);
+
+/* ---- lift-splat pooling (bf_lss.h) ------------------------------------ */
+int bf_lss_geometry_f32_ref(const float *frustum_dhw3, const float *camera_to_lidar_rotation,
+                            const float *camera_to_lidar_translation, const float *intrinsics,
+                            const float *post_rotation, const float *post_translation,
+                            const float *extra_rotation, const float *extra_translation,
+                            float *geometry_bndhw3, size_t batches, size_t cameras,
+                            size_t depth_bins, size_t height, size_t width);
+int bf_lss_lift_f32_ref(const float *depth_logits_bndhw, const float *context_bnchw,
+                        float *lifted_bndhwc, const bf_lss_desc *desc);
+int bf_lss_bev_pool_f32_ref(const float *lifted_bndhwc, const float *geometry_bndhw3,
+                            float *bev_bczxy, const bf_lss_desc *desc);
+int bf_lss_lift_pool_f32_ref(const float *depth_logits_bndhw, const float *context_bnchw,
+                             const float *geometry_bndhw3, float *bev_bczxy,
+                             const bf_lss_desc *desc);
+/* Test helper (no reference counterpart): per-sample cell rank within its
+ * batch, (z * X + x) * Y + y, -1 outside the grid. */
+int bf_oracle_lss_ranks(const float *geometry_bndhw3, int32_t *ranks, const bf_lss_desc *desc);
 
 #ifdef __cplusplus
 }

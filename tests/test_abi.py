@@ -3,7 +3,7 @@
 libbfhip.so must load, export every entry point declared in include/*.h, and
 reject invalid contracts before launching anything (reference
 src/cuda_ops.cu:150-170,192-196; cuda_swin.cu:272-273; cuda_camera.cu:288-290;
-tests/test_cuda_ops.cu:164-174).
+cuda_lss.cu:50-61,617-634,790-797; tests/test_cuda_ops.cu:164-174).
 """
 
 import ctypes as C
@@ -13,8 +13,8 @@ import re
 import bfhip
 
 ROOT = pathlib.Path(__file__).resolve().parent.parent
-HEADERS = ["bf_cuda_ops.h", "bf_cuda_swin.h", "bf_cuda_camera.h", "bfhip_profile.h",
-           "bfhip_debug.h"]
+HEADERS = ["bf_cuda_ops.h", "bf_cuda_swin.h", "bf_cuda_camera.h", "bf_cuda.h",
+           "bfhip_profile.h", "bfhip_debug.h"]
 
 
 def declared(header):
@@ -26,7 +26,7 @@ def declared(header):
 def test_every_declared_entry_point_is_exported():
     lib = bfhip.hip_lib()
     names = set().union(*(declared(h) for h in HEADERS))
-    assert len(names) == 17
+    assert len(names) == 27
     assert names == set(bfhip.SIGNATURES)
     missing = [n for n in sorted(names) if not hasattr(lib, n)]
     assert not missing, missing
@@ -106,3 +106,49 @@ def test_index_probes_reject_invalid():
     assert lib.bfhip_debug_window_attention(s, s, s, s, 70000, 7000, 7000, 96, 3, 3, None, e,
                                             256) == 0
     assert b"too large" in e.value
+
+
+def test_lss_entry_points_reject_invalid_contracts():
+    lib = bfhip.hip_lib()
+    e = _err()
+    s = C.c_void_p(1)
+    good = dict(batches=1, cameras=6, depth_bins=118, height=32, width=88, channels=80,
+                minimum=(-54, -54, -10), step=(0.3, 0.3, 20), cells=(360, 360, 1))
+
+    def desc(**kw):
+        a = {**good, **kw}
+        return bfhip.lss_desc(a["batches"], a["cameras"], a["depth_bins"], a["height"],
+                              a["width"], a["channels"], a["minimum"], a["step"], a["cells"])
+
+    plan = C.c_void_p()
+    assert lib.bf_cuda_lss_plan_create(None, C.byref(plan), e, 256) == 0
+    assert b"invalid" in e.value and not plan
+    bad = [desc(depth_bins=0), desc(depth_bins=129), desc(channels=0),
+           desc(step=(0.3, 0.0, 20)), desc(step=(0.3, -1.0, 20)),
+           desc(step=(float("inf"), 0.3, 20)), desc(minimum=(float("nan"), 0, 0)),
+           desc(cells=(360, 0, 1)), desc(cells=(1 << 31, 1, 1))]
+    for d in bad:
+        e.value = b""
+        assert lib.bf_cuda_lss_plan_create(C.byref(d), C.byref(plan), e, 256) == 0
+        assert b"invalid" in e.value and not plan
+        assert lib.bf_cuda_lss_lift_pool_f32(s, s, s, s, C.byref(d), None, e, 256) == 0
+        assert lib.bf_cuda_lss_geometry_to_ranks_f32(s, s, C.byref(d), None, e, 256) == 0
+        assert lib.bf_cuda_lss_lift_pool_ranks_f32(s, s, s, s, C.byref(d), None, e, 256) == 0
+    # valid contract whose element counts overflow 32-bit indexing
+    huge = desc(cells=(50000, 50000, 1))
+    assert lib.bf_cuda_lss_plan_create(C.byref(huge), C.byref(plan), e, 256) == 0
+    assert b"overflow" in e.value
+    assert lib.bf_cuda_lss_lift_pool_f32(s, s, s, s, C.byref(huge), None, e, 256) == 0
+    assert b"overflow" in e.value
+    d = desc()
+    assert lib.bf_cuda_lss_lift_pool_f32(None, s, s, s, C.byref(d), None, e, 256) == 0
+    assert lib.bf_cuda_lss_lift_pool_ranks_f32(s, s, None, s, C.byref(d), None, e, 256) == 0
+    assert lib.bf_cuda_lss_geometry_to_ranks_f32(s, None, C.byref(d), None, e, 256) == 0
+    assert lib.bf_cuda_lss_plan_prepare_geometry_f32(None, s, None, e, 256) == 0
+    assert lib.bf_cuda_lss_plan_prepare_calibration_f32(None, s, s, s, s, s, s, None, None,
+                                                        None, e, 256) == 0
+    e.value = b""
+    assert lib.bf_cuda_lss_plan_forward_f32(None, s, s, s, None, e, 256) == 0
+    assert b"unprepared" in e.value
+    assert lib.bf_cuda_lss_plan_resident_bytes(None) == 0
+    lib.bf_cuda_lss_plan_destroy(None)
