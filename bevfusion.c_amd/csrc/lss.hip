@@ -24,8 +24,11 @@
 #include "hip_common.h"
 
 #include <rocprim/device/device_radix_sort.hpp>
+#include <rocprim/device/device_scan.hpp>
 #include <rocprim/iterator/counting_iterator.hpp>
+#include <rocprim/iterator/transform_iterator.hpp>
 
+#include <algorithm>
 #include <cfloat>
 #include <climits>
 #include <cmath>
@@ -232,30 +235,125 @@ __global__ __launch_bounds__(256) void cell_starts_kernel(const int *__restrict_
     starts[c] = lo;
 }
 
-// From the sorted sample order: every sample's position in the list (where the
-// forward's softmax stores its probability) and the context row each list
-// entry reads.
-__global__ __launch_bounds__(256) void list_maps_kernel(const int *__restrict__ order,
-                                                       int *__restrict__ position,
-                                                       int *__restrict__ list_pixel, int samples,
-                                                       int depth_hw, int hw) {
+// Padded cell lists.  Every cell's run is padded to a multiple of 4 entries
+// (kQuad) so that cell boundaries fall on quad boundaries; padding entries
+// carry sample -1 (weight 0 on an all-zero context row).
+constexpr int kQuad = 4;
+
+struct PaddedCount {
+    const int *starts;
+    __host__ __device__ int operator()(int c) const {
+        const int n = starts[c + 1] - starts[c];
+        return (n + kQuad - 1) & ~(kQuad - 1);
+    }
+};
+
+// Sorted position i of a valid sample -> its padded slot: {pixel, sample}.
+__global__ __launch_bounds__(256) void list_entries_kernel(const int *__restrict__ order,
+                                                          const int *__restrict__ sorted_keys,
+                                                          const int *__restrict__ starts,
+                                                          const int *__restrict__ padded_starts,
+                                                          int2 *__restrict__ list, int samples,
+                                                          int cell_count, int depth_hw, int hw) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= samples) return;
+    const int key = sorted_keys[i];
+    if (key >= cell_count) return;
     const int s = order[i];
     const int cam = s / depth_hw;
-    position[s] = i;
-    list_pixel[i] = cam * hw + (s - cam * depth_hw) % hw;
+    list[padded_starts[key] + (i - starts[key])] =
+        make_int2(cam * hw + (s - cam * depth_hw) % hw, s);
 }
 
-// Max-shifted depth softmax (reference lss.c:144-158 operation order: float
-// max, double sum of expf(l - max), inverse rounded to float, p = e * inv).
-// Workgroup = 32 pixels x 8 depth slices of kSlice bins; each probability is
-// stored at its sample's list position.
+__global__ __launch_bounds__(256) void list_padding_kernel(const int *__restrict__ starts,
+                                                          const int *__restrict__ padded_starts,
+                                                          int2 *__restrict__ list,
+                                                          int cell_count) {
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= cell_count) return;
+    const int first = padded_starts[c] + (starts[c + 1] - starts[c]);
+    for (int k = first; k < padded_starts[c + 1]; ++k) list[k] = make_int2(0, -1);
+}
+
+// Pool schedule.  The BEV output is cut into tiles of kTileCells consecutive
+// cells of one batch; a tile whose lists hold more than kSliceEntries entries
+// is cut into equal slices, each pooled by its own workgroup into a partial
+// tile that a second pass adds up in slice order.
+constexpr int kTileCells = 64;
+constexpr int kSliceEntries = 2048;
+constexpr int kScheduleThreads = 1024;
+
+// One workgroup: per tile, slice count; exclusive scans give each tile's
+// first work item, its first scratch slot (multi-slice tiles only) and its
+// index among multi-slice tiles.  sched layout: slices[tiles],
+// slice_base[tiles + 1], scratch_base[tiles], multi_base[tiles + 1].
+__global__ __launch_bounds__(kScheduleThreads) void schedule_kernel(const int *__restrict__ starts,
+                                                                   int *__restrict__ sched,
+                                                                   int tiles, int tiles_per_batch,
+                                                                   int cells) {
+    __shared__ int part[3][kScheduleThreads];
+    int *slices = sched, *slice_base = sched + tiles, *scratch_base = slice_base + tiles + 1,
+        *multi_base = scratch_base + tiles;
+    const int t = threadIdx.x, per = (tiles + kScheduleThreads - 1) / kScheduleThreads;
+    const int lo = min(tiles, t * per), hi = min(tiles, lo + per);
+    int sum[3] = {0, 0, 0};
+    for (int i = lo; i < hi; ++i) {
+        const int b = i / tiles_per_batch, j0 = (i - b * tiles_per_batch) * kTileCells;
+        const int first = b * cells + j0, last = b * cells + min(cells, j0 + kTileCells);
+        const int entries = starts[last] - starts[first];
+        const int ns = max(1, (entries + kSliceEntries - 1) / kSliceEntries);
+        slices[i] = ns;
+        sum[0] += ns;
+        sum[1] += ns > 1 ? ns : 0;
+        sum[2] += ns > 1;
+    }
+    for (int q = 0; q < 3; ++q) part[q][t] = sum[q];
+    __syncthreads();
+    for (int off = 1; off < kScheduleThreads; off <<= 1) {  // inclusive scans
+        int v[3];
+        for (int q = 0; q < 3; ++q) v[q] = t >= off ? part[q][t - off] : 0;
+        __syncthreads();
+        for (int q = 0; q < 3; ++q) part[q][t] += v[q];
+        __syncthreads();
+    }
+    int run[3];
+    for (int q = 0; q < 3; ++q) run[q] = part[q][t] - sum[q];
+    for (int i = lo; i < hi; ++i) {
+        const int ns = slices[i];
+        slice_base[i] = run[0];
+        scratch_base[i] = run[1];
+        multi_base[i] = run[2];
+        run[0] += ns;
+        run[1] += ns > 1 ? ns : 0;
+        run[2] += ns > 1;
+    }
+    if (t == kScheduleThreads - 1) {
+        slice_base[tiles] = part[0][t];
+        multi_base[tiles] = part[2][t];
+    }
+}
+
+// Work list: item slice_base[t] + k = (tile t, slice k); multi-slice tiles
+// listed in tile order.
+__global__ __launch_bounds__(256) void work_list_kernel(const int *__restrict__ sched,
+                                                       int2 *__restrict__ work,
+                                                       int *__restrict__ multi, int tiles) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= tiles) return;
+    const int *slices = sched, *slice_base = sched + tiles, *multi_base = slice_base + 2 * tiles + 1;
+    const int ns = slices[t];
+    for (int k = 0; k < ns; ++k) work[slice_base[t] + k] = make_int2(t, k);
+    if (ns > 1) multi[multi_base[t]] = t;
+}
+
+// Per-pixel depth softmax statistics {max, 1 / sum exp(l - max)} (reference
+// lss.c:144-158 operation order: float max, double sum of expf(l - max), the
+// inverse rounded to float); a sample's probability is then
+// expf(l - max) * inv.  Workgroup = 32 pixels x 8 depth slices of kSlice bins.
 constexpr int kSoftmaxPixels = 32, kSlices = 8, kSlice = kMaxDepth / kSlices;
-__global__ __launch_bounds__(256) void softmax_list_kernel(const float *__restrict__ logits,
-                                                          const int *__restrict__ position,
-                                                          float *__restrict__ list_prob,
-                                                          int pixels, int depths, int hw) {
+__global__ __launch_bounds__(256) void softmax_stats_kernel(const float *__restrict__ logits,
+                                                           float2 *__restrict__ stats, int pixels,
+                                                           int depths, int hw) {
     __shared__ float part_max[kSlices][kSoftmaxPixels];
     __shared__ double part_sum[kSlices][kSoftmaxPixels];
     const int lane = threadIdx.x & (kSoftmaxPixels - 1), slice = threadIdx.x / kSoftmaxPixels;
@@ -279,25 +377,15 @@ __global__ __launch_bounds__(256) void softmax_list_kernel(const float *__restri
     for (int j = 1; j < kSlices; ++j) m = fmaxf(m, part_max[j][lane]);
     double sum = 0.0;
 #pragma unroll
-    for (int k = 0; k < kSlice; ++k) {
-        v[k] = (d0 + k < depths) ? expf(v[k] - m) : 0.0f;
-        sum += v[k];
-    }
+    for (int k = 0; k < kSlice; ++k)
+        if (d0 + k < depths) sum += expf(v[k] - m);
     part_sum[slice][lane] = sum;
     __syncthreads();
+    if (slice != 0 || !live) return;
     double total = 0.0;
 #pragma unroll
     for (int j = 0; j < kSlices; ++j) total += part_sum[j][lane];
-    const float inv = (float)(1.0 / total);
-    if (!live) return;
-#pragma unroll
-    for (int k = 0; k < kSlice; ++k) {
-        const int d = d0 + k;
-        if (d < depths) {
-            const size_t s = base + (size_t)d * hw;
-            list_prob[position[s]] = v[k] * inv;
-        }
-    }
+    stats[px] = make_float2(m, (float)(1.0 / total));
 }
 
 // Context [cams][C][hw] -> [cams * hw][C] through a 64 x 64 LDS tile.
@@ -319,89 +407,210 @@ __global__ __launch_bounds__(256) void context_rows_kernel(const float *__restri
     }
 }
 
-// Cell pooling over the sorted lists: a group of L lanes (VW channels each)
-// owns one cell at a time and sums prob * context row over the cell's list in
-// list order; the workgroup's 64 consecutive cells land in an LDS tile
-// [channel][cell] that is stored as coalesced 64-cell rows of every channel
-// plane.  The next chunk of (row, prob) list entries is loaded while the
-// current one is consumed.
-constexpr int kTileCells = 64;
+// ------------------------------------------------------------------ pooling
+// Work item = (tile, slice): quads [e0, e1) of the tile's padded list.  The
+// workgroup's lane groups (L lanes x VW channels each) split [e0, e1) evenly
+// in quads and walk their share in list order, ROUND entries at a time (all
+// their context rows in flight together; ROUND = 16 when every group has at
+// least 16 lanes, else 4).  Lane u of a group prepares entry
+// u of the round (its probability and row offset) and the group reads them by
+// lane permutes.  A cell's sum is closed at each list boundary (a quad
+// boundary) into an LDS tile [channel][cell]; a cell that began in an earlier
+// group is continued as a carry, added to the owner's sum in group order.
+// Single-slice tiles store the tile; slices of larger tiles store partial
+// tiles for the combine pass.  Every sum runs in a fixed order, so results
+// are bit-identical from run to run.
+constexpr int kRoundWide = 16;
+
+struct PoolArgs {
+    const int2 *list;          // padded sorted {pixel, sample}
+    const float *logits;       // [B,N,D,H,W]
+    const float2 *stats;       // per pixel {max, inv}
+    const float *rows;         // [B*N*H*W + 1][C]; the last row is zero
+    const int *starts;         // padded list start per cell [cell_count + 1]
+    const int *sched;          // schedule_kernel layout
+    const int2 *work;          // (tile, slice)
+    float *scratch;            // partial tiles: [slot][pass][chunk_max][64]
+    float *bev;
+    int cells, tiles, tiles_per_batch, C, passes, chunk_max, zero_row;
+    unsigned row_bytes, rows_bytes;  // C * 4; (B*N*H*W + 1) * C * 4 < 2^32
+};
+
 template <int VW>
-__global__ __launch_bounds__(256) void pool_tile_kernel(const float *__restrict__ list_prob,
-                                                       const int *__restrict__ list_pixel,
-                                                       const float *__restrict__ rows,
-                                                       const int *__restrict__ starts,
-                                                       float *__restrict__ bev, int cells, int C) {
-    // [64 * VW channels][64 cells], cell index XOR-swizzled by the channel so
-    // that both the per-cell column writes and the per-channel row reads are
-    // free of bank conflicts.
-    extern __shared__ float tile[];
+__device__ __forceinline__ void close_cell(float *tile, float *carry, int *carry_cell, bool is_carry,
+                                           int t, const float *acc, int g, int L, int lig,
+                                           bool live) {
+    if (is_carry) {
+#pragma unroll
+        for (int j = 0; j < VW; ++j) carry[(g * L + lig) * VW + j] = acc[j];
+        if (lig == 0) carry_cell[g] = t;
+    } else if (live) {
+#pragma unroll
+        for (int j = 0; j < VW; ++j) {
+            const int c = VW * lig + j;
+            tile[c * kTileCells + (t ^ (c & 63))] = acc[j];
+        }
+    }
+}
+
+template <int VW, int ROUND>
+__global__ __launch_bounds__(256) void pool_kernel(PoolArgs a) {
+    static_assert(ROUND % kQuad == 0, "rounds are whole quads");
+    extern __shared__ float tile[];  // [chunk_max][64], cell XOR-swizzled by channel
+    __shared__ int s_start[kTileCells + 1];
+    __shared__ int carry_cell[256];
+    __shared__ float carry[256 * VW];
+    const int *slices = a.sched, *slice_base = a.sched + a.tiles;
+    if ((int)blockIdx.x >= slice_base[a.tiles]) return;
+    const int2 wk = a.work[blockIdx.x];
+    const int tile_id = wk.x, k = wk.y;
+    const int b = tile_id / a.tiles_per_batch, j0 = (tile_id - b * a.tiles_per_batch) * kTileCells;
+    const int tile_cells = min(kTileCells, a.cells - j0);
+    const int oc0 = b * a.cells + j0;
+    if ((int)threadIdx.x <= tile_cells) s_start[threadIdx.x] = a.starts[oc0 + threadIdx.x];
+    __syncthreads();
+    const int ns = slices[tile_id];
+    const int Q0 = s_start[0] / kQuad, Qn = s_start[tile_cells] / kQuad - Q0;
+    const int e0 = kQuad * (Q0 + (int)((long long)Qn * k / ns));
+    const int e1 = kQuad * (Q0 + (int)((long long)Qn * (k + 1) / ns));
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int b = blockIdx.y, cell0 = blockIdx.x * kTileCells;
-    const int tile_cells = min(kTileCells, cells - cell0);
-    for (int c0 = 0; c0 < C; c0 += 64 * VW) {
-        const int chunk = min(64 * VW, C - c0);
-        const int L = (chunk + VW - 1) / VW, G = 64 / L;
-        const int gi = lane / L, lig = lane - gi * L, gbase = gi * L;
-        const int ch = c0 + VW * lig;
-        if (gi < G) {
-            for (int t = wave * G + gi; t < tile_cells; t += 4 * G) {
-                const int oc = b * cells + cell0 + t;
-                const int lo = starts[oc], hi = starts[oc + 1];
-                float acc[VW];
+    for (int pass = 0; pass < a.passes; ++pass) {
+        const int c0 = pass * a.chunk_max, chunk = min(a.chunk_max, a.C - c0);
+        // L >= ROUND lanes per group: lane u < ROUND prepares entry u
+        const int L = max(ROUND, (chunk + VW - 1) / VW), G = 64 / L, NG = 4 * G;
+        constexpr int E = ROUND;
+        const int gi = lane / L, lig = lane - gi * L, gbase = gi * L, g = wave * G + gi;
+        const bool live = VW * lig < chunk;  // this lane owns channels
+        for (int i = threadIdx.x; i < chunk * kTileCells; i += 256) tile[i] = 0.0f;
+        carry_cell[threadIdx.x] = -1;
+        __syncthreads();
+        const int nq = (e1 - e0) / kQuad;
+        const int g_lo = e0 + kQuad * (int)((long long)nq * g / NG);
+        const int g_hi = e0 + kQuad * (int)((long long)nq * (g + 1) / NG);
+        if (gi < G && g_lo < g_hi) {
+            // context rows through a buffer resource: 32-bit byte offsets
+            const __amdgpu_buffer_rsrc_t rows = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float *>(a.rows), 0, (int)a.rows_bytes, 0x00020000);
+            const unsigned ch_bytes = live ? 4u * (unsigned)(c0 + VW * lig) : 0u;
+            // the cell holding entry g_lo: last t with s_start[t] <= g_lo
+            int lo_t = 0, hi_t = tile_cells;
+            while (hi_t - lo_t > 1) {
+                const int mid = (lo_t + hi_t) >> 1;
+                if (s_start[mid] <= g_lo) lo_t = mid;
+                else hi_t = mid;
+            }
+            int t = lo_t, boundary = s_start[t + 1];
+            bool is_carry = g_lo > max(s_start[t], e0);
+            float acc[VW];
 #pragma unroll
-                for (int j = 0; j < VW; ++j) acc[j] = 0.0f;
-                int next_pix = 0;
-                float next_pr = 0.0f;
-                if (lo + lig < hi) {
-                    next_pix = list_pixel[lo + lig];
-                    next_pr = list_prob[lo + lig];
+            for (int j = 0; j < VW; ++j) acc[j] = 0.0f;
+            // Rounds in flight: entries of round r + 2, softmax inputs of
+            // round r + 1, context rows of round r.
+            int2 e_next = make_int2(0, -1), e_cur = make_int2(0, -1);
+            float2 st = make_float2(0.0f, 0.0f);
+            float lg = 0.0f;
+            if (lig < E && g_lo + lig < g_hi) e_cur = a.list[g_lo + lig];
+            if (lig < E && g_lo + E + lig < g_hi) e_next = a.list[g_lo + E + lig];
+            if (e_cur.y >= 0) {
+                st = a.stats[e_cur.x];
+                lg = a.logits[e_cur.y];
+            }
+            for (int base = g_lo; base < g_hi; base += E) {
+                const int n = min(E, g_hi - base);  // whole quads
+                const int2 cur = e_cur;
+                const float2 cst = st;
+                const float clg = lg;
+                e_cur = e_next;
+                e_next = make_int2(0, -1);
+                if (lig < E && base + 2 * E + lig < g_hi) e_next = a.list[base + 2 * E + lig];
+                if (e_cur.y >= 0) {
+                    st = a.stats[e_cur.x];
+                    lg = a.logits[e_cur.y];
                 }
-                for (int base = lo; base < hi; base += L) {
-                    const int n = min(L, hi - base);
-                    const int my_pix = next_pix;
-                    const float my_pr = next_pr;
-                    if (base + L + lig < hi) {
-                        next_pix = list_pixel[base + L + lig];
-                        next_pr = list_prob[base + L + lig];
-                    }
-                    for (int k = 0; k < n; k += 4) {
-                        int pk[4];
-                        float wk[4], vk[4][VW];
+                // entry of lane u: probability and row offset (zero row for padding)
+                const bool real = cur.y >= 0;
+                const float pr = real ? expf(clg - cst.x) * cst.y : 0.0f;
+                const unsigned off = (unsigned)(real ? cur.x : a.zero_row) * a.row_bytes;
+                float v[ROUND][VW], w[ROUND];
 #pragma unroll
-                        for (int u = 0; u < 4; ++u) {
-                            const int src = gbase + (k + u < n ? k + u : 0);
-                            pk[u] = __shfl(my_pix, src);
-                            wk[u] = __shfl(my_pr, src);
-                            const float *row = rows + (size_t)pk[u] * C + ch;
-                            if (VW == 4) {
-                                const float4 q = *reinterpret_cast<const float4 *>(row);
-                                vk[u][0] = q.x; vk[u][1 % VW] = q.y;
-                                vk[u][2 % VW] = q.z; vk[u][3 % VW] = q.w;
-                            } else {
-                                vk[u][0] = ch < C ? row[0] : 0.0f;
-                            }
+                for (int u = 0; u < ROUND; ++u) {
+                    const unsigned pk = (unsigned)__shfl((int)off, gbase + u) + ch_bytes;
+                    w[u] = __shfl(pr, gbase + u);
+                    if constexpr (VW == 4) {
+                        const auto q = __builtin_amdgcn_raw_buffer_load_b128(rows, pk, 0, 0);
+#pragma unroll
+                        for (int j = 0; j < VW; ++j) v[u][j] = __uint_as_float(q[j]);
+                    } else {
+                        v[u][0] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rows, pk, 0, 0));
+                    }
+                }
+#pragma unroll
+                for (int q = 0; q < ROUND / kQuad; ++q) {
+                    if (kQuad * q < n) {
+                        if (base + kQuad * q == boundary) {
+                            close_cell<VW>(tile, carry, carry_cell, is_carry, t, acc, g, L, lig, live);
+                            is_carry = false;
+#pragma unroll
+                            for (int j = 0; j < VW; ++j) acc[j] = 0.0f;
+                            do {
+                                ++t;
+                                boundary = s_start[t + 1];
+                            } while (boundary <= base + kQuad * q);
                         }
 #pragma unroll
-                        for (int u = 0; u < 4; ++u)
-                            if (k + u < n)
+                        for (int u = kQuad * q; u < kQuad * (q + 1); ++u)
 #pragma unroll
-                                for (int j = 0; j < VW; ++j) acc[j] += wk[u] * vk[u][j];
+                            for (int j = 0; j < VW; ++j) acc[j] += w[u] * v[u][j];
                     }
                 }
-#pragma unroll
-                for (int j = 0; j < VW; ++j) {
-                    const int c = VW * lig + j;
-                    tile[c * kTileCells + (t ^ (c & 63))] = acc[j];
-                }
+            }
+            close_cell<VW>(tile, carry, carry_cell, is_carry, t, acc, g, L, lig, live);
+        }
+        __syncthreads();
+        if ((int)threadIdx.x < chunk) {  // carries, in group order
+            const int c = threadIdx.x, lg = c / VW, jj = c - lg * VW;
+            for (int q = 0; q < NG; ++q) {
+                const int t = carry_cell[q];
+                if (t >= 0) tile[c * kTileCells + (t ^ (c & 63))] += carry[(q * L + lg) * VW + jj];
             }
         }
         __syncthreads();
-        float *out = bev + ((size_t)b * C + c0) * cells + cell0;
         const int j = threadIdx.x & 63;
-        for (int c = threadIdx.x >> 6; c < chunk; c += 4)
-            if (j < tile_cells) out[(size_t)c * cells + j] = tile[c * kTileCells + (j ^ (c & 63))];
+        if (ns == 1) {
+            float *out = a.bev + ((size_t)b * a.C + c0) * a.cells + j0;
+            for (int c = threadIdx.x >> 6; c < chunk; c += 4)
+                if (j < tile_cells) out[(size_t)c * a.cells + j] = tile[c * kTileCells + (j ^ (c & 63))];
+        } else {
+            const int slot = a.sched[2 * a.tiles + 1 + tile_id] + k;  // scratch_base[tile] + k
+            float *part = a.scratch + ((size_t)slot * a.passes + pass) * a.chunk_max * kTileCells;
+            for (int c = threadIdx.x >> 6; c < chunk; c += 4)
+                part[c * kTileCells + j] = tile[c * kTileCells + (j ^ (c & 63))];
+        }
         __syncthreads();
+    }
+}
+
+// Sum of a multi-slice tile's partial tiles in slice order.
+__global__ __launch_bounds__(256) void combine_kernel(PoolArgs a, const int *__restrict__ multi) {
+    const int *slices = a.sched, *slice_base = a.sched + a.tiles;
+    const int *scratch_base = slice_base + a.tiles + 1, *multi_base = scratch_base + a.tiles;
+    if ((int)blockIdx.x >= multi_base[a.tiles]) return;
+    const int tile_id = multi[blockIdx.x], ns = slices[tile_id], slot0 = scratch_base[tile_id];
+    const int b = tile_id / a.tiles_per_batch, j0 = (tile_id - b * a.tiles_per_batch) * kTileCells;
+    const int tile_cells = min(kTileCells, a.cells - j0);
+    const int j = threadIdx.x & 63;
+    if (j >= tile_cells) return;
+    for (int pass = 0; pass < a.passes; ++pass) {
+        const int c0 = pass * a.chunk_max, chunk = min(a.chunk_max, a.C - c0);
+        float *out = a.bev + ((size_t)b * a.C + c0) * a.cells + j0;
+        for (int c = threadIdx.x >> 6; c < chunk; c += 4) {
+            const size_t e = (size_t)c * kTileCells + j;
+            const size_t stride = (size_t)a.passes * a.chunk_max * kTileCells;
+            const float *p = a.scratch + ((size_t)slot0 * a.passes + pass) * a.chunk_max * kTileCells + e;
+            float sum = p[0];
+            for (int q = 1; q < ns; ++q) sum += p[q * stride];
+            out[(size_t)c * a.cells + j] = sum;
+        }
     }
 }
 
@@ -475,24 +684,23 @@ int stateless_pool(const float *logits, const float *ctx, const float *geometry,
 
 }  // namespace
 
-// Plan memory (one arena).  Three sample-sized arrays change role once the
-// sort is done:  keys -> position (sample -> list slot),  sorted keys ->
-// list_pixel (list slot -> context row),  order -> list_prob (written by
-// every forward).
+// Plan memory (one arena).  keys / sorted keys / order are used only while
+// preparing; the forward reads the padded list, its starts and the schedule.
 struct bf_cuda_lss_plan {
     bf_lss_desc desc;
     Sizes z;
     int prepared;
     unsigned end_bit;  // sort key width: cell_count (the invalid key) is below 2^end_bit
-    int *keys, *sorted_keys, *order, *starts;
-    float *rows, *calib;
-    void *sort_tmp;
-    size_t sort_tmp_bytes;
+    int tiles, tiles_per_batch, max_work, max_multi, vw, chunk_max, passes, round;
+    size_t list_capacity;  // samples + (kQuad - 1) * cells: every cell padded to whole quads
+    int *keys, *sorted_keys, *order, *starts, *padded_starts, *sched, *multi;
+    int2 *list, *work;
+    float2 *stats;
+    float *rows, *calib, *scratch;
+    void *tmp;  // rocPRIM sort / scan scratch
+    size_t tmp_bytes;
     void *arena;
     size_t resident_bytes;
-    int *position() const { return keys; }
-    int *list_pixel() const { return sorted_keys; }
-    float *list_prob() const { return reinterpret_cast<float *>(order); }
 };
 
 extern "C" int bf_cuda_available(char *error, size_t cap) {
@@ -552,19 +760,49 @@ extern "C" int bf_cuda_lss_plan_create(const bf_lss_desc *d, bf_cuda_lss_plan **
     p->z = z;
     p->end_bit = 1;
     while (p->end_bit < 31 && (size_t(1) << p->end_bit) <= z.cell_count) ++p->end_bit;
-    if (!hip_ok(rocprim::radix_sort_pairs(nullptr, p->sort_tmp_bytes, (const unsigned *)nullptr,
+    p->list_capacity = z.samples + (size_t)(kQuad - 1) * z.cell_count;
+    // the pool addresses the context rows (plus a zero row) with 32-bit
+    // buffer offsets
+    if (p->list_capacity > (size_t)INT_MAX || (z.context_count + d->channels) * 4 > (size_t)INT_MAX) {
+        bf_cuda_lss_plan_destroy(p);
+        return fail(error, cap, "HIP LSS plan size overflow");
+    }
+    size_t sort_bytes = 0, scan_bytes = 0;
+    const auto padded = rocprim::make_transform_iterator(rocprim::counting_iterator<int>(0),
+                                                         PaddedCount{nullptr});
+    if (!hip_ok(rocprim::radix_sort_pairs(nullptr, sort_bytes, (const unsigned *)nullptr,
                                           (unsigned *)nullptr, rocprim::counting_iterator<int>(0),
                                           (int *)nullptr, (unsigned)z.samples, 0u, p->end_bit),
-                error, cap, "size HIP LSS plan sort")) {
+                error, cap, "size HIP LSS plan sort") ||
+        !hip_ok(rocprim::exclusive_scan(nullptr, scan_bytes, padded, (int *)nullptr, 0,
+                                        z.cell_count + 1, rocprim::plus<int>()),
+                error, cap, "size HIP LSS plan scan")) {
         bf_cuda_lss_plan_destroy(p);
         return 0;
     }
-    // keys, sorted keys, order [samples]; starts [cells + 1]; context rows;
-    // calibration; sort scratch.
-    const size_t parts[7] = {z.samples * 4, z.samples * 4, z.samples * 4, (z.cell_count + 1) * 4,
-                             z.context_count * 4, z.cams * kCalib * 4, p->sort_tmp_bytes};
-    size_t offs[7], total = 0;
-    for (int i = 0; i < 7; ++i) {
+    p->tmp_bytes = std::max(sort_bytes, scan_bytes);
+    p->tiles_per_batch = (int)((z.cells + kTileCells - 1) / kTileCells);
+    p->tiles = p->tiles_per_batch * (int)d->batches;
+    p->max_multi = (int)std::max<size_t>(1, (p->list_capacity + kSliceEntries - 1) / kSliceEntries);
+    p->max_work = p->tiles + p->max_multi;
+    p->vw = d->channels % 4 == 0 ? 4 : 1;
+    p->chunk_max = (int)std::min<size_t>(d->channels, p->vw == 4 ? 128 : 64);
+    p->passes = (int)((d->channels + p->chunk_max - 1) / p->chunk_max);
+    // wide rounds need >= 16 lanes per group in every channel pass
+    const int last_chunk = (int)d->channels - (p->passes - 1) * p->chunk_max;
+    p->round = (last_chunk + p->vw - 1) / p->vw >= kRoundWide ? kRoundWide : kQuad;
+    // keys + sorted keys, order [samples]; starts, padded starts [cells + 1];
+    // padded list; softmax stats [pixels]; context rows + one zero row;
+    // calibration; schedule; work list; multi-slice tiles; partial tiles;
+    // rocPRIM scratch.
+    const size_t scratch_floats = (size_t)2 * p->max_multi * p->passes * p->chunk_max * kTileCells;
+    const size_t parts[13] = {z.samples * 8, z.samples * 4, (z.cell_count + 1) * 4,
+                              (z.cell_count + 1) * 4, p->list_capacity * 8, z.pixels * 8,
+                              (z.context_count + d->channels) * 4, z.cams * kCalib * 4,
+                              ((size_t)4 * p->tiles + 2) * 4, (size_t)p->max_work * 8,
+                              (size_t)p->max_multi * 4, scratch_floats * 4, p->tmp_bytes};
+    size_t offs[13], total = 0;
+    for (int i = 0; i < 13; ++i) {
         offs[i] = total;
         total += (parts[i] + 255) & ~size_t(255);
     }
@@ -574,12 +812,26 @@ extern "C" int bf_cuda_lss_plan_create(const bf_lss_desc *d, bf_cuda_lss_plan **
     }
     unsigned char *a = (unsigned char *)p->arena;
     p->keys = (int *)(a + offs[0]);
-    p->sorted_keys = (int *)(a + offs[1]);
-    p->order = (int *)(a + offs[2]);
-    p->starts = (int *)(a + offs[3]);
-    p->rows = (float *)(a + offs[4]);
-    p->calib = (float *)(a + offs[5]);
-    p->sort_tmp = a + offs[6];
+    p->sorted_keys = p->keys + z.samples;
+    p->order = (int *)(a + offs[1]);
+    p->starts = (int *)(a + offs[2]);
+    p->padded_starts = (int *)(a + offs[3]);
+    p->list = (int2 *)(a + offs[4]);
+    p->stats = (float2 *)(a + offs[5]);
+    p->rows = (float *)(a + offs[6]);
+    p->calib = (float *)(a + offs[7]);
+    p->sched = (int *)(a + offs[8]);
+    p->work = (int2 *)(a + offs[9]);
+    p->multi = (int *)(a + offs[10]);
+    p->scratch = (float *)(a + offs[11]);
+    p->tmp = a + offs[12];
+    // the zero context row that padding entries read
+    hipLaunchKernelGGL(fill_float_kernel, dim3(blocks_for(d->channels)), dim3(256), 0, nullptr,
+                       p->rows + z.context_count, (int)d->channels);
+    if (!hip_ok(hipDeviceSynchronize(), error, cap, "initialise HIP LSS plan")) {
+        bf_cuda_lss_plan_destroy(p);
+        return 0;
+    }
     p->resident_bytes = total;
     *out = p;
     return 1;
@@ -593,13 +845,14 @@ namespace {
 
 // Cell lists from the keys in plan->keys: the stable sort of (key, sample)
 // pairs orders every cell's samples by sample index (out-of-grid samples sort
-// after the last cell); a lower bound per cell locates each cell's run; then
-// the sorted order becomes the position / list_pixel maps the forward reads.
+// after the last cell); a lower bound per cell locates each cell's run; runs
+// padded to whole quads give the padded list of {pixel, sample}; then the
+// pool schedule.
 int build_lists(bf_cuda_lss_plan *p, hipStream_t s, char *error, size_t cap) {
     const bf_lss_desc *d = &p->desc;
     const int n = (int)p->z.samples, cell_count = (int)p->z.cell_count;
     const int hw = (int)(d->feature_height * d->feature_width);
-    if (!hip_ok(rocprim::radix_sort_pairs(p->sort_tmp, p->sort_tmp_bytes,
+    if (!hip_ok(rocprim::radix_sort_pairs(p->tmp, p->tmp_bytes,
                                           reinterpret_cast<const unsigned *>(p->keys),
                                           reinterpret_cast<unsigned *>(p->sorted_keys),
                                           rocprim::counting_iterator<int>(0), p->order,
@@ -608,8 +861,23 @@ int build_lists(bf_cuda_lss_plan *p, hipStream_t s, char *error, size_t cap) {
         return 0;
     hipLaunchKernelGGL(cell_starts_kernel, dim3(blocks_for((size_t)cell_count + 1)), dim3(256), 0, s,
                        p->sorted_keys, n, p->starts, cell_count);
-    hipLaunchKernelGGL(list_maps_kernel, dim3(blocks_for(n)), dim3(256), 0, s, p->order,
-                       p->position(), p->list_pixel(), n, (int)d->depth_bins * hw, hw);
+    // padded counts of cells [0, cell_count) and 0 for the end marker
+    const auto padded = rocprim::make_transform_iterator(rocprim::counting_iterator<int>(0),
+                                                         PaddedCount{p->starts});
+    if (!launch_ok(error, cap, "HIP LSS plan starts") ||
+        !hip_ok(rocprim::exclusive_scan(p->tmp, p->tmp_bytes, padded, p->padded_starts, 0,
+                                        (size_t)cell_count + 1, rocprim::plus<int>(), s),
+                error, cap, "HIP LSS plan scan"))
+        return 0;
+    hipLaunchKernelGGL(list_entries_kernel, dim3(blocks_for(n)), dim3(256), 0, s, p->order,
+                       p->sorted_keys, p->starts, p->padded_starts, p->list, n, cell_count,
+                       (int)d->depth_bins * hw, hw);
+    hipLaunchKernelGGL(list_padding_kernel, dim3(blocks_for(cell_count)), dim3(256), 0, s,
+                       p->starts, p->padded_starts, p->list, cell_count);
+    hipLaunchKernelGGL(schedule_kernel, dim3(1), dim3(kScheduleThreads), 0, s, p->padded_starts,
+                       p->sched, p->tiles, p->tiles_per_batch, (int)p->z.cells);
+    hipLaunchKernelGGL(work_list_kernel, dim3(blocks_for(p->tiles)), dim3(256), 0, s, p->sched,
+                       p->work, p->multi, p->tiles);
     if (!launch_ok(error, cap, "HIP LSS plan list build")) return 0;
     p->prepared = 1;
     return 1;
@@ -665,19 +933,40 @@ extern "C" int bf_cuda_lss_plan_forward_f32(bf_cuda_lss_plan *plan, const float 
     const Sizes &z = plan->z;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int hw = (int)(d->feature_height * d->feature_width), C = (int)d->channels;
-    hipLaunchKernelGGL(softmax_list_kernel, dim3(blocks_for(z.pixels, kSoftmaxPixels)), dim3(256),
-                       0, s, logits, plan->position(), plan->list_prob(), (int)z.pixels,
-                       (int)d->depth_bins, hw);
+    hipLaunchKernelGGL(softmax_stats_kernel, dim3(blocks_for(z.pixels, kSoftmaxPixels)), dim3(256),
+                       0, s, logits, plan->stats, (int)z.pixels, (int)d->depth_bins, hw);
     hipLaunchKernelGGL(context_rows_kernel, dim3((hw + 63) / 64, (C + 63) / 64, (unsigned)z.cams),
                        dim3(256), 0, s, context, plan->rows, C, hw);
-    const dim3 grid((unsigned)((z.cells + kTileCells - 1) / kTileCells), (unsigned)d->batches);
-    if (C % 4 == 0)
-        hipLaunchKernelGGL(pool_tile_kernel<4>, grid, dim3(256),
-                           min(C, 256) * kTileCells * sizeof(float), s, plan->list_prob(),
-                           plan->list_pixel(), plan->rows, plan->starts, bev, (int)z.cells, C);
+    PoolArgs args;
+    args.list = plan->list;
+    args.logits = logits;
+    args.stats = plan->stats;
+    args.rows = plan->rows;
+    args.starts = plan->padded_starts;
+    args.sched = plan->sched;
+    args.work = plan->work;
+    args.scratch = plan->scratch;
+    args.bev = bev;
+    args.cells = (int)z.cells;
+    args.tiles = plan->tiles;
+    args.tiles_per_batch = plan->tiles_per_batch;
+    args.C = C;
+    args.passes = plan->passes;
+    args.chunk_max = plan->chunk_max;
+    args.zero_row = (int)z.pixels;
+    args.row_bytes = (unsigned)C * 4u;
+    args.rows_bytes = (unsigned)((z.context_count + C) * 4);
+    const size_t lds = (size_t)plan->chunk_max * kTileCells * sizeof(float);
+    const dim3 grid(plan->max_work);
+    if (plan->vw == 4 && plan->round == kRoundWide)
+        hipLaunchKernelGGL((pool_kernel<4, kRoundWide>), grid, dim3(256), lds, s, args);
+    else if (plan->vw == 4)
+        hipLaunchKernelGGL((pool_kernel<4, kQuad>), grid, dim3(256), lds, s, args);
+    else if (plan->round == kRoundWide)
+        hipLaunchKernelGGL((pool_kernel<1, kRoundWide>), grid, dim3(256), lds, s, args);
     else
-        hipLaunchKernelGGL(pool_tile_kernel<1>, grid, dim3(256),
-                           min(C, 64) * kTileCells * sizeof(float), s, plan->list_prob(),
-                           plan->list_pixel(), plan->rows, plan->starts, bev, (int)z.cells, C);
+        hipLaunchKernelGGL((pool_kernel<1, kQuad>), grid, dim3(256), lds, s, args);
+    hipLaunchKernelGGL(combine_kernel, dim3(plan->max_multi), dim3(256), 0, s, args,
+                       (const int *)plan->multi);
     return launch_ok(error, cap, "HIP LSS plan forward");
 }

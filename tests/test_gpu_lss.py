@@ -190,6 +190,42 @@ def test_plan_channel_widths_and_ragged_grid(channels, device):
     _check(got, sc["depth_logits"], sc["context"], g, od, f"lss plan C={channels}")
 
 
+def _exact_inputs(sc, seed):
+    """Logits with 32 equal maxima per pixel (probabilities exactly 1/32, the
+    rest exactly 0) and small-integer context: every partial sum is exact in
+    float32, so any summation order must reproduce the oracle bit for bit."""
+    rng = np.random.default_rng(seed)
+    b, n, d, h, w = sc["depth_logits"].shape
+    keys = rng.random((b, n, d, h, w))
+    on = np.argsort(keys, axis=2) < 32
+    logits = np.where(on, 0.0, -200.0).astype(np.float32)
+    ctx = rng.integers(-8, 9, size=sc["context"].shape).astype(np.float32)
+    return logits, ctx
+
+
+@pytest.mark.parametrize("channels,cells", [(260, (8, 8, 1)), (6, (1, 1, 1)), (80, (1, 1, 1)),
+                                            (80, (3, 5, 2)), (128, (40, 40, 1))])
+def test_plan_dense_cells_bit_exact(channels, cells, device):
+    """Tiles with tens of thousands of list entries: the work is cut into
+    slices, groups and carries; with exactly representable sums the result
+    must equal the oracle bit for bit, whatever the cut."""
+    sc = lss_scene.rig(seed=7, height=8, width=22, depth_bins=60, channels=channels)
+    sc["desc"] = dict(sc["desc"], minimum=(-60.0, -60.0, -20.0),
+                      step=(120.0 / cells[0], 120.0 / cells[1], 40.0 / cells[2]), cells=cells)
+    bd, od = _descs(sc["desc"])
+    g = _frustum_geometry(sc)
+    logits_h, ctx_h = _exact_inputs(sc, channels)
+    logits, ctx = _dev(logits_h, device), _dev(ctx_h, device)
+    want = ORACLE.lss_lift_pool(logits_h, ctx_h, g, od)
+    assert np.count_nonzero(ORACLE.lss_ranks(g, od) >= 0) > 30000
+    with bfhip.LssPlan(bd) as plan:
+        plan.prepare_geometry(_dev(g, device))
+        got = plan.forward(logits, ctx).cpu().numpy()
+    assert np.array_equal(got, want)
+    geo = _dev(g, device)
+    assert np.array_equal(bfhip.lss_lift_pool(logits, ctx, geo, bd).cpu().numpy(), want)
+
+
 def test_all_samples_outside_or_non_finite(device):
     sc = SCENES["compact"]
     bd, od = _descs(sc["desc"])
