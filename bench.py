@@ -12,6 +12,14 @@ a HIP graph.  The timed region is bracketed by torch.cuda.synchronize().
 Prints one JSON line with ms/frame, achieved TFLOP/s (304.4 GFLOP/frame), the
 dominant kernel's roofline (timed live with HIP events) and the CPU baseline
 (the reference's own CPU path, OpenMP, on this host's cores).
+
+The same line carries an "lss" object: the lift-splat pooling that consumes
+the depth head (include/bf_cuda.h), on the reference's production benchmark
+inputs (tests/test_cuda_lss.cu:26-104: 6 cameras x 118 bins x 32x88, 80
+channels, a 360x360 grid), timed as the reference reports it
+(runs/rtx4060ti-2026-07-18/cuda_lss_intervals.txt): plan preparation from the
+calibration plus one forward per frame, with the forward's roofline, its
+measured HBM traffic and the reference's CPU pooling beside it.
 """
 
 from __future__ import annotations
@@ -52,6 +60,7 @@ def parse():
                    help="skip the rocprofv3 FETCH_SIZE / WRITE_SIZE passes on the dominant kernel")
     p.add_argument("--pmc-child", default="",
                    help=argparse.SUPPRESS)  # internal: the program rocprofv3 profiles
+    p.add_argument("--no-lss", action="store_true", help="skip the LSS pooling leg")
     return p.parse_args()
 
 
@@ -222,6 +231,19 @@ def pmc_child(op):
     import bfhip
     from bfhip import bfw
     dev = torch.device("cuda:0")
+    if op == LSS_OP:
+        plan, fwd = lss_setup(dev)
+        src = torch.zeros(PMC_COPY_BYTES // 4, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(PMC_COPY_REPS):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        for _ in range(PMC_OP_REPS):
+            fwd()
+        torch.cuda.synchronize()
+        plan.close()
+        return
     tmp = pathlib.Path(tempfile.mkdtemp(prefix="pmc_"))
     model_path = bfw.write_camera_branch(tmp / "camera_branch.bfw", seed=0, mode="baseline")
     with bfhip.Model(model_path) as m:
@@ -286,6 +308,114 @@ def measure_traffic(op, timeout_s=120):
             "fetch_kib_raw": round(per["FETCH_SIZE"][0], 1), "write_kib_raw": round(per["WRITE_SIZE"][0], 1),
             "fetch_scale": round(per["FETCH_SIZE"][1], 4), "write_scale": round(per["WRITE_SIZE"][1], 4),
             "calibration": f"{PMC_COPY_BYTES >> 20} MiB device copy"}, None
+
+
+LSS_OP = "lss_forward"
+# Reference timings of the same benchmark on an RTX 4060 Ti
+# (runs/rtx4060ti-2026-07-18/cuda_lss_intervals.txt:14-16).
+LSS_REFERENCE_MS = {"forward": 1.389, "prepare_calibration": 0.363, "total": 1.752}
+
+
+def lss_setup(dev, stream=None):
+    """Production LSS inputs resident on the GPU and a prepared plan; returns
+    (plan, forward callable)."""
+    import torch
+    import bfhip
+    from bfhip import lss_scene
+    sc = lss_scene.production()
+    d = sc["desc"]
+    desc = bfhip.lss_desc(d["batches"], d["cameras"], d["depth_bins"], d["height"], d["width"],
+                          d["channels"], d["minimum"], d["step"], d["cells"])
+    put = lambda a: torch.from_numpy(a).to(dev)  # noqa: E731
+    logits, ctx, frustum = put(sc["depth_logits"]), put(sc["context"]), put(sc["frustum"])
+    cal = [put(sc[k]) for k in lss_scene.CALIBRATION_KEYS]
+    bev = torch.empty((1, d["channels"] * d["cells"][2], d["cells"][0], d["cells"][1]),
+                      device=dev)
+    plan = bfhip.LssPlan(desc)
+    plan.prepare_calibration(frustum, *cal, stream=stream)
+    plan.inputs = (logits, ctx, frustum, cal, bev, sc)
+    return plan, lambda: plan.forward(logits, ctx, out=bev, stream=stream)
+
+
+def lss_leg(dev, reps, traffic):
+    """LSS pooling on the reference's production inputs (see the module
+    docstring): ms for prepare + forward, forward, prepare; the forward's
+    roofline against HBM; the reference CPU pooling on the host."""
+    import torch
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        plan, fwd = lss_setup(dev, stream)
+        logits, ctx, frustum, cal, bev, sc = plan.inputs
+
+        def prep():
+            plan.prepare_calibration(frustum, *cal, stream=stream)
+
+        def timed(fn):
+            for _ in range(3):
+                fn()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            for _ in range(reps):
+                fn()
+            b.record(stream)
+            b.synchronize()
+            return a.elapsed_time(b) / reps
+
+        ms_fwd = timed(fwd)
+        ms_prep = timed(prep)
+        ms_total = timed(lambda: (prep(), fwd()))
+        stream.synchronize()
+    d = sc["desc"]
+    samples = d["cameras"] * d["depth_bins"] * d["height"] * d["width"]
+    # compulsory HBM bytes of one forward: logits + context in, BEV out (fp32)
+    nbytes = 4 * (samples + d["cameras"] * d["channels"] * d["height"] * d["width"]
+                  + d["channels"] * d["cells"][0] * d["cells"][1] * d["cells"][2])
+    gbs = nbytes / (ms_fwd * 1e-3) / 1e9
+    roof = {"kernel": "lss plan forward (softmax stats + context rows + pool + combine)",
+            "bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+            "algorithmic_bytes": nbytes, "avg_us": round(ms_fwd * 1e3, 2),
+            "note": "the pool gathers one 320 B context row per sample (2.0 M samples) "
+                    "through L2; compulsory HBM bytes understate its memory work"}
+    if traffic:
+        t, why = measure_traffic(LSS_OP)
+        if t:
+            roof["traffic"] = t["bytes"]
+            roof["traffic_detail"] = t
+        else:
+            roof["traffic_error"] = why
+    out = {"workload": "reference production LSS benchmark (tests/test_cuda_lss.cu:26-104): "
+                       "1 batch x 6 cameras x 118 depth bins x 32x88, 80 channels, "
+                       "360x360x1 grid of 0.3 m; plan prepared from calibration each frame",
+           "ms_per_frame": round(ms_total, 4), "ms_forward": round(ms_fwd, 4),
+           "ms_prepare_calibration": round(ms_prep, 4),
+           "reference_rtx4060ti_ms": LSS_REFERENCE_MS,
+           "plan_resident_mib": round(plan.resident_bytes() / 2**20, 2),
+           "roofline": roof}
+    plan.close()
+    return out, sc
+
+
+def lss_cpu_baseline(sc):
+    """The reference's CPU geometry + fused lift-pool (oracle/_ref, src/lss.c)
+    on the full production frame, single-threaded (lss.c has no OpenMP)."""
+    import oracle
+    kind = "reference" if oracle.available("ref") else "port"
+    o = oracle.Oracle("ref" if kind == "reference" else "port")
+    d = sc["desc"]
+    desc = oracle.lss_desc(d["batches"], d["cameras"], d["depth_bins"], d["height"],
+                           d["width"], d["channels"], d["minimum"], d["step"], d["cells"])
+    t0 = time.perf_counter()
+    g = o.lss_geometry(sc["frustum"], sc["camera_rotation"], sc["camera_translation"],
+                       sc["intrinsics"], sc["post_rotation"], sc["post_translation"],
+                       sc["extra_rotation"], sc["extra_translation"])
+    t1 = time.perf_counter()
+    o.lss_lift_pool(sc["depth_logits"], sc["context"], g, desc)
+    t2 = time.perf_counter()
+    return {"value": round((t2 - t0) * 1e3, 1), "unit": "ms/frame", "cores": 1, "kind": kind,
+            "sample": f"one full production frame: geometry {1e3 * (t1 - t0):.0f} ms + "
+                      f"lift-pool {1e3 * (t2 - t1):.0f} ms",
+            "cpu_model": _cpu_model()}
 
 
 def cpu_baseline(model_path, cameras):
@@ -432,6 +562,11 @@ def main():
                 result["roofline"]["traffic_error"] = why
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(model_path, args.cpu_cameras)
+    if not args.no_lss:
+        lss, sc = lss_leg(dev, max(args.steps, 20), not (args.no_roofline or args.no_traffic))
+        if not args.no_cpu:
+            lss["cpu_baseline"] = lss_cpu_baseline(sc)
+        result["lss"] = lss
     print(json.dumps(result))
 
 
