@@ -1,9 +1,10 @@
 """Python host side of the gfx950 camera-path library.
 
 Thin ctypes mirror of the C ABI in ``include/bf_cuda_ops.h``,
-``include/bf_cuda_swin.h``, ``include/bf_cuda_camera.h`` and
-``include/bf_cuda.h`` (the reference's operator/plugin interface for this
-path and for the lift-splat pooling that consumes it).  PyTorch supplies device memory and
+``include/bf_cuda_swin.h``, ``include/bf_cuda_camera.h``, ``include/bf_cuda.h``
+and ``include/bf_cuda_bev.h`` (the reference's operator/plugin interface for
+this path, the lift-splat pooling that consumes it and the BEV stage after
+it).  PyTorch supplies device memory and
 the current HIP stream; every computation runs in ``lib/libbfhip.so``.  There
 is no fallback: if the library is missing, importing an entry point raises.
 """
@@ -81,6 +82,10 @@ SIGNATURES = {
     "bf_cuda_lss_plan_prepare_calibration_f32": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                                       _vp, _vp, C.c_char_p, _sz]),
     "bf_cuda_lss_plan_forward_f32": (_i, [_vp, _vp, _vp, _vp, _vp, C.c_char_p, _sz]),
+    "bf_cuda_bev_stage_create": (_i, [_vp, _sz, _sz, C.POINTER(_vp), C.c_char_p, _sz]),
+    "bf_cuda_bev_stage_destroy": (None, [_vp]),
+    "bf_cuda_bev_stage_forward": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, C.c_char_p, _sz]),
+    "bf_cuda_bev_stage_resident_bytes": (_sz, [_vp]),
 }
 
 SWIN_OPS = ("ln1", "qkv", "attention", "proj", "ln2", "fc1", "fc2", "merge", "mlp")
@@ -493,6 +498,49 @@ class LssPlan:
     def close(self):
         if self.handle:
             self.lib.bf_cuda_lss_plan_destroy(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# --------------------------------------------------------------- BEV stage
+class BevStage:
+    """bf_cuda_bev_stage context (include/bf_cuda_bev.h): batch one, H x W BEV."""
+
+    def __init__(self, model: Model, height: int, width: int):
+        self.lib, self.h, self.w = hip_lib(), height, width
+        self.handle, err = _vp(), _err()
+        _check(self.lib.bf_cuda_bev_stage_create(model.handle, height, width, C.byref(self.handle),
+                                                 err, 512), err, "bf_cuda_bev_stage_create")
+
+    def resident_bytes(self) -> int:
+        return self.lib.bf_cuda_bev_stage_resident_bytes(self.handle)
+
+    def forward(self, x, outs=None, stream=None):
+        """x [1,336,H,W] -> (spatial [1,512,H,W], shared [1,128,H,W], heatmap [1,10,H,W])."""
+        torch = _torch()
+        if outs is None:
+            outs = tuple(torch.empty((1, c, self.h, self.w), device=x.device)
+                         for c in (512, 128, 10))
+        err = _err()
+        _check(self.lib.bf_cuda_bev_stage_forward(self.handle, _ptr(x), *map(_ptr, outs),
+                                                  _stream(stream), err, 512),
+               err, "bf_cuda_bev_stage_forward")
+        return outs
+
+    def close(self):
+        if self.handle:
+            self.lib.bf_cuda_bev_stage_destroy(self.handle)
             self.handle = None
 
     def __enter__(self):

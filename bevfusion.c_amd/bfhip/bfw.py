@@ -247,6 +247,46 @@ def write_camera_branch(path, seed: int = 0, mode: str = "baseline", gain: float
     return path
 
 
+def bev_stage_tensors(init: _Init):
+    """Fuser, SECOND backbone + deblocks, TransFusion shared conv and heatmap
+    head under the checkpoint's names and shapes (reference
+    src/cuda_bev_stage.cu:239-255; ConvTranspose2d weights are [in, out, kH, kW])."""
+    out = []
+
+    def conv(name, shape, fan_in, bias=False):
+        out.append((name + ".weight", init.weight(name + ".weight", shape, fan_in)))
+        if bias:
+            out.append((name + ".bias", init.bias(name + ".bias", shape[:1])))
+
+    conv("fuser.conv.0", (256, 336, 3, 3), 336 * 9)
+    out += init.bn("fuser.conv.1", 256)
+    for b, (ch, first) in enumerate(((128, 256), (256, 128))):
+        for l in range(6):
+            ci = ch if l else first
+            conv(f"backbone_2d.blocks.{b}.{3 * l + 1}", (ch, ci, 3, 3), ci * 9)
+            out += init.bn(f"backbone_2d.blocks.{b}.{3 * l + 2}", ch)
+    conv("backbone_2d.deblocks.0.0", (256, 128, 1, 1), 128)
+    out += init.bn("backbone_2d.deblocks.0.1", 256)
+    conv("backbone_2d.deblocks.1.0", (256, 256, 2, 2), 256)
+    out += init.bn("backbone_2d.deblocks.1.1", 256)
+    conv("dense_head.shared_conv", (128, 512, 3, 3), 512 * 9, bias=True)
+    conv("dense_head.heatmap_head.0.conv", (128, 128, 3, 3), 128 * 9)
+    out += init.bn("dense_head.heatmap_head.0.bn", 128)
+    conv("dense_head.heatmap_head.1", (10, 128, 3, 3), 128 * 9, bias=True)
+    return out
+
+
+def write_bev_stage(path, seed: int = 0, mode: str = "baseline", gain: float = 1.0) -> pathlib.Path:
+    path = pathlib.Path(path)
+    write_bfw(bev_stage_tensors(_Init(seed, mode, gain)), path)
+    return path
+
+
+def synthetic_bev(seed: int, height=180, width=180, batches=1) -> np.ndarray:
+    """Fused BEV input [B, 336, H, W] ~N(0,1): 80 image channels, then 256 lidar."""
+    return randn(seed, "bev_input", (batches, 336, height, width))
+
+
 # --------------------------------------------------------------------------
 # Synthetic frame inputs (BASELINE.json config 5)
 # --------------------------------------------------------------------------

@@ -14,8 +14,7 @@
 //   the last downsample conv stores the x/y-transposed map.
 #include "bf_cuda_camera.h"
 #include "bfhip_profile.h"
-#include "conv_core.h"
-#include "host_util.h"
+#include "conv_layers.h"
 
 #include <algorithm>
 #include <climits>
@@ -26,11 +25,8 @@ using namespace bfhip;
 
 namespace {
 
-struct ConvLayer {
-    const bf16 *w;
-    const float *b;
-    int ci, co, k, stride, pad, n, ih, iw, oh, ow;
-};
+// BatchNorm epsilon of the camera modules (cuda_camera.cu:116-122).
+constexpr float kCameraBnEps = 1e-5f;
 
 enum {
     kLat1, kFpn1, kLat0, kFpn0, kDt1, kDt2, kDn0, kDn3, kDn6, kDs0, kDs1, kDs2, kLayers
@@ -50,77 +46,6 @@ struct bf_cuda_camera_neck {
 
 namespace {
 
-// Binds conv (+ optional bias, + optional BN), folds BN in fp32 exactly as the
-// reference (cuda_camera.cu:116-122) and returns the folded weights permuted
-// to [Co][KH][KW][Ci] (channels-last reduction order) plus the fp32 bias.
-int fold_conv(const bf_model *m, const char *wname, const char *bname, const char *bn,
-              int ci, int co, int k, std::vector<float> &w, std::vector<float> &b,
-              char *error, size_t cap) {
-    const uint32_t uco = (uint32_t)co, uci = (uint32_t)ci, uk = (uint32_t)k;
-    const float *src = bind_f32(m, wname, {uco, uci, uk, uk}, error, cap);
-    if (!src) return 0;
-    const size_t span = (size_t)ci * k * k;
-    std::vector<float> folded(src, src + span * co);
-    b.assign(co, 0.0f);
-    if (bname) {
-        const float *sb = bind_f32(m, bname, {uco}, error, cap);
-        if (!sb) return 0;
-        b.assign(sb, sb + co);
-    }
-    if (bn) {
-        static const char *suffix[4] = {"weight", "bias", "running_mean", "running_var"};
-        const float *p[4];
-        char name[192];
-        for (int i = 0; i < 4; ++i) {
-            std::snprintf(name, sizeof(name), "%s.%s", bn, suffix[i]);
-            if (!(p[i] = bind_f32(m, name, {uco}, error, cap))) return 0;
-        }
-        for (int o = 0; o < co; ++o) {
-            const float f = p[0][o] / std::sqrt(p[3][o] + 1e-5f);
-            b[o] = (b[o] - p[2][o]) * f + p[1][o];
-            for (size_t i = 0; i < span; ++i) folded[(size_t)o * span + i] *= f;
-        }
-    }
-    w.resize(span * co);
-    for (int o = 0; o < co; ++o)
-        for (int c = 0; c < ci; ++c)
-            for (int t = 0; t < k * k; ++t)
-                w[((size_t)o * k * k + t) * ci + c] = folded[((size_t)o * ci + c) * k * k + t];
-    return 1;
-}
-
-ConvGeom geom_of(const ConvLayer &l) {
-    ConvGeom g{};
-    g.N = l.n; g.Ci = l.ci; g.IH = l.ih; g.IW = l.iw; g.OH = l.oh; g.OW = l.ow;
-    g.KH = l.k; g.KW = l.k; g.SH = l.stride; g.SW = l.stride; g.PH = l.pad; g.PW = l.pad;
-    g.transpose = 0;
-    g.M = l.n * l.oh * l.ow;
-    g.K = l.ci * l.k * l.k;
-    return g;
-}
-
-template <class T, int KH, int KW, class Src, class Epi>
-void run_conv(const ConvLayer &l, const Src &src, const Epi &epi, hipStream_t s) {
-    const ConvGeom g = geom_of(l);
-    LoadConvNHWC<T::BM, T::BK, T::kThreads, KH, KW, Src> al{};
-    al.src = src;
-    al.g = g;
-    LoadRowsBf16<T::BN, T::BK, T::kThreads> bl{l.w, g.K, l.co, g.K};
-    launch_gemm<T>(al, bl, epi, g.M, l.co, g.K, s);
-}
-
-// LDS-DMA pipeline for convs over plain or concatenated channels-last maps
-// whose channel counts are multiples of the k-tile (every 3x3 / 1x1 conv of
-// the FPN outputs and the depth trunk, and dtransform.6).
-template <class T, int K, class Epi>
-void run_conv_dma(const ConvLayer &l, const bf16 *a, int c0, const bf16 *b, int c1, const Epi &epi,
-                  hipStream_t s) {
-    const ConvGeom g = geom_of(l);
-    DmaConvNHWC<T::BM, T::BK, T::kThreads, K, K> al{a, b, c0, c1, g};
-    DmaRowsBf16<T::BN, T::BK, T::kThreads> bl{l.w, g.K, l.co, g.K};
-    launch_gemm_dma<T>(al, bl, epi, g.M, l.co, g.K, s);
-}
-
 // Tiles from sweeps of both cores on these shapes (MI355X).  DMA-fed: 64 x 128
 // for the 256-channel 3x3 convs at 32x88 and the depthnet.6 1x1, 64 x 64 at
 // level 1 (16x44), a two-wave 32 x 64 tile over 32-deep k-steps for
@@ -134,14 +59,6 @@ using T256 = Tile<128, 128, 64, 2, 2>;       // lateral_convs.0
 using T64 = Tile<64, 64, 64, 2, 2>;          // lateral_convs.1
 using T32 = Tile<128, 32, 32, 4, 1>;         // dtransform.3: 32 output channels
 using T80 = Tile<64, 80, 64, 2, 1>;          // downsample: 80 channels
-
-EpiConvOut out_to(const ConvLayer &l, bf16 *nhwc, float *nchw = nullptr) {
-    return EpiConvOut{nhwc, nchw, l.b, l.n * l.oh * l.ow, l.co, l.oh * l.ow, 1};
-}
-
-EpiConvNHWC nhwc_to(const ConvLayer &l, bf16 *nhwc) {
-    return EpiConvNHWC{nhwc, l.b, l.n * l.oh * l.ow, l.co};
-}
 
 // FPN output conv: channels-last only, or also NCHW fp32 for the boundary.
 template <class T>
@@ -212,7 +129,9 @@ int build(bf_cuda_camera_neck *n, const bf_model *model, char *error, size_t cap
     std::vector<float> fw, fb;
     for (int i = 0; i < kLayers; ++i) {
         const Spec &sp = spec[i];
-        if (!fold_conv(model, sp.w, sp.b, sp.bn, sp.ci, sp.co, sp.k, fw, fb, error, cap)) return 0;
+        if (!fold_conv(model, sp.w, sp.b, sp.bn, sp.ci, sp.co, sp.k, kCameraBnEps, fw, fb, error,
+                       cap))
+            return 0;
         wo[i] = arena.add_bf16(fw);
         bo[i] = arena.add_f32(fb);
         ConvLayer &l = n->L[i];
@@ -222,7 +141,7 @@ int build(bf_cuda_camera_neck *n, const bf_model *model, char *error, size_t cap
         l.ow = (sp.iw + 2 * sp.pad - sp.k) / sp.stride + 1;
     }
     if (!fold_conv(model, "vtransform.dtransform.0.weight", "vtransform.dtransform.0.bias",
-                   "vtransform.dtransform.1", 1, 8, 1, fw, fb, error, cap))
+                   "vtransform.dtransform.1", 1, 8, 1, kCameraBnEps, fw, fb, error, cap))
         return 0;
     const size_t dt0w = arena.add_f32(fw), dt0b = arena.add_f32(fb);
     if (!hip_ok(hipMalloc(&n->params, arena.host.size()), error, cap, "allocate camera parameters") ||

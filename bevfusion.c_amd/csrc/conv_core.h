@@ -400,13 +400,14 @@ struct DmaConvNHWC {
     }
 };
 
-// Row-vector conv epilogue for channels-last bf16 maps: out[row][col] =
-// bf16(relu(v + bias)), Co % 4 == 0.
+// Row-vector conv epilogue for channels-last 16-bit maps: out[row][col] =
+// word(relu(v + bias)), Co % 4 == 0; words are bf16, or fp16 when f16 is set.
 struct EpiConvNHWC {
     static constexpr bool kRowVector = true;
     bf16 *out;
     const float *bias;
     int M, Co;
+    int f16;
     __device__ ColQuad column(int col) const { return ColQuad{col, load_quad(bias, col, Co)}; }
     template <int R>
     __device__ void rows(int row0, int step, const ColQuad &c, const float4 (&v)[R]) const {
@@ -417,23 +418,25 @@ struct EpiConvNHWC {
             if (row >= M) break;
             const float4 y = add4(v[i], c.b);
             bf16x4 o;
-            o[0] = to_bf16(y.x < 0.f ? 0.f : y.x);
-            o[1] = to_bf16(y.y < 0.f ? 0.f : y.y);
-            o[2] = to_bf16(y.z < 0.f ? 0.f : y.z);
-            o[3] = to_bf16(y.w < 0.f ? 0.f : y.w);
+            o[0] = to_word(y.x < 0.f ? 0.f : y.x, f16);
+            o[1] = to_word(y.y < 0.f ? 0.f : y.y, f16);
+            o[2] = to_word(y.z < 0.f ? 0.f : y.z, f16);
+            o[3] = to_word(y.w < 0.f ? 0.f : y.w, f16);
             *reinterpret_cast<bf16x4 *>(out + (size_t)row * Co + c.col) = o;
         }
     }
 };
 
-// Conv epilogue writing bias+ReLU results as NHWC bf16 (internal maps) and/or
-// NCHW fp32 (boundary outputs); either pointer may be null.
+// Conv epilogue writing bias+ReLU results as NHWC 16-bit words (internal
+// maps; bf16, or fp16 when f16 is set) and/or NCHW fp32 (boundary outputs);
+// either pointer may be null.
 struct EpiConvOut {
     static constexpr bool kRowVector = false;
     bf16 *nhwc;
     float *nchw;
     const float *bias;
     int M, Co, ohw, relu;
+    int f16;
     __device__ void operator()(int row, int col, f32x4 v) const {
         if (col >= Co) return;
         const float b = bias[col];
@@ -446,7 +449,7 @@ struct EpiConvOut {
         if (nhwc)
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-                if (row + r < M) nhwc[(size_t)(row + r) * Co + col] = to_bf16(y[r]);
+                if (row + r < M) nhwc[(size_t)(row + r) * Co + col] = to_word(y[r], f16);
         if (nchw) {
             const int n = row / ohw, p = row - n * ohw;
             if ((ohw & 3) == 0 && row + 3 < M) {
@@ -464,10 +467,11 @@ struct EpiConvOut {
     }
 };
 
-// NCHW fp32 [N][C][HW] -> NHWC bf16 [N][HW][C] through a 64-pixel x 64-channel
-// LDS tile (coalesced reads along pixels, 16-byte writes along channels).
-// C must be a multiple of 8.
-static __global__ __launch_bounds__(256) void pack_nhwc_kernel(const float *x, bf16 *y, int C, int HW) {
+// NCHW fp32 [N][C][HW] -> NHWC 16-bit words [N][HW][C] (bf16, or fp16 when
+// f16 is set) through a 64-pixel x 64-channel LDS tile (coalesced reads along
+// pixels, 16-byte writes along channels).  C must be a multiple of 8.
+static __global__ __launch_bounds__(256) void pack_nhwc_kernel(const float *x, bf16 *y, int C, int HW,
+                                                               int f16) {
     __shared__ float tile[64][65];
     const int n = blockIdx.z, c0 = blockIdx.y * 64, p0 = blockIdx.x * 64;
     const int t = threadIdx.x;
@@ -487,14 +491,15 @@ static __global__ __launch_bounds__(256) void pack_nhwc_kernel(const float *x, b
         if (p >= HW || c >= C) continue;
         bf16x8 v;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = to_bf16(tile[ch + e][pl]);
+        for (int e = 0; e < 8; ++e) v[e] = to_word(tile[ch + e][pl], f16);
         *reinterpret_cast<bf16x8 *>(dst + (size_t)p * C + c) = v;
     }
 }
 
-inline void pack_nhwc(const float *x, bf16 *y, int N, int C, int HW, hipStream_t s) {
+inline void pack_nhwc(const float *x, bf16 *y, int N, int C, int HW, hipStream_t s,
+                      bool f16 = false) {
     hipLaunchKernelGGL(pack_nhwc_kernel, dim3((HW + 63) / 64, (C + 63) / 64, N), dim3(256), 0, s,
-                       x, y, C, HW);
+                       x, y, C, HW, (int)f16);
 }
 
 }  // namespace bfhip

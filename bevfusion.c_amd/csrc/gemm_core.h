@@ -18,9 +18,11 @@
 
 namespace bfhip {
 
-template <int BM_, int BN_, int BK_, int WM_, int WN_>
+// F16_: operands are fp16 words (fp16 MFMA) instead of bf16.
+template <int BM_, int BN_, int BK_, int WM_, int WN_, bool F16_ = false>
 struct Tile {
     static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
+    static constexpr bool kF16 = F16_;
     static constexpr int kThreads = WM * WN * kWave;
     static constexpr int kWaveRows = BM / WM, kWaveCols = BN / WN;
     static constexpr int kFragM = kWaveRows / 16, kFragN = kWaveCols / 16;
@@ -230,7 +232,7 @@ __global__ __launch_bounds__(T::kThreads) void gemm_kernel(ALoad al, BLoad bl, E
 #pragma unroll
             for (int i = 0; i < T::kFragM; ++i)
 #pragma unroll
-                for (int j = 0; j < T::kFragN; ++j) acc[i][j] = mfma16(af[i], bfr[j], acc[i][j]);
+                for (int j = 0; j < T::kFragN; ++j) acc[i][j] = mfma16_as<T::kF16>(af[i], bfr[j], acc[i][j]);
         }
         if (more) {
             al.store(sA[cur ^ 1]);
@@ -264,9 +266,10 @@ inline void launch_gemm(const ALoad &al, const BLoad &bl, const Epi &epi, int M,
 // of 8 consecutive rows on distinct banks, chunk c of row r is stored in slot
 // c ^ swz(r); the DMA side applies the same permutation to the global chunk
 // each lane fetches, so the stored image is already swizzled.
-template <int BM_, int BN_, int BK_, int WM_, int WN_, int STAGES_>
+template <int BM_, int BN_, int BK_, int WM_, int WN_, int STAGES_, bool F16_ = false>
 struct DmaTile {
     static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_, kStages = STAGES_;
+    static constexpr bool kF16 = F16_;
     static constexpr int kThreads = WM * WN * kWave;
     static constexpr int kWaveRows = BM / WM, kWaveCols = BN / WN;
     static constexpr int kFragM = kWaveRows / 16, kFragN = kWaveCols / 16;
@@ -427,7 +430,7 @@ __global__ __launch_bounds__(T::kThreads) void gemm_dma_kernel(ALoad al, BLoad b
 #pragma unroll
             for (int i = 0; i < T::kFragM; ++i)
 #pragma unroll
-                for (int j = 0; j < T::kFragN; ++j) acc[i][j] = mfma16(af[i], bfr[j], acc[i][j]);
+                for (int j = 0; j < T::kFragN; ++j) acc[i][j] = mfma16_as<T::kF16>(af[i], bfr[j], acc[i][j]);
         }
     }
     __syncthreads();  // every wave is done with the stage buffers

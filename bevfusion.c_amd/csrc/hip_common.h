@@ -51,6 +51,25 @@ __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 acc) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
 }
 
+// 16-bit operands travel through the loaders, LDS and registers as raw
+// 16-bit words typed bf16; a context that needs more mantissa than bf16's 8
+// bits (a deep conv stack) stores fp16 words instead, and its tiles select
+// the fp16 MFMA (same lane layout, same rate).
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ f32x4 mfma16_f16(bf16x8 a, bf16x8 b, f32x4 acc) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                   __builtin_bit_cast(f16x8, b), acc, 0, 0, 0);
+}
+template <bool F16>
+__device__ __forceinline__ f32x4 mfma16_as(bf16x8 a, bf16x8 b, f32x4 acc) {
+    if constexpr (F16) return mfma16_f16(a, b, acc);
+    else return mfma16(a, b, acc);
+}
+// A float stored as the 16-bit word of the chosen format.
+__device__ __forceinline__ bf16 to_word(float v, bool f16) {
+    return f16 ? __builtin_bit_cast(bf16, static_cast<_Float16>(v)) : static_cast<bf16>(v);
+}
+
 // GELU 0.5*x*(1 + erf(x/sqrt(2))) (the reference's exact-erf form,
 // kernels_ref.c:448-452) evaluated as x * sigmoid(x*(a + b*x^2 + c*x^4)), with
 // (a, b, c) a minimax fit to the exact-erf GELU over [-10, 10] (x clamped

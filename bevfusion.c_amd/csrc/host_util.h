@@ -22,6 +22,27 @@ inline uint16_t bf16_bits(float f) {
     return (uint16_t)(u >> 16);
 }
 
+// Round-to-nearest-even float -> IEEE binary16 bits: overflow to +-Inf,
+// subnormal results rounded at their own precision, NaN kept quiet.
+inline uint16_t f16_bits(float f) {
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    const uint32_t sign = (u >> 16) & 0x8000u, a = u & 0x7fffffffu;
+    if (a > 0x7f800000u) return (uint16_t)(sign | 0x7e00u);
+    if (a >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);  // rounds past 65504
+    if (a >= 0x38800000u) {                                    // normal binary16
+        const uint32_t r = a + 0x0fffu + ((a >> 13) & 1u);
+        return (uint16_t)(sign | ((r - 0x38000000u) >> 13));
+    }
+    if (a < 0x33000000u) return (uint16_t)sign;                // below half the least subnormal
+    const uint32_t e = a >> 23, m = (a & 0x7fffffu) | 0x800000u;
+    const uint32_t shift = 126u - e;                          // 14..24 for this range
+    const uint32_t half = 1u << (shift - 1), rest = m & ((1u << shift) - 1u);
+    uint32_t q = m >> shift;
+    if (rest > half || (rest == half && (q & 1u))) ++q;
+    return (uint16_t)(sign | q);
+}
+
 // Looks a tensor up by name and checks dtype, rank and every dimension
 // (the binding contract of reference cuda_swin.cu:57-63).
 inline const void *bind_tensor(const bf_model *m, const char *name, uint32_t dtype,
@@ -62,8 +83,14 @@ struct ParamArena {
         for (size_t i = 0; i < count; ++i) tmp[i] = bf16_bits(src[i]);
         return add(tmp.data(), count * 2);
     }
+    size_t add_f16(const float *src, size_t count) {
+        std::vector<uint16_t> tmp(count);
+        for (size_t i = 0; i < count; ++i) tmp[i] = f16_bits(src[i]);
+        return add(tmp.data(), count * 2);
+    }
     size_t add_f32(const std::vector<float> &v) { return add_f32(v.data(), v.size()); }
     size_t add_bf16(const std::vector<float> &v) { return add_bf16(v.data(), v.size()); }
+    size_t add_f16(const std::vector<float> &v) { return add_f16(v.data(), v.size()); }
 };
 
 }  // namespace bfhip

@@ -122,7 +122,7 @@ class Oracle:
         L.bf_swin_window_attention_f32_ref.argtypes = [
             _f32p, _f32p, _f32p, _f32p, _i64p, C.c_void_p, _sz, _f32p, _f32p, _f32p,
             _sz, _sz, _sz, _sz, _sz]
-        for mod in ("swin_backbone", "image_fpn", "depth_head", "lss_downsample"):
+        for mod in ("swin_backbone", "image_fpn", "depth_head", "lss_downsample", "bev_stage"):
             getattr(L, f"bf_{mod}_create").argtypes = [C.c_void_p, C.POINTER(C.c_void_p),
                                                        C.c_char_p, _sz]
             getattr(L, f"bf_{mod}_destroy").argtypes = [C.c_void_p]
@@ -143,6 +143,11 @@ class Oracle:
             C.c_char_p, _sz]
         L.bf_lss_downsample_forward_ref.argtypes = [
             C.c_void_p, _f32p, _sz, _sz, _sz, _f32p, C.c_void_p, _sz, C.c_char_p, _sz]
+        L.bf_bev_stage_workspace_bytes.argtypes = [_sz, _sz]
+        L.bf_bev_stage_workspace_bytes.restype = _sz
+        L.bf_bev_stage_forward_ref.argtypes = [
+            C.c_void_p, _f32p, _sz, _sz, _sz, _f32p, _f32p, _f32p, C.c_void_p, _sz,
+            C.c_char_p, _sz]
         L.bf_lss_geometry_f32_ref.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p,
                                               C.c_void_p, C.c_void_p, _f32p, _sz, _sz, _sz,
                                               _sz, _sz]
@@ -327,6 +332,27 @@ class Oracle:
         finally:
             self.lib.bf_lss_downsample_destroy(net)
 
+
+    # ---- BEV stage (bf_bev_stage.h) --------------------------------------
+    def bev_stage(self, model, x):
+        """x [B,336,H,W] -> (spatial [B,512,H,W], shared [B,128,H,W],
+        heatmap [B,10,H,W])."""
+        x = _f32(x)
+        b, c, h, w = x.shape
+        net = model.create("bev_stage")
+        try:
+            nbytes = self.lib.bf_bev_stage_workspace_bytes(h, w)
+            ws = np.empty(max(nbytes, 1), np.uint8)
+            sp = np.empty((b, 512, h, w), np.float32)
+            sh = np.empty((b, 128, h, w), np.float32)
+            hm = np.empty((b, 10, h, w), np.float32)
+            err = C.create_string_buffer(256)
+            if not self.lib.bf_bev_stage_forward_ref(net, x, b, h, w, sp, sh, hm, ws.ctypes.data,
+                                                     nbytes, err, 256):
+                raise OracleError(err.value.decode())
+        finally:
+            self.lib.bf_bev_stage_destroy(net)
+        return sp, sh, hm
 
     # ---- lift-splat pooling (bf_lss.h) ------------------------------------
     def lss_geometry(self, frustum, cam_rot, cam_trans, intrinsics, post_rot, post_trans,

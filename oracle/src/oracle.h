@@ -13,6 +13,7 @@
  *   bf_depth_head.h     -> reference include/bf_depth_head.h,    src/depth_head.c:96-190
  *   bf_lss_downsample.h -> reference include/bf_lss_downsample.h, src/lss_downsample.c:70-148
  *   bf_lss.h            -> reference include/bf_lss.h:18-46,     src/lss.c:8-241
+ *   bf_bev_stage.h      -> reference include/bf_bev_stage.h,     src/bev_stage.c:16-227
  * Floating-point operation order matches the reference per output element, so
  * the scalar build (no OpenMP, BF_CPU_SCALAR=1) is bit-identical to the
  * reference compiled from its own sources (oracle/_ref).
@@ -167,6 +168,20 @@ int bf_oracle_mul(size_t a, size_t b, size_t *out);
 const void *bf_oracle_bind(const bf_model *model, const char *name, uint32_t dtype,
                            uint32_t rank, const uint32_t *dims,
                            char *error, size_t cap);
+
+/* ---- BEV stage (bf_bev_stage.h) --------------------------------------- */
+typedef struct bf_bev_stage bf_bev_stage;
+int bf_bev_stage_create(const bf_model *model, bf_bev_stage **out, char *error,
+                        size_t error_cap);
+void bf_bev_stage_destroy(bf_bev_stage *stage);
+size_t bf_bev_stage_workspace_bytes(size_t height, size_t width);
+/* input [B,336,H,W] (image 80 channels, then lidar 256); spatial [B,512,H,W];
+ * shared [B,128,H,W]; heatmap [B,10,H,W] raw logits. */
+int bf_bev_stage_forward_ref(const bf_bev_stage *stage, const float *input_b336hw,
+                             size_t batches, size_t height, size_t width,
+                             float *spatial_b512hw, float *shared_b128hw,
+                             float *heatmap_b10hw, void *workspace, size_t workspace_bytes,
+                             char *error, size_t error_cap);
 
 /* ---- lift-splat pooling (bf_lss.h) ------------------------------------ */
 int bf_lss_geometry_f32_ref(const float *frustum_dhw3, const float *camera_to_lidar_rotation,

@@ -3,7 +3,8 @@
 libbfhip.so must load, export every entry point declared in include/*.h, and
 reject invalid contracts before launching anything (reference
 src/cuda_ops.cu:150-170,192-196; cuda_swin.cu:272-273; cuda_camera.cu:288-290;
-cuda_lss.cu:50-61,617-634,790-797; tests/test_cuda_ops.cu:164-174).
+cuda_lss.cu:50-61,617-634,790-797; cuda_bev_stage.cu:222-225,320-322;
+tests/test_cuda_ops.cu:164-174).
 """
 
 import ctypes as C
@@ -13,7 +14,7 @@ import re
 import bfhip
 
 ROOT = pathlib.Path(__file__).resolve().parent.parent
-HEADERS = ["bf_cuda_ops.h", "bf_cuda_swin.h", "bf_cuda_camera.h", "bf_cuda.h",
+HEADERS = ["bf_cuda_ops.h", "bf_cuda_swin.h", "bf_cuda_camera.h", "bf_cuda.h", "bf_cuda_bev.h",
            "bfhip_profile.h", "bfhip_debug.h"]
 
 
@@ -26,7 +27,7 @@ def declared(header):
 def test_every_declared_entry_point_is_exported():
     lib = bfhip.hip_lib()
     names = set().union(*(declared(h) for h in HEADERS))
-    assert len(names) == 27
+    assert len(names) == 31
     assert names == set(bfhip.SIGNATURES)
     missing = [n for n in sorted(names) if not hasattr(lib, n)]
     assert not missing, missing
@@ -152,3 +153,26 @@ def test_lss_entry_points_reject_invalid_contracts():
     assert b"unprepared" in e.value
     assert lib.bf_cuda_lss_plan_resident_bytes(None) == 0
     lib.bf_cuda_lss_plan_destroy(None)
+
+
+def test_bev_stage_rejects_invalid_contracts(tmp_path):
+    from bfhip import bfw
+    lib = bfhip.hip_lib()
+    e = _err()
+    s = C.c_void_p(1)
+    out = C.c_void_p()
+    path = bfw.write_bev_stage(tmp_path / "bev.bfw", seed=0)
+    with bfhip.Model(path) as m:
+        for h, w in ((0, 8), (8, 0), (7, 8), (8, 9)):
+            e.value = b""
+            assert lib.bf_cuda_bev_stage_create(m.handle, h, w, C.byref(out), e, 256) == 0
+            assert b"invalid" in e.value and not out
+        assert lib.bf_cuda_bev_stage_create(None, 8, 8, C.byref(out), e, 256) == 0
+        assert lib.bf_cuda_bev_stage_create(m.handle, 8, 8, None, e, 256) == 0
+        assert lib.bf_cuda_bev_stage_create(m.handle, 1 << 20, 1 << 20, C.byref(out), e, 256) == 0
+        assert b"too large" in e.value
+    e.value = b""
+    assert lib.bf_cuda_bev_stage_forward(None, s, s, s, s, None, e, 256) == 0
+    assert b"invalid" in e.value
+    assert lib.bf_cuda_bev_stage_resident_bytes(None) == 0
+    lib.bf_cuda_bev_stage_destroy(None)

@@ -189,3 +189,31 @@ def lss_downsample(p, bev):
     x = _conv_bn_relu(x, p, v + "3.weight", None, v + "4", stride=2, pad=1)
     x = _conv_bn_relu(x, p, v + "6.weight", None, v + "7", pad=1)
     return x.transpose(2, 3).contiguous().numpy()
+
+
+def bev_stage(p, x):
+    """Fuser + SECOND backbone / deblocks + TransFusion shared conv and heatmap
+    head (BatchNorm epsilon 1e-3) in float64: (spatial, shared, heatmap)."""
+    def cbr(y, w, bn, stride=1, pad=1, bias=None, relu=True):
+        y = F.conv2d(y, _t(p[w]), None if bias is None else _t(p[bias]), stride=stride,
+                     padding=pad)
+        if bn:
+            y = _bn(y, p, bn, eps=1e-3)
+        return F.relu(y) if relu else y
+
+    y = cbr(_t(x), "fuser.conv.0.weight", "fuser.conv.1")
+    for l in range(6):
+        y = cbr(y, f"backbone_2d.blocks.0.{3 * l + 1}.weight", f"backbone_2d.blocks.0.{3 * l + 2}")
+    up0 = cbr(y, "backbone_2d.deblocks.0.0.weight", "backbone_2d.deblocks.0.1", pad=0)
+    for l in range(6):
+        y = cbr(y, f"backbone_2d.blocks.1.{3 * l + 1}.weight", f"backbone_2d.blocks.1.{3 * l + 2}",
+                stride=1 if l else 2)
+    up1 = F.relu(_bn(F.conv_transpose2d(y, _t(p["backbone_2d.deblocks.1.0.weight"]), stride=2), p,
+                     "backbone_2d.deblocks.1.1", eps=1e-3))
+    spatial = torch.cat([up0, up1], 1)
+    shared = cbr(spatial, "dense_head.shared_conv.weight", None,
+                 bias="dense_head.shared_conv.bias", relu=False)
+    mid = cbr(shared, "dense_head.heatmap_head.0.conv.weight", "dense_head.heatmap_head.0.bn")
+    heat = cbr(mid, "dense_head.heatmap_head.1.weight", None,
+               bias="dense_head.heatmap_head.1.bias", relu=False)
+    return spatial.numpy(), shared.numpy(), heat.numpy()
