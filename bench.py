@@ -20,6 +20,11 @@ channels, a 360x360 grid), timed as the reference reports it
 (runs/rtx4060ti-2026-07-18/cuda_lss_intervals.txt): plan preparation from the
 calibration plus one forward per frame, with the forward's roofline, its
 measured HBM traffic and the reference's CPU pooling beside it.
+
+A "bev_stage" object times the BEV stage after it (include/bf_cuda_bev.h,
+the reference's 180x180 production shape, tests/test_cuda_bev_stage.cu:
+94-118): 18 BN-folded convolutions on fp16 MFMA operands, with its roofline
+(MFMA-bound) and the reference's CPU stage on the host.
 """
 
 from __future__ import annotations
@@ -61,6 +66,7 @@ def parse():
     p.add_argument("--pmc-child", default="",
                    help=argparse.SUPPRESS)  # internal: the program rocprofv3 profiles
     p.add_argument("--no-lss", action="store_true", help="skip the LSS pooling leg")
+    p.add_argument("--no-bev", action="store_true", help="skip the BEV stage leg")
     return p.parse_args()
 
 
@@ -418,6 +424,85 @@ def lss_cpu_baseline(sc):
             "cpu_model": _cpu_model()}
 
 
+BEV_HW = 180
+# Reference BEV stage on the RTX 4060 Ti (cuDNN, fp32 FMA math;
+# runs/rtx4060ti-2026-07-18/benchmark.csv:4) and its CPU stage (README.md:247).
+BEV_REFERENCE = {"gpu_ms": 19.6, "cpu_ms": 6110.0}
+
+
+def bev_layers(h=BEV_HW, w=BEV_HW):
+    """(name, M, N, K) of every GEMM of the stage (reference layer table,
+    cuda_bev_stage.cu:239-255)."""
+    hw, hw2 = h * w, (h // 2) * (w // 2)
+    out = [("fuser", hw, 256, 336 * 9)]
+    out += [(f"block0.{l}", hw, 128, (128 if l else 256) * 9) for l in range(6)]
+    out += [("deblock0", hw, 256, 128)]
+    out += [(f"block1.{l}", hw2, 256, (256 if l else 128) * 9) for l in range(6)]
+    out += [("deblock1", hw2, 1024, 256), ("shared", hw, 128, 512 * 9),
+            ("heatmap_mid", hw, 128, 128 * 9), ("heatmap_out", hw, 10, 128 * 9)]
+    return out
+
+
+def bev_leg(dev, reps, seed=0):
+    """BEV stage at 180x180: ms per forward, TFLOP/s, MFMA roofline."""
+    import torch
+    import bfhip
+    from bfhip import bfw
+    tmp = pathlib.Path(tempfile.mkdtemp(prefix="bev_"))
+    path = bfw.write_bev_stage(tmp / "bev.bfw", seed=seed, mode="baseline")
+    x = torch.from_numpy(bfw.synthetic_bev(seed, BEV_HW, BEV_HW)).to(dev)
+    stream = torch.cuda.Stream()
+    with bfhip.Model(path) as m:
+        stage = bfhip.BevStage(m, BEV_HW, BEV_HW)
+    with torch.cuda.stream(stream):
+        outs = stage.forward(x, stream=stream)
+        for _ in range(3):
+            stage.forward(x, outs, stream=stream)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(reps):
+            stage.forward(x, outs, stream=stream)
+        b.record(stream)
+        b.synchronize()
+    ms = a.elapsed_time(b) / reps
+    flops = sum(2.0 * m_ * n * k for _, m_, n, k in bev_layers())
+    tflops = flops / (ms * 1e-3) / 1e12
+    hw = BEV_HW * BEV_HW
+    nbytes = 4 * hw * (336 + 512 + 128 + 10) + 2 * sum(n * k for _, _, n, k in bev_layers())
+    out = {"workload": "BEV stage (fuser + SECOND backbone/deblocks + TransFusion shared conv "
+                       "and heatmap head), 1 x 336 x 180 x 180 input, random-init weights "
+                       "N(0,0.02), fp16 MFMA operands, fp32 accumulate",
+           "ms": round(ms, 4), "tflops": round(tflops, 1), "gflop": round(flops / 1e9, 1),
+           "reference_rtx4060ti_ms": BEV_REFERENCE["gpu_ms"],
+           "resident_mib": round(stage.resident_bytes() / 2**20, 1),
+           "roofline": {"kernel": "bev stage forward (18 convolutions)", "bound": "mfma",
+                        "achieved": round(tflops, 1), "peak": PEAK_BF16_TFLOPS,
+                        "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+                        "traffic": None, "algorithmic_bytes": nbytes,
+                        "note": "dense fp16 MFMA peak equals the bf16 one (2.5 PFLOP/s)"}}
+    stage.close()
+    return out, path
+
+
+def bev_cpu_baseline(path, seed=0):
+    """The reference's CPU BEV stage (oracle/_ref, src/bev_stage.c, OpenMP) at
+    a bounded 90x90 sample, scaled to 180x180 by the work ratio (4x)."""
+    import oracle
+    from bfhip import bfw
+    kind = "reference" if oracle.available("ref") else "port"
+    o = oracle.Oracle("ref" if kind == "reference" else "port")
+    x = bfw.synthetic_bev(seed, BEV_HW // 2, BEV_HW // 2)
+    with o.open_model(path) as m:
+        t0 = time.perf_counter()
+        o.bev_stage(m, x)
+        t1 = time.perf_counter()
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or os.cpu_count()
+    return {"value": round((t1 - t0) * 1e3 * 4, 1), "unit": "ms/forward", "cores": threads,
+            "kind": kind, "backend": o.backend(),
+            "sample": f"90x90 BEV ({1e3 * (t1 - t0):.0f} ms), scaled x4 to 180x180",
+            "reference_readme_ms": BEV_REFERENCE["cpu_ms"], "cpu_model": _cpu_model()}
+
+
 def cpu_baseline(model_path, cameras):
     """Reference CPU path (oracle/_ref, the reference's C compiled from its own
     sources, OpenMP) on a bounded sample of `cameras` cameras, scaled to a
@@ -567,6 +652,11 @@ def main():
         if not args.no_cpu:
             lss["cpu_baseline"] = lss_cpu_baseline(sc)
         result["lss"] = lss
+    if not args.no_bev:
+        bev, bev_path = bev_leg(dev, max(args.steps, 20))
+        if not args.no_cpu:
+            bev["cpu_baseline"] = bev_cpu_baseline(bev_path)
+        result["bev_stage"] = bev
     print(json.dumps(result))
 
 
