@@ -276,6 +276,64 @@ def bev_stage_tensors(init: _Init):
     return out
 
 
+def transfusion_tensors(init: _Init):
+    """TransFusion head under the checkpoint's names and shapes (reference
+    src/transfusion_decoder.c:165-208): class encoding, one decoder layer
+    (self / cross nn.MultiheadAttention, FFN, three LayerNorms, two position
+    embedding heads) and six prediction heads.  The position heads' first
+    conv sees cell coordinates up to the grid size, so it keeps std 0.02 in
+    every mode."""
+    out = []
+    d = "dense_head.decoder."
+
+    def w(name, shape, fan_in):
+        out.append((name, init.weight(name, shape, fan_in)))
+
+    def b(name, shape):
+        out.append((name, init.bias(name, shape)))
+
+    w("dense_head.class_encoding.weight", (128, 10, 1), 10)
+    b("dense_head.class_encoding.bias", (128,))
+    for attn in ("self_attn", "multihead_attn"):
+        w(f"{d}{attn}.in_proj_weight", (384, 128), 128)
+        b(f"{d}{attn}.in_proj_bias", (384,))
+        w(f"{d}{attn}.out_proj.weight", (128, 128), 128)
+        b(f"{d}{attn}.out_proj.bias", (128,))
+    w(f"{d}linear1.weight", (256, 128), 128)
+    b(f"{d}linear1.bias", (256,))
+    w(f"{d}linear2.weight", (128, 256), 256)
+    b(f"{d}linear2.bias", (128,))
+    for i in (1, 2, 3):
+        out += init.norm(f"{d}norm{i}", 128)
+    for pos in ("self_posembed", "cross_posembed"):
+        q = f"{d}{pos}.position_embedding_head."
+        out.append((q + "0.weight", randn(init.seed, q + "0.weight", (128, 2, 1), 0.02)))
+        b(q + "0.bias", (128,))
+        out += init.bn(q + "1", 128)
+        w(q + "3.weight", (128, 128, 1), 128)
+        b(q + "3.bias", (128,))
+    for head, ch in (("center", 2), ("height", 1), ("dim", 3), ("rot", 2), ("vel", 2),
+                     ("heatmap", 10)):
+        q = f"dense_head.prediction_head.{head}."
+        w(q + "0.0.weight", (64, 128, 1), 128)
+        out += init.bn(q + "0.1", 64)
+        w(q + "1.weight", (ch, 64, 1), 64)
+        b(q + "1.bias", (ch,))
+    return out
+
+
+def write_transfusion(path, seed: int = 0, mode: str = "baseline", gain: float = 1.0) -> pathlib.Path:
+    path = pathlib.Path(path)
+    write_bfw(transfusion_tensors(_Init(seed, mode, gain)), path)
+    return path
+
+
+def synthetic_transfusion_inputs(seed: int, height=180, width=180):
+    """shared [1,128,H,W] ~N(0,1) and dense heatmap logits [1,10,H,W] ~N(-1, 1.5)."""
+    return (randn(seed, "tf_shared", (1, 128, height, width)),
+            randn(seed, "tf_heatmap", (1, 10, height, width), 1.5, -1.0))
+
+
 def write_bev_stage(path, seed: int = 0, mode: str = "baseline", gain: float = 1.0) -> pathlib.Path:
     path = pathlib.Path(path)
     write_bfw(bev_stage_tensors(_Init(seed, mode, gain)), path)

@@ -71,6 +71,31 @@ class OracleError(RuntimeError):
     pass
 
 
+class TfRaw(C.Structure):
+    """bf_transfusion_raw_outputs (include/bf_transfusion_decoder.h)."""
+    _fields_ = [(n, C.c_void_p) for n in (
+        "center", "height", "dimension_log", "rotation", "velocity", "heatmap_logits",
+        "query_scores", "labels", "indices")]
+
+
+class Detection(C.Structure):
+    """bf_detection (include/bevfusion.h)."""
+    _fields_ = [(n, C.c_float) for n in ("x", "y", "z", "width", "length", "height", "yaw",
+                                         "velocity_x", "velocity_y", "score")] + \
+               [("class_id", C.c_int)]
+
+
+class Detections(C.Structure):
+    """bf_detections (include/bevfusion.h)."""
+    _fields_ = [("items", Detection * 200), ("count", C.c_int)]
+
+
+def detections_array(d):
+    """bf_detections -> float64 array [count, 11]."""
+    rows = [[getattr(d.items[i], f) for f, _ in Detection._fields_] for i in range(d.count)]
+    return np.array(rows, np.float64).reshape(-1, 11)
+
+
 def available(flavour: str) -> bool:
     return LIBS[flavour].exists()
 
@@ -122,7 +147,8 @@ class Oracle:
         L.bf_swin_window_attention_f32_ref.argtypes = [
             _f32p, _f32p, _f32p, _f32p, _i64p, C.c_void_p, _sz, _f32p, _f32p, _f32p,
             _sz, _sz, _sz, _sz, _sz]
-        for mod in ("swin_backbone", "image_fpn", "depth_head", "lss_downsample", "bev_stage"):
+        for mod in ("swin_backbone", "image_fpn", "depth_head", "lss_downsample", "bev_stage",
+                    "transfusion_decoder"):
             getattr(L, f"bf_{mod}_create").argtypes = [C.c_void_p, C.POINTER(C.c_void_p),
                                                        C.c_char_p, _sz]
             getattr(L, f"bf_{mod}_destroy").argtypes = [C.c_void_p]
@@ -148,6 +174,18 @@ class Oracle:
         L.bf_bev_stage_forward_ref.argtypes = [
             C.c_void_p, _f32p, _sz, _sz, _sz, _f32p, _f32p, _f32p, C.c_void_p, _sz,
             C.c_char_p, _sz]
+        L.bf_transfusion_decoder_workspace_bytes.argtypes = [_sz, _sz, _sz]
+        L.bf_transfusion_decoder_workspace_bytes.restype = _sz
+        L.bf_transfusion_decoder_forward_ref.argtypes = [
+            C.c_void_p, _f32p, _f32p, _sz, _sz, _sz, _sz, C.c_void_p, C.c_void_p, _sz,
+            C.c_char_p, _sz]
+        L.bf_transfusion_select_proposals_f32_ref.argtypes = [
+            _f32p, _f32p, _f32p, C.c_void_p, C.c_void_p, _sz, _sz, _sz, _sz, _sz, _sz]
+        L.bf_transfusion_decode_raw_f32_ref.argtypes = [
+            _f32p, _f32p, C.c_void_p, _f32p, _f32p, _f32p, _f32p, C.c_void_p, _f32p, _f32p,
+            C.c_void_p, _sz, _sz, _sz, C.c_float, _f32p, _f32p]
+        L.bf_transfusion_filter_detections.argtypes = [
+            _f32p, _f32p, C.c_void_p, _sz, _sz, C.c_float, _f32p, C.c_void_p]
         L.bf_lss_geometry_f32_ref.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p,
                                               C.c_void_p, C.c_void_p, _f32p, _sz, _sz, _sz,
                                               _sz, _sz]
@@ -353,6 +391,54 @@ class Oracle:
         finally:
             self.lib.bf_bev_stage_destroy(net)
         return sp, sh, hm
+
+    # ---- TransFusion head ------------------------------------------------
+    TF_FIELDS = (("center", 2), ("height", 1), ("dimension_log", 3), ("rotation", 2),
+                 ("velocity", 2), ("heatmap_logits", 10), ("query_scores", 10))
+
+    def transfusion(self, model, shared, heatmap, proposals):
+        """shared [B,128,H,W], heatmap logits [B,10,H,W] -> dict of raw outputs
+        (channel-major [B,C,P] arrays, int64 labels / indices [B,P])."""
+        shared, heatmap = _f32(shared), _f32(heatmap)
+        b, _, h, w = shared.shape
+        outs = {k: np.empty((b, c, proposals), np.float32) for k, c in self.TF_FIELDS}
+        outs["labels"] = np.empty((b, proposals), np.int64)
+        outs["indices"] = np.empty((b, proposals), np.int64)
+        raw = TfRaw(*[outs[k].ctypes.data for k, _ in self.TF_FIELDS],
+                    outs["labels"].ctypes.data, outs["indices"].ctypes.data)
+        net = model.create("transfusion_decoder")
+        try:
+            nbytes = self.lib.bf_transfusion_decoder_workspace_bytes(h, w, proposals)
+            ws = np.empty(max(nbytes, 1), np.uint8)
+            err = C.create_string_buffer(256)
+            if not self.lib.bf_transfusion_decoder_forward_ref(
+                    net, shared, heatmap, b, h, w, proposals, C.byref(raw), ws.ctypes.data,
+                    nbytes, err, 256):
+                raise OracleError(err.value.decode())
+        finally:
+            self.lib.bf_transfusion_decoder_destroy(net)
+        return outs
+
+    def transfusion_detections(self, outs, threshold, stride=8.0, voxel=(0.075, 0.075),
+                               minimum=(-54.0, -54.0),
+                               post_range=(-61.2, -61.2, -10.0, 61.2, 61.2, 10.0)):
+        """decode_raw + filter (transfusion.c:134-193) -> list of per-batch
+        detection arrays [n, 11] (x y z w l h yaw vx vy score class)."""
+        b, _, p = outs["center"].shape
+        boxes = np.empty((b, p, 9), np.float32)
+        scores = np.empty((b, p), np.float32)
+        labels = np.empty((b, p), np.int64)
+        if not self.lib.bf_transfusion_decode_raw_f32_ref(
+                outs["heatmap_logits"], outs["query_scores"], outs["labels"].ctypes.data,
+                outs["center"], outs["height"], outs["dimension_log"], outs["rotation"],
+                outs["velocity"].ctypes.data, boxes, scores, labels.ctypes.data, b, 10, p,
+                stride, _f32(voxel), _f32(minimum)):
+            raise OracleError("TransFusion decode failed")
+        dets = (Detections * b)()
+        if not self.lib.bf_transfusion_filter_detections(boxes, scores, labels.ctypes.data, b, p,
+                                                         threshold, _f32(post_range), dets):
+            raise OracleError("TransFusion filter failed")
+        return [detections_array(d) for d in dets]
 
     # ---- lift-splat pooling (bf_lss.h) ------------------------------------
     def lss_geometry(self, frustum, cam_rot, cam_trans, intrinsics, post_rot, post_trans,

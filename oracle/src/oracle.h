@@ -14,6 +14,8 @@
  *   bf_lss_downsample.h -> reference include/bf_lss_downsample.h, src/lss_downsample.c:70-148
  *   bf_lss.h            -> reference include/bf_lss.h:18-46,     src/lss.c:8-241
  *   bf_bev_stage.h      -> reference include/bf_bev_stage.h,     src/bev_stage.c:16-227
+ *   bf_transfusion*.h   -> reference include/bf_transfusion*.h,  src/transfusion.c:8-193,
+ *                          src/transfusion_decoder.c:23-456
  * Floating-point operation order matches the reference per output element, so
  * the scalar build (no OpenMP, BF_CPU_SCALAR=1) is bit-identical to the
  * reference compiled from its own sources (oracle/_ref).
@@ -21,8 +23,10 @@
 #ifndef BF_ORACLE_H
 #define BF_ORACLE_H
 
+#include "bevfusion.h"
 #include "bf_lss.h"
 #include "bf_model.h"
+#include "bf_transfusion_decoder.h"
 
 #include <stddef.h>
 #include <stdint.h>
@@ -182,6 +186,38 @@ int bf_bev_stage_forward_ref(const bf_bev_stage *stage, const float *input_b336h
                              float *spatial_b512hw, float *shared_b128hw,
                              float *heatmap_b10hw, void *workspace, size_t workspace_bytes,
                              char *error, size_t error_cap);
+
+/* ---- TransFusion head (bf_transfusion.h, bf_transfusion_decoder.h) ---- */
+int bf_transfusion_select_proposals_f32_ref(const float *dense_heatmap_logits_bchw,
+                                            float *suppressed_heatmap_bchw,
+                                            float *proposal_scores_bk, int64_t *proposal_classes_bk,
+                                            int64_t *proposal_indices_bk, size_t batches,
+                                            size_t classes, size_t height, size_t width,
+                                            size_t proposals, size_t nms_kernel_size);
+int bf_transfusion_decode_raw_f32_ref(const float *heatmap_logits_bcp,
+                                      const float *query_heatmap_scores_bcp,
+                                      const int64_t *query_labels_bp, const float *center_b2p,
+                                      const float *height_b1p, const float *dimension_log_b3p,
+                                      const float *rotation_sincos_b2p, const float *velocity_b2p,
+                                      float *boxes_bp9, float *scores_bp, int64_t *labels_bp,
+                                      size_t batches, size_t classes, size_t proposals,
+                                      float feature_stride, const float voxel_size_xy[2],
+                                      const float point_cloud_minimum_xy[2]);
+int bf_transfusion_filter_detections(const float *boxes_bp9, const float *scores_bp,
+                                     const int64_t *labels_bp, size_t batches, size_t proposals,
+                                     float score_threshold, const float post_center_range[6],
+                                     bf_detections *output);
+typedef struct bf_transfusion_decoder bf_transfusion_decoder;
+int bf_transfusion_decoder_create(const bf_model *model, bf_transfusion_decoder **out,
+                                  char *error, size_t error_cap);
+void bf_transfusion_decoder_destroy(bf_transfusion_decoder *decoder);
+size_t bf_transfusion_decoder_workspace_bytes(size_t height, size_t width, size_t proposals);
+int bf_transfusion_decoder_forward_ref(const bf_transfusion_decoder *decoder,
+                                       const float *shared_b128hw,
+                                       const float *dense_heatmap_logits_b10hw, size_t batches,
+                                       size_t height, size_t width, size_t proposals,
+                                       bf_transfusion_raw_outputs *outputs, void *workspace,
+                                       size_t workspace_bytes, char *error, size_t error_cap);
 
 /* ---- lift-splat pooling (bf_lss.h) ------------------------------------ */
 int bf_lss_geometry_f32_ref(const float *frustum_dhw3, const float *camera_to_lidar_rotation,

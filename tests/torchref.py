@@ -217,3 +217,72 @@ def bev_stage(p, x):
     heat = cbr(mid, "dense_head.heatmap_head.1.weight", None,
                bias="dense_head.heatmap_head.1.bias", relu=False)
     return spatial.numpy(), shared.numpy(), heat.numpy()
+
+
+def transfusion(p, shared, heatmap, proposals):
+    """TransFusion head (mmdet3d TransFusionHead with one decoder layer) in
+    float64: heatmap NMS by F.max_pool2d (interior 3x3 maxima; classes 8 and 9
+    exempt; borders suppressed), top-k by a stable descending sort, query =
+    features + class encoding, position embeddings, self and cross
+    nn.MultiheadAttention through F.multi_head_attention_forward, FFN, three
+    LayerNorms and the six prediction heads.  Returns the raw-output dict of
+    oracle.Oracle.transfusion."""
+    sh, hm = _t(shared)[0], torch.sigmoid(_t(heatmap))
+    c, h, w = sh.shape
+    keys = h * w
+    local = torch.zeros_like(hm)
+    local[:, :, 1:-1, 1:-1] = F.max_pool2d(hm, 3, 1, 0)
+    local[:, 8], local[:, 9] = hm[:, 8], hm[:, 9]
+    hm = hm * (hm == local)
+    flat = hm[0].reshape(-1)
+    order = torch.sort(flat, descending=True, stable=True).indices[:proposals]
+    labels, index = order // keys, order % keys
+    feat = sh.reshape(c, keys)
+    query = feat[:, index] + _t(p["dense_head.class_encoding.weight"])[:, :, 0][:, labels] + \
+        _t(p["dense_head.class_encoding.bias"])[:, None]
+    query = query.T  # [P, C]
+
+    def posembed(base, cells):
+        x = (cells % w).to(torch.float64) + 0.5
+        y = torch.div(cells, w, rounding_mode="floor").to(torch.float64) + 0.5
+        q = f"dense_head.decoder.{base}.position_embedding_head."
+        z = F.conv1d(torch.stack([x, y])[None], _t(p[q + "0.weight"]), _t(p[q + "0.bias"]))
+        z = F.relu(_bn(z, p, q + "1"))
+        return F.conv1d(z, _t(p[q + "3.weight"]), _t(p[q + "3.bias"]))[0].T
+
+    query_pos = posembed("self_posembed", index)
+    key_value = posembed("cross_posembed", torch.arange(keys)) + feat.T
+
+    def mha(name, q, kv):
+        pre = f"dense_head.decoder.{name}."
+        out, _ = F.multi_head_attention_forward(
+            q[:, None], kv[:, None], kv[:, None], 128, 8, _t(p[pre + "in_proj_weight"]),
+            _t(p[pre + "in_proj_bias"]), None, None, False, 0.0,
+            _t(p[pre + "out_proj.weight"]), _t(p[pre + "out_proj.bias"]), training=False,
+            need_weights=False)
+        return out[:, 0]
+
+    def norm(x, i):
+        pre = f"dense_head.decoder.norm{i}."
+        return F.layer_norm(x, (128,), _t(p[pre + "weight"]), _t(p[pre + "bias"]), 1e-5)
+
+    t = query + query_pos
+    query = norm(query + mha("self_attn", t, t), 1)
+    query = norm(query + mha("multihead_attn", query + query_pos, key_value), 2)
+    d = "dense_head.decoder."
+    ffn = F.linear(F.relu(F.linear(query, _t(p[d + "linear1.weight"]), _t(p[d + "linear1.bias"]))),
+                   _t(p[d + "linear2.weight"]), _t(p[d + "linear2.bias"]))
+    query = norm(query + ffn, 3)
+    out = {}
+    for key, head in (("center", "center"), ("height", "height"), ("dimension_log", "dim"),
+                      ("rotation", "rot"), ("velocity", "vel"), ("heatmap_logits", "heatmap")):
+        q = f"dense_head.prediction_head.{head}."
+        z = F.conv1d(query.T[None], _t(p[q + "0.0.weight"]))
+        z = F.relu(_bn(z, p, q + "0.1"))
+        out[key] = F.conv1d(z, _t(p[q + "1.weight"]), _t(p[q + "1.bias"])).numpy()
+    out["center"][0, 0] += (index % w).numpy() + 0.5
+    out["center"][0, 1] += torch.div(index, w, rounding_mode="floor").numpy() + 0.5
+    out["query_scores"] = hm[0].reshape(10, keys)[:, index][None].numpy()
+    out["labels"] = labels[None].numpy()
+    out["indices"] = index[None].numpy()
+    return out
