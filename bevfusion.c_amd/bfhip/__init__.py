@@ -1,10 +1,10 @@
 """Python host side of the gfx950 camera-path library.
 
 Thin ctypes mirror of the C ABI in ``include/bf_cuda_ops.h``,
-``include/bf_cuda_swin.h``, ``include/bf_cuda_camera.h``, ``include/bf_cuda.h``
-and ``include/bf_cuda_bev.h`` (the reference's operator/plugin interface for
-this path, the lift-splat pooling that consumes it and the BEV stage after
-it).  PyTorch supplies device memory and
+``include/bf_cuda_swin.h``, ``include/bf_cuda_camera.h``, ``include/bf_cuda.h``,
+``include/bf_cuda_bev.h`` and ``include/bf_cuda_transfusion.h`` (the
+reference's operator/plugin interface for this path, the lift-splat pooling
+that consumes it, the BEV stage after it and the TransFusion decoder).  PyTorch supplies device memory and
 the current HIP stream; every computation runs in ``lib/libbfhip.so``.  There
 is no fallback: if the library is missing, importing an entry point raises.
 """
@@ -49,6 +49,28 @@ def lss_desc(batches, cameras, depth_bins, height, width, channels, minimum, ste
 
 _lssp = C.POINTER(LssDesc)
 
+
+class TfRawOutputs(C.Structure):
+    """``bf_transfusion_raw_outputs`` (include/bf_transfusion_decoder.h)."""
+    _fields_ = [(n, _vp) for n in (
+        "center", "height", "dimension_log", "rotation", "velocity", "heatmap_logits",
+        "query_scores", "labels", "indices")]
+
+
+class Detection(C.Structure):
+    """``bf_detection`` (include/bevfusion.h)."""
+    _fields_ = [(n, C.c_float) for n in ("x", "y", "z", "width", "length", "height", "yaw",
+                                         "velocity_x", "velocity_y", "score")] + \
+               [("class_id", C.c_int)]
+
+
+class Detections(C.Structure):
+    """``bf_detections`` (include/bevfusion.h): BF_MAX_PROPOSALS items + count."""
+    _fields_ = [("items", Detection * 200), ("count", C.c_int)]
+
+
+_tfp = C.POINTER(TfRawOutputs)
+
 # Every symbol declared by include/*.h, with its ctypes signature.
 SIGNATURES = {
     "bf_cuda_conv2d_f32": (_i, [C.POINTER(ConvDesc), _vp, _vp, _vp, _vp, _vp, C.c_char_p, _sz]),
@@ -86,6 +108,12 @@ SIGNATURES = {
     "bf_cuda_bev_stage_destroy": (None, [_vp]),
     "bf_cuda_bev_stage_forward": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, C.c_char_p, _sz]),
     "bf_cuda_bev_stage_resident_bytes": (_sz, [_vp]),
+    "bf_cuda_transfusion_create": (_i, [_vp, _sz, _sz, _sz, C.POINTER(_vp), C.c_char_p, _sz]),
+    "bf_cuda_transfusion_destroy": (None, [_vp]),
+    "bf_cuda_transfusion_forward": (_i, [_vp, _vp, _vp, _tfp, _vp, C.c_char_p, _sz]),
+    "bf_cuda_transfusion_decode_detections": (_i, [_vp, _tfp, C.c_float, C.POINTER(Detections),
+                                                   _vp, C.c_char_p, _sz]),
+    "bf_cuda_transfusion_resident_bytes": (_sz, [_vp]),
 }
 
 SWIN_OPS = ("ln1", "qkv", "attention", "proj", "ln2", "fc1", "fc2", "merge", "mlp")
@@ -541,6 +569,82 @@ class BevStage:
     def close(self):
         if self.handle:
             self.lib.bf_cuda_bev_stage_destroy(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+TF_FIELDS = (("center", 2), ("height", 1), ("dimension_log", 3), ("rotation", 2),
+             ("velocity", 2), ("heatmap_logits", 10), ("query_scores", 10))
+
+
+def _lptr(t):
+    torch = _torch()
+    if not t.is_cuda or t.dtype != torch.int64 or not t.is_contiguous():
+        raise BfHipError("expected a contiguous int64 device tensor")
+    return _vp(t.data_ptr())
+
+
+class TransFusion:
+    """bf_cuda_transfusion context (include/bf_cuda_transfusion.h): batch one,
+    H x W BEV map, `proposals` queries."""
+
+    def __init__(self, model: Model, height: int, width: int, proposals: int = 200):
+        self.lib, self.h, self.w, self.p = hip_lib(), height, width, proposals
+        self.handle, err = _vp(), _err()
+        _check(self.lib.bf_cuda_transfusion_create(model.handle, height, width, proposals,
+                                                   C.byref(self.handle), err, 512),
+               err, "bf_cuda_transfusion_create")
+
+    def resident_bytes(self) -> int:
+        return self.lib.bf_cuda_transfusion_resident_bytes(self.handle)
+
+    def outputs(self, device):
+        """Fresh raw-output tensors: channel-major [1,C,P] fp32 fields plus
+        int64 labels / indices [1,P]."""
+        torch = _torch()
+        outs = {k: torch.empty((1, c, self.p), device=device) for k, c in TF_FIELDS}
+        outs["labels"] = torch.empty((1, self.p), dtype=torch.int64, device=device)
+        outs["indices"] = torch.empty((1, self.p), dtype=torch.int64, device=device)
+        return outs
+
+    @staticmethod
+    def raw(outs):
+        return TfRawOutputs(*[_ptr(outs[k]) for k, _ in TF_FIELDS],
+                            _lptr(outs["labels"]), _lptr(outs["indices"]))
+
+    def forward(self, shared, heatmap, outs=None, stream=None):
+        """shared [1,128,H,W], heatmap logits [1,10,H,W] -> dict of raw outputs."""
+        if outs is None:
+            outs = self.outputs(shared.device)
+        raw, err = self.raw(outs), _err()
+        _check(self.lib.bf_cuda_transfusion_forward(self.handle, _ptr(shared), _ptr(heatmap),
+                                                    C.byref(raw), _stream(stream), err, 512),
+               err, "bf_cuda_transfusion_forward")
+        return outs
+
+    def decode(self, outs, threshold, stream=None):
+        """GPU decode + range filter of one forward's outputs -> Detections
+        (synchronises the stream)."""
+        raw, dets, err = self.raw(outs), Detections(), _err()
+        _check(self.lib.bf_cuda_transfusion_decode_detections(
+            self.handle, C.byref(raw), threshold, C.byref(dets), _stream(stream), err, 512),
+            err, "bf_cuda_transfusion_decode_detections")
+        return dets
+
+    def close(self):
+        if self.handle:
+            self.lib.bf_cuda_transfusion_destroy(self.handle)
             self.handle = None
 
     def __enter__(self):

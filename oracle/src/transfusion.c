@@ -287,14 +287,26 @@ fail:
 
 void bf_transfusion_decoder_destroy(bf_transfusion_decoder *d) { free(d); }
 
-/* transfusion_decoder.c:212-224 */
+/* transfusion_decoder.c:212-224, with one deliberate difference: the
+ * projection and score-slot regions hold max(keys, proposals) rows.  The
+ * reference sizes them by keys alone (transfusion_decoder.c:219, 354-357),
+ * but self attention also runs its P-row K/V projections and P-wide score
+ * rows through them, so for proposals > H * W (allowed by its contract,
+ * proposals <= 10 * H * W) its self attention overruns into the suppressed
+ * map and the query rows.  For proposals <= H * W both layouts give the same
+ * results. */
 size_t bf_transfusion_decoder_workspace_bytes(size_t height, size_t width, size_t proposals) {
-    size_t keys, key_floats, proposal_floats, bytes;
+    size_t keys, rows, key_floats, row_floats, proposal_floats, bytes;
     if (!height || !width || !proposals || proposals > 200 || !bf_oracle_mul(height, width, &keys) ||
-        proposals > 10 * keys || !bf_oracle_mul(keys, 3 * TF_C + 10 + TF_SLOTS, &key_floats) ||
+        proposals > 10 * keys)
+        return 0;
+    rows = keys > proposals ? keys : proposals;
+    if (!bf_oracle_mul(keys, TF_C + 10, &key_floats) ||
+        !bf_oracle_mul(rows, 2 * TF_C + TF_SLOTS, &row_floats) ||
+        key_floats > SIZE_MAX - row_floats ||
         !bf_oracle_mul(proposals, 8 * TF_C + 1, &proposal_floats) ||
-        key_floats > SIZE_MAX - proposal_floats ||
-        !bf_oracle_mul(key_floats + proposal_floats, sizeof(float), &bytes))
+        key_floats + row_floats > SIZE_MAX - proposal_floats ||
+        !bf_oracle_mul(key_floats + row_floats + proposal_floats, sizeof(float), &bytes))
         return 0;
     return bytes;
 }
@@ -407,11 +419,12 @@ int bf_transfusion_decoder_forward_ref(const bf_transfusion_decoder *d, const fl
         return bf_oracle_fail(error, cap, "invalid TransFusion buffers or dimensions");
     const size_t keys = height * width, P = proposals;
     float *w = (float *)workspace;
+    const size_t rows = keys > P ? keys : P;
     float *key_value = w; w += keys * TF_C;
-    float *key_proj = w; w += keys * TF_C;
-    float *value_proj = w; w += keys * TF_C;
+    float *key_proj = w; w += rows * TF_C;
+    float *value_proj = w; w += rows * TF_C;
     float *suppressed = w; w += keys * 10;
-    float *slots = w; w += keys * TF_SLOTS;
+    float *slots = w; w += rows * TF_SLOTS;
     float *query = w; w += P * TF_C;
     float *query_pos = w; w += P * TF_C;
     float *tmp = w; w += P * TF_C;

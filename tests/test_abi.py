@@ -4,7 +4,7 @@ libbfhip.so must load, export every entry point declared in include/*.h, and
 reject invalid contracts before launching anything (reference
 src/cuda_ops.cu:150-170,192-196; cuda_swin.cu:272-273; cuda_camera.cu:288-290;
 cuda_lss.cu:50-61,617-634,790-797; cuda_bev_stage.cu:222-225,320-322;
-tests/test_cuda_ops.cu:164-174).
+cuda_transfusion.cu:274-276,329-333,402-407; tests/test_cuda_ops.cu:164-174).
 """
 
 import ctypes as C
@@ -15,7 +15,7 @@ import bfhip
 
 ROOT = pathlib.Path(__file__).resolve().parent.parent
 HEADERS = ["bf_cuda_ops.h", "bf_cuda_swin.h", "bf_cuda_camera.h", "bf_cuda.h", "bf_cuda_bev.h",
-           "bfhip_profile.h", "bfhip_debug.h"]
+           "bf_cuda_transfusion.h", "bfhip_profile.h", "bfhip_debug.h"]
 
 
 def declared(header):
@@ -27,7 +27,7 @@ def declared(header):
 def test_every_declared_entry_point_is_exported():
     lib = bfhip.hip_lib()
     names = set().union(*(declared(h) for h in HEADERS))
-    assert len(names) == 31
+    assert len(names) == 36
     assert names == set(bfhip.SIGNATURES)
     missing = [n for n in sorted(names) if not hasattr(lib, n)]
     assert not missing, missing
@@ -176,3 +176,31 @@ def test_bev_stage_rejects_invalid_contracts(tmp_path):
     assert b"invalid" in e.value
     assert lib.bf_cuda_bev_stage_resident_bytes(None) == 0
     lib.bf_cuda_bev_stage_destroy(None)
+
+
+def test_transfusion_rejects_invalid_contracts(tmp_path):
+    from bfhip import bfw
+    lib = bfhip.hip_lib()
+    e = _err()
+    s = C.c_void_p(1)
+    out = C.c_void_p()
+    path = bfw.write_transfusion(tmp_path / "tf.bfw", seed=0)
+    with bfhip.Model(path) as m:
+        for h, w, p in ((0, 8, 10), (8, 0, 10), (8, 8, 0), (8, 8, 201), (1 << 17, 1 << 16, 10)):
+            e.value = b""
+            assert lib.bf_cuda_transfusion_create(m.handle, h, w, p, C.byref(out), e, 256) == 0
+            assert b"invalid" in e.value and not out
+        # Fewer candidates (10 * H * W) than proposals.
+        assert lib.bf_cuda_transfusion_create(m.handle, 2, 2, 41, C.byref(out), e, 256) == 0
+        assert b"out of range" in e.value and not out
+        assert lib.bf_cuda_transfusion_create(None, 8, 8, 10, C.byref(out), e, 256) == 0
+        assert lib.bf_cuda_transfusion_create(m.handle, 8, 8, 10, None, e, 256) == 0
+    e.value = b""
+    raw = bfhip.TfRawOutputs(*([1] * 9))
+    assert lib.bf_cuda_transfusion_forward(None, s, s, C.byref(raw), None, e, 256) == 0
+    assert b"invalid" in e.value
+    dets = bfhip.Detections()
+    assert lib.bf_cuda_transfusion_decode_detections(None, C.byref(raw), 0.1, C.byref(dets),
+                                                     None, e, 256) == 0
+    assert lib.bf_cuda_transfusion_resident_bytes(None) == 0
+    lib.bf_cuda_transfusion_destroy(None)

@@ -49,13 +49,16 @@ def test_transfusion_bit_exact_with_reference_build(tf_model, hw, proposals):
     assert len(da[0]) == len(db[0]) and np.array_equal(da[0], db[0])
 
 
-def test_transfusion_against_float64_torch(tf_model):
+@pytest.mark.parametrize("hw,proposals", [((16, 18), 40), ((2, 3), 60), ((1, 1), 10)])
+def test_transfusion_against_float64_torch(tf_model, hw, proposals):
+    """Includes proposals > H * W, where the reference's own workspace is too
+    small for its self attention (the oracle sizes it by max(keys, P))."""
     path, p = tf_model
-    sh, hm = bfw.synthetic_transfusion_inputs(8, 16, 18)
+    sh, hm = bfw.synthetic_transfusion_inputs(8, *hw)
     o = oracle.Oracle("port")
     with o.open_model(path) as m:
-        got = o.transfusion(m, sh, hm, 40)
-    ref = torchref.transfusion(p, sh, hm, 40)
+        got = o.transfusion(m, sh, hm, proposals)
+    ref = torchref.transfusion(p, sh, hm, proposals)
     assert np.array_equal(got["indices"], ref["indices"])
     assert np.array_equal(got["labels"], ref["labels"])
     for k, v in ref.items():
@@ -104,6 +107,9 @@ def test_decoder_rejections(tf_model):
     lib = o.lib
     need = lib.bf_transfusion_decoder_workspace_bytes(12, 14, 20)
     assert need == 4 * (168 * (3 * 128 + 10 + 16) + 20 * (8 * 128 + 1))
+    # Projection and score-slot rows are max(keys, proposals).
+    assert lib.bf_transfusion_decoder_workspace_bytes(2, 3, 60) == 4 * (
+        6 * (128 + 10) + 60 * (2 * 128 + 16) + 60 * (8 * 128 + 1))
     assert lib.bf_transfusion_decoder_workspace_bytes(12, 14, 201) == 0
     assert lib.bf_transfusion_decoder_workspace_bytes(1, 1, 11) == 0
     sh, hm = bfw.synthetic_transfusion_inputs(0, 12, 14)

@@ -231,7 +231,8 @@ def transfusion(p, shared, heatmap, proposals):
     c, h, w = sh.shape
     keys = h * w
     local = torch.zeros_like(hm)
-    local[:, :, 1:-1, 1:-1] = F.max_pool2d(hm, 3, 1, 0)
+    if h > 2 and w > 2:
+        local[:, :, 1:-1, 1:-1] = F.max_pool2d(hm, 3, 1, 0)
     local[:, 8], local[:, 9] = hm[:, 8], hm[:, 9]
     hm = hm * (hm == local)
     flat = hm[0].reshape(-1)
