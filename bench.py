@@ -67,6 +67,7 @@ def parse():
                    help=argparse.SUPPRESS)  # internal: the program rocprofv3 profiles
     p.add_argument("--no-lss", action="store_true", help="skip the LSS pooling leg")
     p.add_argument("--no-bev", action="store_true", help="skip the BEV stage leg")
+    p.add_argument("--no-tf", action="store_true", help="skip the TransFusion decoder leg")
     return p.parse_args()
 
 
@@ -503,6 +504,100 @@ def bev_cpu_baseline(path, seed=0):
             "reference_readme_ms": BEV_REFERENCE["cpu_ms"], "cpu_model": _cpu_model()}
 
 
+TF_HW, TF_PROPOSALS = 180, 200
+# Reference TransFusion decoder on the RTX 4060 Ti, promoted 8-query tile
+# flash attention, warm median of 5 processes (benchmark.csv:7).
+TF_REFERENCE_MS = 17.164
+
+
+def tf_flops(h=TF_HW, w=TF_HW, p=TF_PROPOSALS):
+    """Algorithmic FLOPs of one decoder forward: key-side position head and
+    K/V projections, cross attention (QK^T and PV), and the per-proposal
+    dense layers and self attention."""
+    keys, c = h * w, 128
+    key_side = 2.0 * keys * c * (c + 2 * c)
+    cross = 2.0 * 2 * p * keys * c
+    rows = 2.0 * p * c * (c + 3 * c + c + c + c + 2 * c + 2 * c + 3 * c) + 2.0 * p * 20 * 64
+    self_attn = 2.0 * 2 * p * p * c
+    return key_side + cross + rows + self_attn, cross
+
+
+def tf_leg(dev, reps, seed=0):
+    """TransFusion decoder at 180x180 with 200 proposals: ms per forward
+    (graph replay and eager), TFLOP/s against the MFMA roof."""
+    import torch
+    import bfhip
+    from bfhip import bfw
+    tmp = pathlib.Path(tempfile.mkdtemp(prefix="tf_"))
+    path = bfw.write_transfusion(tmp / "tf.bfw", seed=seed, mode="baseline")
+    sh, hm = (torch.from_numpy(a).to(dev) for a in bfw.synthetic_transfusion_inputs(seed, TF_HW, TF_HW))
+    stream = torch.cuda.Stream()
+    with bfhip.Model(path) as m:
+        dec = bfhip.TransFusion(m, TF_HW, TF_HW, TF_PROPOSALS)
+    with torch.cuda.stream(stream):
+        outs = dec.forward(sh, hm, stream=stream)
+        for _ in range(3):
+            dec.forward(sh, hm, outs, stream=stream)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(reps):
+            dec.forward(sh, hm, outs, stream=stream)
+        b.record(stream)
+        b.synchronize()
+        eager_ms = a.elapsed_time(b) / reps
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            dec.forward(sh, hm, outs, stream=stream)
+        graph.replay()
+        a.record(stream)
+        for _ in range(reps):
+            graph.replay()
+        b.record(stream)
+        b.synchronize()
+        ms = a.elapsed_time(b) / reps
+        dets = dec.decode(outs, 0.1, stream=stream)
+    flops, cross = tf_flops()
+    tflops = flops / (ms * 1e-3) / 1e12
+    keys = TF_HW * TF_HW
+    out = {"workload": "TransFusion decoder (NMS + top-200 proposals, self/cross attention, FFN, "
+                       "six heads), 180 x 180 BEV map, random-init weights N(0,0.02); fp16 MFMA "
+                       "operands on the key side and cross attention, fp32 elsewhere",
+           "ms": round(ms, 4), "ms_eager": round(eager_ms, 4), "gflop": round(flops / 1e9, 2),
+           "tflops": round(tflops, 1), "reference_rtx4060ti_ms": TF_REFERENCE_MS,
+           "speedup_vs_reference": round(TF_REFERENCE_MS / ms, 1),
+           "detections_at_0.1": dets.count,
+           "resident_mib": round(dec.resident_bytes() / 2**20, 1),
+           "roofline": {"kernel": "transfusion forward", "bound": "mfma",
+                        "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
+                        "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+                        "traffic": None,
+                        "note": "dense fp16 MFMA peak; the cross attention's "
+                                f"{8 * TF_PROPOSALS * keys / 1e6:.1f} M exponentials bound it "
+                                "first (v_exp_f32 at a quarter of the VALU rate: ~5 us)"}}
+    dec.close()
+    return out, path
+
+
+def tf_cpu_baseline(path, seed=0):
+    """The reference's CPU TransFusion decoder (oracle/_ref: src/transfusion.c
+    + src/transfusion_decoder.c, OpenMP) on the full 180x180 / 200-proposal
+    workload."""
+    import oracle
+    from bfhip import bfw
+    kind = "reference" if oracle.available("ref") else "port"
+    o = oracle.Oracle("ref" if kind == "reference" else "port")
+    sh, hm = bfw.synthetic_transfusion_inputs(seed, TF_HW, TF_HW)
+    with o.open_model(path) as m:
+        o.transfusion(m, sh, hm, TF_PROPOSALS)
+        t0 = time.perf_counter()
+        o.transfusion(m, sh, hm, TF_PROPOSALS)
+        t1 = time.perf_counter()
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or os.cpu_count()
+    return {"value": round((t1 - t0) * 1e3, 1), "unit": "ms/forward", "cores": threads,
+            "kind": kind, "backend": o.backend(), "sample": "full 180x180 map, 200 proposals",
+            "cpu_model": _cpu_model()}
+
+
 def cpu_baseline(model_path, cameras):
     """Reference CPU path (oracle/_ref, the reference's C compiled from its own
     sources, OpenMP) on a bounded sample of `cameras` cameras, scaled to a
@@ -657,6 +752,11 @@ def main():
         if not args.no_cpu:
             bev["cpu_baseline"] = bev_cpu_baseline(bev_path)
         result["bev_stage"] = bev
+    if not args.no_tf:
+        tf, tf_path = tf_leg(dev, max(args.steps, 20))
+        if not args.no_cpu:
+            tf["cpu_baseline"] = tf_cpu_baseline(tf_path)
+        result["transfusion"] = tf
     print(json.dumps(result))
 
 

@@ -5,13 +5,26 @@
 //
 // Work split by shape (P <= 200 proposals, K = H * W keys, C = 128 channels,
 // 8 heads of 16):
-//   suppress_kernel   sigmoid + 3x3 NMS over the 10 x K heatmap; writes the
-//                     suppressed scores and one unique 64-bit sort key per
-//                     candidate (score bits << 32 | ~flat), so descending key
-//                     order is the reference's (score desc, flat asc) order.
-//   topk_kernel       exact top-256 of each 8192-candidate chunk by an LDS
-//                     bitonic sort, repeated over the chunk winners until one
-//                     chunk remains: deterministic, no atomics, no memsets.
+//   suppress_kernel   sigmoid + 3x3 NMS over the 10 x K heatmap, one 32 x 32
+//                     tile per workgroup with the logistic evaluated once per
+//                     cell into LDS; writes the suppressed scores and one
+//                     unique 64-bit sort key per candidate (score bits << 32 |
+//                     ~flat), so descending key order is the reference's
+//                     (score desc, flat asc) order, and counts the keys' top
+//                     11 bits for the selection below.
+//   top-P selection   exact radix select of the P-th largest key over
+//                     11/10-bit digits, with no atomics between workgroups:
+//                     suppress stores a per-tile histogram of the keys' top
+//                     digit, hist_reduce_kernel sums them, compact_kernel
+//                     picks the top digit and gathers the keys at or above it
+//                     into per-workgroup segments (a few thousand keys at
+//                     production scale), and finish_kernel (one workgroup)
+//                     pulls the segments into LDS, refines the remaining
+//                     digits, keeps the P winners and sorts them (256-slot
+//                     bitonic).  Every buffer is rewritten each forward
+//                     (nothing to reset, no memsets: graph-capturable);
+//                     integer histograms and a sort of unique keys make it
+//                     deterministic.
 //   key_kernel        the K-row side on the matrix cores, one 64-key tile per
 //                     workgroup: cell-centre position head (2 -> 128, BN,
 //                     ReLU, 128 -> 128) + shared -> key_value, then the K and
@@ -47,7 +60,10 @@ namespace {
 
 constexpr int kC = 128, kHeads = 8, kHeadC = 16, kClasses = 10;
 constexpr int kQTiles = 13, kPPad = kQTiles * 16;  // >= BF_MAX_PROPOSALS
-constexpr int kTopSlots = 256, kChunk = 8192;
+constexpr int kTopSlots = 256;
+constexpr int kDigitBins = 2048, kLevels = 6;
+constexpr int kMaxSegments = 4096, kLdsKeys = 8192;
+constexpr int kNmsTile = 32, kNmsHalo = kNmsTile + 2;
 constexpr int kKeyTile = 64, kLdsRow = kC + 8;      // fp16 LDS row: 272 B, conflict-free
 constexpr int kStepKeys = 64, kWaves = 4;
 constexpr int kMaxSplits = 128;
@@ -102,83 +118,298 @@ __device__ __forceinline__ float logistic(float v) {
     return e / (1.0f + e);
 }
 
+// Digit of pass `level`: bits [shift, shift + width) of the key, most
+// significant first (11 + 11 + 10 bits of score, then of ~flat).
+__device__ __forceinline__ int digit_shift(int level) {
+    return level == 0 ? 53 : level == 1 ? 42 : level == 2 ? 32 : level == 3 ? 21 : level == 4 ? 10 : 0;
+}
+__device__ __forceinline__ int digit_width(int level) { return level == 2 || level == 5 ? 10 : 11; }
+
+// Finds the digit of a 2048-bin histogram that holds the k-th largest key
+// (1 <= k <= total): res[0] = digit, res[1] = keys with a larger digit,
+// res[2] = the digit's count.  T threads scan 2048 / T bins each; the suffix
+// sums run in-wave by shuffles, `wsum` (T / 64 words of LDS) joins the waves.
+// Every thread must call it; ends on a barrier.
+template <int T>
+__device__ void pick_digit(const unsigned *hist, unsigned k, unsigned *wsum, unsigned *res) {
+    constexpr int B = kDigitBins / T;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    unsigned h[B], sum = 0;
+#pragma unroll
+    for (int j = 0; j < B; ++j) {
+        h[j] = hist[B * t + j];
+        sum += h[j];
+    }
+    unsigned v = sum;  // becomes the sum over lanes >= lane of this wave
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const unsigned u = __shfl_down(v, o);
+        if (lane + o < 64) v += u;
+    }
+    if (lane == 0) wsum[wave] = v;
+    __syncthreads();
+    unsigned above = v - sum;
+    for (int w2 = wave + 1; w2 < T / 64; ++w2) above += wsum[w2];
+#pragma unroll
+    for (int j = B - 1; j >= 0; --j) {
+        if (above < k && k <= above + h[j]) {
+            res[0] = B * t + j;
+            res[1] = above;
+            res[2] = h[j];
+        }
+        above += h[j];
+    }
+    __syncthreads();
+}
+
 // Reference transfusion.c:75-132 / cuda_transfusion.cu:164-170: classes 8 and
-// 9 bypass NMS, border cells of the other classes are suppressed.
+// 9 bypass NMS, border cells of the other classes are suppressed.  One
+// workgroup per 32 x 32 tile of one class; the tile's histogram of key top
+// digits is stored whole at part_hist[tile][2048].
 __global__ __launch_bounds__(256) void suppress_kernel(const float *__restrict__ logits,
                                                        float *__restrict__ suppressed,
                                                        uint64_t *__restrict__ sort_keys, int h,
-                                                       int w, unsigned keys) {
-    const unsigned f = blockIdx.x * 256u + threadIdx.x;
-    if (f >= 10u * keys) return;
-    const unsigned cls = f / keys, pos = f - cls * keys;
-    const int y = (int)(pos / (unsigned)w), x = (int)pos - y * w;
-    const float v = logistic(logits[f]);
-    bool keep = cls == 8 || cls == 9;
-    if (!keep && y > 0 && x > 0 && y + 1 < h && x + 1 < w) {
-        const float *plane = logits + (size_t)cls * keys;
-        float m = -FLT_MAX;
-        for (int ky = -1; ky <= 1; ++ky)
-            for (int kx = -1; kx <= 1; ++kx) {
-                const float q = logistic(plane[(y + ky) * w + x + kx]);
-                if (q > m) m = q;
-            }
-        keep = v == m;
+                                                       int w, unsigned keys, int tiles_x,
+                                                       int tiles_y, unsigned *__restrict__ part_hist) {
+    __shared__ float sig[kNmsHalo * kNmsHalo];
+    __shared__ unsigned lh[kDigitBins];
+    const int t = threadIdx.x, lane = t & 63;
+    const int tile = blockIdx.x, cls = tile / (tiles_x * tiles_y);
+    const int ty = (tile / tiles_x) % tiles_y, tx = tile % tiles_x;
+    const int y0 = ty * kNmsTile, x0 = tx * kNmsTile;
+    const float *plane = logits + (size_t)cls * keys;
+    for (int i = t; i < kNmsHalo * kNmsHalo; i += 256) {
+        const int yy = y0 - 1 + i / kNmsHalo, xx = x0 - 1 + i % kNmsHalo;
+        sig[i] = yy >= 0 && yy < h && xx >= 0 && xx < w ? logistic(plane[yy * w + xx]) : 0.0f;
     }
-    const float out = keep ? v : 0.0f;
-    suppressed[f] = out;
-    const uint32_t bits = out != out ? 0x7fc00000u : __float_as_uint(out);
-    sort_keys[f] = ((uint64_t)bits << 32) | (uint32_t)(0xffffffffu - f);
+    for (int d = t; d < kDigitBins; d += 256) lh[d] = 0u;
+    __syncthreads();
+    const bool exempt = cls == 8 || cls == 9;
+#pragma unroll
+    for (int j = 0; j < kNmsTile * kNmsTile / 256; ++j) {
+        const int o = t + 256 * j, oy = o / kNmsTile, ox = o % kNmsTile;
+        const int y = y0 + oy, x = x0 + ox;
+        const bool inside = y < h && x < w;
+        unsigned digit = 0;
+        if (inside) {
+            const float *c = &sig[(oy + 1) * kNmsHalo + ox + 1];
+            const float v = c[0];
+            bool keep = exempt;
+            if (!keep && y > 0 && x > 0 && y + 1 < h && x + 1 < w) {
+                float m = -FLT_MAX;
+                for (int ky = -1; ky <= 1; ++ky)
+                    for (int kx = -1; kx <= 1; ++kx) {
+                        const float q = c[ky * kNmsHalo + kx];
+                        if (q > m) m = q;
+                    }
+                keep = v == m;
+            }
+            const float out = keep ? v : 0.0f;
+            const unsigned f = (unsigned)cls * keys + (unsigned)(y * w + x);
+            suppressed[f] = out;
+            const uint32_t bits = out != out ? 0x7fc00000u : __float_as_uint(out);
+            const uint64_t key = ((uint64_t)bits << 32) | (uint32_t)(0xffffffffu - f);
+            sort_keys[f] = key;
+            digit = (unsigned)(key >> 53);
+        }
+        // Suppressed cells (digit 0) dominate: one LDS atomic per wave for them.
+        const uint64_t zero = __ballot(inside && digit == 0);
+        if (lane == 0 && zero) atomicAdd(&lh[0], (unsigned)__popcll(zero));
+        if (inside && digit) atomicAdd(&lh[digit], 1u);
+    }
+    __syncthreads();
+    unsigned *dst = part_hist + (size_t)tile * kDigitBins;
+    for (int d = t; d < kDigitBins; d += 256) dst[d] = lh[d];
 }
 
-// Top 256 keys (descending) of each kChunk-key chunk: LDS bitonic sort of
-// `sort_n` (a power of two, 256..8192) slots, zero-padded (zero is below
-// every real key, whose low word ~flat is never 0 for flat < 2^32 - 1).
-__global__ __launch_bounds__(1024) void topk_kernel(const uint64_t *__restrict__ in, int n,
-                                                    int sort_n, uint64_t *__restrict__ out) {
-    __shared__ uint64_t s[kChunk];
-    const int t = threadIdx.x;
-    const int base = blockIdx.x * kChunk, count = min(kChunk, n - base);
-    for (int i = t; i < sort_n; i += 1024) s[i] = i < count ? in[base + i] : 0ull;
+// hist[d] = sum over tiles of part_hist[tile][d]: workgroup b owns bins
+// 8b .. 8b+7, its 32 thread slices stride over the tiles.
+__global__ __launch_bounds__(256) void hist_reduce_kernel(const unsigned *__restrict__ part_hist,
+                                                          int tiles, unsigned *__restrict__ hist) {
+    __shared__ unsigned red[256];
+    const int t = threadIdx.x, d = blockIdx.x * 8 + (t & 7);
+    unsigned sum = 0;
+#pragma unroll 4
+    for (int p = t >> 3; p < tiles; p += 32) sum += part_hist[(size_t)p * kDigitBins + d];
+    red[t] = sum;
     __syncthreads();
-    for (int k = 2; k <= sort_n; k <<= 1)
-        for (int j = k >> 1; j > 0; j >>= 1) {
-            for (int i = t; i < sort_n / 2; i += 1024) {
-                const int a = ((i & ~(j - 1)) << 1) | (i & (j - 1)), b = a + j;
-                const bool desc = (a & k) == 0;
-                const uint64_t x = s[a], y = s[b];
-                if ((x < y) == desc) {
-                    s[a] = y;
-                    s[b] = x;
-                }
-            }
-            __syncthreads();
+    if (t < 8) {
+        unsigned total = 0;
+        for (int i = 0; i < 32; ++i) total += red[8 * i + t];
+        hist[blockIdx.x * 8 + t] = total;
+    }
+}
+
+// Picks the top digit of the P-th largest key and gathers every key whose
+// top digit is >= it: workgroup g appends (LDS counter) into
+// list[g * chunk ...] and stores its count in counts[g].
+__global__ __launch_bounds__(256) void compact_kernel(const uint64_t *__restrict__ keys, unsigned n,
+                                                      unsigned chunk, const unsigned *__restrict__ hist,
+                                                      int P, uint64_t *__restrict__ list,
+                                                      unsigned *__restrict__ counts) {
+    __shared__ unsigned wsum[4], res[3], taken;
+    pick_digit<256>(hist, (unsigned)P, wsum, res);
+    const unsigned long long threshold = (unsigned long long)res[0] << digit_shift(0);
+    const int t = threadIdx.x, lane = t & 63;
+    if (t == 0) taken = 0u;
+    __syncthreads();
+    const unsigned begin = blockIdx.x * chunk, end = min(begin + chunk, n);
+    for (unsigned base = begin + (t & ~63u); base < end; base += 256u) {
+        const unsigned i = base + lane;
+        const uint64_t key = i < end ? keys[i] : 0ull;
+        const bool take = i < end && key >= threshold;
+        const uint64_t b = __ballot(take);
+        if (!b) continue;
+        unsigned first = 0;
+        if (lane == 0) first = atomicAdd(&taken, (unsigned)__popcll(b));
+        first = __shfl(first, 0);
+        if (take) list[begin + first + __popcll(b & ((1ull << lane) - 1ull))] = key;
+    }
+    __syncthreads();
+    if (t == 0) counts[blockIdx.x] = taken;
+}
+
+// One workgroup: lines the gathered segments up (LDS when they fit, else read
+// in place), refines the remaining digits of the threshold, keeps the P keys
+// >= it and sorts them descending into `top`.
+__global__ __launch_bounds__(1024) void finish_kernel(const uint64_t *__restrict__ list,
+                                                      const unsigned *__restrict__ counts,
+                                                      int segments, unsigned chunk,
+                                                      const unsigned *__restrict__ hist, int P,
+                                                      uint64_t *__restrict__ top) {
+    __shared__ unsigned lh[kDigitBins], wsum[16], res[3], off[kMaxSegments + 1], count;
+    __shared__ uint64_t lk[kLdsKeys];
+    __shared__ uint64_t s[kTopSlots];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    pick_digit<1024>(hist, (unsigned)P, wsum, res);
+    unsigned long long prefix = (unsigned long long)res[0] << digit_shift(0);
+    unsigned k = (unsigned)P - res[1];
+    bool resolved = res[2] == k;
+    // Exclusive scan of the segment counts, four segments per thread.
+    unsigned c[4], sum = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int g = 4 * t + j;
+        c[j] = g < segments ? counts[g] : 0u;
+        sum += c[j];
+    }
+    unsigned v = sum;  // inclusive prefix within the wave
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const unsigned u = __shfl_up(v, o);
+        if (lane >= o) v += u;
+    }
+    if (lane == 63) wsum[wave] = v;
+    __syncthreads();
+    unsigned before = v - sum;
+    for (int w2 = 0; w2 < wave; ++w2) before += wsum[w2];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        if (4 * t + j <= segments) off[4 * t + j] = before;
+        before += c[j];
+    }
+    __syncthreads();
+    const unsigned m = off[segments];
+    const bool in_lds = m <= (unsigned)kLdsKeys;
+    // Global position of the j-th gathered key.
+    auto locate = [&](unsigned j) {
+        int lo = 0, hi = segments - 1;  // last segment with off <= j
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (off[mid] <= j) lo = mid;
+            else hi = mid - 1;
         }
-    for (int i = t; i < kTopSlots; i += 1024) out[blockIdx.x * kTopSlots + i] = s[i];
+        return (size_t)lo * chunk + (j - off[lo]);
+    };
+    if (in_lds) {
+        // Eight loads in flight per thread.
+        for (unsigned j0 = t; j0 < m; j0 += 8 * 1024) {
+            uint64_t v8[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const unsigned j = j0 + 1024u * u;
+                v8[u] = j < m ? list[locate(j)] : 0ull;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const unsigned j = j0 + 1024u * u;
+                if (j < m) lk[j] = v8[u];
+            }
+        }
+        __syncthreads();
+    }
+    auto key_at = [&](unsigned j) { return in_lds ? lk[j] : list[locate(j)]; };
+    for (int level = 1; level < kLevels && !resolved; ++level) {
+        const int shift = digit_shift(level), hi = shift + digit_width(level);
+        const unsigned mask = (1u << digit_width(level)) - 1u;
+        const unsigned long long group = prefix >> hi;
+        for (int d = t; d < kDigitBins; d += 1024) lh[d] = 0u;
+        __syncthreads();
+        for (unsigned j = t; j < m; j += 1024) {
+            const uint64_t key = key_at(j);
+            if ((key >> hi) == group) atomicAdd(&lh[(unsigned)(key >> shift) & mask], 1u);
+        }
+        __syncthreads();
+        pick_digit<1024>(lh, k, wsum, res);
+        prefix |= (unsigned long long)res[0] << shift;
+        k -= res[1];
+        resolved = res[2] == k || level == kLevels - 1;
+    }
+    if (t == 0) count = 0u;
+    __syncthreads();
+    for (unsigned j = t; j < m; j += 1024) {
+        const uint64_t key = key_at(j);
+        if (key >= prefix) {
+            const unsigned slot = atomicAdd(&count, 1u);
+            if (slot < kTopSlots) s[slot] = key;  // exactly P keys by construction
+        }
+    }
+    __syncthreads();
+    // Descending order by rank (keys are unique): four threads per key count
+    // the larger keys among a quarter of the P each.
+    const int i = t >> 2, part = t & 3, quarter = (P + 3) / 4;
+    const uint64_t mine = i < P ? s[i] : 0ull;
+    unsigned rank = 0;
+    for (int j = part * quarter; j < min(P, (part + 1) * quarter); ++j) rank += s[j] > mine;
+    rank += __shfl_xor(rank, 1);
+    rank += __shfl_xor(rank, 2);
+    if (i < P && part == 0) top[rank] = mine;
 }
 
 // ------------------------------------------------ per-proposal fp32 helpers
-// y[n] = b[n] + sum_k x[k] wt[k][n] for one row; x in LDS, wt [K][N].  N = 128
-// splits K over the two halves of the 256 threads; results land in y (LDS)
-// and are visible after the caller's barrier.
+// y[n] = b[n] + sum_k x[k] wt[k][n] for one row; x in LDS, wt [K][N] fp32.
+// Thread t owns four adjacent columns (one float4 of each wt row) over one of
+// S k-slices, so a thread keeps its K / S loads in flight at once; the slices
+// meet in `red` (S * N floats of LDS).  Results land in y (LDS) and are
+// visible after the caller's barrier.
 template <int K, int N>
 __device__ __forceinline__ void row_linear(const float *x, const float *__restrict__ wt,
                                            const float *__restrict__ b, float *y, float *red) {
+    constexpr int G = N / 4, S = 256 / G, KS = K / S;
+    static_assert(N % 4 == 0 && G <= 256 && K % S == 0, "row_linear shape");
     const int t = threadIdx.x;
-    if constexpr (N == 128) {
-        const int n = t & 127, k0 = (t >> 7) * (K / 2);
-        float a = 0.0f;
-#pragma unroll 8
-        for (int k = 0; k < K / 2; ++k) a = fmaf(x[k0 + k], wt[(size_t)(k0 + k) * N + n], a);
-        red[t] = a;
-        __syncthreads();
-        if (t < 128) y[t] = (b ? b[t] : 0.0f) + red[t] + red[t + 128];
-    } else {
-        for (int n = t; n < N; n += 256) {
-            float a = 0.0f;
-#pragma unroll 8
-            for (int k = 0; k < K; ++k) a = fmaf(x[k], wt[(size_t)k * N + n], a);
-            y[n] = (b ? b[n] : 0.0f) + a;
+    if (t < G * S) {
+        const int c4 = t % G, sl = t / G;
+        const float4 *w4 = reinterpret_cast<const float4 *>(wt) + (size_t)sl * KS * G + c4;
+        const float *xs = x + sl * KS;
+        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll 16
+        for (int k = 0; k < KS; ++k) {
+            const float4 w = w4[(size_t)k * G];
+            const float xv = xs[k];
+            acc.x = fmaf(xv, w.x, acc.x);
+            acc.y = fmaf(xv, w.y, acc.y);
+            acc.z = fmaf(xv, w.z, acc.z);
+            acc.w = fmaf(xv, w.w, acc.w);
         }
+        *reinterpret_cast<float4 *>(&red[sl * N + 4 * c4]) = acc;
+    }
+    __syncthreads();
+    for (int n = t; n < N; n += 256) {
+        float a = b ? b[n] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < S; ++j) a += red[j * N + n];
+        y[n] = a;
     }
 }
 
@@ -216,7 +447,8 @@ __global__ __launch_bounds__(256) void query_kernel(
     const float *__restrict__ shared, unsigned keys, int width, int P, float *__restrict__ query,
     float *__restrict__ query_pos, float *__restrict__ qkv, int64_t *__restrict__ labels,
     int64_t *__restrict__ indices, float *__restrict__ query_scores) {
-    __shared__ float hid[kC], tmp[kC], pos[kC], out[3 * kC], red[256];
+    __shared__ float hid[kC], tmp[kC], pos[kC], out[3 * kC];
+    __shared__ __attribute__((aligned(16))) float red[1024];
     const int p = blockIdx.x, t = threadIdx.x;
     // Every one of the first P keys is a real candidate (P <= 10 H W at
     // create); the clamp only keeps a zero pad key from indexing outside.
@@ -251,40 +483,78 @@ __global__ __launch_bounds__(256) void query_kernel(
 // Self attention of one proposal over all P (transfusion_decoder.c:259-313:
 // scores / sqrt(16), max-shifted softmax), out projection, residual +
 // norm1, then the cross-attention query (query + query_pos) projected,
-// scaled by 0.25 log2(e) and stored fp16 for the matrix cores.
+// scaled by 0.25 log2(e) and stored fp16 for the matrix cores.  The 32 lanes
+// of a head take keys l, l + 32, ...; each lane keeps its keys' 16-wide K
+// and V rows in flight together.
 __global__ __launch_bounds__(256) void self_attention_kernel(
     Params prm, const float *__restrict__ qkv, int P, float *__restrict__ query,
     const float *__restrict__ query_pos, _Float16 *__restrict__ cross_q) {
-    __shared__ float q[kC], att[kC], upd[kC], x[kC], red[256], stat[4];
-    __shared__ float prob[kHeads][BF_MAX_PROPOSALS];
+    constexpr int kPerLane = (BF_MAX_PROPOSALS + 31) / 32;
+    __shared__ __attribute__((aligned(16))) float q[kC];
+    __shared__ float att[kC], upd[kC], x[kC], stat[4];
+    __shared__ __attribute__((aligned(16))) float red[1024];
+    __shared__ float part[kHeads][32][kHeadC + 1];
     const int p = blockIdx.x, t = threadIdx.x;
     const float *qs = qkv, *ks = qkv + (size_t)P * kC, *vs = qkv + (size_t)2 * P * kC;
     if (t < kC) q[t] = qs[p * kC + t];
     __syncthreads();
     const int h = t >> 5, l = t & 31;
-    float m = -FLT_MAX;
-    for (int k = l; k < P; k += 32) {
-        const float *kr = ks + (size_t)k * kC + h * kHeadC;
-        float dot = 0.0f;
+    float4 qh[4];
 #pragma unroll
-        for (int d = 0; d < kHeadC; ++d) dot = fmaf(q[h * kHeadC + d], kr[d], dot);
-        dot *= 0.25f;
-        prob[h][k] = dot;
-        m = fmaxf(m, dot);
+    for (int i = 0; i < 4; ++i) qh[i] = reinterpret_cast<const float4 *>(q + h * kHeadC)[i];
+    float sc[kPerLane];
+    float m = -FLT_MAX;
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j) {
+        const int k = l + 32 * j;
+        float dot = 0.0f;
+        if (k < P) {
+            const float4 *kr = reinterpret_cast<const float4 *>(ks + (size_t)k * kC + h * kHeadC);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float4 kv = kr[i];
+                dot = fmaf(qh[i].x, kv.x, dot);
+                dot = fmaf(qh[i].y, kv.y, dot);
+                dot = fmaf(qh[i].z, kv.z, dot);
+                dot = fmaf(qh[i].w, kv.w, dot);
+            }
+            dot *= 0.25f;
+            m = fmaxf(m, dot);
+        }
+        sc[j] = dot;
     }
     m = group_max<32>(m);
     float sum = 0.0f;
-    for (int k = l; k < P; k += 32) {
-        const float e = expf(prob[h][k] - m);
-        prob[h][k] = e;
-        sum += e;
+    float acc[kHeadC];
+#pragma unroll
+    for (int d = 0; d < kHeadC; ++d) acc[d] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j) {
+        const int k = l + 32 * j;
+        if (k < P) {
+            const float e = expf(sc[j] - m);
+            sum += e;
+            const float4 *vr = reinterpret_cast<const float4 *>(vs + (size_t)k * kC + h * kHeadC);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float4 vv = vr[i];
+                acc[4 * i] = fmaf(e, vv.x, acc[4 * i]);
+                acc[4 * i + 1] = fmaf(e, vv.y, acc[4 * i + 1]);
+                acc[4 * i + 2] = fmaf(e, vv.z, acc[4 * i + 2]);
+                acc[4 * i + 3] = fmaf(e, vv.w, acc[4 * i + 3]);
+            }
+        }
     }
     sum = group_sum<32>(sum);
+#pragma unroll
+    for (int d = 0; d < kHeadC; ++d) part[h][l][d] = acc[d];
     __syncthreads();
     {
+        // Thread (h, d, half) adds 16 lanes' partials; the halves meet by shuffle.
         const int d = t & 15, half = (t >> 4) & 1;
         float a = 0.0f;
-        for (int k = half; k < P; k += 2) a = fmaf(prob[h][k], vs[(size_t)k * kC + h * kHeadC + d], a);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) a += part[h][16 * half + i][d];
         a += __shfl_xor(a, 16, 32);
         if (!half) att[h * kHeadC + d] = a / sum;
     }
@@ -563,7 +833,8 @@ __global__ __launch_bounds__(256) void tail_kernel(
     const float *__restrict__ query, const int64_t *__restrict__ indices,
     bf_transfusion_raw_outputs out) {
     __shared__ float ws[kHeads][kMaxSplits], lh[kHeads];
-    __shared__ float att[kC], upd[kC], x[kC], ffn[2 * kC], hid[3 * kC], red[256], stat[4];
+    __shared__ float att[kC], upd[kC], x[kC], ffn[2 * kC], hid[3 * kC], stat[4];
+    __shared__ __attribute__((aligned(16))) float red[1024];
     const int p = blockIdx.x, t = threadIdx.x, h = t >> 5, l32 = t & 31;
     {
         float mm = kNegBig;
@@ -583,6 +854,7 @@ __global__ __launch_bounds__(256) void tail_kernel(
     {
         const int d = t & 15, half = (t >> 4) & 1;
         float a = 0.0f;
+#pragma unroll 8
         for (int s = half; s < splits; s += 2)
             a = fmaf(part_o[(((size_t)s * kHeads + h) * kPPad + p) * kHeadC + d], ws[h][s], a);
         a += __shfl_xor(a, 16, 32);
@@ -671,22 +943,18 @@ __global__ __launch_bounds__(256) void decode_kernel(bf_transfusion_raw_outputs 
     if (p == 0) out->count = wave_count[0] + wave_count[1] + wave_count[2] + wave_count[3];
 }
 
-struct TopPass {
-    int n, chunks, sort_n;
-};
-
 }  // namespace
 
 struct bf_cuda_transfusion {
     size_t height, width, keys, proposals, resident_bytes;
-    int keys64, steps_per_wave, splits;
-    std::vector<TopPass> passes;
+    int keys64, steps_per_wave, splits, nms_tiles_x, nms_tiles_y, segments;
+    unsigned chunk;
     unsigned char *params, *arena;
     Params prm;
     // Views into the arena.
     float *suppressed, *query, *query_pos, *qkv, *part_m, *part_l, *part_o;
-    uint64_t *sort_keys, *tops[2];
-    const uint64_t *final_top;
+    uint64_t *sort_keys, *selected, *top;
+    unsigned *part_hist, *hist, *counts;
     _Float16 *cross_q, *kh, *vt;
     bf_detections *detections;
 };
@@ -888,16 +1156,15 @@ int build_params(bf_cuda_transfusion *d, const bf_model *m, char *error, size_t 
 int build_work(bf_cuda_transfusion *d, char *error, size_t cap) {
     const size_t keys = d->keys, P = d->proposals, cand = 10 * keys;
     d->keys64 = (int)((keys + kKeyTile - 1) / kKeyTile * kKeyTile);
-    // Top-k passes: chunks of kChunk candidates keep kTopSlots each, until one
-    // chunk remains.
-    for (size_t n = cand;;) {
-        const size_t chunks = (n + kChunk - 1) / kChunk;
-        int sort_n = kTopSlots;
-        while ((size_t)sort_n < std::min(n, (size_t)kChunk)) sort_n <<= 1;
-        d->passes.push_back({(int)n, (int)chunks, sort_n});
-        if (chunks == 1) break;
-        n = chunks * kTopSlots;
-    }
+    // NMS tiles, and compaction segments of >= 2048 keys, fewer than
+    // kMaxSegments (the finish scan also stores the total at off[segments]).
+    d->nms_tiles_x = (int)((d->width + kNmsTile - 1) / kNmsTile);
+    d->nms_tiles_y = (int)((d->height + kNmsTile - 1) / kNmsTile);
+    const size_t tiles = (size_t)kClasses * d->nms_tiles_x * d->nms_tiles_y;
+    size_t chunk = std::max<size_t>(2048, (cand + kMaxSegments - 2) / (kMaxSegments - 1));
+    chunk = (chunk + 255) / 256 * 256;
+    d->chunk = (unsigned)chunk;
+    d->segments = (int)((cand + chunk - 1) / chunk);
     // Key splits: about 512 workgroups (two per CU) over 8 heads, at most
     // kMaxSplits splits.
     const int steps = d->keys64 / kStepKeys;
@@ -912,9 +1179,10 @@ int build_work(bf_cuda_transfusion *d, char *error, size_t cap) {
         off += (bytes + 255) & ~size_t(255);
         return at;
     };
-    const size_t chunks0 = d->passes[0].chunks;
     const size_t o_supp = take(cand * 4), o_keys = take(cand * 8);
-    const size_t o_top0 = take(chunks0 * kTopSlots * 8), o_top1 = take(chunks0 * kTopSlots * 8);
+    const size_t o_part = take(tiles * kDigitBins * 4), o_hist = take(kDigitBins * 4);
+    const size_t o_counts = take((size_t)d->segments * 4), o_list = take(cand * 8),
+                 o_top = take(kTopSlots * 8);
     const size_t o_query = take(P * kC * 4), o_pos = take(P * kC * 4), o_qkv = take(3 * P * kC * 4);
     const size_t o_cq = take((size_t)kPPad * kC * 2);
     const size_t o_kh = take((size_t)d->keys64 * kC * 2), o_vt = take((size_t)d->keys64 * kC * 2);
@@ -928,8 +1196,11 @@ int build_work(bf_cuda_transfusion *d, char *error, size_t cap) {
     unsigned char *a = d->arena;
     d->suppressed = (float *)(a + o_supp);
     d->sort_keys = (uint64_t *)(a + o_keys);
-    d->tops[0] = (uint64_t *)(a + o_top0);
-    d->tops[1] = (uint64_t *)(a + o_top1);
+    d->part_hist = (unsigned *)(a + o_part);
+    d->hist = (unsigned *)(a + o_hist);
+    d->counts = (unsigned *)(a + o_counts);
+    d->selected = (uint64_t *)(a + o_list);
+    d->top = (uint64_t *)(a + o_top);
     d->query = (float *)(a + o_query);
     d->query_pos = (float *)(a + o_pos);
     d->qkv = (float *)(a + o_qkv);
@@ -940,7 +1211,6 @@ int build_work(bf_cuda_transfusion *d, char *error, size_t cap) {
     d->part_l = (float *)(a + o_pl);
     d->part_o = (float *)(a + o_po);
     d->detections = (bf_detections *)(a + o_det);
-    d->final_top = d->tops[(d->passes.size() - 1) & 1];
     return 1;
 }
 
@@ -996,17 +1266,16 @@ extern "C" int bf_cuda_transfusion_forward(bf_cuda_transfusion *d, const float *
     const hipStream_t s = reinterpret_cast<hipStream_t>(stream_value);
     const unsigned keys = (unsigned)d->keys, cand = 10u * keys;
     const int P = (int)d->proposals, W = (int)d->width;
-    suppress_kernel<<<(cand + 255) / 256, 256, 0, s>>>(heatmap, d->suppressed, d->sort_keys,
-                                                      (int)d->height, W, keys);
+    const int tiles = kClasses * d->nms_tiles_x * d->nms_tiles_y;
+    suppress_kernel<<<tiles, 256, 0, s>>>(heatmap, d->suppressed, d->sort_keys, (int)d->height, W,
+                                          keys, d->nms_tiles_x, d->nms_tiles_y, d->part_hist);
     key_kernel<<<d->keys64 / kKeyTile, 256, 0, s>>>(d->prm, shared, keys, W, d->keys64, d->kh, d->vt);
-    const uint64_t *in = d->sort_keys;
-    for (size_t i = 0; i < d->passes.size(); ++i) {
-        const TopPass &tp = d->passes[i];
-        uint64_t *dst = d->tops[i & 1];
-        topk_kernel<<<tp.chunks, 1024, 0, s>>>(in, tp.n, tp.sort_n, dst);
-        in = dst;
-    }
-    query_kernel<<<P, 256, 0, s>>>(d->prm, d->final_top, d->suppressed, shared, keys, W, P,
+    hist_reduce_kernel<<<kDigitBins / 8, 256, 0, s>>>(d->part_hist, tiles, d->hist);
+    compact_kernel<<<d->segments, 256, 0, s>>>(d->sort_keys, cand, d->chunk, d->hist, P,
+                                               d->selected, d->counts);
+    finish_kernel<<<1, 1024, 0, s>>>(d->selected, d->counts, d->segments, d->chunk, d->hist, P,
+                                     d->top);
+    query_kernel<<<P, 256, 0, s>>>(d->prm, d->top, d->suppressed, shared, keys, W, P,
                                    d->query, d->query_pos, d->qkv, out->query_labels_bp,
                                    out->query_indices_bp, out->query_heatmap_scores_b10p);
     self_attention_kernel<<<P, 256, 0, s>>>(d->prm, d->qkv, P, d->query, d->query_pos, d->cross_q);
