@@ -699,30 +699,33 @@ __global__ __launch_bounds__(256) void key_kernel(Params prm, const float *__res
 }
 
 // --------------------------------------------------- cross attention (MFMA)
-// Workgroup (split s, head h); wave w takes steps s*4*spw + 4i + w.  Partial
-// results per (split, head, query): running max m (base 2), sum l and the
-// unnormalised 16-wide output.
+// Workgroup (split s, head h), four waves over the split's 64-key steps
+// s spw .. s spw + spw - 1; wave w owns query tiles [tile0(w), tile0(w + 1))
+// (4 + 3 + 3 + 3 of the 13).  Partial results per (split, head, query):
+// running max m (base 2), sum l and the unnormalised 16-wide output.
+constexpr int kTilesPerWave = 4;
+
+__device__ __forceinline__ int first_tile(int w) { return w == 0 ? 0 : 3 * w + 1; }
+
 __global__ __launch_bounds__(256) void cross_attention_kernel(
     const _Float16 *__restrict__ cross_q, const _Float16 *__restrict__ kh,
     const _Float16 *__restrict__ vt, int keys, int keys64, int steps_per_wave,
     float *__restrict__ part_m, float *__restrict__ part_l, float *__restrict__ part_o) {
-    __shared__ float wm[kWaves][kPPad], wl[kWaves][kPPad];
-    __shared__ float wo[kWaves][kPPad * kHeadC];
     const int s = blockIdx.x, h = blockIdx.y, t = threadIdx.x;
     const int w = t >> 6, lane = t & 63, col = lane & 15, g = lane >> 4;
+    const int tile0 = first_tile(w), ntiles = first_tile(w + 1) - tile0;
     const int total_steps = keys64 / kStepKeys;
 
-    h4 qf[kQTiles];
+    h4 qf[kTilesPerWave];
+    float m[kTilesPerWave], l[kTilesPerWave];
+    f32x4 o[kTilesPerWave];
 #pragma unroll
-    for (int qt = 0; qt < kQTiles; ++qt)
-        qf[qt] = *(const h4 *)&cross_q[(qt * 16 + col) * kC + h * kHeadC + 4 * g];
-    float m[kQTiles], l[kQTiles];
-    f32x4 o[kQTiles];
-#pragma unroll
-    for (int qt = 0; qt < kQTiles; ++qt) {
-        m[qt] = kNegBig;
-        l[qt] = 0.0f;
-        o[qt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = 0; i < kTilesPerWave; ++i) {
+        const int qt = min(tile0 + i, kQTiles - 1);
+        qf[i] = *(const h4 *)&cross_q[(qt * 16 + col) * kC + h * kHeadC + 4 * g];
+        m[i] = kNegBig;
+        l[i] = 0.0f;
+        o[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     }
     const _Float16 *kbase = kh + (size_t)h * keys64 * kHeadC;
     const _Float16 *vbase = vt + (size_t)h * kHeadC * keys64;
@@ -731,7 +734,7 @@ __global__ __launch_bounds__(256) void cross_attention_kernel(
     const int krow = 8 * (col >> 2) + (col & 3);
 
     for (int i = 0; i < steps_per_wave; ++i) {
-        const int step = (s * steps_per_wave + i) * kWaves + w;
+        const int step = s * steps_per_wave + i;
         if (step >= total_steps) break;
         const int k0 = step * kStepKeys;
         h4 kf[4];
@@ -745,11 +748,12 @@ __global__ __launch_bounds__(256) void cross_attention_kernel(
         }
         const bool partial = k0 + kStepKeys > keys;
 #pragma unroll
-        for (int qt = 0; qt < kQTiles; ++qt) {
+        for (int qi = 0; qi < kTilesPerWave; ++qi) {
+            if (qi >= ntiles) break;
             f32x4 sc[4];
 #pragma unroll
             for (int i4 = 0; i4 < 4; ++i4)
-                sc[i4] = mfma_16x16x16(kf[i4], qf[qt], f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+                sc[i4] = mfma_16x16x16(kf[i4], qf[qi], f32x4{0.0f, 0.0f, 0.0f, 0.0f});
             if (partial) {
 #pragma unroll
                 for (int a = 0; a < 2; ++a)
@@ -766,9 +770,9 @@ __global__ __launch_bounds__(256) void cross_attention_kernel(
                 for (int j = 0; j < 4; ++j) mx = fmaxf(mx, sc[i4][j]);
             mx = fmaxf(mx, __shfl_xor(mx, 16));
             mx = fmaxf(mx, __shfl_xor(mx, 32));
-            const float mn = fmaxf(m[qt], mx);
-            const float alpha = __builtin_amdgcn_exp2f(m[qt] - mn);
-            m[qt] = mn;
+            const float mn = fmaxf(m[qi], mx);
+            const float alpha = __builtin_amdgcn_exp2f(m[qi] - mn);
+            m[qi] = mn;
             float ps = 0.0f;
             h8 pf[2];
 #pragma unroll
@@ -781,43 +785,24 @@ __global__ __launch_bounds__(256) void cross_attention_kernel(
                         ps += e;
                         pf[a][4 * b + j] = (_Float16)e;
                     }
-            l[qt] = l[qt] * alpha + ps;
-            o[qt] *= alpha;
+            l[qi] = l[qi] * alpha + ps;
+            o[qi] *= alpha;
 #pragma unroll
-            for (int a = 0; a < 2; ++a) o[qt] = mfma_16x16x32(vf[a], pf[a], o[qt]);
+            for (int a = 0; a < 2; ++a) o[qi] = mfma_16x16x32(vf[a], pf[a], o[qi]);
         }
     }
-#pragma unroll
-    for (int qt = 0; qt < kQTiles; ++qt) {
-        float lt = l[qt] + __shfl_xor(l[qt], 16);
-        lt += __shfl_xor(lt, 32);
-        const int q = qt * 16 + col;
-        if (g == 0) {
-            wm[w][q] = m[qt];
-            wl[w][q] = lt;
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) wo[w][q * kHeadC + 4 * g + j] = o[qt][j];
-    }
-    __syncthreads();
     const size_t base = ((size_t)s * kHeads + h) * kPPad;
-    for (int e = t; e < kPPad * kHeadC; e += 256) {
-        const int q = e >> 4;
-        float mm = wm[0][q];
 #pragma unroll
-        for (int v = 1; v < kWaves; ++v) mm = fmaxf(mm, wm[v][q]);
-        float lsum = 0.0f, osum = 0.0f;
-#pragma unroll
-        for (int v = 0; v < kWaves; ++v) {
-            const float f = __builtin_amdgcn_exp2f(wm[v][q] - mm);
-            lsum += wl[v][q] * f;
-            osum += wo[v][e] * f;
+    for (int qi = 0; qi < kTilesPerWave; ++qi) {
+        if (qi >= ntiles) break;
+        float lt = l[qi] + __shfl_xor(l[qi], 16);
+        lt += __shfl_xor(lt, 32);
+        const int q = (tile0 + qi) * 16 + col;
+        if (g == 0) {
+            part_m[base + q] = m[qi];
+            part_l[base + q] = lt;
         }
-        part_o[base * kHeadC + e] = osum;
-        if ((e & 15) == 0) {
-            part_m[base + q] = mm;
-            part_l[base + q] = lsum;
-        }
+        *(f32x4 *)&part_o[(base + q) * kHeadC + 4 * g] = o[qi];
     }
 }
 
@@ -1165,13 +1150,13 @@ int build_work(bf_cuda_transfusion *d, char *error, size_t cap) {
     chunk = (chunk + 255) / 256 * 256;
     d->chunk = (unsigned)chunk;
     d->segments = (int)((cand + chunk - 1) / chunk);
-    // Key splits: about 512 workgroups (two per CU) over 8 heads, at most
-    // kMaxSplits splits.
+    // Key splits of steps_per_wave 64-key steps: about 512 workgroups (two
+    // per CU) over 8 heads, at most kMaxSplits splits.
     const int steps = d->keys64 / kStepKeys;
-    int spw = std::max(1, (steps + kWaves * 64 - 1) / (kWaves * 64));
-    spw = std::max(spw, (steps + kWaves * kMaxSplits - 1) / (kWaves * kMaxSplits));
+    int spw = std::max(1, (steps + 63) / 64);
+    spw = std::max(spw, (steps + kMaxSplits - 1) / kMaxSplits);
     d->steps_per_wave = spw;
-    d->splits = (steps + kWaves * spw - 1) / (kWaves * spw);
+    d->splits = (steps + spw - 1) / spw;
 
     size_t off = 0;
     auto take = [&](size_t bytes) {
