@@ -583,10 +583,12 @@ __global__ __launch_bounds__(256) void key_kernel(Params prm, const float *__res
                                                   _Float16 *__restrict__ vt) {
     __shared__ __attribute__((aligned(16))) _Float16 hid[kKeyTile * kLdsRow];
     __shared__ __attribute__((aligned(16))) _Float16 kv[kKeyTile * kLdsRow];
-    const int t = threadIdx.x, w = t >> 6, lane = t & 63, col = lane & 15, g = lane >> 4;
+    // The wave index is uniform: channel-indexed parameters load as scalars.
+    const int t = threadIdx.x, w = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int lane = t & 63, col = lane & 15, g = lane >> 4;
     const int key0 = blockIdx.x * kKeyTile;
     {
-        const int r = t & 63, c0 = (t >> 6) * 32;
+        const int r = lane, c0 = w * 32;
         const unsigned kk = (unsigned)(key0 + r);
         const float x = (float)(kk % (unsigned)width) + 0.5f, y = (float)(kk / (unsigned)width) + 0.5f;
 #pragma unroll
@@ -598,41 +600,53 @@ __global__ __launch_bounds__(256) void key_kernel(Params prm, const float *__res
         }
     }
     __syncthreads();
-    // key_value^T tile: rows = channels 32w .. 32w+31 (A = W2), columns = keys.
+    // key_value tile: rows = keys (A = hidden), columns = channels
+    // 32w .. 32w+31 (B = W2); a lane then holds four consecutive keys of one
+    // channel, so the channel-major `shared` rows load as 16-byte vectors.
     {
-        f32x4 acc[2][4];
+        f32x4 acc[4][2];
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt)
+        for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
-            for (int ct = 0; ct < 4; ++ct) acc[rt][ct] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int ct = 0; ct < 2; ++ct) acc[rt][ct] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int ks = 0; ks < kC / 32; ++ks) {
-            h8 a[2];
+            h8 b[2];
 #pragma unroll
-            for (int rt = 0; rt < 2; ++rt)
-                a[rt] = *(const h8 *)&prm.cross_pos_w2[(32 * w + 16 * rt + col) * kC + 32 * ks + 8 * g];
+            for (int ct = 0; ct < 2; ++ct)
+                b[ct] = *(const h8 *)&prm.cross_pos_w2[(32 * w + 16 * ct + col) * kC + 32 * ks + 8 * g];
 #pragma unroll
-            for (int ct = 0; ct < 4; ++ct) {
-                const h8 b = *(const h8 *)&hid[(16 * ct + col) * kLdsRow + 32 * ks + 8 * g];
+            for (int rt = 0; rt < 4; ++rt) {
+                const h8 a = *(const h8 *)&hid[(16 * rt + col) * kLdsRow + 32 * ks + 8 * g];
 #pragma unroll
-                for (int rt = 0; rt < 2; ++rt) acc[rt][ct] = mfma_16x16x32(a[rt], b, acc[rt][ct]);
+                for (int ct = 0; ct < 2; ++ct) acc[rt][ct] = mfma_16x16x32(a, b[ct], acc[rt][ct]);
             }
         }
+        const bool vec = (keys & 3u) == 0;
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt)
+        for (int ct = 0; ct < 2; ++ct) {
+            const int c = 32 * w + 16 * ct + col;
+            const float bias = prm.cross_pos_b2[c];
+            const float *row = shared + (size_t)c * keys;
 #pragma unroll
-            for (int ct = 0; ct < 4; ++ct) {
-                const unsigned kk = (unsigned)(key0 + 16 * ct + col);
-                const int c0 = 32 * w + 16 * rt + 4 * g;
-                h4 o;
+            for (int rt = 0; rt < 4; ++rt) {
+                const unsigned k0 = (unsigned)(key0 + 16 * rt + 4 * g);
+                float sv[4];
+                if (vec && k0 + 4 <= keys) {
+                    const float4 v = *reinterpret_cast<const float4 *>(row + k0);
+                    sv[0] = v.x;
+                    sv[1] = v.y;
+                    sv[2] = v.z;
+                    sv[3] = v.w;
+                } else {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int c = c0 + j;
-                    const float sv = kk < keys ? shared[(size_t)c * keys + kk] : 0.0f;
-                    o[j] = (_Float16)(acc[rt][ct][j] + prm.cross_pos_b2[c] + sv);
+                    for (int j = 0; j < 4; ++j) sv[j] = k0 + j < keys ? row[k0 + j] : 0.0f;
                 }
-                *(h4 *)&kv[(16 * ct + col) * kLdsRow + c0] = o;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    kv[(16 * rt + 4 * g + j) * kLdsRow + c] = (_Float16)(acc[rt][ct][j] + bias + sv[j]);
             }
+        }
     }
     __syncthreads();
     f32x4 acc[4][4];
