@@ -334,6 +334,70 @@ def synthetic_transfusion_inputs(seed: int, height=180, width=180):
             randn(seed, "tf_heatmap", (1, 10, height, width), 1.5, -1.0))
 
 
+def lidar_backbone_tensors(init: _Init):
+    """SECOND sparse encoder under the checkpoint's names and shapes (reference
+    src/lidar_backbone.c:94-133): weights [kd, kh, kw, Ci, Co] and a BN per
+    conv (input SubM conv, four stages of two residual blocks, three strided
+    convs, the (3,1,1) output conv)."""
+    out = []
+    p = "backbone_3d."
+
+    def layer(w, bn, ci, co, k=(3, 3, 3)):
+        out.append((w, init.weight(w, (*k, ci, co), k[0] * k[1] * k[2] * ci)))
+        out.extend(init.bn(bn, co))
+
+    layer(p + "conv_input.0.weight", p + "conv_input.1", 5, 16)
+    ch = (16, 32, 64, 128)
+    for s in range(4):
+        for blk in range(2):
+            for c in range(2):
+                q = f"{p}conv{s + 1}.{blk + (1 if s else 0)}."
+                layer(f"{q}conv{c + 1}.weight", f"{q}bn{c + 1}", ch[s], ch[s])
+    for t in range(3):
+        layer(f"{p}conv{t + 2}.0.0.weight", f"{p}conv{t + 2}.0.1", ch[t], ch[t + 1])
+    layer(p + "conv_out.0.weight", p + "conv_out.1", 128, 128, (3, 1, 1))
+    return out
+
+
+def write_lidar_backbone(path, seed: int = 0, mode: str = "baseline",
+                         gain: float = 1.0) -> pathlib.Path:
+    path = pathlib.Path(path)
+    write_bfw(lidar_backbone_tensors(_Init(seed, mode, gain)), path)
+    return path
+
+
+def synthetic_points(seed: int, count: int, clusters: int = 48, extent=54.0, z_range=(-5.0, 3.0)):
+    """A LiDAR-like cloud [count, 5] (x, y, z, intensity, time): half on 32
+    scan rings over a ground band, half in Gaussian clusters (objects) of
+    0.2-1.5 m and, for a quarter of them, 2-5 cm, so voxels have occupied
+    neighbours and some hold more than ten points.  A few points fall outside the range and a few are non-finite."""
+    n_ring = count // 2
+    n_obj = count - n_ring
+    ring = randu(seed, "pts_ring", (n_ring,), 0, 32).astype(np.int64)
+    radius = 2.0 + ring * (extent * 0.95 - 2.0) / 32.0
+    theta = randu(seed, "pts_theta", (n_ring,), 0, 2 * np.pi)
+    ground = np.stack([radius * np.cos(theta), radius * np.sin(theta),
+                       randu(seed, "pts_ground", (n_ring,), -2.0, -1.7)], 1)
+    centre = np.stack([randu(seed, "cl_x", (clusters,), -0.8 * extent, 0.8 * extent),
+                       randu(seed, "cl_y", (clusters,), -0.8 * extent, 0.8 * extent),
+                       randu(seed, "cl_z", (clusters,), -1.5, 1.0)], 1)
+    size = randu(seed, "cl_s", (clusters,), 0.2, 1.5)
+    size[: clusters // 4] = randu(seed, "cl_tight", (clusters // 4,), 0.02, 0.05)
+    which = randu(seed, "pts_cl", (n_obj,), 0, clusters).astype(np.int64)
+    obj = centre[which] + randn(seed, "pts_obj", (n_obj, 3)) * size[which, None]
+    xyz = np.concatenate([ground, obj], 0)
+    out = np.concatenate([xyz, randu(seed, "pts_int", (count, 1)),
+                          randu(seed, "pts_t", (count, 1), 0.0, 0.5)], 1).astype(np.float32)
+    # Shuffle so clusters interleave (first-encounter order matters).
+    order = np.argsort(randu(seed, "pts_perm", (count,)), kind="stable")
+    out = out[order]
+    if count >= 20:
+        out[3, 0] = 70.0                         # outside x
+        out[7, 2] = z_range[1] + 1.0             # outside z
+        out[11, 3] = np.nan                      # non-finite feature
+    return np.ascontiguousarray(out)
+
+
 def write_bev_stage(path, seed: int = 0, mode: str = "baseline", gain: float = 1.0) -> pathlib.Path:
     path = pathlib.Path(path)
     write_bfw(bev_stage_tensors(_Init(seed, mode, gain)), path)

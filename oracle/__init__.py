@@ -78,6 +78,36 @@ class TfRaw(C.Structure):
         "query_scores", "labels", "indices")]
 
 
+class VoxelConfig(C.Structure):
+    """bf_voxel_config (include/bf_voxel.h)."""
+    _fields_ = [("minimum", C.c_float * 3), ("maximum", C.c_float * 3),
+                ("voxel_size", C.c_float * 3), ("point_features", C.c_size_t),
+                ("max_points_per_voxel", C.c_size_t), ("max_voxels", C.c_size_t)]
+
+
+class VoxelStats(C.Structure):
+    """bf_voxel_stats (include/bf_voxel.h)."""
+    _fields_ = [(n, C.c_size_t) for n in (
+        "input_points", "accepted_points", "rejected_nonfinite", "rejected_out_of_range",
+        "dropped_voxel_capacity", "dropped_point_capacity")]
+
+
+class SparseDesc(C.Structure):
+    """bf_sparse_conv3d_desc (include/bf_kernels.h)."""
+    _fields_ = [(n, C.c_size_t) for n in (
+        "batches", "in_depth", "in_height", "in_width", "in_channels", "out_channels",
+        "kernel_depth", "kernel_height", "kernel_width", "stride_depth", "stride_height",
+        "stride_width", "pad_depth", "pad_height", "pad_width", "dilation_depth",
+        "dilation_height", "dilation_width")] + [("submanifold", C.c_int)]
+
+
+def voxel_config(max_voxels, minimum=(-54.0, -54.0, -5.0), maximum=(54.0, 54.0, 3.0),
+                 size=(0.075, 0.075, 0.2), features=5, max_points=10):
+    """The runtime's voxel contract (runtime.c:262-265) by default."""
+    return VoxelConfig((C.c_float * 3)(*minimum), (C.c_float * 3)(*maximum),
+                       (C.c_float * 3)(*size), features, max_points, max_voxels)
+
+
 class Detection(C.Structure):
     """bf_detection (include/bevfusion.h)."""
     _fields_ = [(n, C.c_float) for n in ("x", "y", "z", "width", "length", "height", "yaw",
@@ -194,6 +224,33 @@ class Oracle:
         L.bf_lss_lift_pool_f32_ref.argtypes = [_f32p, _f32p, _f32p, _f32p, C.POINTER(LssDesc)]
         if hasattr(L, "bf_oracle_lss_ranks"):
             L.bf_oracle_lss_ranks.argtypes = [_f32p, C.c_void_p, C.POINTER(LssDesc)]
+        # LiDAR side (depth raster, voxeliser, MeanVFE, sparse conv, backbone).
+        L.bf_depth_rasterize_f32_ref.argtypes = [_f32p, _sz, _sz, _f32p, _f32p, _f32p, _f32p,
+                                                 _sz, _sz, _sz, _sz]
+        L.bf_voxelize_workspace_bytes.argtypes = [C.POINTER(VoxelConfig)]
+        L.bf_voxelize_workspace_bytes.restype = _sz
+        L.bf_voxelize_f32_workspace_ref.argtypes = [
+            _f32p, _sz, _sz, C.c_int32, C.POINTER(VoxelConfig), _f32p, C.c_void_p, C.c_void_p,
+            C.POINTER(_sz), C.POINTER(VoxelStats), C.c_void_p, _sz]
+        L.bf_mean_vfe_f32_ref.argtypes = [_f32p, C.c_void_p, _f32p, _sz, _sz, _sz]
+        L.bf_mean_vfe_f32_ref.restype = None
+        L.bf_sparse_conv3d_workspace_bytes.argtypes = [_sz, _sz]
+        L.bf_sparse_conv3d_workspace_bytes.restype = _sz
+        L.bf_sparse_conv3d_output_shape.argtypes = [C.POINTER(SparseDesc), C.POINTER(_sz),
+                                                    C.POINTER(_sz), C.POINTER(_sz)]
+        L.bf_sparse_conv3d_f32_workspace_ref.argtypes = [
+            C.c_void_p, _f32p, _sz, _f32p, C.c_void_p, C.c_void_p, _f32p, _sz, C.POINTER(_sz),
+            C.POINTER(SparseDesc), C.c_void_p, _sz]
+        L.bf_lidar_backbone_create.argtypes = [C.c_void_p, C.POINTER(C.c_void_p), C.c_char_p, _sz]
+        L.bf_lidar_backbone_destroy.argtypes = [C.c_void_p]
+        L.bf_lidar_backbone_destroy.restype = None
+        L.bf_lidar_backbone_workspace_bytes.argtypes = [_sz]
+        L.bf_lidar_backbone_workspace_bytes.restype = _sz
+        L.bf_lidar_backbone_output_shape.argtypes = [_sz, _sz, _sz, C.POINTER(_sz),
+                                                     C.POINTER(_sz), C.POINTER(_sz)]
+        L.bf_lidar_backbone_forward_ref.argtypes = [
+            C.c_void_p, C.c_void_p, _f32p, _sz, _sz, _sz, _sz, _sz, _sz, _f32p, C.c_void_p, _sz,
+            C.c_char_p, _sz]
 
     # ---- utilities -------------------------------------------------------
     def backend(self) -> str:
@@ -391,6 +448,88 @@ class Oracle:
         finally:
             self.lib.bf_bev_stage_destroy(net)
         return sp, sh, hm
+
+    # ---- LiDAR side --------------------------------------------------------
+    def depth_raster(self, points_b, lidar_aug, lidar_to_image, image_aug, cameras, height,
+                     width, batches=1):
+        """points [P, stride] with column 0 = batch -> dense depth [B,N,H,W]
+        (depth_raster.c:49-105)."""
+        pts = _f32(points_b)
+        out = np.empty((batches, cameras, height, width), np.float32)
+        if not self.lib.bf_depth_rasterize_f32_ref(
+                pts if pts.size else np.zeros((1, pts.shape[1]), np.float32), pts.shape[0],
+                pts.shape[1], _f32(lidar_aug), _f32(lidar_to_image), _f32(image_aug), out,
+                batches, cameras, height, width):
+            raise OracleError("depth raster failed")
+        return out
+
+    def voxelize(self, points, config, batch=0):
+        """points [P, F] -> (voxels [V,M,F], coords int32 [V,4], counts int64 [V], stats)."""
+        pts = _f32(points)
+        M, F, cap = config.max_points_per_voxel, config.point_features, config.max_voxels
+        voxels = np.empty((cap, M, F), np.float32)
+        coords = np.empty((cap, 4), np.int32)
+        counts = np.empty((cap,), np.int64)
+        n, st = _sz(0), VoxelStats()
+        nbytes = self.lib.bf_voxelize_workspace_bytes(C.byref(config))
+        ws = np.empty(max(nbytes, 1), np.uint8)
+        if not self.lib.bf_voxelize_f32_workspace_ref(
+                pts if pts.size else np.zeros((1, F), np.float32), pts.shape[0], pts.shape[1],
+                batch, C.byref(config), voxels, coords.ctypes.data, counts.ctypes.data,
+                C.byref(n), C.byref(st), ws.ctypes.data, nbytes):
+            raise OracleError("voxelize failed")
+        v = n.value
+        return voxels[:v], coords[:v], counts[:v], st
+
+    def mean_vfe(self, voxels, counts):
+        v, m, c = voxels.shape
+        out = np.empty((v, c), np.float32)
+        cnt = np.ascontiguousarray(counts, np.int64)
+        self.lib.bf_mean_vfe_f32_ref(_f32(voxels), cnt.ctypes.data, out, v, m, c)
+        return out
+
+    def sparse_conv3d(self, coords, features, weight, bias, desc, capacity):
+        """coords int32 [N,4], features [N,Ci], weight [kd,kh,kw,Ci,Co] ->
+        (coords [M,4], features [M,Co])."""
+        coords = np.ascontiguousarray(coords, np.int32)
+        feats = _f32(features)
+        oc = np.empty((capacity, 4), np.int32)
+        of = np.empty((capacity, desc.out_channels), np.float32)
+        n = _sz(0)
+        nbytes = self.lib.bf_sparse_conv3d_workspace_bytes(coords.shape[0], capacity)
+        ws = np.empty(max(nbytes, 1), np.uint8)
+        b = None if bias is None else _f32(bias)
+        if not self.lib.bf_sparse_conv3d_f32_workspace_ref(
+                coords.ctypes.data, feats, coords.shape[0], _f32(weight),
+                None if b is None else b.ctypes.data, oc.ctypes.data, of, capacity, C.byref(n),
+                C.byref(desc), ws.ctypes.data, nbytes):
+            raise OracleError("sparse conv3d failed")
+        return oc[:n.value], of[:n.value]
+
+    def lidar_backbone(self, model, coords, features, depth=41, height=1440, width=1440,
+                       capacity=None, batches=1):
+        """voxel coords int32 [N,4] + MeanVFE features [N,5] -> dense
+        [B,128,D',H',W'] (lidar_backbone.c:191-273)."""
+        coords = np.ascontiguousarray(coords, np.int32)
+        feats = _f32(features)
+        cap = capacity or 8 * coords.shape[0]
+        od, oh, ow = _sz(), _sz(), _sz()
+        if not self.lib.bf_lidar_backbone_output_shape(depth, height, width, C.byref(od),
+                                                       C.byref(oh), C.byref(ow)):
+            raise OracleError("lidar backbone output shape")
+        dense = np.empty((batches, 128, od.value, oh.value, ow.value), np.float32)
+        nbytes = self.lib.bf_lidar_backbone_workspace_bytes(cap)
+        ws = np.empty(max(nbytes, 1), np.uint8)
+        err = C.create_string_buffer(256)
+        net = model.create("lidar_backbone")
+        try:
+            if not self.lib.bf_lidar_backbone_forward_ref(
+                    net, coords.ctypes.data, feats, coords.shape[0], batches, depth, height, width,
+                    cap, dense, ws.ctypes.data, nbytes, err, 256):
+                raise OracleError(err.value.decode())
+        finally:
+            self.lib.bf_lidar_backbone_destroy(net)
+        return dense
 
     # ---- TransFusion head ------------------------------------------------
     TF_FIELDS = (("center", 2), ("height", 1), ("dimension_log", 3), ("rotation", 2),

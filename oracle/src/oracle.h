@@ -16,6 +16,10 @@
  *   bf_bev_stage.h      -> reference include/bf_bev_stage.h,     src/bev_stage.c:16-227
  *   bf_transfusion*.h   -> reference include/bf_transfusion*.h,  src/transfusion.c:8-193,
  *                          src/transfusion_decoder.c:23-456
+ *   bf_depth_raster.h   -> reference include/bf_depth_raster.h,  src/depth_raster.c:14-105
+ *   bf_voxel.h          -> reference include/bf_voxel.h:30-45,   src/voxel.c:13-151
+ *   bf_lidar_backbone.h -> reference include/bf_lidar_backbone.h, src/lidar_backbone.c:86-273,
+ *                          with MeanVFE and the sparse conv of src/kernels_ref.c:477-772
  * Floating-point operation order matches the reference per output element, so
  * the scalar build (no OpenMP, BF_CPU_SCALAR=1) is bit-identical to the
  * reference compiled from its own sources (oracle/_ref).
@@ -24,7 +28,9 @@
 #define BF_ORACLE_H
 
 #include "bevfusion.h"
+#include "bf_kernels.h"
 #include "bf_lss.h"
+#include "bf_voxel.h"
 #include "bf_model.h"
 #include "bf_transfusion_decoder.h"
 
@@ -165,6 +171,46 @@ int bf_lss_downsample_forward_ref(const bf_lss_downsample *down, const float *in
                                   size_t batches, size_t height, size_t width,
                                   float *output, void *workspace,
                                   size_t workspace_bytes, char *error, size_t cap);
+
+/* ---- LiDAR side (bf_depth_raster.h, bf_voxel.h, bf_lidar_backbone.h) -- */
+int bf_depth_rasterize_f32_ref(const float *points, size_t point_count, size_t point_stride,
+                               const float *lidar_augmentation, const float *lidar_to_image,
+                               const float *image_augmentation, float *dense_depth,
+                               size_t batches, size_t cameras, size_t image_height,
+                               size_t image_width);
+int bf_voxel_grid_shape(const bf_voxel_config *config, size_t grid_xyz[3]);
+size_t bf_voxelize_workspace_bytes(const bf_voxel_config *config);
+int bf_voxelize_f32_workspace_ref(const float *points, size_t point_count, size_t point_stride,
+                                  int32_t batch_index, const bf_voxel_config *config,
+                                  float *voxels, bf_coord4 *coords, int64_t *counts,
+                                  size_t *voxel_count, bf_voxel_stats *stats, void *workspace,
+                                  size_t workspace_bytes);
+void bf_mean_vfe_f32_ref(const float *points, const int64_t *counts, float *output,
+                         size_t voxels, size_t max_points, size_t channels);
+int bf_sparse_conv3d_output_shape(const bf_sparse_conv3d_desc *desc, size_t *depth,
+                                  size_t *height, size_t *width);
+size_t bf_sparse_conv3d_workspace_bytes(size_t input_capacity, size_t output_capacity);
+int bf_sparse_conv3d_f32_workspace_ref(const bf_coord4 *input_coords,
+                                       const float *input_features, size_t input_count,
+                                       const float *weight_kdhwio, const float *bias,
+                                       bf_coord4 *output_coords, float *output_features,
+                                       size_t output_capacity, size_t *output_count,
+                                       const bf_sparse_conv3d_desc *desc, void *workspace,
+                                       size_t workspace_bytes);
+typedef struct bf_lidar_backbone bf_lidar_backbone;
+int bf_lidar_backbone_create(const bf_model *model, bf_lidar_backbone **out, char *error,
+                             size_t cap);
+void bf_lidar_backbone_destroy(bf_lidar_backbone *backbone);
+size_t bf_lidar_backbone_workspace_bytes(size_t capacity);
+int bf_lidar_backbone_output_shape(size_t depth, size_t height, size_t width, size_t *out_depth,
+                                   size_t *out_height, size_t *out_width);
+/* voxel features [N,5] MeanVFE; dense [B,128,D',H',W'] (logically [B,256,H',W']). */
+int bf_lidar_backbone_forward_ref(const bf_lidar_backbone *backbone,
+                                  const bf_coord4 *voxel_coords, const float *voxel_features,
+                                  size_t voxel_count, size_t batches, size_t depth,
+                                  size_t height, size_t width, size_t capacity, float *dense,
+                                  void *workspace, size_t workspace_bytes, char *error,
+                                  size_t cap);
 
 /* ---- shared helpers (internal to the oracle) --------------------------- */
 int bf_oracle_fail(char *error, size_t cap, const char *fmt, ...);
