@@ -68,6 +68,7 @@ def parse():
     p.add_argument("--no-lss", action="store_true", help="skip the LSS pooling leg")
     p.add_argument("--no-bev", action="store_true", help="skip the BEV stage leg")
     p.add_argument("--no-tf", action="store_true", help="skip the TransFusion decoder leg")
+    p.add_argument("--no-lidar", action="store_true", help="skip the LiDAR branch leg")
     return p.parse_args()
 
 
@@ -598,6 +599,172 @@ def tf_cpu_baseline(path, seed=0):
             "cpu_model": _cpu_model()}
 
 
+LIDAR_POINTS, LIDAR_SWEEPS = 100000, 10  # ~54k voxels, near the reference's stress frame
+LIDAR_GRID = (41, 1440, 1440)
+LIDAR_VOXELS, LIDAR_SPARSE = 160000, 160000  # the reference runtime's capacities
+# Reference CUDA LiDAR branch, points -> LiDAR BEV, 100k points / 50k voxels,
+# warm median (reference docs/draft.md:257-260).
+LIDAR_REFERENCE_MS = 58.936
+
+
+def _lidar_keys(s, dims):
+    return (s[:, 0] * dims[1] + s[:, 1]) * dims[2] + s[:, 2]
+
+
+def _subm_pairs(s, dims):
+    import numpy as np
+    keys = np.sort(_lidar_keys(s, dims))
+    total = 0
+    for dz in (-1, 0, 1):
+        for dy in (-1, 0, 1):
+            for dx in (-1, 0, 1):
+                q = s + np.array([dz, dy, dx])
+                ok = np.all((q >= 0) & (q < np.array(dims)), axis=1)
+                k = _lidar_keys(q[ok], dims)
+                pos = np.searchsorted(keys, k)
+                pos[pos == len(keys)] = 0
+                total += int((keys[pos] == k).sum())
+    return total
+
+
+def _strided(s, dims, kernel, stride, pad):
+    """Output sites and (input, tap) pair count of a strided sparse conv."""
+    import numpy as np
+    out_dims = tuple((dims[a] + 2 * pad[a] - kernel[a]) // stride[a] + 1 for a in range(3))
+    outs, pairs = [], 0
+    for kz in range(kernel[0]):
+        for ky in range(kernel[1]):
+            for kx in range(kernel[2]):
+                n = s + np.array(pad) - np.array([kz, ky, kx])
+                ok = np.all((n >= 0) & (n % np.array(stride) == 0), axis=1)
+                o = n[ok] // np.array(stride)
+                ok2 = np.all(o < np.array(out_dims), axis=1)
+                outs.append(o[ok2])
+                pairs += int(ok2.sum())
+    return np.unique(np.concatenate(outs), axis=0), out_dims, pairs
+
+
+def lidar_work(coords, dims=LIDAR_GRID):
+    """Algorithmic flops of the SECOND encoder on these voxel sites: 2 Ci Co
+    per (output site, active tap) pair, per layer; and the site counts."""
+    import numpy as np
+    s = np.asarray(coords, np.int64)[:, 1:]
+    flops, sites = 0, [len(s)]
+    pairs = _subm_pairs(s, dims)
+    flops += 2 * pairs * 5 * 16 + 4 * 2 * pairs * 16 * 16
+    ch = (16, 32, 64, 128)
+    for st in range(1, 4):
+        s, dims, p = _strided(s, dims, (3, 3, 3), (2, 2, 2), (1 if st < 3 else 0, 1, 1))
+        sites.append(len(s))
+        flops += 2 * p * ch[st - 1] * ch[st] + 4 * 2 * _subm_pairs(s, dims) * ch[st] ** 2
+    s, dims, p = _strided(s, dims, (3, 1, 1), (2, 1, 1), (0, 0, 0))
+    sites.append(len(s))
+    flops += 2 * p * 128 * 128
+    return flops, sites
+
+
+def lidar_leg(dev, reps, seed=0):
+    """LiDAR branch on one frame of 100k synthetic points: depth raster into the
+    six camera images, voxeliser + MeanVFE, SECOND sparse encoder to the dense
+    [256,180,180] BEV; ms per frame (eager and graph replay)."""
+    import torch
+    import bfhip
+    from bfhip import bfw, frame_scene
+    tmp = pathlib.Path(tempfile.mkdtemp(prefix="lidar_"))
+    path = bfw.write_lidar_backbone(tmp / "lidar.bfw", seed=seed, mode="fan_in", gain=1.2)
+    cal = frame_scene.calibration(seed)
+    pts_np = bfw.synthetic_points(seed, LIDAR_POINTS, sweeps=LIDAR_SWEEPS)
+    t = lambda a: torch.from_numpy(a).to(dev)
+    pts = t(pts_np)
+    aug, l2i, post = t(cal["lidar_augmentation"]), t(cal["lidar_to_image"]), t(cal["image_augmentation"])
+    stream = torch.cuda.Stream()
+    raster = bfhip.DepthRaster(300000)
+    vox = bfhip.Voxelizer(bfhip.voxel_config(LIDAR_VOXELS), 300000)
+    with bfhip.Model(path) as m:
+        net = bfhip.LidarBackbone(m, 1, *LIDAR_GRID, LIDAR_SPARSE)
+    depth = torch.empty((6, 256, 704), device=dev)
+    coords = torch.empty((LIDAR_VOXELS, 4), dtype=torch.int32, device=dev)
+    means = torch.empty((LIDAR_VOXELS, 5), device=dev)
+    count = torch.empty((1,), dtype=torch.int32, device=dev)
+    bev = torch.empty(net.out_shape, device=dev)
+
+    def frame():
+        raster.forward(pts, aug, l2i, post, out=depth, stream=stream)
+        vox.forward(pts, coords, means, count, stream=stream)
+        net.forward(coords, means, count, out=bev, stream=stream)
+
+    def timed(fn, n):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(n):
+            fn()
+        b.record(stream)
+        b.synchronize()
+        return a.elapsed_time(b) / n
+
+    with torch.cuda.stream(stream):
+        for _ in range(3):
+            frame()
+        eager_ms = timed(frame, reps)
+        parts = {"depth_raster": timed(lambda: raster.forward(pts, aug, l2i, post, out=depth,
+                                                              stream=stream), reps),
+                 "voxelize": timed(lambda: vox.forward(pts, coords, means, count, stream=stream),
+                                   reps),
+                 "sparse_encoder": timed(lambda: net.forward(coords, means, count, out=bev,
+                                                             stream=stream), reps)}
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            frame()
+        graph.replay()
+        ms = timed(graph.replay, reps)
+    stream.synchronize()
+    n = int(count.item())
+    flops, sites = lidar_work(coords[:n].cpu().numpy())
+    enc_ms = parts["sparse_encoder"]
+    tflops = flops / (enc_ms * 1e-3) / 1e12
+    out = {"workload": f"LiDAR branch, {LIDAR_POINTS} synthetic points ({LIDAR_SWEEPS} sweeps) -> depth raster (6 x 256 x "
+                       f"704) + voxeliser/MeanVFE ({n} voxels) + SECOND sparse encoder on the "
+                       "41 x 1440 x 1440 grid -> [256,180,180] BEV; random-init weights; split "
+                       "fp16 MFMA operands (hi + lo), fp32 accumulation",
+           "ms": round(ms, 4), "ms_eager": round(eager_ms, 4),
+           "parts_ms": {k: round(v, 4) for k, v in parts.items()},
+           "voxels": n, "sites_per_level": sites, "encoder_gflop": round(flops / 1e9, 2),
+           "reference_rtx4060ti_ms": LIDAR_REFERENCE_MS,
+           "speedup_vs_reference": round(LIDAR_REFERENCE_MS / ms, 1),
+           "resident_mib": round((raster.resident_bytes() + vox.resident_bytes() +
+                                  net.resident_bytes()) / 2**20, 1),
+           "roofline": {"kernel": "sparse encoder forward", "bound": "mfma",
+                        "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
+                        "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+                        "traffic": None,
+                        "note": "algorithmic flops (2 Ci Co per active (site, tap) pair) over "
+                                "the encoder's time; the kernels issue three fp16 MFMAs per "
+                                "product (split operands) and pad each wave's taps"}}
+    for ctx in (raster, vox, net):
+        ctx.close()
+    return out, (path, pts_np)
+
+
+def lidar_cpu_baseline(path, pts):
+    """The reference's CPU LiDAR branch (oracle/_ref: src/voxel.c,
+    src/kernels_ref.c MeanVFE, src/lidar_backbone.c) on the same frame."""
+    import oracle
+    kind = "reference" if oracle.available("ref") else "port"
+    o = oracle.Oracle("ref" if kind == "reference" else "port")
+    cfg = oracle.voxel_config(LIDAR_VOXELS)
+    with o.open_model(path) as m:
+        t0 = time.perf_counter()
+        vx, c, cnt, _ = o.voxelize(pts, cfg)
+        f = o.mean_vfe(vx, cnt)
+        o.lidar_backbone(m, c, f, *LIDAR_GRID, capacity=LIDAR_SPARSE)
+        t1 = time.perf_counter()
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or os.cpu_count()
+    return {"value": round((t1 - t0) * 1e3, 1), "unit": "ms/frame", "cores": threads,
+            "kind": kind, "backend": o.backend(),
+            "sample": f"voxeliser + MeanVFE + sparse encoder on the full {LIDAR_POINTS}-point frame",
+            "cpu_model": _cpu_model()}
+
+
 def cpu_baseline(model_path, cameras):
     """Reference CPU path (oracle/_ref, the reference's C compiled from its own
     sources, OpenMP) on a bounded sample of `cameras` cameras, scaled to a
@@ -757,6 +924,11 @@ def main():
         if not args.no_cpu:
             tf["cpu_baseline"] = tf_cpu_baseline(tf_path)
         result["transfusion"] = tf
+    if not args.no_lidar:
+        lidar, (lidar_path, lidar_pts) = lidar_leg(dev, max(args.steps, 20))
+        if not args.no_cpu:
+            lidar["cpu_baseline"] = lidar_cpu_baseline(lidar_path, lidar_pts)
+        result["lidar"] = lidar
     print(json.dumps(result))
 
 

@@ -71,6 +71,20 @@ class Detections(C.Structure):
 
 _tfp = C.POINTER(TfRawOutputs)
 
+
+class VoxelConfig(C.Structure):
+    """``bf_voxel_config`` (include/bf_voxel.h)."""
+    _fields_ = [("minimum", C.c_float * 3), ("maximum", C.c_float * 3),
+                ("voxel_size", C.c_float * 3), ("point_features", _sz),
+                ("max_points_per_voxel", _sz), ("max_voxels", _sz)]
+
+
+def voxel_config(max_voxels, minimum=(-54.0, -54.0, -5.0), maximum=(54.0, 54.0, 3.0),
+                 size=(0.075, 0.075, 0.2), features=5, max_points=10):
+    """The reference runtime's voxel contract (runtime.c:262-265) by default."""
+    return VoxelConfig((C.c_float * 3)(*minimum), (C.c_float * 3)(*maximum),
+                       (C.c_float * 3)(*size), features, max_points, max_voxels)
+
 # Every symbol declared by include/*.h, with its ctypes signature.
 SIGNATURES = {
     "bf_cuda_conv2d_f32": (_i, [C.POINTER(ConvDesc), _vp, _vp, _vp, _vp, _vp, C.c_char_p, _sz]),
@@ -114,6 +128,23 @@ SIGNATURES = {
     "bf_cuda_transfusion_decode_detections": (_i, [_vp, _tfp, C.c_float, C.POINTER(Detections),
                                                    _vp, C.c_char_p, _sz]),
     "bf_cuda_transfusion_resident_bytes": (_sz, [_vp]),
+    "bf_cuda_depth_raster_create": (_i, [_sz, _sz, _sz, _sz, C.POINTER(_vp), C.c_char_p, _sz]),
+    "bf_cuda_depth_raster_destroy": (None, [_vp]),
+    "bf_cuda_depth_raster_resident_bytes": (_sz, [_vp]),
+    "bf_cuda_depth_rasterize_f32": (_i, [_vp, _vp, _sz, _vp, _vp, _vp, _vp, _vp, C.c_char_p,
+                                         _sz]),
+    "bf_cuda_voxelizer_create": (_i, [C.POINTER(VoxelConfig), _sz, C.POINTER(_vp), C.c_char_p,
+                                      _sz]),
+    "bf_cuda_voxelizer_destroy": (None, [_vp]),
+    "bf_cuda_voxelizer_resident_bytes": (_sz, [_vp]),
+    "bf_cuda_voxelize_mean_f32": (_i, [_vp, _vp, _sz, _vp, _vp, _vp, _vp, C.c_char_p, _sz]),
+    "bf_cuda_lidar_backbone_create": (_i, [_vp, _sz, _sz, _sz, _sz, _sz, C.POINTER(_vp),
+                                           C.c_char_p, _sz]),
+    "bf_cuda_lidar_backbone_destroy": (None, [_vp]),
+    "bf_cuda_lidar_backbone_resident_bytes": (_sz, [_vp]),
+    "bf_cuda_lidar_backbone_forward": (_i, [_vp, _vp, _vp, _sz, _vp, _vp, C.c_char_p, _sz]),
+    "bf_cuda_lidar_backbone_forward_count_device": (_i, [_vp, _vp, _vp, _vp, _vp, _vp,
+                                                         C.c_char_p, _sz]),
 }
 
 SWIN_OPS = ("ln1", "qkv", "attention", "proj", "ln2", "fc1", "fc2", "merge", "mlp")
@@ -658,3 +689,127 @@ class TransFusion:
             self.close()
         except Exception:
             pass
+
+
+def _tptr(t, dtype):
+    torch = _torch()
+    if not t.is_cuda or t.dtype != dtype or not t.is_contiguous():
+        raise BfHipError(f"expected a contiguous {dtype} device tensor")
+    return _vp(t.data_ptr())
+
+
+class _Context:
+    _destroy = None
+
+    def close(self):
+        if getattr(self, "handle", None):
+            getattr(self.lib, self._destroy)(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class DepthRaster(_Context):
+    """bf_cuda_depth_raster context (include/bf_cuda_depth_raster.h)."""
+    _destroy = "bf_cuda_depth_raster_destroy"
+
+    def __init__(self, max_points, cameras=6, height=256, width=704):
+        self.lib, self.shape = hip_lib(), (cameras, height, width)
+        self.handle, err = _vp(), _err()
+        _check(self.lib.bf_cuda_depth_raster_create(max_points, cameras, height, width,
+                                                    C.byref(self.handle), err, 512),
+               err, "bf_cuda_depth_raster_create")
+
+    def resident_bytes(self):
+        return self.lib.bf_cuda_depth_raster_resident_bytes(self.handle)
+
+    def forward(self, points, lidar_aug, lidar_to_image, image_aug, out=None, stream=None):
+        """points [P,5] -> dense depth [N,H,W]."""
+        torch = _torch()
+        if out is None:
+            out = torch.empty(self.shape, device=lidar_aug.device)
+        err = _err()
+        pts = _ptr(points) if points.numel() else None
+        _check(self.lib.bf_cuda_depth_rasterize_f32(self.handle, pts, points.shape[0],
+                                                    _ptr(lidar_aug), _ptr(lidar_to_image),
+                                                    _ptr(image_aug), _ptr(out), _stream(stream),
+                                                    err, 512),
+               err, "bf_cuda_depth_rasterize_f32")
+        return out
+
+
+class Voxelizer(_Context):
+    """bf_cuda_voxelizer context (include/bf_cuda_voxel.h)."""
+    _destroy = "bf_cuda_voxelizer_destroy"
+
+    def __init__(self, config, max_points):
+        self.lib, self.config = hip_lib(), config
+        self.handle, err = _vp(), _err()
+        _check(self.lib.bf_cuda_voxelizer_create(C.byref(config), max_points,
+                                                 C.byref(self.handle), err, 512),
+               err, "bf_cuda_voxelizer_create")
+
+    def resident_bytes(self):
+        return self.lib.bf_cuda_voxelizer_resident_bytes(self.handle)
+
+    def forward(self, points, coords=None, means=None, count=None, stream=None):
+        """points [P,5] -> (coords int32 [max_voxels,4], means [max_voxels,5],
+        count int32 [1]); rows below count are valid."""
+        torch = _torch()
+        v, dev = self.config.max_voxels, points.device
+        coords = coords if coords is not None else torch.empty((v, 4), dtype=torch.int32, device=dev)
+        means = means if means is not None else torch.empty((v, 5), device=dev)
+        count = count if count is not None else torch.empty((1,), dtype=torch.int32, device=dev)
+        err = _err()
+        _check(self.lib.bf_cuda_voxelize_mean_f32(
+            self.handle, _ptr(points) if points.numel() else None, points.shape[0],
+            _tptr(coords, torch.int32), _ptr(means), _tptr(count, torch.int32), _stream(stream),
+            err, 512), err, "bf_cuda_voxelize_mean_f32")
+        return coords, means, count
+
+
+class LidarBackbone(_Context):
+    """bf_cuda_lidar_backbone context (include/bf_cuda_lidar.h)."""
+    _destroy = "bf_cuda_lidar_backbone_destroy"
+
+    def __init__(self, model: Model, batches, depth, height, width, capacity):
+        self.lib = hip_lib()
+        d, h, w = depth, height, width
+        for pz in (1, 1, 0):
+            d, h, w = (d + 2 * pz - 3) // 2 + 1, (h - 1) // 2 + 1, (w - 1) // 2 + 1
+        self.out_shape = (batches, 128, (d - 3) // 2 + 1, h, w)
+        self.handle, err = _vp(), _err()
+        _check(self.lib.bf_cuda_lidar_backbone_create(model.handle, batches, depth, height, width,
+                                                      capacity, C.byref(self.handle), err, 512),
+               err, "bf_cuda_lidar_backbone_create")
+
+    def resident_bytes(self):
+        return self.lib.bf_cuda_lidar_backbone_resident_bytes(self.handle)
+
+    def forward(self, coords, features, count, out=None, stream=None):
+        """coords int32 [N,4], MeanVFE features [N,5]; count an int or a
+        device int32 [1] tensor -> dense [B,128,D',H',W']."""
+        torch = _torch()
+        if out is None:
+            out = torch.empty(self.out_shape, device=features.device)
+        err = _err()
+        if isinstance(count, int):
+            ok = self.lib.bf_cuda_lidar_backbone_forward(
+                self.handle, _tptr(coords, torch.int32), _ptr(features), count, _ptr(out),
+                _stream(stream), err, 512)
+        else:
+            ok = self.lib.bf_cuda_lidar_backbone_forward_count_device(
+                self.handle, _tptr(coords, torch.int32), _ptr(features), _tptr(count, torch.int32),
+                _ptr(out), _stream(stream), err, 512)
+        _check(ok, err, "bf_cuda_lidar_backbone_forward")
+        return out

@@ -366,16 +366,24 @@ def write_lidar_backbone(path, seed: int = 0, mode: str = "baseline",
     return path
 
 
-def synthetic_points(seed: int, count: int, clusters: int = 48, extent=54.0, z_range=(-5.0, 3.0)):
+def synthetic_points(seed: int, count: int, clusters: int = 48, extent=54.0, z_range=(-5.0, 3.0),
+                     sweeps: int = 1):
     """A LiDAR-like cloud [count, 5] (x, y, z, intensity, time): half on 32
     scan rings over a ground band, half in Gaussian clusters (objects) of
     0.2-1.5 m and, for a quarter of them, 2-5 cm, so voxels have occupied
-    neighbours and some hold more than ten points.  A few points fall outside the range and a few are non-finite."""
+    neighbours and some hold more than ten points.  With sweeps > 1 the ring
+    returns repeat at `sweeps` azimuths 1 cm apart, as accumulated sweeps of
+    a slowly moving sensor do.  A few points fall outside the range and a few
+    are non-finite."""
     n_ring = count // 2
     n_obj = count - n_ring
     ring = randu(seed, "pts_ring", (n_ring,), 0, 32).astype(np.int64)
     radius = 2.0 + ring * (extent * 0.95 - 2.0) / 32.0
     theta = randu(seed, "pts_theta", (n_ring,), 0, 2 * np.pi)
+    if sweeps > 1:
+        base = np.arange(n_ring) // sweeps * sweeps
+        ring, radius = ring[base], radius[base]
+        theta = theta[base] + (np.arange(n_ring) % sweeps) * 0.01 / radius
     ground = np.stack([radius * np.cos(theta), radius * np.sin(theta),
                        randu(seed, "pts_ground", (n_ring,), -2.0, -1.7)], 1)
     centre = np.stack([randu(seed, "cl_x", (clusters,), -0.8 * extent, 0.8 * extent),

@@ -1,0 +1,713 @@
+// SECOND sparse LiDAR encoder (drop-in for reference src/cuda_lidar.cu).
+//
+// Active sites of each level live in a dense int32 index grid over that
+// level's batches x depth x height x width cells (340 MB at the production
+// 41 x 1440 x 1440 input; the coarser levels add 50 MB): a cell holds the
+// site's row or -1.  The grids are -1 between forwards — a forward writes
+// exactly its sites' cells and clears them at the end — so finding a
+// neighbour is one load, with no hashing and no atomics.
+//
+//   level 0      the caller's voxel rows, in the caller's order;
+//   submanifold  27-tap neighbour table per row (same level, pad 1);
+//   strided      each input site marks every output cell one of its taps
+//                reaches (plain stores of one marker value), then the
+//                marked cells are compacted in cell order — ascending
+//                (batch, z, y, x), the reference's site order — by per-chunk
+//                counts and an in-order write pass (no atomics across
+//                workgroups); then a neighbour table from output to input;
+//   convolution  gather GEMM on the matrix cores: 32 output rows per wave,
+//                K = taps x input channels, each lane gathering its row's
+//                neighbour features as the A operand and the BN-folded
+//                weights [tap][co][ci] as B; taps no row of the wave uses
+//                are skipped; bias, residual add and ReLU fused in the
+//                epilogue.  The 5-channel input conv runs in fp32 on the
+//                vector units (its inputs are metric coordinates).
+// Precision: features and weights are kept as split fp16 pairs, x = hi + lo
+// with hi = fp16(x) and lo = fp16(x - hi), and every product is formed as
+// hi*Whi + lo*Whi + hi*Wlo on fp16 MFMAs with fp32 accumulation (the
+// dropped lo*Wlo term is 2^-22 relative) -- the split-operand scheme of
+// Ootomo and Yokota, "Recovering single precision accuracy from Tensor Cores
+// while surpassing the FP32 theoretical peak performance" (IJHPCA 2022).
+// Sixteen chained layers of plain fp16 operands drift to ~1e-1 of the BEV's
+// RMS at its largest entries; the split keeps the encoder near fp32.
+// The output conv writes fp32 rows, gathered into the dense BEV.
+#include "bf_cuda_lidar.h"
+#include "host_util.h"
+
+#include <algorithm>
+#include <climits>
+#include <cmath>
+#include <cstdlib>
+#include <string>
+#include <type_traits>
+#include <vector>
+
+using namespace bfhip;
+
+namespace {
+
+constexpr int kTaps = 27, kChunk = 8192, kRowsPerWave = 32, kRowsPerGroup = 4 * kRowsPerWave;
+constexpr int kEmpty = -1, kMarked = -2;
+constexpr float kBnEps = 1e-3f;
+
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+
+struct Grid {
+    int b, d, h, w;
+};
+struct Geom {
+    int kd, kh, kw, sd, sh, sw, pd, ph, pw;
+};
+
+__device__ __forceinline__ long long cell_of(const Grid &g, int b, int z, int y, int x) {
+    return (((long long)b * g.d + z) * g.h + y) * g.w + x;
+}
+__device__ __forceinline__ bool inside(const Grid &g, int b, int z, int y, int x) {
+    return (unsigned)b < (unsigned)g.b && (unsigned)z < (unsigned)g.d &&
+           (unsigned)y < (unsigned)g.h && (unsigned)x < (unsigned)g.w;
+}
+
+__global__ void count_init_kernel(const unsigned *__restrict__ src, unsigned host, unsigned cap,
+                                  unsigned *__restrict__ dst) {
+    if (threadIdx.x || blockIdx.x) return;
+    const unsigned n = src ? *src : host;
+    *dst = n < cap ? n : cap;
+}
+
+__global__ __launch_bounds__(256) void index_kernel(const bf_coord4 *__restrict__ coords,
+                                                    const unsigned *__restrict__ count, Grid g,
+                                                    int *__restrict__ grid) {
+    const unsigned n = *count;
+    for (unsigned j = blockIdx.x * 256 + threadIdx.x; j < n; j += gridDim.x * 256) {
+        const bf_coord4 c = coords[j];
+        if (inside(g, c.batch, c.z, c.y, c.x)) grid[cell_of(g, c.batch, c.z, c.y, c.x)] = (int)j;
+    }
+}
+
+__global__ __launch_bounds__(256) void clear_kernel(const bf_coord4 *__restrict__ coords,
+                                                    const unsigned *__restrict__ count, Grid g,
+                                                    int *__restrict__ grid) {
+    const unsigned n = *count;
+    for (unsigned j = blockIdx.x * 256 + threadIdx.x; j < n; j += gridDim.x * 256) {
+        const bf_coord4 c = coords[j];
+        if (inside(g, c.batch, c.z, c.y, c.x)) grid[cell_of(g, c.batch, c.z, c.y, c.x)] = kEmpty;
+    }
+}
+
+// Submanifold 3x3x3 (pad 1): tap (kz, ky, kx) of site s reads s + (k - 1).
+__global__ __launch_bounds__(256) void subm_neighbors_kernel(const bf_coord4 *__restrict__ coords,
+                                                             const unsigned *__restrict__ count,
+                                                             Grid g, const int *__restrict__ grid,
+                                                             int *__restrict__ nbr) {
+    const unsigned n = *count;
+    for (unsigned j = blockIdx.x * 256 + threadIdx.x; j < n; j += gridDim.x * 256) {
+        const bf_coord4 c = coords[j];
+        for (int t = 0; t < kTaps; ++t) {
+            const int z = c.z + t / 9 - 1, y = c.y + (t / 3) % 3 - 1, x = c.x + t % 3 - 1;
+            nbr[(size_t)j * kTaps + t] =
+                inside(g, c.batch, z, y, x) ? grid[cell_of(g, c.batch, z, y, x)] : kEmpty;
+        }
+    }
+}
+
+// Strided conv: tap k of output site o reads input o * s - p + k.
+__global__ __launch_bounds__(256) void down_neighbors_kernel(const bf_coord4 *__restrict__ coords,
+                                                             const unsigned *__restrict__ count,
+                                                             Grid gin, Geom q,
+                                                             const int *__restrict__ grid,
+                                                             int *__restrict__ nbr) {
+    const unsigned n = *count;
+    const int taps = q.kd * q.kh * q.kw;
+    for (unsigned j = blockIdx.x * 256 + threadIdx.x; j < n; j += gridDim.x * 256) {
+        const bf_coord4 c = coords[j];
+        for (int t = 0; t < taps; ++t) {
+            const int kz = t / (q.kh * q.kw), ky = (t / q.kw) % q.kh, kx = t % q.kw;
+            const int z = c.z * q.sd - q.pd + kz, y = c.y * q.sh - q.ph + ky,
+                      x = c.x * q.sw - q.pw + kx;
+            nbr[(size_t)j * kTaps + t] =
+                inside(gin, c.batch, z, y, x) ? grid[cell_of(gin, c.batch, z, y, x)] : kEmpty;
+        }
+    }
+}
+
+// Marks every output cell some tap of an input site reaches (the exact
+// strided images of kernels_ref.c:632-644 / 686-707).
+__global__ __launch_bounds__(256) void mark_kernel(const bf_coord4 *__restrict__ coords,
+                                                   const unsigned *__restrict__ count, Grid gout,
+                                                   Geom q, int *__restrict__ grid) {
+    const unsigned n = *count;
+    for (unsigned j = blockIdx.x * 256 + threadIdx.x; j < n; j += gridDim.x * 256) {
+        const bf_coord4 c = coords[j];
+        for (int kz = 0; kz < q.kd; ++kz) {
+            const int nz = c.z + q.pd - kz;
+            if (nz < 0 || nz % q.sd || nz / q.sd >= gout.d) continue;
+            for (int ky = 0; ky < q.kh; ++ky) {
+                const int ny = c.y + q.ph - ky;
+                if (ny < 0 || ny % q.sh || ny / q.sh >= gout.h) continue;
+                for (int kx = 0; kx < q.kw; ++kx) {
+                    const int nx = c.x + q.pw - kx;
+                    if (nx < 0 || nx % q.sw || nx / q.sw >= gout.w) continue;
+                    if ((unsigned)c.batch < (unsigned)gout.b)
+                        grid[cell_of(gout, c.batch, nz / q.sd, ny / q.sh, nx / q.sw)] = kMarked;
+                }
+            }
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void compact_count_kernel(const int *__restrict__ grid,
+                                                            long long cells,
+                                                            unsigned *__restrict__ chunk_counts) {
+    __shared__ unsigned part[4];
+    const long long base = (long long)blockIdx.x * kChunk;
+    unsigned c = 0;
+    for (int r = 0; r < kChunk / 256; ++r) {
+        const long long i = base + r * 256 + threadIdx.x;
+        c += i < cells && grid[i] == kMarked;
+    }
+    for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = c;
+    __syncthreads();
+    if (threadIdx.x == 0) chunk_counts[blockIdx.x] = part[0] + part[1] + part[2] + part[3];
+}
+
+// In-order compaction of the marked cells: chunk c starts at the sum of the
+// earlier chunks' counts; inside a chunk, 32 rounds of 256 consecutive cells
+// are ranked by wave ballots.  Rows past the capacity are dropped.
+__global__ __launch_bounds__(256) void compact_write_kernel(
+    int *__restrict__ grid, long long cells, const unsigned *__restrict__ chunk_counts,
+    int chunks, unsigned capacity, Grid g, bf_coord4 *__restrict__ coords,
+    unsigned *__restrict__ count_out) {
+    __shared__ unsigned part[4], wave_base[4];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    unsigned before = 0, total = 0;
+    for (int c = t; c < chunks; c += 256) {
+        const unsigned v = chunk_counts[c];
+        before += c < (int)blockIdx.x ? v : 0u;
+        total += v;
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        before += __shfl_xor(before, o);
+        total += __shfl_xor(total, o);
+    }
+    if (lane == 0) {
+        part[wave] = before;
+        wave_base[wave] = total;
+    }
+    __syncthreads();
+    unsigned offset = part[0] + part[1] + part[2] + part[3];
+    if (blockIdx.x == 0 && t == 0) {
+        const unsigned all = wave_base[0] + wave_base[1] + wave_base[2] + wave_base[3];
+        *count_out = all < capacity ? all : capacity;
+    }
+    __syncthreads();
+    const long long base = (long long)blockIdx.x * kChunk;
+    for (int r = 0; r < kChunk / 256; ++r) {
+        const long long i = base + r * 256 + t;
+        const bool marked = i < cells && grid[i] == kMarked;
+        const uint64_t ballot = __ballot(marked);
+        if (lane == 0) part[wave] = (unsigned)__popcll(ballot);
+        __syncthreads();
+        unsigned wb = 0;
+        for (int w2 = 0; w2 < wave; ++w2) wb += part[w2];
+        const unsigned round_total = part[0] + part[1] + part[2] + part[3];
+        if (marked) {
+            const unsigned idx = offset + wb + (unsigned)__popcll(ballot & ((1ull << lane) - 1ull));
+            if (idx < capacity) {
+                grid[i] = (int)idx;
+                long long q = i;
+                const int x = (int)(q % g.w);
+                q /= g.w;
+                const int y = (int)(q % g.h);
+                q /= g.h;
+                const int z = (int)(q % g.d);
+                coords[idx] = bf_coord4{(int)(q / g.d), z, y, x};
+            } else {
+                grid[i] = kEmpty;
+            }
+        }
+        offset += round_total;
+        __syncthreads();
+    }
+}
+
+// Input SubM conv, 5 -> 16 channels, fp32 on the vector units; output fp16.
+__device__ __forceinline__ void split_store(float v, _Float16 *hi, _Float16 *lo) {
+    const _Float16 h = (_Float16)v;
+    *hi = h;
+    *lo = (_Float16)(v - (float)h);
+}
+
+__global__ __launch_bounds__(256) void conv_input_kernel(const int *__restrict__ nbr,
+                                                         const unsigned *__restrict__ count,
+                                                         const float *__restrict__ feat,
+                                                         const float *__restrict__ w,
+                                                         const float *__restrict__ bias,
+                                                         _Float16 *__restrict__ out_hi,
+                                                         _Float16 *__restrict__ out_lo) {
+    const unsigned n = *count;
+    for (unsigned j = blockIdx.x * 256 + threadIdx.x; j < n; j += gridDim.x * 256) {
+        float acc[16];
+#pragma unroll
+        for (int co = 0; co < 16; ++co) acc[co] = bias[co];
+        for (int t = 0; t < kTaps; ++t) {
+            const int src = nbr[(size_t)j * kTaps + t];
+            if (src < 0) continue;
+            const float *x = feat + (size_t)src * 5;
+#pragma unroll
+            for (int ci = 0; ci < 5; ++ci) {
+                const float xv = x[ci];
+#pragma unroll
+                for (int co = 0; co < 16; ++co) acc[co] = fmaf(xv, w[(t * 5 + ci) * 16 + co], acc[co]);
+            }
+        }
+        h8 hi[2], lo[2];
+#pragma unroll
+        for (int co = 0; co < 16; ++co) {
+            const float v = fmaxf(acc[co], 0.0f);
+            const _Float16 h = (_Float16)v;
+            hi[co >> 3][co & 7] = h;
+            lo[co >> 3][co & 7] = (_Float16)(v - (float)h);
+        }
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            *(h8 *)&out_hi[(size_t)j * 16 + 8 * q] = hi[q];
+            *(h8 *)&out_lo[(size_t)j * 16 + 8 * q] = lo[q];
+        }
+    }
+}
+
+template <int CI>
+struct KOp {
+    static constexpr int kb = CI >= 32 ? 32 : 16;  // k per MFMA
+    typedef typename std::conditional<(CI >= 32), h8, h4>::type frag;
+    static constexpr int per_lane = CI >= 32 ? 8 : 4;
+    __device__ static f32x4 mfma(frag a, frag b, f32x4 c) {
+        if constexpr (CI >= 32) return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+        else return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+    }
+};
+
+// Split fp16 feature planes of one level (rows x channels each).
+struct Feat {
+    _Float16 *hi, *lo;
+};
+
+// Gather GEMM: out[r][co] = bias[co] + sum_t sum_ci in[nbr[r][t]][ci] w[t][co][ci]
+// (+ identity[r][co]) (ReLU), operands split as hi + lo.  Each wave owns 32
+// rows (two 16-row MFMA tiles) x all CO columns; workgroups stride over the
+// rows.  out32, when set, receives fp32 rows instead of a split pair.
+template <int CI, int CO>
+__global__ __launch_bounds__(256) void sparse_conv_kernel(
+    const int *__restrict__ nbr, const unsigned *__restrict__ count, int taps, Feat in,
+    const _Float16 *__restrict__ w_hi, const _Float16 *__restrict__ w_lo,
+    const float *__restrict__ bias, Feat identity, int relu, Feat out,
+    float *__restrict__ out32) {
+    using K = KOp<CI>;
+    typedef typename K::frag frag;
+    constexpr int CT = CO / 16, KC = CI / K::kb;
+    const unsigned n = *count;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, col = lane & 15, g = lane >> 4;
+    for (unsigned base = blockIdx.x * kRowsPerGroup; base < n; base += gridDim.x * kRowsPerGroup) {
+        const unsigned row0 = base + wave * kRowsPerWave;
+        f32x4 acc[2][CT];
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) acc[rt][ct] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int t = 0; t < taps; ++t) {
+            int src[2];
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt) {
+                const unsigned r = row0 + 16 * rt + col;
+                src[rt] = r < n ? nbr[(size_t)r * kTaps + t] : kEmpty;
+            }
+            // Wave-uniform: a tap none of the wave's rows reaches adds nothing.
+            if (!__ballot(src[0] >= 0 || src[1] >= 0)) continue;
+#pragma unroll
+            for (int kc = 0; kc < KC; ++kc) {
+                const int k0 = kc * K::kb + g * K::per_lane;
+                frag ah[2], al[2];
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt) {
+                    if (src[rt] >= 0) {
+                        ah[rt] = *(const frag *)&in.hi[(size_t)src[rt] * CI + k0];
+                        al[rt] = *(const frag *)&in.lo[(size_t)src[rt] * CI + k0];
+                    } else {
+                        ah[rt] = frag{};
+                        al[rt] = frag{};
+                    }
+                }
+#pragma unroll
+                for (int ct = 0; ct < CT; ++ct) {
+                    const size_t wo = ((size_t)t * CO + 16 * ct + col) * CI + k0;
+                    const frag bh = *(const frag *)&w_hi[wo], bl = *(const frag *)&w_lo[wo];
+#pragma unroll
+                    for (int rt = 0; rt < 2; ++rt) {
+                        acc[rt][ct] = K::mfma(al[rt], bh, acc[rt][ct]);
+                        acc[rt][ct] = K::mfma(ah[rt], bl, acc[rt][ct]);
+                        acc[rt][ct] = K::mfma(ah[rt], bh, acc[rt][ct]);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) {
+            const int co = 16 * ct + col;
+            const float b = bias[co];
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const unsigned r = row0 + 16 * rt + 4 * g + j;
+                    if (r >= n) continue;
+                    const size_t at = (size_t)r * CO + co;
+                    float v = acc[rt][ct][j] + b;
+                    if (identity.hi) v += (float)identity.hi[at] + (float)identity.lo[at];
+                    if (relu) v = fmaxf(v, 0.0f);
+                    if (out32) out32[at] = v;
+                    else split_store(v, out.hi + at, out.lo + at);
+                }
+        }
+    }
+}
+
+// dense[b][c][z][y][x] = row features of the site at (b, z, y, x), else 0.
+__global__ __launch_bounds__(256) void dense_kernel(const int *__restrict__ grid, Grid g,
+                                                    const float *__restrict__ feat,
+                                                    float *__restrict__ dense) {
+    const size_t plane = (size_t)g.d * g.h * g.w, total = (size_t)g.b * 128 * plane;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < total;
+         i += (size_t)gridDim.x * 256) {
+        const size_t cell = i % plane, bc = i / plane, c = bc % 128, b = bc / 128;
+        const int idx = grid[b * plane + cell];
+        dense[i] = idx >= 0 ? feat[(size_t)idx * 128 + c] : 0.0f;
+    }
+}
+
+struct Conv {
+    const _Float16 *w_hi, *w_lo;
+    const float *w32, *bias;
+    int ci, co, taps;
+    Geom q;
+};
+
+}  // namespace
+
+struct bf_cuda_lidar_backbone {
+    size_t batches, capacity, resident_bytes;
+    Grid lv[5];
+    long long cells[5];
+    int max_chunks;
+    unsigned char *params, *work;
+    Conv input, res[4][2][2], down[3], out;
+    int *grid[5], *nbr;
+    bf_coord4 *coords[5];
+    unsigned *counts, *chunk_counts;
+    Feat feat[3];
+    float *out32;
+};
+
+namespace {
+
+int fold_layer(const bf_model *m, const char *wname, const char *bn, int ci, int co, int kd,
+               int kh, int kw, std::vector<float> &w, std::vector<float> &b, char *error,
+               size_t cap) {
+    const float *src = bind_f32(m, wname, {(uint32_t)kd, (uint32_t)kh, (uint32_t)kw,
+                                          (uint32_t)ci, (uint32_t)co}, error, cap);
+    if (!src) return 0;
+    static const char *suffix[4] = {"weight", "bias", "running_mean", "running_var"};
+    const float *p[4];
+    char name[192];
+    for (int i = 0; i < 4; ++i) {
+        std::snprintf(name, sizeof(name), "%s.%s", bn, suffix[i]);
+        if (!(p[i] = bind_f32(m, name, {(uint32_t)co}, error, cap))) return 0;
+    }
+    const int taps = kd * kh * kw;
+    w.assign((size_t)taps * ci * co, 0.0f);
+    b.assign(co, 0.0f);
+    for (int o = 0; o < co; ++o) {
+        // Eval BN folded as the reference GPU path (cuda_lidar.cu:41-43).
+        const float f = p[0][o] / std::sqrt(p[3][o] + kBnEps);
+        b[o] = p[1][o] - p[2][o] * f;
+        for (int t = 0; t < taps; ++t)
+            for (int i = 0; i < ci; ++i) w[((size_t)t * ci + i) * co + o] = src[((size_t)t * ci + i) * co + o] * f;
+    }
+    return 1;
+}
+
+int axis_out(int in, int k, int s, int p) { return in + 2 * p >= k ? (in + 2 * p - k) / s + 1 : 0; }
+
+int build(bf_cuda_lidar_backbone *n, const bf_model *m, char *error, size_t cap) {
+    struct Spec {
+        Conv *dst;
+        std::string w, bn;
+        int ci, co, kd, kh, kw, sd, sh, sw, pd, ph, pw;
+    };
+    std::vector<Spec> specs;
+    specs.push_back({&n->input, "backbone_3d.conv_input.0.weight", "backbone_3d.conv_input.1", 5,
+                     16, 3, 3, 3, 1, 1, 1, 1, 1, 1});
+    static const int ch[4] = {16, 32, 64, 128};
+    char w[160], bn[160];
+    for (int s = 0; s < 4; ++s)
+        for (int blk = 0; blk < 2; ++blk)
+            for (int c = 0; c < 2; ++c) {
+                // Layer table of reference cuda_lidar.cu:96-100.
+                std::snprintf(w, sizeof(w), "backbone_3d.conv%d.%d.conv%d.weight", s + 1,
+                              blk + (s ? 1 : 0), c + 1);
+                std::snprintf(bn, sizeof(bn), "backbone_3d.conv%d.%d.bn%d", s + 1,
+                              blk + (s ? 1 : 0), c + 1);
+                specs.push_back({&n->res[s][blk][c], w, bn, ch[s], ch[s], 3, 3, 3, 1, 1, 1, 1, 1, 1});
+            }
+    for (int t = 0; t < 3; ++t) {
+        std::snprintf(w, sizeof(w), "backbone_3d.conv%d.0.0.weight", t + 2);
+        std::snprintf(bn, sizeof(bn), "backbone_3d.conv%d.0.1", t + 2);
+        specs.push_back({&n->down[t], w, bn, ch[t], ch[t + 1], 3, 3, 3, 2, 2, 2, t == 2 ? 0 : 1, 1, 1});
+    }
+    specs.push_back({&n->out, "backbone_3d.conv_out.0.weight", "backbone_3d.conv_out.1", 128, 128,
+                     3, 1, 1, 2, 1, 1, 0, 0, 0});
+    ParamArena pa;
+    struct Off {
+        size_t w, w_lo, b;
+        bool f32;
+    };
+    std::vector<Off> offs;
+    for (const Spec &sp : specs) {
+        std::vector<float> wf, bf;
+        if (!fold_layer(m, sp.w.c_str(), sp.bn.c_str(), sp.ci, sp.co, sp.kd, sp.kh, sp.kw, wf, bf,
+                        error, cap))
+            return 0;
+        const int taps = sp.kd * sp.kh * sp.kw;
+        Off o{};
+        o.f32 = sp.ci == 5;
+        if (o.f32) {
+            o.w = pa.add_f32(wf);  // [tap][ci][co]
+        } else {
+            std::vector<float> t((size_t)taps * sp.co * sp.ci);  // [tap][co][ci]
+            for (int k = 0; k < taps; ++k)
+                for (int i = 0; i < sp.ci; ++i)
+                    for (int c = 0; c < sp.co; ++c)
+                        t[((size_t)k * sp.co + c) * sp.ci + i] = wf[((size_t)k * sp.ci + i) * sp.co + c];
+            // Split pair: hi = fp16(w), lo = fp16(w - hi).
+            std::vector<float> lo(t.size());
+            for (size_t i = 0; i < t.size(); ++i)
+                lo[i] = t[i] - (float)(_Float16)t[i];
+            o.w = pa.add_f16(t);
+            o.w_lo = pa.add_f16(lo);
+        }
+        o.b = pa.add_f32(bf);
+        offs.push_back(o);
+        *sp.dst = Conv{nullptr, nullptr, nullptr, nullptr, sp.ci, sp.co, taps,
+                       Geom{sp.kd, sp.kh, sp.kw, sp.sd, sp.sh, sp.sw, sp.pd, sp.ph, sp.pw}};
+    }
+    if (!hip_ok(hipMalloc((void **)&n->params, pa.host.size()), error, cap,
+                "allocate LiDAR weights") ||
+        !hip_ok(hipMemcpy(n->params, pa.host.data(), pa.host.size(), hipMemcpyHostToDevice), error,
+                cap, "upload LiDAR weights"))
+        return 0;
+    n->resident_bytes += pa.host.size();
+    for (size_t i = 0; i < specs.size(); ++i) {
+        Conv &c = *specs[i].dst;
+        if (offs[i].f32) c.w32 = (const float *)(n->params + offs[i].w);
+        else {
+            c.w_hi = (const _Float16 *)(n->params + offs[i].w);
+            c.w_lo = (const _Float16 *)(n->params + offs[i].w_lo);
+        }
+        c.bias = (const float *)(n->params + offs[i].b);
+    }
+    // Work buffers.
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t at = off;
+        off += (bytes + 255) & ~size_t(255);
+        return at;
+    };
+    size_t o_grid[5], o_coords[5];
+    long long max_cells = 0;
+    for (int l = 0; l < 5; ++l) {
+        o_grid[l] = take((size_t)n->cells[l] * sizeof(int));
+        o_coords[l] = take(n->capacity * sizeof(bf_coord4));
+        max_cells = std::max(max_cells, l ? n->cells[l] : 0);
+    }
+    n->max_chunks = (int)((max_cells + kChunk - 1) / kChunk);
+    const size_t o_nbr = take(n->capacity * kTaps * sizeof(int));
+    const size_t o_counts = take(8 * sizeof(unsigned));
+    const size_t o_chunks = take((size_t)std::max(n->max_chunks, 1) * sizeof(unsigned));
+    size_t o_feat[3];
+    for (int i = 0; i < 3; ++i) o_feat[i] = take(2 * n->capacity * 128 * sizeof(_Float16));
+    const size_t o_out = take(n->capacity * 128 * sizeof(float));
+    if (!hip_ok(hipMalloc((void **)&n->work, off), error, cap, "allocate LiDAR workspace"))
+        return 0;
+    n->resident_bytes += off;
+    unsigned char *a = n->work;
+    for (int l = 0; l < 5; ++l) {
+        n->grid[l] = (int *)(a + o_grid[l]);
+        n->coords[l] = (bf_coord4 *)(a + o_coords[l]);
+        // Every index grid is -1 between forwards.
+        if (!hip_ok(hipMemset(n->grid[l], 0xff, (size_t)n->cells[l] * sizeof(int)), error, cap,
+                    "clear LiDAR index grid"))
+            return 0;
+    }
+    n->nbr = (int *)(a + o_nbr);
+    n->counts = (unsigned *)(a + o_counts);
+    n->chunk_counts = (unsigned *)(a + o_chunks);
+    for (int i = 0; i < 3; ++i) {
+        n->feat[i].hi = (_Float16 *)(a + o_feat[i]);
+        n->feat[i].lo = n->feat[i].hi + n->capacity * 128;
+    }
+    n->out32 = (float *)(a + o_out);
+    return 1;
+}
+
+unsigned row_blocks(size_t capacity, int rows_per_block) {
+    return (unsigned)std::max<size_t>(1, std::min<size_t>(2048, (capacity + rows_per_block - 1) / rows_per_block));
+}
+
+void launch_conv(const bf_cuda_lidar_backbone *n, const Conv &c, const unsigned *count,
+                 Feat in, Feat identity, int relu, Feat out, float *out32, hipStream_t s) {
+    const unsigned blocks = row_blocks(n->capacity, kRowsPerGroup);
+#define BF_CONV(CI, CO)                                                                        \
+    if (c.ci == CI && c.co == CO) {                                                            \
+        sparse_conv_kernel<CI, CO><<<blocks, 256, 0, s>>>(n->nbr, count, c.taps, in, c.w_hi,  \
+                                                          c.w_lo, c.bias, identity, relu, out,  \
+                                                          out32);                               \
+        return;                                                                                \
+    }
+    BF_CONV(16, 16)
+    BF_CONV(16, 32)
+    BF_CONV(32, 32)
+    BF_CONV(32, 64)
+    BF_CONV(64, 64)
+    BF_CONV(64, 128)
+    BF_CONV(128, 128)
+#undef BF_CONV
+}
+
+// Marks and compacts the output sites of strided conv `c` from level l into
+// level l + 1, then builds its output -> input neighbour table.
+void strided_sites(bf_cuda_lidar_backbone *n, const Conv &c, int l, const bf_coord4 *in_coords,
+                   hipStream_t s) {
+    const unsigned rb = row_blocks(n->capacity, 256);
+    mark_kernel<<<rb, 256, 0, s>>>(in_coords, n->counts + l, n->lv[l + 1], c.q, n->grid[l + 1]);
+    const int chunks = (int)((n->cells[l + 1] + kChunk - 1) / kChunk);
+    compact_count_kernel<<<chunks, 256, 0, s>>>(n->grid[l + 1], n->cells[l + 1], n->chunk_counts);
+    compact_write_kernel<<<chunks, 256, 0, s>>>(n->grid[l + 1], n->cells[l + 1], n->chunk_counts,
+                                                chunks, (unsigned)n->capacity, n->lv[l + 1],
+                                                n->coords[l + 1], n->counts + l + 1);
+    down_neighbors_kernel<<<rb, 256, 0, s>>>(n->coords[l + 1], n->counts + l + 1, n->lv[l], c.q,
+                                             n->grid[l], n->nbr);
+}
+
+void forward_impl(bf_cuda_lidar_backbone *n, const bf_coord4 *coords, const float *feats,
+                  const unsigned *count_dev, unsigned count_host, float *dense, hipStream_t s) {
+    const unsigned rb = row_blocks(n->capacity, 256);
+    count_init_kernel<<<1, 1, 0, s>>>(count_dev, count_host, (unsigned)n->capacity, n->counts);
+    index_kernel<<<rb, 256, 0, s>>>(coords, n->counts, n->lv[0], n->grid[0]);
+    subm_neighbors_kernel<<<rb, 256, 0, s>>>(coords, n->counts, n->lv[0], n->grid[0], n->nbr);
+    conv_input_kernel<<<rb, 256, 0, s>>>(n->nbr, n->counts, feats, n->input.w32, n->input.bias,
+                                         n->feat[0].hi, n->feat[0].lo);
+    const Feat none{nullptr, nullptr};
+    int x = 0;
+    const bf_coord4 *level_coords = coords;
+    for (int st = 0; st < 4; ++st) {
+        const unsigned *cnt = n->counts + st;
+        if (st) {
+            strided_sites(n, n->down[st - 1], st - 1, level_coords, s);
+            const int y = (x + 1) % 3;
+            launch_conv(n, n->down[st - 1], cnt, n->feat[x], none, 1, n->feat[y], nullptr, s);
+            x = y;
+            level_coords = n->coords[st];
+            subm_neighbors_kernel<<<rb, 256, 0, s>>>(level_coords, cnt, n->lv[st], n->grid[st],
+                                                     n->nbr);
+        }
+        for (int blk = 0; blk < 2; ++blk) {
+            const int y = (x + 1) % 3, z = (x + 2) % 3;
+            launch_conv(n, n->res[st][blk][0], cnt, n->feat[x], none, 1, n->feat[y], nullptr, s);
+            launch_conv(n, n->res[st][blk][1], cnt, n->feat[y], n->feat[x], 1, n->feat[z], nullptr,
+                        s);
+            x = z;
+        }
+    }
+    strided_sites(n, n->out, 3, level_coords, s);
+    launch_conv(n, n->out, n->counts + 4, n->feat[x], none, 1, none, n->out32, s);
+    const size_t total = (size_t)128 * n->cells[4];
+    dense_kernel<<<(unsigned)std::min<size_t>(8192, (total + 255) / 256), 256, 0, s>>>(
+        n->grid[4], n->lv[4], n->out32, dense);
+    clear_kernel<<<rb, 256, 0, s>>>(coords, n->counts, n->lv[0], n->grid[0]);
+    for (int l = 1; l < 5; ++l)
+        clear_kernel<<<rb, 256, 0, s>>>(n->coords[l], n->counts + l, n->lv[l], n->grid[l]);
+}
+
+}  // namespace
+
+extern "C" void bf_cuda_lidar_backbone_destroy(bf_cuda_lidar_backbone *n) {
+    if (!n) return;
+    if (n->params) (void)hipFree(n->params);
+    if (n->work) (void)hipFree(n->work);
+    std::free(n);
+}
+
+extern "C" size_t bf_cuda_lidar_backbone_resident_bytes(const bf_cuda_lidar_backbone *n) {
+    return n ? n->resident_bytes : 0;
+}
+
+extern "C" int bf_cuda_lidar_backbone_create(const bf_model *model, size_t batches, size_t d,
+                                             size_t h, size_t w, size_t capacity,
+                                             bf_cuda_lidar_backbone **out, char *error,
+                                             size_t cap) {
+    if (out) *out = nullptr;
+    if (!model || !out || !batches || !d || !h || !w || !capacity || batches > INT_MAX ||
+        d > INT_MAX || h > INT_MAX || w > INT_MAX || capacity > UINT_MAX)
+        return fail(error, cap, "invalid HIP LiDAR contract");
+    if (capacity > (size_t)INT_MAX / kTaps)
+        return fail(error, cap, "HIP LiDAR capacity is too large");
+    bf_cuda_lidar_backbone *n = (bf_cuda_lidar_backbone *)std::calloc(1, sizeof(*n));
+    if (!n) return fail(error, cap, "HIP LiDAR allocation failed");
+    n->batches = batches;
+    n->capacity = capacity;
+    // Level shapes (lidar_backbone.c:147-162).
+    Grid g{(int)batches, (int)d, (int)h, (int)w};
+    n->lv[0] = g;
+    static const int pz[3] = {1, 1, 0};
+    for (int l = 1; l < 4; ++l) {
+        g = Grid{g.b, axis_out(g.d, 3, 2, pz[l - 1]), axis_out(g.h, 3, 2, 1), axis_out(g.w, 3, 2, 1)};
+        n->lv[l] = g;
+    }
+    n->lv[4] = Grid{g.b, axis_out(g.d, 3, 2, 0), g.h, g.w};
+    for (int l = 0; l < 5; ++l) {
+        if (n->lv[l].d <= 0 || n->lv[l].h <= 0 || n->lv[l].w <= 0) {
+            bf_cuda_lidar_backbone_destroy(n);
+            return fail(error, cap, "invalid HIP LiDAR output shape");
+        }
+        n->cells[l] = (long long)n->lv[l].b * n->lv[l].d * n->lv[l].h * n->lv[l].w;
+    }
+    if (!build(n, model, error, cap)) {
+        bf_cuda_lidar_backbone_destroy(n);
+        return 0;
+    }
+    *out = n;
+    return 1;
+}
+
+extern "C" int bf_cuda_lidar_backbone_forward(bf_cuda_lidar_backbone *n, const bf_coord4 *coords,
+                                              const float *feats, size_t count, float *dense,
+                                              void *stream, char *error, size_t cap) {
+    if (!n || !coords || !feats || !count || count > n->capacity || !dense)
+        return fail(error, cap, "invalid HIP LiDAR buffers");
+    forward_impl(n, coords, feats, nullptr, (unsigned)count, dense,
+                 reinterpret_cast<hipStream_t>(stream));
+    return launch_ok(error, cap, "HIP LiDAR launch");
+}
+
+extern "C" int bf_cuda_lidar_backbone_forward_count_device(bf_cuda_lidar_backbone *n,
+                                                           const bf_coord4 *coords,
+                                                           const float *feats,
+                                                           const unsigned *count, float *dense,
+                                                           void *stream, char *error,
+                                                           size_t cap) {
+    if (!n || !coords || !feats || !count || !dense)
+        return fail(error, cap, "invalid device-count HIP LiDAR buffers");
+    forward_impl(n, coords, feats, count, 0u, dense, reinterpret_cast<hipStream_t>(stream));
+    return launch_ok(error, cap, "HIP LiDAR launch");
+}

@@ -15,7 +15,8 @@ import bfhip
 
 ROOT = pathlib.Path(__file__).resolve().parent.parent
 HEADERS = ["bf_cuda_ops.h", "bf_cuda_swin.h", "bf_cuda_camera.h", "bf_cuda.h", "bf_cuda_bev.h",
-           "bf_cuda_transfusion.h", "bfhip_profile.h", "bfhip_debug.h"]
+           "bf_cuda_transfusion.h", "bf_cuda_depth_raster.h", "bf_cuda_voxel.h",
+           "bf_cuda_lidar.h", "bfhip_profile.h", "bfhip_debug.h"]
 
 
 def declared(header):
@@ -27,7 +28,7 @@ def declared(header):
 def test_every_declared_entry_point_is_exported():
     lib = bfhip.hip_lib()
     names = set().union(*(declared(h) for h in HEADERS))
-    assert len(names) == 36
+    assert len(names) == 49
     assert names == set(bfhip.SIGNATURES)
     missing = [n for n in sorted(names) if not hasattr(lib, n)]
     assert not missing, missing
@@ -204,3 +205,34 @@ def test_transfusion_rejects_invalid_contracts(tmp_path):
                                                      None, e, 256) == 0
     assert lib.bf_cuda_transfusion_resident_bytes(None) == 0
     lib.bf_cuda_transfusion_destroy(None)
+
+
+def test_lidar_side_rejects_invalid_contracts(tmp_path):
+    from bfhip import bfw
+    lib = bfhip.hip_lib()
+    e = _err()
+    out = C.c_void_p()
+    for args in ((0, 6, 256, 704), (10, 0, 256, 704), (1 << 33, 6, 256, 704)):
+        assert lib.bf_cuda_depth_raster_create(*args, C.byref(out), e, 256) == 0 and not out
+    assert lib.bf_cuda_depth_rasterize_f32(None, None, 0, None, None, None, None, None, e,
+                                           256) == 0
+    cfg = bfhip.voxel_config(100)
+    assert lib.bf_cuda_voxelizer_create(C.byref(cfg), 0, C.byref(out), e, 256) == 0
+    bad = bfhip.voxel_config(100, features=4)
+    assert lib.bf_cuda_voxelizer_create(C.byref(bad), 10, C.byref(out), e, 256) == 0
+    uneven = bfhip.voxel_config(100, size=(0.1234, 0.075, 0.2))
+    assert lib.bf_cuda_voxelizer_create(C.byref(uneven), 10, C.byref(out), e, 256) == 0
+    assert b"invalid" in e.value and not out
+    assert lib.bf_cuda_voxelize_mean_f32(None, None, 0, None, None, None, None, e, 256) == 0
+    path = bfw.write_lidar_backbone(tmp_path / "lidar.bfw", seed=0)
+    with bfhip.Model(path) as m:
+        for args in ((0, 41, 96, 96, 100), (1, 41, 96, 96, 0), (1, 2, 96, 96, 100)):
+            e.value = b""
+            assert lib.bf_cuda_lidar_backbone_create(m.handle, *args, C.byref(out), e, 256) == 0
+            assert b"invalid" in e.value and not out
+    assert lib.bf_cuda_lidar_backbone_forward(None, None, None, 0, None, None, e, 256) == 0
+    assert lib.bf_cuda_lidar_backbone_forward_count_device(None, None, None, None, None, None, e,
+                                                           256) == 0
+    for fn in ("depth_raster", "voxelizer", "lidar_backbone"):
+        assert getattr(lib, f"bf_cuda_{fn}_resident_bytes")(None) == 0
+        getattr(lib, f"bf_cuda_{fn}_destroy")(None)

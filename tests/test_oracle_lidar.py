@@ -20,6 +20,7 @@ import pytest
 
 import oracle
 from bfhip import bfw, frame_scene
+from util import clustered_sites as _sites
 
 pytestmark = []
 
@@ -122,17 +123,6 @@ def _dense_conv(coords, feats, weight, bias, d, h, w, stride, pad):
     wt = torch.from_numpy(weight.astype(np.float64)).permute(4, 3, 0, 1, 2).contiguous()
     b = None if bias is None else torch.from_numpy(bias.astype(np.float64))
     return F.conv3d(x, wt, b, stride=stride, padding=pad)[0].numpy()
-
-
-def _sites(seed, n, d, h, w):
-    rng = np.random.default_rng(seed)
-    # clustered sites so taps find neighbours
-    centres = rng.integers(0, [d, h, w], size=(6, 3))
-    pts = centres[rng.integers(0, 6, n)] + rng.integers(-2, 3, size=(n, 3))
-    pts = np.clip(pts, 0, [d - 1, h - 1, w - 1])
-    uniq = np.unique(pts, axis=0)
-    rng.shuffle(uniq)
-    return np.concatenate([np.zeros((len(uniq), 1), np.int32), uniq.astype(np.int32)], 1)
 
 
 @pytest.mark.parametrize("case", [

@@ -52,3 +52,15 @@ def assert_close(actual, expected, name="", rel_l2=REL_L2, max_abs_rms=MAX_ABS_R
     assert rl2 <= rel_l2, f"{name}: rel L2 {rl2:.3e} > {rel_l2:.1e}"
     assert mabs <= max_abs_rms * rms, f"{name}: max abs {mabs:.3e} > {max_abs_rms} x rms {rms:.3e}"
     return rl2, mabs / max(rms, 1e-30)
+
+
+def clustered_sites(seed, n, d, h, w):
+    """Unique sparse sites [M,4] (batch 0, z, y, x) in six clusters over a
+    d x h x w grid, shuffled, so convolution taps find neighbours."""
+    rng = np.random.default_rng(seed)
+    centres = rng.integers(0, [d, h, w], size=(6, 3))
+    pts = centres[rng.integers(0, 6, n)] + rng.integers(-2, 3, size=(n, 3))
+    pts = np.clip(pts, 0, [d - 1, h - 1, w - 1])
+    uniq = np.unique(pts, axis=0)
+    rng.shuffle(uniq)
+    return np.concatenate([np.zeros((len(uniq), 1), np.int32), uniq.astype(np.int32)], 1)
