@@ -69,6 +69,7 @@ def parse():
     p.add_argument("--no-bev", action="store_true", help="skip the BEV stage leg")
     p.add_argument("--no-tf", action="store_true", help="skip the TransFusion decoder leg")
     p.add_argument("--no-lidar", action="store_true", help="skip the LiDAR branch leg")
+    p.add_argument("--no-runtime", action="store_true", help="skip the full-frame runtime leg")
     return p.parse_args()
 
 
@@ -765,6 +766,62 @@ def lidar_cpu_baseline(path, pts):
             "cpu_model": _cpu_model()}
 
 
+# Reference CUDA runtime, real nuScenes mini frame, warm wall median
+# (reference docs/draft.md:262-266).
+RUNTIME_REFERENCE_MS = 142.381
+
+
+def runtime_leg(reps, seed=1):
+    """The full frame through bf_cuda_runtime_infer: host frame in (images,
+    100k points, calibration), detections out; wall-clock ms per frame with
+    the H2D copies, the graph replay and the D2H copy of the detections."""
+    import bfhip
+    from bfhip import bfw, frame_scene
+    tmp = pathlib.Path(tempfile.mkdtemp(prefix="rt_"))
+    path = bfw.write_full_model(tmp / "full.bfw", seed=seed)
+    frame = frame_scene.frame(seed, LIDAR_POINTS, sweeps=LIDAR_SWEEPS)
+    fi, keep = bfhip.frame_input(frame)
+    with bfhip.Runtime(path, 300000, LIDAR_VOXELS, LIDAR_SPARSE) as rt:
+        t0 = time.perf_counter()
+        dets = rt.infer(fi)
+        cold_ms = (time.perf_counter() - t0) * 1e3
+        for _ in range(3):
+            rt.infer(fi)
+        times = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            rt.infer(fi)
+            times.append((time.perf_counter() - t0) * 1e3)
+        resident = rt.resident_bytes()
+    times.sort()
+    ms = times[len(times) // 2]
+    h2d = sum(keep[k].nbytes for k in keep)
+    del keep
+    return {"workload": f"full frame: 6 x 3 x 256 x 704 images + {LIDAR_POINTS} points "
+                        f"({LIDAR_SWEEPS} sweeps) -> detections; random-init checkpoint "
+                        "(N(0, 1/fan_in) weights); one HIP graph per frame",
+            "ms": round(ms, 3), "ms_min": round(times[0], 3), "cold_ms": round(cold_ms, 1),
+            "detections": dets.count, "h2d_mib": round(h2d / 2**20, 1),
+            "resident_mib": round(resident / 2**20, 1),
+            "reference_rtx4060ti_ms": RUNTIME_REFERENCE_MS,
+            "speedup_vs_reference": round(RUNTIME_REFERENCE_MS / ms, 1)}, (path, frame)
+
+
+def runtime_cpu_baseline(path, frame):
+    """The reference's CPU frame runtime (oracle/_ref: src/runtime.c and its
+    modules, OpenMP) on the same frame."""
+    import oracle
+    kind = "reference" if oracle.available("ref") else "port"
+    o = oracle.Oracle("ref" if kind == "reference" else "port")
+    t0 = time.perf_counter()
+    o.runtime_infer(path, frame, 300000, LIDAR_VOXELS, LIDAR_SPARSE)
+    t1 = time.perf_counter()
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or os.cpu_count()
+    return {"value": round((t1 - t0) * 1e3, 1), "unit": "ms/frame", "cores": threads,
+            "kind": kind, "backend": o.backend(), "sample": "the same full frame, once",
+            "cpu_model": _cpu_model()}
+
+
 def cpu_baseline(model_path, cameras):
     """Reference CPU path (oracle/_ref, the reference's C compiled from its own
     sources, OpenMP) on a bounded sample of `cameras` cameras, scaled to a
@@ -929,6 +986,11 @@ def main():
         if not args.no_cpu:
             lidar["cpu_baseline"] = lidar_cpu_baseline(lidar_path, lidar_pts)
         result["lidar"] = lidar
+    if not args.no_runtime:
+        rt, (rt_path, rt_frame) = runtime_leg(max(args.steps, 10))
+        if not args.no_cpu:
+            rt["cpu_baseline"] = runtime_cpu_baseline(rt_path, rt_frame)
+        result["runtime"] = rt
     print(json.dumps(result))
 
 

@@ -79,6 +79,30 @@ class VoxelConfig(C.Structure):
                 ("max_points_per_voxel", _sz), ("max_voxels", _sz)]
 
 
+class FrameInput(C.Structure):
+    """``bf_frame_input`` (include/bf_runtime.h)."""
+    _fields_ = [("camera_images", C.c_void_p), ("points", C.c_void_p), ("point_count", C.c_size_t),
+                ("camera_intrinsics_6x16", C.c_void_p), ("camera_to_lidar_6x16", C.c_void_p),
+                ("image_augmentation_6x16", C.c_void_p), ("lidar_augmentation_16", C.c_void_p),
+                ("lidar_to_image_6x16", C.c_void_p)]
+
+
+FRAME_KEYS = ("images", "points", "camera_intrinsics", "camera_to_lidar", "image_augmentation",
+              "lidar_augmentation", "lidar_to_image")
+
+
+def frame_input(frame):
+    """A FrameInput over a dict of host float32 arrays (frame_scene.frame
+    layout); returns (FrameInput, arrays kept alive by the caller)."""
+    import numpy as np
+    arrs = {k: np.ascontiguousarray(frame[k], np.float32) for k in FRAME_KEYS}
+    ptr = lambda k: arrs[k].ctypes.data
+    fi = FrameInput(ptr("images"), ptr("points"), arrs["points"].shape[0],
+                    ptr("camera_intrinsics"), ptr("camera_to_lidar"), ptr("image_augmentation"),
+                    ptr("lidar_augmentation"), ptr("lidar_to_image"))
+    return fi, arrs
+
+
 def voxel_config(max_voxels, minimum=(-54.0, -54.0, -5.0), maximum=(54.0, 54.0, 3.0),
                  size=(0.075, 0.075, 0.2), features=5, max_points=10):
     """The reference runtime's voxel contract (runtime.c:262-265) by default."""
@@ -145,6 +169,13 @@ SIGNATURES = {
     "bf_cuda_lidar_backbone_forward": (_i, [_vp, _vp, _vp, _sz, _vp, _vp, C.c_char_p, _sz]),
     "bf_cuda_lidar_backbone_forward_count_device": (_i, [_vp, _vp, _vp, _vp, _vp, _vp,
                                                          C.c_char_p, _sz]),
+    "bf_cuda_runtime_create": (_i, [C.c_char_p, _sz, _sz, _sz, C.POINTER(_vp), C.c_char_p, _sz]),
+    "bf_cuda_runtime_destroy": (None, [_vp]),
+    "bf_cuda_runtime_infer": (_i, [_vp, C.POINTER(FrameInput), C.POINTER(Detections),
+                                   C.c_char_p, _sz]),
+    "bf_cuda_runtime_resident_bytes": (_sz, [_vp]),
+    "bf_cuda_runtime_debug_bev_stats": (_i, [_vp, C.POINTER(C.c_float), C.c_char_p, _sz]),
+    "bf_cuda_runtime_debug_hashes": (_i, [_vp, C.POINTER(C.c_ulonglong), C.c_char_p, _sz]),
 }
 
 SWIN_OPS = ("ln1", "qkv", "attention", "proj", "ln2", "fc1", "fc2", "merge", "mlp")
@@ -159,6 +190,10 @@ MODEL_SIGNATURES = {
     "bf_model_validate_tensor": (_i, [_vp, _vp, C.c_char_p, _sz]),
     "bf_model_validate_all": (_i, [_vp, C.c_char_p, _sz]),
     "bf_dtype_name": (C.c_char_p, [C.c_uint32]),
+    "bf_frame_open": (_i, [C.c_char_p, C.POINTER(_vp), C.c_char_p, _sz]),
+    "bf_frame_close": (None, [_vp]),
+    "bf_frame_input_view": (C.POINTER(FrameInput), [_vp]),
+    "bf_frame_file_bytes": (_sz, [_vp]),
 }
 
 _model_lib = None
@@ -813,3 +848,62 @@ class LidarBackbone(_Context):
                 _ptr(out), _stream(stream), err, 512)
         _check(ok, err, "bf_cuda_lidar_backbone_forward")
         return out
+
+
+class FrameFile(_Context):
+    """A BFI frame mapped by libbfmodel.so (include/bf_frame.h)."""
+    _destroy = "bf_frame_close"
+
+    def __init__(self, path):
+        self.lib = model_lib()
+        self.handle, err = _vp(), _err()
+        _check(self.lib.bf_frame_open(str(path).encode(), C.byref(self.handle), err, 512), err,
+               "bf_frame_open")
+
+    @property
+    def input(self) -> FrameInput:
+        return self.lib.bf_frame_input_view(self.handle).contents
+
+    def bytes(self):
+        return self.lib.bf_frame_file_bytes(self.handle)
+
+
+class Runtime(_Context):
+    """bf_cuda_runtime (include/bf_cuda_runtime.h): BFW checkpoint in, host
+    frame in, canonical detections out."""
+    _destroy = "bf_cuda_runtime_destroy"
+
+    def __init__(self, model_path, point_capacity=300000, voxel_capacity=160000,
+                 sparse_capacity=160000):
+        self.lib = hip_lib()
+        self.handle, err = _vp(), _err()
+        _check(self.lib.bf_cuda_runtime_create(str(model_path).encode(), point_capacity,
+                                               voxel_capacity, sparse_capacity,
+                                               C.byref(self.handle), err, 512),
+               err, "bf_cuda_runtime_create")
+
+    def resident_bytes(self):
+        return self.lib.bf_cuda_runtime_resident_bytes(self.handle)
+
+    def infer(self, frame) -> Detections:
+        """frame: a FrameInput, or a dict of host arrays (frame_scene.frame)."""
+        keep = None
+        if not isinstance(frame, FrameInput):
+            frame, keep = frame_input(frame)
+        dets, err = Detections(), _err()
+        _check(self.lib.bf_cuda_runtime_infer(self.handle, C.byref(frame), C.byref(dets), err,
+                                              512), err, "bf_cuda_runtime_infer")
+        del keep
+        return dets
+
+    def debug_bev_stats(self):
+        out, err = (C.c_float * 4)(), _err()
+        _check(self.lib.bf_cuda_runtime_debug_bev_stats(self.handle, out, err, 512), err,
+               "bf_cuda_runtime_debug_bev_stats")
+        return list(out)
+
+    def debug_hashes(self):
+        out, err = (C.c_ulonglong * 11)(), _err()
+        _check(self.lib.bf_cuda_runtime_debug_hashes(self.handle, out, err, 512), err,
+               "bf_cuda_runtime_debug_hashes")
+        return list(out)

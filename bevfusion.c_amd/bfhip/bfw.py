@@ -412,6 +412,23 @@ def write_bev_stage(path, seed: int = 0, mode: str = "baseline", gain: float = 1
     return path
 
 
+def full_model_tensors(seed: int = 0, mode: str = "fan_in", gain: float = 1.0):
+    """Every tensor the frame runtime binds: Swin-T, camera neck (FPN, depth
+    head, LSS downsample), SECOND encoder, BEV stage, TransFusion head and the
+    LSS frustum vtransform.frustum [118,32,88,3]."""
+    from . import frame_scene
+    init = _Init(seed, mode, gain)
+    return (swin_tensors(init) + neck_tensors(init) + lidar_backbone_tensors(init) +
+            bev_stage_tensors(init) + transfusion_tensors(init) +
+            [("vtransform.frustum", frame_scene.frustum())])
+
+
+def write_full_model(path, seed: int = 0, mode: str = "fan_in", gain: float = 1.0) -> pathlib.Path:
+    path = pathlib.Path(path)
+    write_bfw(full_model_tensors(seed, mode, gain), path)
+    return path
+
+
 def synthetic_bev(seed: int, height=180, width=180, batches=1) -> np.ndarray:
     """Fused BEV input [B, 336, H, W] ~N(0,1): 80 image channels, then 256 lidar."""
     return randn(seed, "bev_input", (batches, 336, height, width))

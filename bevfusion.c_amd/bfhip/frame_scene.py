@@ -61,13 +61,54 @@ def calibration(seed: int = 0) -> dict:
                 lidar_to_image=f32(lidar_to_image))
 
 
+def frustum(bins: int = 118, height: int = 32, width: int = 88) -> np.ndarray:
+    """The LSS frustum [D,H,W,3] of (pixel x, pixel y, depth): feature columns
+    and rows spread evenly over the 704 x 256 image, depth bins 1.0 + 0.5 k m
+    (the checkpoint's vtransform.frustum for dbound [1, 60, 0.5])."""
+    xs = np.linspace(0.0, IMAGE_W - 1, width, dtype=np.float32)
+    ys = np.linspace(0.0, IMAGE_H - 1, height, dtype=np.float32)
+    ds = (1.0 + 0.5 * np.arange(bins)).astype(np.float32)
+    f = np.stack(np.broadcast_arrays(xs.reshape(1, 1, width), ys.reshape(1, height, 1),
+                                     ds.reshape(bins, 1, 1)), -1)
+    return np.ascontiguousarray(f, np.float32)
+
+
+BFI_FIELDS = ("images", "points", "camera_intrinsics", "camera_to_lidar", "image_augmentation",
+              "lidar_augmentation", "lidar_to_image")
+
+
+def write_bfi(frame: dict, path) -> int:
+    """Pack a frame as a BFI file (layout in include/bf_frame.h): 128-byte
+    little-endian header, then the seven float32 payloads densely in order,
+    CRC-32 of the payload in the header.  Returns the file size."""
+    import struct
+    import zlib
+    parts = [np.ascontiguousarray(frame[k], "<f4").tobytes() for k in BFI_FIELDS]
+    points = frame["points"].shape[0]
+    offsets, at = [], 128
+    for part in parts:
+        offsets.append(at)
+        at += len(part)
+    crc = 0
+    for part in parts:
+        crc = zlib.crc32(part, crc)
+    header = struct.pack("<4sIIIQQII7Q", b"BFI1", 1, 128, 0, at, points, crc & 0xffffffff, 0,
+                         *offsets)
+    header += bytes(128 - len(header))
+    with open(path, "wb") as f:
+        f.write(header)
+        for part in parts:
+            f.write(part)
+    return at
+
+
 def images(seed: int) -> np.ndarray:
     raw = bfw.randu(seed, "frame_images", (CAMERAS, IMAGE_H, IMAGE_W, 3))
     return np.ascontiguousarray(((raw - _MEAN) / _STD).transpose(0, 3, 1, 2).astype(np.float32))
 
 
-def frame(seed: int = 0, points: int = 60000) -> dict:
+def frame(seed: int = 0, points: int = 60000, sweeps: int = 1) -> dict:
     out = calibration(seed)
     out["images"] = images(seed)
-    out["points"] = bfw.synthetic_points(seed, points)
+    out["points"] = bfw.synthetic_points(seed, points, sweeps=sweeps)
     return out

@@ -1,7 +1,7 @@
 """Build recipe for the native libraries (invoked by __graft_entry__.build()).
 
 Products (in-tree, next to their sources, so they travel with the tree):
-  bevfusion.c_amd/lib/libbfmodel.so  BFW container reader (C11, gcc)
+  bevfusion.c_amd/lib/libbfmodel.so  BFW checkpoint and BFI frame readers (C11, gcc)
   bevfusion.c_amd/lib/libbfhip.so    gfx950 HIP kernels + the C-ABI entry points
 Test infrastructure (built by the same call, never linked by the products):
   oracle/_build/liboracle*.so        CPU restatement of the reference path
@@ -50,7 +50,7 @@ def build_model_lib() -> pathlib.Path:
     LIB.mkdir(exist_ok=True)
     out = LIB / "libbfmodel.so"
     _run(["gcc", "-O2", "-std=c11", "-fPIC", "-shared", "-Wall", "-Wextra", f"-I{INCLUDE}",
-          str(CSRC / "bfw_model.c"), "-o", str(out)])
+          str(CSRC / "bfw_model.c"), str(CSRC / "bfi_frame.c"), "-o", str(out)])
     return out
 
 

@@ -9,6 +9,7 @@
 // reads the winner's depth and clears the owner word for the next call.
 #include "bf_cuda_depth_raster.h"
 #include "hip_common.h"
+#include "internal.h"
 
 #include <cfloat>
 #include <climits>
@@ -46,13 +47,15 @@ __global__ void inverse_kernel(const float *__restrict__ m, float *__restrict__ 
 }
 
 __global__ __launch_bounds__(256) void project_kernel(
-    const float *__restrict__ points, unsigned count, int cameras, int height, int width,
+    const float *__restrict__ points, const unsigned *__restrict__ count_device, unsigned count,
+    int cameras, int height, int width,
     const float *__restrict__ aug, const float *__restrict__ inv, const int *__restrict__ valid,
     const float *__restrict__ l2i, const float *__restrict__ post, unsigned *__restrict__ owners,
     float *__restrict__ distances) {
 #pragma clang fp contract(off)
     const size_t item = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (item >= (size_t)count * cameras || !*valid) return;
+    const unsigned n = count_device ? min(*count_device, count) : count;
+    if (item >= (size_t)n * cameras || !*valid) return;
     const unsigned p = (unsigned)(item / cameras);
     const int cam = (int)(item % cameras);
     const float *pt = points + (size_t)p * 5;
@@ -151,11 +154,12 @@ extern "C" int bf_cuda_depth_raster_create(size_t max_points, size_t cameras, si
     return 1;
 }
 
-extern "C" int bf_cuda_depth_rasterize_f32(bf_cuda_depth_raster *r, const float *points,
-                                           size_t point_count, const float *lidar_aug,
-                                           const float *lidar_to_image, const float *image_aug,
-                                           float *depth, void *stream_value, char *error,
-                                           size_t cap) {
+namespace {
+
+// point_count is the exact count, or with count_device the bound of *count_device.
+int rasterize(bf_cuda_depth_raster *r, const float *points, const unsigned *count_device,
+              size_t point_count, const float *lidar_aug, const float *lidar_to_image,
+              const float *image_aug, float *depth, void *stream_value, char *error, size_t cap) {
     if (!r || (!points && point_count) || point_count > r->max_points || !lidar_aug ||
         !lidar_to_image || !image_aug || !depth)
         return fail(error, cap, "invalid HIP depth raster buffers");
@@ -164,10 +168,31 @@ extern "C" int bf_cuda_depth_rasterize_f32(bf_cuda_depth_raster *r, const float 
     const size_t items = point_count * r->cameras;
     if (items)
         project_kernel<<<(unsigned)((items + 255) / 256), 256, 0, s>>>(
-            points, (unsigned)point_count, (int)r->cameras, (int)r->height, (int)r->width,
-            lidar_aug, r->inverse, r->valid, lidar_to_image, image_aug, r->owners, r->distances);
+            points, count_device, (unsigned)point_count, (int)r->cameras, (int)r->height,
+            (int)r->width, lidar_aug, r->inverse, r->valid, lidar_to_image, image_aug, r->owners,
+            r->distances);
     const size_t plane = r->height * r->width, pixels = plane * r->cameras;
     materialize_kernel<<<(unsigned)((pixels + 255) / 256), 256, 0, s>>>(
         r->owners, r->distances, (int)r->cameras, plane, depth);
     return launch_ok(error, cap, "HIP depth raster launch");
+}
+
+}  // namespace
+
+extern "C" int bf_cuda_depth_rasterize_f32(bf_cuda_depth_raster *r, const float *points,
+                                           size_t point_count, const float *lidar_aug,
+                                           const float *lidar_to_image, const float *image_aug,
+                                           float *depth, void *stream, char *error, size_t cap) {
+    return rasterize(r, points, nullptr, point_count, lidar_aug, lidar_to_image, image_aug, depth,
+                     stream, error, cap);
+}
+
+int bfhip::depth_rasterize_count_device(bf_cuda_depth_raster *r, const float *points,
+                                        const unsigned *count_device, size_t bound,
+                                        const float *lidar_aug, const float *lidar_to_image,
+                                        const float *image_aug, float *depth, void *stream,
+                                        char *error, size_t cap) {
+    if (!count_device || !points) return fail(error, cap, "invalid HIP depth raster buffers");
+    return rasterize(r, points, count_device, bound, lidar_aug, lidar_to_image, image_aug, depth,
+                     stream, error, cap);
 }

@@ -45,6 +45,7 @@
 //                     read them coalesced).
 #include "bf_cuda_transfusion.h"
 #include "host_util.h"
+#include "internal.h"
 
 #include <algorithm>
 #include <cfloat>
@@ -1284,6 +1285,18 @@ extern "C" int bf_cuda_transfusion_forward(bf_cuda_transfusion *d, const float *
     tail_kernel<<<P, 256, 0, s>>>(d->prm, d->part_m, d->part_l, d->part_o, d->splits, P, W,
                                   d->query, out->query_indices_bp, *out);
     return launch_ok(error, cap, "HIP TransFusion launch");
+}
+
+int bfhip::transfusion_decode_launch(bf_cuda_transfusion *d, const bf_transfusion_raw_outputs *out,
+                                     float threshold, void *stream_value,
+                                     const bf_detections **device_detections, char *error,
+                                     size_t cap) {
+    if (!d || !device_detections || !std::isfinite(threshold) || !outputs_ok(out))
+        return fail(error, cap, "invalid HIP detection decode contract");
+    decode_kernel<<<1, 256, 0, reinterpret_cast<hipStream_t>(stream_value)>>>(
+        *out, (int)d->proposals, threshold, d->detections);
+    *device_detections = d->detections;
+    return launch_ok(error, cap, "HIP detection decode launch");
 }
 
 extern "C" int bf_cuda_transfusion_decode_detections(bf_cuda_transfusion *d,

@@ -22,6 +22,7 @@
 //      cell words are reset for the next call.
 #include "bf_cuda_voxel.h"
 #include "hip_common.h"
+#include "internal.h"
 
 #include <algorithm>
 #include <climits>
@@ -42,12 +43,20 @@ struct VoxelGeom {
     unsigned max_voxels;
 };
 
+__global__ void count_init_kernel(const unsigned *__restrict__ src, unsigned host, unsigned bound,
+                                  unsigned *__restrict__ dst) {
+    if (threadIdx.x || blockIdx.x) return;
+    const unsigned n = src ? *src : host;
+    *dst = n < bound ? n : bound;
+}
+
 __global__ __launch_bounds__(256) void key_kernel(const float *__restrict__ points,
-                                                  unsigned count, VoxelGeom g,
+                                                  const unsigned *__restrict__ count_word,
+                                                  VoxelGeom g,
                                                   unsigned *__restrict__ keys,
                                                   unsigned *__restrict__ first) {
     const unsigned i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= count) return;
+    if (i >= *count_word) return;
     const float *p = points + (size_t)i * 5;
     bool ok = isfinite(p[0]) && isfinite(p[1]) && isfinite(p[2]) && isfinite(p[3]) &&
               isfinite(p[4]);
@@ -98,8 +107,9 @@ __device__ __forceinline__ bool is_head(const unsigned *keys, const unsigned *fi
 // Head flags per tile of kTile points -> tile sums.
 __global__ __launch_bounds__(256) void flag_kernel(const unsigned *__restrict__ keys,
                                                    const unsigned *__restrict__ first,
-                                                   unsigned count, unsigned *__restrict__ sums) {
-    const unsigned base = blockIdx.x * kTile + threadIdx.x * 4;
+                                                   const unsigned *__restrict__ count_word,
+                                                   unsigned *__restrict__ sums) {
+    const unsigned count = *count_word, base = blockIdx.x * kTile + threadIdx.x * 4;
     unsigned c = 0;
 #pragma unroll
     for (int k = 0; k < 4; ++k)
@@ -128,12 +138,12 @@ __global__ __launch_bounds__(256) void sums_kernel(unsigned *__restrict__ sums, 
 // Ranks of the head points; a kept voxel gets its coordinate and empty slots.
 __global__ __launch_bounds__(256) void rank_kernel(const unsigned *__restrict__ keys,
                                                    const unsigned *__restrict__ first,
-                                                   unsigned count,
+                                                   const unsigned *__restrict__ count_word,
                                                    const unsigned *__restrict__ offsets,
                                                    VoxelGeom g, unsigned *__restrict__ rank,
                                                    bf_coord4 *__restrict__ coords,
                                                    unsigned *__restrict__ slots) {
-    const unsigned base = blockIdx.x * kTile + threadIdx.x * 4;
+    const unsigned count = *count_word, base = blockIdx.x * kTile + threadIdx.x * 4;
     bool head[4];
     unsigned c = 0;
 #pragma unroll
@@ -160,10 +170,10 @@ __global__ __launch_bounds__(256) void rank_kernel(const unsigned *__restrict__ 
 __global__ __launch_bounds__(256) void insert_kernel(const unsigned *__restrict__ keys,
                                                      const unsigned *__restrict__ first,
                                                      const unsigned *__restrict__ rank,
-                                                     unsigned count, VoxelGeom g,
-                                                     unsigned *__restrict__ slots) {
+                                                     const unsigned *__restrict__ count_word,
+                                                     VoxelGeom g, unsigned *__restrict__ slots) {
     const unsigned i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= count) return;
+    if (i >= *count_word) return;
     const unsigned key = keys[i];
     if (key == kInvalid) return;
     const unsigned v = rank[first[key]];
@@ -197,9 +207,10 @@ __global__ __launch_bounds__(256) void mean_kernel(const float *__restrict__ poi
 }
 
 __global__ __launch_bounds__(256) void clear_kernel(const unsigned *__restrict__ keys,
-                                                    unsigned count, unsigned *__restrict__ first) {
+                                                    const unsigned *__restrict__ count_word,
+                                                    unsigned *__restrict__ first) {
     const unsigned i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= count) return;
+    if (i >= *count_word) return;
     const unsigned key = keys[i];
     if (key != kInvalid) first[key] = kEmpty;
 }
@@ -213,13 +224,13 @@ __global__ void zero_count_kernel(unsigned *__restrict__ out) {
 struct bf_cuda_voxelizer {
     VoxelGeom geom;
     size_t max_points, resident_bytes;
-    unsigned *keys, *first, *rank, *sums, *slots;
+    unsigned *keys, *first, *rank, *sums, *slots, *count_word;
 };
 
 extern "C" void bf_cuda_voxelizer_destroy(bf_cuda_voxelizer *v) {
     if (!v) return;
     for (void *p : {(void *)v->keys, (void *)v->first, (void *)v->rank, (void *)v->sums,
-                    (void *)v->slots})
+                    (void *)v->slots, (void *)v->count_word})
         if (p) (void)hipFree(p);
     std::free(v);
 }
@@ -261,9 +272,9 @@ extern "C" int bf_cuda_voxelizer_create(const bf_voxel_config *cfg, size_t max_p
     v->max_points = max_points;
     const size_t n = max_points, tiles = (n + kTile - 1) / kTile;
     const size_t slot_words = (size_t)g.max_voxels * g.max_points;
-    const size_t bytes[5] = {n * 4, (size_t)cells * 4, n * 4, tiles * 4, slot_words * 4};
-    unsigned **bufs[5] = {&v->keys, &v->first, &v->rank, &v->sums, &v->slots};
-    for (int b = 0; b < 5; ++b) {
+    const size_t bytes[6] = {n * 4, (size_t)cells * 4, n * 4, tiles * 4, slot_words * 4, 4};
+    unsigned **bufs[6] = {&v->keys, &v->first, &v->rank, &v->sums, &v->slots, &v->count_word};
+    for (int b = 0; b < 6; ++b) {
         if (!hip_ok(hipMalloc((void **)bufs[b], bytes[b]), error, cap, "allocate voxel buffers")) {
             bf_cuda_voxelizer_destroy(v);
             return 0;
@@ -280,10 +291,12 @@ extern "C" int bf_cuda_voxelizer_create(const bf_voxel_config *cfg, size_t max_p
     return 1;
 }
 
-extern "C" int bf_cuda_voxelize_mean_f32(bf_cuda_voxelizer *v, const float *points,
-                                         size_t count, bf_coord4 *coords, float *means,
-                                         unsigned *voxel_count, void *stream_value, char *error,
-                                         size_t cap) {
+namespace {
+
+// count is the exact point count, or with count_device the bound of *count_device.
+int voxelize(bf_cuda_voxelizer *v, const float *points, const unsigned *count_device,
+             size_t count, bf_coord4 *coords, float *means, unsigned *voxel_count,
+             void *stream_value, char *error, size_t cap) {
     if (!v || (!points && count) || count > v->max_points || !coords || !means || !voxel_count)
         return fail(error, cap, "invalid HIP voxelize buffers");
     const hipStream_t s = reinterpret_cast<hipStream_t>(stream_value);
@@ -293,13 +306,32 @@ extern "C" int bf_cuda_voxelize_mean_f32(bf_cuda_voxelizer *v, const float *poin
         return launch_ok(error, cap, "HIP voxelize launch");
     }
     const VoxelGeom &g = v->geom;
-    key_kernel<<<blocks, 256, 0, s>>>(points, n, g, v->keys, v->first);
-    flag_kernel<<<tiles, 256, 0, s>>>(v->keys, v->first, n, v->sums);
+    count_init_kernel<<<1, 64, 0, s>>>(count_device, n, n, v->count_word);
+    key_kernel<<<blocks, 256, 0, s>>>(points, v->count_word, g, v->keys, v->first);
+    flag_kernel<<<tiles, 256, 0, s>>>(v->keys, v->first, v->count_word, v->sums);
     sums_kernel<<<1, 256, 0, s>>>(v->sums, tiles, g.max_voxels, voxel_count);
-    rank_kernel<<<tiles, 256, 0, s>>>(v->keys, v->first, n, v->sums, g, v->rank, coords, v->slots);
-    insert_kernel<<<blocks, 256, 0, s>>>(v->keys, v->first, v->rank, n, g, v->slots);
-    const unsigned vblocks = (unsigned)std::min<size_t>((g.max_voxels + 255) / 256, (n + 255) / 256);
+    rank_kernel<<<tiles, 256, 0, s>>>(v->keys, v->first, v->count_word, v->sums, g, v->rank,
+                                      coords, v->slots);
+    insert_kernel<<<blocks, 256, 0, s>>>(v->keys, v->first, v->rank, v->count_word, g, v->slots);
+    const unsigned vblocks = (unsigned)std::min<size_t>((g.max_voxels + 255) / 256, blocks);
     mean_kernel<<<vblocks, 256, 0, s>>>(points, v->slots, voxel_count, g.max_points, means);
-    clear_kernel<<<blocks, 256, 0, s>>>(v->keys, n, v->first);
+    clear_kernel<<<blocks, 256, 0, s>>>(v->keys, v->count_word, v->first);
     return launch_ok(error, cap, "HIP voxelize launch");
+}
+
+}  // namespace
+
+extern "C" int bf_cuda_voxelize_mean_f32(bf_cuda_voxelizer *v, const float *points,
+                                         size_t count, bf_coord4 *coords, float *means,
+                                         unsigned *voxel_count, void *stream, char *error,
+                                         size_t cap) {
+    return voxelize(v, points, nullptr, count, coords, means, voxel_count, stream, error, cap);
+}
+
+int bfhip::voxelize_count_device(bf_cuda_voxelizer *v, const float *points,
+                                 const unsigned *count_device, size_t bound, bf_coord4 *coords,
+                                 float *means, unsigned *voxel_count, void *stream, char *error,
+                                 size_t cap) {
+    if (!count_device || !points || !bound) return fail(error, cap, "invalid HIP voxelize buffers");
+    return voxelize(v, points, count_device, bound, coords, means, voxel_count, stream, error, cap);
 }

@@ -120,6 +120,14 @@ class Detections(C.Structure):
     _fields_ = [("items", Detection * 200), ("count", C.c_int)]
 
 
+class FrameInput(C.Structure):
+    """bf_frame_input (reference include/bf_runtime.h:14-27)."""
+    _fields_ = [("camera_images", C.c_void_p), ("points", C.c_void_p),
+                ("point_count", C.c_size_t), ("camera_intrinsics_6x16", C.c_void_p),
+                ("camera_to_lidar_6x16", C.c_void_p), ("image_augmentation_6x16", C.c_void_p),
+                ("lidar_augmentation_16", C.c_void_p), ("lidar_to_image_6x16", C.c_void_p)]
+
+
 def detections_array(d):
     """bf_detections -> float64 array [count, 11]."""
     rows = [[getattr(d.items[i], f) for f, _ in Detection._fields_] for i in range(d.count)]
@@ -578,6 +586,43 @@ class Oracle:
                                                          threshold, _f32(post_range), dets):
             raise OracleError("TransFusion filter failed")
         return [detections_array(d) for d in dets]
+
+    # ---- frame runtime (bf_runtime.h) --------------------------------------
+    def runtime_infer(self, model_path, frame, point_capacity=300000, voxel_capacity=160000,
+                      sparse_capacity=160000):
+        """The CPU frame runtime (runtime.c:238-413) on a dict of host arrays
+        (images, points, camera_intrinsics, camera_to_lidar, image_augmentation,
+        lidar_augmentation, lidar_to_image) -> bf_detections."""
+        L = self.lib
+        L.bf_runtime_create.argtypes = [C.c_char_p, C.POINTER(C.c_void_p), C.c_char_p, _sz]
+        L.bf_runtime_destroy.argtypes = [C.c_void_p]
+        L.bf_runtime_destroy.restype = None
+        L.bf_runtime_workspace_bytes.argtypes = [_sz, _sz, _sz]
+        L.bf_runtime_workspace_bytes.restype = _sz
+        L.bf_runtime_infer_cpu_ref.argtypes = [C.c_void_p, C.POINTER(FrameInput), _sz, _sz, _sz,
+                                               C.POINTER(Detections), C.c_void_p, _sz,
+                                               C.c_char_p, _sz]
+        keys = ("images", "points", "camera_intrinsics", "camera_to_lidar", "image_augmentation",
+                "lidar_augmentation", "lidar_to_image")
+        arrs = {k: _f32(frame[k]) for k in keys}
+        fi = FrameInput(*[arrs[k].ctypes.data for k in keys[:2]], arrs["points"].shape[0],
+                        *[arrs[k].ctypes.data for k in keys[2:]])
+        handle, err = C.c_void_p(), C.create_string_buffer(256)
+        if not L.bf_runtime_create(str(model_path).encode(), C.byref(handle), err, 256):
+            raise OracleError(err.value.decode())
+        try:
+            nbytes = L.bf_runtime_workspace_bytes(point_capacity, voxel_capacity, sparse_capacity)
+            if not nbytes:
+                raise OracleError("invalid runtime capacities")
+            ws = np.empty(nbytes, np.uint8)
+            dets = Detections()
+            if not L.bf_runtime_infer_cpu_ref(handle, C.byref(fi), point_capacity, voxel_capacity,
+                                              sparse_capacity, C.byref(dets), ws.ctypes.data,
+                                              nbytes, err, 256):
+                raise OracleError(err.value.decode())
+        finally:
+            L.bf_runtime_destroy(handle)
+        return dets
 
     # ---- lift-splat pooling (bf_lss.h) ------------------------------------
     def lss_geometry(self, frustum, cam_rot, cam_trans, intrinsics, post_rot, post_trans,

@@ -33,6 +33,7 @@
 #include "bf_voxel.h"
 #include "bf_model.h"
 #include "bf_transfusion_decoder.h"
+#include "bf_runtime.h"
 
 #include <stddef.h>
 #include <stdint.h>
@@ -264,6 +265,17 @@ int bf_transfusion_decoder_forward_ref(const bf_transfusion_decoder *decoder,
                                        size_t height, size_t width, size_t proposals,
                                        bf_transfusion_raw_outputs *outputs, void *workspace,
                                        size_t workspace_bytes, char *error, size_t error_cap);
+
+/* ---- frame runtime (reference include/bf_runtime.h:29-49) ------------- */
+typedef struct bf_runtime bf_runtime;
+int bf_runtime_create(const char *model_path, bf_runtime **out, char *error, size_t cap);
+void bf_runtime_destroy(bf_runtime *runtime);
+size_t bf_runtime_workspace_bytes(size_t point_capacity, size_t voxel_capacity,
+                                  size_t sparse_capacity);
+int bf_runtime_infer_cpu_ref(const bf_runtime *runtime, const bf_frame_input *frame,
+                             size_t point_capacity, size_t voxel_capacity,
+                             size_t sparse_capacity, bf_detections *detections,
+                             void *workspace, size_t workspace_bytes, char *error, size_t cap);
 
 /* ---- lift-splat pooling (bf_lss.h) ------------------------------------ */
 int bf_lss_geometry_f32_ref(const float *frustum_dhw3, const float *camera_to_lidar_rotation,

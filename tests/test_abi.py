@@ -16,7 +16,8 @@ import bfhip
 ROOT = pathlib.Path(__file__).resolve().parent.parent
 HEADERS = ["bf_cuda_ops.h", "bf_cuda_swin.h", "bf_cuda_camera.h", "bf_cuda.h", "bf_cuda_bev.h",
            "bf_cuda_transfusion.h", "bf_cuda_depth_raster.h", "bf_cuda_voxel.h",
-           "bf_cuda_lidar.h", "bfhip_profile.h", "bfhip_debug.h"]
+           "bf_cuda_lidar.h", "bf_cuda_runtime.h", "bfhip_profile.h", "bfhip_debug.h"]
+MODEL_HEADERS = ["bf_model.h", "bf_frame.h"]  # host readers in libbfmodel.so
 
 
 def declared(header):
@@ -28,12 +29,14 @@ def declared(header):
 def test_every_declared_entry_point_is_exported():
     lib = bfhip.hip_lib()
     names = set().union(*(declared(h) for h in HEADERS))
-    assert len(names) == 49
+    assert len(names) == 55
     assert names == set(bfhip.SIGNATURES)
     missing = [n for n in sorted(names) if not hasattr(lib, n)]
     assert not missing, missing
     model = bfhip.model_lib()
-    assert all(hasattr(model, n) for n in declared("bf_model.h"))
+    host = set().union(*(declared(h) for h in MODEL_HEADERS))
+    assert host == set(bfhip.MODEL_SIGNATURES)
+    assert all(hasattr(model, n) for n in host)
 
 
 def _err():
@@ -236,3 +239,25 @@ def test_lidar_side_rejects_invalid_contracts(tmp_path):
     for fn in ("depth_raster", "voxelizer", "lidar_backbone"):
         assert getattr(lib, f"bf_cuda_{fn}_resident_bytes")(None) == 0
         getattr(lib, f"bf_cuda_{fn}_destroy")(None)
+
+
+def test_runtime_rejects_invalid_contracts(tmp_path):
+    lib = bfhip.hip_lib()
+    e = _err()
+    out = C.c_void_p()
+    missing = str(tmp_path / "missing.bfw").encode()
+    for args in ((None, 10, 10, 10), (missing, 0, 10, 10), (missing, 10, 0, 10),
+                 (missing, 10, 20, 10)):
+        e.value = b""
+        assert lib.bf_cuda_runtime_create(*args, C.byref(out), e, 256) == 0 and not out
+        assert e.value
+    assert lib.bf_cuda_runtime_infer(None, None, None, e, 256) == 0
+    assert lib.bf_cuda_runtime_debug_bev_stats(None, None, e, 256) == 0
+    assert lib.bf_cuda_runtime_debug_hashes(None, None, e, 256) == 0
+    assert lib.bf_cuda_runtime_resident_bytes(None) == 0
+    lib.bf_cuda_runtime_destroy(None)
+    m = bfhip.model_lib()
+    assert m.bf_frame_open(missing, C.byref(out), e, 256) == 0 and not out
+    assert m.bf_frame_input_view(None) is not None and not m.bf_frame_input_view(None)
+    assert m.bf_frame_file_bytes(None) == 0
+    m.bf_frame_close(None)

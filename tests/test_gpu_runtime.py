@@ -1,0 +1,139 @@
+"""Full-frame GPU runtime (include/bf_cuda_runtime.h) against the CPU frame
+runtime (oracle/src/runtime.c, bit-exact with the reference's src/runtime.c).
+
+Follows the reference's tests/test_cuda_runtime.cu: detections of a frame
+against the CPU chain by class-aware nearest-centre matching, repeats, the
+debug hashes and statistics, the invalid-frame gates.  The GPU chain computes
+the camera GEMMs with bf16 operands and the sparse encoder with split-fp16
+operands (fp32 accumulation throughout), so box values drift slightly from
+the fp32 CPU chain; the bars below are stated with each assertion.  Every
+replay of the captured graph must equal eager launches bit for bit.
+"""
+
+import os
+
+import numpy as np
+import pytest
+
+import bfhip
+import oracle
+from bfhip import bfw, frame_scene
+
+pytestmark = pytest.mark.gpu
+
+FIELDS = ("x", "y", "z", "width", "length", "height", "yaw", "velocity_x", "velocity_y", "score")
+
+
+@pytest.fixture(scope="module")
+def model_path(tmp_path_factory):
+    return bfw.write_full_model(tmp_path_factory.mktemp("rt") / "full.bfw", seed=1)
+
+
+@pytest.fixture(scope="module")
+def frames():
+    return [frame_scene.frame(1, 100000, sweeps=10), frame_scene.frame(5, 60000, sweeps=3)]
+
+
+def _rows(d):
+    return oracle.detections_array(d) if isinstance(d, oracle.Detections) else np.array(
+        [[getattr(d.items[i], f) for f in FIELDS] + [d.items[i].class_id] for i in range(d.count)],
+        np.float64).reshape(-1, 11)
+
+
+def match(a, b):
+    """Class-aware nearest-centre matching of detection rows (reference
+    tests/test_cuda_runtime.cu:9-18): for each row of a, the closest unused
+    row of b with the same class.  Returns (matched pairs, per-field max
+    |difference| over matched pairs)."""
+    used = np.zeros(len(b), bool)
+    pairs = []
+    for i, r in enumerate(a):
+        cand = np.flatnonzero((b[:, 10] == r[10]) & ~used)
+        if not len(cand):
+            continue
+        d = ((b[cand, :3] - r[:3]) ** 2).sum(1)
+        j = cand[np.argmin(d)]
+        used[j] = True
+        pairs.append((i, j))
+    if not pairs:
+        return pairs, np.full(10, np.inf)
+    ia, ib = map(np.array, zip(*pairs))
+    diff = np.abs(a[ia, :10] - b[ib, :10])
+    diff[:, 6] = np.abs((a[ia, 6] - b[ib, 6] + np.pi) % (2 * np.pi) - np.pi)  # yaw wraps
+    return pairs, diff.max(0)
+
+
+def test_runtime_matches_cpu_runtime(model_path, frames):
+    frame = frames[0]
+    print("[case] runtime vs CPU runtime, 100k points", flush=True)
+    want = _rows(oracle.Oracle("port").runtime_infer(model_path, frame))
+    with bfhip.Runtime(model_path) as rt:
+        got = _rows(rt.infer(frame))
+        stats = rt.debug_bev_stats()
+        assert rt.resident_bytes() > 0
+    pairs, drift = match(got, want)
+    print(f"[parity] runtime: gpu {len(got)} cpu {len(want)} matched {len(pairs)} drift "
+          + " ".join(f"{f}={v:.3g}" for f, v in zip(FIELDS, drift)), flush=True)
+    assert stats[0] > 0 and stats[2] > 0 and stats[1] > 0 and stats[3] > 0
+    assert len(got) == len(want) > 0
+    assert len(pairs) == len(want)
+    # Centres within 5 cm, sizes within 1 cm, yaw within 0.05 rad, velocities
+    # within 0.01 m/s, scores within 2e-3.
+    assert drift[:3].max() <= 0.05
+    assert drift[3:6].max() <= 0.01
+    assert drift[6] <= 0.05
+    assert drift[7:9].max() <= 0.01
+    assert drift[9] <= 2e-3
+
+
+def test_runtime_graph_replays_equal_eager(model_path, frames):
+    os.environ["BFHIP_RUNTIME_GRAPH"] = "0"
+    try:
+        eager = bfhip.Runtime(model_path)
+    finally:
+        del os.environ["BFHIP_RUNTIME_GRAPH"]
+    graph = bfhip.Runtime(model_path)
+    print("[case] runtime graph vs eager", flush=True)
+    # Calibration changes between frames (seeds 1, 5, 1): the LSS cell lists
+    # are rebuilt each time and the replays still match.
+    for k in (0, 1, 0, 0):
+        e = eager.infer(frames[k])
+        he = eager.debug_hashes()
+        g = graph.infer(frames[k])
+        hg = graph.debug_hashes()
+        assert he == hg, f"frame {k}: hashes differ"
+        assert e.count == g.count and bytes(e) == bytes(g), f"frame {k}: detections differ"
+    eager.close()
+    graph.close()
+
+
+def test_runtime_bfi_frame(model_path, frames, tmp_path):
+    frame = dict(frames[1])
+    frame["points"] = np.nan_to_num(frame["points"], nan=0.5)  # BFI holds finite values
+    path = tmp_path / "f.bfi"
+    frame_scene.write_bfi(frame, path)
+    print("[case] runtime on a BFI frame", flush=True)
+    with bfhip.Runtime(model_path) as rt, bfhip.FrameFile(path) as ff:
+        a = rt.infer(ff.input)
+        b = rt.infer(frame)
+    assert a.count > 0 and bytes(a) == bytes(b)
+
+
+def test_runtime_rejects_invalid_frames(model_path, frames):
+    frame = frames[1]
+    print("[case] runtime invalid frames", flush=True)
+    with bfhip.Runtime(model_path, point_capacity=70000) as rt:
+        good = rt.infer(frame)
+        too_many = dict(frame, points=np.zeros((70001, 5), np.float32))
+        with pytest.raises(bfhip.BfHipError):
+            rt.infer(too_many)
+        with pytest.raises(bfhip.BfHipError):
+            rt.infer(dict(frame, lidar_augmentation=np.zeros((4, 4), np.float32)))
+        intr = frame["camera_intrinsics"].copy()
+        intr[3, :3, :3] = 0.0
+        with pytest.raises(bfhip.BfHipError):
+            rt.infer(dict(frame, camera_intrinsics=intr))
+        with pytest.raises(bfhip.BfHipError):
+            rt.infer(dict(frame, points=np.zeros((0, 5), np.float32)))
+        again = rt.infer(frame)
+        assert bytes(again) == bytes(good)
