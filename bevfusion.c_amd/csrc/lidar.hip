@@ -294,10 +294,31 @@ struct Feat {
     _Float16 *hi, *lo;
 };
 
+// LDS plan of one conv instantiation: the tap's split weights, double
+// buffered, rows padded by 8 halves so the 16 lanes of a fragment read spread
+// over the banks; then the workgroup's neighbour table and active-tap list.
+template <int CI, int CO>
+struct ConvLds {
+    static constexpr int LD = CI + 8;        // halves per weight row in LDS
+    static constexpr int PLANE = CO * LD;    // halves per hi or lo plane
+    static constexpr int CHUNKS = 2 * CO * CI / 8;  // 16-byte pieces of one tap (hi + lo)
+    static constexpr int PER = (CHUNKS + 255) / 256;
+    static constexpr size_t W_BYTES = (size_t)2 * 2 * PLANE * sizeof(_Float16);
+    static constexpr size_t NBR_BYTES = (size_t)kRowsPerGroup * kTaps * sizeof(int);
+    static constexpr size_t BYTES = W_BYTES + NBR_BYTES + 32 * sizeof(int);
+};
+
 // Gather GEMM: out[r][co] = bias[co] + sum_t sum_ci in[nbr[r][t]][ci] w[t][co][ci]
-// (+ identity[r][co]) (ReLU), operands split as hi + lo.  Each wave owns 32
-// rows (two 16-row MFMA tiles) x all CO columns; workgroups stride over the
-// rows.  out32, when set, receives fp32 rows instead of a split pair.
+// (+ identity[r][co]) (ReLU), operands split as hi + lo.  A workgroup owns
+// 128 rows; each wave 32 of them (two 16-row MFMA tiles) x all CO columns.
+// Per workgroup: the rows' neighbour lists go to LDS and the taps some row
+// uses are listed; per listed tap the split weights [co][ci] are staged in
+// LDS (double buffered: the next tap's weights are fetched into registers
+// while this tap's MFMAs run) and every wave reads its B fragments there, so
+// a weight leaves L2 once per 128 rows instead of once per 32.  A fragments
+// are gathered straight from the feature rows, one tap ahead.  A wave skips
+// the MFMAs of a tap none of its rows reaches.  out32, when set, receives
+// fp32 rows instead of a split pair.
 template <int CI, int CO>
 __global__ __launch_bounds__(256) void sparse_conv_kernel(
     const int *__restrict__ nbr, const unsigned *__restrict__ count, int taps, Feat in,
@@ -305,53 +326,141 @@ __global__ __launch_bounds__(256) void sparse_conv_kernel(
     const float *__restrict__ bias, Feat identity, int relu, Feat out,
     float *__restrict__ out32) {
     using K = KOp<CI>;
+    using L = ConvLds<CI, CO>;
     typedef typename K::frag frag;
     constexpr int CT = CO / 16, KC = CI / K::kb;
+    extern __shared__ __align__(16) unsigned char smem[];
+    _Float16 *sw = reinterpret_cast<_Float16 *>(smem);  // [buffer][hi, lo][CO][LD]
+    int *snbr = reinterpret_cast<int *>(smem + L::W_BYTES);  // [row][kTaps]
+    int *stap = snbr + kRowsPerGroup * kTaps;                // [0] mask, [1] count, [2..] list
     const unsigned n = *count;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, col = lane & 15, g = lane >> 4;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, col = lane & 15, g = lane >> 4;
+    const int wrow = wave * kRowsPerWave;
+
+    // 16-byte pieces of tap t's weights: piece c < CHUNKS/2 of the hi plane,
+    // the rest of the lo plane; row co, halves k..k+7.
+    auto fetch = [&](int t, h8 (&reg)[L::PER]) {
+#pragma unroll
+        for (int q = 0; q < L::PER; ++q) {
+            const int c = tid + 256 * q;
+            if (c < L::CHUNKS) {
+                const int half = c >= L::CHUNKS / 2, cc = c - half * (L::CHUNKS / 2);
+                const _Float16 *src = (half ? w_lo : w_hi) + (size_t)t * CO * CI + (size_t)cc * 8;
+                reg[q] = *reinterpret_cast<const h8 *>(src);
+            }
+        }
+    };
+    auto stage = [&](int buf, const h8 (&reg)[L::PER]) {
+#pragma unroll
+        for (int q = 0; q < L::PER; ++q) {
+            const int c = tid + 256 * q;
+            if (c < L::CHUNKS) {
+                const int half = c >= L::CHUNKS / 2, cc = c - half * (L::CHUNKS / 2);
+                const int co = cc / (CI / 8), k = (cc % (CI / 8)) * 8;
+                *reinterpret_cast<h8 *>(sw + (size_t)(2 * buf + half) * L::PLANE + co * L::LD + k) =
+                    reg[q];
+            }
+        }
+    };
+    auto gather = [&](int t, frag (&ah)[2][KC], frag (&al)[2][KC], bool (&live)[2]) {
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+            const int src = snbr[(wrow + 16 * rt + col) * kTaps + t];
+            live[rt] = src >= 0;
+#pragma unroll
+            for (int kc = 0; kc < KC; ++kc) {
+                const int k0 = kc * K::kb + g * K::per_lane;
+                if (src >= 0) {
+                    ah[rt][kc] = *(const frag *)&in.hi[(size_t)src * CI + k0];
+                    al[rt][kc] = *(const frag *)&in.lo[(size_t)src * CI + k0];
+                } else {
+                    ah[rt][kc] = frag{};
+                    al[rt][kc] = frag{};
+                }
+            }
+        }
+    };
+
     for (unsigned base = blockIdx.x * kRowsPerGroup; base < n; base += gridDim.x * kRowsPerGroup) {
-        const unsigned row0 = base + wave * kRowsPerWave;
+        if (tid == 0) stap[0] = 0;
+        __syncthreads();
+        unsigned used = 0;
+        for (int i = tid; i < kRowsPerGroup * taps; i += 256) {
+            const int r = i / taps, t = i - r * taps;
+            const int v = base + r < n ? nbr[(size_t)(base + r) * kTaps + t] : kEmpty;
+            snbr[r * kTaps + t] = v;
+            if (v >= 0) used |= 1u << t;
+        }
+        for (int o = 32; o > 0; o >>= 1) used |= __shfl_xor(used, o);
+        if (lane == 0) atomicOr(reinterpret_cast<unsigned *>(stap), used);
+        __syncthreads();
+        if (tid == 0) {
+            const unsigned m = (unsigned)stap[0];
+            int c = 0;
+            for (int t = 0; t < taps; ++t)
+                if (m >> t & 1u) stap[2 + c++] = t;
+            stap[1] = c;
+        }
+        __syncthreads();
+        const int active = stap[1];
+
         f32x4 acc[2][CT];
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
             for (int ct = 0; ct < CT; ++ct) acc[rt][ct] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        for (int t = 0; t < taps; ++t) {
-            int src[2];
-#pragma unroll
-            for (int rt = 0; rt < 2; ++rt) {
-                const unsigned r = row0 + 16 * rt + col;
-                src[rt] = r < n ? nbr[(size_t)r * kTaps + t] : kEmpty;
-            }
+        h8 wreg[L::PER];
+        frag ah[2][KC], al[2][KC];
+        bool live[2] = {false, false};
+        if (active) {
+            fetch(stap[2], wreg);
+            stage(0, wreg);
+            gather(stap[2], ah, al, live);
+        }
+        __syncthreads();
+        for (int i = 0; i < active; ++i) {
+            const int buf = i & 1;
+            const bool more = i + 1 < active;
+            if (more) fetch(stap[3 + i], wreg);
+            frag nh[2][KC], nl[2][KC];
+            bool nlive[2] = {false, false};
+            if (more) gather(stap[3 + i], nh, nl, nlive);
             // Wave-uniform: a tap none of the wave's rows reaches adds nothing.
-            if (!__ballot(src[0] >= 0 || src[1] >= 0)) continue;
+            if (__ballot(live[0] || live[1])) {
+                const _Float16 *bh_base = sw + (size_t)(2 * buf) * L::PLANE;
+                const _Float16 *bl_base = bh_base + L::PLANE;
 #pragma unroll
-            for (int kc = 0; kc < KC; ++kc) {
-                const int k0 = kc * K::kb + g * K::per_lane;
-                frag ah[2], al[2];
+                for (int kc = 0; kc < KC; ++kc) {
+                    const int k0 = kc * K::kb + g * K::per_lane;
+#pragma unroll
+                    for (int ct = 0; ct < CT; ++ct) {
+                        const int wo = (16 * ct + col) * L::LD + k0;
+                        const frag bh = *(const frag *)&bh_base[wo];
+                        const frag bl = *(const frag *)&bl_base[wo];
+#pragma unroll
+                        for (int rt = 0; rt < 2; ++rt) {
+                            acc[rt][ct] = K::mfma(al[rt][kc], bh, acc[rt][ct]);
+                            acc[rt][ct] = K::mfma(ah[rt][kc], bl, acc[rt][ct]);
+                            acc[rt][ct] = K::mfma(ah[rt][kc], bh, acc[rt][ct]);
+                        }
+                    }
+                }
+            }
+            if (more) {
+                stage(buf ^ 1, wreg);
 #pragma unroll
                 for (int rt = 0; rt < 2; ++rt) {
-                    if (src[rt] >= 0) {
-                        ah[rt] = *(const frag *)&in.hi[(size_t)src[rt] * CI + k0];
-                        al[rt] = *(const frag *)&in.lo[(size_t)src[rt] * CI + k0];
-                    } else {
-                        ah[rt] = frag{};
-                        al[rt] = frag{};
-                    }
-                }
+                    live[rt] = nlive[rt];
 #pragma unroll
-                for (int ct = 0; ct < CT; ++ct) {
-                    const size_t wo = ((size_t)t * CO + 16 * ct + col) * CI + k0;
-                    const frag bh = *(const frag *)&w_hi[wo], bl = *(const frag *)&w_lo[wo];
-#pragma unroll
-                    for (int rt = 0; rt < 2; ++rt) {
-                        acc[rt][ct] = K::mfma(al[rt], bh, acc[rt][ct]);
-                        acc[rt][ct] = K::mfma(ah[rt], bl, acc[rt][ct]);
-                        acc[rt][ct] = K::mfma(ah[rt], bh, acc[rt][ct]);
+                    for (int kc = 0; kc < KC; ++kc) {
+                        ah[rt][kc] = nh[rt][kc];
+                        al[rt][kc] = nl[rt][kc];
                     }
                 }
             }
+            __syncthreads();
         }
+        const unsigned row0 = base + wrow;
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct) {
             const int co = 16 * ct + col;
@@ -370,6 +479,7 @@ __global__ __launch_bounds__(256) void sparse_conv_kernel(
                     else split_store(v, out.hi + at, out.lo + at);
                 }
         }
+        __syncthreads();  // LDS is rewritten by the next row group
     }
 }
 
@@ -569,9 +679,8 @@ void launch_conv(const bf_cuda_lidar_backbone *n, const Conv &c, const unsigned 
     const unsigned blocks = row_blocks(n->capacity, kRowsPerGroup);
 #define BF_CONV(CI, CO)                                                                        \
     if (c.ci == CI && c.co == CO) {                                                            \
-        sparse_conv_kernel<CI, CO><<<blocks, 256, 0, s>>>(n->nbr, count, c.taps, in, c.w_hi,  \
-                                                          c.w_lo, c.bias, identity, relu, out,  \
-                                                          out32);                               \
+        sparse_conv_kernel<CI, CO><<<blocks, 256, ConvLds<CI, CO>::BYTES, s>>>(                \
+            n->nbr, count, c.taps, in, c.w_hi, c.w_lo, c.bias, identity, relu, out, out32);    \
         return;                                                                                \
     }
     BF_CONV(16, 16)
@@ -652,6 +761,18 @@ extern "C" size_t bf_cuda_lidar_backbone_resident_bytes(const bf_cuda_lidar_back
     return n ? n->resident_bytes : 0;
 }
 
+namespace {
+
+template <int CI, int CO>
+int allow_lds(char *error, size_t cap) {
+    return hip_ok(hipFuncSetAttribute(reinterpret_cast<const void *>(&sparse_conv_kernel<CI, CO>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      (int)ConvLds<CI, CO>::BYTES),
+                  error, cap, "set LiDAR conv LDS size");
+}
+
+}  // namespace
+
 extern "C" int bf_cuda_lidar_backbone_create(const bf_model *model, size_t batches, size_t d,
                                              size_t h, size_t w, size_t capacity,
                                              bf_cuda_lidar_backbone **out, char *error,
@@ -662,6 +783,11 @@ extern "C" int bf_cuda_lidar_backbone_create(const bf_model *model, size_t batch
         return fail(error, cap, "invalid HIP LiDAR contract");
     if (capacity > (size_t)INT_MAX / kTaps)
         return fail(error, cap, "HIP LiDAR capacity is too large");
+    if (!allow_lds<16, 16>(error, cap) || !allow_lds<16, 32>(error, cap) ||
+        !allow_lds<32, 32>(error, cap) || !allow_lds<32, 64>(error, cap) ||
+        !allow_lds<64, 64>(error, cap) || !allow_lds<64, 128>(error, cap) ||
+        !allow_lds<128, 128>(error, cap))
+        return 0;
     bf_cuda_lidar_backbone *n = (bf_cuda_lidar_backbone *)std::calloc(1, sizeof(*n));
     if (!n) return fail(error, cap, "HIP LiDAR allocation failed");
     n->batches = batches;
