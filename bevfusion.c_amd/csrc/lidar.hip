@@ -483,6 +483,130 @@ __global__ __launch_bounds__(256) void sparse_conv_kernel(
     }
 }
 
+// Gather GEMM for the 16-channel-input layers of the finest level: there
+// is little math per tap, so the time is the latency of each tap's gather.
+// A workgroup owns 32 rows x all CO; its four waves take the active taps in
+// turn (wave w: list entries w, w + 4, ...), each keeping the next tap's
+// feature and weight fragments in flight while it multiplies the current
+// one; the weights ([co][ci] per tap, a few KB) stay in L1/L2.  The four
+// partial sums meet in LDS and are added in wave order (deterministic), then
+// bias, residual and ReLU are applied on coalesced rows.
+template <int CI, int CO>
+__global__ __launch_bounds__(256) void sparse_conv_split_kernel(
+    const int *__restrict__ nbr, const unsigned *__restrict__ count, int taps, Feat in,
+    const _Float16 *__restrict__ w_hi, const _Float16 *__restrict__ w_lo,
+    const float *__restrict__ bias, Feat identity, int relu, Feat out,
+    float *__restrict__ out32) {
+    using K = KOp<CI>;
+    typedef typename K::frag frag;
+    constexpr int CT = CO / 16, KC = CI / K::kb, R = 32;
+    __shared__ int snbr[R * kTaps];
+    __shared__ int stap[2 + kTaps];
+    __shared__ float part[4][R][CO + 1];
+    const unsigned n = *count;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, col = lane & 15, g = lane >> 4;
+
+    struct Frags {
+        frag ah[2][KC], al[2][KC], bh[CT][KC], bl[CT][KC];
+        bool live;
+    };
+    auto load = [&](int t, Frags &f) {
+        f.live = false;
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+            const int src = snbr[(16 * rt + col) * kTaps + t];
+            f.live |= src >= 0;
+#pragma unroll
+            for (int kc = 0; kc < KC; ++kc) {
+                const int k0 = kc * K::kb + g * K::per_lane;
+                if (src >= 0) {
+                    f.ah[rt][kc] = *(const frag *)&in.hi[(size_t)src * CI + k0];
+                    f.al[rt][kc] = *(const frag *)&in.lo[(size_t)src * CI + k0];
+                } else {
+                    f.ah[rt][kc] = frag{};
+                    f.al[rt][kc] = frag{};
+                }
+            }
+        }
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+            for (int kc = 0; kc < KC; ++kc) {
+                const size_t wo = ((size_t)t * CO + 16 * ct + col) * CI + kc * K::kb + g * K::per_lane;
+                f.bh[ct][kc] = *(const frag *)&w_hi[wo];
+                f.bl[ct][kc] = *(const frag *)&w_lo[wo];
+            }
+    };
+
+    for (unsigned base = blockIdx.x * R; base < n; base += gridDim.x * R) {
+        if (tid == 0) stap[0] = 0;
+        __syncthreads();
+        unsigned used = 0;
+        for (int i = tid; i < R * taps; i += 256) {
+            const int r = i / taps, t = i - r * taps;
+            const int v = base + r < n ? nbr[(size_t)(base + r) * kTaps + t] : kEmpty;
+            snbr[r * kTaps + t] = v;
+            if (v >= 0) used |= 1u << t;
+        }
+        for (int o = 32; o > 0; o >>= 1) used |= __shfl_xor(used, o);
+        if (lane == 0) atomicOr(reinterpret_cast<unsigned *>(stap), used);
+        __syncthreads();
+        if (tid == 0) {
+            const unsigned m = (unsigned)stap[0];
+            int c = 0;
+            for (int t = 0; t < taps; ++t)
+                if (m >> t & 1u) stap[2 + c++] = t;
+            stap[1] = c;
+        }
+        __syncthreads();
+        const int active = stap[1];
+
+        f32x4 acc[2][CT];
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) acc[rt][ct] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        Frags cur, nxt;
+        if (wave < active) load(stap[2 + wave], cur);
+        for (int i = wave; i < active; i += 4) {
+            const bool more = i + 4 < active;
+            if (more) load(stap[2 + i + 4], nxt);
+            if (__ballot(cur.live)) {
+#pragma unroll
+                for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+                    for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+                        for (int rt = 0; rt < 2; ++rt) {
+                            acc[rt][ct] = K::mfma(cur.al[rt][kc], cur.bh[ct][kc], acc[rt][ct]);
+                            acc[rt][ct] = K::mfma(cur.ah[rt][kc], cur.bl[ct][kc], acc[rt][ct]);
+                            acc[rt][ct] = K::mfma(cur.ah[rt][kc], cur.bh[ct][kc], acc[rt][ct]);
+                        }
+            }
+            if (more) cur = nxt;
+        }
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) part[wave][16 * rt + 4 * g + j][16 * ct + col] = acc[rt][ct][j];
+        __syncthreads();
+        for (int e = tid; e < R * CO; e += 256) {
+            const int r = e / CO, co = e - r * CO;
+            const unsigned row = base + r;
+            if (row >= n) continue;
+            const size_t at = (size_t)row * CO + co;
+            float v = part[0][r][co] + part[1][r][co] + part[2][r][co] + part[3][r][co] + bias[co];
+            if (identity.hi) v += (float)identity.hi[at] + (float)identity.lo[at];
+            if (relu) v = fmaxf(v, 0.0f);
+            if (out32) out32[at] = v;
+            else split_store(v, out.hi + at, out.lo + at);
+        }
+        __syncthreads();  // LDS is rewritten by the next row group
+    }
+}
+
 // dense[b][c][z][y][x] = row features of the site at (b, z, y, x), else 0.
 __global__ __launch_bounds__(256) void dense_kernel(const int *__restrict__ grid, Grid g,
                                                     const float *__restrict__ feat,
@@ -677,14 +801,23 @@ unsigned row_blocks(size_t capacity, int rows_per_block) {
 void launch_conv(const bf_cuda_lidar_backbone *n, const Conv &c, const unsigned *count,
                  Feat in, Feat identity, int relu, Feat out, float *out32, hipStream_t s) {
     const unsigned blocks = row_blocks(n->capacity, kRowsPerGroup);
+    const unsigned split_blocks =
+        (unsigned)std::max<size_t>(1, std::min<size_t>(16384, (n->capacity + 31) / 32));
+#define BF_SPLIT(CI, CO)                                                                       \
+    if (c.ci == CI && c.co == CO) {                                                            \
+        sparse_conv_split_kernel<CI, CO><<<split_blocks, 256, 0, s>>>(                         \
+            n->nbr, count, c.taps, in, c.w_hi, c.w_lo, c.bias, identity, relu, out, out32);    \
+        return;                                                                                \
+    }
+    BF_SPLIT(16, 16)
+    BF_SPLIT(16, 32)
+#undef BF_SPLIT
 #define BF_CONV(CI, CO)                                                                        \
     if (c.ci == CI && c.co == CO) {                                                            \
         sparse_conv_kernel<CI, CO><<<blocks, 256, ConvLds<CI, CO>::BYTES, s>>>(                \
             n->nbr, count, c.taps, in, c.w_hi, c.w_lo, c.bias, identity, relu, out, out32);    \
         return;                                                                                \
     }
-    BF_CONV(16, 16)
-    BF_CONV(16, 32)
     BF_CONV(32, 32)
     BF_CONV(32, 64)
     BF_CONV(64, 64)
@@ -783,8 +916,7 @@ extern "C" int bf_cuda_lidar_backbone_create(const bf_model *model, size_t batch
         return fail(error, cap, "invalid HIP LiDAR contract");
     if (capacity > (size_t)INT_MAX / kTaps)
         return fail(error, cap, "HIP LiDAR capacity is too large");
-    if (!allow_lds<16, 16>(error, cap) || !allow_lds<16, 32>(error, cap) ||
-        !allow_lds<32, 32>(error, cap) || !allow_lds<32, 64>(error, cap) ||
+    if (!allow_lds<32, 32>(error, cap) || !allow_lds<32, 64>(error, cap) ||
         !allow_lds<64, 64>(error, cap) || !allow_lds<64, 128>(error, cap) ||
         !allow_lds<128, 128>(error, cap))
         return 0;
