@@ -608,15 +608,34 @@ __global__ __launch_bounds__(256) void sparse_conv_split_kernel(
 }
 
 // dense[b][c][z][y][x] = row features of the site at (b, z, y, x), else 0.
+// A workgroup takes 64 consecutive cells of one batch: the sites' 128-float
+// rows are read whole into LDS and written back channel by channel, so both
+// the row reads and the channel-major writes are contiguous.
 __global__ __launch_bounds__(256) void dense_kernel(const int *__restrict__ grid, Grid g,
                                                     const float *__restrict__ feat,
                                                     float *__restrict__ dense) {
-    const size_t plane = (size_t)g.d * g.h * g.w, total = (size_t)g.b * 128 * plane;
-    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < total;
-         i += (size_t)gridDim.x * 256) {
-        const size_t cell = i % plane, bc = i / plane, c = bc % 128, b = bc / 128;
-        const int idx = grid[b * plane + cell];
-        dense[i] = idx >= 0 ? feat[(size_t)idx * 128 + c] : 0.0f;
+    __shared__ float tile[64][129];
+    __shared__ int rows[64];
+    const size_t plane = (size_t)g.d * g.h * g.w;
+    const size_t tiles = (plane + 63) / 64;
+    for (size_t bt = blockIdx.x; bt < (size_t)g.b * tiles; bt += gridDim.x) {
+        const size_t b = bt / tiles, cell0 = (bt % tiles) * 64;
+        if (threadIdx.x < 64) {
+            const size_t cell = cell0 + threadIdx.x;
+            rows[threadIdx.x] = cell < plane ? grid[b * plane + cell] : kEmpty;
+        }
+        __syncthreads();
+        for (int e = threadIdx.x; e < 64 * 128; e += 256) {
+            const int k = e >> 7, c = e & 127, idx = rows[k];
+            tile[k][c] = idx >= 0 ? feat[(size_t)idx * 128 + c] : 0.0f;
+        }
+        __syncthreads();
+        for (int e = threadIdx.x; e < 64 * 128; e += 256) {
+            const int c = e >> 6, k = e & 63;
+            const size_t cell = cell0 + k;
+            if (cell < plane) dense[(b * 128 + c) * plane + cell] = tile[k][c];
+        }
+        __syncthreads();
     }
 }
 
@@ -873,8 +892,8 @@ void forward_impl(bf_cuda_lidar_backbone *n, const bf_coord4 *coords, const floa
     }
     strided_sites(n, n->out, 3, level_coords, s);
     launch_conv(n, n->out, n->counts + 4, n->feat[x], none, 1, none, n->out32, s);
-    const size_t total = (size_t)128 * n->cells[4];
-    dense_kernel<<<(unsigned)std::min<size_t>(8192, (total + 255) / 256), 256, 0, s>>>(
+    const size_t dense_tiles = (size_t)n->lv[4].b * (((size_t)n->cells[4] / n->lv[4].b + 63) / 64);
+    dense_kernel<<<(unsigned)std::min<size_t>(16384, dense_tiles), 256, 0, s>>>(
         n->grid[4], n->lv[4], n->out32, dense);
     clear_kernel<<<rb, 256, 0, s>>>(coords, n->counts, n->lv[0], n->grid[0]);
     for (int l = 1; l < 5; ++l)
