@@ -935,10 +935,6 @@ extern "C" int bf_cuda_lidar_backbone_create(const bf_model *model, size_t batch
         return fail(error, cap, "invalid HIP LiDAR contract");
     if (capacity > (size_t)INT_MAX / kTaps)
         return fail(error, cap, "HIP LiDAR capacity is too large");
-    if (!allow_lds<32, 32>(error, cap) || !allow_lds<32, 64>(error, cap) ||
-        !allow_lds<64, 64>(error, cap) || !allow_lds<64, 128>(error, cap) ||
-        !allow_lds<128, 128>(error, cap))
-        return 0;
     bf_cuda_lidar_backbone *n = (bf_cuda_lidar_backbone *)std::calloc(1, sizeof(*n));
     if (!n) return fail(error, cap, "HIP LiDAR allocation failed");
     n->batches = batches;
@@ -959,7 +955,9 @@ extern "C" int bf_cuda_lidar_backbone_create(const bf_model *model, size_t batch
         }
         n->cells[l] = (long long)n->lv[l].b * n->lv[l].d * n->lv[l].h * n->lv[l].w;
     }
-    if (!build(n, model, error, cap)) {
+    if (!allow_lds<32, 32>(error, cap) || !allow_lds<32, 64>(error, cap) ||
+        !allow_lds<64, 64>(error, cap) || !allow_lds<64, 128>(error, cap) ||
+        !allow_lds<128, 128>(error, cap) || !build(n, model, error, cap)) {
         bf_cuda_lidar_backbone_destroy(n);
         return 0;
     }
