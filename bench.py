@@ -774,7 +774,7 @@ RUNTIME_REFERENCE_MS = 142.381
 def runtime_leg(reps, seed=1):
     """The full frame through bf_cuda_runtime_infer: host frame in (images,
     100k points, calibration), detections out; wall-clock ms per frame with
-    the H2D copies, the graph replay and the D2H copy of the detections."""
+    the H2D copies, the graph replays and the D2H copy of the detections."""
     import bfhip
     from bfhip import bfw, frame_scene
     tmp = pathlib.Path(tempfile.mkdtemp(prefix="rt_"))
@@ -799,7 +799,7 @@ def runtime_leg(reps, seed=1):
     del keep
     return {"workload": f"full frame: 6 x 3 x 256 x 704 images + {LIDAR_POINTS} points "
                         f"({LIDAR_SWEEPS} sweeps) -> detections; random-init checkpoint "
-                        "(N(0, 1/fan_in) weights); one HIP graph per frame",
+                        "(N(0, 1/fan_in) weights); LiDAR and camera branches concurrent in HIP graphs",
             "ms": round(ms, 3), "ms_min": round(times[0], 3), "cold_ms": round(cold_ms, 1),
             "detections": dets.count, "h2d_mib": round(h2d / 2**20, 1),
             "resident_mib": round(resident / 2**20, 1),

@@ -1,12 +1,19 @@
 // Full-frame BEVFusion runtime (drop-in for reference src/cuda_runtime.cu:53-98).
 //
-// One stream, one HIP graph per runtime.  The frame's host arrays are copied
-// into fixed device buffers (with the point count as a device word), then a
-// graph captured on the first frame replays the whole chain:
-//   depth raster -> voxeliser -> SECOND encoder  (LiDAR BEV)
-//   Swin-T -> FPN + depth head -> lift-splat -> downsample  (image BEV)
-//   BEV stage -> TransFusion -> canonical decode (score threshold 0)
-// and the detections are copied back.  The two modality BEVs are written
+// Three HIP graphs per runtime, captured on the first frame.  The frame's
+// host arrays are copied into fixed device buffers (the point count as a
+// device word) and the graphs replay the chain:
+//   main   points + matrices upload -> fork
+//   side   (after fork) LiDAR graph: voxeliser -> SECOND encoder -> join
+//   main   images + calibration upload -> camera graph: depth raster ->
+//          Swin-T -> FPN + depth head -> lift-splat -> downsample
+//   main   (after join) tail graph: BEV stage -> TransFusion -> decode
+//          (threshold 0) -> detections copied back
+// The two branches are independent until the BEV stage and neither fills the
+// chip (the deep sparse convs run one wave per SIMD, the camera GEMMs are
+// small), so they run concurrently, and the LiDAR branch starts while the
+// images are still being uploaded.  Events order the graph launches; both
+// streams keep the default priority.  The two modality BEVs are written
 // straight into their channel ranges of the fused [336,180,180] input (image
 // channels 0-79, LiDAR 80-335), so the reference's concat copy disappears.
 // Kernels that depend on the point count read it from device memory and are
@@ -140,7 +147,8 @@ __global__ void hash_final_kernel(const unsigned long long *__restrict__ parts, 
 
 struct bf_cuda_runtime {
     size_t point_capacity, voxel_capacity, sparse_capacity, resident_bytes;
-    hipStream_t stream;
+    hipStream_t stream, side;
+    hipEvent_t fork, join;
     bf_cuda_depth_raster *raster;
     bf_cuda_voxelizer *voxelizer;
     bf_cuda_lidar_backbone *lidar;
@@ -161,58 +169,74 @@ struct bf_cuda_runtime {
     unsigned *voxel_count;
     bf_transfusion_raw_outputs raw;
     const bf_detections *detections;
-    hipGraphExec_t graph;
+    hipGraphExec_t graph[3];  // LiDAR, camera, tail
     bool use_graph, calib_valid;
     float calib_key[kCalib];
 };
 
 namespace {
 
-// Every launch of one frame, on r->stream (captured into the graph).
-int enqueue(bf_cuda_runtime *r, char *error, size_t cap) {
+// The launches of one frame in three parts: the LiDAR branch (on r->side),
+// the camera branch and the tail (on r->stream).
+int enqueue_lidar(bf_cuda_runtime *r, char *error, size_t cap) {
+    void *l = r->side;
+    return voxelize_count_device(r->voxelizer, r->points, r->point_count, r->point_capacity,
+                                 r->voxel_coords, r->voxel_features, r->voxel_count, l, error,
+                                 cap) &&
+           bf_cuda_lidar_backbone_forward_count_device(r->lidar, r->voxel_coords,
+                                                       r->voxel_features, r->voxel_count,
+                                                       r->lidar_bev, l, error, cap);
+}
+
+int enqueue_camera(bf_cuda_runtime *r, char *error, size_t cap) {
     void *s = r->stream;
     return depth_rasterize_count_device(r->raster, r->points, r->point_count, r->point_capacity,
                                         r->lidar_aug, r->lidar_to_image, r->image_aug,
                                         r->dense_depth, s, error, cap) &&
-           voxelize_count_device(r->voxelizer, r->points, r->point_count, r->point_capacity,
-                                 r->voxel_coords, r->voxel_features, r->voxel_count, s, error,
-                                 cap) &&
-           bf_cuda_lidar_backbone_forward_count_device(r->lidar, r->voxel_coords,
-                                                       r->voxel_features, r->voxel_count,
-                                                       r->lidar_bev, s, error, cap) &&
            bf_cuda_swin_forward(r->swin, r->images, r->swin0, r->swin1, r->swin2, s, error, cap) &&
            bf_cuda_camera_neck_forward(r->camera, r->swin0, r->swin1, r->swin2, r->dense_depth,
                                        r->depth_logits, r->context, s, error, cap) &&
            bf_cuda_lss_plan_forward_f32(r->lss, r->depth_logits, r->context, r->full_image_bev, s,
                                         error, cap) &&
            bf_cuda_camera_downsample_forward(r->camera, r->full_image_bev, r->image_bev, s, error,
-                                             cap) &&
-           bf_cuda_bev_stage_forward(r->bev, r->fusion, r->spatial, r->shared, r->heatmap, s,
+                                             cap);
+}
+
+int enqueue_tail(bf_cuda_runtime *r, char *error, size_t cap) {
+    void *s = r->stream;
+    return bf_cuda_bev_stage_forward(r->bev, r->fusion, r->spatial, r->shared, r->heatmap, s,
                                      error, cap) &&
            bf_cuda_transfusion_forward(r->decoder, r->shared, r->heatmap, &r->raw, s, error,
                                        cap) &&
            transfusion_decode_launch(r->decoder, &r->raw, 0.0f, s, &r->detections, error, cap);
 }
 
-int capture(bf_cuda_runtime *r, char *error, size_t cap) {
-    if (!hip_ok(hipStreamBeginCapture(r->stream, hipStreamCaptureModeThreadLocal), error, cap,
-                "begin runtime graph capture"))
-        return 0;
-    const int ok = enqueue(r, error, cap);
-    hipGraph_t g = nullptr;
-    const hipError_t end = hipStreamEndCapture(r->stream, &g);
-    if (!ok) {
-        if (g) (void)hipGraphDestroy(g);
-        return 0;
+typedef int (*Part)(bf_cuda_runtime *, char *, size_t);
+
+// Part k of the frame on `stream`: replayed from its graph (captured on first
+// use), or launched eagerly when graphs are off.
+int run_part(bf_cuda_runtime *r, int k, Part part, hipStream_t stream, char *error, size_t cap) {
+    if (!r->use_graph) return part(r, error, cap);
+    if (!r->graph[k]) {
+        if (!hip_ok(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), error, cap,
+                    "begin runtime graph capture"))
+            return 0;
+        const int ok = part(r, error, cap);
+        hipGraph_t g = nullptr;
+        const hipError_t end = hipStreamEndCapture(stream, &g);
+        if (!ok) {
+            if (g) (void)hipGraphDestroy(g);
+            return 0;
+        }
+        if (!hip_ok(end, error, cap, "end runtime graph capture")) return 0;
+        const hipError_t inst = hipGraphInstantiate(&r->graph[k], g, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(g);
+        if (!hip_ok(inst, error, cap, "instantiate runtime graph")) {
+            r->graph[k] = nullptr;
+            return 0;
+        }
     }
-    if (!hip_ok(end, error, cap, "end runtime graph capture")) return 0;
-    const hipError_t inst = hipGraphInstantiate(&r->graph, g, nullptr, nullptr, 0);
-    (void)hipGraphDestroy(g);
-    if (!hip_ok(inst, error, cap, "instantiate runtime graph")) {
-        r->graph = nullptr;
-        return 0;
-    }
-    return 1;
+    return hip_ok(hipGraphLaunch(r->graph[k], stream), error, cap, "launch HIP runtime graph");
 }
 
 }  // namespace
@@ -220,7 +244,9 @@ int capture(bf_cuda_runtime *r, char *error, size_t cap) {
 extern "C" void bf_cuda_runtime_destroy(bf_cuda_runtime *r) {
     if (!r) return;
     if (r->stream) (void)hipStreamSynchronize(r->stream);
-    if (r->graph) (void)hipGraphExecDestroy(r->graph);
+    if (r->side) (void)hipStreamSynchronize(r->side);
+    for (hipGraphExec_t g : r->graph)
+        if (g) (void)hipGraphExecDestroy(g);
     bf_cuda_transfusion_destroy(r->decoder);
     bf_cuda_bev_stage_destroy(r->bev);
     bf_cuda_lss_plan_destroy(r->lss);
@@ -230,6 +256,9 @@ extern "C" void bf_cuda_runtime_destroy(bf_cuda_runtime *r) {
     bf_cuda_voxelizer_destroy(r->voxelizer);
     bf_cuda_depth_raster_destroy(r->raster);
     if (r->arena) (void)hipFree(r->arena);
+    if (r->fork) (void)hipEventDestroy(r->fork);
+    if (r->join) (void)hipEventDestroy(r->join);
+    if (r->side) (void)hipStreamDestroy(r->side);
     if (r->stream) (void)hipStreamDestroy(r->stream);
     std::free(r);
 }
@@ -265,6 +294,12 @@ extern "C" int bf_cuda_runtime_create(const char *model_path, size_t point_capac
     const bf_tensor *fr = bf_model_find(model, "vtransform.frustum");
     int ok = hip_ok(hipStreamCreateWithFlags(&r->stream, hipStreamNonBlocking), error, cap,
                     "create HIP runtime stream") &&
+             hip_ok(hipStreamCreateWithFlags(&r->side, hipStreamNonBlocking), error, cap,
+                    "create HIP runtime LiDAR stream") &&
+             hip_ok(hipEventCreateWithFlags(&r->fork, hipEventDisableTiming), error, cap,
+                    "create HIP runtime events") &&
+             hip_ok(hipEventCreateWithFlags(&r->join, hipEventDisableTiming), error, cap,
+                    "create HIP runtime events") &&
              bf_cuda_depth_raster_create(point_capacity, kCams, kImgH, kImgW, &r->raster, error,
                                          cap) &&
              bf_cuda_voxelizer_create(&vcfg, point_capacity, &r->voxelizer, error, cap) &&
@@ -388,20 +423,25 @@ extern "C" int bf_cuda_runtime_infer(bf_cuda_runtime *r, const bf_frame_input *f
     const hipStream_t s = r->stream;
     const unsigned count = (unsigned)f->point_count;
     const size_t F = sizeof(float);
-    if (!hip_ok(hipMemcpyAsync(r->images, f->camera_images, (size_t)kCams * 3 * kImgH * kImgW * F,
-                               hipMemcpyHostToDevice, s), error, cap, "upload HIP images") ||
-        !hip_ok(hipMemcpyAsync(r->points, f->points, f->point_count * 5 * F,
+    // Points and matrices first: the LiDAR branch needs nothing else.
+    if (!hip_ok(hipMemcpyAsync(r->points, f->points, f->point_count * 5 * F,
                                hipMemcpyHostToDevice, s), error, cap, "upload HIP points") ||
+        !hip_ok(hipMemcpyAsync(r->point_count, &count, sizeof(count), hipMemcpyHostToDevice, s),
+                error, cap, "upload HIP point count") ||
         !hip_ok(hipMemcpyAsync(r->lidar_aug, f->lidar_augmentation_16, 16 * F,
                                hipMemcpyHostToDevice, s), error, cap, "upload HIP lidar aug") ||
         !hip_ok(hipMemcpyAsync(r->lidar_to_image, f->lidar_to_image_6x16, 96 * F,
                                hipMemcpyHostToDevice, s), error, cap, "upload HIP lidar-to-image") ||
         !hip_ok(hipMemcpyAsync(r->image_aug, f->image_augmentation_6x16, 96 * F,
                                hipMemcpyHostToDevice, s), error, cap, "upload HIP image aug") ||
+        !hip_ok(hipEventRecord(r->fork, s), error, cap, "fork LiDAR branch") ||
+        !hip_ok(hipStreamWaitEvent(r->side, r->fork, 0), error, cap, "fork LiDAR branch") ||
+        !run_part(r, 0, enqueue_lidar, r->side, error, cap) ||
+        !hip_ok(hipEventRecord(r->join, r->side), error, cap, "join LiDAR branch") ||
+        !hip_ok(hipMemcpyAsync(r->images, f->camera_images, (size_t)kCams * 3 * kImgH * kImgW * F,
+                               hipMemcpyHostToDevice, s), error, cap, "upload HIP images") ||
         !hip_ok(hipMemcpyAsync(r->calib, key, sizeof(key), hipMemcpyHostToDevice, s), error, cap,
-                "upload HIP calibration") ||
-        !hip_ok(hipMemcpyAsync(r->point_count, &count, sizeof(count), hipMemcpyHostToDevice, s),
-                error, cap, "upload HIP point count"))
+                "upload HIP calibration"))
         return 0;
     const bool changed = !r->calib_valid || std::memcmp(key, r->calib_key, sizeof(key)) != 0;
     if (changed &&
@@ -409,12 +449,10 @@ extern "C" int bf_cuda_runtime_infer(bf_cuda_runtime *r, const bf_frame_input *f
                                                   r->calib + 72, r->calib + 126, r->calib + 180,
                                                   r->calib + 198, r->calib + 207, s, error, cap))
         return 0;
-    if (r->use_graph) {
-        if (!r->graph && !capture(r, error, cap)) return 0;
-        if (!hip_ok(hipGraphLaunch(r->graph, s), error, cap, "launch HIP runtime graph")) return 0;
-    } else if (!enqueue(r, error, cap)) {
+    if (!run_part(r, 1, enqueue_camera, s, error, cap) ||
+        !hip_ok(hipStreamWaitEvent(s, r->join, 0), error, cap, "join LiDAR branch") ||
+        !run_part(r, 2, enqueue_tail, s, error, cap))
         return 0;
-    }
     if (!hip_ok(hipMemcpyAsync(detections, r->detections, sizeof(*detections),
                                hipMemcpyDeviceToHost, s), error, cap, "copy HIP detections") ||
         !hip_ok(hipStreamSynchronize(s), error, cap, "synchronize HIP runtime"))

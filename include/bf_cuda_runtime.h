@@ -13,12 +13,14 @@
  * and the TransFusion decoder (180 x 180, 200 proposals).  voxel_capacity must
  * not exceed sparse_capacity.
  *
- * infer copies the frame to the device (the only host->device traffic) and
- * replays one HIP graph holding the whole frame -- depth raster, voxeliser,
- * sparse encoder, Swin-T, neck, lift-splat, downsample, BEV concat, BEV
- * stage, TransFusion and the canonical decode at score threshold 0 -- then
- * copies the detections back.  The point count travels in device memory, so
- * one graph serves every frame; the graph is captured on the first frame.
+ * infer copies the frame to the device (the only host->device traffic),
+ * replays three HIP graphs -- the LiDAR branch (voxeliser, sparse encoder) on
+ * a second stream, concurrent with the camera branch (depth raster, Swin-T,
+ * neck, lift-splat, downsample), then BEV stage, TransFusion and the
+ * canonical decode at score threshold 0 -- and copies the detections back.
+ * The LiDAR branch starts once the points are uploaded, while the images
+ * still are.  The point count travels in device memory, so the graphs,
+ * captured on the first frame, serve every frame.
  * The LSS cell lists are rebuilt (outside the graph) only when the
  * calibration differs from the previous frame's.  Singular intrinsics,
  * image-augmentation or lidar-augmentation rotations are rejected as in the
