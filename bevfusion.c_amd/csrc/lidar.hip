@@ -294,9 +294,10 @@ struct Feat {
     _Float16 *hi, *lo;
 };
 
-// LDS plan of one conv instantiation: the tap's split weights, double
-// buffered, rows padded by 8 halves so the 16 lanes of a fragment read spread
-// over the banks; then the workgroup's neighbour table and active-tap list.
+// LDS plan of one conv instantiation (CO = the workgroup's output columns):
+// the tap's split weights, double buffered, rows padded by 8 halves so the 16
+// lanes of a fragment read spread over the banks; then the workgroup's
+// neighbour table and active-tap list.
 template <int CI, int CO>
 struct ConvLds {
     static constexpr int LD = CI + 8;        // halves per weight row in LDS
@@ -308,9 +309,20 @@ struct ConvLds {
     static constexpr size_t BYTES = W_BYTES + NBR_BYTES + 32 * sizeof(int);
 };
 
+// Output columns per workgroup.  All of them: slicing CO across workgroups
+// (tried at 32 columns) fits more workgroups per CU but gathers every feature
+// row once per slice, and the gathers already run near the L2 bandwidth
+// (level-2 64-channel convs: ~420 MB of gathered rows in 74 us); sliced, the
+// level-2 and level-3 convs took 1.3-1.9x longer.
+template <int CO>
+constexpr int conv_cow() {
+    return CO;
+}
+
 // Gather GEMM: out[r][co] = bias[co] + sum_t sum_ci in[nbr[r][t]][ci] w[t][co][ci]
 // (+ identity[r][co]) (ReLU), operands split as hi + lo.  A workgroup owns
-// 128 rows; each wave 32 of them (two 16-row MFMA tiles) x all CO columns.
+// 128 rows x COW of the CO output columns (blockIdx.y picks the slice); each
+// wave 32 rows (two 16-row MFMA tiles) x the COW columns.
 // Per workgroup: the rows' neighbour lists go to LDS and the taps some row
 // uses are listed; per listed tap the split weights [co][ci] are staged in
 // LDS (double buffered: the next tap's weights are fetched into registers
@@ -319,16 +331,17 @@ struct ConvLds {
 // are gathered straight from the feature rows, one tap ahead.  A wave skips
 // the MFMAs of a tap none of its rows reaches.  out32, when set, receives
 // fp32 rows instead of a split pair.
-template <int CI, int CO>
+template <int CI, int CO, int COW>
 __global__ __launch_bounds__(256) void sparse_conv_kernel(
     const int *__restrict__ nbr, const unsigned *__restrict__ count, int taps, Feat in,
     const _Float16 *__restrict__ w_hi, const _Float16 *__restrict__ w_lo,
     const float *__restrict__ bias, Feat identity, int relu, Feat out,
     float *__restrict__ out32) {
     using K = KOp<CI>;
-    using L = ConvLds<CI, CO>;
+    using L = ConvLds<CI, COW>;
     typedef typename K::frag frag;
-    constexpr int CT = CO / 16, KC = CI / K::kb;
+    constexpr int CT = COW / 16, KC = CI / K::kb;
+    const int co0 = (int)blockIdx.y * COW;
     extern __shared__ __align__(16) unsigned char smem[];
     _Float16 *sw = reinterpret_cast<_Float16 *>(smem);  // [buffer][hi, lo][CO][LD]
     int *snbr = reinterpret_cast<int *>(smem + L::W_BYTES);  // [row][kTaps]
@@ -337,15 +350,17 @@ __global__ __launch_bounds__(256) void sparse_conv_kernel(
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, col = lane & 15, g = lane >> 4;
     const int wrow = wave * kRowsPerWave;
 
-    // 16-byte pieces of tap t's weights: piece c < CHUNKS/2 of the hi plane,
-    // the rest of the lo plane; row co, halves k..k+7.
+    // 16-byte pieces of the slice of tap t's weights (rows co0..co0+COW-1,
+    // contiguous): piece c < CHUNKS/2 of the hi plane, the rest of the lo
+    // plane; slice row cc / (CI/8), halves k..k+7.
     auto fetch = [&](int t, h8 (&reg)[L::PER]) {
 #pragma unroll
         for (int q = 0; q < L::PER; ++q) {
             const int c = tid + 256 * q;
             if (c < L::CHUNKS) {
                 const int half = c >= L::CHUNKS / 2, cc = c - half * (L::CHUNKS / 2);
-                const _Float16 *src = (half ? w_lo : w_hi) + (size_t)t * CO * CI + (size_t)cc * 8;
+                const _Float16 *src = (half ? w_lo : w_hi) + ((size_t)t * CO + co0) * CI +
+                                      (size_t)cc * 8;
                 reg[q] = *reinterpret_cast<const h8 *>(src);
             }
         }
@@ -463,7 +478,7 @@ __global__ __launch_bounds__(256) void sparse_conv_kernel(
         const unsigned row0 = base + wrow;
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct) {
-            const int co = 16 * ct + col;
+            const int co = co0 + 16 * ct + col;
             const float b = bias[co];
 #pragma unroll
             for (int rt = 0; rt < 2; ++rt)
@@ -833,8 +848,11 @@ void launch_conv(const bf_cuda_lidar_backbone *n, const Conv &c, const unsigned 
 #undef BF_SPLIT
 #define BF_CONV(CI, CO)                                                                        \
     if (c.ci == CI && c.co == CO) {                                                            \
-        sparse_conv_kernel<CI, CO><<<blocks, 256, ConvLds<CI, CO>::BYTES, s>>>(                \
-            n->nbr, count, c.taps, in, c.w_hi, c.w_lo, c.bias, identity, relu, out, out32);    \
+        constexpr int COW = conv_cow<CO>();                                                    \
+        sparse_conv_kernel<CI, CO, COW>                                                        \
+            <<<dim3(blocks, CO / COW), 256, ConvLds<CI, COW>::BYTES, s>>>(                     \
+                n->nbr, count, c.taps, in, c.w_hi, c.w_lo, c.bias, identity, relu, out,        \
+                out32);                                                                        \
         return;                                                                                \
     }
     BF_CONV(32, 32)
@@ -917,9 +935,10 @@ namespace {
 
 template <int CI, int CO>
 int allow_lds(char *error, size_t cap) {
-    return hip_ok(hipFuncSetAttribute(reinterpret_cast<const void *>(&sparse_conv_kernel<CI, CO>),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize,
-                                      (int)ConvLds<CI, CO>::BYTES),
+    constexpr int COW = conv_cow<CO>();
+    return hip_ok(hipFuncSetAttribute(
+                      reinterpret_cast<const void *>(&sparse_conv_kernel<CI, CO, COW>),
+                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)ConvLds<CI, COW>::BYTES),
                   error, cap, "set LiDAR conv LDS size");
 }
 
