@@ -10,11 +10,12 @@
 //   level 0      the caller's voxel rows, in the caller's order;
 //   submanifold  27-tap neighbour table per row (same level, pad 1);
 //   strided      each input site marks every output cell one of its taps
-//                reaches (plain stores of one marker value), then the
-//                marked cells are compacted in cell order — ascending
+//                reaches, one byte per cell in a mark map, then the marked
+//                cells are compacted in cell order — ascending
 //                (batch, z, y, x), the reference's site order — by per-chunk
-//                counts and an in-order write pass (no atomics across
-//                workgroups); then a neighbour table from output to input;
+//                counts and an in-order write pass that also clears the map
+//                (no atomics across workgroups); then a neighbour table from
+//                output to input;
 //   convolution  gather GEMM on the matrix cores: 32 output rows per wave,
 //                K = taps x input channels, each lane gathering its row's
 //                neighbour features as the A operand and the BN-folded
@@ -47,7 +48,7 @@ using namespace bfhip;
 namespace {
 
 constexpr int kTaps = 27, kChunk = 8192, kRowsPerWave = 32, kRowsPerGroup = 4 * kRowsPerWave;
-constexpr int kEmpty = -1, kMarked = -2;
+constexpr int kEmpty = -1;
 constexpr float kBnEps = 1e-3f;
 
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
@@ -132,13 +133,15 @@ __global__ __launch_bounds__(256) void down_neighbors_kernel(const bf_coord4 *__
 }
 
 // Marks every output cell some tap of an input site reaches (the exact
-// strided images of kernels_ref.c:632-644 / 686-707).
+// strided images of kernels_ref.c:632-644 / 686-707): byte `cell` of the
+// mark map, by plain stores of one value (no atomics).
 __global__ __launch_bounds__(256) void mark_kernel(const bf_coord4 *__restrict__ coords,
                                                    const unsigned *__restrict__ count, Grid gout,
-                                                   Geom q, int *__restrict__ grid) {
+                                                   Geom q, unsigned char *__restrict__ marks) {
     const unsigned n = *count;
     for (unsigned j = blockIdx.x * 256 + threadIdx.x; j < n; j += gridDim.x * 256) {
         const bf_coord4 c = coords[j];
+        if ((unsigned)c.batch >= (unsigned)gout.b) continue;
         for (int kz = 0; kz < q.kd; ++kz) {
             const int nz = c.z + q.pd - kz;
             if (nz < 0 || nz % q.sd || nz / q.sd >= gout.d) continue;
@@ -148,24 +151,34 @@ __global__ __launch_bounds__(256) void mark_kernel(const bf_coord4 *__restrict__
                 for (int kx = 0; kx < q.kw; ++kx) {
                     const int nx = c.x + q.pw - kx;
                     if (nx < 0 || nx % q.sw || nx / q.sw >= gout.w) continue;
-                    if ((unsigned)c.batch < (unsigned)gout.b)
-                        grid[cell_of(gout, c.batch, nz / q.sd, ny / q.sh, nx / q.sw)] = kMarked;
+                    marks[cell_of(gout, c.batch, nz / q.sd, ny / q.sh, nx / q.sw)] = 1;
                 }
             }
         }
     }
 }
 
-__global__ __launch_bounds__(256) void compact_count_kernel(const int *__restrict__ grid,
-                                                            long long cells,
+// Bit b of the result: byte b of the 32-cell group w of the mark map is set.
+// The map is padded to whole chunks, so every group is in bounds.
+__device__ __forceinline__ unsigned group_bits(const unsigned char *marks, long long w) {
+    const uint4 *p = reinterpret_cast<const uint4 *>(marks + w * 32);
+    const uint4 lo = p[0], hi = p[1];
+    const unsigned v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+    unsigned bits = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) bits |= (unsigned)((v[i] >> (8 * k)) & 0xffu ? 1u : 0u) << (4 * i + k);
+    return bits;
+}
+
+// Marked cells per chunk of kChunk cells (256 groups of 32 cells).
+__global__ __launch_bounds__(256) void compact_count_kernel(const unsigned char *__restrict__ marks,
+                                                            long long words,
                                                             unsigned *__restrict__ chunk_counts) {
     __shared__ unsigned part[4];
-    const long long base = (long long)blockIdx.x * kChunk;
-    unsigned c = 0;
-    for (int r = 0; r < kChunk / 256; ++r) {
-        const long long i = base + r * 256 + threadIdx.x;
-        c += i < cells && grid[i] == kMarked;
-    }
+    const long long w = (long long)blockIdx.x * 256 + threadIdx.x;
+    unsigned c = w < words ? (unsigned)__popc(group_bits(marks, w)) : 0u;
     for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o);
     if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = c;
     __syncthreads();
@@ -173,13 +186,15 @@ __global__ __launch_bounds__(256) void compact_count_kernel(const int *__restric
 }
 
 // In-order compaction of the marked cells: chunk c starts at the sum of the
-// earlier chunks' counts; inside a chunk, 32 rounds of 256 consecutive cells
-// are ranked by wave ballots.  Rows past the capacity are dropped.
+// earlier chunks' counts; inside a chunk, each thread's word starts at the
+// exclusive scan of the words' popcounts, and its set bits follow in
+// ascending order.  Rows past the capacity are dropped (their cells stay
+// empty).  The groups are cleared for the next strided conv.
 __global__ __launch_bounds__(256) void compact_write_kernel(
-    int *__restrict__ grid, long long cells, const unsigned *__restrict__ chunk_counts,
-    int chunks, unsigned capacity, Grid g, bf_coord4 *__restrict__ coords,
+    unsigned char *__restrict__ marks, long long words, const unsigned *__restrict__ chunk_counts,
+    int chunks, unsigned capacity, Grid g, int *__restrict__ grid, bf_coord4 *__restrict__ coords,
     unsigned *__restrict__ count_out) {
-    __shared__ unsigned part[4], wave_base[4];
+    __shared__ unsigned part[4], wave_total[4];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     unsigned before = 0, total = 0;
     for (int c = t; c < chunks; c += 256) {
@@ -193,42 +208,50 @@ __global__ __launch_bounds__(256) void compact_write_kernel(
     }
     if (lane == 0) {
         part[wave] = before;
-        wave_base[wave] = total;
+        wave_total[wave] = total;
     }
     __syncthreads();
-    unsigned offset = part[0] + part[1] + part[2] + part[3];
+    const unsigned base = part[0] + part[1] + part[2] + part[3];
     if (blockIdx.x == 0 && t == 0) {
-        const unsigned all = wave_base[0] + wave_base[1] + wave_base[2] + wave_base[3];
+        const unsigned all = wave_total[0] + wave_total[1] + wave_total[2] + wave_total[3];
         *count_out = all < capacity ? all : capacity;
     }
     __syncthreads();
-    const long long base = (long long)blockIdx.x * kChunk;
-    for (int r = 0; r < kChunk / 256; ++r) {
-        const long long i = base + r * 256 + t;
-        const bool marked = i < cells && grid[i] == kMarked;
-        const uint64_t ballot = __ballot(marked);
-        if (lane == 0) part[wave] = (unsigned)__popcll(ballot);
-        __syncthreads();
-        unsigned wb = 0;
-        for (int w2 = 0; w2 < wave; ++w2) wb += part[w2];
-        const unsigned round_total = part[0] + part[1] + part[2] + part[3];
-        if (marked) {
-            const unsigned idx = offset + wb + (unsigned)__popcll(ballot & ((1ull << lane) - 1ull));
-            if (idx < capacity) {
-                grid[i] = (int)idx;
-                long long q = i;
-                const int x = (int)(q % g.w);
-                q /= g.w;
-                const int y = (int)(q % g.h);
-                q /= g.h;
-                const int z = (int)(q % g.d);
-                coords[idx] = bf_coord4{(int)(q / g.d), z, y, x};
-            } else {
-                grid[i] = kEmpty;
-            }
+    const long long w = (long long)blockIdx.x * 256 + t;
+    unsigned bits = 0;
+    if (w < words) {
+        bits = group_bits(marks, w);
+        if (bits) {
+            uint4 *p = reinterpret_cast<uint4 *>(marks + w * 32);
+            p[0] = make_uint4(0u, 0u, 0u, 0u);
+            p[1] = make_uint4(0u, 0u, 0u, 0u);
         }
-        offset += round_total;
-        __syncthreads();
+    }
+    const unsigned c = (unsigned)__popc(bits);
+    unsigned inc = c;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const unsigned u = __shfl_up(inc, o);
+        if (lane >= o) inc += u;
+    }
+    if (lane == 63) part[wave] = inc;
+    __syncthreads();
+    unsigned idx = base + inc - c;
+    for (int w2 = 0; w2 < wave; ++w2) idx += part[w2];
+    while (bits) {
+        const int b = __ffs(bits) - 1;
+        bits &= bits - 1;
+        if (idx < capacity) {
+            long long q = w * 32 + b;
+            grid[q] = (int)idx;
+            const int x = (int)(q % g.w);
+            q /= g.w;
+            const int y = (int)(q % g.h);
+            q /= g.h;
+            const int z = (int)(q % g.d);
+            coords[idx] = bf_coord4{(int)(q / g.d), z, y, x};
+        }
+        ++idx;
     }
 }
 
@@ -673,6 +696,7 @@ struct bf_cuda_lidar_backbone {
     int *grid[5], *nbr;
     bf_coord4 *coords[5];
     unsigned *counts, *chunk_counts;
+    unsigned char *marks;
     Feat feat[3];
     float *out32;
 };
@@ -802,6 +826,8 @@ int build(bf_cuda_lidar_backbone *n, const bf_model *m, char *error, size_t cap)
     const size_t o_nbr = take(n->capacity * kTaps * sizeof(int));
     const size_t o_counts = take(8 * sizeof(unsigned));
     const size_t o_chunks = take((size_t)std::max(n->max_chunks, 1) * sizeof(unsigned));
+    const size_t mark_bytes = (size_t)std::max(n->max_chunks, 1) * kChunk;  // whole chunks
+    const size_t o_marks = take(mark_bytes);
     size_t o_feat[3];
     for (int i = 0; i < 3; ++i) o_feat[i] = take(2 * n->capacity * 128 * sizeof(_Float16));
     const size_t o_out = take(n->capacity * 128 * sizeof(float));
@@ -820,6 +846,10 @@ int build(bf_cuda_lidar_backbone *n, const bf_model *m, char *error, size_t cap)
     n->nbr = (int *)(a + o_nbr);
     n->counts = (unsigned *)(a + o_counts);
     n->chunk_counts = (unsigned *)(a + o_chunks);
+    n->marks = a + o_marks;
+    // The mark map is clear between strided convs: each compaction clears it.
+    if (!hip_ok(hipMemset(n->marks, 0, mark_bytes), error, cap, "clear LiDAR mark map"))
+        return 0;
     for (int i = 0; i < 3; ++i) {
         n->feat[i].hi = (_Float16 *)(a + o_feat[i]);
         n->feat[i].lo = n->feat[i].hi + n->capacity * 128;
@@ -868,11 +898,12 @@ void launch_conv(const bf_cuda_lidar_backbone *n, const Conv &c, const unsigned 
 void strided_sites(bf_cuda_lidar_backbone *n, const Conv &c, int l, const bf_coord4 *in_coords,
                    hipStream_t s) {
     const unsigned rb = row_blocks(n->capacity, 256);
-    mark_kernel<<<rb, 256, 0, s>>>(in_coords, n->counts + l, n->lv[l + 1], c.q, n->grid[l + 1]);
+    mark_kernel<<<rb, 256, 0, s>>>(in_coords, n->counts + l, n->lv[l + 1], c.q, n->marks);
     const int chunks = (int)((n->cells[l + 1] + kChunk - 1) / kChunk);
-    compact_count_kernel<<<chunks, 256, 0, s>>>(n->grid[l + 1], n->cells[l + 1], n->chunk_counts);
-    compact_write_kernel<<<chunks, 256, 0, s>>>(n->grid[l + 1], n->cells[l + 1], n->chunk_counts,
-                                                chunks, (unsigned)n->capacity, n->lv[l + 1],
+    const long long words = (n->cells[l + 1] + 31) / 32;
+    compact_count_kernel<<<chunks, 256, 0, s>>>(n->marks, words, n->chunk_counts);
+    compact_write_kernel<<<chunks, 256, 0, s>>>(n->marks, words, n->chunk_counts, chunks,
+                                                (unsigned)n->capacity, n->lv[l + 1], n->grid[l + 1],
                                                 n->coords[l + 1], n->counts + l + 1);
     down_neighbors_kernel<<<rb, 256, 0, s>>>(n->coords[l + 1], n->counts + l + 1, n->lv[l], c.q,
                                              n->grid[l], n->nbr);
