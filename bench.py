@@ -600,7 +600,7 @@ def tf_cpu_baseline(path, seed=0):
             "cpu_model": _cpu_model()}
 
 
-LIDAR_POINTS, LIDAR_SWEEPS = 100000, 10  # ~54k voxels, near the reference's stress frame
+LIDAR_POINTS, LIDAR_SWEEPS = 100000, 10  # the runtime frame's cloud: ~54k voxels
 LIDAR_GRID = (41, 1440, 1440)
 LIDAR_VOXELS, LIDAR_SPARSE = 160000, 160000  # the reference runtime's capacities
 # Reference CUDA LiDAR branch, points -> LiDAR BEV, 100k points / 50k voxels,
@@ -665,16 +665,17 @@ def lidar_work(coords, dims=LIDAR_GRID):
 
 
 def lidar_leg(dev, reps, seed=0):
-    """LiDAR branch on one frame of 100k synthetic points: depth raster into the
-    six camera images, voxeliser + MeanVFE, SECOND sparse encoder to the dense
-    [256,180,180] BEV; ms per frame (eager and graph replay)."""
+    """LiDAR branch on the reference's stress frame (100k points, two per voxel,
+    50k voxels; bfw.stress_points): depth raster into the six camera images,
+    voxeliser + MeanVFE, SECOND sparse encoder to the dense [256,180,180] BEV;
+    ms per frame (eager and graph replay)."""
     import torch
     import bfhip
     from bfhip import bfw, frame_scene
     tmp = pathlib.Path(tempfile.mkdtemp(prefix="lidar_"))
     path = bfw.write_lidar_backbone(tmp / "lidar.bfw", seed=seed, mode="fan_in", gain=1.2)
     cal = frame_scene.calibration(seed)
-    pts_np = bfw.synthetic_points(seed, LIDAR_POINTS, sweeps=LIDAR_SWEEPS)
+    pts_np = bfw.stress_points(LIDAR_POINTS)
     t = lambda a: torch.from_numpy(a).to(dev)
     pts = t(pts_np)
     aug, l2i, post = t(cal["lidar_augmentation"]), t(cal["lidar_to_image"]), t(cal["image_augmentation"])
@@ -723,10 +724,11 @@ def lidar_leg(dev, reps, seed=0):
     flops, sites = lidar_work(coords[:n].cpu().numpy())
     enc_ms = parts["sparse_encoder"]
     tflops = flops / (enc_ms * 1e-3) / 1e12
-    out = {"workload": f"LiDAR branch, {LIDAR_POINTS} synthetic points ({LIDAR_SWEEPS} sweeps) -> depth raster (6 x 256 x "
-                       f"704) + voxeliser/MeanVFE ({n} voxels) + SECOND sparse encoder on the "
-                       "41 x 1440 x 1440 grid -> [256,180,180] BEV; random-init weights; split "
-                       "fp16 MFMA operands (hi + lo), fp32 accumulation",
+    out = {"workload": f"LiDAR branch, the reference's stress frame ({LIDAR_POINTS} points, two per "
+                       f"voxel) -> depth raster (6 x 256 x 704) + voxeliser/MeanVFE ({n} voxels) "
+                       "+ SECOND sparse encoder on the 41 x 1440 x 1440 grid -> [256,180,180] "
+                       "BEV; random-init weights; split fp16 MFMA operands (hi + lo), fp32 "
+                       "accumulation",
            "ms": round(ms, 4), "ms_eager": round(eager_ms, 4),
            "parts_ms": {k: round(v, 4) for k, v in parts.items()},
            "voxels": n, "sites_per_level": sites, "encoder_gflop": round(flops / 1e9, 2),
@@ -762,7 +764,7 @@ def lidar_cpu_baseline(path, pts):
     threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or os.cpu_count()
     return {"value": round((t1 - t0) * 1e3, 1), "unit": "ms/frame", "cores": threads,
             "kind": kind, "backend": o.backend(),
-            "sample": f"voxeliser + MeanVFE + sparse encoder on the full {LIDAR_POINTS}-point frame",
+            "sample": f"voxeliser + MeanVFE + sparse encoder on the full {LIDAR_POINTS}-point stress frame",
             "cpu_model": _cpu_model()}
 
 

@@ -406,6 +406,26 @@ def synthetic_points(seed: int, count: int, clusters: int = 48, extent=54.0, z_r
     return np.ascontiguousarray(out)
 
 
+def stress_points(count: int = 100000) -> np.ndarray:
+    """The reference's LiDAR stress frame (tests/test_cuda_lidar.cu, its
+    initialize_points): point i sits at the centre of voxel v = i // 2 of the
+    production grid, x = v mod 1440, y = (v // 1440) mod 1440, z = hash(v) mod
+    40 with hash(v) = (v * 2654435761) >> 16 (64-bit); intensity
+    ((i mod 31) - 15) * 0.02, time ((i mod 17) - 8) * 0.01.  100k points give
+    50k voxels, two points each, in a 1440 x 35 strip of columns."""
+    i = np.arange(count, dtype=np.uint64)
+    v = i // np.uint64(2)
+    x = (v % np.uint64(1440)).astype(np.float32)
+    y = ((v // np.uint64(1440)) % np.uint64(1440)).astype(np.float32)
+    z = (((v * np.uint64(2654435761)) >> np.uint64(16)) % np.uint64(40)).astype(np.float32)
+    f = np.float32
+    out = np.stack([f(-54.0) + (x + f(0.5)) * f(0.075), f(-54.0) + (y + f(0.5)) * f(0.075),
+                    f(-5.0) + (z + f(0.5)) * f(0.2),
+                    ((i % np.uint64(31)).astype(np.int64) - 15).astype(np.float32) * f(0.02),
+                    ((i % np.uint64(17)).astype(np.int64) - 8).astype(np.float32) * f(0.01)], 1)
+    return np.ascontiguousarray(out, np.float32)
+
+
 def write_bev_stage(path, seed: int = 0, mode: str = "baseline", gain: float = 1.0) -> pathlib.Path:
     path = pathlib.Path(path)
     write_bfw(bev_stage_tensors(_Init(seed, mode, gain)), path)

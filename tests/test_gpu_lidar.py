@@ -188,6 +188,32 @@ def test_lidar_pipeline_production_grid(device, lidar_path):
         net.close()
 
 
+def test_lidar_pipeline_reference_stress_frame(device, lidar_path):
+    """The reference's own stress frame (tests/test_cuda_lidar.cu: 100k
+    points, two per voxel, 50k voxels; level 1 holds 155 985 sites, just
+    under the runtime's 160 000 capacity) through the GPU voxeliser and
+    encoder against the oracle chain."""
+    import torch
+    pts = bfw.stress_points(100000)
+    o = oracle.Oracle("port")
+    vx, oc, on, _ = o.voxelize(pts, oracle.voxel_config(160000))
+    assert len(oc) == 50000 and np.all(on == 2)
+    om = o.mean_vfe(vx, on)
+    want = _backbone_oracle(lidar_path, oc, om, 41, 1440, 1440)
+    with bfhip.Voxelizer(bfhip.voxel_config(160000), 100000) as vox, bfhip.Model(lidar_path) as m:
+        net = bfhip.LidarBackbone(m, 1, 41, 1440, 1440, 160000)
+        print("[case] lidar stress frame 100k points", flush=True)
+        coords, means, count = vox.forward(_t(pts, device))
+        got = net.forward(coords, means, count)
+        torch.cuda.synchronize()
+        n = int(count.item())
+        assert n == 50000
+        assert np.array_equal(coords[:n].cpu().numpy(), oc)
+        assert np.array_equal(means[:n].cpu().numpy(), om)
+        _check_bev(got.cpu().numpy(), want, "stress")
+        net.close()
+
+
 def test_lidar_graph_replay(device, lidar_path):
     """Raster + voxeliser + encoder captured in one graph; every replay, with
     eager work and synchronisation in between, equals the eager frame."""
