@@ -317,8 +317,7 @@ struct Feat {
     _Float16 *hi, *lo;
 };
 
-// LDS plan of one conv instantiation (CO = the workgroup's output columns):
-// the tap's split weights, double buffered, rows padded by 8 halves so the 16
+// LDS plan of one conv instantiation: the tap's split weights, double buffered, rows padded by 8 halves so the 16
 // lanes of a fragment read spread over the banks; then the workgroup's
 // neighbour table and active-tap list.
 template <int CI, int CO>
@@ -332,20 +331,24 @@ struct ConvLds {
     static constexpr size_t BYTES = W_BYTES + NBR_BYTES + 32 * sizeof(int);
 };
 
-// Output columns per workgroup.  All of them: slicing CO across workgroups
-// (tried at 32 columns) fits more workgroups per CU but gathers every feature
-// row once per slice, and the gathers already run near the L2 bandwidth
-// (level-2 64-channel convs: ~420 MB of gathered rows in 74 us); sliced, the
-// level-2 and level-3 convs took 1.3-1.9x longer.
-template <int CO>
-constexpr int conv_cow() {
-    return CO;
+// Tap groups: a level with few rows has few 128-row workgroups, each walking
+// every tap in turn while most CUs idle, so up to kTapGroups workgroups share
+// a row block, each taking a contiguous part of its active-tap list and
+// writing fp32 partial sums; split_reduce_kernel adds them in group order.
+// Whether to split is decided on the device from the row count (the launch
+// carries the groups and the extra ones exit), so one graph fits any frame.
+constexpr int kTapGroups = 4;
+constexpr unsigned kSplitRows = 16384;  // split at most this many rows
+
+__device__ __forceinline__ int tap_groups(unsigned n, int launched) {
+    return n <= kSplitRows ? launched : 1;
 }
 
 // Gather GEMM: out[r][co] = bias[co] + sum_t sum_ci in[nbr[r][t]][ci] w[t][co][ci]
 // (+ identity[r][co]) (ReLU), operands split as hi + lo.  A workgroup owns
-// 128 rows x COW of the CO output columns (blockIdx.y picks the slice); each
-// wave 32 rows (two 16-row MFMA tiles) x the COW columns.
+// 128 rows x all CO columns; each wave 32 rows (two 16-row MFMA tiles).
+// blockIdx.y is the tap group; with several groups in effect the workgroup
+// writes its fp32 partial sums to `part` [group][row][co] instead.
 // Per workgroup: the rows' neighbour lists go to LDS and the taps some row
 // uses are listed; per listed tap the split weights [co][ci] are staged in
 // LDS (double buffered: the next tap's weights are fetched into registers
@@ -354,36 +357,35 @@ constexpr int conv_cow() {
 // are gathered straight from the feature rows, one tap ahead.  A wave skips
 // the MFMAs of a tap none of its rows reaches.  out32, when set, receives
 // fp32 rows instead of a split pair.
-template <int CI, int CO, int COW>
+template <int CI, int CO>
 __global__ __launch_bounds__(256) void sparse_conv_kernel(
     const int *__restrict__ nbr, const unsigned *__restrict__ count, int taps, Feat in,
     const _Float16 *__restrict__ w_hi, const _Float16 *__restrict__ w_lo,
     const float *__restrict__ bias, Feat identity, int relu, Feat out,
-    float *__restrict__ out32) {
+    float *__restrict__ out32, float *__restrict__ part) {
     using K = KOp<CI>;
-    using L = ConvLds<CI, COW>;
+    using L = ConvLds<CI, CO>;
     typedef typename K::frag frag;
-    constexpr int CT = COW / 16, KC = CI / K::kb;
-    const int co0 = (int)blockIdx.y * COW;
+    constexpr int CT = CO / 16, KC = CI / K::kb;
     extern __shared__ __align__(16) unsigned char smem[];
     _Float16 *sw = reinterpret_cast<_Float16 *>(smem);  // [buffer][hi, lo][CO][LD]
     int *snbr = reinterpret_cast<int *>(smem + L::W_BYTES);  // [row][kTaps]
     int *stap = snbr + kRowsPerGroup * kTaps;                // [0] mask, [1] count, [2..] list
     const unsigned n = *count;
+    const int groups = tap_groups(n, (int)gridDim.y), group = (int)blockIdx.y;
+    if (group >= groups) return;  // whole workgroup: before any barrier
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, col = lane & 15, g = lane >> 4;
     const int wrow = wave * kRowsPerWave;
 
-    // 16-byte pieces of the slice of tap t's weights (rows co0..co0+COW-1,
-    // contiguous): piece c < CHUNKS/2 of the hi plane, the rest of the lo
-    // plane; slice row cc / (CI/8), halves k..k+7.
+    // 16-byte pieces of tap t's weights: piece c < CHUNKS/2 of the hi plane,
+    // the rest of the lo plane; row cc / (CI/8), halves k..k+7.
     auto fetch = [&](int t, h8 (&reg)[L::PER]) {
 #pragma unroll
         for (int q = 0; q < L::PER; ++q) {
             const int c = tid + 256 * q;
             if (c < L::CHUNKS) {
                 const int half = c >= L::CHUNKS / 2, cc = c - half * (L::CHUNKS / 2);
-                const _Float16 *src = (half ? w_lo : w_hi) + ((size_t)t * CO + co0) * CI +
-                                      (size_t)cc * 8;
+                const _Float16 *src = (half ? w_lo : w_hi) + (size_t)t * CO * CI + (size_t)cc * 8;
                 reg[q] = *reinterpret_cast<const h8 *>(src);
             }
         }
@@ -440,7 +442,11 @@ __global__ __launch_bounds__(256) void sparse_conv_kernel(
             stap[1] = c;
         }
         __syncthreads();
-        const int active = stap[1];
+        // This group's part of the active-tap list: entries [first, last).
+        const int listed = stap[1], per = (listed + groups - 1) / groups;
+        const int first = min(listed, group * per), last = min(listed, first + per);
+        const int *list = stap + 2 + first;
+        const int active = last - first;
 
         f32x4 acc[2][CT];
 #pragma unroll
@@ -451,18 +457,18 @@ __global__ __launch_bounds__(256) void sparse_conv_kernel(
         frag ah[2][KC], al[2][KC];
         bool live[2] = {false, false};
         if (active) {
-            fetch(stap[2], wreg);
+            fetch(list[0], wreg);
             stage(0, wreg);
-            gather(stap[2], ah, al, live);
+            gather(list[0], ah, al, live);
         }
         __syncthreads();
         for (int i = 0; i < active; ++i) {
             const int buf = i & 1;
             const bool more = i + 1 < active;
-            if (more) fetch(stap[3 + i], wreg);
+            if (more) fetch(list[i + 1], wreg);
             frag nh[2][KC], nl[2][KC];
             bool nlive[2] = {false, false};
-            if (more) gather(stap[3 + i], nh, nl, nlive);
+            if (more) gather(list[i + 1], nh, nl, nlive);
             // Wave-uniform: a tap none of the wave's rows reaches adds nothing.
             if (__ballot(live[0] || live[1])) {
                 const _Float16 *bh_base = sw + (size_t)(2 * buf) * L::PLANE;
@@ -501,7 +507,7 @@ __global__ __launch_bounds__(256) void sparse_conv_kernel(
         const unsigned row0 = base + wrow;
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct) {
-            const int co = co0 + 16 * ct + col;
+            const int co = 16 * ct + col;
             const float b = bias[co];
 #pragma unroll
             for (int rt = 0; rt < 2; ++rt)
@@ -510,6 +516,10 @@ __global__ __launch_bounds__(256) void sparse_conv_kernel(
                     const unsigned r = row0 + 16 * rt + 4 * g + j;
                     if (r >= n) continue;
                     const size_t at = (size_t)r * CO + co;
+                    if (groups > 1) {
+                        part[((size_t)group * kSplitRows + r) * CO + co] = acc[rt][ct][j];
+                        continue;
+                    }
                     float v = acc[rt][ct][j] + b;
                     if (identity.hi) v += (float)identity.hi[at] + (float)identity.lo[at];
                     if (relu) v = fmaxf(v, 0.0f);
@@ -518,6 +528,28 @@ __global__ __launch_bounds__(256) void sparse_conv_kernel(
                 }
         }
         __syncthreads();  // LDS is rewritten by the next row group
+    }
+}
+
+// Sum of the tap groups' partials in group order, then bias, residual and
+// ReLU; nothing to do when the conv ran unsplit.
+template <int CO>
+__global__ __launch_bounds__(256) void split_reduce_kernel(
+    const unsigned *__restrict__ count, int launched, const float *__restrict__ part,
+    const float *__restrict__ bias, Feat identity, int relu, Feat out, float *__restrict__ out32) {
+    const unsigned n = *count;
+    const int groups = tap_groups(n, launched);
+    if (groups == 1) return;
+    for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < (size_t)n * CO;
+         e += (size_t)gridDim.x * 256) {
+        const int co = (int)(e % CO);
+        float v = 0.0f;
+        for (int gi = 0; gi < groups; ++gi) v += part[(size_t)gi * kSplitRows * CO + e];
+        v += bias[co];
+        if (identity.hi) v += (float)identity.hi[e] + (float)identity.lo[e];
+        if (relu) v = fmaxf(v, 0.0f);
+        if (out32) out32[e] = v;
+        else split_store(v, out.hi + e, out.lo + e);
     }
 }
 
@@ -698,7 +730,7 @@ struct bf_cuda_lidar_backbone {
     unsigned *counts, *chunk_counts;
     unsigned char *marks;
     Feat feat[3];
-    float *out32;
+    float *out32, *part;
 };
 
 namespace {
@@ -831,6 +863,7 @@ int build(bf_cuda_lidar_backbone *n, const bf_model *m, char *error, size_t cap)
     size_t o_feat[3];
     for (int i = 0; i < 3; ++i) o_feat[i] = take(2 * n->capacity * 128 * sizeof(_Float16));
     const size_t o_out = take(n->capacity * 128 * sizeof(float));
+    const size_t o_part = take((size_t)kTapGroups * kSplitRows * 128 * sizeof(float));
     if (!hip_ok(hipMalloc((void **)&n->work, off), error, cap, "allocate LiDAR workspace"))
         return 0;
     n->resident_bytes += off;
@@ -855,6 +888,7 @@ int build(bf_cuda_lidar_backbone *n, const bf_model *m, char *error, size_t cap)
         n->feat[i].lo = n->feat[i].hi + n->capacity * 128;
     }
     n->out32 = (float *)(a + o_out);
+    n->part = (float *)(a + o_part);
     return 1;
 }
 
@@ -878,11 +912,13 @@ void launch_conv(const bf_cuda_lidar_backbone *n, const Conv &c, const unsigned 
 #undef BF_SPLIT
 #define BF_CONV(CI, CO)                                                                        \
     if (c.ci == CI && c.co == CO) {                                                            \
-        constexpr int COW = conv_cow<CO>();                                                    \
-        sparse_conv_kernel<CI, CO, COW>                                                        \
-            <<<dim3(blocks, CO / COW), 256, ConvLds<CI, COW>::BYTES, s>>>(                     \
-                n->nbr, count, c.taps, in, c.w_hi, c.w_lo, c.bias, identity, relu, out,        \
-                out32);                                                                        \
+        const int groups = CI >= 64 ? kTapGroups : 1;                                          \
+        sparse_conv_kernel<CI, CO><<<dim3(blocks, groups), 256, ConvLds<CI, CO>::BYTES, s>>>(  \
+            n->nbr, count, c.taps, in, c.w_hi, c.w_lo, c.bias, identity, relu, out, out32,     \
+            n->part);                                                                          \
+        if (groups > 1)                                                                        \
+            split_reduce_kernel<CO><<<1024, 256, 0, s>>>(count, groups, n->part, c.bias,       \
+                                                         identity, relu, out, out32);          \
         return;                                                                                \
     }
     BF_CONV(32, 32)
@@ -966,10 +1002,9 @@ namespace {
 
 template <int CI, int CO>
 int allow_lds(char *error, size_t cap) {
-    constexpr int COW = conv_cow<CO>();
-    return hip_ok(hipFuncSetAttribute(
-                      reinterpret_cast<const void *>(&sparse_conv_kernel<CI, CO, COW>),
-                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)ConvLds<CI, COW>::BYTES),
+    return hip_ok(hipFuncSetAttribute(reinterpret_cast<const void *>(&sparse_conv_kernel<CI, CO>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      (int)ConvLds<CI, CO>::BYTES),
                   error, cap, "set LiDAR conv LDS size");
 }
 
