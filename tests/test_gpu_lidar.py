@@ -214,6 +214,32 @@ def test_lidar_pipeline_reference_stress_frame(device, lidar_path):
         net.close()
 
 
+def test_lidar_backbone_capacity_overflow(device, lidar_path):
+    """Scattered sites whose strided images outnumber `sparse_capacity` at
+    level 1: the forward drops the sites beyond the capacity in cell order
+    (the reference GPU path drops an arbitrary subset), stays finite and
+    repeats bit for bit; with room for every site it matches the oracle."""
+    import torch
+    rng = np.random.default_rng(12)
+    cells = rng.choice(41 * 96 * 96, size=400, replace=False)
+    coords = np.stack([np.zeros(400, np.int64), cells // (96 * 96), cells // 96 % 96, cells % 96],
+                      1).astype(np.int32)
+    feats = rng.standard_normal((400, 5)).astype(np.float32)
+    c, f = _t(coords, device), _t(feats, device)
+    with bfhip.Model(lidar_path) as m:
+        small = bfhip.LidarBackbone(m, 1, 41, 96, 96, 1000)
+        roomy = bfhip.LidarBackbone(m, 1, 41, 96, 96, 20000)
+    print("[case] lidar capacity overflow 400 sites, capacity 1000", flush=True)
+    a = small.forward(c, f, 400).cpu().numpy()
+    b = small.forward(c, f, 400).cpu().numpy()
+    full = roomy.forward(c, f, 400).cpu().numpy()
+    assert np.isfinite(a).all() and np.array_equal(a, b)
+    assert (a != 0).any() and not np.array_equal(a, full)
+    _check_bev(full, _backbone_oracle(lidar_path, coords, feats, 41, 96, 96), "scattered")
+    small.close()
+    roomy.close()
+
+
 def test_lidar_graph_replay(device, lidar_path):
     """Raster + voxeliser + encoder captured in one graph; every replay, with
     eager work and synchronisation in between, equals the eager frame."""
