@@ -320,15 +320,27 @@ struct Feat {
 // LDS plan of one conv instantiation: the tap's split weights, double buffered, rows padded by 8 halves so the 16
 // lanes of a fragment read spread over the banks; then the workgroup's
 // neighbour table and active-tap list.
-template <int CI, int CO>
+// CO here is the workgroup's output columns; BUFS is 2 (double buffered) or 1.
+template <int CI, int CO, int BUFS = 2>
 struct ConvLds {
     static constexpr int LD = CI + 8;        // halves per weight row in LDS
     static constexpr int PLANE = CO * LD;    // halves per hi or lo plane
     static constexpr int CHUNKS = 2 * CO * CI / 8;  // 16-byte pieces of one tap (hi + lo)
     static constexpr int PER = (CHUNKS + 255) / 256;
-    static constexpr size_t W_BYTES = (size_t)2 * 2 * PLANE * sizeof(_Float16);
+    static constexpr size_t W_BYTES = (size_t)BUFS * 2 * PLANE * sizeof(_Float16);
     static constexpr size_t NBR_BYTES = (size_t)kRowsPerGroup * kTaps * sizeof(int);
     static constexpr size_t BYTES = W_BYTES + NBR_BYTES + 32 * sizeof(int);
+};
+
+// Workgroup shape per layer width: output columns per workgroup and weight
+// buffers.  The 128-channel convs split their columns in two and stage one
+// tap at a time: 49 KB of LDS instead of 153 KB, so two workgroups share a
+// CU (the level-3 convs otherwise run one wave per SIMD), at the price of
+// gathering each feature row twice.
+template <int CI, int CO>
+struct ConvShape {
+    static constexpr int COW = CI == 128 ? 64 : CO;
+    static constexpr int BUFS = CI == 128 ? 1 : 2;
 };
 
 // Tap groups: a level with few rows has few 128-row workgroups, each walking
@@ -346,7 +358,9 @@ __device__ __forceinline__ int tap_groups(unsigned n, int launched) {
 
 // Gather GEMM: out[r][co] = bias[co] + sum_t sum_ci in[nbr[r][t]][ci] w[t][co][ci]
 // (+ identity[r][co]) (ReLU), operands split as hi + lo.  A workgroup owns
-// 128 rows x all CO columns; each wave 32 rows (two 16-row MFMA tiles).
+// 128 rows x COW of the CO columns (blockIdx.z picks the slice); each wave
+// 32 rows (two 16-row MFMA tiles).  BUFS = 1 stages one tap's weights at a
+// time (two barriers per tap) to leave room for more workgroups per CU.
 // blockIdx.y is the tap group; with several groups in effect the workgroup
 // writes its fp32 partial sums to `part` [group][row][co] instead.
 // Per workgroup: the rows' neighbour lists go to LDS and the taps some row
@@ -357,16 +371,17 @@ __device__ __forceinline__ int tap_groups(unsigned n, int launched) {
 // are gathered straight from the feature rows, one tap ahead.  A wave skips
 // the MFMAs of a tap none of its rows reaches.  out32, when set, receives
 // fp32 rows instead of a split pair.
-template <int CI, int CO>
+template <int CI, int CO, int COW, int BUFS>
 __global__ __launch_bounds__(256) void sparse_conv_kernel(
     const int *__restrict__ nbr, const unsigned *__restrict__ count, int taps, Feat in,
     const _Float16 *__restrict__ w_hi, const _Float16 *__restrict__ w_lo,
     const float *__restrict__ bias, Feat identity, int relu, Feat out,
     float *__restrict__ out32, float *__restrict__ part) {
     using K = KOp<CI>;
-    using L = ConvLds<CI, CO>;
+    using L = ConvLds<CI, COW, BUFS>;
     typedef typename K::frag frag;
-    constexpr int CT = CO / 16, KC = CI / K::kb;
+    constexpr int CT = COW / 16, KC = CI / K::kb;
+    const int co0 = (int)blockIdx.z * COW;
     extern __shared__ __align__(16) unsigned char smem[];
     _Float16 *sw = reinterpret_cast<_Float16 *>(smem);  // [buffer][hi, lo][CO][LD]
     int *snbr = reinterpret_cast<int *>(smem + L::W_BYTES);  // [row][kTaps]
@@ -385,7 +400,8 @@ __global__ __launch_bounds__(256) void sparse_conv_kernel(
             const int c = tid + 256 * q;
             if (c < L::CHUNKS) {
                 const int half = c >= L::CHUNKS / 2, cc = c - half * (L::CHUNKS / 2);
-                const _Float16 *src = (half ? w_lo : w_hi) + (size_t)t * CO * CI + (size_t)cc * 8;
+                const _Float16 *src = (half ? w_lo : w_hi) + ((size_t)t * CO + co0) * CI +
+                                      (size_t)cc * 8;
                 reg[q] = *reinterpret_cast<const h8 *>(src);
             }
         }
@@ -463,7 +479,7 @@ __global__ __launch_bounds__(256) void sparse_conv_kernel(
         }
         __syncthreads();
         for (int i = 0; i < active; ++i) {
-            const int buf = i & 1;
+            const int buf = BUFS == 2 ? i & 1 : 0;
             const bool more = i + 1 < active;
             if (more) fetch(list[i + 1], wreg);
             frag nh[2][KC], nl[2][KC];
@@ -491,7 +507,8 @@ __global__ __launch_bounds__(256) void sparse_conv_kernel(
                 }
             }
             if (more) {
-                stage(buf ^ 1, wreg);
+                if (BUFS == 1) __syncthreads();  // every wave is done with this tap's weights
+                stage(BUFS == 2 ? buf ^ 1 : 0, wreg);
 #pragma unroll
                 for (int rt = 0; rt < 2; ++rt) {
                     live[rt] = nlive[rt];
@@ -507,7 +524,7 @@ __global__ __launch_bounds__(256) void sparse_conv_kernel(
         const unsigned row0 = base + wrow;
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct) {
-            const int co = 16 * ct + col;
+            const int co = co0 + 16 * ct + col;
             const float b = bias[co];
 #pragma unroll
             for (int rt = 0; rt < 2; ++rt)
@@ -912,10 +929,12 @@ void launch_conv(const bf_cuda_lidar_backbone *n, const Conv &c, const unsigned 
 #undef BF_SPLIT
 #define BF_CONV(CI, CO)                                                                        \
     if (c.ci == CI && c.co == CO) {                                                            \
+        using S = ConvShape<CI, CO>;                                                           \
         const int groups = CI >= 64 ? kTapGroups : 1;                                          \
-        sparse_conv_kernel<CI, CO><<<dim3(blocks, groups), 256, ConvLds<CI, CO>::BYTES, s>>>(  \
-            n->nbr, count, c.taps, in, c.w_hi, c.w_lo, c.bias, identity, relu, out, out32,     \
-            n->part);                                                                          \
+        sparse_conv_kernel<CI, CO, S::COW, S::BUFS>                                            \
+            <<<dim3(blocks, groups, CO / S::COW), 256, ConvLds<CI, S::COW, S::BUFS>::BYTES,    \
+               s>>>(n->nbr, count, c.taps, in, c.w_hi, c.w_lo, c.bias, identity, relu, out,    \
+                    out32, n->part);                                                           \
         if (groups > 1)                                                                        \
             split_reduce_kernel<CO><<<1024, 256, 0, s>>>(count, groups, n->part, c.bias,       \
                                                          identity, relu, out, out32);          \
@@ -1002,9 +1021,11 @@ namespace {
 
 template <int CI, int CO>
 int allow_lds(char *error, size_t cap) {
-    return hip_ok(hipFuncSetAttribute(reinterpret_cast<const void *>(&sparse_conv_kernel<CI, CO>),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize,
-                                      (int)ConvLds<CI, CO>::BYTES),
+    using S = ConvShape<CI, CO>;
+    return hip_ok(hipFuncSetAttribute(
+                      reinterpret_cast<const void *>(&sparse_conv_kernel<CI, CO, S::COW, S::BUFS>),
+                      hipFuncAttributeMaxDynamicSharedMemorySize,
+                      (int)ConvLds<CI, S::COW, S::BUFS>::BYTES),
                   error, cap, "set LiDAR conv LDS size");
 }
 
