@@ -423,6 +423,14 @@ extern "C" int bf_cuda_runtime_infer(bf_cuda_runtime *r, const bf_frame_input *f
     const hipStream_t s = r->stream;
     const unsigned count = (unsigned)f->point_count;
     const size_t F = sizeof(float);
+    // Once anything is enqueued, a failure drains both streams before
+    // returning: copies still read `count` and `key` from this frame, and the
+    // next call rewrites the buffers the LiDAR stream may still be reading.
+    auto drain = [&]() {
+        (void)hipStreamSynchronize(r->side);
+        (void)hipStreamSynchronize(s);
+        return 0;
+    };
     // Points and matrices first: the LiDAR branch needs nothing else.
     if (!hip_ok(hipMemcpyAsync(r->points, f->points, f->point_count * 5 * F,
                                hipMemcpyHostToDevice, s), error, cap, "upload HIP points") ||
@@ -442,21 +450,21 @@ extern "C" int bf_cuda_runtime_infer(bf_cuda_runtime *r, const bf_frame_input *f
                                hipMemcpyHostToDevice, s), error, cap, "upload HIP images") ||
         !hip_ok(hipMemcpyAsync(r->calib, key, sizeof(key), hipMemcpyHostToDevice, s), error, cap,
                 "upload HIP calibration"))
-        return 0;
+        return drain();
     const bool changed = !r->calib_valid || std::memcmp(key, r->calib_key, sizeof(key)) != 0;
     if (changed &&
         !bf_cuda_lss_plan_prepare_calibration_f32(r->lss, r->frustum, r->calib, r->calib + 54,
                                                   r->calib + 72, r->calib + 126, r->calib + 180,
                                                   r->calib + 198, r->calib + 207, s, error, cap))
-        return 0;
+        return drain();
     if (!run_part(r, 1, enqueue_camera, s, error, cap) ||
         !hip_ok(hipStreamWaitEvent(s, r->join, 0), error, cap, "join LiDAR branch") ||
         !run_part(r, 2, enqueue_tail, s, error, cap))
-        return 0;
+        return drain();
     if (!hip_ok(hipMemcpyAsync(detections, r->detections, sizeof(*detections),
                                hipMemcpyDeviceToHost, s), error, cap, "copy HIP detections") ||
         !hip_ok(hipStreamSynchronize(s), error, cap, "synchronize HIP runtime"))
-        return 0;
+        return drain();
     if (changed) {
         std::memcpy(r->calib_key, key, sizeof(key));
         r->calib_valid = true;
