@@ -96,19 +96,21 @@ __global__ __launch_bounds__(256) void clear_kernel(const bf_coord4 *__restrict_
     }
 }
 
-// Submanifold 3x3x3 (pad 1): tap (kz, ky, kx) of site s reads s + (k - 1).
+// Neighbour tables, one thread per (row, tap) entry so the table stores are
+// contiguous.  Submanifold 3x3x3 (pad 1): tap (kz, ky, kx) of site s reads
+// s + (k - 1).
 __global__ __launch_bounds__(256) void subm_neighbors_kernel(const bf_coord4 *__restrict__ coords,
                                                              const unsigned *__restrict__ count,
                                                              Grid g, const int *__restrict__ grid,
                                                              int *__restrict__ nbr) {
-    const unsigned n = *count;
-    for (unsigned j = blockIdx.x * 256 + threadIdx.x; j < n; j += gridDim.x * 256) {
+    const size_t total = (size_t)*count * kTaps;
+    for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < total;
+         e += (size_t)gridDim.x * 256) {
+        const unsigned j = (unsigned)(e / kTaps);
+        const int t = (int)(e - (size_t)j * kTaps);
         const bf_coord4 c = coords[j];
-        for (int t = 0; t < kTaps; ++t) {
-            const int z = c.z + t / 9 - 1, y = c.y + (t / 3) % 3 - 1, x = c.x + t % 3 - 1;
-            nbr[(size_t)j * kTaps + t] =
-                inside(g, c.batch, z, y, x) ? grid[cell_of(g, c.batch, z, y, x)] : kEmpty;
-        }
+        const int z = c.z + t / 9 - 1, y = c.y + (t / 3) % 3 - 1, x = c.x + t % 3 - 1;
+        nbr[e] = inside(g, c.batch, z, y, x) ? grid[cell_of(g, c.batch, z, y, x)] : kEmpty;
     }
 }
 
@@ -118,17 +120,17 @@ __global__ __launch_bounds__(256) void down_neighbors_kernel(const bf_coord4 *__
                                                              Grid gin, Geom q,
                                                              const int *__restrict__ grid,
                                                              int *__restrict__ nbr) {
-    const unsigned n = *count;
     const int taps = q.kd * q.kh * q.kw;
-    for (unsigned j = blockIdx.x * 256 + threadIdx.x; j < n; j += gridDim.x * 256) {
+    const size_t total = (size_t)*count * kTaps;
+    for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < total;
+         e += (size_t)gridDim.x * 256) {
+        const unsigned j = (unsigned)(e / kTaps);
+        const int t = (int)(e - (size_t)j * kTaps);
+        if (t >= taps) continue;
         const bf_coord4 c = coords[j];
-        for (int t = 0; t < taps; ++t) {
-            const int kz = t / (q.kh * q.kw), ky = (t / q.kw) % q.kh, kx = t % q.kw;
-            const int z = c.z * q.sd - q.pd + kz, y = c.y * q.sh - q.ph + ky,
-                      x = c.x * q.sw - q.pw + kx;
-            nbr[(size_t)j * kTaps + t] =
-                inside(gin, c.batch, z, y, x) ? grid[cell_of(gin, c.batch, z, y, x)] : kEmpty;
-        }
+        const int kz = t / (q.kh * q.kw), ky = (t / q.kw) % q.kh, kx = t % q.kw;
+        const int z = c.z * q.sd - q.pd + kz, y = c.y * q.sh - q.ph + ky, x = c.x * q.sw - q.pw + kx;
+        nbr[e] = inside(gin, c.batch, z, y, x) ? grid[cell_of(gin, c.batch, z, y, x)] : kEmpty;
     }
 }
 
@@ -909,6 +911,10 @@ int build(bf_cuda_lidar_backbone *n, const bf_model *m, char *error, size_t cap)
     return 1;
 }
 
+unsigned nbr_blocks(const bf_cuda_lidar_backbone *n) {
+    return (unsigned)std::max<size_t>(1, std::min<size_t>(16384, (n->capacity * kTaps + 255) / 256));
+}
+
 unsigned row_blocks(size_t capacity, int rows_per_block) {
     return (unsigned)std::max<size_t>(1, std::min<size_t>(2048, (capacity + rows_per_block - 1) / rows_per_block));
 }
@@ -960,8 +966,8 @@ void strided_sites(bf_cuda_lidar_backbone *n, const Conv &c, int l, const bf_coo
     compact_write_kernel<<<chunks, 256, 0, s>>>(n->marks, words, n->chunk_counts, chunks,
                                                 (unsigned)n->capacity, n->lv[l + 1], n->grid[l + 1],
                                                 n->coords[l + 1], n->counts + l + 1);
-    down_neighbors_kernel<<<rb, 256, 0, s>>>(n->coords[l + 1], n->counts + l + 1, n->lv[l], c.q,
-                                             n->grid[l], n->nbr);
+    down_neighbors_kernel<<<nbr_blocks(n), 256, 0, s>>>(n->coords[l + 1], n->counts + l + 1,
+                                                        n->lv[l], c.q, n->grid[l], n->nbr);
 }
 
 void forward_impl(bf_cuda_lidar_backbone *n, const bf_coord4 *coords, const float *feats,
@@ -969,7 +975,8 @@ void forward_impl(bf_cuda_lidar_backbone *n, const bf_coord4 *coords, const floa
     const unsigned rb = row_blocks(n->capacity, 256);
     count_init_kernel<<<1, 1, 0, s>>>(count_dev, count_host, (unsigned)n->capacity, n->counts);
     index_kernel<<<rb, 256, 0, s>>>(coords, n->counts, n->lv[0], n->grid[0]);
-    subm_neighbors_kernel<<<rb, 256, 0, s>>>(coords, n->counts, n->lv[0], n->grid[0], n->nbr);
+    subm_neighbors_kernel<<<nbr_blocks(n), 256, 0, s>>>(coords, n->counts, n->lv[0], n->grid[0],
+                                                        n->nbr);
     conv_input_kernel<<<rb, 256, 0, s>>>(n->nbr, n->counts, feats, n->input.w32, n->input.bias,
                                          n->feat[0].hi, n->feat[0].lo);
     const Feat none{nullptr, nullptr};
@@ -983,8 +990,8 @@ void forward_impl(bf_cuda_lidar_backbone *n, const bf_coord4 *coords, const floa
             launch_conv(n, n->down[st - 1], cnt, n->feat[x], none, 1, n->feat[y], nullptr, s);
             x = y;
             level_coords = n->coords[st];
-            subm_neighbors_kernel<<<rb, 256, 0, s>>>(level_coords, cnt, n->lv[st], n->grid[st],
-                                                     n->nbr);
+            subm_neighbors_kernel<<<nbr_blocks(n), 256, 0, s>>>(level_coords, cnt, n->lv[st],
+                                                                n->grid[st], n->nbr);
         }
         for (int blk = 0; blk < 2; ++blk) {
             const int y = (x + 1) % 3, z = (x + 2) % 3;
