@@ -148,3 +148,26 @@ def test_runtime_rejects_invalid_frames(model_path, frames):
             rt.infer(dict(frame, points=np.zeros((0, 5), np.float32)))
         again = rt.infer(frame)
         assert bytes(again) == bytes(good)
+
+
+def test_runtime_degenerate_point_clouds(model_path, frames):
+    """No point in range (zero voxels: the LiDAR BEV is all zero) and a single
+    point.  The GPU runtime, like the reference's cuda_runtime.cu, does not
+    read the voxel count back, so both frames run (the reference CPU runtime
+    rejects a frame without voxels) and repeat bit for bit."""
+    frame = frames[1]
+    outside = np.tile(np.array([[80.0, 80.0, 0.0, 0.5, 0.0]], np.float32), (500, 1))
+    single = np.array([[10.0, 5.0, -1.0, 0.5, 0.0]], np.float32)
+    print("[case] runtime degenerate clouds", flush=True)
+    with bfhip.Runtime(model_path) as rt:
+        for pts in (outside, single):
+            f = dict(frame, points=pts)
+            a = rt.infer(f)
+            stats = rt.debug_bev_stats()
+            b = rt.infer(f)
+            assert bytes(a) == bytes(b)
+            assert stats[0] > 0  # image BEV
+            if pts is outside:
+                assert stats[2] == 0.0 and stats[3] == 0.0  # no LiDAR site
+            else:
+                assert stats[2] > 0.0
