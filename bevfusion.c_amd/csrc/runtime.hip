@@ -84,7 +84,7 @@ __global__ __launch_bounds__(256) void stats_partial_kernel(const float *__restr
     ss[threadIdx.x] = s;
     mm[threadIdx.x] = m;
     __syncthreads();
-    for (int o = 128; o; o >>= 1) {
+    for (unsigned o = 128; o; o >>= 1) {
         if (threadIdx.x < o) {
             ss[threadIdx.x] += ss[threadIdx.x + o];
             mm[threadIdx.x] = fmaxf(mm[threadIdx.x], mm[threadIdx.x + o]);
@@ -128,7 +128,7 @@ __global__ __launch_bounds__(256) void hash_partial_kernel(const float *__restri
         v ^= mix64(((unsigned long long)i << 32) ^ __float_as_uint(x[i]));
     h[threadIdx.x] = v;
     __syncthreads();
-    for (int o = 128; o; o >>= 1) {
+    for (unsigned o = 128; o; o >>= 1) {
         if (threadIdx.x < o) h[threadIdx.x] ^= h[threadIdx.x + o];
         __syncthreads();
     }

@@ -66,7 +66,7 @@ constexpr int kDigitBins = 2048, kLevels = 6;
 constexpr int kMaxSegments = 4096, kLdsKeys = 8192;
 constexpr int kNmsTile = 32, kNmsHalo = kNmsTile + 2;
 constexpr int kKeyTile = 64, kLdsRow = kC + 8;      // fp16 LDS row: 272 B, conflict-free
-constexpr int kStepKeys = 64, kWaves = 4;
+constexpr int kStepKeys = 64;
 constexpr int kMaxSplits = 128;
 constexpr int kHeadOutputs = 20;                    // 2 + 1 + 3 + 2 + 2 + 10
 constexpr float kBnEps = 1e-5f;
