@@ -15,10 +15,15 @@
 //   top-P selection   exact radix select of the P-th largest key over
 //                     11/10-bit digits, with no atomics between workgroups:
 //                     suppress stores a per-tile histogram of the keys' top
-//                     digit, hist_reduce_kernel sums them, compact_kernel
-//                     picks the top digit and gathers the keys at or above it
-//                     into per-workgroup segments (a few thousand keys at
-//                     production scale), and finish_kernel (one workgroup)
+//                     digit and hist_reduce_kernel sums them.  When more than
+//                     8192 keys share or pass the P-th key's top digit (a
+//                     flat heatmap: random weights put ~10^5 candidates in
+//                     one bin), refine_kernel histograms the second digit
+//                     within that bin and a second hist_reduce sums those;
+//                     otherwise both return at once.  compact_kernel picks
+//                     the threshold's top digit (two digits when refined) and
+//                     gathers the keys at or above it into per-workgroup
+//                     segments, and finish_kernel (one workgroup)
 //                     pulls the segments into LDS, refines the remaining
 //                     digits, keeps the P winners and sorts them (256-slot
 //                     bitonic).  Every buffer is rewritten each forward
@@ -224,9 +229,12 @@ __global__ __launch_bounds__(256) void suppress_kernel(const float *__restrict__
 }
 
 // hist[d] = sum over tiles of part_hist[tile][d]: workgroup b owns bins
-// 8b .. 8b+7, its 32 thread slices stride over the tiles.
+// 8b .. 8b+7, its 32 thread slices stride over the tiles.  With `only_if`
+// set, returns at once unless *only_if is nonzero.
 __global__ __launch_bounds__(256) void hist_reduce_kernel(const unsigned *__restrict__ part_hist,
-                                                          int tiles, unsigned *__restrict__ hist) {
+                                                          int tiles, unsigned *__restrict__ hist,
+                                                          const unsigned *__restrict__ only_if) {
+    if (only_if && !*only_if) return;  // whole workgroup: before the barrier
     __shared__ unsigned red[256];
     const int t = threadIdx.x, d = blockIdx.x * 8 + (t & 7);
     unsigned sum = 0;
@@ -241,16 +249,74 @@ __global__ __launch_bounds__(256) void hist_reduce_kernel(const unsigned *__rest
     }
 }
 
-// Picks the top digit of the P-th largest key and gathers every key whose
-// top digit is >= it: workgroup g appends (LDS counter) into
-// list[g * chunk ...] and stores its count in counts[g].
+// Second radix level over the whole candidate set, for when the P-th key's
+// top digit leaves more keys than the finish holds in LDS: workgroup g
+// histograms the second digit of the keys in chunk g whose top digit is that
+// digit, into part_hist1[g].  Workgroup 0 stores whether this level runs in
+// *refined (every forward: nothing to reset).
+__global__ __launch_bounds__(256) void refine_kernel(const uint64_t *__restrict__ keys, unsigned n,
+                                                     unsigned chunk, const unsigned *__restrict__ hist,
+                                                     int P, unsigned *__restrict__ part_hist1,
+                                                     unsigned *__restrict__ refined) {
+    __shared__ unsigned lh[kDigitBins], wsum[4], res[3];
+    pick_digit<256>(hist, (unsigned)P, wsum, res);
+    const int t = threadIdx.x;
+    const bool run = res[1] + res[2] > (unsigned)kLdsKeys;  // keys the finish would gather
+    if (blockIdx.x == 0 && t == 0) *refined = run ? 1u : 0u;
+    if (!run) return;  // uniform over the workgroup
+    const uint64_t top = res[0];
+    const int shift = digit_shift(1);
+    for (int d = t; d < kDigitBins; d += 256) lh[d] = 0u;
+    __syncthreads();
+    const unsigned begin = blockIdx.x * chunk, end = min(begin + chunk, n);
+    for (unsigned i = begin + t; i < end; i += 256u) {
+        const uint64_t key = keys[i];
+        if (key >> digit_shift(0) == top)
+            atomicAdd(&lh[(unsigned)(key >> shift) & (kDigitBins - 1u)], 1u);
+    }
+    __syncthreads();
+    unsigned *dst = part_hist1 + (size_t)blockIdx.x * kDigitBins;
+    for (int d = t; d < kDigitBins; d += 256) dst[d] = lh[d];
+}
+
+// Threshold of the gathered keys: the P-th largest key's top digit, and when
+// refined its second digit too (hist1 then counts the second digits within
+// the top digit's bin).  Returns the threshold key and leaves in *k the rank
+// of the P-th key among the keys sharing that prefix, in *exact whether
+// those are exactly the keys left.  Every thread must call it.
+template <int T>
+__device__ unsigned long long threshold_prefix(const unsigned *hist, const unsigned *hist1,
+                                               bool refined, int P, unsigned *wsum,
+                                               unsigned *res, unsigned *k, bool *exact) {
+    pick_digit<T>(hist, (unsigned)P, wsum, res);
+    unsigned long long prefix = (unsigned long long)res[0] << digit_shift(0);
+    unsigned left = (unsigned)P - res[1];
+    bool done = res[2] == left;
+    if (refined) {
+        pick_digit<T>(hist1, left, wsum, res);  // res is read above before its barrier
+        prefix |= (unsigned long long)res[0] << digit_shift(1);
+        left -= res[1];
+        done = res[2] == left;
+    }
+    *k = left;
+    *exact = done;
+    return prefix;
+}
+
+// Gathers every key at or above the threshold prefix (threshold_prefix):
+// workgroup g appends (LDS counter) into list[g * chunk ...] and stores its
+// count in counts[g].
 __global__ __launch_bounds__(256) void compact_kernel(const uint64_t *__restrict__ keys, unsigned n,
                                                       unsigned chunk, const unsigned *__restrict__ hist,
-                                                      int P, uint64_t *__restrict__ list,
+                                                      const unsigned *__restrict__ hist1,
+                                                      const unsigned *__restrict__ refined, int P,
+                                                      uint64_t *__restrict__ list,
                                                       unsigned *__restrict__ counts) {
     __shared__ unsigned wsum[4], res[3], taken;
-    pick_digit<256>(hist, (unsigned)P, wsum, res);
-    const unsigned long long threshold = (unsigned long long)res[0] << digit_shift(0);
+    unsigned k;
+    bool exact;
+    const unsigned long long threshold =
+        threshold_prefix<256>(hist, hist1, *refined != 0u, P, wsum, res, &k, &exact);
     const int t = threadIdx.x, lane = t & 63;
     if (t == 0) taken = 0u;
     __syncthreads();
@@ -276,16 +342,19 @@ __global__ __launch_bounds__(256) void compact_kernel(const uint64_t *__restrict
 __global__ __launch_bounds__(1024) void finish_kernel(const uint64_t *__restrict__ list,
                                                       const unsigned *__restrict__ counts,
                                                       int segments, unsigned chunk,
-                                                      const unsigned *__restrict__ hist, int P,
+                                                      const unsigned *__restrict__ hist,
+                                                      const unsigned *__restrict__ hist1,
+                                                      const unsigned *__restrict__ refined, int P,
                                                       uint64_t *__restrict__ top) {
     __shared__ unsigned lh[kDigitBins], wsum[16], res[3], off[kMaxSegments + 1], count;
     __shared__ uint64_t lk[kLdsKeys];
     __shared__ uint64_t s[kTopSlots];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    pick_digit<1024>(hist, (unsigned)P, wsum, res);
-    unsigned long long prefix = (unsigned long long)res[0] << digit_shift(0);
-    unsigned k = (unsigned)P - res[1];
-    bool resolved = res[2] == k;
+    const bool two = *refined != 0u;
+    unsigned k;
+    bool resolved;
+    unsigned long long prefix =
+        threshold_prefix<1024>(hist, hist1, two, P, wsum, res, &k, &resolved);
     // Exclusive scan of the segment counts, four segments per thread.
     unsigned c[4], sum = 0;
 #pragma unroll
@@ -339,17 +408,36 @@ __global__ __launch_bounds__(1024) void finish_kernel(const uint64_t *__restrict
         }
         __syncthreads();
     }
-    auto key_at = [&](unsigned j) { return in_lds ? lk[j] : list[locate(j)]; };
-    for (int level = 1; level < kLevels && !resolved; ++level) {
+    // Visits every gathered key once, in no set order: from LDS, or read in
+    // place with eight loads in flight per thread (a flat heatmap leaves
+    // ~10^5 keys past the first digit, and one load at a time per thread
+    // took ~0.2 ms over the passes below).
+    auto scan = [&](auto &&visit) {
+        if (in_lds) {
+            for (unsigned j = t; j < m; j += 1024) visit(lk[j]);
+            return;
+        }
+        for (unsigned j0 = t; j0 < m; j0 += 8 * 1024) {
+            uint64_t v8[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const unsigned j = j0 + 1024u * u;
+                v8[u] = j < m ? list[locate(j)] : 0ull;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (j0 + 1024u * u < m) visit(v8[u]);
+        }
+    };
+    for (int level = two ? 2 : 1; level < kLevels && !resolved; ++level) {
         const int shift = digit_shift(level), hi = shift + digit_width(level);
         const unsigned mask = (1u << digit_width(level)) - 1u;
         const unsigned long long group = prefix >> hi;
         for (int d = t; d < kDigitBins; d += 1024) lh[d] = 0u;
         __syncthreads();
-        for (unsigned j = t; j < m; j += 1024) {
-            const uint64_t key = key_at(j);
+        scan([&](uint64_t key) {
             if ((key >> hi) == group) atomicAdd(&lh[(unsigned)(key >> shift) & mask], 1u);
-        }
+        });
         __syncthreads();
         pick_digit<1024>(lh, k, wsum, res);
         prefix |= (unsigned long long)res[0] << shift;
@@ -358,13 +446,12 @@ __global__ __launch_bounds__(1024) void finish_kernel(const uint64_t *__restrict
     }
     if (t == 0) count = 0u;
     __syncthreads();
-    for (unsigned j = t; j < m; j += 1024) {
-        const uint64_t key = key_at(j);
+    scan([&](uint64_t key) {
         if (key >= prefix) {
             const unsigned slot = atomicAdd(&count, 1u);
             if (slot < kTopSlots) s[slot] = key;  // exactly P keys by construction
         }
-    }
+    });
     __syncthreads();
     // Descending order by rank (keys are unique): four threads per key count
     // the larger keys among a quarter of the P each.
@@ -954,7 +1041,7 @@ struct bf_cuda_transfusion {
     // Views into the arena.
     float *suppressed, *query, *query_pos, *qkv, *part_m, *part_l, *part_o;
     uint64_t *sort_keys, *selected, *top;
-    unsigned *part_hist, *hist, *counts;
+    unsigned *part_hist, *hist, *counts, *part_hist1, *hist1, *refined;
     _Float16 *cross_q, *kh, *vt;
     bf_detections *detections;
 };
@@ -1183,6 +1270,8 @@ int build_work(bf_cuda_transfusion *d, char *error, size_t cap) {
     const size_t o_part = take(tiles * kDigitBins * 4), o_hist = take(kDigitBins * 4);
     const size_t o_counts = take((size_t)d->segments * 4), o_list = take(cand * 8),
                  o_top = take(kTopSlots * 8);
+    const size_t o_part1 = take((size_t)d->segments * kDigitBins * 4),
+                 o_hist1 = take(kDigitBins * 4), o_refined = take(4);
     const size_t o_query = take(P * kC * 4), o_pos = take(P * kC * 4), o_qkv = take(3 * P * kC * 4);
     const size_t o_cq = take((size_t)kPPad * kC * 2);
     const size_t o_kh = take((size_t)d->keys64 * kC * 2), o_vt = take((size_t)d->keys64 * kC * 2);
@@ -1199,6 +1288,9 @@ int build_work(bf_cuda_transfusion *d, char *error, size_t cap) {
     d->part_hist = (unsigned *)(a + o_part);
     d->hist = (unsigned *)(a + o_hist);
     d->counts = (unsigned *)(a + o_counts);
+    d->part_hist1 = (unsigned *)(a + o_part1);
+    d->hist1 = (unsigned *)(a + o_hist1);
+    d->refined = (unsigned *)(a + o_refined);
     d->selected = (uint64_t *)(a + o_list);
     d->top = (uint64_t *)(a + o_top);
     d->query = (float *)(a + o_query);
@@ -1270,11 +1362,15 @@ extern "C" int bf_cuda_transfusion_forward(bf_cuda_transfusion *d, const float *
     suppress_kernel<<<tiles, 256, 0, s>>>(heatmap, d->suppressed, d->sort_keys, (int)d->height, W,
                                           keys, d->nms_tiles_x, d->nms_tiles_y, d->part_hist);
     key_kernel<<<d->keys64 / kKeyTile, 256, 0, s>>>(d->prm, shared, keys, W, d->keys64, d->kh, d->vt);
-    hist_reduce_kernel<<<kDigitBins / 8, 256, 0, s>>>(d->part_hist, tiles, d->hist);
-    compact_kernel<<<d->segments, 256, 0, s>>>(d->sort_keys, cand, d->chunk, d->hist, P,
-                                               d->selected, d->counts);
-    finish_kernel<<<1, 1024, 0, s>>>(d->selected, d->counts, d->segments, d->chunk, d->hist, P,
-                                     d->top);
+    hist_reduce_kernel<<<kDigitBins / 8, 256, 0, s>>>(d->part_hist, tiles, d->hist, nullptr);
+    refine_kernel<<<d->segments, 256, 0, s>>>(d->sort_keys, cand, d->chunk, d->hist, P,
+                                              d->part_hist1, d->refined);
+    hist_reduce_kernel<<<kDigitBins / 8, 256, 0, s>>>(d->part_hist1, d->segments, d->hist1,
+                                                      d->refined);
+    compact_kernel<<<d->segments, 256, 0, s>>>(d->sort_keys, cand, d->chunk, d->hist, d->hist1,
+                                               d->refined, P, d->selected, d->counts);
+    finish_kernel<<<1, 1024, 0, s>>>(d->selected, d->counts, d->segments, d->chunk, d->hist,
+                                     d->hist1, d->refined, P, d->top);
     query_kernel<<<P, 256, 0, s>>>(d->prm, d->top, d->suppressed, shared, keys, W, P,
                                    d->query, d->query_pos, d->qkv, out->query_labels_bp,
                                    out->query_indices_bp, out->query_heatmap_scores_b10p);

@@ -91,6 +91,24 @@ def test_transfusion_selection_ties(tf_path, kind, device):
     dec.close()
 
 
+@pytest.mark.parametrize("kind", ["constant", "flat"])
+def test_transfusion_selection_many_candidates(tf_path, kind, device):
+    """Production map with far more candidates past the first radix digit
+    than the one-workgroup finish holds in LDS (8192), so it reads them in
+    place: every cell at one score (324 000 exact ties), and the flat
+    heatmap of random weights (logits -1 +- 0.05, scores 0.26-0.28, as in
+    the runtime's synthetic frames)."""
+    sh, hm = bfw.synthetic_transfusion_inputs(15, 180, 180)
+    if kind == "constant":
+        hm = np.full_like(hm, 0.75)
+    else:
+        hm = (-1.0 + 0.05 * np.random.default_rng(15).standard_normal(hm.shape)).astype(np.float32)
+    dec, _, got = _gpu(tf_path, sh, hm, 200, device)
+    _, want = _oracle(tf_path, sh, hm, 200)
+    _check(got, want, kind)
+    dec.close()
+
+
 def test_transfusion_decode_matches_oracle(tf_path, device):
     """GPU decode + filter of one forward's raw outputs against the oracle's
     decode_raw + filter of the same outputs: same kept set and order, class
