@@ -38,6 +38,7 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <vector>
 
 using namespace bfhip;
 
@@ -292,10 +293,25 @@ extern "C" int bf_cuda_runtime_create(const char *model_path, size_t point_capac
     const bf_lss_desc lss = {1, kCams, kBins, kFeatH, kFeatW, kCtx, {-54.0f, -54.0f, -10.0f},
                              {0.3f, 0.3f, 20.0f}, {kFull, kFull, 1}};
     const bf_tensor *fr = bf_model_find(model, "vtransform.frustum");
-    int ok = hip_ok(hipStreamCreateWithFlags(&r->stream, hipStreamNonBlocking), error, cap,
+    // The LiDAR stream gets a hardware queue of its own: HIP spreads ordinary
+    // streams over a few shared queues (GPU_MAX_HW_QUEUES), and when both
+    // runtime streams land on one queue the branches run back to back (4.3
+    // instead of 3.5 ms per frame on MI355X once a caller holds three other
+    // streams).  A stream with a CU mask is never shared; the mask names
+    // every CU.  Such a stream is a blocking one: work on the null stream
+    // waits for it.
+    int device = 0, cus = 0;
+    int ok = hip_ok(hipGetDevice(&device), error, cap, "query HIP device") &&
+             hip_ok(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device),
+                    error, cap, "query HIP CU count");
+    std::vector<uint32_t> every_cu(ok ? (size_t)(cus + 31) / 32 : 0, 0u);
+    for (int c = 0; c < cus; ++c) every_cu[c / 32] |= 1u << (c % 32);
+    ok = ok && cus > 0 &&
+             hip_ok(hipStreamCreateWithFlags(&r->stream, hipStreamNonBlocking), error, cap,
                     "create HIP runtime stream") &&
-             hip_ok(hipStreamCreateWithFlags(&r->side, hipStreamNonBlocking), error, cap,
-                    "create HIP runtime LiDAR stream") &&
+             hip_ok(hipExtStreamCreateWithCUMask(&r->side, (uint32_t)every_cu.size(),
+                                                 every_cu.data()),
+                    error, cap, "create HIP runtime LiDAR stream") &&
              hip_ok(hipEventCreateWithFlags(&r->fork, hipEventDisableTiming), error, cap,
                     "create HIP runtime events") &&
              hip_ok(hipEventCreateWithFlags(&r->join, hipEventDisableTiming), error, cap,
