@@ -86,10 +86,22 @@ __global__ __launch_bounds__(256) void index_kernel(const bf_coord4 *__restrict_
     }
 }
 
-__global__ __launch_bounds__(256) void clear_kernel(const bf_coord4 *__restrict__ coords,
-                                                    const unsigned *__restrict__ count, Grid g,
-                                                    int *__restrict__ grid) {
-    const unsigned n = *count;
+// The five levels' site lists and index grids, for one clearing launch.
+struct LevelGrids {
+    const bf_coord4 *coords[5];
+    const unsigned *count[5];
+    int *grid[5];
+    Grid g[5];
+};
+
+// Returns every level's index grid to empty at its own sites (blockIdx.y is
+// the level), so the grids are clean for the next forward.
+__global__ __launch_bounds__(256) void clear_kernel(LevelGrids lg) {
+    const int l = (int)blockIdx.y;
+    const bf_coord4 *coords = lg.coords[l];
+    int *grid = lg.grid[l];
+    const Grid g = lg.g[l];
+    const unsigned n = *lg.count[l];
     for (unsigned j = blockIdx.x * 256 + threadIdx.x; j < n; j += gridDim.x * 256) {
         const bf_coord4 c = coords[j];
         if (inside(g, c.batch, c.z, c.y, c.x)) grid[cell_of(g, c.batch, c.z, c.y, c.x)] = kEmpty;
@@ -1037,9 +1049,14 @@ void forward_impl(bf_cuda_lidar_backbone *n, const bf_coord4 *coords, const floa
     const size_t dense_tiles = (size_t)n->lv[4].b * (((size_t)n->cells[4] / n->lv[4].b + 63) / 64);
     dense_kernel<<<(unsigned)std::min<size_t>(16384, dense_tiles), 256, 0, s>>>(
         n->grid[4], n->lv[4], n->out32, dense);
-    clear_kernel<<<rb, 256, 0, s>>>(coords, n->counts, n->lv[0], n->grid[0]);
-    for (int l = 1; l < 5; ++l)
-        clear_kernel<<<rb, 256, 0, s>>>(n->coords[l], n->counts + l, n->lv[l], n->grid[l]);
+    LevelGrids lg;
+    for (int l = 0; l < 5; ++l) {
+        lg.coords[l] = l ? n->coords[l] : coords;
+        lg.count[l] = n->counts + l;
+        lg.grid[l] = n->grid[l];
+        lg.g[l] = n->lv[l];
+    }
+    clear_kernel<<<dim3(rb, 5), 256, 0, s>>>(lg);
 }
 
 }  // namespace
