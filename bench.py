@@ -54,15 +54,19 @@ def parse():
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--no-graph", action="store_true", help="launch eagerly instead of a HIP graph")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    p.add_argument("--cpu-cameras", type=int, default=2,
-                   help="cameras in the bounded CPU-baseline sample")
+    p.add_argument("--cpu-cameras", type=int, default=6,
+                   help="cameras in the CPU-baseline sample (6 = one full frame)")
     p.add_argument("--no-roofline", action="store_true", help="skip per-kernel timing")
     p.add_argument("--kernel-reps", type=int, default=20,
                    help="HIP-event timed launches per kernel in the roofline leg")
     p.add_argument("--kernels", default="",
                    help="comma-separated op names to time in the roofline leg (default: all)")
     p.add_argument("--no-traffic", action="store_true",
-                   help="skip the rocprofv3 FETCH_SIZE / WRITE_SIZE passes on the dominant kernel")
+                   help="skip the rocprofv3 counter passes (MFMA utilisation and flops, "
+                        "FETCH_SIZE / WRITE_SIZE) over every op")
+    p.add_argument("--no-downsample", action="store_true", help="skip the downsample leg")
+    p.add_argument("--no-config1", action="store_true", help="skip the config-1 linear leg")
+    p.add_argument("--no-calibrate", action="store_true", help="skip the machine calibration leg")
     p.add_argument("--pmc-child", default="",
                    help=argparse.SUPPRESS)  # internal: the program rocprofv3 profiles
     p.add_argument("--no-lss", action="store_true", help="skip the LSS pooling leg")
@@ -73,8 +77,12 @@ def parse():
     return p.parse_args()
 
 
-def frame_flops():
-    """Algorithmic FLOPs of one frame, recomputed from the graph shapes."""
+def frame_flops(window_rows=True):
+    """FLOPs of one frame, recomputed from the graph shapes.  With
+    window_rows the QKV and proj GEMMs are charged at windows x 49 rows, as
+    the reference computes them (padding tokens included: the
+    reference-equivalent work); without, at the real token rows this build's
+    kernels compute (the executed work)."""
     b = 6
     total = 0.0
     dims = [(64, 176), (32, 88), (16, 44), (8, 22)]
@@ -82,7 +90,8 @@ def frame_flops():
         h, w = dims[s]
         tok = b * h * w
         win_rows = b * ((h + 6) // 7) * ((w + 6) // 7) * 49
-        per_block = (2 * win_rows * c * 3 * c + 2 * win_rows * c * c          # qkv, proj
+        rows = win_rows if window_rows else tok
+        per_block = (2 * rows * c * 3 * c + 2 * rows * c * c                  # qkv, proj
                      + 2 * 2 * win_rows * 49 * c                              # QK^T, AV
                      + 2 * 2 * tok * c * 4 * c)                               # fc1, fc2
         total += d * per_block
@@ -101,15 +110,26 @@ def frame_flops():
 
 SWIN_STAGES = [(64, 176, 96, 3, 2), (32, 88, 192, 6, 2), (16, 44, 384, 12, 6),
                (8, 22, 768, 24, 2)]
-NECK_LAYERS = {  # layer index: (name, M pixels, Ci, Co, k, input pixels)
-    0: ("fpn.lateral1", 6 * 16 * 44, 1152, 256, 1, 6 * 16 * 44),
-    1: ("fpn.output1", 6 * 16 * 44, 256, 256, 3, 6 * 16 * 44),
-    2: ("fpn.lateral0", 6 * 32 * 88, 448, 256, 1, 6 * 32 * 88),
-    3: ("fpn.output0", 6 * 32 * 88, 256, 256, 3, 6 * 32 * 88),
-    5: ("depth.dtransform6", 6 * 32 * 88, 32, 64, 5, 6 * 64 * 176),
-    6: ("depth.depthnet0", 6 * 32 * 88, 320, 256, 3, 6 * 32 * 88),
-    7: ("depth.depthnet3", 6 * 32 * 88, 256, 256, 3, 6 * 32 * 88),
+# layer index: (name, output pixels M, Ci, Co, k, input bytes, output bytes
+# per element).  Inputs are channels-last bf16 maps except dtransform.3,
+# which reads the fp32 dense depth (its 8 input channels are computed from one
+# value per pixel); depthnet.6 and the last downsample conv store fp32 NCHW.
+DOWN_IN_HW = 360  # LSS BEV grid the downsample reads (reference production shape)
+NECK_LAYERS = {
+    0: ("fpn.lateral1", 6 * 16 * 44, 1152, 256, 1, 6 * 16 * 44 * 1152 * 2, 2),
+    1: ("fpn.output1", 6 * 16 * 44, 256, 256, 3, 6 * 16 * 44 * 256 * 2, 2),
+    2: ("fpn.lateral0", 6 * 32 * 88, 448, 256, 1, 6 * 32 * 88 * 448 * 2, 2),
+    3: ("fpn.output0", 6 * 32 * 88, 256, 256, 3, 6 * 32 * 88 * 256 * 2, 2),
+    4: ("depth.dtransform3", 6 * 64 * 176, 8, 32, 5, 6 * 256 * 704 * 4, 2),
+    5: ("depth.dtransform6", 6 * 32 * 88, 32, 64, 5, 6 * 64 * 176 * 32 * 2, 2),
+    6: ("depth.depthnet0", 6 * 32 * 88, 320, 256, 3, 6 * 32 * 88 * 320 * 2, 2),
+    7: ("depth.depthnet3", 6 * 32 * 88, 256, 256, 3, 6 * 32 * 88 * 256 * 2, 2),
+    8: ("depth.depthnet6", 6 * 32 * 88, 256, 198, 1, 6 * 32 * 88 * 256 * 2, 4),
+    9: ("downsample.0", 360 * 360, 80, 80, 3, 360 * 360 * 80 * 2, 2),
+    10: ("downsample.1", 180 * 180, 80, 80, 3, 360 * 360 * 80 * 2, 2),
+    11: ("downsample.2", 180 * 180, 80, 80, 3, 180 * 180 * 80 * 2, 4),
 }
+IO_LAYERS = (4, 8, 11)  # timed on caller buffers (bfhip_camera_profile_layer_io)
 
 
 def swin_op_cost(stage, op, b=6):
@@ -143,8 +163,19 @@ def swin_op_cost(stage, op, b=6):
 
 
 def neck_layer_cost(layer):
-    name, m, ci, co, k, m_in = NECK_LAYERS[layer]
-    return 2.0 * m * co * ci * k * k, m_in * ci * 2 + co * ci * k * k * 2 + m * co * 2
+    name, m, ci, co, k, in_bytes, out_el = NECK_LAYERS[layer]
+    return 2.0 * m * co * ci * k * k, in_bytes + co * ci * k * k * 2 + m * co * out_el
+
+
+def neck_io(dev):
+    """Caller buffers the IO layers read or write: dense depth, logits,
+    context and the downsample output."""
+    import torch
+    g = torch.Generator(device="cpu").manual_seed(0)
+    return {"depth": torch.rand((6, 1, 256, 704), generator=g).to(dev),
+            "logits": torch.empty((6, 118, 32, 88), device=dev),
+            "ctx": torch.empty((6, 80, 32, 88), device=dev),
+            "down": torch.empty((1, 80, DOWN_IN_HW // 2, DOWN_IN_HW // 2), device=dev)}
 
 
 def roofline_entry(name, avg_s, per_frame, flops, nbytes):
@@ -176,9 +207,10 @@ def fused_stages(swin, stream):
     return out
 
 
-def op_table(swin, neck, stream):
+def op_table(swin, neck, stream, io):
     """name -> (launch fn, launches per frame, (flops, bytes) per launch) for
-    every op the forward launches (profiling hooks of include/bfhip_profile.h)."""
+    every op the forward launches (profiling hooks of include/bfhip_profile.h);
+    `io` holds the caller buffers of neck_io()."""
     import bfhip
     table = {}
     fused = fused_stages(swin, stream)
@@ -198,18 +230,28 @@ def op_table(swin, neck, stream):
             table[f"swin.s{st}.merge"] = (lambda st=st: swin.profile_op(st, 0, "merge", stream),
                                           1, swin_op_cost(st, "merge"))
     for layer, (name, *_rest) in NECK_LAYERS.items():
-        table[f"neck.{name}"] = (lambda layer=layer: neck.profile_layer(layer, stream), 1,
-                                 neck_layer_cost(layer))
+        if layer == 4:
+            fn = lambda: neck.profile_layer_io(4, inp=io["depth"], stream=stream)
+        elif layer == 8:
+            fn = lambda: neck.profile_layer_io(8, out0=io["logits"], out1=io["ctx"], stream=stream)
+        elif layer == 11:
+            fn = lambda: neck.profile_layer_io(11, out0=io["down"], stream=stream)
+        else:
+            fn = lambda layer=layer: neck.profile_layer(layer, stream)
+        table[f"neck.{name}"] = (fn, 1, neck_layer_cost(layer))
     return table
 
 
-def time_kernels(swin, neck, stream, reps=20, only=()):
+def time_kernels(swin, neck, stream, io, reps=20, only=()):
     """Time single ops of the path with HIP events on the stream they are
-    launched on; returns roofline entries sorted by time per frame."""
+    launched on; returns roofline entries sorted by time per frame.  The
+    downsample layers run once per LSS output, not per camera frame: they are
+    timed here (and reported under "downsample") but kept out of the frame's
+    ranking."""
     import torch
     out = []
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    for name, (fn, per_frame, (flops, nbytes)) in op_table(swin, neck, stream).items():
+    for name, (fn, per_frame, (flops, nbytes)) in op_table(swin, neck, stream, io).items():
         if only and name not in only:
             continue
         for _ in range(3):
@@ -232,13 +274,36 @@ def time_kernels(swin, neck, stream, reps=20, only=()):
 PMC_OP_REPS, PMC_COPY_REPS, PMC_COPY_BYTES = 23, 29, 64 << 20
 
 
-def pmc_child(op):
-    """Body of the profiled child: a 64 MiB device-to-device copy
-    PMC_COPY_REPS times (the calibration kernel), then the op PMC_OP_REPS
-    times; every dispatch after the last copy belongs to the op."""
+ALL_OPS = "@all"        # --pmc-child: every op of the table, separated by marker launches
+ALL_OP_REPS = 5
+MARKER_KERNEL = "calib_empty_kernel"
+
+
+def _camera_contexts(dev):
+    """The bench's Swin and camera-neck contexts at 6 x 256 x 704 on a
+    synthetic checkpoint, after one forward (so every scratch buffer holds
+    realistic activations)."""
     import torch
     import bfhip
     from bfhip import bfw
+    tmp = pathlib.Path(tempfile.mkdtemp(prefix="pmc_"))
+    model_path = bfw.write_camera_branch(tmp / "camera_branch.bfw", seed=0, mode="baseline")
+    with bfhip.Model(model_path) as m:
+        swin = bfhip.Swin(m, 6, 256, 704)
+        neck = bfhip.CameraNeck(m, 6, 32, 88, DOWN_IN_HW, DOWN_IN_HW)
+    img = torch.from_numpy(bfw.synthetic_images(0, 6, 256, 704)).to(dev)
+    dep = torch.from_numpy(bfw.synthetic_depth(0, 6, 256, 704)).to(dev)
+    return swin, neck, img, dep
+
+
+def pmc_child(op):
+    """Body of the profiled child: a 64 MiB device-to-device copy
+    PMC_COPY_REPS times (the calibration kernel), then the op PMC_OP_REPS
+    times; every dispatch after the last copy belongs to the op.  With
+    op == ALL_OPS, every op of op_table() runs ALL_OP_REPS times instead,
+    each preceded by one empty marker kernel, and one marker closes the run."""
+    import torch
+    import bfhip
     dev = torch.device("cuda:0")
     if op == LSS_OP:
         plan, fwd = lss_setup(dev)
@@ -253,27 +318,123 @@ def pmc_child(op):
         torch.cuda.synchronize()
         plan.close()
         return
-    tmp = pathlib.Path(tempfile.mkdtemp(prefix="pmc_"))
-    model_path = bfw.write_camera_branch(tmp / "camera_branch.bfw", seed=0, mode="baseline")
-    with bfhip.Model(model_path) as m:
-        swin = bfhip.Swin(m, 6, 256, 704)
-        neck = bfhip.CameraNeck(m, 6, 32, 88, 360, 360)
-    img = torch.from_numpy(bfw.synthetic_images(0, 6, 256, 704)).to(dev)
-    dep = torch.from_numpy(bfw.synthetic_depth(0, 6, 256, 704)).to(dev)
+    swin, neck, img, dep = _camera_contexts(dev)
+    io = neck_io(dev)
     stream = torch.cuda.Stream()
     with torch.cuda.stream(stream):
         outs = swin.forward(img, stream=stream)
         neck.neck_forward(*outs, dep, stream=stream)
-        fn = op_table(swin, neck, stream)[op][0]
+        neck.downsample_forward(torch.rand((1, 80, DOWN_IN_HW, DOWN_IN_HW), device=dev),
+                                stream=stream)
+        table = op_table(swin, neck, stream, io)
         src = torch.zeros(PMC_COPY_BYTES // 4, device=dev)
         dst = torch.empty_like(src)
         stream.synchronize()
         for _ in range(PMC_COPY_REPS):
             dst.copy_(src)
         stream.synchronize()
-        for _ in range(PMC_OP_REPS):
-            fn()
+        if op == ALL_OPS:
+            for name, (fn, *_rest) in table.items():
+                bfhip.calibrate("empty", 1, stream=stream)
+                for _ in range(ALL_OP_REPS):
+                    fn()
+                stream.synchronize()
+            bfhip.calibrate("empty", 1, stream=stream)
+        else:
+            for _ in range(PMC_OP_REPS):
+                table[op][0]()
         stream.synchronize()
+
+
+def _pmc_pass(counters, child_op, timeout_s):
+    """One rocprofv3 counter pass over `bench.py --pmc-child child_op`:
+    returns (dispatch rows sorted by id as dicts {id, kernel, grid, values},
+    None) or (None, reason)."""
+    import csv
+    import shutil
+    import subprocess
+    prof = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    if not os.path.exists(prof):
+        return None, "rocprofv3 not found"
+    out = pathlib.Path(tempfile.mkdtemp(prefix="pmc_", dir="/tmp"))
+    cmd = ["timeout", "-s", "KILL", str(timeout_s), prof, "--pmc", *counters,
+           "--output-format", "csv", "-d", str(out), "-o", "p", "--",
+           os.path.realpath(sys.executable), str(ROOT / "bench.py"), "--pmc-child", child_op]
+    env = dict(os.environ, TMPDIR="/tmp")
+    proc = subprocess.run(cmd, cwd="/tmp", env=env, capture_output=True, text=True)
+    files = list(out.rglob("*counter_collection.csv"))
+    if not files:
+        tail = (proc.stderr or proc.stdout).strip().splitlines()[-3:]
+        return None, f"{' '.join(counters)}: no counters (exit {proc.returncode}): {' | '.join(tail)}"
+    rows = {}
+    for r in csv.DictReader(open(files[0])):
+        d = rows.setdefault(int(r["Dispatch_Id"]), {"id": int(r["Dispatch_Id"]),
+                                                     "kernel": r["Kernel_Name"],
+                                                     "grid": r["Grid_Size"], "values": {}})
+        d["values"][r["Counter_Name"]] = d["values"].get(r["Counter_Name"], 0.0) + \
+            float(r["Counter_Value"])
+    shutil.rmtree(out, ignore_errors=True)
+    return [rows[k] for k in sorted(rows)], None
+
+
+def _copy_scale(rows, counter):
+    """(index of the first dispatch after the calibration copies, bytes per
+    counter unit) from the PMC_COPY_REPS copies at the start of a pass."""
+    import statistics
+    groups = {}
+    for i, r in enumerate(rows):
+        groups.setdefault((r["kernel"], r["grid"]), []).append(i)
+    copy = [g for g in groups.values() if len(g) == PMC_COPY_REPS]
+    if len(copy) != 1:
+        return None, None
+    kib = statistics.median(rows[i]["values"][counter] for i in copy[0])
+    return max(copy[0]) + 1, PMC_COPY_BYTES / (kib * 1024)
+
+
+def measure_op_counters(names, timeout_s=240):
+    """Per-launch counters of every op in `names` (op_table order) from three
+    rocprofv3 passes over one child run each: MFMA (MfmaUtil, MfmaFlopsBF16,
+    MfmaFlopsF16) and HBM traffic (FETCH_SIZE, WRITE_SIZE; KiB scaled by a
+    64 MiB copy).  Returns ({name: {...}}, [errors])."""
+    passes = [("mfma", ["MfmaUtil", "MfmaFlopsBF16", "MfmaFlopsF16"]),
+              ("fetch", ["FETCH_SIZE"]), ("write", ["WRITE_SIZE"])]
+    result = {n: {} for n in names}
+    errors = []
+    for kind, counters in passes:
+        rows, why = _pmc_pass(counters, ALL_OPS, timeout_s)
+        if rows is None:
+            errors.append(why)
+            continue
+        start, scale = _copy_scale(rows, counters[0]) if kind != "mfma" else (0, 1.0)
+        if start is None:
+            errors.append(f"{kind}: calibration copy not identified")
+            continue
+        marks = [i for i in range(start, len(rows)) if MARKER_KERNEL in rows[i]["kernel"]]
+        if len(marks) != len(names) + 1:
+            errors.append(f"{kind}: {len(marks)} markers for {len(names)} ops")
+            continue
+        for k, name in enumerate(names):
+            seg = rows[marks[k] + 1:marks[k + 1]]
+            if not seg or len(seg) % ALL_OP_REPS:
+                errors.append(f"{kind}: {name} has {len(seg)} dispatches")
+                continue
+            tot = {c: sum(r["values"].get(c, 0.0) for r in seg) for c in counters}
+            e = result[name]
+            if kind == "mfma":
+                # An op of several kernels (merge: LayerNorm + GEMM) reports
+                # the utilisation of its MFMA kernel, the one with most flops.
+                per = len(seg) // ALL_OP_REPS
+                flops = lambda r: r["values"].get("MfmaFlopsBF16", 0.0) + \
+                    r["values"].get("MfmaFlopsF16", 0.0)
+                main = max(range(per), key=lambda j: sum(flops(r) for r in seg[j::per]))
+                util = [r["values"].get("MfmaUtil", 0.0) for r in seg[main::per]]
+                e["mfma_util_pct"] = round(sum(util) / len(util), 2)
+                e["mfma_flops"] = (tot["MfmaFlopsBF16"] + tot["MfmaFlopsF16"]) / ALL_OP_REPS
+                e["kernels_per_launch"] = per
+            else:
+                e[f"{kind}_bytes"] = round(tot[counters[0]] * 1024 * scale / ALL_OP_REPS)
+                e[f"{kind}_scale"] = round(scale, 4)
+    return result, errors
 
 
 def measure_traffic(op, timeout_s=120):
@@ -317,6 +478,173 @@ def measure_traffic(op, timeout_s=120):
             "fetch_kib_raw": round(per["FETCH_SIZE"][0], 1), "write_kib_raw": round(per["WRITE_SIZE"][0], 1),
             "fetch_scale": round(per["FETCH_SIZE"][1], 4), "write_scale": round(per["WRITE_SIZE"][1], 4),
             "calibration": f"{PMC_COPY_BYTES >> 20} MiB device copy"}, None
+
+
+# Post-LSS downsample (three 3x3 80->80 convs from 360x360 plus the x/y
+# transpose), reference RTX 4060 Ti warm time (runs/rtx4060ti-2026-07-18/
+# cuda_camera_slice.txt:13; benchmark.csv:16; entry src/cuda_camera.cu:409-422).
+DOWN_REFERENCE_MS = 2.397
+
+
+def downsample_leg(neck, dev, stream, reps, kernels):
+    """bf_cuda_camera_downsample_forward on the reference's production BEV
+    (1 x 80 x 360 x 360 fp32 in, 1 x 80 x 180 x 180 out), replayed from a HIP
+    graph and timed with HIP events; the per-layer entries come from the
+    roofline leg's `kernels` list."""
+    import torch
+    hw = DOWN_IN_HW
+    g = torch.Generator(device="cpu").manual_seed(7)
+    bev = torch.rand((1, 80, hw, hw), generator=g).to(dev)
+    out = torch.empty((1, 80, hw // 2, hw // 2), device=dev)
+    flops = sum(neck_layer_cost(l)[0] for l in (9, 10, 11))
+    nbytes = bev.numel() * 4 + out.numel() * 4 + 3 * 80 * 80 * 9 * 2
+    with torch.cuda.stream(stream):
+        neck.downsample_forward(bev, out, stream=stream)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            neck.downsample_forward(bev, out, stream=stream)
+        for _ in range(3):
+            graph.replay()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(reps):
+            graph.replay()
+        stop.record(stream)
+        stop.synchronize()
+    ms = start.elapsed_time(stop) / reps
+    roof = roofline_entry("downsample forward (pack + 3 convs + transposed store)", ms / 1e3, 1,
+                          flops, nbytes)
+    layers = [k for k in kernels if k["kernel"].startswith("neck.downsample")]
+    return {"workload": "post-LSS downsample, reference production shape: 1 x 80 x 360 x 360 fp32 "
+                        "-> 3x3 s1 -> 3x3 s2 -> 3x3 s1 (BN-folded, ReLU) -> x/y-transposed "
+                        "1 x 80 x 180 x 180",
+            "ms": round(ms, 4), "gflop": round(flops / 1e9, 2),
+            "tflops": round(flops / ms / 1e9, 1),
+            "reference_rtx4060ti_ms": DOWN_REFERENCE_MS,
+            "speedup_vs_reference": round(DOWN_REFERENCE_MS / ms, 1),
+            "roofline": {k: roof[k] for k in ("kernel", "bound", "achieved", "peak", "unit", "frac",
+                                               "traffic")},
+            "layers": layers}
+
+
+# BASELINE.json config 1: one fp32 linear as in Swin-T stage-1 QKV, X[11264 x 96]
+# W[288 x 96] + bias, N(0,1)/sqrt(96), seed 0 (reference CPU kernels_ref.c:
+# 292-339 and its dispatch test tests/test_cpu_dispatch.c:25-70; GPU entry
+# point bf_cuda_gemm_f32, src/cuda_ops.cu:188-208).
+CONFIG1 = (11264, 96, 288)
+
+
+def config1_inputs():
+    import numpy as np
+    m, k, n = CONFIG1
+    rng = np.random.default_rng(0)
+    sc = 1.0 / np.sqrt(k)
+    x = (rng.standard_normal((m, k)) * sc).astype(np.float32)
+    w = (rng.standard_normal((n, k)) * sc).astype(np.float32)
+    b = (rng.standard_normal(n) * sc).astype(np.float32)
+    return x, w, b
+
+
+def config1_leg(dev, reps, with_cpu):
+    """bf_cuda_gemm_f32 at config 1 (HIP events, eager launches on one
+    stream); the CPU side times the reference's linear (its OpenMP split and
+    its scalar kernel) as a median of >= 20 calls."""
+    import statistics
+    import torch
+    import bfhip
+    m, k, n = CONFIG1
+    x, w, b = config1_inputs()
+    flops = 2.0 * m * n * k
+    nbytes = (x.size + w.size + b.size + m * n) * 4
+    xd, wd, bd = (torch.from_numpy(a).to(dev) for a in (x, w, b))
+    yd = torch.empty((m, n), device=dev)
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        for _ in range(5):
+            bfhip.gemm_f32(xd, wd, bd, out=yd, stream=stream)
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(reps):
+            bfhip.gemm_f32(xd, wd, bd, out=yd, stream=stream)
+        stop.record(stream)
+        stop.synchronize()
+    avg_s = start.elapsed_time(stop) / 1e3 / reps
+    roof = roofline_entry("bf_cuda_gemm_f32 11264x96 -> 288 (fp32 in/out)", avg_s, 1, flops, nbytes)
+    out = {"workload": "BASELINE config 1: fp32 linear X[11264x96] W[288x96]^T + b, "
+                       "N(0,1)/sqrt(96), seed 0",
+           "gpu": {"us": round(avg_s * 1e6, 2), "gflop_per_s": round(flops / avg_s / 1e9, 1),
+                   "roofline": {kk: roof[kk] for kk in ("bound", "achieved", "peak", "unit",
+                                                        "frac")}}}
+    if with_cpu:
+        import oracle
+        flavour = "ref_o3" if oracle.available("ref_o3") else "port"
+        o = oracle.Oracle(flavour)
+        cpu = {}
+        for label, scalar in (("optimized", False), ("scalar", True)):
+            times = []
+            for _ in range(21):
+                t0 = time.perf_counter()
+                o.linear(x, w, b, scalar=scalar)
+                times.append(time.perf_counter() - t0)
+            med = statistics.median(times[1:])
+            cpu[label] = {"ms": round(med * 1e3, 3), "gflop_per_s": round(flops / med / 1e9, 2),
+                          "reps": len(times) - 1}
+        cpu.update(_cpu_host(), kind="reference" if flavour == "ref_o3" else "port",
+                   backend=o.backend())
+        out["cpu"] = cpu
+    return out
+
+
+def calibrate_leg(dev):
+    """Machine rates behind the roofline discussion, from the calibration
+    kernels of include/bfhip_profile.h: launch cost (eager and inside a HIP
+    graph), sustained bf16 MFMA rate of the 16x16x32 and 32x32x16 shapes, LDS
+    read bandwidth and device copy bandwidth."""
+    import torch
+    import bfhip
+    stream = torch.cuda.Stream()
+    ev = lambda: torch.cuda.Event(enable_timing=True)
+
+    def timed(fn, reps):
+        fn()
+        start, stop = ev(), ev()
+        start.record(stream)
+        for _ in range(reps):
+            fn()
+        stop.record(stream)
+        stop.synchronize()
+        return start.elapsed_time(stop) / 1e3 / reps
+
+    out = {}
+    with torch.cuda.stream(stream):
+        launches = 200
+        out["launch_us_eager"] = round(1e6 * timed(lambda: bfhip.calibrate("empty", 1, stream=stream),
+                                                   launches), 3)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for _ in range(launches):
+                bfhip.calibrate("empty", 1, stream=stream)
+        out["launch_us_graph"] = round(1e6 * timed(graph.replay, 5) / launches, 3)
+        sink = torch.empty(1024 * 256, device=dev)
+        grid, iters = 512, 2000
+        t = timed(lambda: bfhip.calibrate("mfma16", grid, iters, dst=sink, stream=stream), 5)
+        out["mfma16x16x32_bf16_tflops"] = round(grid * 4 * iters * 8 * 16384 / t / 1e12, 1)
+        t = timed(lambda: bfhip.calibrate("mfma32", grid, iters, dst=sink, stream=stream), 5)
+        out["mfma32x32x16_bf16_tflops"] = round(grid * 4 * iters * 8 * 32768 / t / 1e12, 1)
+        lgrid, liters = 1024, 4000
+        t = timed(lambda: bfhip.calibrate("lds", lgrid, liters, dst=sink, stream=stream), 5)
+        lds = lgrid * 256 * liters * 16 / t
+        out["lds_read_tb_s"] = round(lds / 1e12, 2)
+        out["lds_read_b_per_clk_per_cu_at_2_4ghz"] = round(lds / 256 / 2.4e9, 1)
+        src = torch.zeros(256 << 20, device=dev)  # 1 GiB
+        dst = torch.empty_like(src)
+        t = timed(lambda: bfhip.calibrate("copy", 4096, src=src, dst=dst, stream=stream), 5)
+        out["copy_gb_s"] = round(2 * src.numel() * 4 / t / 1e9, 1)
+        del src, dst
+    out["note"] = ("MFMA kernels: 2 workgroups of 4 waves per CU, 8 independent accumulator "
+                   "chains per wave; LDS: 4 workgroups per CU, conflict-free 16-byte reads issued "
+                   "8 at a time; copy: 1 GiB float4, read + write bytes")
+    return out
 
 
 LSS_OP = "lss_forward"
@@ -409,8 +737,8 @@ def lss_cpu_baseline(sc):
     """The reference's CPU geometry + fused lift-pool (oracle/_ref, src/lss.c)
     on the full production frame, single-threaded (lss.c has no OpenMP)."""
     import oracle
-    kind = "reference" if oracle.available("ref") else "port"
-    o = oracle.Oracle("ref" if kind == "reference" else "port")
+    kind = "reference" if oracle.available("ref_o3") else "port"
+    o = oracle.Oracle("ref_o3" if kind == "reference" else "port")
     d = sc["desc"]
     desc = oracle.lss_desc(d["batches"], d["cameras"], d["depth_bins"], d["height"],
                            d["width"], d["channels"], d["minimum"], d["step"], d["cells"])
@@ -492,8 +820,8 @@ def bev_cpu_baseline(path, seed=0):
     a bounded 90x90 sample, scaled to 180x180 by the work ratio (4x)."""
     import oracle
     from bfhip import bfw
-    kind = "reference" if oracle.available("ref") else "port"
-    o = oracle.Oracle("ref" if kind == "reference" else "port")
+    kind = "reference" if oracle.available("ref_o3") else "port"
+    o = oracle.Oracle("ref_o3" if kind == "reference" else "port")
     x = bfw.synthetic_bev(seed, BEV_HW // 2, BEV_HW // 2)
     with o.open_model(path) as m:
         t0 = time.perf_counter()
@@ -586,8 +914,8 @@ def tf_cpu_baseline(path, seed=0):
     workload."""
     import oracle
     from bfhip import bfw
-    kind = "reference" if oracle.available("ref") else "port"
-    o = oracle.Oracle("ref" if kind == "reference" else "port")
+    kind = "reference" if oracle.available("ref_o3") else "port"
+    o = oracle.Oracle("ref_o3" if kind == "reference" else "port")
     sh, hm = bfw.synthetic_transfusion_inputs(seed, TF_HW, TF_HW)
     with o.open_model(path) as m:
         o.transfusion(m, sh, hm, TF_PROPOSALS)
@@ -752,8 +1080,8 @@ def lidar_cpu_baseline(path, pts):
     """The reference's CPU LiDAR branch (oracle/_ref: src/voxel.c,
     src/kernels_ref.c MeanVFE, src/lidar_backbone.c) on the same frame."""
     import oracle
-    kind = "reference" if oracle.available("ref") else "port"
-    o = oracle.Oracle("ref" if kind == "reference" else "port")
+    kind = "reference" if oracle.available("ref_o3") else "port"
+    o = oracle.Oracle("ref_o3" if kind == "reference" else "port")
     cfg = oracle.voxel_config(LIDAR_VOXELS)
     with o.open_model(path) as m:
         t0 = time.perf_counter()
@@ -813,8 +1141,8 @@ def runtime_cpu_baseline(path, frame):
     """The reference's CPU frame runtime (oracle/_ref: src/runtime.c and its
     modules, OpenMP) on the same frame."""
     import oracle
-    kind = "reference" if oracle.available("ref") else "port"
-    o = oracle.Oracle("ref" if kind == "reference" else "port")
+    kind = "reference" if oracle.available("ref_o3") else "port"
+    o = oracle.Oracle("ref_o3" if kind == "reference" else "port")
     t0 = time.perf_counter()
     o.runtime_infer(path, frame, 300000, LIDAR_VOXELS, LIDAR_SPARSE)
     t1 = time.perf_counter()
@@ -825,14 +1153,14 @@ def runtime_cpu_baseline(path, frame):
 
 
 def cpu_baseline(model_path, cameras):
-    """Reference CPU path (oracle/_ref, the reference's C compiled from its own
-    sources, OpenMP) on a bounded sample of `cameras` cameras, scaled to a
-    6-camera frame.  Falls back to the restatement if _ref is absent."""
-    import numpy as np
+    """Reference CPU path (oracle/_ref/libbfref_o3.so: the reference's C
+    compiled from its own sources under its own -O3 OpenMP CFLAGS) on
+    `cameras` cameras, scaled to a 6-camera frame when fewer.  Falls back to
+    the restatement if the reference build is absent."""
     import oracle
     from bfhip import bfw
-    kind = "reference" if oracle.available("ref") else "port"
-    o = oracle.Oracle("ref" if kind == "reference" else "port")
+    flavour = "ref_o3" if oracle.available("ref_o3") else "port"
+    o = oracle.Oracle(flavour)
     images = bfw.synthetic_images(0, cameras, 256, 704)
     depth = bfw.synthetic_depth(0, cameras, 256, 704)
     with o.open_model(model_path) as m:
@@ -843,16 +1171,47 @@ def cpu_baseline(model_path, cameras):
         o.depth_head(m, f0, depth)
         t2 = time.perf_counter()
     per_frame_ms = (t2 - t0) * 1e3 * 6 / cameras
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or os.cpu_count()
-    return {"value": round(per_frame_ms, 1), "unit": "ms/frame", "cores": threads,
-            "kind": kind, "backend": o.backend(),
-            "sample": f"{cameras} of 6 cameras, Swin-T + FPN + depth head at 256x704 "
-                      f"(swin {1e3 * (t1 - t0):.0f} ms, neck {1e3 * (t2 - t1):.0f} ms), "
-                      f"scaled x{6 / cameras:g}",
-            "cpu_model": _cpu_model()}
+    sample = (f"{cameras} of 6 cameras" if cameras < 6 else "one full 6-camera frame") + \
+        f", Swin-T + FPN + depth head at 256x704 (swin {1e3 * (t1 - t0):.0f} ms, " \
+        f"neck {1e3 * (t2 - t1):.0f} ms)" + (f", scaled x{6 / cameras:g}" if cameras < 6 else "")
+    out = {"value": round(per_frame_ms, 1), "unit": "ms/frame",
+           "kind": "reference" if flavour == "ref_o3" else "port", "backend": o.backend(),
+           "build": "-O3 -std=c11 -fopenmp -DBF_WITH_OPENMP (reference Makefile:4,40-45)"
+                    if flavour == "ref_o3" else "restatement", "sample": sample}
+    out.update(_cpu_host())
+    return out
+
+
+def _cpu_host():
+    """Host facts for a CPU figure: the threads OpenMP used (`cores`), nproc,
+    the process's CPU affinity and the CPU model."""
+    aff = sorted(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else []
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or len(aff) or os.cpu_count()
+    return {"cores": threads, "omp_num_threads": os.environ.get("OMP_NUM_THREADS"),
+            "nproc": os.cpu_count(), "affinity_cpus": len(aff),
+            "affinity": _ranges(aff), "cpu_model": _cpu_model()}
+
+
+def _ranges(cpus):
+    out, i = [], 0
+    while i < len(cpus):
+        j = i
+        while j + 1 < len(cpus) and cpus[j + 1] == cpus[j] + 1:
+            j += 1
+        out.append(f"{cpus[i]}-{cpus[j]}" if j > i else f"{cpus[i]}")
+        i = j + 1
+    return ",".join(out)
 
 
 def _cpu_model():
+    import subprocess
+    try:
+        txt = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in txt.splitlines():
+            if line.startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
     try:
         for line in open("/proc/cpuinfo"):
             if line.startswith("model name"):
@@ -882,7 +1241,7 @@ def main():
     model_path = bfw.write_camera_branch(tmp / "camera_branch.bfw", seed=0, mode="baseline")
     with bfhip.Model(model_path) as m:
         swin = bfhip.Swin(m, 6, 256, 704)
-        neck = bfhip.CameraNeck(m, 6, 32, 88, 360, 360)
+        neck = bfhip.CameraNeck(m, 6, 32, 88, DOWN_IN_HW, DOWN_IN_HW)
 
     frames = 20
     imgs = [torch.from_numpy(bfw.synthetic_images(s, 6, 256, 704)).to(dev) for s in range(frames)]
@@ -926,6 +1285,7 @@ def main():
         t1 = time.perf_counter()
     ms = (t1 - t0) * 1e3 / args.steps
     gflop = frame_flops() / 1e9
+    gflop_exec = frame_flops(window_rows=False) / 1e9
     tflops = gflop / ms
 
     result = {
@@ -947,25 +1307,55 @@ def main():
                    "cameras": 6, "image_hw": [256, 704], "graph": graph is not None},
         "tflops": round(tflops, 2),
         "gflop_per_frame": round(gflop, 1),
+        "gflop_note": "reference-equivalent work: QKV and proj charged at windows x 49 rows "
+                      "(padding tokens included), as the reference computes them",
         "frac_bf16_peak": round(tflops / PEAK_BF16_TFLOPS, 4),
+        "gflop_per_frame_executed": round(gflop_exec, 1),
+        "tflops_executed": round(gflop_exec / ms, 2),
+        "frac_bf16_peak_executed": round(gflop_exec / ms / PEAK_BF16_TFLOPS, 4),
         "frames_per_s": round(1e3 / ms, 1),
     }
+    kernels = []
     if not args.no_roofline:
+        io = neck_io(dev)
         with torch.cuda.stream(stream):
             only = tuple(k for k in args.kernels.split(",") if k)
-            kernels = time_kernels(swin, neck, stream, args.kernel_reps, only)
-        result["roofline"] = kernels[0]
-        result["kernels"] = [{k: e[k] for k in ("kernel", "bound", "frac", "avg_us",
-                                                  "us_per_frame", "tflops", "gbs")}
-                             for e in kernels[:12]]
+            kernels = time_kernels(swin, neck, stream, io, args.kernel_reps, only)
         if not args.no_traffic:
             torch.cuda.synchronize()
-            traffic, why = measure_traffic(kernels[0]["kernel"])
-            if traffic:
-                result["roofline"]["traffic"] = traffic["bytes"]
-                result["roofline"]["traffic_detail"] = traffic
-            else:
-                result["roofline"]["traffic_error"] = why
+            # The counter child launches the ops in op_table order.
+            with torch.cuda.stream(stream):
+                order = list(op_table(swin, neck, stream, io))
+            counters, errors = measure_op_counters(order)
+            for e in kernels:
+                c = counters.get(e["kernel"], {})
+                avg_s = e["avg_us"] / 1e6
+                if "mfma_util_pct" in c:
+                    e["mfma_util_pct"] = c["mfma_util_pct"]
+                    e["mfma_flops_per_launch"] = c["mfma_flops"]
+                    e["mfma_tflops"] = round(c["mfma_flops"] / avg_s / 1e12, 1)
+                if "fetch_bytes" in c and "write_bytes" in c:
+                    e["traffic"] = c["fetch_bytes"] + c["write_bytes"]
+                    e["traffic_detail"] = {k: c[k] for k in ("fetch_bytes", "write_bytes",
+                                                             "fetch_scale", "write_scale")}
+                    e["traffic_gbs"] = round(e["traffic"] / avg_s / 1e9, 1)
+            if errors:
+                result["counter_errors"] = errors
+        frame_ops = [e for e in kernels if not e["kernel"].startswith("neck.downsample")]
+        if frame_ops:
+            result["roofline"] = dict(frame_ops[0])
+        keep = ("kernel", "bound", "frac", "avg_us", "us_per_frame", "tflops", "gbs",
+                "mfma_util_pct", "mfma_tflops", "traffic", "traffic_gbs")
+        result["kernels"] = [{k: e[k] for k in keep if k in e} for e in frame_ops]
+    if not args.no_downsample:
+        result["downsample"] = downsample_leg(neck, dev, stream, max(args.steps, 20),
+                                              [{k: e[k] for k in ("kernel", "frac", "avg_us",
+                                                                  "tflops", "mfma_util_pct")
+                                                if k in e} for e in kernels])
+    if not args.no_config1:
+        result["config1"] = config1_leg(dev, 50, not args.no_cpu)
+    if not args.no_calibrate:
+        result["calibration"] = calibrate_leg(dev)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(model_path, args.cpu_cameras)
     if not args.no_lss:

@@ -128,6 +128,9 @@ SIGNATURES = {
     "bf_cuda_camera_downsample_forward": (_i, [_vp, _vp, _vp, _vp, C.c_char_p, _sz]),
     "bfhip_swin_profile_op": (_i, [_vp, _i, _i, _i, _vp, C.c_char_p, _sz]),
     "bfhip_camera_profile_layer": (_i, [_vp, _i, _vp, C.c_char_p, _sz]),
+    "bfhip_camera_profile_layer_io": (_i, [_vp, _i, _vp, _vp, _vp, _vp, C.c_char_p, _sz]),
+    "bfhip_calibrate": (_i, [_i, _i, _i, _vp, _vp, _sz, _vp, C.c_char_p, _sz]),
+    "bfhip_debug_runtime_fail_next": (_i, [_vp, C.c_char_p, _sz]),
     "bfhip_debug_window_map": (_i, [_i, _i, _i, _i, _vp, _vp, _vp, C.c_char_p, _sz]),
     "bfhip_debug_window_attention": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp,
                                           C.c_char_p, _sz]),
@@ -311,6 +314,21 @@ def gemm_f32(x, w, b=None, relu=False, out=None, stream=None):
     return out
 
 
+CALIB_KINDS = ("empty", "mfma16", "mfma32", "lds", "copy")
+
+
+def calibrate(kind, grid, iters=0, src=None, dst=None, stream=None):
+    """Enqueue one calibration kernel (include/bfhip_profile.h): `kind` in
+    CALIB_KINDS; `dst` (and `src` for "copy") are device tensors."""
+    err = _err()
+    nbytes = dst.numel() * dst.element_size() if dst is not None else 0
+    _check(hip_lib().bfhip_calibrate(CALIB_KINDS.index(kind), grid, iters,
+                                     _vp(src.data_ptr()) if src is not None else None,
+                                     _vp(dst.data_ptr()) if dst is not None else None,
+                                     nbytes, _stream(stream), err, 512),
+           err, "bfhip_calibrate")
+
+
 def conv_desc(x_shape, w_shape, stride=(1, 1), padding=(0, 0), transpose=False, relu=False,
               out_hw=None, output_channels=None):
     n, ci, ih, iw = x_shape
@@ -486,8 +504,9 @@ class CameraNeck:
                "bf_cuda_camera_neck_forward")
         return logits, ctx
 
-    def downsample_forward(self, bev, stream=None):
-        out = self._empty((1, 80, self.bev_w // 2, self.bev_h // 2), bev)
+    def downsample_forward(self, bev, out=None, stream=None):
+        if out is None:
+            out = self._empty((1, 80, self.bev_w // 2, self.bev_h // 2), bev)
         err = _err()
         _check(self.lib.bf_cuda_camera_downsample_forward(self.handle, _ptr(bev), _ptr(out),
                                                           _stream(stream), err, 512), err,
@@ -499,6 +518,15 @@ class CameraNeck:
         err = _err()
         _check(self.lib.bfhip_camera_profile_layer(self.handle, layer, _stream(stream), err, 512),
                err, "bfhip_camera_profile_layer")
+
+    def profile_layer_io(self, layer, inp=None, out0=None, out1=None, stream=None):
+        """Enqueue dtransform.3 (layer 4, reads `inp`), depthnet.6 (layer 8,
+        writes `out0` / `out1`) or the last downsample conv (layer 11, writes
+        `out0`) on caller buffers (include/bfhip_profile.h)."""
+        err = _err()
+        _check(self.lib.bfhip_camera_profile_layer_io(self.handle, layer, _ptr(inp), _ptr(out0),
+                                                      _ptr(out1), _stream(stream), err, 512),
+               err, "bfhip_camera_profile_layer_io")
 
     def close(self):
         if self.handle:
@@ -907,3 +935,10 @@ class Runtime(_Context):
         _check(self.lib.bf_cuda_runtime_debug_hashes(self.handle, out, err, 512), err,
                "bf_cuda_runtime_debug_hashes")
         return list(out)
+
+    def debug_fail_next(self):
+        """Arm a one-shot failure of the next infer after its calibration
+        upload (bfhip_debug_runtime_fail_next, include/bfhip_debug.h)."""
+        err = _err()
+        _check(self.lib.bfhip_debug_runtime_fail_next(self.handle, err, 512), err,
+               "bfhip_debug_runtime_fail_next")

@@ -87,18 +87,48 @@ void fpn_impl(bf_cuda_camera_neck *n, const float *s0, const float *s1, const fl
     fpn_conv<D256>(n->L[kFpn0], n->t0, n->f0, out0, s);
 }
 
+// One layer of the depth head (dtransform.3 .. depthnet.6); the forward and
+// the profiling hooks launch through here.
+void depth_layer(bf_cuda_camera_neck *n, int layer, const float *depth, float *logits,
+                 float *context, hipStream_t s) {
+    const int h = (int)n->h, w = (int)n->w;
+    const ConvLayer &l = n->L[layer];
+    switch (layer) {
+        case kDt1:
+            run_conv<T32, 5, 5>(l, SrcNHWCDepthAffine{depth, n->dt0_w, n->dt0_b, 8 * h, 8 * w},
+                                nhwc_to(l, n->e1), s);
+            break;
+        case kDt2: run_conv_dma<D32, 5>(l, n->e1, 32, nullptr, 0, nhwc_to(l, n->e2), s); break;
+        case kDn0: run_conv_dma<D256, 3>(l, n->e2, 64, n->f0, 256, nhwc_to(l, n->d0), s); break;
+        case kDn3: run_conv_dma<D256, 3>(l, n->d0, 256, nullptr, 0, nhwc_to(l, n->d1), s); break;
+        case kDn6:
+            run_conv_dma<D256, 1>(l, n->d1, 256, nullptr, 0,
+                                  EpiSplitDepth{logits, context, l.b, l.n * h * w, h * w, 118, 80}, s);
+            break;
+        default: break;
+    }
+}
+
+// One layer of the post-LSS downsample from the packed BEV in n->bp; the last
+// one stores the x/y-transposed NCHW output.
+void downsample_layer(bf_cuda_camera_neck *n, int layer, float *output, hipStream_t s) {
+    const int bh = (int)n->bev_h, bw = (int)n->bev_w;
+    const ConvLayer &l = n->L[layer];
+    switch (layer) {
+        case kDs0: run_conv<T80, 3, 3>(l, SrcNHWC{n->bp, 80, bh, bw}, nhwc_to(l, n->b0), s); break;
+        case kDs1: run_conv<T80, 3, 3>(l, SrcNHWC{n->b0, 80, bh, bw}, nhwc_to(l, n->b1), s); break;
+        case kDs2:
+            run_conv<T80, 3, 3>(l, SrcNHWC{n->b1, 80, bh / 2, bw / 2},
+                                EpiTransposeXY{output, l.b, l.oh * l.ow, 80, l.oh, l.ow}, s);
+            break;
+        default: break;
+    }
+}
+
 // Depth head from the channels-last fpn0 in n->f0.
 void depth_impl(bf_cuda_camera_neck *n, const float *depth, float *logits, float *context,
                 hipStream_t s) {
-    const int h = (int)n->h, w = (int)n->w;
-    run_conv<T32, 5, 5>(n->L[kDt1], SrcNHWCDepthAffine{depth, n->dt0_w, n->dt0_b, 8 * h, 8 * w},
-                        nhwc_to(n->L[kDt1], n->e1), s);
-    run_conv_dma<D32, 5>(n->L[kDt2], n->e1, 32, nullptr, 0, nhwc_to(n->L[kDt2], n->e2), s);
-    run_conv_dma<D256, 3>(n->L[kDn0], n->e2, 64, n->f0, 256, nhwc_to(n->L[kDn0], n->d0), s);
-    run_conv_dma<D256, 3>(n->L[kDn3], n->d0, 256, nullptr, 0, nhwc_to(n->L[kDn3], n->d1), s);
-    const ConvLayer &l = n->L[kDn6];
-    run_conv_dma<D256, 1>(l, n->d1, 256, nullptr, 0,
-                          EpiSplitDepth{logits, context, l.b, l.n * h * w, h * w, 118, 80}, s);
+    for (int layer : {kDt1, kDt2, kDn0, kDn3, kDn6}) depth_layer(n, layer, depth, logits, context, s);
 }
 
 int build(bf_cuda_camera_neck *n, const bf_model *model, char *error, size_t cap) {
@@ -252,13 +282,8 @@ extern "C" int bf_cuda_camera_downsample_forward(bf_cuda_camera_neck *n, const f
                                                  size_t cap) {
     if (!n || !input || !output) return fail(error, cap, "invalid HIP downsample buffers");
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    const int bh = (int)n->bev_h, bw = (int)n->bev_w;
-    pack_nhwc(input, n->bp, 1, 80, bh * bw, s);
-    run_conv<T80, 3, 3>(n->L[kDs0], SrcNHWC{n->bp, 80, bh, bw}, nhwc_to(n->L[kDs0], n->b0), s);
-    run_conv<T80, 3, 3>(n->L[kDs1], SrcNHWC{n->b0, 80, bh, bw}, nhwc_to(n->L[kDs1], n->b1), s);
-    const ConvLayer &l = n->L[kDs2];
-    run_conv<T80, 3, 3>(l, SrcNHWC{n->b1, 80, bh / 2, bw / 2},
-                        EpiTransposeXY{output, l.b, l.oh * l.ow, 80, l.oh, l.ow}, s);
+    pack_nhwc(input, n->bp, 1, 80, (int)(n->bev_h * n->bev_w), s);
+    for (int layer : {kDs0, kDs1, kDs2}) downsample_layer(n, layer, output, s);
     return launch_ok(error, cap, "HIP downsample launch");
 }
 
@@ -267,7 +292,7 @@ extern "C" int bfhip_camera_profile_layer(bf_cuda_camera_neck *n, int layer, voi
     if (!n || layer < 0 || layer >= kLayers) return fail(error, cap, "invalid HIP camera layer");
     if (layer == kDt1 || layer == kDn6)
         return fail(error, cap, "camera layer %d reads or writes caller buffers; time it through "
-                    "bf_cuda_camera_depth_forward", layer);
+                    "bfhip_camera_profile_layer_io", layer);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int h = (int)n->h, w = (int)n->w, h1 = (int)n->h1, w1 = (int)n->w1;
     const int h2 = (int)n->h2, w2 = (int)n->w2, bh = (int)n->bev_h, bw = (int)n->bev_w;
@@ -278,13 +303,24 @@ extern "C" int bfhip_camera_profile_layer(bf_cuda_camera_neck *n, int layer, voi
         case kFpn1: fpn_conv<D64>(l, n->t1, n->f1, nullptr, s); break;
         case kLat0: run_conv<T256, 1, 1>(l, SrcNHWCUpConcat{n->p0, n->f1, 192, 256, h, w, h1, w1}, nhwc_to(l, n->t0), s); break;
         case kFpn0: fpn_conv<D256>(l, n->t0, n->f0, nullptr, s); break;
-        case kDt2: run_conv_dma<D32, 5>(l, n->e1, 32, nullptr, 0, nhwc_to(l, n->e2), s); break;
-        case kDn0: run_conv_dma<D256, 3>(l, n->e2, 64, n->f0, 256, nhwc_to(l, n->d0), s); break;
-        case kDn3: run_conv_dma<D256, 3>(l, n->d0, 256, nullptr, 0, nhwc_to(l, n->d1), s); break;
-        case kDs0: run_conv<T80, 3, 3>(l, SrcNHWC{n->bp, 80, bh, bw}, nhwc_to(l, n->b0), s); break;
-        case kDs1: run_conv<T80, 3, 3>(l, SrcNHWC{n->b0, 80, bh, bw}, nhwc_to(l, n->b1), s); break;
+        case kDt2: case kDn0: case kDn3: depth_layer(n, layer, nullptr, nullptr, nullptr, s); break;
+        case kDs0: case kDs1: downsample_layer(n, layer, nullptr, s); break;
         case kDs2: run_conv<T80, 3, 3>(l, SrcNHWC{n->b1, 80, bh / 2, bw / 2}, nhwc_to(l, n->b0), s); break;
         default: break;
     }
     return launch_ok(error, cap, "launch HIP camera profiling layer");
+}
+
+extern "C" int bfhip_camera_profile_layer_io(bf_cuda_camera_neck *n, int layer, const float *input,
+                                             float *out0, float *out1, void *stream, char *error,
+                                             size_t cap) {
+    if (!n || (layer != kDt1 && layer != kDn6 && layer != kDs2) || (layer == kDt1 && !input) ||
+        (layer == kDn6 && (!out0 || !out1)) || (layer == kDs2 && !out0))
+        return fail(error, cap, "invalid HIP camera layer profiling call");
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (layer == kDs2)
+        downsample_layer(n, layer, out0, s);
+    else
+        depth_layer(n, layer, input, out0, out1, s);
+    return launch_ok(error, cap, "launch HIP camera layer profiling");
 }

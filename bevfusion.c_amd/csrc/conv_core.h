@@ -353,6 +353,10 @@ struct LoadConvNHWC {
 // and the source are uniform per stage and each lane moves one 16-byte chunk
 // of 8 channels.  Taps outside the map read as zero through an out-of-range
 // buffer offset.  Each source must span < 2 GiB.
+//
+// The lane's offset depends on the tap and the source only; it is computed
+// when they change (every C/BK k-tiles) and the channel offset within the
+// source rides in soffset, so most k-tiles issue with no vector arithmetic.
 template <int ROWS, int BK, int THREADS, int KH, int KW>
 struct DmaConvNHWC {
     static constexpr int kCpr = BK / 8, kWaves = THREADS / kWave;
@@ -362,13 +366,17 @@ struct DmaConvNHWC {
     const bf16 *a, *b;
     int C0, C1;
     ConvGeom g;
-    int wave;
+    int wave;         // wave-uniform (SGPR)
     int pix[kIssue];  // n * IH * IW of the lane's output pixel, or -1 past M
     int iy0[kIssue], ix0[kIssue];
     int cofs[kIssue];  // channel offset of the lane's chunk within the k-tile
+    // Cache: tap and source of the offsets below (-1: none yet).
+    int cached;
+    uint32_t voff[kIssue];
 
     __device__ void setup(int m0, int tid) {
-        wave = tid / kWave;
+        wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+        cached = -1;
         const int lane = tid % kWave, ohw = g.OH * g.OW;
 #pragma unroll
         for (int j = 0; j < kIssue; ++j) {
@@ -382,21 +390,26 @@ struct DmaConvNHWC {
             cofs[j] = 8 * (slot ^ dma_swizzle<BK>(r));
         }
     }
-    __device__ void issue(bf16 *lds, int k0) const {
+    __device__ void issue(bf16 *lds, int k0) {
         const int ci = C0 + C1, tap = k0 / ci, cb = k0 - tap * ci;
-        const int ky = tap / KW, kx = tap - ky * KW;
         const bool hi = cb >= C0;
         const int cs = hi ? C1 : C0, c0 = hi ? cb - C0 : cb;
+        const int key = 2 * tap + (hi ? 1 : 0);
+        if (key != cached) {  // wave-uniform
+            cached = key;
+            const int ky = tap / KW, kx = tap - ky * KW;
+#pragma unroll
+            for (int j = 0; j < kIssue; ++j) {
+                const int iy = iy0[j] + ky, ix = ix0[j] + kx;
+                const bool in = pix[j] >= 0 && (unsigned)iy < (unsigned)g.IH && (unsigned)ix < (unsigned)g.IW;
+                voff[j] = in ? (uint32_t)(((pix[j] + iy * g.IW + ix) * cs + cofs[j]) * 2) : kDmaOutOfRange;
+            }
+        }
         const uint32_t pixels = (uint32_t)g.N * g.IH * g.IW;
         const __amdgpu_buffer_rsrc_t rsrc = buffer_rsrc(hi ? b : a, pixels * (uint32_t)cs * 2u);
 #pragma unroll
-        for (int j = 0; j < kIssue; ++j) {
-            const int iy = iy0[j] + ky, ix = ix0[j] + kx;
-            const bool in = pix[j] >= 0 && (unsigned)iy < (unsigned)g.IH && (unsigned)ix < (unsigned)g.IW;
-            const uint32_t off = in ? (uint32_t)(((pix[j] + iy * g.IW + ix) * cs + c0 + cofs[j]) * 2)
-                                    : kDmaOutOfRange;
-            dma16(rsrc, lds + (j * kWaves + wave) * kWave * 8, off);
-        }
+        for (int j = 0; j < kIssue; ++j)
+            dma16(rsrc, lds + (j * kWaves + wave) * kWave * 8, voff[j], 2u * (uint32_t)c0);
     }
 };
 

@@ -307,14 +307,21 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, 
 
 constexpr uint32_t kDmaOutOfRange = 0x80000000u;  // >= any num_records used here
 
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, bf16 *lds, uint32_t voffset) {
+// One 16-byte LDS-DMA per lane: LDS[M0 + 16 * lane] = buffer[voffset + soffset].
+// soffset is wave-uniform (an SGPR), so per-step address arithmetic that is
+// the same for every lane (the k offset) costs no vector instructions.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, bf16 *lds, uint32_t voffset,
+                                      uint32_t soffset = 0) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        rsrc, (__attribute__((address_space(3))) void *)(lds), 16, voffset, 0, 0, 0);
+        rsrc, (__attribute__((address_space(3))) void *)(lds), 16, voffset, (int)soffset, 0, 0);
 }
 
 // Row-major bf16 operand X[R, K] (leading dimension ld elements, K % 8 == 0,
 // 16-byte aligned rows, R * ld * 2 < 2^31 bytes).  Rows past R and k past K
-// read as zero.
+// read as zero.  The lane's row and chunk offset are fixed per tile (vector
+// registers); the k-tile offset rides in soffset, so a full k-tile issues
+// with no vector arithmetic.  A partial last k-tile (K % BK != 0) checks k
+// per lane.
 template <int ROWS, int BK, int THREADS>
 struct DmaRowsBf16 {
     static constexpr int kCpr = BK / 8, kWaves = THREADS / kWave;
@@ -323,28 +330,34 @@ struct DmaRowsBf16 {
     static constexpr int kIssue = kChunks / (kWave * kWaves);  // DMA instructions per wave per stage
     const bf16 *base;
     int ld, rows, K;
-    int wave;
-    uint32_t row_off[kIssue];  // byte offset of the lane's row, or kDmaOutOfRange
+    int wave;                  // wave-uniform (SGPR)
+    uint32_t voff[kIssue];     // byte offset of the lane's row + chunk, or kDmaOutOfRange
     int kcol[kIssue];          // first k of the lane's chunk within the tile
 
     __device__ void setup(int r0, int tid) {
-        wave = tid / kWave;
+        wave = __builtin_amdgcn_readfirstlane(tid / kWave);
         const int lane = tid % kWave;
 #pragma unroll
         for (int j = 0; j < kIssue; ++j) {
             const int q = (j * kWaves + wave) * kWave + lane;
             const int r = q / kCpr, slot = q % kCpr;
-            row_off[j] = r0 + r < rows ? (uint32_t)(r0 + r) * (uint32_t)ld * 2u : kDmaOutOfRange;
             kcol[j] = 8 * (slot ^ dma_swizzle<BK>(r));
+            voff[j] = r0 + r < rows ? ((uint32_t)(r0 + r) * (uint32_t)ld + (uint32_t)kcol[j]) * 2u
+                                    : kDmaOutOfRange;
         }
     }
     __device__ void issue(bf16 *lds, int k0) const {
         const __amdgpu_buffer_rsrc_t rsrc = buffer_rsrc(base, (uint32_t)rows * (uint32_t)ld * 2u);
+        if (k0 + BK <= K) {
 #pragma unroll
-        for (int j = 0; j < kIssue; ++j) {
-            const int k = k0 + kcol[j];
-            const uint32_t off = (row_off[j] != kDmaOutOfRange && k < K) ? row_off[j] + 2u * k : kDmaOutOfRange;
-            dma16(rsrc, lds + (j * kWaves + wave) * kWave * 8, off);
+            for (int j = 0; j < kIssue; ++j)
+                dma16(rsrc, lds + (j * kWaves + wave) * kWave * 8, voff[j], 2u * (uint32_t)k0);
+        } else {
+#pragma unroll
+            for (int j = 0; j < kIssue; ++j) {
+                const bool in = voff[j] != kDmaOutOfRange && k0 + kcol[j] < K;
+                dma16(rsrc, lds + (j * kWaves + wave) * kWave * 8, in ? voff[j] + 2u * k0 : kDmaOutOfRange);
+            }
         }
     }
 };

@@ -31,6 +31,7 @@
 #include "bf_cuda_transfusion.h"
 #include "bf_cuda_voxel.h"
 #include "bf_model.h"
+#include "bfhip_debug.h"
 #include "hip_common.h"
 #include "internal.h"
 
@@ -172,6 +173,7 @@ struct bf_cuda_runtime {
     const bf_detections *detections;
     hipGraphExec_t graph[3];  // LiDAR, camera, tail
     bool use_graph, calib_valid;
+    bool inject_failure;  // bfhip_debug_runtime_fail_next armed
     float calib_key[kCalib];
 };
 
@@ -229,7 +231,15 @@ int run_part(bf_cuda_runtime *r, int k, Part part, hipStream_t stream, char *err
             if (g) (void)hipGraphDestroy(g);
             return 0;
         }
-        if (!hip_ok(end, error, cap, "end runtime graph capture")) return 0;
+        // The LiDAR stream is a blocking stream (it carries a CU mask): work
+        // that another host thread puts on the legacy null stream while the
+        // first frame captures it synchronises with it implicitly, which
+        // invalidates the capture.
+        if (!hip_ok(end, error, cap,
+                    k == 0 ? "end runtime graph capture (LiDAR stream; was the legacy null stream "
+                             "used by another thread during the first frame?)"
+                           : "end runtime graph capture"))
+            return 0;
         const hipError_t inst = hipGraphInstantiate(&r->graph[k], g, nullptr, nullptr, 0);
         (void)hipGraphDestroy(g);
         if (!hip_ok(inst, error, cap, "instantiate runtime graph")) {
@@ -467,12 +477,25 @@ extern "C" int bf_cuda_runtime_infer(bf_cuda_runtime *r, const bf_frame_input *f
         !hip_ok(hipMemcpyAsync(r->calib, key, sizeof(key), hipMemcpyHostToDevice, s), error, cap,
                 "upload HIP calibration"))
         return drain();
-    const bool changed = !r->calib_valid || std::memcmp(key, r->calib_key, sizeof(key)) != 0;
-    if (changed &&
-        !bf_cuda_lss_plan_prepare_calibration_f32(r->lss, r->frustum, r->calib, r->calib + 54,
-                                                  r->calib + 72, r->calib + 126, r->calib + 180,
-                                                  r->calib + 198, r->calib + 207, s, error, cap))
+    if (!r->calib_valid || std::memcmp(key, r->calib_key, sizeof(key)) != 0) {
+        // The cell lists are rebuilt in place: until the rebuild is queued
+        // they match no calibration, so a failure here leaves the cache
+        // invalid and the next frame rebuilds them again.
+        r->calib_valid = false;
+        if (!bf_cuda_lss_plan_prepare_calibration_f32(r->lss, r->frustum, r->calib, r->calib + 54,
+                                                      r->calib + 72, r->calib + 126, r->calib + 180,
+                                                      r->calib + 198, r->calib + 207, s, error, cap))
+            return drain();
+        // Queued: the lists now hold this calibration whatever fails later
+        // (every failure path drains the stream, which completes the rebuild).
+        std::memcpy(r->calib_key, key, sizeof(key));
+        r->calib_valid = true;
+    }
+    if (r->inject_failure) {  // debug hook: fail after the rebuild is queued
+        r->inject_failure = false;
+        fail(error, cap, "injected HIP runtime failure after the calibration upload");
         return drain();
+    }
     if (!run_part(r, 1, enqueue_camera, s, error, cap) ||
         !hip_ok(hipStreamWaitEvent(s, r->join, 0), error, cap, "join LiDAR branch") ||
         !run_part(r, 2, enqueue_tail, s, error, cap))
@@ -481,10 +504,6 @@ extern "C" int bf_cuda_runtime_infer(bf_cuda_runtime *r, const bf_frame_input *f
                                hipMemcpyDeviceToHost, s), error, cap, "copy HIP detections") ||
         !hip_ok(hipStreamSynchronize(s), error, cap, "synchronize HIP runtime"))
         return drain();
-    if (changed) {
-        std::memcpy(r->calib_key, key, sizeof(key));
-        r->calib_valid = true;
-    }
     if (detections->count < 0 || detections->count > BF_MAX_PROPOSALS)
         return fail(error, cap, "HIP runtime detection count out of range");
     return 1;
@@ -544,4 +563,10 @@ extern "C" int bf_cuda_runtime_debug_hashes(const bf_cuda_runtime *r, unsigned l
                    hip_ok(hipStreamSynchronize(s), error, cap, "synchronize HIP tensor hashes");
     (void)hipFree(tmp);
     return ok;
+}
+
+extern "C" int bfhip_debug_runtime_fail_next(bf_cuda_runtime *r, char *error, size_t cap) {
+    if (!r) return fail(error, cap, "invalid HIP runtime failure hook");
+    r->inject_failure = true;
+    return 1;
 }

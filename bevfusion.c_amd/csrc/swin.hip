@@ -211,8 +211,8 @@ static int swin_build(bf_cuda_swin *s, const bf_model *model, size_t batches, si
             o.fc2_w = arena.add_bf16(fc2_w, (size_t)4 * c * c);
             o.mlp_w = o.mlp_proj = 0;
             if (kFusedMlp[st]) {
-                std::vector<uint16_t> packed((size_t)8 * c * c);
-                pack_mlp_weights<MlpS0>(fc1_w, fc2_w, packed.data(), bf16_bits);
+                std::vector<uint16_t> packed((size_t)MlpS0::kChunks * MlpS0::kChunkBytes / 2);
+                pack_mlp_weights<MlpS0>(fc1_w, fc2_w, fc1_b, packed.data(), bf16_bits);
                 o.mlp_w = arena.add(packed.data(), packed.size() * 2);
                 std::vector<uint16_t> proj((size_t)c * c);
                 pack_proj_weights<MlpS0>(proj_w, proj.data(), bf16_bits);

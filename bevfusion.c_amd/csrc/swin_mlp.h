@@ -36,6 +36,8 @@
 
 #include "gemm_core.h"
 
+#include <cstring>
+
 namespace bfhip {
 
 template <int C_, int TF_, int WAVES_, int NBUF_, bool PROJ_>
@@ -46,13 +48,18 @@ struct MlpCfg {
     static constexpr int kChunks = kHid / 32;
     static constexpr int kKs = C / 32;            // k-steps over channels
     static constexpr int kCf = C / 16;            // output-channel fragments
-    static constexpr int kFrags = 2 * kKs + kCf;  // 1 KiB fragments per chunk
-    static constexpr int kChunkBytes = kFrags * 1024;
+    static constexpr int kFrags = 2 * kKs + kCf;  // 1 KiB weight fragments per chunk
+    // A chunk is its weight fragments followed by the fc1 bias of its 32
+    // hidden units (fp32, in accumulator order: [g][f][r] -> 32q+16f+4g+r).
+    static constexpr int kBiasBytes = 32 * 4;
+    static constexpr int kChunkBytes = kFrags * 1024 + kBiasBytes;
     static constexpr int kTokens = kWaves * TF * 16;
     static constexpr int kThreads = kWaves * kWave;
-    static constexpr int kPerWave = kFrags / kWaves;  // DMA instructions per wave per chunk
+    static constexpr int kPerWave = kFrags / kWaves + 1;  // DMA instructions per wave per chunk
+    static constexpr int kBiasLanes = kBiasBytes / 16 / kWaves;  // bias DMA lanes per wave
     static_assert(C % 32 == 0, "channels must be a multiple of 32");
     static_assert(kFrags % kWaves == 0, "chunk fragments must split evenly over the waves");
+    static_assert(kBiasLanes * 16 * kWaves == kBiasBytes, "bias block must split evenly over the waves");
     static_assert(kBufs >= 2 && kBufs <= kChunks, "2 .. kChunks chunk buffers");
 };
 
@@ -60,9 +67,11 @@ struct MlpCfg {
 constexpr int kslot(int g, int e) { return 16 * (e >> 2) + 4 * g + (e & 3); }
 
 // Host-side packing of W1 [4C][C] and W2 [C][4C] (fp32, PyTorch [out, in])
-// into the chunked fragment order above, as bf16 bit patterns.
+// into the chunked fragment order above, as bf16 bit patterns, each chunk
+// followed by its fp32 fc1 bias block (dst holds kChunks * kChunkBytes bytes).
 template <class Cfg, class ToBf16>
-void pack_mlp_weights(const float *w1, const float *w2, uint16_t *dst, ToBf16 to_bf16_bits) {
+void pack_mlp_weights(const float *w1, const float *w2, const float *b1, uint16_t *dst,
+                      ToBf16 to_bf16_bits) {
     constexpr int C = Cfg::C, H = Cfg::kHid;
     size_t o = 0;
     for (int q = 0; q < Cfg::kChunks; ++q) {
@@ -75,6 +84,13 @@ void pack_mlp_weights(const float *w1, const float *w2, uint16_t *dst, ToBf16 to
             for (int l = 0; l < 64; ++l)
                 for (int e = 0; e < 8; ++e)
                     dst[o++] = to_bf16_bits(w2[(size_t)(16 * j + (l & 15)) * H + 32 * q + kslot(l >> 4, e)]);
+        for (int g = 0; g < 4; ++g)
+            for (int f = 0; f < 2; ++f)
+                for (int r = 0; r < 4; ++r) {
+                    const float b = b1[32 * q + 16 * f + 4 * g + r];
+                    std::memcpy(dst + o, &b, 4);
+                    o += 2;
+                }
     }
 }
 
@@ -100,9 +116,12 @@ __global__ __launch_bounds__(Cfg::kThreads) __attribute__((amdgpu_waves_per_eu(4
     // lane group that later writes it (epilogue), so neither is __restrict__.
     constexpr int C = Cfg::C, TF = Cfg::TF, KS = Cfg::kKs, CF = Cfg::kCf;
     constexpr int NB = Cfg::kBufs, P = Cfg::kPerWave;
-    constexpr int kBiasPer = (Cfg::kHid + Cfg::kThreads - 1) / Cfg::kThreads;
+    // The chunk buffers are the kernel's only LDS object: a second __shared__
+    // array makes the compiler attach alias scopes to LDS accesses and then
+    // wait for every chunk DMA in flight before any chunk read, serialising
+    // the weight stream with the MFMAs.  The fc1 bias therefore travels inside
+    // each chunk.
     __shared__ __attribute__((aligned(1024))) bf16 sw[NB][Cfg::kChunkBytes / 2];
-    __shared__ float sb1[Cfg::kHid];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, l16 = lane & 15;
@@ -110,11 +129,23 @@ __global__ __launch_bounds__(Cfg::kThreads) __attribute__((amdgpu_waves_per_eu(4
 
     const __amdgpu_buffer_rsrc_t rsrc =
         buffer_rsrc(wpk, (uint32_t)Cfg::kChunks * (uint32_t)Cfg::kChunkBytes);
+    // Chunk q into buffer q % NB: P - 1 weight fragments per wave, then the
+    // wave's share of the bias block (kBiasLanes lanes of 16 bytes).  Past the
+    // last chunk the offsets are out of range, so the DMA only zero-fills that
+    // (free) buffer; issuing it anyway keeps every iteration's vmcnt
+    // arithmetic the same.
     auto issue = [&](int q) {
+        const bool in = q < Cfg::kChunks;
 #pragma unroll
-        for (int p = 0; p < P; ++p) {
+        for (int p = 0; p < P - 1; ++p) {
             const int frag = p * Cfg::kWaves + wave;
-            dma16(rsrc, sw[q % NB] + frag * 512, (uint32_t)(q * Cfg::kChunkBytes + frag * 1024 + lane * 16));
+            dma16(rsrc, sw[q % NB] + frag * 512,
+                  in ? (uint32_t)(q * Cfg::kChunkBytes + frag * 1024 + lane * 16) : kDmaOutOfRange);
+        }
+        if (lane < Cfg::kBiasLanes) {
+            const int at = Cfg::kFrags * 1024 + wave * Cfg::kBiasLanes * 16;
+            dma16(rsrc, sw[q % NB] + at / 2,
+                  in ? (uint32_t)(q * Cfg::kChunkBytes + at + lane * 16) : kDmaOutOfRange);
         }
     };
 
@@ -136,12 +167,6 @@ __global__ __launch_bounds__(Cfg::kThreads) __attribute__((amdgpu_waves_per_eu(4
 #pragma unroll
             for (int k = 0; k < KS; ++k)
                 af[i][k] = ok ? *reinterpret_cast<const bf16x8 *>(attn + row + 32 * k + 8 * g) : bf16x8{};
-    }
-    float bias1[kBiasPer];
-#pragma unroll
-    for (int r = 0; r < kBiasPer; ++r) {
-        const int i = threadIdx.x + r * Cfg::kThreads;
-        bias1[r] = i < Cfg::kHid ? b1[i] : 0.0f;
     }
     if constexpr (Cfg::kProj) {
         // x += proj(a) + b_proj, accumulated in the C layout.
@@ -166,11 +191,6 @@ __global__ __launch_bounds__(Cfg::kThreads) __attribute__((amdgpu_waves_per_eu(4
     }
 #pragma unroll
     for (int q = 0; q < NB - 1; ++q) issue(q);
-#pragma unroll
-    for (int r = 0; r < kBiasPer; ++r) {
-        const int i = threadIdx.x + r * Cfg::kThreads;
-        if (i < Cfg::kHid) sb1[i] = bias1[r];
-    }
 
     // LN2 in the C layout, then into fc1 B operands (k-slot order).
     bf16x8 xf[TF][KS];
@@ -213,22 +233,28 @@ __global__ __launch_bounds__(Cfg::kThreads) __attribute__((amdgpu_waves_per_eu(4
     }
 
     for (int q = 0; q < Cfg::kChunks; ++q) {
-        // Chunks issued after q: min(NB - 2, kChunks - 1 - q); wait for q only.
-        DmaWait<NB - 2>::template stages<P>(min(NB - 2, Cfg::kChunks - 1 - q));
+        // NB - 2 chunk loads were issued after chunk q: wait for q only.
+        DmaWait<NB - 2>::template stages<P>(NB - 2);
         // Every wave's part of chunk q landed, and buffer (q - 1) % NB is no
-        // longer read by anyone.  (sb1 was written before the first barrier.)
+        // longer read by anyone.
         if (q == 0) __syncthreads(); else lds_barrier();
-        if (q + NB - 1 < Cfg::kChunks) issue(q + NB - 1);
+        // fc1 bias of hidden rows 32q + 16f + 4g + r, from the chunk's bias
+        // block.  Read before the next chunk's DMA is issued: the compiler
+        // makes this read wait for every chunk DMA in flight, which here is
+        // only the chunk issued an iteration ago.
+        float4 bq[2];
+#pragma unroll
+        for (int f = 0; f < 2; ++f)
+            bq[f] = __builtin_bit_cast(
+                float4, *reinterpret_cast<const bf16x8 *>(sw[q % NB] + (Cfg::kFrags * 1024 + g * 32 + f * 16) / 2));
+        issue(q + NB - 1);
         const bf16 *wb = sw[q % NB] + lane * 8;
 
-        // fc1 accumulators start at the bias of their hidden rows 32q + 16f + 4g + r.
         f32x4 h[2][TF];
 #pragma unroll
-        for (int f = 0; f < 2; ++f) {
-            const float4 bq = *reinterpret_cast<const float4 *>(sb1 + 32 * q + 16 * f + 4 * g);
+        for (int f = 0; f < 2; ++f)
 #pragma unroll
-            for (int i = 0; i < TF; ++i) h[f][i] = f32x4{bq.x, bq.y, bq.z, bq.w};
-        }
+            for (int i = 0; i < TF; ++i) h[f][i] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int k = 0; k < KS; ++k)
 #pragma unroll
@@ -242,7 +268,11 @@ __global__ __launch_bounds__(Cfg::kThreads) __attribute__((amdgpu_waves_per_eu(4
 #pragma unroll
         for (int i = 0; i < TF; ++i)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) hb[i][e] = to_bf16(gelu(h[e >> 2][i][e & 3]));
+            for (int e = 0; e < 8; ++e) {
+                const float4 b = bq[e >> 2];
+                const float bias = (e & 3) == 0 ? b.x : (e & 3) == 1 ? b.y : (e & 3) == 2 ? b.z : b.w;
+                hb[i][e] = to_bf16(gelu(h[e >> 2][i][e & 3] + bias));
+            }
 #pragma unroll
         for (int j = 0; j < CF; ++j) {
             const bf16x8 a = *reinterpret_cast<const bf16x8 *>(wb + (2 * KS + j) * 512);

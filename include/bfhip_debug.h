@@ -20,11 +20,21 @@
  *       qkv_bias fp32 [3C], bias_mat fp32 [heads, 49, 49] (relative-position
  *       bias already gathered), out bf16 [tokens, C].  C = 32 * heads.
  *
+ *   bfhip_debug_runtime_fail_next
+ *       Arms a one-shot failure in the next bf_cuda_runtime_infer of
+ *       `runtime`: that call uploads the frame, queues the LSS cell-list
+ *       rebuild if the calibration changed, then fails (returns 0) before
+ *       the camera graph, draining both streams as any later failure does.
+ *       Lets a test check that the calibration cache stays consistent with
+ *       the queued cell lists across a failed frame.
+ *
  * All pointers are device pointers; stream is a hipStream_t.  Returns 1 on
  * success, 0 with a message in error[0..error_cap).
  */
 #ifndef BFHIP_DEBUG_H
 #define BFHIP_DEBUG_H
+
+#include "bf_cuda_runtime.h"
 
 #include <stddef.h>
 
@@ -40,6 +50,8 @@ int bfhip_debug_window_attention(const void *qkv_bf16_device, const float *qkv_b
                                  const float *bias_mat_device, void *out_bf16_device,
                                  int batches, int height, int width, int channels, int heads,
                                  int shift, void *stream, char *error, size_t error_cap);
+
+int bfhip_debug_runtime_fail_next(bf_cuda_runtime *runtime, char *error, size_t error_cap);
 
 #ifdef __cplusplus
 }

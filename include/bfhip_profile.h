@@ -46,9 +46,48 @@ int bfhip_swin_profile_op(bf_cuda_swin *swin, int stage, int block, int op,
 /* Camera-neck convolution `layer` in the context's layer table: 0 lateral 1,
  * 1 fpn 1, 2 lateral 0, 3 fpn 0, 5 dtransform.6, 6 depthnet.0, 7 depthnet.3,
  * 9-11 downsample.  Layers 4 (dtransform.3, reads the caller's dense depth)
- * and 8 (depthnet.6, writes the caller's logits/context) are refused. */
+ * and 8 (depthnet.6, writes the caller's logits/context) are refused here;
+ * bfhip_camera_profile_layer_io runs them on caller buffers.  Layer 11 here
+ * stores channels-last into context scratch instead of the transposed
+ * caller output (bfhip_camera_profile_layer_io runs the forward's kernel). */
 int bfhip_camera_profile_layer(bf_cuda_camera_neck *neck, int layer, void *stream,
                                char *error, size_t error_cap);
+
+/* The layers whose forward launch reads or writes caller buffers, on caller
+ * device buffers, at the forward's shape and kernel instance:
+ *   4   dtransform.0 fused into dtransform.3: reads `input`, the dense depth
+ *       [B,1,8h,8w];
+ *   8   depthnet.6: writes `out0` (logits [B,118,h,w]) and `out1` (context
+ *       [B,80,h,w]);
+ *   11  the last downsample conv: writes `out0`, the x/y-transposed
+ *       [1,80,bev_w/2,bev_h/2] output.
+ * Unused pointers may be NULL. */
+int bfhip_camera_profile_layer_io(bf_cuda_camera_neck *neck, int layer, const float *input,
+                                  float *out0, float *out1, void *stream, char *error,
+                                  size_t error_cap);
+
+/* Calibration kernels (machine rates for the roofline discussion).  Each
+ * enqueues one launch of `grid` workgroups on `stream`:
+ *   EMPTY   an empty kernel of 64 threads per workgroup (launch cost);
+ *   MFMA16  256 threads, each wave `iters` x 8 independent
+ *           v_mfma_f32_16x16x32_bf16 (16384 flops each);
+ *   MFMA32  same with v_mfma_f32_32x32x16_bf16 (32768 flops each);
+ *   LDS     256 threads, each `iters` (a multiple of 8) conflict-free 16-byte
+ *           LDS reads, issued 8 at a time;
+ *   COPY    a float4 copy of `bytes` from src to dst (16-byte aligned).
+ * For MFMA16/MFMA32/LDS, dst may receive one float per thread when `bytes`
+ * covers grid * 256 floats (it keeps the work observable); otherwise nothing
+ * is stored. */
+enum {
+    BFHIP_CALIB_EMPTY = 0,
+    BFHIP_CALIB_MFMA16 = 1,
+    BFHIP_CALIB_MFMA32 = 2,
+    BFHIP_CALIB_LDS = 3,
+    BFHIP_CALIB_COPY = 4
+};
+
+int bfhip_calibrate(int kind, int grid, int iters, const void *src, void *dst, size_t bytes,
+                    void *stream, char *error, size_t error_cap);
 
 #ifdef __cplusplus
 }

@@ -8,6 +8,8 @@ four interchangeable libraries with identical C signatures:
   ``port_scalar`` oracle/_build/liboracle_scalar.so  restatement, no OpenMP
   ``ref``         oracle/_ref/libbfref.so            reference C compiled from its sources
   ``ref_scalar``  oracle/_ref/libbfref_scalar.so     same, no OpenMP
+  ``ref_o3``      oracle/_ref/libbfref_o3.so         reference C under its own -O3 CFLAGS
+                                                     (timed CPU baseline only)
 
 Each library carries its own BFW reader, so models are opened through the
 library that consumes them.
@@ -27,6 +29,7 @@ LIBS = {
     "port_scalar": HERE / "_build" / "liboracle_scalar.so",
     "ref": HERE / "_ref" / "libbfref.so",
     "ref_scalar": HERE / "_ref" / "libbfref_scalar.so",
+    "ref_o3": HERE / "_ref" / "libbfref_o3.so",
 }
 
 _f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")

@@ -118,6 +118,57 @@ def test_runtime_graph_replays_equal_eager(model_path, frames):
     graph.close()
 
 
+def test_runtime_failed_frame_keeps_calibration_cache_consistent(model_path, frames):
+    """A frame whose calibration differs queues the LSS cell-list rebuild and
+    then fails (injected after the upload).  The next frame, back on the
+    previous calibration, must rebuild the lists again: its detections equal
+    a fresh runtime's bit for bit.  A stale cache would replay the graph with
+    the failed frame's lists."""
+    a = frames[0]
+    b = dict(a, camera_to_lidar=a["camera_to_lidar"].copy())
+    b["camera_to_lidar"][:, :3, 3] += np.float32(2.5)  # every camera moved: new cell lists
+    print("[case] runtime failure after calibration upload", flush=True)
+    with bfhip.Runtime(model_path) as fresh:
+        want = fresh.infer(a)
+    with bfhip.Runtime(model_path) as rt:
+        first = rt.infer(a)
+        other = rt.infer(b)
+        assert bytes(other) != bytes(first)  # the moved cameras change the result
+        rt.infer(a)
+        rt.debug_fail_next()
+        with pytest.raises(bfhip.BfHipError, match="injected"):
+            rt.infer(b)
+        again = rt.infer(a)
+    assert bytes(first) == bytes(want)
+    assert bytes(again) == bytes(want)
+
+
+def test_runtime_with_null_stream_work_in_flight(model_path, frames):
+    """The runtime's LiDAR stream carries a CU mask, which makes it a blocking
+    stream.  Work the caller queued on the legacy null stream (torch's default
+    stream) before the first, capturing frame and before a replayed frame must
+    neither break the capture nor change the detections."""
+    import torch
+    frame = frames[1]
+    print("[case] runtime with null-stream work in flight", flush=True)
+    with bfhip.Runtime(model_path) as quiet:
+        want = quiet.infer(frame)
+    x = torch.randn((2048, 2048), device="cuda:0")
+    assert torch.cuda.current_stream().cuda_stream == 0  # the legacy null stream
+    with bfhip.Runtime(model_path) as rt:
+        y = x
+        for _ in range(8):
+            y = torch.mm(y, x) * 1e-3
+        first = rt.infer(frame)  # captures the graphs
+        for _ in range(8):
+            y = torch.mm(y, x) * 1e-3
+        second = rt.infer(frame)
+        torch.cuda.synchronize()
+    assert torch.isfinite(y).all()
+    assert bytes(first) == bytes(want)
+    assert bytes(second) == bytes(want)
+
+
 def test_runtime_bfi_frame(model_path, frames, tmp_path):
     frame = dict(frames[1])
     frame["points"] = np.nan_to_num(frame["points"], nan=0.5)  # BFI holds finite values
