@@ -291,11 +291,18 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// Workgroup barrier without the release/acquire fences of __syncthreads (which
-// would drain every outstanding DMA); the empty asm statements keep the
-// compiler from moving LDS accesses across it.
+// Workgroup barrier for LDS traffic: waits for this wave's own LDS accesses
+// (lgkmcnt), then s_barrier; unlike __syncthreads it leaves global loads and
+// LDS-DMA in flight (vmcnt), so a prefetch survives it.  The lgkmcnt wait is
+// what makes a stage buffer free after the barrier: the compiler may sink the
+// MFMAs that consume a wave's last fragment reads below the barrier, leaving
+// those reads outstanding, and another wave's next DMA into that buffer could
+// overtake them.  The empty asm statements keep the compiler from moving LDS
+// accesses across it.  s_waitcnt encoding (gfx9): vmcnt 63, expcnt 7,
+// lgkmcnt 0.
 __device__ __forceinline__ void lds_barrier() {
     asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
 }
