@@ -4,11 +4,15 @@
 // Operands stream into LDS through buffer_load ... lds (DmaRowsBf16).  The
 // tile per layer comes from a sweep of this core over the Swin-T layer shapes
 // at 6 x 256 x 704 on MI355X (all 19 (N, K) pairs: qkv, proj, fc1, fc2 per
-// stage and the three patch merges).  64 x 64 tiles win everywhere: the grids
-// are small enough that more workgroups in flight beat larger per-wave tiles;
-// K = 96 layers run three 32-deep steps, the K >= 768 reductions one more
-// stage of 128.  (N, K) identifies the layer, so the table holds for any
-// camera count; other shapes take the 64-deep default.
+// stage and the three patch merges).  The grids are small (1-6 rounds of
+// 64 x 64 tiles on 256 CUs), so more workgroups in flight mostly beat larger
+// per-wave tiles: 64 x 64 is the default, K = 96 layers run three 32-deep
+// steps and the N = 768, K >= 768 reductions one more stage of 128.  Where a
+// wider tile measured faster it is listed by (N, K): 128 x 64 for stage-1
+// qkv / fc2 and the first merge (M = 16896), 64 x 128 for stage-1 fc1,
+// stage-2 qkv and stage-3 fc1, 128 x 128 for stage-2 fc1.  (N, K)
+// identifies the layer, so the table holds for any camera count; other shapes
+// take the 64-deep default.
 #pragma once
 
 #include <cstdint>
@@ -25,12 +29,15 @@ inline void linear_tile(const bf16 *x, const bf16 *w, int M, int N, int K, const
     launch_gemm_dma<T>(al, bl, epi, M, N, K, s);
 }
 
-enum LinearTile { kK32, kK64, kK128 };
+enum LinearTile { kK32, kK64, kK128, kTall, kWide, kBig };
 
 inline LinearTile pick_linear_tile(int N, int K) {
     struct Entry { int n, k; LinearTile t; };
     static const Entry table[] = {
         {768, 768, kK128}, {768, 3072, kK128}, {768, 1536, kK128},
+        {576, 192, kTall}, {192, 768, kTall},  {192, 384, kTall},
+        {768, 192, kWide}, {1152, 384, kWide}, {3072, 768, kWide},
+        {1536, 384, kBig},
     };
     for (const Entry &e : table)
         if (e.n == N && e.k == K) return e.t;
@@ -52,6 +59,9 @@ inline void linear_bf16(const bf16 *x, const bf16 *w, int M, int N, int K, const
         case kK32: linear_tile<DmaTile<64, 64, 32, 2, 2, 2>>(x, w, M, N, K, epi, s); break;
         case kK64: linear_tile<DmaTile<64, 64, 64, 2, 2, 2>>(x, w, M, N, K, epi, s); break;
         case kK128: linear_tile<DmaTile<64, 64, 128, 2, 2, 3>>(x, w, M, N, K, epi, s); break;
+        case kTall: linear_tile<DmaTile<128, 64, 64, 2, 2, 2>>(x, w, M, N, K, epi, s); break;
+        case kWide: linear_tile<DmaTile<64, 128, 64, 2, 2, 2>>(x, w, M, N, K, epi, s); break;
+        case kBig: linear_tile<DmaTile<128, 128, 64, 2, 2, 2>>(x, w, M, N, K, epi, s); break;
     }
 }
 

@@ -20,7 +20,7 @@
 #ifndef BF_CUDA_LIDAR_H
 #define BF_CUDA_LIDAR_H
 
-#include "bf_kernels.h"
+#include "bf_sparse_types.h"
 #include "bf_model.h"
 
 #include <stddef.h>

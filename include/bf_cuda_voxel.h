@@ -21,7 +21,7 @@
 #ifndef BF_CUDA_VOXEL_H
 #define BF_CUDA_VOXEL_H
 
-#include "bf_kernels.h"
+#include "bf_sparse_types.h"
 #include "bf_voxel.h"
 
 #include <stddef.h>

@@ -8,7 +8,7 @@
 #ifndef BF_VOXEL_H
 #define BF_VOXEL_H
 
-#include "bf_kernels.h"
+#include "bf_sparse_types.h"
 
 #include <stddef.h>
 

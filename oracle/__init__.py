@@ -96,7 +96,7 @@ class VoxelStats(C.Structure):
 
 
 class SparseDesc(C.Structure):
-    """bf_sparse_conv3d_desc (include/bf_kernels.h)."""
+    """bf_sparse_conv3d_desc (reference include/bf_kernels.h:37-46)."""
     _fields_ = [(n, C.c_size_t) for n in (
         "batches", "in_depth", "in_height", "in_width", "in_channels", "out_channels",
         "kernel_depth", "kernel_height", "kernel_width", "stride_depth", "stride_height",

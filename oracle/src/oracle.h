@@ -28,7 +28,7 @@
 #define BF_ORACLE_H
 
 #include "bevfusion.h"
-#include "bf_kernels.h"
+#include "bf_sparse_types.h"
 #include "bf_lss.h"
 #include "bf_voxel.h"
 #include "bf_model.h"

@@ -10,6 +10,10 @@ cuda_transfusion.cu:274-276,329-333,402-407; tests/test_cuda_ops.cu:164-174).
 import ctypes as C
 import pathlib
 import re
+import shutil
+import subprocess
+
+import pytest
 
 import bfhip
 
@@ -261,3 +265,34 @@ def test_runtime_rejects_invalid_contracts(tmp_path):
     assert m.bf_frame_input_view(None) is not None and not m.bf_frame_input_view(None)
     assert m.bf_frame_file_bytes(None) == 0
     m.bf_frame_close(None)
+
+
+@pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not installed")
+@pytest.mark.parametrize("order", ["sparse_first", "operators_first", "sparse_only"])
+def test_sparse_types_header_coexists_with_operator_header(tmp_path, order):
+    """include/bf_sparse_types.h carries only the two sparse types of the
+    reference's CPU operator header (include/bf_kernels.h:34-46).  With a
+    header of that name and guard on the include path (a stand-in declaring
+    the types and one operator), a translation unit that includes both in
+    either order must compile and still see the operator declaration; with
+    none on the path the types come from bf_sparse_types.h alone."""
+    ops = tmp_path / "ops"
+    ops.mkdir()
+    (ops / "bf_kernels.h").write_text(
+        "#ifndef BF_KERNELS_H\n#define BF_KERNELS_H\n#include <stddef.h>\n#include <stdint.h>\n"
+        "typedef struct { int32_t batch, z, y, x; } bf_coord4;\n"
+        "typedef struct { size_t batches; int submanifold; } bf_sparse_conv3d_desc;\n"
+        "int operator_marker(const bf_coord4 *c);\n#endif\n")
+    lines = {"sparse_first": ['#include "bf_cuda_lidar.h"', '#include "bf_kernels.h"'],
+             "operators_first": ['#include "bf_kernels.h"', '#include "bf_cuda_lidar.h"'],
+             "sparse_only": ['#include "bf_cuda_lidar.h"', '#include "bf_voxel.h"',
+                             '#include "bf_cuda_voxel.h"']}[order]
+    use = ("int f(const bf_coord4 *c) { return operator_marker(c); }\n" if order != "sparse_only"
+           else "int f(const bf_coord4 *c, const bf_sparse_conv3d_desc *d) "
+                "{ return c->x + (int)d->pad_width; }\n")
+    src = tmp_path / "tu.c"
+    src.write_text("\n".join(lines) + "\n" + use)
+    inc = [f"-I{ROOT / 'include'}"] + ([f"-I{ops}"] if order != "sparse_only" else [])
+    r = subprocess.run(["gcc", "-std=c11", "-Wall", "-Werror", "-c", str(src), "-o",
+                        str(tmp_path / "tu.o"), *inc], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
