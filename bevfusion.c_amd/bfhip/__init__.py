@@ -134,6 +134,8 @@ SIGNATURES = {
     "bfhip_debug_window_map": (_i, [_i, _i, _i, _i, _vp, _vp, _vp, C.c_char_p, _sz]),
     "bfhip_debug_window_attention": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp,
                                           C.c_char_p, _sz]),
+    "bfhip_debug_window_attention_noalloc": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i,
+                                                  _vp, C.c_char_p, _sz]),
     "bf_cuda_available": (_i, [C.c_char_p, _sz]),
     "bf_cuda_lss_lift_pool_f32": (_i, [_vp, _vp, _vp, _vp, _lssp, _vp, C.c_char_p, _sz]),
     "bf_cuda_lss_geometry_to_ranks_f32": (_i, [_vp, _vp, _lssp, _vp, C.c_char_p, _sz]),
@@ -382,10 +384,12 @@ def window_map(batches, height, width, shift, device, stream=None):
 
 
 def window_attention(qkv, qkv_bias, bias_mat, batches, height, width, heads, shift, out=None,
-                     stream=None):
+                     stream=None, noalloc=False):
     """Production window-attention kernel on caller buffers (include/bfhip_debug.h):
     qkv bf16 [tokens, 96*heads], qkv_bias fp32 [96*heads], bias_mat fp32
-    [heads, 49, 49]; returns out bf16 [tokens, 32*heads]."""
+    [heads, 49, 49]; returns out bf16 [tokens, 32*heads].  noalloc selects
+    bfhip_debug_window_attention_noalloc (score terms in the library's static
+    device array; the call does not synchronise)."""
     torch = _torch()
     c = 32 * heads
     tokens = batches * height * width
@@ -397,10 +401,10 @@ def window_attention(qkv, qkv_bias, bias_mat, batches, height, width, heads, shi
     out = out if out is not None else torch.zeros((tokens, c), dtype=torch.bfloat16,
                                                   device=qkv.device)
     err = _err()
-    _check(hip_lib().bfhip_debug_window_attention(
+    name = "bfhip_debug_window_attention_noalloc" if noalloc else "bfhip_debug_window_attention"
+    _check(getattr(hip_lib(), name)(
         _vp(qkv.data_ptr()), _ptr(qkv_bias), _ptr(bias_mat), _vp(out.data_ptr()), batches,
-        height, width, c, heads, shift, _stream(stream), err, 512), err,
-        "bfhip_debug_window_attention")
+        height, width, c, heads, shift, _stream(stream), err, 512), err, name)
     return out
 
 

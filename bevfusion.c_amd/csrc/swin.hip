@@ -29,6 +29,7 @@
 #include <algorithm>
 #include <climits>
 #include <cstdlib>
+#include <mutex>
 #include <vector>
 
 using namespace bfhip;
@@ -486,10 +487,13 @@ extern "C" int bfhip_debug_window_map(int batches, int height, int width, int sh
     return launch_ok(error, cap, "launch window-map probe");
 }
 
-extern "C" int bfhip_debug_window_attention(const void *qkv, const float *qkv_bias,
-                                            const float *bias_mat, void *out, int batches,
-                                            int height, int width, int channels, int heads,
-                                            int shift, void *stream, char *error, size_t cap) {
+namespace {
+
+// Contract of the window-attention probes: returns the (window, head) item
+// count, or 0 with a message in error.
+int window_attention_items(const void *qkv, const float *qkv_bias, const float *bias_mat,
+                           const void *out, int batches, int height, int width, int channels,
+                           int heads, int shift, char *error, size_t cap) {
     if (!qkv || !qkv_bias || !bias_mat || !out || batches <= 0 || height <= 0 || width <= 0 ||
         heads <= 0 || channels != 32 * heads || shift < 0 || shift >= 7)
         return fail(error, cap, "invalid window-attention probe");
@@ -497,21 +501,116 @@ extern "C" int bfhip_debug_window_attention(const void *qkv, const float *qkv_bi
     const long long items = (long long)batches * wy_n * wx_n * heads;
     if (items > INT_MAX || (long long)batches * height * width * 3 * channels > INT_MAX)
         return fail(error, cap, "window-attention probe is too large");
-    // The probe builds the score terms with the context's builder into its own
-    // buffer (test path only: it allocates and synchronises).
+    return (int)items;
+}
+
+// Builds the score terms with the context's builder into `term` (at least
+// attn_term_elems(heads, shift) words), then runs the attention kernel.
+void window_attention_launch(const void *qkv, const float *qkv_bias, const float *bias_mat,
+                             void *out, bf16 *term, int height, int width, int channels,
+                             int heads, int shift, int items, hipStream_t s) {
+    const int wy_n = (height + 6) / 7, wx_n = (width + 6) / 7;
+    hipLaunchKernelGGL(attn_term_kernel, dim3(window_types(shift) * heads * 8), dim3(64), 0, s,
+                       bias_mat, term, heads, wy_n, wx_n, shift);
+    hipLaunchKernelGGL(window_attention_kernel, dim3((unsigned)((items + kAttnWaves - 1) / kAttnWaves)),
+                       dim3(64 * kAttnWaves), 0, s, static_cast<const bf16 *>(qkv), qkv_bias, term,
+                       static_cast<bf16 *>(out), height, width, channels, heads, wy_n, wx_n, shift,
+                       items);
+}
+
+}  // namespace
+
+extern "C" int bfhip_debug_window_attention(const void *qkv, const float *qkv_bias,
+                                            const float *bias_mat, void *out, int batches,
+                                            int height, int width, int channels, int heads,
+                                            int shift, void *stream, char *error, size_t cap) {
+    const int items = window_attention_items(qkv, qkv_bias, bias_mat, out, batches, height, width,
+                                             channels, heads, shift, error, cap);
+    if (!items) return 0;
+    // The probe builds the score terms into its own buffer (test path only:
+    // it allocates and synchronises).
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     bf16 *term = nullptr;
     if (!hip_ok(hipMalloc(&term, attn_term_elems(heads, shift) * 2), error, cap,
                 "allocate probe attention terms"))
         return 0;
-    hipLaunchKernelGGL(attn_term_kernel, dim3(window_types(shift) * heads * 8), dim3(64), 0, s,
-                       bias_mat, term, heads, (int)wy_n, (int)wx_n, shift);
-    hipLaunchKernelGGL(window_attention_kernel, dim3((unsigned)((items + kAttnWaves - 1) / kAttnWaves)),
-                       dim3(64 * kAttnWaves), 0, s, static_cast<const bf16 *>(qkv), qkv_bias, term,
-                       static_cast<bf16 *>(out), height, width, channels, heads, (int)wy_n, (int)wx_n,
-                       shift, (int)items);
+    window_attention_launch(qkv, qkv_bias, bias_mat, out, term, height, width, channels, heads,
+                            shift, items, s);
     const int ok = launch_ok(error, cap, "launch window-attention probe") &&
                    hip_ok(hipStreamSynchronize(s), error, cap, "window-attention probe");
     (void)hipFree(term);
     return ok;
+}
+
+// ---- Window attention without allocation ---------------------------------
+// The score terms of one call (window types x heads x 8 KiB of bf16) go to a
+// file-scope device array instead of a per-call allocation: at most
+// kScratchHeads heads, 4 x 32 x 8 KiB = 1 MiB on every device the library
+// runs this entry point on, held until the process ends.  Every call on a
+// device rebuilds the terms it reads before reading them (no state carries
+// over between calls and nothing needs clearing), and all calls on a device
+// share the array: calls that overlap in time on one device (different
+// streams, or host threads) race on it.
+namespace {
+constexpr int kScratchHeads = 32;
+constexpr size_t kScratchElems = (size_t)4 * kScratchHeads * 8 * 64 * 8;
+static_assert(kScratchElems >= attn_term_elems(kScratchHeads, 1), "scratch covers the largest term");
+constexpr int kScratchDevices = 64;
+}  // namespace
+
+static __device__ __align__(256) bf16 scratch[kScratchElems];
+
+namespace {
+std::mutex g_scratch_mutex;
+void *g_scratch_address[kScratchDevices];  // per device; guarded by g_scratch_mutex
+
+// This device's copy of `scratch`: the host-side name of the array is not a
+// device address, so it is resolved once per device (with that device
+// current) and only the resolved pointer is ever passed to a kernel.
+bf16 *scratch_on(int device, char *error, size_t cap) {
+    if (device < 0 || device >= kScratchDevices) {
+        fail(error, cap, "window attention without allocation supports HIP devices 0..%d (got %d)",
+             kScratchDevices - 1, device);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_address[device]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            fail(error, cap, "resolve the window-attention scratch array: %s",
+                 e != hipSuccess ? hipGetErrorString(e) : "null address");
+            return nullptr;
+        }
+        g_scratch_address[device] = p;
+    }
+    return static_cast<bf16 *>(g_scratch_address[device]);
+}
+}  // namespace
+
+extern "C" int bfhip_debug_window_attention_noalloc(const void *qkv, const float *qkv_bias,
+                                                    const float *bias_mat, void *out, int batches,
+                                                    int height, int width, int channels, int heads,
+                                                    int shift, void *stream, char *error,
+                                                    size_t cap) {
+    const int items = window_attention_items(qkv, qkv_bias, bias_mat, out, batches, height, width,
+                                             channels, heads, shift, error, cap);
+    if (!items) return 0;
+    if (heads > kScratchHeads)
+        return fail(error, cap,
+                    "window attention without allocation supports at most %d heads (got %d)",
+                    kScratchHeads, heads);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    int device = -1, stream_device = -1;
+    if (!hip_ok(hipGetDevice(&device), error, cap, "query the current HIP device") ||
+        !hip_ok(hipStreamGetDevice(s, &stream_device), error, cap, "query the stream's device"))
+        return 0;
+    if (stream_device != device)
+        return fail(error, cap, "stream belongs to HIP device %d, but device %d is current",
+                    stream_device, device);
+    bf16 *term = scratch_on(device, error, cap);
+    if (!term) return 0;
+    window_attention_launch(qkv, qkv_bias, bias_mat, out, term, height, width, channels, heads,
+                            shift, items, s);
+    return launch_ok(error, cap, "launch window attention without allocation");
 }

@@ -258,7 +258,7 @@ static __global__ __launch_bounds__(64) void attn_term_kernel(const float *__res
     *reinterpret_cast<bf16x8 *>(term + ((size_t)(th * 8 + c) * 64 + lane) * 8) = o;
 }
 
-inline size_t attn_term_elems(int heads, int shift) {
+constexpr size_t attn_term_elems(int heads, int shift) {
     return (size_t)window_types(shift) * heads * 8 * 64 * 8;
 }
 

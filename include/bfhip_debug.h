@@ -20,6 +20,17 @@
  *       qkv_bias fp32 [3C], bias_mat fp32 [heads, 49, 49] (relative-position
  *       bias already gathered), out bf16 [tokens, C].  C = 32 * heads.
  *
+ *   bfhip_debug_window_attention_noalloc
+ *       The same operation with no allocation: no counterpart in the
+ *       reference.  It is for callers that cannot call hipMalloc (code under
+ *       HIP graph capture, serving loops that forbid allocation): the score
+ *       terms go to a 1 MiB file-scope device array instead of a per-call
+ *       buffer, and the call neither allocates nor synchronises.  At most 32
+ *       heads (larger counts return 0 with a message); the stream must belong
+ *       to the current device.  Every call on a device shares that device's
+ *       array, so calls that overlap in time on one device (other streams or
+ *       host threads) race; calls queued on one stream do not.
+ *
  *   bfhip_debug_runtime_fail_next
  *       Arms a one-shot failure in the next bf_cuda_runtime_infer of
  *       `runtime`: that call uploads the frame, queues the LSS cell-list
@@ -50,6 +61,13 @@ int bfhip_debug_window_attention(const void *qkv_bf16_device, const float *qkv_b
                                  const float *bias_mat_device, void *out_bf16_device,
                                  int batches, int height, int width, int channels, int heads,
                                  int shift, void *stream, char *error, size_t error_cap);
+
+int bfhip_debug_window_attention_noalloc(const void *qkv_bf16_device,
+                                         const float *qkv_bias_device,
+                                         const float *bias_mat_device, void *out_bf16_device,
+                                         int batches, int height, int width, int channels,
+                                         int heads, int shift, void *stream, char *error,
+                                         size_t error_cap);
 
 int bfhip_debug_runtime_fail_next(bf_cuda_runtime *runtime, char *error, size_t error_cap);
 

@@ -33,7 +33,7 @@ def declared(header):
 def test_every_declared_entry_point_is_exported():
     lib = bfhip.hip_lib()
     names = set().union(*(declared(h) for h in HEADERS))
-    assert len(names) == 58
+    assert len(names) == 59
     assert names == set(bfhip.SIGNATURES)
     missing = [n for n in sorted(names) if not hasattr(lib, n)]
     assert not missing, missing
@@ -115,6 +115,15 @@ def test_index_probes_reject_invalid():
     assert lib.bfhip_debug_window_attention(s, s, s, s, 70000, 7000, 7000, 96, 3, 3, None, e,
                                             256) == 0
     assert b"too large" in e.value
+    # The no-allocation variant shares the contract and bounds the head count
+    # by its static array; both are checked before any HIP call.
+    noalloc = lib.bfhip_debug_window_attention_noalloc
+    assert noalloc(s, s, s, s, 1, 7, 7, 64, 3, 0, None, e, 256) == 0
+    assert b"invalid" in e.value
+    assert noalloc(s, s, s, s, 70000, 7000, 7000, 96, 3, 3, None, e, 256) == 0
+    assert b"too large" in e.value
+    assert noalloc(s, s, s, s, 1, 7, 7, 32 * 33, 33, 3, None, e, 256) == 0
+    assert b"at most 32 heads" in e.value
 
 
 def test_lss_entry_points_reject_invalid_contracts():
