@@ -110,3 +110,43 @@ def test_neck_forward_equals_fpn_then_depth(device, tmp_models):
         rl, rc = o.depth_head(m, r0, depth)
     assert_close(lg.cpu().numpy(), rl, "neck logits")
     assert_close(cx.cpu().numpy(), rc, "neck context")
+
+
+def test_neck_production_batch_invariance_and_repeat(device, tmp_models):
+    """6x32x88 production neck (BASELINE config 4's camera shape; reference
+    gate tests/test_cuda_camera_full.cu:69-72 repeats the production chain and
+    compares bit for bit): repeated forwards are bit-identical, camera k of
+    the 6-camera forward is bit-identical to the 1-camera forward of the same
+    inputs (FPN levels, depth logits and context: no cross-camera coupling),
+    and the last camera matches the oracle."""
+    import oracle
+    import torch
+    from bfhip import bfw
+    path = tmp_models("fan_in", 1)
+    b, h, w = 6, 32, 88
+    s = _swin_like(b, h, w, seed=31)
+    depth = bfw.synthetic_depth(6, b, 8 * h, 8 * w)
+    six = _neck(path, b, h, w, (360, 360))
+    one = _neck(path, 1, h, w, (360, 360))
+    st = [_t(a, device) for a in s]
+    dt = _t(depth, device)
+    lg, cx = six.neck_forward(*st, dt)
+    lg2, cx2 = six.neck_forward(*st, dt)
+    f0, f1 = six.fpn_forward(*st)
+    torch.cuda.synchronize()
+    assert torch.equal(lg, lg2) and torch.equal(cx, cx2), "repeat neck forward differs"
+    for cam in (0, 3, 5):
+        sl = [a[cam:cam + 1].contiguous() for a in st]
+        lg1, cx1 = one.neck_forward(*sl, dt[cam:cam + 1].contiguous())
+        g0, g1 = one.fpn_forward(*sl)
+        torch.cuda.synchronize()
+        assert torch.equal(lg[cam:cam + 1], lg1), f"camera {cam} logits depend on batch"
+        assert torch.equal(cx[cam:cam + 1], cx1), f"camera {cam} context depends on batch"
+        assert torch.equal(f0[cam:cam + 1], g0) and torch.equal(f1[cam:cam + 1], g1), \
+            f"camera {cam} FPN levels depend on batch"
+    o = oracle.Oracle("port")
+    with o.open_model(path) as m:
+        r0, _ = o.image_fpn(m, *[a[5:6] for a in s])
+        rl, rc = o.depth_head(m, r0, depth[5:6])
+    assert_close(lg[5:6].cpu().numpy(), rl, "camera 5 logits")
+    assert_close(cx[5:6].cpu().numpy(), rc, "camera 5 context")
