@@ -386,19 +386,19 @@ def window_map(batches, height, width, shift, device, stream=None):
 def window_attention(qkv, qkv_bias, bias_mat, batches, height, width, heads, shift, out=None,
                      stream=None, noalloc=False):
     """Production window-attention kernel on caller buffers (include/bfhip_debug.h):
-    qkv bf16 [tokens, 96*heads], qkv_bias fp32 [96*heads], bias_mat fp32
-    [heads, 49, 49]; returns out bf16 [tokens, 32*heads].  noalloc selects
+    qkv fp16 [tokens, 96*heads], qkv_bias fp32 [96*heads], bias_mat fp32
+    [heads, 49, 49]; returns out fp16 [tokens, 32*heads].  noalloc selects
     bfhip_debug_window_attention_noalloc (score terms in the library's static
     device array; the call does not synchronise)."""
     torch = _torch()
     c = 32 * heads
     tokens = batches * height * width
-    if (qkv.dtype != torch.bfloat16 or tuple(qkv.shape) != (tokens, 3 * c)
+    if (qkv.dtype != torch.float16 or tuple(qkv.shape) != (tokens, 3 * c)
             or not qkv.is_contiguous()):
-        raise BfHipError("qkv must be a contiguous bf16 [tokens, 3C] tensor")
+        raise BfHipError("qkv must be a contiguous fp16 [tokens, 3C] tensor")
     if tuple(qkv_bias.shape) != (3 * c,) or tuple(bias_mat.shape) != (heads, 49, 49):
         raise BfHipError("qkv_bias must be [3C] and bias_mat [heads, 49, 49]")
-    out = out if out is not None else torch.zeros((tokens, c), dtype=torch.bfloat16,
+    out = out if out is not None else torch.zeros((tokens, c), dtype=torch.float16,
                                                   device=qkv.device)
     err = _err()
     name = "bfhip_debug_window_attention_noalloc" if noalloc else "bfhip_debug_window_attention"

@@ -38,7 +38,8 @@ struct SrcNCHW {
 
 // ----------------------------------------------------------------- A loader
 // KH/KW > 0 fix the kernel size at compile time; 0 means runtime geometry.
-template <int BM, int BK, int THREADS, int KH_, int KW_, class Src>
+// F16 stages fp16 words instead of bf16 (for an fp16 tile).
+template <int BM, int BK, int THREADS, int KH_, int KW_, class Src, bool F16 = false>
 struct LoadConvA {
     static constexpr int kGroups = THREADS / BM;
     static constexpr int kPer = BK / kGroups;
@@ -92,7 +93,7 @@ struct LoadConvA {
                 if (tap && (unsigned)iy < (unsigned)g.IH && (unsigned)ix < (unsigned)g.IW)
                     v = src(n, ci, iy, ix);
             }
-            st[e] = to_bf16(v);
+            st[e] = to_word(v, F16);
             if (++kx == kw()) {
                 kx = 0;
                 if (++ky == kh()) {

@@ -525,7 +525,7 @@ struct EpiRowsF32 {  // out[row*ld + col] = v (+bias) (ReLU)
 };
 
 template <bool GELU>
-struct EpiRowsBf16 {  // out[row*ld + col] = bf16(act(v + bias)); ld % 4 == 0
+struct EpiRowsF16 {  // out[row*ld + col] = fp16(act(v + bias)); ld % 4 == 0
     static constexpr bool kRowVector = true;
     bf16 *out;
     const float *bias;
@@ -542,7 +542,7 @@ struct EpiRowsBf16 {  // out[row*ld + col] = bf16(act(v + bias)); ld % 4 == 0
             const float t[4] = {y.x, y.y, y.z, y.w};
             bf16x4 o;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) o[e] = to_bf16(GELU ? gelu(t[e]) : t[e]);
+            for (int e = 0; e < 4; ++e) o[e] = to_half(GELU ? gelu(t[e]) : t[e]);
             bf16 *p = out + (size_t)row * ld + c.col;
             if (c.col + 3 < N) {
                 *reinterpret_cast<bf16x4 *>(p) = o;

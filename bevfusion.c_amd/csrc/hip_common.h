@@ -65,9 +65,23 @@ __device__ __forceinline__ f32x4 mfma16_as(bf16x8 a, bf16x8 b, f32x4 acc) {
     if constexpr (F16) return mfma16_f16(a, b, acc);
     else return mfma16(a, b, acc);
 }
+// fp16 words (IEEE binary16, round to nearest even) in the bf16 container,
+// rounded once from the fp32 value.  The empty asm keeps the compiler from
+// folding the multiply or add that produced v into the conversion
+// (v_fma_mix*_f16 rounds a*b+c straight to fp16): the folded and unfolded
+// forms can differ by one fp16 ulp, and the compiler chooses per unrolled
+// copy, so a row's result would depend on the tile slot it was computed in
+// (the GEMM epilogues unroll over rows).
+__device__ __forceinline__ bf16 to_half(float v) {
+    asm("" : "+v"(v));
+    return __builtin_bit_cast(bf16, static_cast<_Float16>(v));
+}
+__device__ __forceinline__ float half_to_f32(bf16 v) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, v));
+}
 // A float stored as the 16-bit word of the chosen format.
 __device__ __forceinline__ bf16 to_word(float v, bool f16) {
-    return f16 ? __builtin_bit_cast(bf16, static_cast<_Float16>(v)) : static_cast<bf16>(v);
+    return f16 ? to_half(v) : static_cast<bf16>(v);
 }
 
 // GELU 0.5*x*(1 + erf(x/sqrt(2))) (the reference's exact-erf form,

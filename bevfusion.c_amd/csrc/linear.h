@@ -1,5 +1,6 @@
-// bf16 x bf16 linear layers for the Swin context: Y = X W^T (+ epilogue),
-// X [M, K] bf16 row-major, W [N, K] bf16 (the PyTorch [out, in] layout).
+// fp16 x fp16 linear layers for the Swin context: Y = X W^T (+ epilogue),
+// X [M, K] fp16 row-major, W [N, K] fp16 (the PyTorch [out, in] layout), fp32
+// accumulation on the fp16 MFMA.
 //
 // Operands stream into LDS through buffer_load ... lds (DmaRowsBf16).  The
 // tile per layer comes from a sweep of this core over the Swin-T layer shapes
@@ -53,15 +54,15 @@ inline bool linear_operands_ok(const void *x, const void *w, int M, int N, int K
 }
 
 template <class Epi>
-inline void linear_bf16(const bf16 *x, const bf16 *w, int M, int N, int K, const Epi &epi,
+inline void linear_f16(const bf16 *x, const bf16 *w, int M, int N, int K, const Epi &epi,
                         hipStream_t s) {
     switch (pick_linear_tile(N, K)) {
-        case kK32: linear_tile<DmaTile<64, 64, 32, 2, 2, 2>>(x, w, M, N, K, epi, s); break;
-        case kK64: linear_tile<DmaTile<64, 64, 64, 2, 2, 2>>(x, w, M, N, K, epi, s); break;
-        case kK128: linear_tile<DmaTile<64, 64, 128, 2, 2, 3>>(x, w, M, N, K, epi, s); break;
-        case kTall: linear_tile<DmaTile<128, 64, 64, 2, 2, 2>>(x, w, M, N, K, epi, s); break;
-        case kWide: linear_tile<DmaTile<64, 128, 64, 2, 2, 2>>(x, w, M, N, K, epi, s); break;
-        case kBig: linear_tile<DmaTile<128, 128, 64, 2, 2, 2>>(x, w, M, N, K, epi, s); break;
+        case kK32: linear_tile<DmaTile<64, 64, 32, 2, 2, 2, true>>(x, w, M, N, K, epi, s); break;
+        case kK64: linear_tile<DmaTile<64, 64, 64, 2, 2, 2, true>>(x, w, M, N, K, epi, s); break;
+        case kK128: linear_tile<DmaTile<64, 64, 128, 2, 2, 3, true>>(x, w, M, N, K, epi, s); break;
+        case kTall: linear_tile<DmaTile<128, 64, 64, 2, 2, 2, true>>(x, w, M, N, K, epi, s); break;
+        case kWide: linear_tile<DmaTile<64, 128, 64, 2, 2, 2, true>>(x, w, M, N, K, epi, s); break;
+        case kBig: linear_tile<DmaTile<128, 128, 64, 2, 2, 2, true>>(x, w, M, N, K, epi, s); break;
     }
 }
 

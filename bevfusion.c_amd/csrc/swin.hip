@@ -2,16 +2,19 @@
 //
 // Data layout in HBM:
 //   x    fp32 [tokens, C]   residual stream, NHWC token order, in place
-//   xn   bf16 [tokens, C]   LayerNorm output -> QKV input; reused for the
+//   xn   fp16 [tokens, C]   LayerNorm output -> QKV input; reused for the
 //                           attention output and for the 2x2 merge rows
-//   big  bf16 [tokens, 4C]  QKV [tokens, 3C], later the GELU hidden [tokens, 4C]
+//   big  fp16 [tokens, 4C]  QKV [tokens, 3C], later the GELU hidden [tokens, 4C]
 // Window partitioning never materialises: the attention kernel gathers its 49
 // (padded, cyclically shifted) tokens straight from the token-major QKV rows
 // and scatters its output back the same way, so QKV and proj run as plain
 // token GEMMs over B*H*W rows instead of windows*49 rows.
 //
-// Per block: LN1 -> QKV GEMM(+bias, bf16) -> window attention ->
-// proj GEMM(+bias, += into x) -> LN2 -> fc1 GEMM(+bias, GELU, bf16) ->
+// 16-bit words are fp16 (stored in the bf16 container type): every GEMM and
+// the attention run on the fp16 MFMA with fp32 accumulation.
+//
+// Per block: LN1 -> QKV GEMM(+bias, fp16) -> window attention ->
+// proj GEMM(+bias, += into x) -> LN2 -> fc1 GEMM(+bias, GELU, fp16) ->
 // fc2 GEMM(+bias, += into x).  Stage 0 (C = 96) runs LN2 -> fc1 -> GELU ->
 // fc2 -> residual as one fused kernel whose hidden layer stays on chip
 // (swin_mlp.h), with the proj GEMM and its residual fused in front; it also
@@ -155,7 +158,7 @@ static int swin_build(bf_cuda_swin *s, const bf_model *model, size_t batches, si
         const float *nb = bind_f32(model, "image_backbone.patch_embed.norm.bias", {96}, error,
                                    cap);
         if (!pw || !pb || !ns || !nb) return 0;
-        o_patch_w = arena.add_bf16(pw, 96 * 48);
+        o_patch_w = arena.add_f16(pw, 96 * 48);
         o_patch_b = arena.add_f32(pb, 96);
         o_patch_ns = arena.add_f32(ns, 96);
         o_patch_nb = arena.add_f32(nb, 96);
@@ -206,17 +209,17 @@ static int swin_build(bf_cuda_swin *s, const bf_model *model, size_t batches, si
             o.fc1_b = arena.add_f32(fc1_b, 4 * c); o.fc2_b = arena.add_f32(fc2_b, c);
             o.bias_mat = arena.add_f32(bias);
             o.attn_term = arena.add(nullptr, attn_term_elems((int)hd, (b & 1) ? 3 : 0) * 2);
-            o.qkv_w = arena.add_bf16(qkv_w, (size_t)3 * c * c);
-            o.proj_w = arena.add_bf16(proj_w, (size_t)c * c);
-            o.fc1_w = arena.add_bf16(fc1_w, (size_t)4 * c * c);
-            o.fc2_w = arena.add_bf16(fc2_w, (size_t)4 * c * c);
+            o.qkv_w = arena.add_f16(qkv_w, (size_t)3 * c * c);
+            o.proj_w = arena.add_f16(proj_w, (size_t)c * c);
+            o.fc1_w = arena.add_f16(fc1_w, (size_t)4 * c * c);
+            o.fc2_w = arena.add_f16(fc2_w, (size_t)4 * c * c);
             o.mlp_w = o.mlp_proj = 0;
             if (kFusedMlp[st]) {
                 std::vector<uint16_t> packed((size_t)MlpS0::kChunks * MlpS0::kChunkBytes / 2);
-                pack_mlp_weights<MlpS0>(fc1_w, fc2_w, fc1_b, packed.data(), bf16_bits);
+                pack_mlp_weights<MlpS0>(fc1_w, fc2_w, fc1_b, packed.data(), f16_bits);
                 o.mlp_w = arena.add(packed.data(), packed.size() * 2);
                 std::vector<uint16_t> proj((size_t)c * c);
-                pack_proj_weights<MlpS0>(proj_w, proj.data(), bf16_bits);
+                pack_proj_weights<MlpS0>(proj_w, proj.data(), f16_bits);
                 o.mlp_proj = arena.add(proj.data(), proj.size() * 2);
             }
         }
@@ -236,7 +239,7 @@ static int swin_build(bf_cuda_swin *s, const bf_model *model, size_t batches, si
         if (!ms || !mb || !mw || !os || !ob) return 0;
         o_ms[st] = arena.add_f32(ms, 4 * c);
         o_mb[st] = arena.add_f32(mb, 4 * c);
-        o_mw[st] = arena.add_bf16(mw, (size_t)8 * c * c);
+        o_mw[st] = arena.add_f16(mw, (size_t)8 * c * c);
         o_os[st] = arena.add_f32(os, kC[st + 1]);
         o_ob[st] = arena.add_f32(ob, kC[st + 1]);
     }
@@ -296,7 +299,7 @@ static int swin_build(bf_cuda_swin *s, const bf_model *model, size_t batches, si
                 x_elems = std::max(x_elems, t2 * 2 * kC[st]);
             }
         }
-        // The linears address their bf16 operands through 32-bit buffer offsets.
+        // The linears address their 16-bit operands through 32-bit buffer offsets.
         if (std::max(xn_elems, big_elems) * 2 >= (size_t(1) << 31)) {
             fail(error, cap, "Swin batch too large: %zu images exceed the 2 GiB activation limit",
                  batches);
@@ -342,14 +345,14 @@ namespace {
 void patch_embed(bf_cuda_swin *s, const float *images, hipStream_t stream) {
     // 4x4/s4 conv 3->96 straight from NCHW images into NHWC tokens, then
     // LayerNorm in place.
-    using T = Tile<128, 96, 32, 2, 2>;
+    using T = Tile<128, 96, 32, 2, 2, true>;
     const int B = (int)s->batches;
     ConvGeom g{};
     g.N = B; g.Ci = 3; g.IH = (int)s->input_h; g.IW = (int)s->input_w;
     g.OH = s->h[0]; g.OW = s->w[0]; g.KH = 4; g.KW = 4; g.SH = 4; g.SW = 4;
     g.PH = 0; g.PW = 0; g.transpose = 0;
     g.M = B * s->h[0] * s->w[0]; g.K = 48;
-    LoadConvA<T::BM, T::BK, T::kThreads, 4, 4, SrcNCHW> al{};
+    LoadConvA<T::BM, T::BK, T::kThreads, 4, 4, SrcNCHW, true> al{};
     al.src = SrcNCHW{images, 3, g.IH, g.IW};
     al.g = g;
     LoadRowsBf16<T::BN, T::BK, T::kThreads> bl{s->patch_w, 48, 96, 48};
@@ -368,8 +371,8 @@ void block_op(bf_cuda_swin *s, int st, int b, int op, hipStream_t stream) {
             launch_ln<bf16>(C, s->x, s->xn, w.n1s, w.n1b, T, stream);
             break;
         case BFHIP_SWIN_QKV:
-            linear_bf16(s->xn, w.qkv_w, T, 3 * C, C,
-                        EpiRowsBf16<false>{s->big, w.qkv_b, 3 * C, T, 3 * C}, stream);
+            linear_f16(s->xn, w.qkv_w, T, 3 * C, C,
+                        EpiRowsF16<false>{s->big, w.qkv_b, 3 * C, T, 3 * C}, stream);
             break;
         case BFHIP_SWIN_ATTENTION:
             hipLaunchKernelGGL(window_attention_kernel, dim3((items + kAttnWaves - 1) / kAttnWaves),
@@ -377,17 +380,17 @@ void block_op(bf_cuda_swin *s, int st, int b, int op, hipStream_t stream) {
                                s->xn, H, W, C, heads, wy_n, wx_n, (b & 1) ? 3 : 0, items);
             break;
         case BFHIP_SWIN_PROJ:
-            linear_bf16(s->xn, w.proj_w, T, C, C, EpiResidualF32{s->x, w.proj_b, C, T, C}, stream);
+            linear_f16(s->xn, w.proj_w, T, C, C, EpiResidualF32{s->x, w.proj_b, C, T, C}, stream);
             break;
         case BFHIP_SWIN_LN2:
             launch_ln<bf16>(C, s->x, s->xn, w.n2s, w.n2b, T, stream);
             break;
         case BFHIP_SWIN_FC1:
-            linear_bf16(s->xn, w.fc1_w, T, 4 * C, C,
-                        EpiRowsBf16<true>{s->big, w.fc1_b, 4 * C, T, 4 * C}, stream);
+            linear_f16(s->xn, w.fc1_w, T, 4 * C, C,
+                        EpiRowsF16<true>{s->big, w.fc1_b, 4 * C, T, 4 * C}, stream);
             break;
         case BFHIP_SWIN_FC2:
-            linear_bf16(s->big, w.fc2_w, T, C, 4 * C, EpiResidualF32{s->x, w.fc2_b, C, T, C}, stream);
+            linear_f16(s->big, w.fc2_w, T, C, 4 * C, EpiResidualF32{s->x, w.fc2_b, C, T, C}, stream);
             break;
         case BFHIP_SWIN_MLP: {
             // The next block's LN1 is fused into the epilogue; the last block
@@ -426,7 +429,7 @@ void merge_op(bf_cuda_swin *s, int st, hipStream_t stream) {
     const int B = (int)s->batches, C = kC[st];
     const int T2 = B * s->h[st + 1] * s->w[st + 1];
     launch_merge(C, s->x, s->xn, s->merge_s[st], s->merge_b[st], B, s->h[st], s->w[st], stream);
-    linear_bf16(s->xn, s->merge_w[st], T2, 2 * C, 4 * C,
+    linear_f16(s->xn, s->merge_w[st], T2, 2 * C, 4 * C,
                 EpiRowsF32{s->x, nullptr, 2 * C, T2, 2 * C, 0}, stream);
 }
 
@@ -543,7 +546,7 @@ extern "C" int bfhip_debug_window_attention(const void *qkv, const float *qkv_bi
 }
 
 // ---- Window attention without allocation ---------------------------------
-// The score terms of one call (window types x heads x 8 KiB of bf16) go to a
+// The score terms of one call (window types x heads x 8 KiB of fp16) go to a
 // file-scope device array instead of a per-call allocation: at most
 // kScratchHeads heads, 4 x 32 x 8 KiB = 1 MiB on every device the library
 // runs this entry point on, held until the process ends.  Every call on a

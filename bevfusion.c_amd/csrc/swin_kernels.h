@@ -1,6 +1,9 @@
 // Swin-T building blocks on gfx950: row LayerNorms, the patch-merge gather,
 // the stage-output LayerNorm with NHWC->NCHW store, and batched shifted-
-// window attention on MFMA.
+// window attention on MFMA.  The Swin path's 16-bit operands (LayerNorm
+// outputs, QKV, attention terms and output, MLP hidden, weights) are fp16
+// words held in the bf16 container type, multiplied on the fp16 MFMA with
+// fp32 accumulation.
 #pragma once
 
 #include "hip_common.h"
@@ -24,8 +27,8 @@ __device__ __forceinline__ void store4(float *p, float a, float b, float c, floa
     *reinterpret_cast<float4 *>(p) = make_float4(a, b, c, d);
 }
 __device__ __forceinline__ void store4(bf16 *p, float a, float b, float c, float d) {
-    bf16x4 v;
-    v[0] = to_bf16(a); v[1] = to_bf16(b); v[2] = to_bf16(c); v[3] = to_bf16(d);
+    bf16x4 v;  // fp16 words
+    v[0] = to_half(a); v[1] = to_half(b); v[2] = to_half(c); v[3] = to_half(d);
     *reinterpret_cast<bf16x4 *>(p) = v;
 }
 
@@ -70,7 +73,7 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(const float *x, OutT *y, c
 
 // Patch merging: output row (n, oy, ox) is the 2x2 nn.Unfold of x[n,H,W,C]
 // with element order c*4 + ky*2 + kx (zero beyond odd edges; reference
-// swin_backbone.c:278-302, cuda_swin.cu:218-225), LayerNorm over 4C, bf16.
+// swin_backbone.c:278-302, cuda_swin.cu:218-225), LayerNorm over 4C, fp16.
 template <int C>
 __global__ __launch_bounds__(256) void merge_ln_kernel(const float *x, bf16 *y, const float *g,
                                                        const float *b, int batches, int H,
@@ -226,7 +229,7 @@ __host__ __device__ constexpr int window_types(int shift) { return shift ? 4 : 1
 //                                           key   j = 16*jb + 4*(l >> 4) + e
 //   term = rel_bias[h][i][j] - 100 * (label(i) != label(j))  for i, j < 49,
 //          0 for padded queries (i >= 49), -inf for padded keys (j >= 49).
-// Stored per (type, head) as 8 chunks of [64 lanes][8] bf16, so chunk c is one
+// Stored per (type, head) as 8 chunks of [64 lanes][8] fp16, so chunk c is one
 // coalesced 16-byte load per lane.  A representative window of each type
 // supplies the labels (bias_mat is [heads][49][49] fp32).
 static __global__ __launch_bounds__(64) void attn_term_kernel(const float *__restrict__ bias_mat,
@@ -253,7 +256,7 @@ static __global__ __launch_bounds__(64) void attn_term_kernel(const float *__res
                 t -= 100.0f;
             t *= kLog2e;
         }
-        o[k] = to_bf16(t);
+        o[k] = to_half(t);
     }
     *reinterpret_cast<bf16x8 *>(term + ((size_t)(th * 8 + c) * 64 + lane) * 8) = o;
 }
@@ -314,9 +317,9 @@ static __global__ __launch_bounds__(256) void window_attention_kernel(
             const float *bq = qkv_bias + h * 32 + 8 * g;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                q[e] = to_bf16(bq[e]);
-                k[e] = to_bf16(bq[C + e]);
-                v[e] = to_bf16(bq[2 * C + e]);
+                q[e] = to_half(bq[e]);
+                k[e] = to_half(bq[C + e]);
+                v[e] = to_half(bq[2 * C + e]);
             }
         }
         qf[b] = q;
@@ -330,7 +333,7 @@ static __global__ __launch_bounds__(256) void window_attention_kernel(
 #pragma unroll
     for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
-        for (int ib = 0; ib < 4; ++ib) s[jb][ib] = mfma16(kf[jb], qf[ib], f32x4{0, 0, 0, 0});
+        for (int ib = 0; ib < 4; ++ib) s[jb][ib] = mfma16_f16(kf[jb], qf[ib], f32x4{0, 0, 0, 0});
 
     // Softmax in base 2: scores and terms carry log2(e).
     const float scale = 0.17677669529663687f * 1.4426950408889634f;  // log2(e) / sqrt(32)
@@ -343,7 +346,7 @@ static __global__ __launch_bounds__(256) void window_attention_kernel(
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int v = 16 * jb + 4 * ib + e;
-                const float x = fmaf(s[jb][ib][e], scale, to_f32(add[v >> 3][v & 7]));
+                const float x = fmaf(s[jb][ib][e], scale, half_to_f32(add[v >> 3][v & 7]));
                 s[jb][ib][e] = x;
                 m = fmaxf(m, x);
             }
@@ -382,7 +385,7 @@ static __global__ __launch_bounds__(256) void window_attention_kernel(
 #pragma unroll
         for (int ib = 0; ib < 4; ++ib)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) pf[ib][e] = to_bf16(s[2 * c + (e >> 2)][ib][e & 3]);
+            for (int e = 0; e < 8; ++e) pf[ib][e] = to_half(s[2 * c + (e >> 2)][ib][e & 3]);
 #pragma unroll
         for (int db = 0; db < 2; ++db) {
             const bf16 *r = Vt + (16 * db + l16) * VS + 32 * c + 4 * g;
@@ -397,7 +400,7 @@ static __global__ __launch_bounds__(256) void window_attention_kernel(
 #pragma unroll
         for (int db = 0; db < 2; ++db)
 #pragma unroll
-            for (int ib = 0; ib < 4; ++ib) o[db][ib] = mfma16(vf[db], pf[ib], o[db][ib]);
+            for (int ib = 0; ib < 4; ++ib) o[db][ib] = mfma16_f16(vf[db], pf[ib], o[db][ib]);
     }
     // o[db][ib][e] = O[i = 16ib + l16][d = 16db + 4g + e] (unnormalised).
 #pragma unroll

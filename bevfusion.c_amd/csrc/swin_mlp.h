@@ -5,7 +5,8 @@
 // in one launch: x is read and written once, the 4C-wide hidden layer never
 // leaves the chip.
 //
-// Transposed formulation on v_mfma_f32_16x16x32_bf16 (A = weights, B = tokens).
+// Transposed formulation on v_mfma_f32_16x16x32_f16 (A = weights, B = tokens;
+// fp16 words, fp32 accumulation).
 // Every lane owns token (l & 15) of its 16-token fragment and, in the fp32
 // accumulator ("C") layout, channels 16j + 4(l>>4) + e (j < C/16, e < 4): the
 // residual row, the proj output, LN2, the fc2 output and LN1' all live in
@@ -67,11 +68,11 @@ struct MlpCfg {
 constexpr int kslot(int g, int e) { return 16 * (e >> 2) + 4 * g + (e & 3); }
 
 // Host-side packing of W1 [4C][C] and W2 [C][4C] (fp32, PyTorch [out, in])
-// into the chunked fragment order above, as bf16 bit patterns, each chunk
+// into the chunked fragment order above, as fp16 bit patterns, each chunk
 // followed by its fp32 fc1 bias block (dst holds kChunks * kChunkBytes bytes).
-template <class Cfg, class ToBf16>
+template <class Cfg, class ToWord>
 void pack_mlp_weights(const float *w1, const float *w2, const float *b1, uint16_t *dst,
-                      ToBf16 to_bf16_bits) {
+                      ToWord to_word_bits) {
     constexpr int C = Cfg::C, H = Cfg::kHid;
     size_t o = 0;
     for (int q = 0; q < Cfg::kChunks; ++q) {
@@ -79,11 +80,11 @@ void pack_mlp_weights(const float *w1, const float *w2, const float *b1, uint16_
             for (int s = 0; s < Cfg::kKs; ++s)
                 for (int l = 0; l < 64; ++l)
                     for (int e = 0; e < 8; ++e)
-                        dst[o++] = to_bf16_bits(w1[(size_t)(32 * q + 16 * f + (l & 15)) * C + 32 * s + kslot(l >> 4, e)]);
+                        dst[o++] = to_word_bits(w1[(size_t)(32 * q + 16 * f + (l & 15)) * C + 32 * s + kslot(l >> 4, e)]);
         for (int j = 0; j < Cfg::kCf; ++j)
             for (int l = 0; l < 64; ++l)
                 for (int e = 0; e < 8; ++e)
-                    dst[o++] = to_bf16_bits(w2[(size_t)(16 * j + (l & 15)) * H + 32 * q + kslot(l >> 4, e)]);
+                    dst[o++] = to_word_bits(w2[(size_t)(16 * j + (l & 15)) * H + 32 * q + kslot(l >> 4, e)]);
         for (int g = 0; g < 4; ++g)
             for (int f = 0; f < 2; ++f)
                 for (int r = 0; r < 4; ++r) {
@@ -95,15 +96,15 @@ void pack_mlp_weights(const float *w1, const float *w2, const float *b1, uint16_
 }
 
 // Host-side packing of the proj weight Wp [C][C] (fragment (j, s) order).
-template <class Cfg, class ToBf16>
-void pack_proj_weights(const float *wp, uint16_t *dst, ToBf16 to_bf16_bits) {
+template <class Cfg, class ToWord>
+void pack_proj_weights(const float *wp, uint16_t *dst, ToWord to_word_bits) {
     constexpr int C = Cfg::C;
     size_t o = 0;
     for (int j = 0; j < Cfg::kCf; ++j)
         for (int s = 0; s < Cfg::kKs; ++s)
             for (int l = 0; l < 64; ++l)
                 for (int e = 0; e < 8; ++e)
-                    dst[o++] = to_bf16_bits(wp[(size_t)(16 * j + (l & 15)) * C + 32 * s + 8 * (l >> 4) + e]);
+                    dst[o++] = to_word_bits(wp[(size_t)(16 * j + (l & 15)) * C + 32 * s + 8 * (l >> 4) + e]);
 }
 
 template <class Cfg>
@@ -180,7 +181,7 @@ __global__ __launch_bounds__(Cfg::kThreads) __attribute__((amdgpu_waves_per_eu(4
             for (int k = 0; k < KS; ++k) {
                 const bf16x8 w = *reinterpret_cast<const bf16x8 *>(wproj + ((j * KS + k) * 64 + lane) * 8);
 #pragma unroll
-                for (int i = 0; i < TF; ++i) pa[i] = mfma16(w, af[i][k], pa[i]);
+                for (int i = 0; i < TF; ++i) pa[i] = mfma16_f16(w, af[i][k], pa[i]);
             }
 #pragma unroll
             for (int i = 0; i < TF; ++i) {
@@ -217,10 +218,10 @@ __global__ __launch_bounds__(Cfg::kThreads) __attribute__((amdgpu_waves_per_eu(4
             const float4 gg = *reinterpret_cast<const float4 *>(ln_g + 16 * j + 4 * g);
             const float4 bb = *reinterpret_cast<const float4 *>(ln_b + 16 * j + 4 * g);
             const int k = j >> 1, e0 = 4 * (j & 1);
-            xf[i][k][e0 + 0] = to_bf16((xr[i][j].x - mean) * rstd * gg.x + bb.x);
-            xf[i][k][e0 + 1] = to_bf16((xr[i][j].y - mean) * rstd * gg.y + bb.y);
-            xf[i][k][e0 + 2] = to_bf16((xr[i][j].z - mean) * rstd * gg.z + bb.z);
-            xf[i][k][e0 + 3] = to_bf16((xr[i][j].w - mean) * rstd * gg.w + bb.w);
+            xf[i][k][e0 + 0] = to_half((xr[i][j].x - mean) * rstd * gg.x + bb.x);
+            xf[i][k][e0 + 1] = to_half((xr[i][j].y - mean) * rstd * gg.y + bb.y);
+            xf[i][k][e0 + 2] = to_half((xr[i][j].z - mean) * rstd * gg.z + bb.z);
+            xf[i][k][e0 + 3] = to_half((xr[i][j].w - mean) * rstd * gg.w + bb.w);
         }
     }
 
@@ -261,7 +262,7 @@ __global__ __launch_bounds__(Cfg::kThreads) __attribute__((amdgpu_waves_per_eu(4
             for (int f = 0; f < 2; ++f) {
                 const bf16x8 a = *reinterpret_cast<const bf16x8 *>(wb + (f * KS + k) * 512);
 #pragma unroll
-                for (int i = 0; i < TF; ++i) h[f][i] = mfma16(a, xf[i][k], h[f][i]);
+                for (int i = 0; i < TF; ++i) h[f][i] = mfma16_f16(a, xf[i][k], h[f][i]);
             }
         // GELU(H + b1) -> fc2 B operands (k-slot order).
         bf16x8 hb[TF];
@@ -271,13 +272,13 @@ __global__ __launch_bounds__(Cfg::kThreads) __attribute__((amdgpu_waves_per_eu(4
             for (int e = 0; e < 8; ++e) {
                 const float4 b = bq[e >> 2];
                 const float bias = (e & 3) == 0 ? b.x : (e & 3) == 1 ? b.y : (e & 3) == 2 ? b.z : b.w;
-                hb[i][e] = to_bf16(gelu(h[e >> 2][i][e & 3] + bias));
+                hb[i][e] = to_half(gelu(h[e >> 2][i][e & 3] + bias));
             }
 #pragma unroll
         for (int j = 0; j < CF; ++j) {
             const bf16x8 a = *reinterpret_cast<const bf16x8 *>(wb + (2 * KS + j) * 512);
 #pragma unroll
-            for (int i = 0; i < TF; ++i) acc[j][i] = mfma16(a, hb[i], acc[j][i]);
+            for (int i = 0; i < TF; ++i) acc[j][i] = mfma16_f16(a, hb[i], acc[j][i]);
         }
     }
 
@@ -318,10 +319,10 @@ __global__ __launch_bounds__(Cfg::kThreads) __attribute__((amdgpu_waves_per_eu(4
             const float4 gg = *reinterpret_cast<const float4 *>(next_g + c);
             const float4 bb = *reinterpret_cast<const float4 *>(next_b + c);
             bf16x4 o;
-            o[0] = to_bf16((xr[i][j].x - mean) * rstd * gg.x + bb.x);
-            o[1] = to_bf16((xr[i][j].y - mean) * rstd * gg.y + bb.y);
-            o[2] = to_bf16((xr[i][j].z - mean) * rstd * gg.z + bb.z);
-            o[3] = to_bf16((xr[i][j].w - mean) * rstd * gg.w + bb.w);
+            o[0] = to_half((xr[i][j].x - mean) * rstd * gg.x + bb.x);
+            o[1] = to_half((xr[i][j].y - mean) * rstd * gg.y + bb.y);
+            o[2] = to_half((xr[i][j].z - mean) * rstd * gg.z + bb.z);
+            o[3] = to_half((xr[i][j].w - mean) * rstd * gg.w + bb.w);
             *reinterpret_cast<bf16x4 *>(xn + (size_t)t * C + c) = o;
         }
     }

@@ -8,8 +8,9 @@
  *
  *   create:   binds the Swin-T tensors of a BFW container by name and shape
  *             (reference cuda_swin.cu:290-317), converts linear weights to
- *             bf16 and uploads them; input height/width must be multiples of
- *             4.  The model mapping need only outlive this call.
+ *             fp16 and uploads them (the forward multiplies fp16 operands
+ *             with fp32 accumulation); input height/width must be multiples
+ *             of 4.  The model mapping need only outlive this call.
  *   forward:  images [B,3,H,W] fp32 -> stage outputs
  *             [B,192,H/8,W/8], [B,384,H/16,W/16], [B,768,H/32,ceil(W/32)]
  *             fp32 NCHW; all device pointers; stream is a hipStream_t.

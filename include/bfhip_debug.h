@@ -16,9 +16,10 @@
  *
  *   bfhip_debug_window_attention
  *       Launches the production window-attention kernel on caller buffers:
- *       qkv bf16 [tokens, 3C] (token-major, tokens = batches*height*width),
+ *       qkv fp16 [tokens, 3C] (token-major, tokens = batches*height*width),
  *       qkv_bias fp32 [3C], bias_mat fp32 [heads, 49, 49] (relative-position
- *       bias already gathered), out bf16 [tokens, C].  C = 32 * heads.
+ *       bias already gathered), out fp16 [tokens, C].  C = 32 * heads.
+ *       (fp16 is the Swin path's operand format.)
  *
  *   bfhip_debug_window_attention_noalloc
  *       The same operation with no allocation: no counterpart in the
@@ -57,14 +58,14 @@ int bfhip_debug_window_map(int batches, int height, int width, int shift,
                            int *token_device, int *label_device, void *stream,
                            char *error, size_t error_cap);
 
-int bfhip_debug_window_attention(const void *qkv_bf16_device, const float *qkv_bias_device,
-                                 const float *bias_mat_device, void *out_bf16_device,
+int bfhip_debug_window_attention(const void *qkv_f16_device, const float *qkv_bias_device,
+                                 const float *bias_mat_device, void *out_f16_device,
                                  int batches, int height, int width, int channels, int heads,
                                  int shift, void *stream, char *error, size_t error_cap);
 
-int bfhip_debug_window_attention_noalloc(const void *qkv_bf16_device,
+int bfhip_debug_window_attention_noalloc(const void *qkv_f16_device,
                                          const float *qkv_bias_device,
-                                         const float *bias_mat_device, void *out_bf16_device,
+                                         const float *bias_mat_device, void *out_f16_device,
                                          int batches, int height, int width, int channels,
                                          int heads, int shift, void *stream, char *error,
                                          size_t error_cap);

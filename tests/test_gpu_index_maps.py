@@ -8,7 +8,7 @@ tests/test_index_maps.py).
   bias that is 0 on one key per query (a permutation) and -1000 elsewhere,
   softmax is exactly one-hot, so every output row must equal, bit for bit, the
   v row of the token the oracle's map puts at the permuted window position
-  (v holds small integers, exact in bf16).
+  (v holds small integers, exact in fp16, the Swin operand format).
 * Shifted-window mask: with a zero bias, each query averages exactly the keys
   of its own region (-100 elsewhere), which the oracle's labels predict; in
   unshifted blocks the padded keys (v = qkv bias) take part.
@@ -66,7 +66,7 @@ def test_window_attention_gather_scatter_bit_exact(device, shape):
     for hh in range(heads):
         bias_mat[hh, np.arange(49), perm[hh]] = 0.0
     qkv_bias = np.zeros(3 * c, np.float32)   # padded keys carry v = 0
-    q = torch.from_numpy(qkv).to(device).to(torch.bfloat16)
+    q = torch.from_numpy(qkv).to(device).to(torch.float16)
     out = bfhip.window_attention(q, torch.from_numpy(qkv_bias).to(device),
                                  torch.from_numpy(bias_mat).to(device), b, h, w, heads, shift)
     torch.cuda.synchronize()
@@ -101,7 +101,7 @@ def test_window_attention_region_mask(device, shape):
     qkv_bias = np.zeros(3 * c, np.float32)
     qkv_bias[2 * c:] = r.integers(1, 64, size=c)      # v of zero-padded keys
     bias_mat = np.zeros((heads, 49, 49), np.float32)
-    out = bfhip.window_attention(torch.from_numpy(qkv).to(device).to(torch.bfloat16),
+    out = bfhip.window_attention(torch.from_numpy(qkv).to(device).to(torch.float16),
                                  torch.from_numpy(qkv_bias).to(device),
                                  torch.from_numpy(bias_mat).to(device), b, h, w, heads, shift)
     torch.cuda.synchronize()

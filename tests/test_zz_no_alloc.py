@@ -29,7 +29,7 @@ def _inputs(seed, shape, device):
     qkv = torch.from_numpy((0.5 * r.standard_normal((tokens, 3 * c))).astype(np.float32))
     qkv_bias = torch.from_numpy((0.1 * r.standard_normal(3 * c)).astype(np.float32))
     bias_mat = torch.from_numpy((0.5 * r.standard_normal((heads, 49, 49))).astype(np.float32))
-    return (qkv.to(device).to(torch.bfloat16), qkv_bias.to(device), bias_mat.to(device))
+    return (qkv.to(device).to(torch.float16), qkv_bias.to(device), bias_mat.to(device))
 
 
 @pytest.mark.parametrize("first,second", CASES)
