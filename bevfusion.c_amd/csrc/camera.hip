@@ -49,16 +49,24 @@ namespace {
 // Tiles from sweeps of both cores on these shapes (MI355X).  DMA-fed: 64 x 128
 // for the 256-channel 3x3 convs at 32x88 and the depthnet.6 1x1, 64 x 64 at
 // level 1 (16x44), a two-wave 32 x 64 tile over 32-deep k-steps for
-// dtransform.6 (32 input channels).  Register-fed gathers (bilinear / depth
-// affine sources, 80-channel BEV maps): 128 x 128 / 64 x 64 for the lateral
-// 1x1s, narrow tiles for the 32 / 80-channel layers.
+// dtransform.6 (32 input channels), 80-column tiles for the downsample (below).
+// Register-fed gathers (bilinear / depth affine sources): 128 x 128 / 64 x 64
+// for the lateral 1x1s, a narrow tile for the 32-channel dtransform.3.
 using D256 = DmaTile<64, 128, 64, 2, 2, 2>;  // 3x3 256-channel convs and depthnet.6 at level 0
 using D64 = DmaTile<64, 64, 64, 2, 2, 2>;    // fpn_convs.1 at level 1
 using D32 = DmaTile<32, 64, 32, 1, 2, 4>;    // dtransform.6: 32 input channels
 using T256 = Tile<128, 128, 64, 2, 2>;       // lateral_convs.0
 using T64 = Tile<64, 64, 64, 2, 2>;          // lateral_convs.1
 using T32 = Tile<128, 32, 32, 4, 1>;         // dtransform.3: 32 output channels
-using T80 = Tile<64, 80, 64, 2, 1>;          // downsample: 80 channels
+// The downsample's 80-channel maps are stored channels-last with a row
+// stride of kDsPad = 96 (channels 80..95 zero, written once at create) and its
+// weights carry zero input channels 80..95, so each 3x3 tap is three 32-deep
+// k-steps on the LDS-DMA core (the zeros add exact zeros: same results as
+// the 80-channel reduction, at 1.2x the MFMA work).  Five waves of 16 or 32
+// rows x all 80 output channels per tile.
+constexpr int kDsPad = 96;
+using DDs0 = DmaTile<80, 80, 32, 5, 1, 4>;    // downsample.0 at the full BEV grid
+using DDs1 = DmaTile<160, 80, 32, 5, 1, 4>;   // downsample.1 / .2 at half resolution
 
 // FPN output conv: channels-last only, or also NCHW fp32 for the boundary.
 template <class T>
@@ -115,11 +123,15 @@ void downsample_layer(bf_cuda_camera_neck *n, int layer, float *output, hipStrea
     const int bh = (int)n->bev_h, bw = (int)n->bev_w;
     const ConvLayer &l = n->L[layer];
     switch (layer) {
-        case kDs0: run_conv<T80, 3, 3>(l, SrcNHWC{n->bp, 80, bh, bw}, nhwc_to(l, n->b0), s); break;
-        case kDs1: run_conv<T80, 3, 3>(l, SrcNHWC{n->b0, 80, bh, bw}, nhwc_to(l, n->b1), s); break;
+        case kDs0:
+            run_conv_dma<DDs0, 3>(l, n->bp, kDsPad, nullptr, 0, nhwc_to(l, n->b0, false, kDsPad), s);
+            break;
+        case kDs1:
+            run_conv_dma<DDs1, 3>(l, n->b0, kDsPad, nullptr, 0, nhwc_to(l, n->b1, false, kDsPad), s);
+            break;
         case kDs2:
-            run_conv<T80, 3, 3>(l, SrcNHWC{n->b1, 80, bh / 2, bw / 2},
-                                EpiTransposeXY{output, l.b, l.oh * l.ow, 80, l.oh, l.ow}, s);
+            run_conv_dma<DDs1, 3>(l, n->b1, kDsPad, nullptr, 0,
+                                  EpiTransposeXY{output, l.b, l.oh * l.ow, 80, l.oh, l.ow}, s);
             break;
         default: break;
     }
@@ -162,10 +174,20 @@ int build(bf_cuda_camera_neck *n, const bf_model *model, char *error, size_t cap
         if (!fold_conv(model, sp.w, sp.b, sp.bn, sp.ci, sp.co, sp.k, kCameraBnEps, fw, fb, error,
                        cap))
             return 0;
+        int ci = sp.ci;
+        if (i >= kDs0) {
+            // [Co][3x3][80] -> [Co][3x3][kDsPad], zero input channels past 80.
+            std::vector<float> padded((size_t)sp.co * 9 * kDsPad, 0.0f);
+            for (size_t r = 0; r < (size_t)sp.co * 9; ++r)
+                std::copy(fw.begin() + r * sp.ci, fw.begin() + (r + 1) * sp.ci,
+                          padded.begin() + r * kDsPad);
+            fw.swap(padded);
+            ci = kDsPad;
+        }
         wo[i] = arena.add_bf16(fw);
         bo[i] = arena.add_f32(fb);
         ConvLayer &l = n->L[i];
-        l.ci = sp.ci; l.co = sp.co; l.k = sp.k; l.stride = sp.stride; l.pad = sp.pad;
+        l.ci = ci; l.co = sp.co; l.k = sp.k; l.stride = sp.stride; l.pad = sp.pad;
         l.n = sp.batch; l.ih = sp.ih; l.iw = sp.iw;
         l.oh = (sp.ih + 2 * sp.pad - sp.k) / sp.stride + 1;
         l.ow = (sp.iw + 2 * sp.pad - sp.k) / sp.stride + 1;
@@ -190,8 +212,8 @@ int build(bf_cuda_camera_neck *n, const bf_model *model, char *error, size_t cap
     const size_t bev = (size_t)bh * bw;
     const size_t elems[14] = {
         B * 192 * hw, B * 384 * hw1, B * 768 * hw2, B * 256 * hw1, B * 256 * hw1, B * 256 * hw,
-        B * 256 * hw, B * 32 * 4 * hw, B * 64 * hw, B * 256 * hw, B * 256 * hw, 80 * bev,
-        80 * bev, 80 * (bev / 4)};
+        B * 256 * hw, B * 32 * 4 * hw, B * 64 * hw, B * 256 * hw, B * 256 * hw, kDsPad * bev,
+        kDsPad * bev, kDsPad * (bev / 4)};
     bf16 **slots[14] = {&n->p0, &n->p1, &n->p2, &n->t1, &n->f1, &n->t0, &n->f0,
                         &n->e1, &n->e2, &n->d0, &n->d1, &n->bp, &n->b0, &n->b1};
     size_t total = 0, offs[14];
@@ -202,6 +224,11 @@ int build(bf_cuda_camera_neck *n, const bf_model *model, char *error, size_t cap
     if (!hip_ok(hipMalloc(&n->acts, total), error, cap, "allocate camera activations")) return 0;
     n->resident_bytes += total;
     for (int i = 0; i < 14; ++i) *slots[i] = (bf16 *)(n->acts + offs[i]);
+    // The downsample maps' padding channels are never written by a kernel:
+    // zero them (with the rest of those maps) once.
+    if (!hip_ok(hipMemset(n->bp, 0, (size_t)(offs[13] - offs[11]) + elems[13] * 2), error, cap,
+                "clear the downsample maps"))
+        return 0;
     return 1;
 }
 
@@ -282,7 +309,7 @@ extern "C" int bf_cuda_camera_downsample_forward(bf_cuda_camera_neck *n, const f
                                                  size_t cap) {
     if (!n || !input || !output) return fail(error, cap, "invalid HIP downsample buffers");
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    pack_nhwc(input, n->bp, 1, 80, (int)(n->bev_h * n->bev_w), s);
+    pack_nhwc(input, n->bp, 1, 80, (int)(n->bev_h * n->bev_w), s, false, kDsPad);
     for (int layer : {kDs0, kDs1, kDs2}) downsample_layer(n, layer, output, s);
     return launch_ok(error, cap, "HIP downsample launch");
 }
@@ -305,7 +332,9 @@ extern "C" int bfhip_camera_profile_layer(bf_cuda_camera_neck *n, int layer, voi
         case kFpn0: fpn_conv<D256>(l, n->t0, n->f0, nullptr, s); break;
         case kDt2: case kDn0: case kDn3: depth_layer(n, layer, nullptr, nullptr, nullptr, s); break;
         case kDs0: case kDs1: downsample_layer(n, layer, nullptr, s); break;
-        case kDs2: run_conv<T80, 3, 3>(l, SrcNHWC{n->b1, 80, bh / 2, bw / 2}, nhwc_to(l, n->b0), s); break;
+        case kDs2:
+            run_conv_dma<DDs1, 3>(l, n->b1, kDsPad, nullptr, 0, nhwc_to(l, n->b0, false, kDsPad), s);
+            break;
         default: break;
     }
     return launch_ok(error, cap, "launch HIP camera profiling layer");

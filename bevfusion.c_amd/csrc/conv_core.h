@@ -414,14 +414,17 @@ struct DmaConvNHWC {
     }
 };
 
-// Row-vector conv epilogue for channels-last 16-bit maps: out[row][col] =
-// word(relu(v + bias)), Co % 4 == 0; words are bf16, or fp16 when f16 is set.
+// Row-vector conv epilogue for channels-last 16-bit maps: out[row * ld + col] =
+// word(relu(v + bias)) for col < Co, Co % 4 == 0, ld >= Co a multiple of 4
+// (a row stride above Co leaves the channels past Co untouched); words are
+// bf16, or fp16 when f16 is set.
 struct EpiConvNHWC {
     static constexpr bool kRowVector = true;
     bf16 *out;
     const float *bias;
     int M, Co;
     int f16;
+    int ld;
     __device__ ColQuad column(int col) const { return ColQuad{col, load_quad(bias, col, Co)}; }
     template <int R>
     __device__ void rows(int row0, int step, const ColQuad &c, const float4 (&v)[R]) const {
@@ -436,7 +439,7 @@ struct EpiConvNHWC {
             o[1] = to_word(y.y < 0.f ? 0.f : y.y, f16);
             o[2] = to_word(y.z < 0.f ? 0.f : y.z, f16);
             o[3] = to_word(y.w < 0.f ? 0.f : y.w, f16);
-            *reinterpret_cast<bf16x4 *>(out + (size_t)row * Co + c.col) = o;
+            *reinterpret_cast<bf16x4 *>(out + (size_t)row * ld + c.col) = o;
         }
     }
 };
@@ -481,11 +484,12 @@ struct EpiConvOut {
     }
 };
 
-// NCHW fp32 [N][C][HW] -> NHWC 16-bit words [N][HW][C] (bf16, or fp16 when
-// f16 is set) through a 64-pixel x 64-channel LDS tile (coalesced reads along
-// pixels, 16-byte writes along channels).  C must be a multiple of 8.
+// NCHW fp32 [N][C][HW] -> NHWC 16-bit words [N][HW][ld] (bf16, or fp16 when
+// f16 is set; channels C..ld-1 of each row are left untouched) through a
+// 64-pixel x 64-channel LDS tile (coalesced reads along pixels, 16-byte writes
+// along channels).  C and ld must be multiples of 8.
 static __global__ __launch_bounds__(256) void pack_nhwc_kernel(const float *x, bf16 *y, int C, int HW,
-                                                               int f16) {
+                                                               int f16, int ld) {
     __shared__ float tile[64][65];
     const int n = blockIdx.z, c0 = blockIdx.y * 64, p0 = blockIdx.x * 64;
     const int t = threadIdx.x;
@@ -497,7 +501,7 @@ static __global__ __launch_bounds__(256) void pack_nhwc_kernel(const float *x, b
         tile[cl][pl] = (c < C && p < HW) ? src[(size_t)c * HW + p] : 0.0f;
     }
     __syncthreads();
-    bf16 *dst = y + (size_t)n * HW * C;
+    bf16 *dst = y + (size_t)n * HW * ld;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const int q = t + 256 * i, pl = q >> 3, ch = (q & 7) * 8;
@@ -506,14 +510,14 @@ static __global__ __launch_bounds__(256) void pack_nhwc_kernel(const float *x, b
         bf16x8 v;
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[e] = to_word(tile[ch + e][pl], f16);
-        *reinterpret_cast<bf16x8 *>(dst + (size_t)p * C + c) = v;
+        *reinterpret_cast<bf16x8 *>(dst + (size_t)p * ld + c) = v;
     }
 }
 
 inline void pack_nhwc(const float *x, bf16 *y, int N, int C, int HW, hipStream_t s,
-                      bool f16 = false) {
+                      bool f16 = false, int ld = 0) {
     hipLaunchKernelGGL(pack_nhwc_kernel, dim3((HW + 63) / 64, (C + 63) / 64, N), dim3(256), 0, s,
-                       x, y, C, HW, (int)f16);
+                       x, y, C, HW, (int)f16, ld ? ld : C);
 }
 
 }  // namespace bfhip

@@ -96,8 +96,8 @@ inline EpiConvOut out_to(const ConvLayer &l, bf16 *nhwc, float *nchw = nullptr, 
     return EpiConvOut{nhwc, nchw, l.b, l.n * l.oh * l.ow, l.co, l.oh * l.ow, relu, (int)f16};
 }
 
-inline EpiConvNHWC nhwc_to(const ConvLayer &l, bf16 *nhwc, bool f16 = false) {
-    return EpiConvNHWC{nhwc, l.b, l.n * l.oh * l.ow, l.co, (int)f16};
+inline EpiConvNHWC nhwc_to(const ConvLayer &l, bf16 *nhwc, bool f16 = false, int ld = 0) {
+    return EpiConvNHWC{nhwc, l.b, l.n * l.oh * l.ow, l.co, (int)f16, ld ? ld : l.co};
 }
 
 }  // namespace bfhip
