@@ -1304,7 +1304,7 @@ def main():
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "fp16",  # fp16 MFMA operands, fp32 accumulation (dense fp16 peak = bf16 peak)
         "data": "synthetic (images U[0,1] ImageNet-normalised, dense depth |N(0,1)|, "
                 "random-init weights N(0,0.02), seeds 0-19)",
         "config": {"workload": "BASELINE config 5: 6x3x256x704 images -> Swin-T -> FPN -> "

@@ -1,10 +1,11 @@
 // Camera neck context: GeneralizedLSSFPN + DepthLSS head + post-LSS
 // downsample (drop-in for reference src/cuda_camera.cu).
 //
-// Every convolution is a channels-last implicit GEMM on the bf16 MFMA core with
-// BN folded into bf16 [Co][KH][KW][Ci] weights and an fp32 bias at create.
-// Boundary maps (NCHW fp32 by the ABI) are packed to NHWC bf16 once; every
-// intermediate stays NHWC bf16.  The reference's glue passes become operand
+// Every convolution is a channels-last implicit GEMM on the fp16 MFMA core
+// (fp32 accumulation) with BN folded into fp16 [Co][KH][KW][Ci] weights and an
+// fp32 bias at create.  Boundary maps (NCHW fp32 by the ABI) are packed to
+// NHWC fp16 once; every intermediate stays NHWC fp16 (16-bit words in the
+// bf16 container type).  The reference's glue passes become operand
 // gathers or epilogues, so no concat / upsample / split / transpose buffer
 // exists:
 //   lateral 1x1 convs read concat(lower, bilinear-up(upper)) taps directly;
@@ -52,12 +53,12 @@ namespace {
 // dtransform.6 (32 input channels), 80-column tiles for the downsample (below).
 // Register-fed gathers (bilinear / depth affine sources): 128 x 128 / 64 x 64
 // for the lateral 1x1s, a narrow tile for the 32-channel dtransform.3.
-using D256 = DmaTile<64, 128, 64, 2, 2, 2>;  // 3x3 256-channel convs and depthnet.6 at level 0
-using D64 = DmaTile<64, 64, 64, 2, 2, 2>;    // fpn_convs.1 at level 1
-using D32 = DmaTile<32, 64, 32, 1, 2, 4>;    // dtransform.6: 32 input channels
-using T256 = Tile<128, 128, 64, 2, 2>;       // lateral_convs.0
-using T64 = Tile<64, 64, 64, 2, 2>;          // lateral_convs.1
-using T32 = Tile<128, 32, 32, 4, 1>;         // dtransform.3: 32 output channels
+using D256 = DmaTile<64, 128, 64, 2, 2, 2, true>;  // 3x3 256-channel convs and depthnet.6 at level 0
+using D64 = DmaTile<64, 64, 64, 2, 2, 2, true>;    // fpn_convs.1 at level 1
+using D32 = DmaTile<32, 64, 32, 1, 2, 4, true>;    // dtransform.6: 32 input channels
+using T256 = Tile<128, 128, 64, 2, 2, true>;       // lateral_convs.0
+using T64 = Tile<64, 64, 64, 2, 2, true>;          // lateral_convs.1
+using T32 = Tile<128, 32, 32, 4, 1, true>;         // dtransform.3: 32 output channels
 // The downsample's 80-channel maps are stored channels-last with a row
 // stride of kDsPad = 96 (channels 80..95 zero, written once at create) and its
 // weights carry zero input channels 80..95, so each 3x3 tap is three 32-deep
@@ -65,16 +66,16 @@ using T32 = Tile<128, 32, 32, 4, 1>;         // dtransform.3: 32 output channels
 // the 80-channel reduction, at 1.2x the MFMA work).  Five waves of 16 or 32
 // rows x all 80 output channels per tile.
 constexpr int kDsPad = 96;
-using DDs0 = DmaTile<80, 80, 32, 5, 1, 4>;    // downsample.0 at the full BEV grid
-using DDs1 = DmaTile<160, 80, 32, 5, 1, 4>;   // downsample.1 / .2 at half resolution
+using DDs0 = DmaTile<80, 80, 32, 5, 1, 4, true>;    // downsample.0 at the full BEV grid
+using DDs1 = DmaTile<160, 80, 32, 5, 1, 4, true>;   // downsample.1 / .2 at half resolution
 
 // FPN output conv: channels-last only, or also NCHW fp32 for the boundary.
 template <class T>
 void fpn_conv(const ConvLayer &l, const bf16 *in, bf16 *nhwc, float *nchw, hipStream_t s) {
     if (nchw)
-        run_conv_dma<T, 3>(l, in, 256, nullptr, 0, out_to(l, nhwc, nchw), s);
+        run_conv_dma<T, 3>(l, in, 256, nullptr, 0, out_to(l, nhwc, nchw, 1, true), s);
     else
-        run_conv_dma<T, 3>(l, in, 256, nullptr, 0, nhwc_to(l, nhwc), s);
+        run_conv_dma<T, 3>(l, in, 256, nullptr, 0, nhwc_to(l, nhwc, true), s);
 }
 
 // FPN from NCHW fp32 Swin levels; FPN levels land channels-last in f0/f1 and,
@@ -84,14 +85,14 @@ void fpn_impl(bf_cuda_camera_neck *n, const float *s0, const float *s1, const fl
     const int B = (int)n->batches;
     const int h = (int)n->h, w = (int)n->w, h1 = (int)n->h1, w1 = (int)n->w1;
     const int h2 = (int)n->h2, w2 = (int)n->w2;
-    pack_nhwc(s0, n->p0, B, 192, h * w, s);
-    pack_nhwc(s1, n->p1, B, 384, h1 * w1, s);
-    pack_nhwc(s2, n->p2, B, 768, h2 * w2, s);
-    run_conv<T64, 1, 1>(n->L[kLat1], SrcNHWCUpConcat{n->p1, n->p2, 384, 768, h1, w1, h2, w2},
-                        nhwc_to(n->L[kLat1], n->t1), s);
+    pack_nhwc(s0, n->p0, B, 192, h * w, s, true);
+    pack_nhwc(s1, n->p1, B, 384, h1 * w1, s, true);
+    pack_nhwc(s2, n->p2, B, 768, h2 * w2, s, true);
+    run_conv<T64, 1, 1>(n->L[kLat1], SrcNHWCUpConcat<true>{n->p1, n->p2, 384, 768, h1, w1, h2, w2},
+                        nhwc_to(n->L[kLat1], n->t1, true), s);
     fpn_conv<D64>(n->L[kFpn1], n->t1, n->f1, out1, s);
-    run_conv<T256, 1, 1>(n->L[kLat0], SrcNHWCUpConcat{n->p0, n->f1, 192, 256, h, w, h1, w1},
-                         nhwc_to(n->L[kLat0], n->t0), s);
+    run_conv<T256, 1, 1>(n->L[kLat0], SrcNHWCUpConcat<true>{n->p0, n->f1, 192, 256, h, w, h1, w1},
+                         nhwc_to(n->L[kLat0], n->t0, true), s);
     fpn_conv<D256>(n->L[kFpn0], n->t0, n->f0, out0, s);
 }
 
@@ -103,12 +104,12 @@ void depth_layer(bf_cuda_camera_neck *n, int layer, const float *depth, float *l
     const ConvLayer &l = n->L[layer];
     switch (layer) {
         case kDt1:
-            run_conv<T32, 5, 5>(l, SrcNHWCDepthAffine{depth, n->dt0_w, n->dt0_b, 8 * h, 8 * w},
-                                nhwc_to(l, n->e1), s);
+            run_conv<T32, 5, 5>(l, SrcNHWCDepthAffine<true>{depth, n->dt0_w, n->dt0_b, 8 * h, 8 * w},
+                                nhwc_to(l, n->e1, true), s);
             break;
-        case kDt2: run_conv_dma<D32, 5>(l, n->e1, 32, nullptr, 0, nhwc_to(l, n->e2), s); break;
-        case kDn0: run_conv_dma<D256, 3>(l, n->e2, 64, n->f0, 256, nhwc_to(l, n->d0), s); break;
-        case kDn3: run_conv_dma<D256, 3>(l, n->d0, 256, nullptr, 0, nhwc_to(l, n->d1), s); break;
+        case kDt2: run_conv_dma<D32, 5>(l, n->e1, 32, nullptr, 0, nhwc_to(l, n->e2, true), s); break;
+        case kDn0: run_conv_dma<D256, 3>(l, n->e2, 64, n->f0, 256, nhwc_to(l, n->d0, true), s); break;
+        case kDn3: run_conv_dma<D256, 3>(l, n->d0, 256, nullptr, 0, nhwc_to(l, n->d1, true), s); break;
         case kDn6:
             run_conv_dma<D256, 1>(l, n->d1, 256, nullptr, 0,
                                   EpiSplitDepth{logits, context, l.b, l.n * h * w, h * w, 118, 80}, s);
@@ -124,10 +125,10 @@ void downsample_layer(bf_cuda_camera_neck *n, int layer, float *output, hipStrea
     const ConvLayer &l = n->L[layer];
     switch (layer) {
         case kDs0:
-            run_conv_dma<DDs0, 3>(l, n->bp, kDsPad, nullptr, 0, nhwc_to(l, n->b0, false, kDsPad), s);
+            run_conv_dma<DDs0, 3>(l, n->bp, kDsPad, nullptr, 0, nhwc_to(l, n->b0, true, kDsPad), s);
             break;
         case kDs1:
-            run_conv_dma<DDs1, 3>(l, n->b0, kDsPad, nullptr, 0, nhwc_to(l, n->b1, false, kDsPad), s);
+            run_conv_dma<DDs1, 3>(l, n->b0, kDsPad, nullptr, 0, nhwc_to(l, n->b1, true, kDsPad), s);
             break;
         case kDs2:
             run_conv_dma<DDs1, 3>(l, n->b1, kDsPad, nullptr, 0,
@@ -184,7 +185,7 @@ int build(bf_cuda_camera_neck *n, const bf_model *model, char *error, size_t cap
             fw.swap(padded);
             ci = kDsPad;
         }
-        wo[i] = arena.add_bf16(fw);
+        wo[i] = arena.add_f16(fw);
         bo[i] = arena.add_f32(fb);
         ConvLayer &l = n->L[i];
         l.ci = ci; l.co = sp.co; l.k = sp.k; l.stride = sp.stride; l.pad = sp.pad;
@@ -287,7 +288,7 @@ extern "C" int bf_cuda_camera_depth_forward(bf_cuda_camera_neck *n, const float 
     if (!n || !fpn0 || !depth || !logits || !context)
         return fail(error, cap, "invalid HIP depth buffers");
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    pack_nhwc(fpn0, n->f0, (int)n->batches, 256, (int)(n->h * n->w), s);
+    pack_nhwc(fpn0, n->f0, (int)n->batches, 256, (int)(n->h * n->w), s, true);
     depth_impl(n, depth, logits, context, s);
     return launch_ok(error, cap, "HIP depth launch");
 }
@@ -309,7 +310,7 @@ extern "C" int bf_cuda_camera_downsample_forward(bf_cuda_camera_neck *n, const f
                                                  size_t cap) {
     if (!n || !input || !output) return fail(error, cap, "invalid HIP downsample buffers");
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    pack_nhwc(input, n->bp, 1, 80, (int)(n->bev_h * n->bev_w), s, false, kDsPad);
+    pack_nhwc(input, n->bp, 1, 80, (int)(n->bev_h * n->bev_w), s, true, kDsPad);
     for (int layer : {kDs0, kDs1, kDs2}) downsample_layer(n, layer, output, s);
     return launch_ok(error, cap, "HIP downsample launch");
 }
@@ -326,14 +327,14 @@ extern "C" int bfhip_camera_profile_layer(bf_cuda_camera_neck *n, int layer, voi
     const ConvLayer &l = n->L[layer];
     // Same kernels and shapes as the forward entry points, on context buffers.
     switch (layer) {
-        case kLat1: run_conv<T64, 1, 1>(l, SrcNHWCUpConcat{n->p1, n->p2, 384, 768, h1, w1, h2, w2}, nhwc_to(l, n->t1), s); break;
+        case kLat1: run_conv<T64, 1, 1>(l, SrcNHWCUpConcat<true>{n->p1, n->p2, 384, 768, h1, w1, h2, w2}, nhwc_to(l, n->t1, true), s); break;
         case kFpn1: fpn_conv<D64>(l, n->t1, n->f1, nullptr, s); break;
-        case kLat0: run_conv<T256, 1, 1>(l, SrcNHWCUpConcat{n->p0, n->f1, 192, 256, h, w, h1, w1}, nhwc_to(l, n->t0), s); break;
+        case kLat0: run_conv<T256, 1, 1>(l, SrcNHWCUpConcat<true>{n->p0, n->f1, 192, 256, h, w, h1, w1}, nhwc_to(l, n->t0, true), s); break;
         case kFpn0: fpn_conv<D256>(l, n->t0, n->f0, nullptr, s); break;
         case kDt2: case kDn0: case kDn3: depth_layer(n, layer, nullptr, nullptr, nullptr, s); break;
         case kDs0: case kDs1: downsample_layer(n, layer, nullptr, s); break;
         case kDs2:
-            run_conv_dma<DDs1, 3>(l, n->b1, kDsPad, nullptr, 0, nhwc_to(l, n->b0, false, kDsPad), s);
+            run_conv_dma<DDs1, 3>(l, n->b1, kDsPad, nullptr, 0, nhwc_to(l, n->b0, true, kDsPad), s);
             break;
         default: break;
     }

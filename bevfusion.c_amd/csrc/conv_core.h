@@ -237,7 +237,9 @@ struct SrcNHWCConcat {
 
 // concat(lower, bilinear-up(upper)) read by a 1x1/s1 convolution; bilinear
 // coordinates follow the reference's fpn_concat_kernel (cuda_camera.cu:234-242)
-// and are computed once per output pixel.
+// and are computed once per output pixel.  F16: the maps hold fp16 words (and
+// the interpolated taps are stored as fp16), else bf16.
+template <bool F16 = false>
 struct SrcNHWCUpConcat {
     const bf16 *lower, *upper;
     int Cl, Cu, H, W, h, w;
@@ -267,16 +269,22 @@ struct SrcNHWCUpConcat {
         bf16x8 o;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const float top = to_f32(a[e]) * (1.0f - r.fx) + to_f32(b[e]) * r.fx;
-            const float bot = to_f32(c[e]) * (1.0f - r.fx) + to_f32(d[e]) * r.fx;
-            o[e] = to_bf16(top * (1.0f - r.fy) + bot * r.fy);
+            const float fa = F16 ? half_to_f32(a[e]) : to_f32(a[e]);
+            const float fb = F16 ? half_to_f32(b[e]) : to_f32(b[e]);
+            const float fc = F16 ? half_to_f32(c[e]) : to_f32(c[e]);
+            const float fd = F16 ? half_to_f32(d[e]) : to_f32(d[e]);
+            const float top = fa * (1.0f - r.fx) + fb * r.fx;
+            const float bot = fc * (1.0f - r.fx) + fd * r.fx;
+            o[e] = to_word(top * (1.0f - r.fy) + bot * r.fy, F16);
         }
         return o;
     }
 };
 
 // dtransform.0 fused into dtransform.3's gather: the 8 virtual channels of tap
-// (iy, ix) are relu(depth*w[c] + b[c]) from one fp32 depth value.
+// (iy, ix) are relu(depth*w[c] + b[c]) from one fp32 depth value, as fp16
+// words when F16 is set, else bf16.
+template <bool F16 = false>
 struct SrcNHWCDepthAffine {
     const float *depth;
     const float *w, *b;
@@ -289,7 +297,7 @@ struct SrcNHWCDepthAffine {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const float v = fmaf(d, w[e], 0.0f) + b[e];
-            o[e] = to_bf16(v > 0.0f ? v : 0.0f);
+            o[e] = to_word(v > 0.0f ? v : 0.0f, F16);
         }
         return o;
     }
