@@ -147,6 +147,9 @@ def swin_op_cost(stage, op, b=6):
         return 2.0 * t * c * 3 * c, t * c * 2 + 3 * c * c * 2 + t * 3 * c * 2
     if op == "attention":
         return 4.0 * win * 49 * 49 * c, t * 3 * c * 2 + t * c * 2 + heads * 49 * 49 * 4
+    if op == "wmsa":  # fused QKV projection + attention: q, k, v stay on chip
+        return (2.0 * t * c * 3 * c + 4.0 * win * 49 * 49 * c,
+                t * c * 2 + 3 * c * c * 2 + t * c * 2 + heads * 49 * 49 * 4)
     if op == "proj":
         return 2.0 * t * c * c, t * c * 2 + c * c * 2 + 2 * t * c * 4
     if op == "fc1":
@@ -217,7 +220,7 @@ def op_table(swin, neck, stream, io):
     fused = fused_stages(swin, stream)
     for st in range(4):
         depth = SWIN_STAGES[st][4]
-        for op in ("ln1", "qkv", "attention", "proj", "ln2", "fc1", "fc2", "mlp"):
+        for op in ("ln1", "qkv", "attention", "wmsa", "proj", "ln2", "fc1", "fc2", "mlp"):
             try:  # ops a stage does not launch are refused by the library
                 swin.profile_op(st, 0, op, stream)
             except bfhip.BfHipError:

@@ -183,7 +183,7 @@ SIGNATURES = {
     "bf_cuda_runtime_debug_hashes": (_i, [_vp, C.POINTER(C.c_ulonglong), C.c_char_p, _sz]),
 }
 
-SWIN_OPS = ("ln1", "qkv", "attention", "proj", "ln2", "fc1", "fc2", "merge", "mlp")
+SWIN_OPS = ("ln1", "qkv", "attention", "proj", "ln2", "fc1", "fc2", "merge", "mlp", "wmsa")
 
 MODEL_SIGNATURES = {
     "bf_model_open": (_i, [C.c_char_p, C.POINTER(_vp), C.c_char_p, _sz]),

@@ -48,6 +48,12 @@ constexpr int kDepth[4] = {2, 2, 6, 2};
 // 6x256x704).
 using MlpS0 = MlpCfg<96, 1, 4, 3, true>;
 constexpr bool kFusedMlp[4] = {true, false, false, false};
+// Stages whose QKV projection runs inside the attention kernel (one workgroup
+// per window, window_msa_kernel).  Measured at 6x256x704: stage 0 26.5 us
+// fused vs 32.8 us for QKV GEMM + attention (the 39 MB of q, k, v stay on
+// chip); stage 1 25.5 us vs 23.1 us (six waves of ~226 VGPRs per window and
+// 390 windows), so it keeps the separate kernels.
+constexpr bool kFusedWmsa[4] = {true, false, false, false};
 
 struct BlockW {
     const float *n1s, *n1b, *n2s, *n2b, *qkv_b, *proj_b, *fc1_b, *fc2_b, *bias_mat;
@@ -379,6 +385,19 @@ void block_op(bf_cuda_swin *s, int st, int b, int op, hipStream_t stream) {
                                dim3(64 * kAttnWaves), 0, stream, s->big, w.qkv_b, w.attn_term,
                                s->xn, H, W, C, heads, wy_n, wx_n, (b & 1) ? 3 : 0, items);
             break;
+        case BFHIP_SWIN_WMSA:
+            // xn -> attention output, in place: a window's rows are gathered
+            // into LDS before any wave of that window writes, and windows
+            // own disjoint token rows.
+            if (C == 96)
+                hipLaunchKernelGGL(window_msa_kernel<96>, dim3(B * wy_n * wx_n), dim3(64 * 3), 0,
+                                   stream, s->xn, w.qkv_w, w.qkv_b, w.attn_term, s->xn, H, W, wy_n,
+                                   wx_n, (b & 1) ? 3 : 0);
+            else
+                hipLaunchKernelGGL(window_msa_kernel<192>, dim3(B * wy_n * wx_n), dim3(64 * 6), 0,
+                                   stream, s->xn, w.qkv_w, w.qkv_b, w.attn_term, s->xn, H, W, wy_n,
+                                   wx_n, (b & 1) ? 3 : 0);
+            break;
         case BFHIP_SWIN_PROJ:
             linear_f16(s->xn, w.proj_w, T, C, C, EpiResidualF32{s->x, w.proj_b, C, T, C}, stream);
             break;
@@ -412,8 +431,12 @@ void block_op(bf_cuda_swin *s, int st, int b, int op, hipStream_t stream) {
 int block_ops(int st, int b, int *ops) {
     int n = 0;
     if (!kFusedMlp[st] || b == 0) ops[n++] = BFHIP_SWIN_LN1;
-    ops[n++] = BFHIP_SWIN_QKV;
-    ops[n++] = BFHIP_SWIN_ATTENTION;
+    if (kFusedWmsa[st]) {
+        ops[n++] = BFHIP_SWIN_WMSA;  // QKV + attention
+    } else {
+        ops[n++] = BFHIP_SWIN_QKV;
+        ops[n++] = BFHIP_SWIN_ATTENTION;
+    }
     if (kFusedMlp[st]) {
         ops[n++] = BFHIP_SWIN_MLP;  // proj + residual + LN2 + fc1 + fc2 + residual (+ LN1')
     } else {
@@ -461,7 +484,7 @@ extern "C" int bf_cuda_swin_forward(bf_cuda_swin *s, const float *images, float 
 extern "C" int bfhip_swin_profile_op(bf_cuda_swin *s, int stage, int block, int op, void *stream,
                                      char *error, size_t cap) {
     if (!s || stage < 0 || stage > 3 || block < 0 || block >= kDepth[stage] ||
-        op < BFHIP_SWIN_LN1 || op > BFHIP_SWIN_MLP || (op == BFHIP_SWIN_MERGE && stage > 2))
+        op < BFHIP_SWIN_LN1 || op > BFHIP_SWIN_WMSA || (op == BFHIP_SWIN_MERGE && stage > 2))
         return fail(error, cap, "invalid HIP Swin profiling op");
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     if (op == BFHIP_SWIN_MERGE) {

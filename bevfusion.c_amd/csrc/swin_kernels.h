@@ -265,69 +265,20 @@ constexpr size_t attn_term_elems(int heads, int shift) {
     return (size_t)window_types(shift) * heads * 8 * 64 * 8;
 }
 
-// One wave64 per (window, head) with head dim 32.  Window slot r = 16b + (l&15)
-// (b = 0..3, 49 tokens padded to 64) is lane l's row in every operand: the
-// S^T = K Q^T MFMAs take K and Q fragments (8 channels 8*(l>>4).. of that row)
-// straight from global memory, V goes through LDS once to become V^T, and the
-// output row of slot r is stored by the same lane.  The fp32 softmax over keys
-// runs on the accumulator registers (the 64 keys of a query sit in 16
-// registers x 4 lanes), and O^T = V^T P^T takes P straight from those
-// registers as the B operand (the key order of the k-slots is a permutation
-// shared by both operands).  Scores are q.k/sqrt(32) + rel_bias[h][i][j]
-// (- 100 across shifted regions), the latter read as one precomputed bf16 term
-// per accumulator (attn_term_kernel); keys t >= 49 get -inf.  Each wave works
-// on its own LDS slice, so waves never synchronise.
 constexpr int kAttnWaves = 4;
+constexpr int kAttnVS = 72;  // LDS row stride of V^T (16-bit words)
 
-static __global__ __launch_bounds__(256) void window_attention_kernel(
-    const bf16 *__restrict__ qkv, const float *__restrict__ qkv_bias,
-    const bf16 *__restrict__ term, bf16 *__restrict__ out, int H, int W, int C, int heads,
-    int wy_n, int wx_n, int shift, int items) {
-    constexpr int VS = 72;  // LDS row stride of V^T (bf16)
-    __shared__ __attribute__((aligned(16))) bf16 sV[kAttnWaves][32 * VS];
-
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int item = blockIdx.x * kAttnWaves + wave;
-    if (item >= items) return;  // no workgroup barrier follows
-    const int h = item % heads, win = item / heads;
-    const int wx = win % wx_n, t1 = win / wx_n, wy = t1 % wy_n, n = t1 / wy_n;
-    const int Hp = wy_n * 7, Wp = wx_n * 7;
-    const size_t ld = 3 * (size_t)C;
+// Scores, softmax and O = P V of one (window, head) whose Q and K fragments
+// are in registers (lane l: slot 16b + (l&15), the 8 k-slots of lane group
+// l>>4, any channel order both operands share), whose V^T sits in this wave's
+// LDS slice Vt[channel * kAttnVS + slot] (written by this wave), and whose score
+// terms are in add[]; stores the output row of every real slot (tok >= 0).
+__device__ __forceinline__ void attend_store(const bf16x8 (&qf)[4], const bf16x8 (&kf)[4],
+                                             const bf16x8 (&add)[8], const bf16 *Vt,
+                                             const int (&tok)[4], bf16 *out,
+                                             int C, int h, int lane) {
+    constexpr int VS = kAttnVS;
     const int l16 = lane & 15, g = lane >> 4;
-
-    // This window type's score terms: 8 coalesced 16-byte loads per lane.
-    const bf16 *tp = term + ((size_t)(window_type(wy, wx, wy_n, wx_n, shift) * heads + h) * 512 + lane) * 8;
-    bf16x8 add[8];
-#pragma unroll
-    for (int c = 0; c < 8; ++c) add[c] = *reinterpret_cast<const bf16x8 *>(tp + c * 512);
-
-    int tok[4];
-    bf16x8 qf[4], kf[4];
-    bf16 *Vt = sV[wave];
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-        tok[b] = window_token(16 * b + l16, n, wy, wx, H, W, Hp, Wp, shift);
-        bf16x8 q = {}, k = {}, v = {};
-        if (tok[b] >= 0) {
-            const bf16 *src = qkv + (size_t)tok[b] * ld + h * 32 + 8 * g;
-            q = *reinterpret_cast<const bf16x8 *>(src);
-            k = *reinterpret_cast<const bf16x8 *>(src + C);
-            v = *reinterpret_cast<const bf16x8 *>(src + 2 * C);
-        } else if (tok[b] == -1) {  // zero-padded source: q/k/v are the qkv bias
-            const float *bq = qkv_bias + h * 32 + 8 * g;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                q[e] = to_half(bq[e]);
-                k[e] = to_half(bq[C + e]);
-                v[e] = to_half(bq[2 * C + e]);
-            }
-        }
-        qf[b] = q;
-        kf[b] = k;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) Vt[(8 * g + e) * VS + 16 * b + l16] = v[e];
-    }
-
     // S^T[j][i] blocks: s[jb][ib][e] = S[i = 16ib + l16][j = 16jb + 4g + e].
     f32x4 s[4][4];
 #pragma unroll
@@ -413,5 +364,176 @@ static __global__ __launch_bounds__(256) void window_attention_kernel(
                    o[db][ib][2] * inv[ib], o[db][ib][3] * inv[ib]);
     }
 }
+
+// One wave64 per (window, head) with head dim 32.  Window slot r = 16b + (l&15)
+// (b = 0..3, 49 tokens padded to 64) is lane l's row in every operand: the
+// S^T = K Q^T MFMAs take K and Q fragments (8 channels 8*(l>>4).. of that row)
+// straight from global memory, V goes through LDS once to become V^T, and the
+// output row of slot r is stored by the same lane.  The fp32 softmax over keys
+// runs on the accumulator registers (the 64 keys of a query sit in 16
+// registers x 4 lanes), and O^T = V^T P^T takes P straight from those
+// registers as the B operand (the key order of the k-slots is a permutation
+// shared by both operands).  Scores are q.k/sqrt(32) + rel_bias[h][i][j]
+// (- 100 across shifted regions), the latter read as one precomputed fp16 term
+// per accumulator (attn_term_kernel); keys t >= 49 get -inf.  Each wave works
+// on its own LDS slice, so waves never synchronise.
+static __global__ __launch_bounds__(256) void window_attention_kernel(
+    const bf16 *__restrict__ qkv, const float *__restrict__ qkv_bias,
+    const bf16 *__restrict__ term, bf16 *__restrict__ out, int H, int W, int C, int heads,
+    int wy_n, int wx_n, int shift, int items) {
+    constexpr int VS = kAttnVS;
+    __shared__ __attribute__((aligned(16))) bf16 sV[kAttnWaves][32 * VS];
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int item = blockIdx.x * kAttnWaves + wave;
+    if (item >= items) return;  // no workgroup barrier follows
+    const int h = item % heads, win = item / heads;
+    const int wx = win % wx_n, t1 = win / wx_n, wy = t1 % wy_n, n = t1 / wy_n;
+    const int Hp = wy_n * 7, Wp = wx_n * 7;
+    const size_t ld = 3 * (size_t)C;
+    const int l16 = lane & 15, g = lane >> 4;
+
+    // This window type's score terms: 8 coalesced 16-byte loads per lane.
+    const bf16 *tp = term + ((size_t)(window_type(wy, wx, wy_n, wx_n, shift) * heads + h) * 512 + lane) * 8;
+    bf16x8 add[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) add[c] = *reinterpret_cast<const bf16x8 *>(tp + c * 512);
+
+    int tok[4];
+    bf16x8 qf[4], kf[4];
+    bf16 *Vt = sV[wave];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        tok[b] = window_token(16 * b + l16, n, wy, wx, H, W, Hp, Wp, shift);
+        bf16x8 q = {}, k = {}, v = {};
+        if (tok[b] >= 0) {
+            const bf16 *src = qkv + (size_t)tok[b] * ld + h * 32 + 8 * g;
+            q = *reinterpret_cast<const bf16x8 *>(src);
+            k = *reinterpret_cast<const bf16x8 *>(src + C);
+            v = *reinterpret_cast<const bf16x8 *>(src + 2 * C);
+        } else if (tok[b] == -1) {  // zero-padded source: q/k/v are the qkv bias
+            const float *bq = qkv_bias + h * 32 + 8 * g;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                q[e] = to_half(bq[e]);
+                k[e] = to_half(bq[C + e]);
+                v[e] = to_half(bq[2 * C + e]);
+            }
+        }
+        qf[b] = q;
+        kf[b] = k;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) Vt[(8 * g + e) * VS + 16 * b + l16] = v[e];
+    }
+
+    attend_store(qf, kf, add, Vt, tok, out, C, h, lane);
+}
+
+// Fused window MSA for the small-channel stages: QKV projection + attention in
+// one workgroup per window, one wave per head (C = 32 * heads).  The window's
+// 64 slots of LayerNorm-1 output (zero rows for padded and t >= 49 slots) are
+// gathered into LDS once; each wave projects its head's q, k and v with the
+// weights read from L2, then runs the same scores / softmax / AV tail as
+// window_attention_kernel.  The projection is computed transposed,
+// Y^T[32 ch][64 slots] = W_h X^T, so that a lane holds one slot (16b + (l&15))
+// and channels {4g + i, 16 + 4g + i} (g = l>>4, i < 4): eight channels per
+// slot, in one k-slot order that Q and K share, which is all the S = Q K^T
+// MFMAs need; V^T goes to LDS as before.  Every projected value is the fp32
+// MFMA sum over the input channels in ascending 32-wide steps plus the bias,
+// rounded once to fp16 (the separate QKV GEMM's computation), so a zero
+// (padded) row yields the bias, as in the unfused path.  The q, k, v rows
+// never reach HBM.
+template <int C>
+__global__ __launch_bounds__(64 * (C / 32)) void window_msa_kernel(
+    const bf16 *xn, const bf16 *__restrict__ wqkv, const float *__restrict__ bqkv,
+    const bf16 *__restrict__ term, bf16 *out, int H, int W, int wy_n, int wx_n, int shift) {
+    // xn and out may be the same buffer: a window's rows are all read (into
+    // LDS, before the barrier) by the workgroup that later writes them, and
+    // windows own disjoint token rows, so neither pointer is __restrict__.
+    constexpr int HEADS = C / 32, KS = C / 32, XS = C + 8;  // XS: LDS row stride (words)
+    constexpr int VS = kAttnVS;
+    __shared__ __attribute__((aligned(16))) bf16 sX[64 * XS];
+    __shared__ __attribute__((aligned(16))) bf16 sV[HEADS][32 * VS];
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = wave;
+    const int win = blockIdx.x;
+    const int wx = win % wx_n, t1 = win / wx_n, wy = t1 % wy_n, n = t1 / wy_n;
+    const int Hp = wy_n * 7, Wp = wx_n * 7;
+    const int l16 = lane & 15, g = lane >> 4;
+
+    // The window's rows, 16 bytes per thread and step.
+    for (int c = threadIdx.x; c < 64 * (C / 8); c += 64 * HEADS) {
+        const int r = c / (C / 8), q = c - r * (C / 8);
+        const int t = window_token(r, n, wy, wx, H, W, Hp, Wp, shift);
+        bf16x8 v = {};
+        if (t >= 0) v = *reinterpret_cast<const bf16x8 *>(xn + (size_t)t * C + 8 * q);
+        *reinterpret_cast<bf16x8 *>(sX + r * XS + 8 * q) = v;
+    }
+
+    // Score terms of this window type and head (global loads, in flight
+    // across the barrier).
+    const bf16 *tp = term + ((size_t)(window_type(wy, wx, wy_n, wx_n, shift) * HEADS + h) * 512 + lane) * 8;
+    bf16x8 add[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) add[c] = *reinterpret_cast<const bf16x8 *>(tp + c * 512);
+    int tok[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) tok[b] = window_token(16 * b + l16, n, wy, wx, H, W, Hp, Wp, shift);
+    __syncthreads();
+
+    // Y^T for matrix m (0 q, 1 k, 2 v) of head h: acc[cb][b] holds channels
+    // 16cb + 4g + i of slot 16b + l16.
+    auto project = [&](int m, f32x4 (&acc)[2][4]) {
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+            for (int b = 0; b < 4; ++b) acc[cb][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            bf16x8 xb[4];
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+                xb[b] = *reinterpret_cast<const bf16x8 *>(sX + (16 * b + l16) * XS + 32 * s + 8 * g);
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb) {
+                const bf16x8 wa = *reinterpret_cast<const bf16x8 *>(
+                    wqkv + (size_t)(m * C + h * 32 + 16 * cb + l16) * C + 32 * s + 8 * g);
+#pragma unroll
+                for (int b = 0; b < 4; ++b) acc[cb][b] = mfma16_f16(wa, xb[b], acc[cb][b]);
+            }
+        }
+    };
+    // fp16 words of Y^T + bias in k-slot order: e < 4 -> channel 4g + e,
+    // e >= 4 -> channel 16 + 4g + (e - 4).
+    auto words = [&](int m, const f32x4 (&acc)[2][4], bf16x8 (&f)[4]) {
+        const float *bm = bqkv + m * C + h * 32 + 4 * g;
+        const float4 b0 = *reinterpret_cast<const float4 *>(bm);
+        const float4 b1 = *reinterpret_cast<const float4 *>(bm + 16);
+        const float bias[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) f[b][e] = to_half(acc[e >> 2][b][e & 3] + bias[e]);
+    };
+
+    f32x4 acc[2][4];
+    bf16x8 qf[4], kf[4], vf[4];
+    project(0, acc);
+    words(0, acc, qf);
+    project(1, acc);
+    words(1, acc, kf);
+    project(2, acc);
+    words(2, acc, vf);
+    bf16 *Vt = sV[wave];
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int ch = (e < 4 ? 0 : 16) + 4 * g + (e & 3);
+            Vt[ch * VS + 16 * b + l16] = vf[b][e];
+        }
+    attend_store(qf, kf, add, Vt, tok, out, C, h, lane);
+}
+
 
 }  // namespace bfhip

@@ -27,7 +27,9 @@ extern "C" {
  * proj -> residual -> LN2 -> fc1 -> GELU -> fc2 -> residual (+ next block's
  * LN1) kernel of the stages that run it (stage 0); those stages launch LN1
  * only in block 0 and refuse PROJ / LN2 / FC1 / FC2, the other stages refuse
- * MLP. */
+ * MLP.  WMSA is the fused QKV projection + window attention of the stages
+ * that run it (stage 0), which refuse QKV and ATTENTION; the other stages
+ * refuse WMSA. */
 enum {
     BFHIP_SWIN_LN1 = 0,
     BFHIP_SWIN_QKV = 1,
@@ -37,7 +39,8 @@ enum {
     BFHIP_SWIN_FC1 = 5,
     BFHIP_SWIN_FC2 = 6,
     BFHIP_SWIN_MERGE = 7,
-    BFHIP_SWIN_MLP = 8
+    BFHIP_SWIN_MLP = 8,
+    BFHIP_SWIN_WMSA = 9
 };
 
 int bfhip_swin_profile_op(bf_cuda_swin *swin, int stage, int block, int op,
