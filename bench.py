@@ -141,28 +141,34 @@ def swin_op_cost(stage, op, b=6):
     h, w, c, heads, _ = SWIN_STAGES[stage]
     t = b * h * w
     win = b * ((h + 6) // 7) * ((w + 6) // 7)
+    st_b = t * (c // 64) * 8  # (mean, M2) per 64-channel group
     if op in ("ln1", "ln2"):
         return 8.0 * t * c, t * c * 4 + t * c * 2 + 8 * c
-    if op == "qkv":
-        return 2.0 * t * c * 3 * c, t * c * 2 + 3 * c * c * 2 + t * 3 * c * 2
+    if op == "qkv":  # LN1 folded: reads the fp16 residual copy and its statistics
+        return 2.0 * t * c * 3 * c, t * c * 2 + st_b + 3 * c * c * 2 + t * 3 * c * 2
     if op == "attention":
         return 4.0 * win * 49 * 49 * c, t * 3 * c * 2 + t * c * 2 + heads * 49 * 49 * 4
     if op == "wmsa":  # fused QKV projection + attention: q, k, v stay on chip
         return (2.0 * t * c * 3 * c + 4.0 * win * 49 * 49 * c,
                 t * c * 2 + 3 * c * c * 2 + t * c * 2 + heads * 49 * 49 * 4)
-    if op == "proj":
-        return 2.0 * t * c * c, t * c * 2 + c * c * 2 + 2 * t * c * 4
-    if op == "fc1":
-        return 2.0 * t * c * 4 * c, t * c * 2 + 4 * c * c * 2 + t * 4 * c * 2
-    if op == "fc2":
-        return 2.0 * t * 4 * c * c, t * 4 * c * 2 + 4 * c * c * 2 + 2 * t * c * 4
+    if op == "proj":  # residual add; writes x, its fp16 copy and statistics
+        return 2.0 * t * c * c, t * c * 2 + c * c * 2 + 2 * t * c * 4 + t * c * 2 + st_b
+    if op == "fc1":  # LN2 folded
+        return 2.0 * t * c * 4 * c, t * c * 2 + st_b + 4 * c * c * 2 + t * 4 * c * 2
+    if op == "fc2":  # residual add (+ fp16 copy and statistics, except the last block)
+        extra = 0 if stage == 3 else t * c * 2 + st_b
+        return 2.0 * t * 4 * c * c, t * 4 * c * 2 + 4 * c * c * 2 + 2 * t * c * 4 + extra
     if op == "mlp":  # fused proj -> LN2 -> fc1 -> GELU -> fc2 -> residual (+ next LN1)
         return (2.0 * t * c * c + 4.0 * t * c * 4 * c,
                 t * c * 4 * 2 + t * c * 2 * 2 + 9 * c * c * 2)
     if op == "merge":
         h2, w2 = SWIN_STAGES[stage + 1][:2]
         t2 = b * h2 * w2
-        return 2.0 * t2 * 4 * c * 2 * c, t * c * 4 + 2 * t2 * 4 * c * 2 + 8 * c * c * 2 + t2 * 2 * c * 4
+        out = t2 * 2 * c * (4 + 2) + t2 * (2 * c // 64) * 8  # x, fp16 copy, statistics
+        if stage == 0:  # LayerNorm kernel over 4C, then the reduction GEMM
+            return 2.0 * t2 * 4 * c * 2 * c, t * c * 4 + 2 * t2 * 4 * c * 2 + 8 * c * c * 2 + out
+        # LayerNorm folded: 2x2 tokens gathered from the fp16 copy
+        return 2.0 * t2 * 4 * c * 2 * c, t * c * 2 + st_b + 8 * c * c * 2 + out
     raise ValueError(op)
 
 

@@ -16,6 +16,8 @@
 
 #include "hip_common.h"
 
+#include <type_traits>
+
 namespace bfhip {
 
 // F16_: operands are fp16 words (fp16 MFMA) instead of bf16.
@@ -118,18 +120,49 @@ struct LoadRowsF32 {
 };
 
 // ------------------------------------------------------------------ epilogue
+// Optional epilogue traits: kRowStat epilogues need one float2 per output row
+// (e.g. LayerNorm statistics): thread t < BM fetches row m0 + t's inputs at
+// kernel start (Pre stat_load(row), so the loads overlap the main loop),
+// reduces them after it (float2 stat_finish(pre)) into LDS, and rows() gets
+// them; kFullRow epilogues take the whole staged fp32 tile
+// (tile<T>(sC, stride, m0, tid)) because they reduce across full rows.
+template <class E, class = void>
+struct EpiRowStat : std::false_type {};
+template <class E>
+struct EpiRowStat<E, std::void_t<decltype(E::kRowStat)>> : std::bool_constant<E::kRowStat> {};
+struct NoRowStat {};
+template <class E, bool = EpiRowStat<E>::value>
+struct EpiPre { using type = NoRowStat; };
+template <class E>
+struct EpiPre<E, true> { using type = typename E::Pre; };
+
+template <class T, class Epi>
+__device__ __forceinline__ typename EpiPre<Epi>::type epi_prefetch(const Epi &epi, int m0, int tid) {
+    static_assert(!EpiRowStat<Epi>::value || T::BM <= T::kThreads, "one thread per tile row");
+    typename EpiPre<Epi>::type pre{};
+    if constexpr (EpiRowStat<Epi>::value)
+        if (tid < T::BM) pre = epi.stat_load(m0 + tid);
+    return pre;
+}
+template <class E, class = void>
+struct EpiFullRow : std::false_type {};
+template <class E>
+struct EpiFullRow<E, std::void_t<decltype(E::kFullRow)>> : std::bool_constant<E::kFullRow> {};
+
 // Hands the accumulators of one BM x BN tile to the epilogue policy.  Row-vector
 // epilogues get the tile staged through LDS (the caller has synchronised the
 // arena) so that whole rows leave as 16-byte vectors; column-fragment
 // epilogues take the four rows of each MFMA fragment directly.
 template <class T, class Epi>
 __device__ __forceinline__ void store_tile(const f32x4 (&acc)[T::kFragM][T::kFragN], const Epi &epi,
-                                           unsigned char *smem, int m0, int n0, int tid) {
+                                           unsigned char *smem, int m0, int n0, int tid,
+                                           const typename EpiPre<Epi>::type &pre = {}) {
     const int lane = tid & 63, wave = tid >> 6;
     const int wm = wave / T::WN, wn = wave % T::WN;
     if constexpr (Epi::kRowVector) {
         constexpr int kCStride = T::BN + 4;  // floats; staggers rows across banks
         float *sC = reinterpret_cast<float *>(smem);
+        float2 *sStat = reinterpret_cast<float2 *>(smem + (size_t)T::BM * kCStride * sizeof(float));
         const int r0 = wm * T::kWaveRows + 4 * (lane >> 4), c0 = wn * T::kWaveCols + (lane & 15);
 #pragma unroll
         for (int i = 0; i < T::kFragM; ++i)
@@ -138,9 +171,16 @@ __device__ __forceinline__ void store_tile(const f32x4 (&acc)[T::kFragM][T::kFra
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
                     sC[(r0 + i * 16 + r) * kCStride + c0 + j * 16] = acc[i][j][r];
+        if constexpr (EpiRowStat<Epi>::value)
+            if (tid < T::BM) sStat[tid] = epi.stat_finish(pre);
         __syncthreads();
         constexpr int kQuads = T::BN / 4;
-        if constexpr (T::kThreads % kQuads == 0 && T::BM % (T::kThreads / kQuads) == 0) {
+        static_assert(!EpiRowStat<Epi>::value ||
+                          (T::kThreads % kQuads == 0 && T::BM % (T::kThreads / kQuads) == 0),
+                      "row-statistics epilogues need whole column quads per thread");
+        if constexpr (EpiFullRow<Epi>::value) {
+            epi.template tile<T>(sC, kCStride, m0, tid);
+        } else if constexpr (T::kThreads % kQuads == 0 && T::BM % (T::kThreads / kQuads) == 0) {
             // Each thread owns one column quad for the whole tile: the
             // epilogue's per-column state (bias) is fetched once, and all of
             // the thread's rows are handed over together so that their
@@ -151,7 +191,10 @@ __device__ __forceinline__ void store_tile(const f32x4 (&acc)[T::kFragM][T::kFra
 #pragma unroll
             for (int i = 0; i < kRows; ++i)
                 v[i] = *reinterpret_cast<const float4 *>(sC + (r + i * kStep) * kCStride + 4 * q);
-            epi.template rows<kRows>(m0 + r, kStep, epi.column(n0 + 4 * q), v);
+            if constexpr (EpiRowStat<Epi>::value)
+                epi.template rows<kRows>(m0 + r, kStep, epi.column(n0 + 4 * q), v, sStat + r);
+            else
+                epi.template rows<kRows>(m0 + r, kStep, epi.column(n0 + 4 * q), v);
         } else {
             for (int c = tid; c < T::BM * kQuads; c += T::kThreads) {
                 const int r = c / kQuads, q = c - r * kQuads;
@@ -171,7 +214,9 @@ __device__ __forceinline__ void store_tile(const f32x4 (&acc)[T::kFragM][T::kFra
 
 template <class T, class Epi>
 constexpr size_t epilogue_bytes() {
-    return Epi::kRowVector ? (size_t)T::BM * (T::BN + 4) * sizeof(float) : 0;
+    return Epi::kRowVector ? (size_t)T::BM * (T::BN + 4) * sizeof(float) +
+                                 (EpiRowStat<Epi>::value ? (size_t)T::BM * sizeof(float2) : 0)
+                           : 0;
 }
 
 // ------------------------------------------------------------------ main loop
@@ -194,6 +239,7 @@ __global__ __launch_bounds__(T::kThreads) void gemm_kernel(ALoad al, BLoad bl, E
 
     al.setup(m0, tid);
     bl.setup(n0, tid);
+    const auto pre = epi_prefetch<T>(epi, m0, tid);
 
     f32x4 acc[T::kFragM][T::kFragN];
 #pragma unroll
@@ -241,7 +287,7 @@ __global__ __launch_bounds__(T::kThreads) void gemm_kernel(ALoad al, BLoad bl, E
         __syncthreads();
     }
 
-    store_tile<T>(acc, epi, smem, m0, n0, tid);
+    store_tile<T>(acc, epi, smem, m0, n0, tid, pre);
 }
 
 // Host launcher: one workgroup per output tile.
@@ -400,6 +446,7 @@ __global__ __launch_bounds__(T::kThreads) void gemm_dma_kernel(ALoad al, BLoad b
 
     al.setup(m0, tid);
     bl.setup(n0, tid);
+    const auto pre = epi_prefetch<T>(epi, m0, tid);
 
     f32x4 acc[T::kFragM][T::kFragN];
 #pragma unroll
@@ -454,7 +501,7 @@ __global__ __launch_bounds__(T::kThreads) void gemm_dma_kernel(ALoad al, BLoad b
         }
     }
     __syncthreads();  // every wave is done with the stage buffers
-    store_tile<T>(acc, epi, smem, m0, n0, tid);
+    store_tile<T>(acc, epi, smem, m0, n0, tid, pre);
 }
 
 template <class T, class ALoad, class BLoad, class Epi>

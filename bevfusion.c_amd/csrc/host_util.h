@@ -43,6 +43,16 @@ inline uint16_t f16_bits(float f) {
     return (uint16_t)(sign | q);
 }
 
+// IEEE binary16 bits -> float (exact).
+inline float f16_value(uint16_t h) {
+    const uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+    float v;
+    if (e == 0) v = std::ldexp((float)m, -24);
+    else if (e == 31) v = m ? NAN : INFINITY;
+    else v = std::ldexp((float)(m | 0x400u), (int)e - 25);
+    return (h & 0x8000u) ? -v : v;
+}
+
 // Looks a tensor up by name and checks dtype, rank and every dimension
 // (the binding contract of reference cuda_swin.cu:57-63).
 inline const void *bind_tensor(const bf_model *m, const char *name, uint32_t dtype,

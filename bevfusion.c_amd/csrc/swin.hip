@@ -13,19 +13,30 @@
 // 16-bit words are fp16 (stored in the bf16 container type): every GEMM and
 // the attention run on the fp16 MFMA with fp32 accumulation.
 //
-// Per block: LN1 -> QKV GEMM(+bias, fp16) -> window attention ->
-// proj GEMM(+bias, += into x) -> LN2 -> fc1 GEMM(+bias, GELU, fp16) ->
-// fc2 GEMM(+bias, += into x).  Stage 0 (C = 96) runs LN2 -> fc1 -> GELU ->
-// fc2 -> residual as one fused kernel whose hidden layer stays on chip
-// (swin_mlp.h), with the proj GEMM and its residual fused in front; it also
-// writes the next block's LN1 output, so only the first block of the stage
-// launches LN1.
+//   xh   fp16 [tokens, C]   stages 1-3: fp16 copy of x, the A operand of the
+//                           LN-folded QKV / fc1 linears (ln_fold.h); two
+//                           buffers, alternating per stage, because the patch
+//                           merge reads one stage's copy while writing the next
+//   stats float2 [tokens, C/64] (mean, M2) of x per 64-channel group, written
+//                           with x, read by the LN-folded linears (two, like xh)
+//
+// Per block at stages 1-3: QKV GEMM(LN1 folded, fp16) -> window attention ->
+// proj GEMM(+bias, += into x; writes xh and stats) -> fc1 GEMM(LN2 folded,
+// GELU, fp16) -> fc2 GEMM(+bias, += into x; writes xh and stats): no
+// LayerNorm pass.  Stage 0 (C = 96) runs LN2 -> fc1 -> GELU -> fc2 ->
+// residual as one fused kernel whose hidden layer stays on chip (swin_mlp.h),
+// with the proj GEMM and its residual fused in front; it also writes the next
+// block's LN1 output, and the patch embedding's epilogue writes block 0's, so
+// stage 0 launches no LayerNorm either.  The patch merges after stages 1 and 2
+// fold their LayerNorm over 4C the same way, reading the 2x2 tokens straight
+// from xh; the one after stage 0 keeps its LayerNorm kernel.
 #include "bf_cuda_swin.h"
 #include "bfhip_debug.h"
 #include "bfhip_profile.h"
 #include "conv_core.h"
 #include "host_util.h"
 #include "linear.h"
+#include "ln_fold.h"
 #include "swin_kernels.h"
 #include "swin_mlp.h"
 
@@ -57,6 +68,9 @@ constexpr bool kFusedWmsa[4] = {true, false, false, false};
 
 struct BlockW {
     const float *n1s, *n1b, *n2s, *n2b, *qkv_b, *proj_b, *fc1_b, *fc2_b, *bias_mat;
+    // Stages 1-3: qkv_w and fc1_w hold the LN-folded weights W' (ln_fold.h),
+    // with their column sums c and shifts d.
+    const float *qkv_c, *qkv_d, *fc1_c, *fc1_d;
     const bf16 *qkv_w, *proj_w, *fc1_w, *fc2_w;
     const bf16 *mlp_w;      // fc1/fc2 packed for the fused MLP (fused stages only)
     const bf16 *mlp_proj;   // proj packed for the fused MLP (fused stages only)
@@ -65,6 +79,7 @@ struct BlockW {
 
 struct BlockOff {
     size_t n1s, n1b, n2s, n2b, qkv_b, proj_b, fc1_b, fc2_b, bias_mat, qkv_w, proj_w, fc1_w, fc2_w;
+    size_t qkv_c, qkv_d, fc1_c, fc1_d;
     size_t mlp_w, mlp_proj, attn_term;
 };
 
@@ -78,26 +93,15 @@ struct bf_cuda_swin {
     const float *patch_b, *patch_ns, *patch_nb;
     BlockW blocks[4][6];
     const float *merge_s[3], *merge_b[3], *out_s[3], *out_b[3];
-    const bf16 *merge_w[3];
+    const bf16 *merge_w[3];           // merges 1, 2: LN-folded, columns in tap-major order
+    const float *merge_c[3], *merge_d[3];
     float *x;
     bf16 *xn, *big;
+    bf16 *xh[2];
+    float2 *stats[2];
 };
 
 namespace {
-
-template <typename OutT>
-void launch_ln(int C, const float *x, OutT *y, const float *g, const float *b, int rows,
-               hipStream_t s) {
-#define BF_LN(CC)                                                                            \
-    case CC: {                                                                               \
-        const int per_block = RowLayout<CC>::RPW * 4;                                        \
-        hipLaunchKernelGGL((ln_rows_kernel<CC, OutT>), dim3((rows + per_block - 1) / per_block), \
-                           dim3(256), 0, s, x, y, g, b, rows);                               \
-        break;                                                                               \
-    }
-    switch (C) { BF_LN(96) BF_LN(192) BF_LN(384) BF_LN(768) default: break; }
-#undef BF_LN
-}
 
 void launch_merge(int C, const float *x, bf16 *y, const float *g, const float *b, int batches,
                   int H, int W, hipStream_t s) {
@@ -109,8 +113,39 @@ void launch_merge(int C, const float *x, bf16 *y, const float *g, const float *b
                            dim3(256), 0, s, x, y, g, b, batches, H, W);                      \
         break;                                                                               \
     }
-    switch (C) { BF_MERGE(96) BF_MERGE(192) BF_MERGE(384) default: break; }
+    switch (C) { BF_MERGE(96) default: break; }  // merges 1 and 2 fold their LayerNorm
 #undef BF_MERGE
+}
+
+// A linear fed by a LayerNorm, folded (ln_fold.h): W'[j][kk] =
+// fp16(g[k] W[j][k]) with k = perm(kk) (identity when perm is null),
+// c_j = sum of the fp16 W' row, d_j = b_j + sum_k beta_k W[j][k] (b may be
+// null); sums in double.
+struct FoldedLinear {
+    std::vector<uint16_t> w;
+    std::vector<float> c, d;
+};
+
+FoldedLinear fold_ln(const float *W, const float *b, const float *g, const float *beta, int N,
+                     int K, const std::vector<int> *perm) {
+    FoldedLinear f;
+    f.w.resize((size_t)N * K);
+    f.c.resize(N);
+    f.d.resize(N);
+    for (int j = 0; j < N; ++j) {
+        const float *row = W + (size_t)j * K;
+        double cs = 0.0, ds = b ? (double)b[j] : 0.0;
+        for (int kk = 0; kk < K; ++kk) {
+            const int k = perm ? (*perm)[kk] : kk;
+            const uint16_t h = f16_bits(g[k] * row[k]);
+            f.w[(size_t)j * K + kk] = h;
+            cs += (double)f16_value(h);
+            ds += (double)beta[k] * (double)row[k];
+        }
+        f.c[j] = (float)cs;
+        f.d[j] = (float)ds;
+    }
+    return f;
 }
 
 void launch_out_ln(int C, const float *x, float *out, const float *g, const float *b, int rows,
@@ -153,7 +188,7 @@ static int swin_build(bf_cuda_swin *s, const bf_model *model, size_t batches, si
     char name[224];
     size_t o_patch_w, o_patch_b, o_patch_ns, o_patch_nb;
     BlockOff off[4][6];
-    size_t o_ms[3], o_mb[3], o_mw[3], o_os[3], o_ob[3];
+    size_t o_ms[3], o_mb[3], o_mw[3], o_os[3], o_ob[3], o_mc[3] = {}, o_md[3] = {};
     {
         const float *pw = bind_f32(model, "image_backbone.patch_embed.projection.weight",
                                    {96, 3, 4, 4}, error, cap);
@@ -215,10 +250,22 @@ static int swin_build(bf_cuda_swin *s, const bf_model *model, size_t batches, si
             o.fc1_b = arena.add_f32(fc1_b, 4 * c); o.fc2_b = arena.add_f32(fc2_b, c);
             o.bias_mat = arena.add_f32(bias);
             o.attn_term = arena.add(nullptr, attn_term_elems((int)hd, (b & 1) ? 3 : 0) * 2);
-            o.qkv_w = arena.add_f16(qkv_w, (size_t)3 * c * c);
             o.proj_w = arena.add_f16(proj_w, (size_t)c * c);
-            o.fc1_w = arena.add_f16(fc1_w, (size_t)4 * c * c);
             o.fc2_w = arena.add_f16(fc2_w, (size_t)4 * c * c);
+            o.qkv_c = o.qkv_d = o.fc1_c = o.fc1_d = 0;
+            if (st == 0) {  // fused window MSA and MLP: LayerNorm kept explicit
+                o.qkv_w = arena.add_f16(qkv_w, (size_t)3 * c * c);
+                o.fc1_w = arena.add_f16(fc1_w, (size_t)4 * c * c);
+            } else {
+                const FoldedLinear fq = fold_ln(qkv_w, qkv_b, n1s, n1b, 3 * c, c, nullptr);
+                const FoldedLinear f1 = fold_ln(fc1_w, fc1_b, n2s, n2b, 4 * c, c, nullptr);
+                o.qkv_w = arena.add(fq.w.data(), fq.w.size() * 2);
+                o.qkv_c = arena.add_f32(fq.c);
+                o.qkv_d = arena.add_f32(fq.d);
+                o.fc1_w = arena.add(f1.w.data(), f1.w.size() * 2);
+                o.fc1_c = arena.add_f32(f1.c);
+                o.fc1_d = arena.add_f32(f1.d);
+            }
             o.mlp_w = o.mlp_proj = 0;
             if (kFusedMlp[st]) {
                 std::vector<uint16_t> packed((size_t)MlpS0::kChunks * MlpS0::kChunkBytes / 2);
@@ -245,7 +292,18 @@ static int swin_build(bf_cuda_swin *s, const bf_model *model, size_t batches, si
         if (!ms || !mb || !mw || !os || !ob) return 0;
         o_ms[st] = arena.add_f32(ms, 4 * c);
         o_mb[st] = arena.add_f32(mb, 4 * c);
-        o_mw[st] = arena.add_f16(mw, (size_t)8 * c * c);
+        if (st == 0) {
+            o_mw[st] = arena.add_f16(mw, (size_t)8 * c * c);
+        } else {
+            // Folded column q*C + ch reads unfold column ch*4 + q (DmaMergeRows).
+            std::vector<int> perm(4 * c);
+            for (uint32_t q = 0; q < 4; ++q)
+                for (uint32_t ch = 0; ch < c; ++ch) perm[q * c + ch] = (int)(ch * 4 + q);
+            const FoldedLinear fm = fold_ln(mw, nullptr, ms, mb, 2 * c, 4 * c, &perm);
+            o_mw[st] = arena.add(fm.w.data(), fm.w.size() * 2);
+            o_mc[st] = arena.add_f32(fm.c);
+            o_md[st] = arena.add_f32(fm.d);
+        }
         o_os[st] = arena.add_f32(os, kC[st + 1]);
         o_ob[st] = arena.add_f32(ob, kC[st + 1]);
     }
@@ -269,6 +327,8 @@ static int swin_build(bf_cuda_swin *s, const bf_model *model, size_t batches, si
                 w.fc2_b = F(o.fc2_b); w.bias_mat = F(o.bias_mat);
                 w.qkv_w = H(o.qkv_w); w.proj_w = H(o.proj_w); w.fc1_w = H(o.fc1_w);
                 w.fc2_w = H(o.fc2_w);
+                w.qkv_c = st ? F(o.qkv_c) : nullptr; w.qkv_d = st ? F(o.qkv_d) : nullptr;
+                w.fc1_c = st ? F(o.fc1_c) : nullptr; w.fc1_d = st ? F(o.fc1_d) : nullptr;
                 w.mlp_w = kFusedMlp[st] ? H(o.mlp_w) : nullptr;
                 w.mlp_proj = kFusedMlp[st] ? H(o.mlp_proj) : nullptr;
                 w.attn_term = H(o.attn_term);
@@ -276,6 +336,8 @@ static int swin_build(bf_cuda_swin *s, const bf_model *model, size_t batches, si
         for (int st = 0; st < 3; ++st) {
             s->merge_s[st] = F(o_ms[st]); s->merge_b[st] = F(o_mb[st]);
             s->merge_w[st] = H(o_mw[st]); s->out_s[st] = F(o_os[st]); s->out_b[st] = F(o_ob[st]);
+            s->merge_c[st] = st ? F(o_mc[st]) : nullptr;
+            s->merge_d[st] = st ? F(o_md[st]) : nullptr;
         }
         // Attention score terms (relative bias + shift mask, in the kernel's
         // accumulator order) from the uploaded bias matrices.
@@ -293,10 +355,14 @@ static int swin_build(bf_cuda_swin *s, const bf_model *model, size_t batches, si
             return 0;
     }
     {
-        size_t x_elems = 0, xn_elems = 0, big_elems = 0;
+        size_t x_elems = 0, xn_elems = 0, big_elems = 0, xh_elems = 0, stat_elems = 0;
         for (int st = 0; st < 4; ++st) {
             const size_t t = batches * (size_t)s->h[st] * s->w[st];
             x_elems = std::max(x_elems, t * kC[st]);
+            if (st > 0) {
+                xh_elems = std::max(xh_elems, t * kC[st]);
+                stat_elems = std::max(stat_elems, t * (kC[st] / kStatCols));
+            }
             xn_elems = std::max(xn_elems, t * kC[st]);
             big_elems = std::max(big_elems, t * 4 * kC[st]);
             if (st < 3) {
@@ -306,7 +372,7 @@ static int swin_build(bf_cuda_swin *s, const bf_model *model, size_t batches, si
             }
         }
         // The linears address their 16-bit operands through 32-bit buffer offsets.
-        if (std::max(xn_elems, big_elems) * 2 >= (size_t(1) << 31)) {
+        if (std::max(std::max(xn_elems, big_elems), xh_elems) * 2 >= (size_t(1) << 31)) {
             fail(error, cap, "Swin batch too large: %zu images exceed the 2 GiB activation limit",
                  batches);
             return 0;
@@ -314,13 +380,22 @@ static int swin_build(bf_cuda_swin *s, const bf_model *model, size_t batches, si
         const size_t x_bytes = (x_elems * 4 + 255) & ~size_t(255);
         const size_t xn_bytes = (xn_elems * 2 + 255) & ~size_t(255);
         const size_t big_bytes = (big_elems * 2 + 255) & ~size_t(255);
-        if (!hip_ok(hipMalloc(&s->acts, x_bytes + xn_bytes + big_bytes), error, cap,
-                    "allocate Swin activations"))
+        const size_t xh_bytes = (xh_elems * 2 + 255) & ~size_t(255);
+        const size_t stat_bytes = (stat_elems * sizeof(float2) + 255) & ~size_t(255);
+        const size_t total = x_bytes + xn_bytes + big_bytes + 2 * (xh_bytes + stat_bytes);
+        if (!hip_ok(hipMalloc(&s->acts, total), error, cap, "allocate Swin activations"))
             return 0;
-        s->x = (float *)s->acts;
-        s->xn = (bf16 *)(s->acts + x_bytes);
-        s->big = (bf16 *)(s->acts + x_bytes + xn_bytes);
-        s->resident_bytes += x_bytes + xn_bytes + big_bytes;
+        unsigned char *p = s->acts;
+        s->x = (float *)p;
+        s->xn = (bf16 *)(p += x_bytes);
+        s->big = (bf16 *)(p += xn_bytes);
+        p += big_bytes;
+        for (int i = 0; i < 2; ++i) {
+            s->xh[i] = (bf16 *)p;
+            s->stats[i] = (float2 *)(p + xh_bytes);
+            p += xh_bytes + stat_bytes;
+        }
+        s->resident_bytes += total;
     }
     return 1;
 }
@@ -349,8 +424,9 @@ namespace {
 // The launches of one frame, factored per op so that the forward and the
 // profiling hook (bfhip_swin_profile_op) run exactly the same kernels.
 void patch_embed(bf_cuda_swin *s, const float *images, hipStream_t stream) {
-    // 4x4/s4 conv 3->96 straight from NCHW images into NHWC tokens, then
-    // LayerNorm in place.
+    // 4x4/s4 conv 3->96 straight from NCHW images into NHWC tokens; the
+    // epilogue holds whole rows and applies the patch norm (-> x) and block
+    // 0's LN1 (-> xn).
     using T = Tile<128, 96, 32, 2, 2, true>;
     const int B = (int)s->batches;
     ConvGeom g{};
@@ -362,9 +438,21 @@ void patch_embed(bf_cuda_swin *s, const float *images, hipStream_t stream) {
     al.src = SrcNCHW{images, 3, g.IH, g.IW};
     al.g = g;
     LoadRowsBf16<T::BN, T::BK, T::kThreads> bl{s->patch_w, 48, 96, 48};
-    EpiRowsF32 epi{s->x, s->patch_b, 96, g.M, 96, 0};
+    const BlockW &b0 = s->blocks[0][0];
+    EpiPatchNorms epi{s->x, s->xn, s->patch_b, s->patch_ns, s->patch_nb, b0.n1s, b0.n1b, g.M};
     launch_gemm<T>(al, bl, epi, g.M, 96, 48, stream);
-    launch_ln<float>(96, s->x, s->x, s->patch_ns, s->patch_nb, g.M, stream);
+}
+
+// Calls f(std::integral_constant<int, C / 64>) for the channel counts of
+// stages 1-3 (the statistics groups per token).
+template <class F>
+void with_groups(int C, F &&f) {
+    switch (C) {
+        case 192: f(std::integral_constant<int, 3>{}); break;
+        case 384: f(std::integral_constant<int, 6>{}); break;
+        case 768: f(std::integral_constant<int, 12>{}); break;
+        default: break;
+    }
 }
 
 void block_op(bf_cuda_swin *s, int st, int b, int op, hipStream_t stream) {
@@ -372,13 +460,16 @@ void block_op(bf_cuda_swin *s, int st, int b, int op, hipStream_t stream) {
     const int T = B * H * W, wy_n = (H + 6) / 7, wx_n = (W + 6) / 7;
     const int items = B * wy_n * wx_n * heads;
     const BlockW &w = s->blocks[st][b];
+    bf16 *xh = s->xh[st & 1];
+    float2 *stats = s->stats[st & 1];
     switch (op) {
-        case BFHIP_SWIN_LN1:
-            launch_ln<bf16>(C, s->x, s->xn, w.n1s, w.n1b, T, stream);
-            break;
-        case BFHIP_SWIN_QKV:
-            linear_f16(s->xn, w.qkv_w, T, 3 * C, C,
-                        EpiRowsF16<false>{s->big, w.qkv_b, 3 * C, T, 3 * C}, stream);
+        case BFHIP_SWIN_QKV:  // LN1 folded
+            with_groups(C, [&](auto g) {
+                using Src = LnRows<decltype(g)::value>;
+                linear_f16(xh, w.qkv_w, T, 3 * C, C,
+                           EpiLnF16<false, Src>{s->big, w.qkv_d, w.qkv_c, Src{stats}, 3 * C, T, 3 * C},
+                           stream);
+            });
             break;
         case BFHIP_SWIN_ATTENTION:
             hipLaunchKernelGGL(window_attention_kernel, dim3((items + kAttnWaves - 1) / kAttnWaves),
@@ -399,17 +490,27 @@ void block_op(bf_cuda_swin *s, int st, int b, int op, hipStream_t stream) {
                                    wx_n, (b & 1) ? 3 : 0);
             break;
         case BFHIP_SWIN_PROJ:
-            linear_f16(s->xn, w.proj_w, T, C, C, EpiResidualF32{s->x, w.proj_b, C, T, C}, stream);
+            linear_f16(s->xn, w.proj_w, T, C, C,
+                       EpiStatsRows<false, true>{s->x, xh, stats, w.proj_b, nullptr, {}, T, C},
+                       stream);
             break;
-        case BFHIP_SWIN_LN2:
-            launch_ln<bf16>(C, s->x, s->xn, w.n2s, w.n2b, T, stream);
-            break;
-        case BFHIP_SWIN_FC1:
-            linear_f16(s->xn, w.fc1_w, T, 4 * C, C,
-                        EpiRowsF16<true>{s->big, w.fc1_b, 4 * C, T, 4 * C}, stream);
+        case BFHIP_SWIN_FC1:  // LN2 folded
+            with_groups(C, [&](auto g) {
+                using Src = LnRows<decltype(g)::value>;
+                linear_f16(xh, w.fc1_w, T, 4 * C, C,
+                           EpiLnF16<true, Src>{s->big, w.fc1_d, w.fc1_c, Src{stats}, 4 * C, T, 4 * C},
+                           stream);
+            });
             break;
         case BFHIP_SWIN_FC2:
-            linear_f16(s->big, w.fc2_w, T, C, 4 * C, EpiResidualF32{s->x, w.fc2_b, C, T, C}, stream);
+            // The last block's x feeds only the stage-3 output norm.
+            if (st == 3 && b == kDepth[3] - 1)
+                linear_f16(s->big, w.fc2_w, T, C, 4 * C, EpiResidualF32{s->x, w.fc2_b, C, T, C},
+                           stream);
+            else
+                linear_f16(s->big, w.fc2_w, T, C, 4 * C,
+                           EpiStatsRows<false, true>{s->x, xh, stats, w.fc2_b, nullptr, {}, T, C},
+                           stream);
             break;
         case BFHIP_SWIN_MLP: {
             // The next block's LN1 is fused into the epilogue; the last block
@@ -427,10 +528,12 @@ void block_op(bf_cuda_swin *s, int st, int b, int op, hipStream_t stream) {
     }
 }
 
-// The ops one block launches, in order.
+// The ops one block launches, in order (no LayerNorm launch: the patch
+// embedding writes stage 0's first LN1, the fused MLP the next ones, and the
+// other stages fold theirs into the linears).
 int block_ops(int st, int b, int *ops) {
+    (void)b;
     int n = 0;
-    if (!kFusedMlp[st] || b == 0) ops[n++] = BFHIP_SWIN_LN1;
     if (kFusedWmsa[st]) {
         ops[n++] = BFHIP_SWIN_WMSA;  // QKV + attention
     } else {
@@ -441,19 +544,48 @@ int block_ops(int st, int b, int *ops) {
         ops[n++] = BFHIP_SWIN_MLP;  // proj + residual + LN2 + fc1 + fc2 + residual (+ LN1')
     } else {
         ops[n++] = BFHIP_SWIN_PROJ;
-        ops[n++] = BFHIP_SWIN_LN2;
         ops[n++] = BFHIP_SWIN_FC1;
         ops[n++] = BFHIP_SWIN_FC2;
     }
     return n;
 }
 
+// Patch merge after stage 1 or 2 with its LayerNorm over 4C folded: the A
+// operand gathers the 2x2 tokens from xh, the statistics combine the tokens'
+// group partials, and the epilogue writes the next stage's x, xh and stats.
+// Tiles as linear_f16 picks for these (N, K).
+template <int C, class T>
+void merge_folded(bf_cuda_swin *s, int st, hipStream_t stream) {
+    const int B = (int)s->batches, H = s->h[st], W = s->w[st];
+    const int T2 = B * s->h[st + 1] * s->w[st + 1];
+    DmaMergeRows<T::BM, T::BK, T::kThreads, C> al{};
+    al.base = s->xh[st & 1];
+    al.batches = B;
+    al.H = H;
+    al.W = W;
+    DmaRowsBf16<T::BN, T::BK, T::kThreads> bl{s->merge_w[st], 4 * C, 2 * C, 4 * C};
+    const int nx = (st + 1) & 1;
+    using Src = LnMerge<C / kStatCols>;
+    EpiStatsRows<true, false, Src> epi{s->x,          s->xh[nx],     s->stats[nx],
+                                       s->merge_d[st], s->merge_c[st], Src{s->stats[st & 1], H, W},
+                                       T2,            2 * C};
+    launch_gemm_dma<T>(al, bl, epi, T2, 2 * C, 4 * C, stream);
+}
+
 void merge_op(bf_cuda_swin *s, int st, hipStream_t stream) {
     const int B = (int)s->batches, C = kC[st];
     const int T2 = B * s->h[st + 1] * s->w[st + 1];
-    launch_merge(C, s->x, s->xn, s->merge_s[st], s->merge_b[st], B, s->h[st], s->w[st], stream);
-    linear_f16(s->xn, s->merge_w[st], T2, 2 * C, 4 * C,
-                EpiRowsF32{s->x, nullptr, 2 * C, T2, 2 * C, 0}, stream);
+    if (st == 0) {
+        launch_merge(C, s->x, s->xn, s->merge_s[st], s->merge_b[st], B, s->h[st], s->w[st], stream);
+        linear_f16(s->xn, s->merge_w[st], T2, 2 * C, 4 * C,
+                   EpiStatsRows<false, false>{s->x, s->xh[1], s->stats[1], nullptr, nullptr, {}, T2,
+                                              2 * C},
+                   stream);
+    } else if (st == 1) {
+        merge_folded<192, DmaTile<64, 64, 64, 2, 2, 2, true>>(s, st, stream);
+    } else {
+        merge_folded<384, DmaTile<64, 64, 128, 2, 2, 3, true>>(s, st, stream);
+    }
 }
 
 }  // namespace

@@ -1,4 +1,4 @@
-// Swin-T building blocks on gfx950: row LayerNorms, the patch-merge gather,
+// Swin-T building blocks on gfx950: the patch-merge gather with its LayerNorm,
 // the stage-output LayerNorm with NHWC->NCHW store, and batched shifted-
 // window attention on MFMA.  The Swin path's 16-bit operands (LayerNorm
 // outputs, QKV, attention terms and output, MLP hidden, weights) are fp16
@@ -30,45 +30,6 @@ __device__ __forceinline__ void store4(bf16 *p, float a, float b, float c, float
     bf16x4 v;  // fp16 words
     v[0] = to_half(a); v[1] = to_half(b); v[2] = to_half(c); v[3] = to_half(d);
     *reinterpret_cast<bf16x4 *>(p) = v;
-}
-
-// y = LN(x) * g + b over rows of C (eps 1e-5, two-pass statistics held in
-// registers).  In-place (y == x) is safe: a row is fully read before written.
-template <int C, typename OutT>
-__global__ __launch_bounds__(256) void ln_rows_kernel(const float *x, OutT *y, const float *g,
-                                                      const float *b, int rows) {
-    using L = RowLayout<C>;
-    const int lane = threadIdx.x & 63;
-    const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-    const int sub = lane / L::LPR, li = lane % L::LPR;
-    const int row = wave * L::RPW + sub;
-    const bool ok = row < rows;
-    float4 v[L::PER];
-    float s = 0.0f;
-#pragma unroll
-    for (int p = 0; p < L::PER; ++p) {
-        v[p] = ok ? reinterpret_cast<const float4 *>(x + (size_t)row * C)[li + p * L::LPR]
-                  : make_float4(0.f, 0.f, 0.f, 0.f);
-        s += (v[p].x + v[p].y) + (v[p].z + v[p].w);
-    }
-    const float mean = group_sum<L::LPR>(s) * (1.0f / C);
-    float q = 0.0f;
-#pragma unroll
-    for (int p = 0; p < L::PER; ++p) {
-        const float a = v[p].x - mean, bb = v[p].y - mean, c = v[p].z - mean, d = v[p].w - mean;
-        q += (a * a + bb * bb) + (c * c + d * d);
-    }
-    const float rstd = rsqrtf(group_sum<L::LPR>(q) * (1.0f / C) + 1e-5f);
-    if (!ok) return;
-#pragma unroll
-    for (int p = 0; p < L::PER; ++p) {
-        const int c4 = (li + p * L::LPR) * 4;
-        const float4 gg = *reinterpret_cast<const float4 *>(g + c4);
-        const float4 bb = *reinterpret_cast<const float4 *>(b + c4);
-        store4(y + (size_t)row * C + c4, (v[p].x - mean) * rstd * gg.x + bb.x,
-               (v[p].y - mean) * rstd * gg.y + bb.y, (v[p].z - mean) * rstd * gg.z + bb.z,
-               (v[p].w - mean) * rstd * gg.w + bb.w);
-    }
 }
 
 // Patch merging: output row (n, oy, ox) is the 2x2 nn.Unfold of x[n,H,W,C]
