@@ -91,6 +91,16 @@ void run_conv_dma(const ConvLayer &l, const bf16 *a, int c0, const bf16 *b, int 
     launch_gemm_dma<T>(al, bl, epi, g.M, l.co, g.K, s);
 }
 
+// Wave-specialised LDS-DMA pipeline (gemm_spec_kernel) for the same convs.
+template <class T, int K, class Epi>
+void run_conv_spec(const ConvLayer &l, const bf16 *a, int c0, const bf16 *b, int c1, const Epi &epi,
+                   hipStream_t s) {
+    const ConvGeom g = geom_of(l);
+    DmaConvNHWC<T::BM, T::BK, kWave, K, K> al{a, b, c0, c1, g};
+    DmaRowsBf16<T::BN, T::BK, kWave> bl{l.w, g.K, l.co, g.K};
+    launch_gemm_spec<T>(al, bl, epi, g.M, l.co, g.K, s);
+}
+
 inline EpiConvOut out_to(const ConvLayer &l, bf16 *nhwc, float *nchw = nullptr, int relu = 1,
                          bool f16 = false) {
     return EpiConvOut{nhwc, nchw, l.b, l.n * l.oh * l.ow, l.co, l.oh * l.ow, relu, (int)f16};

@@ -321,7 +321,7 @@ struct DmaTile {
     static constexpr int kFragM = kWaveRows / 16, kFragN = kWaveCols / 16;
     static_assert(BK == 32 || BK == 64 || BK == 128, "swizzle covers BK of 32, 64 or 128");
     static_assert(kWaveRows % 16 == 0 && kWaveCols % 16 == 0, "wave tile must be 16-aligned");
-    static_assert(kStages >= 2 && kStages <= 4, "2 to 4 stages");
+    static_assert(kStages >= 2 && kStages <= 8, "2 to 8 stages");
 };
 
 template <int BK>
@@ -415,12 +415,15 @@ struct DmaRowsBf16 {
     }
 };
 
+// Wait until at most n stages of P instructions are outstanding.  The counter
+// holds 63 at most: a larger bound is clamped, which waits for more stages
+// than needed (always safe).
 template <int N>
-struct DmaWait {  // wait until at most n stages of P instructions are outstanding
+struct DmaWait {
     template <int P>
     __device__ static void stages(int n) {
         if constexpr (N > 0) {
-            if (n >= N) { wait_vmcnt<N * P>(); return; }
+            if (n >= N) { wait_vmcnt<(N * P > 63 ? 63 : N * P)>(); return; }
             DmaWait<N - 1>::template stages<P>(n);
         } else {
             wait_vmcnt<0>();
@@ -510,6 +513,115 @@ inline void launch_gemm_dma(const ALoad &al, const BLoad &bl, const Epi &epi, in
     const int tiles_m = (M + T::BM - 1) / T::BM, tiles_n = (N + T::BN - 1) / T::BN;
     hipLaunchKernelGGL((gemm_dma_kernel<T, ALoad, BLoad, Epi>), dim3(tiles_m * tiles_n),
                        dim3(T::kThreads), 0, stream, al, bl, epi, M, N, K, tiles_n);
+}
+
+// ======================================== wave-specialised LDS-DMA pipeline
+// Same tile, LDS image, loaders and epilogues as gemm_dma_kernel, plus one
+// loader wave that issues every DMA; the WM x WN compute waves never issue a
+// vector-memory instruction in the main loop.  In gemm_dma_kernel each wave
+// issues its share of the next stage and then runs its MFMAs: when the fetch
+// path is the bottleneck the issue itself stalls until the texture unit takes
+// the request, and the SIMD's matrix core idles meanwhile, so fetch and math
+// add up instead of overlapping (measured on MI355X with a 128 x 64 tile, K =
+// 1536: 5.8 us of DMA alone, 11.8 us with the MFMAs).  With the issue moved
+// to its own wave, the stall holds that wave only.
+//
+// Per k-step kt both sides meet at one barrier: the loader has waited for
+// stage kt to land, the compute waves have finished reading stage kt - 1, so
+// after it the loader refills that buffer with stage kt + S - 1 while the
+// compute waves multiply stage kt.  The loader then takes part in the
+// epilogue's barriers (it has no rows of its own) and exits.
+// ALoad / BLoad are instantiated for THREADS = kWave and set up with the
+// loader's lane index.
+template <class T, class ALoad, class BLoad, class Epi>
+__global__ __launch_bounds__(T::kThreads + kWave) void gemm_spec_kernel(ALoad al, BLoad bl, Epi epi,
+                                                                        int M, int N, int K,
+                                                                        int tiles_n) {
+    constexpr int S = T::kStages;
+    constexpr int kA = T::BM * T::BK, kB = T::BN * T::BK;  // elements per stage
+    constexpr size_t kABBytes = (size_t)S * (kA + kB) * sizeof(bf16);
+    constexpr size_t kCBytes = epilogue_bytes<T, Epi>();
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[kABBytes > kCBytes ? kABBytes : kCBytes];
+    bf16 *sA = reinterpret_cast<bf16 *>(smem);
+    bf16 *sB = sA + S * kA;
+
+    const int pid = xcd_swizzle((int)blockIdx.x, (int)gridDim.x);
+    const int m0 = (pid / tiles_n) * T::BM, n0 = (pid % tiles_n) * T::BN;
+    const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nk = (K + T::BK - 1) / T::BK;
+
+    if (wave == T::WM * T::WN) {  // loader (wave-uniform branch)
+        al.setup(m0, lane);
+        bl.setup(n0, lane);
+        constexpr int P = ALoad::kIssue + BLoad::kIssue;
+#pragma unroll
+        for (int st = 0; st < S - 1; ++st)
+            if (st < nk) {
+                al.issue(sA + st * kA, st * T::BK);
+                bl.issue(sB + st * kB, st * T::BK);
+            }
+        for (int kt = 0; kt < nk; ++kt) {
+            const int ahead = nk - 1 - kt;  // stages issued after this one
+            DmaWait<S - 2>::template stages<P>(ahead < S - 2 ? ahead : S - 2);
+            lds_barrier();
+            const int nxt = kt + S - 1;
+            if (nxt < nk) {
+                al.issue(sA + (nxt % S) * kA, nxt * T::BK);
+                bl.issue(sB + (nxt % S) * kB, nxt * T::BK);
+            }
+        }
+        __syncthreads();  // the compute waves' end-of-loop barrier
+        if constexpr (Epi::kRowVector) __syncthreads();  // store_tile's staging barrier
+        return;
+    }
+
+    const int wm = wave / T::WN, wn = wave % T::WN;
+    const auto pre = epi_prefetch<T>(epi, m0, tid);
+    f32x4 acc[T::kFragM][T::kFragN];
+#pragma unroll
+    for (int i = 0; i < T::kFragM; ++i)
+#pragma unroll
+        for (int j = 0; j < T::kFragN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int swz = dma_swizzle<T::BK>(lane & 15);
+    const int a_row = (wm * T::kWaveRows + (lane & 15)) * T::BK;
+    const int b_row = (wn * T::kWaveCols + (lane & 15)) * T::BK;
+    constexpr int kSteps = T::BK / 32;
+    int koff[kSteps];
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) koff[s] = 8 * ((4 * s + (lane >> 4)) ^ swz);
+
+    for (int kt = 0; kt < nk; ++kt) {
+        lds_barrier();
+        const bf16 *a = sA + (kt % S) * kA + a_row;
+        const bf16 *b = sB + (kt % S) * kB + b_row;
+#pragma unroll
+        for (int s = 0; s < kSteps; ++s) {
+            bf16x8 af[T::kFragM], bfr[T::kFragN];
+#pragma unroll
+            for (int i = 0; i < T::kFragM; ++i)
+                af[i] = *reinterpret_cast<const bf16x8 *>(a + i * 16 * T::BK + koff[s]);
+#pragma unroll
+            for (int j = 0; j < T::kFragN; ++j)
+                bfr[j] = *reinterpret_cast<const bf16x8 *>(b + j * 16 * T::BK + koff[s]);
+#pragma unroll
+            for (int i = 0; i < T::kFragM; ++i)
+#pragma unroll
+                for (int j = 0; j < T::kFragN; ++j) acc[i][j] = mfma16_as<T::kF16>(af[i], bfr[j], acc[i][j]);
+        }
+    }
+    __syncthreads();  // every wave is done with the stage buffers
+    store_tile<T>(acc, epi, smem, m0, n0, tid, pre);
+}
+
+// Loaders for the spec kernel are built with THREADS = kWave.
+template <class T, class ALoad, class BLoad, class Epi>
+inline void launch_gemm_spec(const ALoad &al, const BLoad &bl, const Epi &epi, int M, int N, int K,
+                             hipStream_t stream) {
+    static_assert(ALoad::kWaves == 1 && BLoad::kWaves == 1, "loaders of one wave");
+    const int tiles_m = (M + T::BM - 1) / T::BM, tiles_n = (N + T::BN - 1) / T::BN;
+    hipLaunchKernelGGL((gemm_spec_kernel<T, ALoad, BLoad, Epi>), dim3(tiles_m * tiles_n),
+                       dim3(T::kThreads + kWave), 0, stream, al, bl, epi, M, N, K, tiles_n);
 }
 
 // ---------------------------------------------------------------- epilogues
