@@ -646,14 +646,31 @@ def calibrate_leg(dev):
         lds = lgrid * 256 * liters * 16 / t
         out["lds_read_tb_s"] = round(lds / 1e12, 2)
         out["lds_read_b_per_clk_per_cu_at_2_4ghz"] = round(lds / 256 / 2.4e9, 1)
+        # MFMA fed from LDS as in the GEMM cores: 4 workgroups of 8 waves per
+        # CU; 64 x 64 wave tiles with random or constant fp16 operands, and
+        # 32 x 32 wave tiles (LDS-heavy) for the fragment-read bandwidth.
+        mgrid, miters = 1024, 2000
+        for kind, fm, key in (("mfma_lds", 4, "mfma16_lds_random_tflops"),
+                              ("mfma_lds_flat", 4, "mfma16_lds_constant_tflops"),
+                              ("mfma_lds_narrow", 2, "mfma16_lds_random_32x32_tflops")):
+            t = timed(lambda kind=kind: bfhip.calibrate(kind, mgrid, miters, dst=sink, stream=stream), 5)
+            waves = mgrid * 8 * miters
+            out[key] = round(waves * 2 * fm * fm * 16384 / t / 1e12, 1)
+            if fm == 2:
+                lds_f = waves * 2 * (2 * fm) * 1024 / t
+                out["lds_fragment_read_tb_s"] = round(lds_f / 1e12, 1)
+                out["lds_fragment_read_b_per_clk_per_cu_at_2_4ghz"] = round(lds_f / 256 / 2.4e9, 1)
         src = torch.zeros(256 << 20, device=dev)  # 1 GiB
         dst = torch.empty_like(src)
         t = timed(lambda: bfhip.calibrate("copy", 4096, src=src, dst=dst, stream=stream), 5)
         out["copy_gb_s"] = round(2 * src.numel() * 4 / t / 1e9, 1)
         del src, dst
     out["note"] = ("MFMA kernels: 2 workgroups of 4 waves per CU, 8 independent accumulator "
-                   "chains per wave; LDS: 4 workgroups per CU, conflict-free 16-byte reads issued "
-                   "8 at a time; copy: 1 GiB float4, read + write bytes")
+                   "chains per wave, register operands; LDS: 4 workgroups per CU, conflict-free "
+                   "16-byte reads issued 8 at a time with a VALU add per read; mfma16_lds_*: 4 "
+                   "workgroups of 8 waves per CU reading fp16 fragments from LDS each step as the "
+                   "GEMM cores do (random operands draw more power, hence a lower clock, than "
+                   "constant ones); copy: 1 GiB float4, read + write bytes")
     return out
 
 

@@ -316,7 +316,8 @@ def gemm_f32(x, w, b=None, relu=False, out=None, stream=None):
     return out
 
 
-CALIB_KINDS = ("empty", "mfma16", "mfma32", "lds", "copy")
+CALIB_KINDS = ("empty", "mfma16", "mfma32", "lds", "copy", "mfma_lds", "mfma_lds_flat",
+               "mfma_lds_narrow")
 
 
 def calibrate(kind, grid, iters=0, src=None, dst=None, stream=None):

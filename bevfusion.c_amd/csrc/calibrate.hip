@@ -1,6 +1,8 @@
 // Machine calibration kernels for the roofline discussion: launch cost, the
 // sustained bf16 MFMA rate of the two instruction shapes the contractions
-// use, LDS read bandwidth and device-memory copy bandwidth.  Each kernel
+// use, the fp16 MFMA rate when the operands come from LDS as in the GEMM
+// cores (with random or constant operand values), LDS read bandwidth and
+// device-memory copy bandwidth.  Each kernel
 // does a known amount of work; the caller times it with HIP events and turns
 // the count into a rate.  Nothing here is on the product path.
 #include "bfhip_profile.h"
@@ -92,6 +94,67 @@ __global__ __launch_bounds__(256) void calib_lds_kernel(int iters, float *sink, 
     if (flag) sink[blockIdx.x * blockDim.x + t] = acc.x + acc.y + acc.z + acc.w;
 }
 
+// MFMA fed from LDS the way the GEMM main loops feed it: WAVES waves, each
+// owning an (FM*16) x (FN*16) tile, read their A and B fragments for every
+// 32-deep step from a 64-deep swizzled LDS tile (conflict-free
+// ds_read_b128), then issue FM*FN v_mfma_f32_16x16x32_f16.  RANDOM fills the
+// tiles with hashed fp16 values in [-1, 1); otherwise with a few small
+// integers.  The matrix cores draw more power on toggling operand bits, so
+// the random variant is the rate real activations and weights can sustain.
+// Per workgroup and iteration: 2 * FM * FN MFMAs and 2 * (FM + FN) KiB of
+// LDS reads per wave.
+template <int FM, int FN, int WAVES, bool RANDOM>
+__global__ __launch_bounds__(WAVES * 64) void calib_lds_mfma_kernel(int iters, float *sink, int flag) {
+    constexpr int kRows = 128, kBK = 64;
+    __shared__ __attribute__((aligned(1024))) bf16 sA[kRows * kBK], sB[kRows * kBK];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int i = tid; i < kRows * kBK; i += WAVES * 64) {
+        if (RANDOM) {
+            uint32_t h = (uint32_t)i * 2654435761u + blockIdx.x * 97u;
+            h ^= h >> 13;
+            h *= 0x5bd1e995u;
+            h ^= h >> 15;
+            sA[i] = to_half((float)(h & 0xffffu) * (1.0f / 32768.0f) - 1.0f);
+            sB[i] = to_half((float)(h >> 16) * (1.0f / 32768.0f) - 1.0f);
+        } else {
+            sA[i] = to_half((float)(i & 7));
+            sB[i] = to_half((float)(i & 3));
+        }
+    }
+    __syncthreads();
+    const int swz = lane & 7;  // 64-deep tile swizzle of the LDS-DMA core
+    const int a_row = ((wave * 16) % (kRows - FM * 16 + 16) + (lane & 15)) * kBK;
+    const int b_row = ((wave * 32) % (kRows - FN * 16 + 16) + (lane & 15)) * kBK;
+    int koff[2];
+    for (int st = 0; st < 2; ++st) koff[st] = 8 * ((4 * st + (lane >> 4)) ^ swz);
+    f32x4 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            bf16x8 af[FM], bfr[FN];
+#pragma unroll
+            for (int i = 0; i < FM; ++i) af[i] = *reinterpret_cast<const bf16x8 *>(sA + a_row + i * 16 * kBK + koff[st]);
+#pragma unroll
+            for (int j = 0; j < FN; ++j) bfr[j] = *reinterpret_cast<const bf16x8 *>(sB + b_row + j * 16 * kBK + koff[st]);
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j) acc[i][j] = mfma16_f16(af[i], bfr[j], acc[i][j]);
+        }
+        asm volatile("" ::: "memory");
+    }
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) t += acc[i][j][0];
+    if (flag) sink[blockIdx.x * blockDim.x + tid] = t;
+}
+
 // y = x over n float4 (grid-stride): 2 * 16 * n bytes of device memory traffic.
 __global__ __launch_bounds__(256) void calib_copy_kernel(const float4 *__restrict__ x,
                                                          float4 *__restrict__ y, size_t n) {
@@ -125,6 +188,22 @@ extern "C" int bfhip_calibrate(int kind, int grid, int iters, const void *src, v
                 hipLaunchKernelGGL(calib_mfma32_kernel, dim3(grid), dim3(256), 0, s, iters, sink, flag);
             else
                 hipLaunchKernelGGL(calib_lds_kernel, dim3(grid), dim3(256), 0, s, iters, sink, flag);
+            break;
+        }
+        case BFHIP_CALIB_MFMA_LDS:
+        case BFHIP_CALIB_MFMA_LDS_FLAT:
+        case BFHIP_CALIB_MFMA_LDS_NARROW: {
+            const size_t need = (size_t)grid * 512 * sizeof(float);
+            const int flag = sink && bytes >= need ? 1 : 0;
+            if (kind == BFHIP_CALIB_MFMA_LDS)
+                hipLaunchKernelGGL((calib_lds_mfma_kernel<4, 4, 8, true>), dim3(grid), dim3(512), 0, s,
+                                   iters, sink, flag);
+            else if (kind == BFHIP_CALIB_MFMA_LDS_FLAT)
+                hipLaunchKernelGGL((calib_lds_mfma_kernel<4, 4, 8, false>), dim3(grid), dim3(512), 0, s,
+                                   iters, sink, flag);
+            else
+                hipLaunchKernelGGL((calib_lds_mfma_kernel<2, 2, 8, true>), dim3(grid), dim3(512), 0, s,
+                                   iters, sink, flag);
             break;
         }
         case BFHIP_CALIB_COPY:

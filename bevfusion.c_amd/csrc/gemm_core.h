@@ -119,6 +119,22 @@ struct LoadRowsF32 {
     }
 };
 
+// Workgroup barrier for LDS traffic: waits for this wave's own LDS accesses
+// (lgkmcnt), then s_barrier; unlike __syncthreads it leaves global loads and
+// LDS-DMA in flight (vmcnt), so a prefetch survives it.  The lgkmcnt wait is
+// what makes a stage buffer free after the barrier: the compiler may sink the
+// MFMAs that consume a wave's last fragment reads below the barrier, leaving
+// those reads outstanding, and another wave's next DMA into that buffer could
+// overtake them.  The empty asm statements keep the compiler from moving LDS
+// accesses across it.  s_waitcnt encoding (gfx9): vmcnt 63, expcnt 7,
+// lgkmcnt 0.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // ------------------------------------------------------------------ epilogue
 // Optional epilogue traits: kRowStat epilogues need one float2 per output row
 // (e.g. LayerNorm statistics): thread t < BM fetches row m0 + t's inputs at
@@ -173,7 +189,7 @@ __device__ __forceinline__ void store_tile(const f32x4 (&acc)[T::kFragM][T::kFra
                     sC[(r0 + i * 16 + r) * kCStride + c0 + j * 16] = acc[i][j][r];
         if constexpr (EpiRowStat<Epi>::value)
             if (tid < T::BM) sStat[tid] = epi.stat_finish(pre);
-        __syncthreads();
+        lds_barrier();  // LDS only: prefetches in flight stay in flight
         constexpr int kQuads = T::BN / 4;
         static_assert(!EpiRowStat<Epi>::value ||
                           (T::kThreads % kQuads == 0 && T::BM % (T::kThreads / kQuads) == 0),
@@ -337,21 +353,6 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// Workgroup barrier for LDS traffic: waits for this wave's own LDS accesses
-// (lgkmcnt), then s_barrier; unlike __syncthreads it leaves global loads and
-// LDS-DMA in flight (vmcnt), so a prefetch survives it.  The lgkmcnt wait is
-// what makes a stage buffer free after the barrier: the compiler may sink the
-// MFMAs that consume a wave's last fragment reads below the barrier, leaving
-// those reads outstanding, and another wave's next DMA into that buffer could
-// overtake them.  The empty asm statements keep the compiler from moving LDS
-// accesses across it.  s_waitcnt encoding (gfx9): vmcnt 63, expcnt 7,
-// lgkmcnt 0.
-__device__ __forceinline__ void lds_barrier() {
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_waitcnt(0xC07F);
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-}
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, uint32_t bytes) {
     // Raw buffer, 32-bit data format: offsets at or past `bytes` read as zero.

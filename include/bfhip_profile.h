@@ -25,11 +25,13 @@ extern "C" {
 /* Ops of one Swin block, in forward order; MERGE is the patch merge that
  * follows stage `stage` (0..2; `block` is ignored).  MLP is the fused
  * proj -> residual -> LN2 -> fc1 -> GELU -> fc2 -> residual (+ next block's
- * LN1) kernel of the stages that run it (stage 0); those stages launch LN1
- * only in block 0 and refuse PROJ / LN2 / FC1 / FC2, the other stages refuse
- * MLP.  WMSA is the fused QKV projection + window attention of the stages
- * that run it (stage 0), which refuse QKV and ATTENTION; the other stages
- * refuse WMSA. */
+ * LN1) kernel of the stages that run it (stage 0), which refuse PROJ / FC1 /
+ * FC2; the other stages refuse MLP.  WMSA is the fused QKV projection +
+ * window attention of the stages that run it (stage 0), which refuse QKV and
+ * ATTENTION; the other stages refuse WMSA.  No stage launches LN1 or LN2 any
+ * more (the patch embedding and the fused MLP write stage 0's LN1, and stages
+ * 1-3 fold both norms into their QKV and fc1 linears), so both are refused;
+ * the ids stay reserved. */
 enum {
     BFHIP_SWIN_LN1 = 0,
     BFHIP_SWIN_QKV = 1,
@@ -77,16 +79,26 @@ int bfhip_camera_profile_layer_io(bf_cuda_camera_neck *neck, int layer, const fl
  *   MFMA32  same with v_mfma_f32_32x32x16_bf16 (32768 flops each);
  *   LDS     256 threads, each `iters` (a multiple of 8) conflict-free 16-byte
  *           LDS reads, issued 8 at a time;
- *   COPY    a float4 copy of `bytes` from src to dst (16-byte aligned).
- * For MFMA16/MFMA32/LDS, dst may receive one float per thread when `bytes`
- * covers grid * 256 floats (it keeps the work observable); otherwise nothing
- * is stored. */
+ *   COPY    a float4 copy of `bytes` from src to dst (16-byte aligned);
+ *   MFMA_LDS         512 threads (8 waves); per iteration each wave reads
+ *                    8 KiB of fragments from LDS and issues 32
+ *                    v_mfma_f32_16x16x32_f16 on a 64 x 64 tile, operands
+ *                    random fp16 values in [-1, 1);
+ *   MFMA_LDS_FLAT    the same with constant small-integer operands;
+ *   MFMA_LDS_NARROW  the same as MFMA_LDS on 32 x 32 tiles: per iteration
+ *                    4 KiB of LDS reads and 8 MFMAs per wave (LDS-heavy).
+ * For the compute kinds, dst may receive one float per thread when `bytes`
+ * covers grid * threads floats (it keeps the work observable); otherwise
+ * nothing is stored. */
 enum {
     BFHIP_CALIB_EMPTY = 0,
     BFHIP_CALIB_MFMA16 = 1,
     BFHIP_CALIB_MFMA32 = 2,
     BFHIP_CALIB_LDS = 3,
-    BFHIP_CALIB_COPY = 4
+    BFHIP_CALIB_COPY = 4,
+    BFHIP_CALIB_MFMA_LDS = 5,
+    BFHIP_CALIB_MFMA_LDS_FLAT = 6,
+    BFHIP_CALIB_MFMA_LDS_NARROW = 7
 };
 
 int bfhip_calibrate(int kind, int grid, int iters, const void *src, void *dst, size_t bytes,
