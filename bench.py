@@ -101,9 +101,13 @@ def frame_flops(window_rows=True):
             total += 2 * b * h2 * w2 * 4 * c * 2 * c                         # merge
     total += 2 * b * 64 * 176 * 96 * 48                                      # patch embed
     h, w = 32, 88
-    convs = [(16, 44, 1152, 256, 1), (16, 44, 256, 256, 3), (h, w, 448, 256, 1),
-             (h, w, 256, 256, 3), (256, 704, 1, 8, 1), (64, 176, 8, 32, 5), (h, w, 32, 64, 5),
-             (h, w, 320, 256, 3), (h, w, 256, 256, 3), (h, w, 256, 198, 1)]
+    convs = [(16, 44, 256, 256, 3), (h, w, 256, 256, 3), (256, 704, 1, 8, 1), (64, 176, 8, 32, 5),
+             (h, w, 32, 64, 5), (h, w, 320, 256, 3), (h, w, 256, 256, 3), (h, w, 256, 198, 1)]
+    if window_rows:  # lateral 1x1 convs over the upsampled concat, as the reference runs them
+        convs += [(16, 44, 1152, 256, 1), (h, w, 448, 256, 1)]
+    else:  # lower halves at full resolution, upper halves at the upper level's
+        convs += [(16, 44, 384, 256, 1), (8, 22, 768, 256, 1), (h, w, 192, 256, 1),
+                  (16, 44, 256, 256, 1)]
     for oh, ow, ci, co, k in convs:
         total += 2 * b * oh * ow * co * ci * k * k
     return total
@@ -131,6 +135,10 @@ NECK_LAYERS = {
     11: ("downsample.2", 180 * 180, 80, 80, 3, 180 * 180 * 80 * 2, 4),
 }
 IO_LAYERS = (4, 8, 11)  # timed on caller buffers (bfhip_camera_profile_layer_io)
+# The lateral 1x1 convs over concat(lower, bilinear-up(upper)) run as two
+# GEMMs (W_lower . lower, and W_upper . upper at the upper resolution, added
+# upsampled in the first one's epilogue): layer -> (M, Cl, M_upper, Cu).
+LATERALS = {0: (6 * 16 * 44, 384, 6 * 8 * 22, 768), 2: (6 * 32 * 88, 192, 6 * 16 * 44, 256)}
 
 
 def swin_op_cost(stage, op, b=6):
@@ -173,6 +181,10 @@ def swin_op_cost(stage, op, b=6):
 
 
 def neck_layer_cost(layer):
+    if layer in LATERALS:  # executed work of the two GEMMs (fp32 upper product written and read)
+        m, cl, mu, cu = LATERALS[layer]
+        return (2.0 * 256 * (m * cl + mu * cu),
+                m * cl * 2 + mu * cu * 2 + 256 * (cl + cu) * 2 + 2 * mu * 256 * 4 + m * 256 * 2)
     name, m, ci, co, k, in_bytes, out_el = NECK_LAYERS[layer]
     return 2.0 * m * co * ci * k * k, in_bytes + co * ci * k * k * 2 + m * co * out_el
 

@@ -8,7 +8,9 @@
 // bf16 container type).  The reference's glue passes become operand
 // gathers or epilogues, so no concat / upsample / split / transpose buffer
 // exists:
-//   lateral 1x1 convs read concat(lower, bilinear-up(upper)) taps directly;
+//   a lateral 1x1 conv over concat(lower, bilinear-up(upper)) runs as
+//   W_lower . lower with up(W_upper . upper) added in its epilogue (the
+//   upper product computed at the upper resolution, EpiUpAddNHWC);
 //   dtransform.0 (1x1, 1->8) is evaluated inside dtransform.3's gather;
 //   depthnet.0 reads concat(dtransform out, fpn0) taps directly;
 //   depthnet.6 stores logits / context from its epilogue;
@@ -43,6 +45,9 @@ struct bf_cuda_camera_neck {
     // Channels-last bf16 maps: packed Swin levels, FPN laterals / outputs,
     // depth encoder, depth trunk, packed BEV and downsample intermediates.
     bf16 *p0, *p1, *p2, *t1, *f1, *t0, *f0, *e1, *e2, *d0, *d1, *bp, *b0, *b1;
+    // fp32 upper-level lateral products W_upper . upper: [B][h2][w2][256]
+    // (lateral 1) and [B][h1][w1][256] (lateral 0).
+    float *u1, *u0;
 };
 
 namespace {
@@ -51,8 +56,8 @@ namespace {
 // for the 256-channel 3x3 convs at 32x88 and the depthnet.6 1x1, 64 x 64 at
 // level 1 (16x44), a two-wave 32 x 64 tile over 32-deep k-steps for
 // dtransform.6 (32 input channels), 80-column tiles for the downsample (below).
-// Register-fed gathers (bilinear / depth affine sources): 128 x 128 / 64 x 64
-// for the lateral 1x1s, a narrow tile for the 32-channel dtransform.3.
+// Register-fed gather (depth affine source): a narrow tile for the
+// 32-channel dtransform.3.
 using D256 = DmaTile<64, 128, 64, 2, 2, 2, true>;  // 3x3 256-channel convs and depthnet.6 at level 0
 // The level-0 3x3 convs with 256 outputs at full camera batch (M = 6 x 32 x
 // 88 = 16896 rows) run one 80-row x 256-channel stripe per CU on the
@@ -68,8 +73,6 @@ inline bool use_stripes(const ConvLayer &l) {
 }
 using D64 = DmaTile<64, 64, 64, 2, 2, 2, true>;    // fpn_convs.1 at level 1
 using D32 = DmaTile<32, 64, 32, 1, 2, 4, true>;    // dtransform.6: 32 input channels
-using T256 = Tile<128, 128, 64, 2, 2, true>;       // lateral_convs.0
-using T64 = Tile<64, 64, 64, 2, 2, true>;          // lateral_convs.1
 using T32 = Tile<128, 32, 32, 4, 1, true>;         // dtransform.3: 32 output channels
 // The downsample's 80-channel maps are stored channels-last with a row
 // stride of kDsPad = 96 (channels 80..95 zero, written once at create) and its
@@ -97,21 +100,50 @@ void fpn_conv(const ConvLayer &l, const bf16 *in, bf16 *nhwc, float *nchw, hipSt
         run_conv_dma<T, 3>(l, in, 256, nullptr, 0, nhwc_to(l, nhwc, true), s);
 }
 
+// Lateral 1x1 conv `layer` over concat(lower [B][H][W][Cl], up(upper
+// [B][h][w][Cu])): the upper product W[:, Cl:] . upper goes to `up` (fp32),
+// then W[:, :Cl] . lower + bias + bilinear(up) (ReLU) to `out`.  The folded
+// weights are [256][Cl + Cu] rows; each half is read in place.
+using DLatUp = DmaTile<32, 64, 64, 1, 2, 3, true>;  // upper products (M = B*h*w)
+using DLat = DmaTile<64, 64, 64, 2, 2, 2, true>;    // lower halves
+void lateral(const ConvLayer &l, const bf16 *lower, int Cl, int H, int W, const bf16 *upper, int Cu,
+             int h, int w, float *up, bf16 *out, hipStream_t s) {
+    const int B = l.n, Mu = B * h * w, M = B * H * W, ci = Cl + Cu;
+    {
+        using T = DLatUp;
+        DmaRowsBf16<T::BM, T::BK, T::kThreads> al{upper, Cu, Mu, Cu};
+        DmaRowsBf16<T::BN, T::BK, T::kThreads> bl{l.w + Cl, ci, 256, Cu};
+        launch_gemm_dma<T>(al, bl, EpiRowsF32{up, nullptr, 256, Mu, 256, 0}, Mu, 256, Cu, s);
+    }
+    {
+        using T = DLat;
+        DmaRowsBf16<T::BM, T::BK, T::kThreads> al{lower, Cl, M, Cl};
+        DmaRowsBf16<T::BN, T::BK, T::kThreads> bl{l.w, ci, 256, Cl};
+        launch_gemm_dma<T>(al, bl, EpiUpAddNHWC{out, l.b, up, M, 256, H, W, h, w, 1}, M, 256, Cl, s);
+    }
+}
+
+void lateral1(bf_cuda_camera_neck *n, hipStream_t s) {
+    lateral(n->L[kLat1], n->p1, 384, (int)n->h1, (int)n->w1, n->p2, 768, (int)n->h2, (int)n->w2,
+            n->u1, n->t1, s);
+}
+
+void lateral0(bf_cuda_camera_neck *n, hipStream_t s) {
+    lateral(n->L[kLat0], n->p0, 192, (int)n->h, (int)n->w, n->f1, 256, (int)n->h1, (int)n->w1, n->u0,
+            n->t0, s);
+}
+
 // FPN from NCHW fp32 Swin levels; FPN levels land channels-last in f0/f1 and,
 // when requested, also NCHW fp32 in out0/out1.
 void fpn_impl(bf_cuda_camera_neck *n, const float *s0, const float *s1, const float *s2,
               float *out0, float *out1, hipStream_t s) {
     const int B = (int)n->batches;
-    const int h = (int)n->h, w = (int)n->w, h1 = (int)n->h1, w1 = (int)n->w1;
-    const int h2 = (int)n->h2, w2 = (int)n->w2;
-    pack_nhwc(s0, n->p0, B, 192, h * w, s, true);
-    pack_nhwc(s1, n->p1, B, 384, h1 * w1, s, true);
-    pack_nhwc(s2, n->p2, B, 768, h2 * w2, s, true);
-    run_conv<T64, 1, 1>(n->L[kLat1], SrcNHWCUpConcat<true>{n->p1, n->p2, 384, 768, h1, w1, h2, w2},
-                        nhwc_to(n->L[kLat1], n->t1, true), s);
+    const int hw = (int)(n->h * n->w), hw1 = (int)(n->h1 * n->w1), hw2 = (int)(n->h2 * n->w2);
+    pack_nhwc_many(PackJobs<3>{{{s0, n->p0, 192, hw}, {s1, n->p1, 384, hw1}, {s2, n->p2, 768, hw2}}}, B,
+                   s, true);
+    lateral1(n, s);
     fpn_conv<D64>(n->L[kFpn1], n->t1, n->f1, out1, s);
-    run_conv<T256, 1, 1>(n->L[kLat0], SrcNHWCUpConcat<true>{n->p0, n->f1, 192, 256, h, w, h1, w1},
-                         nhwc_to(n->L[kLat0], n->t0, true), s);
+    lateral0(n, s);
     fpn_conv<D256>(n->L[kFpn0], n->t0, n->f0, out0, s);
 }
 
@@ -251,9 +283,13 @@ int build(bf_cuda_camera_neck *n, const bf_model *model, char *error, size_t cap
         offs[i] = total;
         total += (elems[i] * 2 + 255) & ~size_t(255);
     }
+    const size_t u1_off = total, u0_off = u1_off + ((B * 256 * hw2 * 4 + 255) & ~size_t(255));
+    total = u0_off + ((B * 256 * hw1 * 4 + 255) & ~size_t(255));
     if (!hip_ok(hipMalloc(&n->acts, total), error, cap, "allocate camera activations")) return 0;
     n->resident_bytes += total;
     for (int i = 0; i < 14; ++i) *slots[i] = (bf16 *)(n->acts + offs[i]);
+    n->u1 = (float *)(n->acts + u1_off);
+    n->u0 = (float *)(n->acts + u0_off);
     // The downsample maps' padding channels are never written by a kernel:
     // zero them (with the rest of those maps) once.
     if (!hip_ok(hipMemset(n->bp, 0, (size_t)(offs[13] - offs[11]) + elems[13] * 2), error, cap,
@@ -356,9 +392,9 @@ extern "C" int bfhip_camera_profile_layer(bf_cuda_camera_neck *n, int layer, voi
     const ConvLayer &l = n->L[layer];
     // Same kernels and shapes as the forward entry points, on context buffers.
     switch (layer) {
-        case kLat1: run_conv<T64, 1, 1>(l, SrcNHWCUpConcat<true>{n->p1, n->p2, 384, 768, h1, w1, h2, w2}, nhwc_to(l, n->t1, true), s); break;
+        case kLat1: lateral1(n, s); break;
         case kFpn1: fpn_conv<D64>(l, n->t1, n->f1, nullptr, s); break;
-        case kLat0: run_conv<T256, 1, 1>(l, SrcNHWCUpConcat<true>{n->p0, n->f1, 192, 256, h, w, h1, w1}, nhwc_to(l, n->t0, true), s); break;
+        case kLat0: lateral0(n, s); break;
         case kFpn0: fpn_conv<D256>(l, n->t0, n->f0, nullptr, s); break;
         case kDt2: case kDn0: case kDn3: depth_layer(n, layer, nullptr, nullptr, nullptr, s); break;
         case kDs0: case kDs1: downsample_layer(n, layer, nullptr, s); break;

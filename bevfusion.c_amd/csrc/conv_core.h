@@ -235,52 +235,6 @@ struct SrcNHWCConcat {
     }
 };
 
-// concat(lower, bilinear-up(upper)) read by a 1x1/s1 convolution; bilinear
-// coordinates follow the reference's fpn_concat_kernel (cuda_camera.cu:234-242)
-// and are computed once per output pixel.  F16: the maps hold fp16 words (and
-// the interpolated taps are stored as fp16), else bf16.
-template <bool F16 = false>
-struct SrcNHWCUpConcat {
-    const bf16 *lower, *upper;
-    int Cl, Cu, H, W, h, w;
-    struct Row { int y0, y1, x0, x1; float fy, fx; };
-    __device__ Row row(int, int oy, int ox) const {
-        Row r;
-        float sy = ((float)oy + 0.5f) * (float)h / (float)H - 0.5f;
-        float sx = ((float)ox + 0.5f) * (float)w / (float)W - 0.5f;
-        sy = fmaxf(sy, 0.0f);
-        sx = fmaxf(sx, 0.0f);
-        r.y0 = (int)floorf(sy);
-        r.x0 = (int)floorf(sx);
-        r.y1 = min(r.y0 + 1, h - 1);
-        r.x1 = min(r.x0 + 1, w - 1);
-        r.fy = sy - (float)r.y0;
-        r.fx = sx - (float)r.x0;
-        return r;
-    }
-    __device__ bf16x8 load(const Row &r, int n, int iy, int ix, int c0) const {
-        if (c0 < Cl)
-            return *reinterpret_cast<const bf16x8 *>(lower + (((size_t)n * H + iy) * W + ix) * Cl + c0);
-        const bf16 *p = upper + (size_t)n * h * w * Cu + (c0 - Cl);
-        const bf16x8 a = *reinterpret_cast<const bf16x8 *>(p + ((size_t)r.y0 * w + r.x0) * Cu);
-        const bf16x8 b = *reinterpret_cast<const bf16x8 *>(p + ((size_t)r.y0 * w + r.x1) * Cu);
-        const bf16x8 c = *reinterpret_cast<const bf16x8 *>(p + ((size_t)r.y1 * w + r.x0) * Cu);
-        const bf16x8 d = *reinterpret_cast<const bf16x8 *>(p + ((size_t)r.y1 * w + r.x1) * Cu);
-        bf16x8 o;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float fa = F16 ? half_to_f32(a[e]) : to_f32(a[e]);
-            const float fb = F16 ? half_to_f32(b[e]) : to_f32(b[e]);
-            const float fc = F16 ? half_to_f32(c[e]) : to_f32(c[e]);
-            const float fd = F16 ? half_to_f32(d[e]) : to_f32(d[e]);
-            const float top = fa * (1.0f - r.fx) + fb * r.fx;
-            const float bot = fc * (1.0f - r.fx) + fd * r.fx;
-            o[e] = to_word(top * (1.0f - r.fy) + bot * r.fy, F16);
-        }
-        return o;
-    }
-};
-
 // dtransform.0 fused into dtransform.3's gather: the 8 virtual channels of tap
 // (iy, ix) are relu(depth*w[c] + b[c]) from one fp32 depth value, as fp16
 // words when F16 is set, else bf16.
@@ -492,14 +446,65 @@ struct EpiConvOut {
     }
 };
 
+// Lateral 1x1 conv of concat(lower, bilinear-up(upper)) (reference
+// image_fpn.c fuse_level / bilinear_channel, align_corners = False) computed
+// as W_lower . lower + up(W_upper . upper): a 1x1 conv acts on channels and
+// the upsampling on pixels, both linearly, so they commute, and the upper
+// half of the conv runs at the upper level's resolution.  This epilogue
+// belongs to the GEMM over the lower channels: out[row][col] =
+// word(relu(acc + bias[col] + bilinear(up)(pixel row)[col])), NHWC, where
+// `up` is the fp32 product W_upper . upper, [n][h][w][Co], and output row =
+// n*H*W + oy*W + ox.  Co % 4 == 0.
+struct EpiUpAddNHWC {
+    static constexpr bool kRowVector = true;
+    bf16 *out;
+    const float *bias, *up;
+    int M, Co, H, W, h, w;
+    int f16;
+    __device__ ColQuad column(int col) const { return ColQuad{col, load_quad(bias, col, Co)}; }
+    template <int R>
+    __device__ void rows(int row0, int step, const ColQuad &c, const float4 (&v)[R]) const {
+        if (c.col >= Co) return;
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            const int row = row0 + i * step;
+            if (row >= M) break;
+            const int n = row / (H * W), p = row - n * (H * W), oy = p / W, ox = p - oy * W;
+            float sy = ((float)oy + 0.5f) * (float)h / (float)H - 0.5f;
+            float sx = ((float)ox + 0.5f) * (float)w / (float)W - 0.5f;
+            sy = fmaxf(sy, 0.0f);
+            sx = fmaxf(sx, 0.0f);
+            const int y0 = (int)floorf(sy), x0 = (int)floorf(sx);
+            const int y1 = min(y0 + 1, h - 1), x1 = min(x0 + 1, w - 1);
+            const float fy = sy - (float)y0, fx = sx - (float)x0;
+            const float *base = up + (size_t)n * h * w * Co + c.col;
+            const float4 a = *reinterpret_cast<const float4 *>(base + ((size_t)y0 * w + x0) * Co);
+            const float4 b = *reinterpret_cast<const float4 *>(base + ((size_t)y0 * w + x1) * Co);
+            const float4 cc = *reinterpret_cast<const float4 *>(base + ((size_t)y1 * w + x0) * Co);
+            const float4 d = *reinterpret_cast<const float4 *>(base + ((size_t)y1 * w + x1) * Co);
+            const float va[4] = {a.x, a.y, a.z, a.w}, vb[4] = {b.x, b.y, b.z, b.w};
+            const float vc[4] = {cc.x, cc.y, cc.z, cc.w}, vd[4] = {d.x, d.y, d.z, d.w};
+            const float acc[4] = {v[i].x, v[i].y, v[i].z, v[i].w}, bias4[4] = {c.b.x, c.b.y, c.b.z, c.b.w};
+            bf16x4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float top = va[e] * (1.0f - fx) + vb[e] * fx;
+                const float bot = vc[e] * (1.0f - fx) + vd[e] * fx;
+                float y = acc[e] + bias4[e] + (top * (1.0f - fy) + bot * fy);
+                y = y < 0.0f ? 0.0f : y;
+                o[e] = to_word(y, f16);
+            }
+            *reinterpret_cast<bf16x4 *>(out + (size_t)row * Co + c.col) = o;
+        }
+    }
+};
+
 // NCHW fp32 [N][C][HW] -> NHWC 16-bit words [N][HW][ld] (bf16, or fp16 when
 // f16 is set; channels C..ld-1 of each row are left untouched) through a
 // 64-pixel x 64-channel LDS tile (coalesced reads along pixels, 16-byte writes
 // along channels).  C and ld must be multiples of 8.
-static __global__ __launch_bounds__(256) void pack_nhwc_kernel(const float *x, bf16 *y, int C, int HW,
-                                                               int f16, int ld) {
-    __shared__ float tile[64][65];
-    const int n = blockIdx.z, c0 = blockIdx.y * 64, p0 = blockIdx.x * 64;
+__device__ __forceinline__ void pack_nhwc_block(const float *x, bf16 *y, int C, int HW, int f16,
+                                                int ld, int n, int c0, int p0, float (&tile)[64][65]) {
     const int t = threadIdx.x;
     const float *src = x + (size_t)n * C * HW;
 #pragma unroll
@@ -522,10 +527,53 @@ static __global__ __launch_bounds__(256) void pack_nhwc_kernel(const float *x, b
     }
 }
 
+static __global__ __launch_bounds__(256) void pack_nhwc_kernel(const float *x, bf16 *y, int C, int HW,
+                                                               int f16, int ld) {
+    __shared__ float tile[64][65];
+    pack_nhwc_block(x, y, C, HW, f16, ld, blockIdx.z, blockIdx.y * 64, blockIdx.x * 64, tile);
+}
+
 inline void pack_nhwc(const float *x, bf16 *y, int N, int C, int HW, hipStream_t s,
                       bool f16 = false, int ld = 0) {
     hipLaunchKernelGGL(pack_nhwc_kernel, dim3((HW + 63) / 64, (C + 63) / 64, N), dim3(256), 0, s,
                        x, y, C, HW, (int)f16, ld ? ld : C);
+}
+
+// Several NCHW -> NHWC packs of the same batch in one launch (one grid over
+// the 64 x 64 blocks of every map; row stride = C).
+struct PackJob {
+    const float *x;
+    bf16 *y;
+    int C, HW;
+};
+template <int J>
+struct PackJobs {
+    PackJob job[J];
+};
+
+template <int J>
+__global__ __launch_bounds__(256) void pack_nhwc_many_kernel(PackJobs<J> jobs, int N, int f16) {
+    __shared__ float tile[64][65];
+    int b = (int)blockIdx.x;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const PackJob &pj = jobs.job[j];
+        const int bp = (pj.HW + 63) / 64, bc = (pj.C + 63) / 64, count = bp * bc * N;
+        if (b < count) {  // uniform over the workgroup
+            const int n = b / (bp * bc), r = b - n * (bp * bc), cb = r / bp, pb = r - cb * bp;
+            pack_nhwc_block(pj.x, pj.y, pj.C, pj.HW, f16, pj.C, n, cb * 64, pb * 64, tile);
+            return;
+        }
+        b -= count;
+    }
+}
+
+template <int J>
+inline void pack_nhwc_many(const PackJobs<J> &jobs, int N, hipStream_t s, bool f16) {
+    int blocks = 0;
+    for (int j = 0; j < J; ++j)
+        blocks += ((jobs.job[j].HW + 63) / 64) * ((jobs.job[j].C + 63) / 64) * N;
+    hipLaunchKernelGGL((pack_nhwc_many_kernel<J>), dim3(blocks), dim3(256), 0, s, jobs, N, (int)f16);
 }
 
 }  // namespace bfhip
