@@ -116,6 +116,56 @@ struct LoadConvA {
     }
 };
 
+// A operand of a 4x4 / stride-4 / unpadded conv (the Swin patch embedding)
+// from fp32 NCHW input: for a fixed (channel, ky) the four kx taps are four
+// consecutive floats, so each thread fetches its k-run as float4s, and the
+// lanes of a wave (consecutive output pixels ox) read 64 consecutive float4s
+// of one image row.  Requires IW % 4 == 0, a 16-byte aligned base and the
+// k order ci*16 + ky*4 + kx of LoadConvA.
+template <int BM, int BK, int THREADS, bool F16 = false>
+struct LoadPatch4x4 {
+    static constexpr int kGroups = THREADS / BM;
+    static constexpr int kPer = BK / kGroups;
+    static_assert(THREADS % BM == 0 && kPer % 8 == 0, "whole 16-byte chunks per thread");
+    const float *x;
+    ConvGeom g;
+    int row, kg;
+    const float *pix;  // image n, row 4*oy, column 4*ox, channel 0
+    bool ok;
+    bf16 st[kPer];
+
+    __device__ void setup(int m0, int tid) {
+        row = tid % BM;
+        kg = tid / BM;
+        const int m = m0 + row, ohw = g.OH * g.OW;
+        ok = m < g.M;
+        const int mm = ok ? m : 0, n = mm / ohw, p = mm - n * ohw, oy = p / g.OW, ox = p - oy * g.OW;
+        pix = x + (((size_t)n * g.Ci) * g.IH + 4 * oy) * g.IW + 4 * ox;
+    }
+    __device__ void load(int k0) {
+        const int k = k0 + kg * kPer;
+#pragma unroll
+        for (int q = 0; q < kPer; q += 4) {
+            const int kk = k + q, ci = kk >> 4, ky = (kk >> 2) & 3;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (ok && kk < g.K)
+                v = *reinterpret_cast<const float4 *>(pix + ((size_t)ci * g.IH + ky) * g.IW);
+            st[q] = to_word(v.x, F16); st[q + 1] = to_word(v.y, F16);
+            st[q + 2] = to_word(v.z, F16); st[q + 3] = to_word(v.w, F16);
+        }
+    }
+    __device__ void store(bf16 *lds) const {
+        bf16 *dst = lds + row * (BK + 8) + kg * kPer;
+#pragma unroll
+        for (int c = 0; c < kPer; c += 8) {
+            bf16x8 v;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = st[c + e];
+            *reinterpret_cast<bf16x8 *>(dst + c) = v;
+        }
+    }
+};
+
 // Transposed-convolution weights are IOHW: B[co][k] = W[ci][co][ky][kx].
 template <int ROWS, int BK, int THREADS>
 struct LoadWeightIOHW {

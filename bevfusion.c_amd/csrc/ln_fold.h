@@ -222,7 +222,9 @@ struct EpiLnF16 {
 // Patch embedding output over whole 96-channel rows: x = LN_p(acc + b) (the
 // patch norm, reference swin_backbone.c patch embed) and xn = fp16(LN_1(x))
 // (block 0's norm1), both two-pass fp32, eps 1e-5.  Two threads per row, 48
-// channels each.
+// channels each, normalise in registers and put the rows back into the
+// staged tile; the tile's rows are one contiguous block of x (and of xn), so
+// all threads then store it as consecutive 16-byte vectors.
 struct EpiPatchNorms {
     static constexpr bool kRowVector = true;
     static constexpr bool kFullRow = true;
@@ -232,33 +234,57 @@ struct EpiPatchNorms {
     const float *bias, *g0, *b0, *g1, *b1;
     int M;
     template <class T>
-    __device__ void tile(const float *sC, int stride, int m0, int tid) const {
+    __device__ void tile(float *sC, int stride, int m0, int tid) const {
         static_assert(T::BN == C && T::kThreads == 2 * T::BM, "two threads per 96-channel row");
-        const int r = tid >> 1, h = tid & 1, row = m0 + r, c0 = h * kHalf;
+        const int r = tid >> 1, h = tid & 1, c0 = h * kHalf;
+        float *rowp = sC + r * stride + c0;
         float v[kHalf];
         float s = 0.0f;
 #pragma unroll
         for (int i = 0; i < kHalf; i += 4) {
-            const float4 a = *reinterpret_cast<const float4 *>(sC + r * stride + c0 + i);
+            const float4 a = *reinterpret_cast<const float4 *>(rowp + i);
             const float4 b = *reinterpret_cast<const float4 *>(bias + c0 + i);
             v[i] = a.x + b.x; v[i + 1] = a.y + b.y; v[i + 2] = a.z + b.z; v[i + 3] = a.w + b.w;
             s += (v[i] + v[i + 1]) + (v[i + 2] + v[i + 3]);
         }
         normalise(v, s, g0, b0, c0);
-        const bool ok = row < M;
+        float u[kHalf];
         s = 0.0f;
 #pragma unroll
-        for (int i = 0; i < kHalf; i += 4) {
-            if (ok)
-                *reinterpret_cast<float4 *>(x + (size_t)row * C + c0 + i) =
-                    make_float4(v[i], v[i + 1], v[i + 2], v[i + 3]);
-            s += (v[i] + v[i + 1]) + (v[i + 2] + v[i + 3]);
+        for (int i = 0; i < kHalf; ++i) {
+            u[i] = v[i];
+            s += v[i];
         }
-        normalise(v, s, g1, b1, c0);
-        if (ok)
+        normalise(u, s, g1, b1, c0);
+        // x rows back into the tile (the second LN is in registers).
 #pragma unroll
-            for (int i = 0; i < kHalf; i += 4)
-                store_half4(xn + (size_t)row * C + c0 + i, make_float4(v[i], v[i + 1], v[i + 2], v[i + 3]));
+        for (int i = 0; i < kHalf; i += 4)
+            *reinterpret_cast<float4 *>(rowp + i) = make_float4(v[i], v[i + 1], v[i + 2], v[i + 3]);
+        lds_barrier();
+        const int rows = min(T::BM, M - m0);
+        float *xo = x + (size_t)m0 * C;
+        for (int q = tid; q < rows * (C / 4); q += T::kThreads) {
+            const int rr = q / (C / 4), cq = q - rr * (C / 4);
+            *reinterpret_cast<float4 *>(xo + (size_t)q * 4) =
+                *reinterpret_cast<const float4 *>(sC + rr * stride + cq * 4);
+        }
+        lds_barrier();
+        // LN1 rows into the tile as fp16 words (row stride `stride` floats).
+        bf16 *hrow = reinterpret_cast<bf16 *>(sC + r * stride) + c0;
+#pragma unroll
+        for (int i = 0; i < kHalf; i += 8) {
+            bf16x8 o;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = to_half(u[i + e]);
+            *reinterpret_cast<bf16x8 *>(hrow + i) = o;
+        }
+        lds_barrier();
+        bf16 *xno = xn + (size_t)m0 * C;
+        for (int q = tid; q < rows * (C / 8); q += T::kThreads) {
+            const int rr = q / (C / 8), cq = q - rr * (C / 8);
+            *reinterpret_cast<bf16x8 *>(xno + (size_t)q * 8) =
+                *reinterpret_cast<const bf16x8 *>(reinterpret_cast<const bf16 *>(sC + rr * stride) + cq * 8);
+        }
     }
 
 private:

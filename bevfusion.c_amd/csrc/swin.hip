@@ -434,13 +434,18 @@ void patch_embed(bf_cuda_swin *s, const float *images, hipStream_t stream) {
     g.OH = s->h[0]; g.OW = s->w[0]; g.KH = 4; g.KW = 4; g.SH = 4; g.SW = 4;
     g.PH = 0; g.PW = 0; g.transpose = 0;
     g.M = B * s->h[0] * s->w[0]; g.K = 48;
-    LoadConvA<T::BM, T::BK, T::kThreads, 4, 4, SrcNCHW, true> al{};
-    al.src = SrcNCHW{images, 3, g.IH, g.IW};
-    al.g = g;
     LoadRowsBf16<T::BN, T::BK, T::kThreads> bl{s->patch_w, 48, 96, 48};
     const BlockW &b0 = s->blocks[0][0];
     EpiPatchNorms epi{s->x, s->xn, s->patch_b, s->patch_ns, s->patch_nb, b0.n1s, b0.n1b, g.M};
-    launch_gemm<T>(al, bl, epi, g.M, 96, 48, stream);
+    if (((uintptr_t)images & 15) == 0) {  // IW % 4 == 0 by contract: float4 patch rows
+        LoadPatch4x4<T::BM, T::BK, T::kThreads, true> al{images, g};
+        launch_gemm<T>(al, bl, epi, g.M, 96, 48, stream);
+    } else {
+        LoadConvA<T::BM, T::BK, T::kThreads, 4, 4, SrcNCHW, true> al{};
+        al.src = SrcNCHW{images, 3, g.IH, g.IW};
+        al.g = g;
+        launch_gemm<T>(al, bl, epi, g.M, 96, 48, stream);
+    }
 }
 
 // Calls f(std::integral_constant<int, C / 64>) for the channel counts of

@@ -86,3 +86,28 @@ def test_swin_production_batch_invariance_and_repeat(device, tmp_models):
             assert torch.equal(oa[cam:cam + 1], os), f"camera {cam} depends on batch"
     six.close()
     one.close()
+
+
+def test_swin_unaligned_images_match_aligned(device, tmp_models):
+    """Images that start 4 bytes past a 16-byte boundary (a valid fp32
+    pointer for the C ABI) take the scalar patch gather instead of the float4
+    one; both stage the same fp16 operands, so every output is bit-identical
+    to the aligned forward."""
+    import bfhip
+    import torch
+    from bfhip import bfw
+    path = tmp_models("fan_in", 1)
+    images = bfw.synthetic_images(5, 2, 32, 48)
+    x = torch.from_numpy(images).to(device)
+    buf = torch.empty(x.numel() + 1, device=device)
+    buf[1:].copy_(x.reshape(-1))
+    xu = buf[1:].view(x.shape)
+    assert xu.data_ptr() % 16 == 4
+    with bfhip.Model(path) as m:
+        ctx = bfhip.Swin(m, 2, 32, 48)
+    a = ctx.forward(x)
+    b = ctx.forward(xu)
+    torch.cuda.synchronize()
+    for oa, ob in zip(a, b):
+        assert torch.equal(oa, ob), "unaligned images change the result"
+    ctx.close()
