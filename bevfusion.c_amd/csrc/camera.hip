@@ -192,8 +192,14 @@ void downsample_layer(bf_cuda_camera_neck *n, int layer, float *output, hipStrea
             run_conv_dma<DDs1, 3>(l, n->b0, kDsPad, nullptr, 0, nhwc_to(l, n->b1, true, kDsPad), s);
             break;
         case kDs2:
-            run_conv_dma<DDs1, 3>(l, n->b1, kDsPad, nullptr, 0,
-                                  EpiTransposeXY{output, l.b, l.oh * l.ow, 80, l.oh, l.ow}, s);
+            // The checkpoint's x/y permute out[c][x][y] = y(c, y, x) (reference
+            // transpose_xy_kernel, cuda_camera.cu:265-271; lss_downsample.c:
+            // 142-146): with the GEMM rows in x-major pixel order the
+            // transposed NCHW output is plain channel planes along the rows.
+            run_conv_dma<DDs1, 3, EpiPlanesNCHW, true>(l, n->b1, kDsPad, nullptr, 0,
+                                                       EpiPlanesNCHW{output, l.b, l.oh * l.ow, 80,
+                                                                     l.oh * l.ow},
+                                                       s);
             break;
         default: break;
     }

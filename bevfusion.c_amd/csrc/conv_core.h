@@ -209,46 +209,87 @@ struct LoadWeightIOHW {
 // Final 1x1 of the depth head: channels [0,118) are depth logits, [118,198)
 // context, both NCHW (reference split_depth_kernel, cuda_camera.cu:255-263).
 struct EpiSplitDepth {
-    static constexpr bool kRowVector = false;
+    static constexpr bool kRowVector = true;
+    static constexpr bool kFullRow = true;
     float *logits, *context;
     const float *bias;
     int M, ohw, bins, ctx;
-    __device__ void operator()(int row, int col, f32x4 v) const {
-        if (col >= bins + ctx) return;
-        const float b = bias[col];
-        float *base = col < bins ? logits + (size_t)col * ohw : context + (size_t)(col - bins) * ohw;
-        const int planes = col < bins ? bins : ctx;
+    // The staged fp32 tile is read column by column: consecutive threads take
+    // consecutive 4-pixel quads of one channel, so a wave writes 16-byte
+    // vectors in runs of BM/4 along a channel plane.
+    template <class T>
+    __device__ void tile(float *sC, int stride, int m0, int n0, int tid) const {
+        constexpr int kQuads = T::BM / 4;
+        for (int item = tid; item < T::BN * kQuads; item += T::kThreads) {
+            const int c = item / kQuads, q = item - c * kQuads;
+            const int col = n0 + c, row = m0 + 4 * q;
+            if (col >= bins + ctx || row >= M) continue;
+            const float b = bias[col];
+            float v[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int rr = row + r;
-            if (rr >= M) break;
-            const int n = rr / ohw, p = rr - n * ohw;
-            base[(size_t)n * planes * ohw + p] = v[r] + b;
+            for (int r = 0; r < 4; ++r) v[r] = sC[(4 * q + r) * stride + c] + b;
+            const bool lo = col < bins;
+            float *base = lo ? logits + (size_t)col * ohw : context + (size_t)(col - bins) * ohw;
+            const int planes = lo ? bins : ctx;
+            const int n = row / ohw, p = row - n * ohw;
+            float *dst = base + (size_t)n * planes * ohw + p;
+            if (row + 3 < M && p + 3 < ohw && ((uintptr_t)dst & 15) == 0) {
+                *reinterpret_cast<float4 *>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int rr = row + r;
+                    if (rr >= M) break;
+                    const int nn = rr / ohw, pp = rr - nn * ohw;
+                    base[(size_t)nn * planes * ohw + pp] = v[r];
+                }
+            }
         }
     }
 };
 
-// Last downsample conv: BN-folded bias + ReLU, then the checkpoint's x/y
-// permute out[c][x][y] = y(c, y, x) on a [C, H, W] map (reference
-// transpose_xy_kernel, cuda_camera.cu:265-271; lss_downsample.c:142-146).
-struct EpiTransposeXY {
-    static constexpr bool kRowVector = false;
+// Channel planes out[n][c][p] = relu(v + bias[c]) for GEMM row n*HW + p: the
+// staged fp32 tile is read column by column, consecutive threads taking
+// consecutive 4-row quads of one channel, so a wave writes 16-byte vectors in
+// runs of BM/4 along a plane.  With rows in YFAST order this stores the x/y-
+// transposed map of the last downsample conv (below) contiguously.
+struct EpiPlanesNCHW {
+    static constexpr bool kRowVector = true;
+    static constexpr bool kFullRow = true;
     float *out;
     const float *bias;
-    int M, C, H, W;
-    __device__ void operator()(int row, int col, f32x4 v) const {
-        if (col >= C) return;
-        const float b = bias[col];
+    int M, C, hw;
+    template <class T>
+    __device__ void tile(float *sC, int stride, int m0, int n0, int tid) const {
+        constexpr int kQuads = T::BM / 4;
+        for (int item = tid; item < T::BN * kQuads; item += T::kThreads) {
+            const int c = item / kQuads, q = item - c * kQuads;
+            const int col = n0 + c, row = m0 + 4 * q;
+            if (col >= C || row >= M) continue;
+            const float b = bias[col];
+            float v[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int rr = row + r;
-            if (rr >= M) break;
-            const int hw = H * W, n = rr / hw, p = rr - n * hw, y = p / W, x = p - y * W;
-            float o = v[r] + b;
-            out[(((size_t)n * C + col) * W + x) * H + y] = o > 0.0f ? o : 0.0f;
+            for (int r = 0; r < 4; ++r) {
+                const float o = sC[(4 * q + r) * stride + c] + b;
+                v[r] = o > 0.0f ? o : 0.0f;
+            }
+            const int n = row / hw, p = row - n * hw;
+            float *dst = out + ((size_t)n * C + col) * hw + p;
+            if (row + 3 < M && p + 3 < hw && ((uintptr_t)dst & 15) == 0) {
+                *reinterpret_cast<float4 *>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int rr = row + r;
+                    if (rr >= M) break;
+                    const int nn = rr / hw, pp = rr - nn * hw;
+                    out[((size_t)nn * C + col) * hw + pp] = v[r];
+                }
+            }
         }
     }
 };
+
 
 }  // namespace bfhip
 
@@ -370,7 +411,10 @@ struct LoadConvNHWC {
 // The lane's offset depends on the tap and the source only; it is computed
 // when they change (every C/BK k-tiles) and the channel offset within the
 // source rides in soffset, so most k-tiles issue with no vector arithmetic.
-template <int ROWS, int BK, int THREADS, int KH, int KW>
+// YFAST orders the GEMM rows of each image column-major over output pixels
+// (row = n*OH*OW + ox*OH + oy), so a store in row order writes an x/y-
+// transposed map contiguously.
+template <int ROWS, int BK, int THREADS, int KH, int KW, bool YFAST = false>
 struct DmaConvNHWC {
     static constexpr int kCpr = BK / 8, kWaves = THREADS / kWave;
     static constexpr int kChunks = ROWS * kCpr;
@@ -396,7 +440,8 @@ struct DmaConvNHWC {
             const int q = (j * kWaves + wave) * kWave + lane;
             const int r = q / kCpr, slot = q % kCpr, m = m0 + r;
             const int mm = m < g.M ? m : 0;
-            const int n = mm / ohw, p = mm - n * ohw, oy = p / g.OW, ox = p - oy * g.OW;
+            const int n = mm / ohw, p = mm - n * ohw;
+            const int oy = YFAST ? p % g.OH : p / g.OW, ox = YFAST ? p / g.OH : p % g.OW;
             pix[j] = m < g.M ? n * g.IH * g.IW : -1;
             iy0[j] = oy * g.SH - g.PH;
             ix0[j] = ox * g.SW - g.PW;

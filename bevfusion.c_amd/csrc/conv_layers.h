@@ -82,11 +82,11 @@ void run_conv(const ConvLayer &l, const Src &src, const Epi &epi, hipStream_t s)
 
 // LDS-DMA pipeline for convs over plain or concatenated channels-last maps
 // whose channel counts are multiples of the k-tile.
-template <class T, int K, class Epi>
+template <class T, int K, class Epi, bool YFAST = false>
 void run_conv_dma(const ConvLayer &l, const bf16 *a, int c0, const bf16 *b, int c1, const Epi &epi,
                   hipStream_t s) {
     const ConvGeom g = geom_of(l);
-    DmaConvNHWC<T::BM, T::BK, T::kThreads, K, K> al{a, b, c0, c1, g};
+    DmaConvNHWC<T::BM, T::BK, T::kThreads, K, K, YFAST> al{a, b, c0, c1, g};
     DmaRowsBf16<T::BN, T::BK, T::kThreads> bl{l.w, g.K, l.co, g.K};
     launch_gemm_dma<T>(al, bl, epi, g.M, l.co, g.K, s);
 }

@@ -141,7 +141,8 @@ __device__ __forceinline__ void lds_barrier() {
 // kernel start (Pre stat_load(row), so the loads overlap the main loop),
 // reduces them after it (float2 stat_finish(pre)) into LDS, and rows() gets
 // them; kFullRow epilogues take the whole staged fp32 tile
-// (tile<T>(sC, stride, m0, tid)) because they reduce across full rows.
+// (tile<T>(sC, stride, m0, n0, tid)) to reduce across full rows or to store it
+// in another order.
 template <class E, class = void>
 struct EpiRowStat : std::false_type {};
 template <class E>
@@ -195,7 +196,7 @@ __device__ __forceinline__ void store_tile(const f32x4 (&acc)[T::kFragM][T::kFra
                           (T::kThreads % kQuads == 0 && T::BM % (T::kThreads / kQuads) == 0),
                       "row-statistics epilogues need whole column quads per thread");
         if constexpr (EpiFullRow<Epi>::value) {
-            epi.template tile<T>(sC, kCStride, m0, tid);
+            epi.template tile<T>(sC, kCStride, m0, n0, tid);
         } else if constexpr (T::kThreads % kQuads == 0 && T::BM % (T::kThreads / kQuads) == 0) {
             // Each thread owns one column quad for the whole tile: the
             // epilogue's per-column state (bias) is fetched once, and all of

@@ -234,7 +234,7 @@ struct EpiPatchNorms {
     const float *bias, *g0, *b0, *g1, *b1;
     int M;
     template <class T>
-    __device__ void tile(float *sC, int stride, int m0, int tid) const {
+    __device__ void tile(float *sC, int stride, int m0, int, int tid) const {
         static_assert(T::BN == C && T::kThreads == 2 * T::BM, "two threads per 96-channel row");
         const int r = tid >> 1, h = tid & 1, c0 = h * kHalf;
         float *rowp = sC + r * stride + c0;
