@@ -150,11 +150,22 @@ FoldedLinear fold_ln(const float *W, const float *b, const float *g, const float
 
 void launch_out_ln(int C, const float *x, float *out, const float *g, const float *b, int rows,
                    int hw, hipStream_t s) {
-    const dim3 grid((rows + 15) / 16);
+    // Rows per block: 16 / 8 / 4 for C = 192 / 384 / 768 (1056, 528 and 264
+    // blocks at 6 x 256 x 704; 16 rows per block left stages 2 and 3 at 264
+    // and 66 blocks).
     switch (C) {
-        case 192: hipLaunchKernelGGL((out_ln_kernel<192>), grid, dim3(256), 0, s, x, out, g, b, rows, hw); break;
-        case 384: hipLaunchKernelGGL((out_ln_kernel<384>), grid, dim3(256), 0, s, x, out, g, b, rows, hw); break;
-        case 768: hipLaunchKernelGGL((out_ln_kernel<768>), grid, dim3(256), 0, s, x, out, g, b, rows, hw); break;
+        case 192:
+            hipLaunchKernelGGL((out_ln_kernel<192, 16>), dim3((rows + 15) / 16), dim3(256), 0, s, x, out,
+                               g, b, rows, hw);
+            break;
+        case 384:
+            hipLaunchKernelGGL((out_ln_kernel<384, 8>), dim3((rows + 7) / 8), dim3(256), 0, s, x, out, g,
+                               b, rows, hw);
+            break;
+        case 768:
+            hipLaunchKernelGGL((out_ln_kernel<768, 4>), dim3((rows + 3) / 4), dim3(256), 0, s, x, out, g,
+                               b, rows, hw);
+            break;
         default: break;
     }
 }

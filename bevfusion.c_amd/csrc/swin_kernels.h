@@ -83,13 +83,13 @@ __global__ __launch_bounds__(256) void merge_ln_kernel(const float *x, bf16 *y, 
 }
 
 // Stage output: LayerNorm over C of tokens [n, HW, C], stored NCHW.  A block
-// normalises 16 consecutive tokens into LDS, then writes 16-token runs of each
-// channel plane (reference store_output, swin_backbone.c:265-276).
-template <int C>
+// normalises kRows consecutive tokens into LDS, then writes kRows-token runs
+// of each channel plane (reference store_output, swin_backbone.c:265-276).
+// kRows is chosen per stage so the grid has several hundred blocks.
+template <int C, int kRows>
 __global__ __launch_bounds__(256) void out_ln_kernel(const float *x, float *out, const float *g,
                                                      const float *b, int rows, int hw) {
     using L = RowLayout<C>;
-    constexpr int kRows = 16;
     __shared__ float tile[C * (kRows + 1)];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int sub = lane / L::LPR, li = lane % L::LPR;
