@@ -60,21 +60,26 @@ namespace {
 // 32-channel dtransform.3.
 using D256 = DmaTile<64, 128, 64, 2, 2, 2, true>;  // 3x3 256-channel convs and depthnet.6 at level 0
 // The level-0 3x3 convs with 256 outputs at full camera batch (M = 6 x 32 x
-// 88 = 16896 rows) run one 80-row x 256-channel stripe per CU on the
-// wave-specialised pipeline: 212 tiles in one round, each CU fetching its A
-// rows once for all 256 outputs (1.55 MB per CU instead of 2.65 MB for the
-// CUs that take three 64 x 128 tiles), eight compute waves of 80 x 32 plus
-// one loader wave, three 64-deep stages (129 KiB of LDS).  Measured on
-// MI355X as a 16896 x 256 x 2304 GEMM: 29.3 us vs 35.5 us; smaller batches
+// 88 = 16896 rows) run 160-row x 128-channel tiles on the wave-specialised
+// pipeline: 212 tiles in one round, each CU fetching 1.33 MB (instead of 2.65
+// MB for the CUs that take three 64 x 128 tiles), eight compute waves of 80 x
+// 32, three 64-deep stages (110 KiB of LDS) and four loader waves: operand
+// fetch, not the MFMAs, bounds these convs, and one loader wave stops at its
+// 63 in-flight DMA instructions.  Measured on MI355X through this loader
+// (fpn_convs.0 / depthnet.0): 28.3 / 34.7 us, vs 31.2 / 38.5 us as 80 x 256
+// stripes with two loader waves and 38.9 / 48.4 us with one; smaller batches
 // keep the 64 x 128 tiles.
-using S256 = DmaTile<80, 256, 64, 1, 8, 3, true>;
-inline bool use_stripes(const ConvLayer &l) {
-    return l.co == 256 && (l.n * l.oh * l.ow + 79) / 80 >= 128;
+using S256 = DmaTile<160, 128, 64, 2, 4, 3, true>;
+constexpr int kS256Loaders = 4;
+inline bool use_s256(const ConvLayer &l) {
+    return l.co == 256 && 2 * ((l.n * l.oh * l.ow + 159) / 160) >= 128;
 }
-// fpn_convs.1 at level 1 (M = 4224) and dtransform.6 (32 input channels, so
-// 32-deep k-steps) on the wave-specialised pipeline: measured as GEMMs of
-// their shapes on MI355X, 13.9 vs 17.1 us (64 x 64 plain) and 7.6 us.
+// fpn_convs.1 at level 1 (M = 4224, two loader waves) and dtransform.6 (32
+// input channels, so 32-deep k-steps) on the wave-specialised pipeline:
+// measured through the conv loader on MI355X, 17.6 us (18.2 us with one loader
+// wave, 19.3 us as 64 x 64 tiles) and 11.7 us.
 using S64 = DmaTile<32, 64, 64, 1, 2, 4, true>;
+constexpr int kS64Loaders = 2;
 using S32 = DmaTile<32, 64, 32, 1, 2, 6, true>;
 using T32 = Tile<128, 32, 32, 4, 1, true>;         // dtransform.3: 32 output channels
 // The downsample's 80-channel maps are stored channels-last with a row
@@ -92,16 +97,16 @@ template <class T>
 void fpn_conv(const ConvLayer &l, const bf16 *in, bf16 *nhwc, float *nchw, hipStream_t s) {
     if constexpr (std::is_same_v<T, S64>) {
         if (nchw)
-            run_conv_spec<T, 3>(l, in, 256, nullptr, 0, out_to(l, nhwc, nchw, 1, true), s);
+            run_conv_spec<T, 3, kS64Loaders>(l, in, 256, nullptr, 0, out_to(l, nhwc, nchw, 1, true), s);
         else
-            run_conv_spec<T, 3>(l, in, 256, nullptr, 0, nhwc_to(l, nhwc, true), s);
+            run_conv_spec<T, 3, kS64Loaders>(l, in, 256, nullptr, 0, nhwc_to(l, nhwc, true), s);
         return;
     }
-    if (use_stripes(l)) {
+    if (use_s256(l)) {
         if (nchw)
-            run_conv_spec<S256, 3>(l, in, 256, nullptr, 0, out_to(l, nhwc, nchw, 1, true), s);
+            run_conv_spec<S256, 3, kS256Loaders>(l, in, 256, nullptr, 0, out_to(l, nhwc, nchw, 1, true), s);
         else
-            run_conv_spec<S256, 3>(l, in, 256, nullptr, 0, nhwc_to(l, nhwc, true), s);
+            run_conv_spec<S256, 3, kS256Loaders>(l, in, 256, nullptr, 0, nhwc_to(l, nhwc, true), s);
         return;
     }
     if (nchw)
@@ -170,14 +175,14 @@ void depth_layer(bf_cuda_camera_neck *n, int layer, const float *depth, float *l
             break;
         case kDt2: run_conv_spec<S32, 5>(l, n->e1, 32, nullptr, 0, nhwc_to(l, n->e2, true), s); break;
         case kDn0:
-            if (use_stripes(l))
-                run_conv_spec<S256, 3>(l, n->e2, 64, n->f0, 256, nhwc_to(l, n->d0, true), s);
+            if (use_s256(l))
+                run_conv_spec<S256, 3, kS256Loaders>(l, n->e2, 64, n->f0, 256, nhwc_to(l, n->d0, true), s);
             else
                 run_conv_dma<D256, 3>(l, n->e2, 64, n->f0, 256, nhwc_to(l, n->d0, true), s);
             break;
         case kDn3:
-            if (use_stripes(l))
-                run_conv_spec<S256, 3>(l, n->d0, 256, nullptr, 0, nhwc_to(l, n->d1, true), s);
+            if (use_s256(l))
+                run_conv_spec<S256, 3, kS256Loaders>(l, n->d0, 256, nullptr, 0, nhwc_to(l, n->d1, true), s);
             else
                 run_conv_dma<D256, 3>(l, n->d0, 256, nullptr, 0, nhwc_to(l, n->d1, true), s);
             break;

@@ -518,27 +518,29 @@ inline void launch_gemm_dma(const ALoad &al, const BLoad &bl, const Epi &epi, in
 }
 
 // ======================================== wave-specialised LDS-DMA pipeline
-// Same tile, LDS image, loaders and epilogues as gemm_dma_kernel, plus one
-// loader wave that issues every DMA; the WM x WN compute waves never issue a
+// Same tile, LDS image, loaders and epilogues as gemm_dma_kernel, plus LW
+// loader waves that issue every DMA; the WM x WN compute waves never issue a
 // vector-memory instruction in the main loop.  In gemm_dma_kernel each wave
 // issues its share of the next stage and then runs its MFMAs: when the fetch
 // path is the bottleneck the issue itself stalls until the texture unit takes
 // the request, and the SIMD's matrix core idles meanwhile, so fetch and math
 // add up instead of overlapping (measured on MI355X with a 128 x 64 tile, K =
 // 1536: 5.8 us of DMA alone, 11.8 us with the MFMAs).  With the issue moved
-// to its own wave, the stall holds that wave only.
+// to its own wave, the stall holds that wave only.  A wave keeps at most 63
+// vector-memory instructions (63 KiB of LDS-DMA) in flight, which caps one
+// loader wave near 70 GB/s per CU at L2 latency: the 80 x 256 conv stripes
+// (43 KiB per stage) take two loader waves (their DMA alone 28.8 -> 20.7 us).
 //
 // Per k-step kt both sides meet at one barrier: the loader has waited for
 // stage kt to land, the compute waves have finished reading stage kt - 1, so
 // after it the loader refills that buffer with stage kt + S - 1 while the
 // compute waves multiply stage kt.  The loader then takes part in the
 // epilogue's barriers (it has no rows of its own) and exits.
-// ALoad / BLoad are instantiated for THREADS = kWave and set up with the
-// loader's lane index.
+// ALoad / BLoad are instantiated for THREADS = LW * kWave and set up with the
+// thread's index within the loader waves.
 template <class T, class ALoad, class BLoad, class Epi>
-__global__ __launch_bounds__(T::kThreads + kWave) void gemm_spec_kernel(ALoad al, BLoad bl, Epi epi,
-                                                                        int M, int N, int K,
-                                                                        int tiles_n) {
+__global__ __launch_bounds__(T::kThreads + ALoad::kWaves * kWave) void gemm_spec_kernel(
+    ALoad al, BLoad bl, Epi epi, int M, int N, int K, int tiles_n) {
     constexpr int S = T::kStages;
     constexpr int kA = T::BM * T::BK, kB = T::BN * T::BK;  // elements per stage
     constexpr size_t kABBytes = (size_t)S * (kA + kB) * sizeof(bf16);
@@ -552,9 +554,9 @@ __global__ __launch_bounds__(T::kThreads + kWave) void gemm_spec_kernel(ALoad al
     const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nk = (K + T::BK - 1) / T::BK;
 
-    if (wave == T::WM * T::WN) {  // loader (wave-uniform branch)
-        al.setup(m0, lane);
-        bl.setup(n0, lane);
+    if (wave >= T::WM * T::WN) {  // loader (wave-uniform branch)
+        al.setup(m0, tid - T::kThreads);
+        bl.setup(n0, tid - T::kThreads);
         constexpr int P = ALoad::kIssue + BLoad::kIssue;
 #pragma unroll
         for (int st = 0; st < S - 1; ++st)
@@ -616,14 +618,16 @@ __global__ __launch_bounds__(T::kThreads + kWave) void gemm_spec_kernel(ALoad al
     store_tile<T>(acc, epi, smem, m0, n0, tid, pre);
 }
 
-// Loaders for the spec kernel are built with THREADS = kWave.
+// Loaders for the spec kernel are built with THREADS = LW * kWave, the same LW
+// for both.
 template <class T, class ALoad, class BLoad, class Epi>
 inline void launch_gemm_spec(const ALoad &al, const BLoad &bl, const Epi &epi, int M, int N, int K,
                              hipStream_t stream) {
-    static_assert(ALoad::kWaves == 1 && BLoad::kWaves == 1, "loaders of one wave");
+    static_assert(ALoad::kWaves == BLoad::kWaves, "both loaders span the same loader waves");
     const int tiles_m = (M + T::BM - 1) / T::BM, tiles_n = (N + T::BN - 1) / T::BN;
     hipLaunchKernelGGL((gemm_spec_kernel<T, ALoad, BLoad, Epi>), dim3(tiles_m * tiles_n),
-                       dim3(T::kThreads + kWave), 0, stream, al, bl, epi, M, N, K, tiles_n);
+                       dim3(T::kThreads + ALoad::kWaves * kWave), 0, stream, al, bl, epi, M, N,
+                       K, tiles_n);
 }
 
 // ---------------------------------------------------------------- epilogues

@@ -36,11 +36,11 @@ inline void linear_tile(const bf16 *x, const bf16 *w, int M, int N, int K, const
     launch_gemm_dma<T>(al, bl, epi, M, N, K, s);
 }
 
-template <class T, class Epi>
+template <class T, int LW = 1, class Epi>
 inline void linear_spec(const bf16 *x, const bf16 *w, int M, int N, int K, const Epi &epi,
                         hipStream_t s) {
-    DmaRowsBf16<T::BM, T::BK, kWave> al{x, K, M, K};
-    DmaRowsBf16<T::BN, T::BK, kWave> bl{w, K, N, K};
+    DmaRowsBf16<T::BM, T::BK, LW * kWave> al{x, K, M, K};
+    DmaRowsBf16<T::BN, T::BK, LW * kWave> bl{w, K, N, K};
     launch_gemm_spec<T>(al, bl, epi, M, N, K, s);
 }
 
