@@ -93,11 +93,11 @@ void run_conv_dma(const ConvLayer &l, const bf16 *a, int c0, const bf16 *b, int 
 
 // Wave-specialised LDS-DMA pipeline (gemm_spec_kernel) for the same convs,
 // with LW loader waves.
-template <class T, int K, int LW = 1, class Epi>
+template <class T, int K, int LW = 1, bool YFAST = false, class Epi>
 void run_conv_spec(const ConvLayer &l, const bf16 *a, int c0, const bf16 *b, int c1, const Epi &epi,
                    hipStream_t s) {
     const ConvGeom g = geom_of(l);
-    DmaConvNHWC<T::BM, T::BK, LW * kWave, K, K> al{a, b, c0, c1, g};
+    DmaConvNHWC<T::BM, T::BK, LW * kWave, K, K, YFAST> al{a, b, c0, c1, g};
     DmaRowsBf16<T::BN, T::BK, LW * kWave> bl{l.w, g.K, l.co, g.K};
     launch_gemm_spec<T>(al, bl, epi, g.M, l.co, g.K, s);
 }

@@ -11,15 +11,19 @@
 // steps and the N = 768, K >= 768 reductions one more stage of 128.  Where a
 // wider tile measured faster it is listed by (N, K): 128 x 64 for stage-1
 // qkv / fc2 and the first merge (M = 16896), 64 x 128 for stage-1 fc1,
-// stage-2 qkv and stage-3 fc1, 128 x 128 for stage-2 fc1.  (N, K)
+// stage-2 qkv and stage-3 fc1.  (N, K)
 // identifies the layer, so the table holds for any camera count; other shapes
 // take the 64-deep default.
 //
-// Three layers measured faster on the wave-specialised pipeline
-// (gemm_spec_kernel: one loader wave issues every DMA, so the compute waves'
-// MFMAs no longer wait behind a stalled DMA issue): stage-3 fc2 (64 x 64 x 128,
-// three stages: 13.8 vs 16.3 us), stage-2 fc2 (64 x 64 x 64, three stages:
-// 12.2 vs 12.6 us) and stage-3 proj (32 x 64 x 64, four stages: 6.0 vs 6.5 us).
+// Four layers measured faster on the wave-specialised pipeline
+// (gemm_spec_kernel: loader waves issue every DMA, so the compute waves'
+// MFMAs never wait behind a stalled DMA issue), each with four loader waves
+// (one wave's 63 in-flight DMA instructions cap its workgroup's fetch):
+// stage-2 fc1 (128 x 128 x 64, eight compute waves, two stages: 12.7 vs 14.0
+// us as 128 x 128 on the plain core), stage-2 fc2 (64 x 64 x 64, four stages:
+// 11.5 vs 11.9 us with one loader wave), stage-3 fc2 (64 x 64 x 128, three
+// stages: 12.8 vs 14.2 us with one loader wave, 16.3 us plain) and stage-3
+// proj (64 x 64 x 128, three stages: 5.6 vs 6.4 us as 32 x 64 with one).
 #pragma once
 
 #include <cstdint>
@@ -44,15 +48,15 @@ inline void linear_spec(const bf16 *x, const bf16 *w, int M, int N, int K, const
     launch_gemm_spec<T>(al, bl, epi, M, N, K, s);
 }
 
-enum LinearTile { kK32, kK64, kK128, kTall, kWide, kBig, kSpec64, kSpec128, kSpecNarrow };
+enum LinearTile { kK32, kK64, kK128, kTall, kWide, kSpecBig, kSpec64, kSpec128 };
 
 inline LinearTile pick_linear_tile(int N, int K) {
     struct Entry { int n, k; LinearTile t; };
     static const Entry table[] = {
-        {768, 3072, kSpec128}, {384, 1536, kSpec64}, {768, 768, kSpecNarrow}, {768, 1536, kK128},
+        {768, 3072, kSpec128}, {384, 1536, kSpec64}, {768, 768, kSpec128}, {768, 1536, kK128},
         {576, 192, kTall}, {192, 768, kTall},  {192, 384, kTall},
         {768, 192, kWide}, {1152, 384, kWide}, {3072, 768, kWide},
-        {1536, 384, kBig},
+        {1536, 384, kSpecBig},
     };
     for (const Entry &e : table)
         if (e.n == N && e.k == K) return e.t;
@@ -76,10 +80,9 @@ inline void linear_f16(const bf16 *x, const bf16 *w, int M, int N, int K, const 
         case kK128: linear_tile<DmaTile<64, 64, 128, 2, 2, 3, true>>(x, w, M, N, K, epi, s); break;
         case kTall: linear_tile<DmaTile<128, 64, 64, 2, 2, 2, true>>(x, w, M, N, K, epi, s); break;
         case kWide: linear_tile<DmaTile<64, 128, 64, 2, 2, 2, true>>(x, w, M, N, K, epi, s); break;
-        case kBig: linear_tile<DmaTile<128, 128, 64, 2, 2, 2, true>>(x, w, M, N, K, epi, s); break;
-        case kSpec64: linear_spec<DmaTile<64, 64, 64, 2, 2, 3, true>>(x, w, M, N, K, epi, s); break;
-        case kSpec128: linear_spec<DmaTile<64, 64, 128, 2, 2, 3, true>>(x, w, M, N, K, epi, s); break;
-        case kSpecNarrow: linear_spec<DmaTile<32, 64, 64, 1, 2, 4, true>>(x, w, M, N, K, epi, s); break;
+        case kSpecBig: linear_spec<DmaTile<128, 128, 64, 2, 4, 2, true>, 4>(x, w, M, N, K, epi, s); break;
+        case kSpec64: linear_spec<DmaTile<64, 64, 64, 2, 2, 4, true>, 4>(x, w, M, N, K, epi, s); break;
+        case kSpec128: linear_spec<DmaTile<64, 64, 128, 2, 2, 3, true>, 4>(x, w, M, N, K, epi, s); break;
     }
 }
 

@@ -569,23 +569,29 @@ int block_ops(int st, int b, int *ops) {
 // Patch merge after stage 1 or 2 with its LayerNorm over 4C folded: the A
 // operand gathers the 2x2 tokens from xh, the statistics combine the tokens'
 // group partials, and the epilogue writes the next stage's x, xh and stats.
-// Tiles as linear_f16 picks for these (N, K).
-template <int C, class T>
+// Tiles as linear_f16 picks for these (N, K); LW > 0 runs the tile on the
+// wave-specialised pipeline with LW loader waves (measured on MI355X for the
+// second merge, 1056 x 768 x 1536: 7.3 vs 8.9 us).
+template <int C, class T, int LW = 0>
 void merge_folded(bf_cuda_swin *s, int st, hipStream_t stream) {
     const int B = (int)s->batches, H = s->h[st], W = s->w[st];
     const int T2 = B * s->h[st + 1] * s->w[st + 1];
-    DmaMergeRows<T::BM, T::BK, T::kThreads, C> al{};
+    constexpr int kLoadThreads = LW > 0 ? LW * kWave : T::kThreads;
+    DmaMergeRows<T::BM, T::BK, kLoadThreads, C> al{};
     al.base = s->xh[st & 1];
     al.batches = B;
     al.H = H;
     al.W = W;
-    DmaRowsBf16<T::BN, T::BK, T::kThreads> bl{s->merge_w[st], 4 * C, 2 * C, 4 * C};
+    DmaRowsBf16<T::BN, T::BK, kLoadThreads> bl{s->merge_w[st], 4 * C, 2 * C, 4 * C};
     const int nx = (st + 1) & 1;
     using Src = LnMerge<C / kStatCols>;
     EpiStatsRows<true, false, Src> epi{s->x,          s->xh[nx],     s->stats[nx],
                                        s->merge_d[st], s->merge_c[st], Src{s->stats[st & 1], H, W},
                                        T2,            2 * C};
-    launch_gemm_dma<T>(al, bl, epi, T2, 2 * C, 4 * C, stream);
+    if constexpr (LW > 0)
+        launch_gemm_spec<T>(al, bl, epi, T2, 2 * C, 4 * C, stream);
+    else
+        launch_gemm_dma<T>(al, bl, epi, T2, 2 * C, 4 * C, stream);
 }
 
 void merge_op(bf_cuda_swin *s, int st, hipStream_t stream) {
@@ -600,7 +606,7 @@ void merge_op(bf_cuda_swin *s, int st, hipStream_t stream) {
     } else if (st == 1) {
         merge_folded<192, DmaTile<64, 64, 64, 2, 2, 2, true>>(s, st, stream);
     } else {
-        merge_folded<384, DmaTile<64, 64, 128, 2, 2, 3, true>>(s, st, stream);
+        merge_folded<384, DmaTile<64, 64, 128, 2, 2, 3, true>, 4>(s, st, stream);
     }
 }
 
