@@ -77,15 +77,23 @@ struct EpiDeconv2x2 {
 // (block0.0 / block0.1 / shared / block1.1): 27.9 / 18.4 / 53.9 / 19.3 us vs
 // 30.6 / 18.8 / 56.5 / 22.0 us on the plain core (64 x 128, 64 x 64 at half
 // resolution).  The 1x1 deblock, the transposed deblock and the 10-channel
-// heatmap output keep the plain core; the fuser a register-fed 128 x 128 tile
-// (336 input channels are not a multiple of the DMA k-tile).  Every tile sums
-// k in the same order, so the choice does not change results.
+// heatmap output keep the plain core.  Every tile sums k in the same order,
+// so the choice does not change results.
+// The fuser's 336 input channels are not a multiple of the 64-deep DMA k-tile:
+// its packed input is stored with a row stride of kFuserPad = 384 channels
+// (336..383 zero, written once at create) and its weights carry zero input
+// channels 336..383, so each 3x3 tap is six 64-deep k-steps (the zeros add
+// exact zeros, at 1.14x the MFMA work).  As 128 x 256 tiles (eight waves of
+// 64 x 64, three stages, four loader waves; 254 tiles at 180 x 180, one per
+// CU) it measured 56.5 us on MI355X vs 94.5 us for the register-fed 128 x 128
+// tile over the 336 channels.
 using DFull = DmaTile<64, 128, 64, 2, 2, 2, true>;
 using DHalf = DmaTile<64, 64, 64, 2, 2, 2, true>;
 using SFull = DmaTile<160, 128, 64, 2, 4, 3, true>;
 using SHalf = DmaTile<64, 128, 64, 2, 2, 3, true>;
+using SFuser = DmaTile<128, 256, 64, 2, 4, 3, true>;
 constexpr int kLoaders = 4;
-using TFuser = Tile<128, 128, 64, 2, 2, true>;
+constexpr int kFuserIn = 336, kFuserPad = 384;
 
 }  // namespace
 
@@ -95,7 +103,7 @@ struct bf_cuda_bev_stage {
     ConvLayer L[kConvs];
     const bf16 *deconv_w;  // [4 * 256][256]: row (dy * 2 + dx) * 256 + co, column ci
     const float *deconv_b;
-    // Channels-last fp16 maps: packed input (336), ping-pong (<= 256),
+    // Channels-last fp16 maps: packed input (336 in rows of 384), ping-pong (<= 256),
     // deblock outputs (256 each, read together by the shared conv), shared.
     bf16 *in, *pa, *pb, *s0, *s1, *sh;
 };
@@ -163,10 +171,20 @@ int build(bf_cuda_bev_stage *s, const bf_model *model, char *error, size_t cap) 
         const Spec &sp = spec[i];
         if (!fold_conv(model, sp.w, sp.b, sp.bn, sp.ci, sp.co, sp.k, kBevBnEps, fw, fb, error, cap))
             return 0;
+        int ci = sp.ci;
+        if (i == kFuser) {
+            // [Co][3x3][336] -> [Co][3x3][384], zero input channels past 336.
+            std::vector<float> padded((size_t)sp.co * 9 * kFuserPad, 0.0f);
+            for (size_t r = 0; r < (size_t)sp.co * 9; ++r)
+                std::copy(fw.begin() + r * sp.ci, fw.begin() + (r + 1) * sp.ci,
+                          padded.begin() + r * kFuserPad);
+            fw.swap(padded);
+            ci = kFuserPad;
+        }
         wo[i] = arena.add_f16(fw);
         bo[i] = arena.add_f32(fb);
         ConvLayer &l = s->L[i];
-        l.ci = sp.ci; l.co = sp.co; l.k = sp.k; l.stride = sp.stride; l.pad = sp.pad;
+        l.ci = ci; l.co = sp.co; l.k = sp.k; l.stride = sp.stride; l.pad = sp.pad;
         l.n = 1; l.ih = sp.ih; l.iw = sp.iw;
         l.oh = (sp.ih + 2 * sp.pad - sp.k) / sp.stride + 1;
         l.ow = (sp.iw + 2 * sp.pad - sp.k) / sp.stride + 1;
@@ -186,7 +204,7 @@ int build(bf_cuda_bev_stage *s, const bf_model *model, char *error, size_t cap) 
     s->deconv_b = (const float *)(s->params + db);
 
     const size_t hw = (size_t)H * W;
-    const size_t elems[6] = {336 * hw, 256 * hw, 256 * hw, 256 * hw, 256 * hw, 128 * hw};
+    const size_t elems[6] = {kFuserPad * hw, 256 * hw, 256 * hw, 256 * hw, 256 * hw, 128 * hw};
     bf16 **slots[6] = {&s->in, &s->pa, &s->pb, &s->s0, &s->s1, &s->sh};
     size_t total = 0, offs[6];
     for (int i = 0; i < 6; ++i) {
@@ -196,16 +214,18 @@ int build(bf_cuda_bev_stage *s, const bf_model *model, char *error, size_t cap) 
     if (!hip_ok(hipMalloc(&s->acts, total), error, cap, "allocate BEV activations")) return 0;
     s->resident_bytes += total;
     for (int i = 0; i < 6; ++i) *slots[i] = (bf16 *)(s->acts + offs[i]);
-    return 1;
+    // The packed input's padding channels are never written by a kernel: zero
+    // the map once.
+    return hip_ok(hipMemset(s->in, 0, elems[0] * 2), error, cap, "clear the packed BEV input");
 }
 
 void forward_impl(bf_cuda_bev_stage *s, const float *input, float *spatial, float *shared,
                   float *heatmap, hipStream_t st) {
     const int H = (int)s->h, W = (int)s->w, H2 = H / 2, W2 = W / 2;
     const size_t hw = (size_t)H * W;
-    pack_nhwc(input, s->in, 1, 336, H * W, st, true);
-    run_conv<TFuser, 3, 3>(s->L[kFuser], SrcNHWC{s->in, 336, H, W},
-                           nhwc_to(s->L[kFuser], s->pa, true), st);
+    pack_nhwc(input, s->in, 1, kFuserIn, H * W, st, true, kFuserPad);
+    run_conv_spec<SFuser, 3, kLoaders>(s->L[kFuser], s->in, kFuserPad, nullptr, 0,
+                                       nhwc_to(s->L[kFuser], s->pa, true), st);
     bf16 *cur = s->pa, *nxt = s->pb;
     for (int l = 0; l < 6; ++l) {
         const ConvLayer &c = s->L[kBlock0 + l];
