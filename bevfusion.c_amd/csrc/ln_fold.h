@@ -248,18 +248,15 @@ struct EpiPatchNorms {
             s += (v[i] + v[i + 1]) + (v[i + 2] + v[i + 3]);
         }
         normalise(v, s, g0, b0, c0);
-        float u[kHalf];
+        // x rows back into the tile, then LN1 of them in place (one row half
+        // of registers live instead of two).
         s = 0.0f;
 #pragma unroll
-        for (int i = 0; i < kHalf; ++i) {
-            u[i] = v[i];
-            s += v[i];
-        }
-        normalise(u, s, g1, b1, c0);
-        // x rows back into the tile (the second LN is in registers).
+        for (int i = 0; i < kHalf; ++i) s += v[i];
 #pragma unroll
         for (int i = 0; i < kHalf; i += 4)
             *reinterpret_cast<float4 *>(rowp + i) = make_float4(v[i], v[i + 1], v[i + 2], v[i + 3]);
+        normalise(v, s, g1, b1, c0);
         lds_barrier();
         const int rows = min(T::BM, M - m0);
         float *xo = x + (size_t)m0 * C;
@@ -275,7 +272,7 @@ struct EpiPatchNorms {
         for (int i = 0; i < kHalf; i += 8) {
             bf16x8 o;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) o[e] = to_half(u[i + e]);
+            for (int e = 0; e < 8; ++e) o[e] = to_half(v[i + e]);
             *reinterpret_cast<bf16x8 *>(hrow + i) = o;
         }
         lds_barrier();
