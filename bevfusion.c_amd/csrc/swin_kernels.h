@@ -405,7 +405,7 @@ static __global__ __launch_bounds__(256) void window_attention_kernel(
 // (padded) row yields the bias, as in the unfused path.  The q, k, v rows
 // never reach HBM.
 template <int C>
-__global__ __launch_bounds__(64 * (C / 32)) void window_msa_kernel(
+__global__ __launch_bounds__(64 * (C / 32)) __attribute__((amdgpu_waves_per_eu(C == 96 ? 3 : 2))) void window_msa_kernel(
     const bf16 *xn, const bf16 *__restrict__ wqkv, const float *__restrict__ bqkv,
     const bf16 *__restrict__ term, bf16 *out, int H, int W, int wy_n, int wx_n, int shift) {
     // xn and out may be the same buffer: a window's rows are all read (into
@@ -431,12 +431,6 @@ __global__ __launch_bounds__(64 * (C / 32)) void window_msa_kernel(
         *reinterpret_cast<bf16x8 *>(sX + r * XS + 8 * q) = v;
     }
 
-    // Score terms of this window type and head (global loads, in flight
-    // across the barrier).
-    const bf16 *tp = term + ((size_t)(window_type(wy, wx, wy_n, wx_n, shift) * HEADS + h) * 512 + lane) * 8;
-    bf16x8 add[8];
-#pragma unroll
-    for (int c = 0; c < 8; ++c) add[c] = *reinterpret_cast<const bf16x8 *>(tp + c * 512);
     int tok[4];
 #pragma unroll
     for (int b = 0; b < 4; ++b) tok[b] = window_token(16 * b + l16, n, wy, wx, H, W, Hp, Wp, shift);
@@ -493,6 +487,13 @@ __global__ __launch_bounds__(64 * (C / 32)) void window_msa_kernel(
             const int ch = (e < 4 ? 0 : 16) + 4 * g + (e & 3);
             Vt[ch * VS + 16 * b + l16] = vf[b][e];
         }
+    // Score terms of this window type and head, loaded only now so that their
+    // 32 registers are not held through the projections (three waves per
+    // SIMD need the kernel under 168 VGPRs).
+    const bf16 *tp = term + ((size_t)(window_type(wy, wx, wy_n, wx_n, shift) * HEADS + h) * 512 + lane) * 8;
+    bf16x8 add[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) add[c] = *reinterpret_cast<const bf16x8 *>(tp + c * 512);
     attend_store(qf, kf, add, Vt, tok, out, C, h, lane);
 }
 
