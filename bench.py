@@ -173,9 +173,8 @@ def swin_op_cost(stage, op, b=6):
         h2, w2 = SWIN_STAGES[stage + 1][:2]
         t2 = b * h2 * w2
         out = t2 * 2 * c * (4 + 2) + t2 * (2 * c // 64) * 8  # x, fp16 copy, statistics
-        if stage == 0:  # LayerNorm kernel over 4C, then the reduction GEMM
-            return 2.0 * t2 * 4 * c * 2 * c, t * c * 4 + 2 * t2 * 4 * c * 2 + 8 * c * c * 2 + out
-        # LayerNorm folded: 2x2 tokens gathered from the fp16 copy
+        # LayerNorm folded: 2x2 tokens gathered from the fp16 copy and their
+        # statistics (one 96-channel group per token at stage 0: st_b holds)
         return 2.0 * t2 * 4 * c * 2 * c, t * c * 2 + st_b + 8 * c * c * 2 + out
     raise ValueError(op)
 

@@ -28,9 +28,10 @@ namespace bfhip {
 
 constexpr int kStatCols = 64;  // columns per statistics group
 
-// Combines equal-count (mean, M2) group partials in index order into
-// (mean, 1/sqrt(var + 1e-5)); absent groups are passed as (0, 0).
-template <int N>
+// Combines equal-count (mean, M2) group partials of COLS columns each in
+// index order into (mean, 1/sqrt(var + 1e-5)); absent groups are passed as
+// (0, 0).
+template <int N, int COLS = kStatCols>
 __device__ __forceinline__ float2 ln_combine(const float2 (&p)[N]) {
     float s = 0.0f;
 #pragma unroll
@@ -43,7 +44,7 @@ __device__ __forceinline__ float2 ln_combine(const float2 (&p)[N]) {
         m2 += p[g].y;
         dev += d * d;
     }
-    const float var = (m2 + (float)kStatCols * dev) * (1.0f / (kStatCols * N));
+    const float var = (m2 + (float)COLS * dev) * (1.0f / (COLS * N));
     return make_float2(mean, rsqrtf(var + 1e-5f));
 }
 
@@ -66,10 +67,10 @@ struct LnRows {
 };
 
 // Patch-merge row (n, oy, ox): its 2x2 source tokens of the previous stage
-// ([B, H, W] tokens, G groups each), taps q = 2 dy + dx in order; a tap past
-// an odd edge is a token of zeros (mean 0, M2 0), as the zero padding before
-// the reference's unfold (swin_backbone.c:278-302).
-template <int G>
+// ([B, H, W] tokens, G groups of COLS columns each), taps q = 2 dy + dx in
+// order; a tap past an odd edge is a token of zeros (mean 0, M2 0), as the
+// zero padding before the reference's unfold (swin_backbone.c:278-302).
+template <int G, int COLS = kStatCols>
 struct LnMerge {
     static constexpr int kGroups = G;
     struct Pre { float2 p[4 * G]; };
@@ -89,7 +90,7 @@ struct LnMerge {
         }
         return r;
     }
-    __device__ float2 finish(const Pre &r) const { return ln_combine(r.p); }
+    __device__ float2 finish(const Pre &r) const { return ln_combine<4 * G, COLS>(r.p); }
 };
 
 struct LnNone {  // producers that take no LayerNorm on their input

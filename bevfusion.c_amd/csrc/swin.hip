@@ -2,8 +2,8 @@
 //
 // Data layout in HBM:
 //   x    fp32 [tokens, C]   residual stream, NHWC token order, in place
-//   xn   fp16 [tokens, C]   LayerNorm output -> QKV input; reused for the
-//                           attention output and for the 2x2 merge rows
+//   xn   fp16 [tokens, C]   stage 0: LayerNorm output -> fused W-MSA input,
+//                           reused for the attention output
 //   big  fp16 [tokens, 4C]  QKV [tokens, 3C], later the GELU hidden [tokens, 4C]
 // Window partitioning never materialises: the attention kernel gathers its 49
 // (padded, cyclically shifted) tokens straight from the token-major QKV rows
@@ -14,11 +14,15 @@
 // the attention run on the fp16 MFMA with fp32 accumulation.
 //
 //   xh   fp16 [tokens, C]   stages 1-3: fp16 copy of x, the A operand of the
-//                           LN-folded QKV / fc1 linears (ln_fold.h); two
-//                           buffers, alternating per stage, because the patch
-//                           merge reads one stage's copy while writing the next
+//                           LN-folded QKV / fc1 linears and patch merges
+//                           (ln_fold.h); two buffers, alternating per stage,
+//                           because a merge reads one stage's copy while
+//                           writing the next (stage 0's copy, for its merge
+//                           only, is written over xn)
 //   stats float2 [tokens, C/64] (mean, M2) of x per 64-channel group, written
-//                           with x, read by the LN-folded linears (two, like xh)
+//                           with xh, read by the LN-folded linears (two, like
+//                           xh; stage 0's, one group of all 96 channels, at the
+//                           front of big)
 //
 // Per block at stages 1-3: QKV GEMM(LN1 folded, fp16) -> window attention ->
 // proj GEMM(+bias, += into x; writes xh and stats) -> fc1 GEMM(LN2 folded,
@@ -26,10 +30,10 @@
 // LayerNorm pass.  Stage 0 (C = 96) runs LN2 -> fc1 -> GELU -> fc2 ->
 // residual as one fused kernel whose hidden layer stays on chip (swin_mlp.h),
 // with the proj GEMM and its residual fused in front; it also writes the next
-// block's LN1 output, and the patch embedding's epilogue writes block 0's, so
-// stage 0 launches no LayerNorm either.  The patch merges after stages 1 and 2
-// fold their LayerNorm over 4C the same way, reading the 2x2 tokens straight
-// from xh; the one after stage 0 keeps its LayerNorm kernel.
+// block's LN1 output (the last block: xh and the row statistics), and the
+// patch embedding's epilogue writes block 0's, so stage 0 launches no
+// LayerNorm either.  The three patch merges fold their LayerNorm over 4C the
+// same way, reading the 2x2 tokens straight from xh.
 #include "bf_cuda_swin.h"
 #include "bfhip_debug.h"
 #include "bfhip_profile.h"
@@ -92,8 +96,8 @@ struct bf_cuda_swin {
     const bf16 *patch_w;
     const float *patch_b, *patch_ns, *patch_nb;
     BlockW blocks[4][6];
-    const float *merge_s[3], *merge_b[3], *out_s[3], *out_b[3];
-    const bf16 *merge_w[3];           // merges 1, 2: LN-folded, columns in tap-major order
+    const float *out_s[3], *out_b[3];
+    const bf16 *merge_w[3];           // LN-folded, columns in tap-major order
     const float *merge_c[3], *merge_d[3];
     float *x;
     bf16 *xn, *big;
@@ -102,20 +106,6 @@ struct bf_cuda_swin {
 };
 
 namespace {
-
-void launch_merge(int C, const float *x, bf16 *y, const float *g, const float *b, int batches,
-                  int H, int W, hipStream_t s) {
-    const int rows = batches * ((H + 1) / 2) * ((W + 1) / 2);
-#define BF_MERGE(CC)                                                                         \
-    case CC: {                                                                               \
-        const int per_block = (64 / ((CC % 64 == 0) ? 64 : 32)) * 4;                         \
-        hipLaunchKernelGGL((merge_ln_kernel<CC>), dim3((rows + per_block - 1) / per_block),  \
-                           dim3(256), 0, s, x, y, g, b, batches, H, W);                      \
-        break;                                                                               \
-    }
-    switch (C) { BF_MERGE(96) default: break; }  // merges 1 and 2 fold their LayerNorm
-#undef BF_MERGE
-}
 
 // A linear fed by a LayerNorm, folded (ln_fold.h): W'[j][kk] =
 // fp16(g[k] W[j][k]) with k = perm(kk) (identity when perm is null),
@@ -199,7 +189,7 @@ static int swin_build(bf_cuda_swin *s, const bf_model *model, size_t batches, si
     char name[224];
     size_t o_patch_w, o_patch_b, o_patch_ns, o_patch_nb;
     BlockOff off[4][6];
-    size_t o_ms[3], o_mb[3], o_mw[3], o_os[3], o_ob[3], o_mc[3] = {}, o_md[3] = {};
+    size_t o_mw[3], o_os[3], o_ob[3], o_mc[3] = {}, o_md[3] = {};
     {
         const float *pw = bind_f32(model, "image_backbone.patch_embed.projection.weight",
                                    {96, 3, 4, 4}, error, cap);
@@ -301,20 +291,14 @@ static int swin_build(bf_cuda_swin *s, const bf_model *model, size_t batches, si
         std::snprintf(name, sizeof(name), "image_backbone.norm%d.bias", st + 1);
         const float *ob = bind_f32(model, name, {(uint32_t)kC[st + 1]}, error, cap);
         if (!ms || !mb || !mw || !os || !ob) return 0;
-        o_ms[st] = arena.add_f32(ms, 4 * c);
-        o_mb[st] = arena.add_f32(mb, 4 * c);
-        if (st == 0) {
-            o_mw[st] = arena.add_f16(mw, (size_t)8 * c * c);
-        } else {
-            // Folded column q*C + ch reads unfold column ch*4 + q (DmaMergeRows).
-            std::vector<int> perm(4 * c);
-            for (uint32_t q = 0; q < 4; ++q)
-                for (uint32_t ch = 0; ch < c; ++ch) perm[q * c + ch] = (int)(ch * 4 + q);
-            const FoldedLinear fm = fold_ln(mw, nullptr, ms, mb, 2 * c, 4 * c, &perm);
-            o_mw[st] = arena.add(fm.w.data(), fm.w.size() * 2);
-            o_mc[st] = arena.add_f32(fm.c);
-            o_md[st] = arena.add_f32(fm.d);
-        }
+        // Folded column q*C + ch reads unfold column ch*4 + q (DmaMergeRows).
+        std::vector<int> perm(4 * c);
+        for (uint32_t q = 0; q < 4; ++q)
+            for (uint32_t ch = 0; ch < c; ++ch) perm[q * c + ch] = (int)(ch * 4 + q);
+        const FoldedLinear fm = fold_ln(mw, nullptr, ms, mb, 2 * c, 4 * c, &perm);
+        o_mw[st] = arena.add(fm.w.data(), fm.w.size() * 2);
+        o_mc[st] = arena.add_f32(fm.c);
+        o_md[st] = arena.add_f32(fm.d);
         o_os[st] = arena.add_f32(os, kC[st + 1]);
         o_ob[st] = arena.add_f32(ob, kC[st + 1]);
     }
@@ -345,10 +329,9 @@ static int swin_build(bf_cuda_swin *s, const bf_model *model, size_t batches, si
                 w.attn_term = H(o.attn_term);
             }
         for (int st = 0; st < 3; ++st) {
-            s->merge_s[st] = F(o_ms[st]); s->merge_b[st] = F(o_mb[st]);
             s->merge_w[st] = H(o_mw[st]); s->out_s[st] = F(o_os[st]); s->out_b[st] = F(o_ob[st]);
-            s->merge_c[st] = st ? F(o_mc[st]) : nullptr;
-            s->merge_d[st] = st ? F(o_md[st]) : nullptr;
+            s->merge_c[st] = F(o_mc[st]);
+            s->merge_d[st] = F(o_md[st]);
         }
         // Attention score terms (relative bias + shift mask, in the kernel's
         // accumulator order) from the uploaded bias matrices.
@@ -370,6 +353,10 @@ static int swin_build(bf_cuda_swin *s, const bf_model *model, size_t batches, si
         for (int st = 0; st < 4; ++st) {
             const size_t t = batches * (size_t)s->h[st] * s->w[st];
             x_elems = std::max(x_elems, t * kC[st]);
+            // Stage 0's copy and statistics (one group of all 96 channels per
+            // token) live in xn and big, which are free when it ends; the
+            // activation layout is that of stages 1-3 alone (changing it
+            // measured up to 9 us per frame slower).
             if (st > 0) {
                 xh_elems = std::max(xh_elems, t * kC[st]);
                 stat_elems = std::max(stat_elems, t * (kC[st] / kStatCols));
@@ -459,6 +446,15 @@ void patch_embed(bf_cuda_swin *s, const float *images, hipStream_t stream) {
     }
 }
 
+// The fp16 copy of x and its row statistics that stage st's folded consumers
+// read: xh / stats of its parity at stages 1-3; at stage 0, whose last block
+// writes them for the merge only, xn (the attention rows it overwrites in
+// place) and the front of big (free then).
+bf16 *stage_xh(bf_cuda_swin *s, int st) { return st ? s->xh[st & 1] : s->xn; }
+float2 *stage_stats(bf_cuda_swin *s, int st) {
+    return st ? s->stats[st & 1] : reinterpret_cast<float2 *>(s->big);
+}
+
 // Calls f(std::integral_constant<int, C / 64>) for the channel counts of
 // stages 1-3 (the statistics groups per token).
 template <class F>
@@ -530,13 +526,16 @@ void block_op(bf_cuda_swin *s, int st, int b, int op, hipStream_t stream) {
             break;
         case BFHIP_SWIN_MLP: {
             // The next block's LN1 is fused into the epilogue; the last block
-            // of the stage feeds the merge / stage output, which read x.
+            // of the stage writes xh and the row statistics for the patch
+            // merge, which folds its LayerNorm (x itself is not read again).
             const bool next = b + 1 < kDepth[st];
             const BlockW *nw = next ? &s->blocks[st][b + 1] : nullptr;
             // proj reads the attention output in xn; LN1' overwrites it row by row.
             launch_swin_mlp<MlpS0>(s->x, s->xn, w.mlp_proj, w.proj_b, w.n2s, w.n2b, w.mlp_w,
                                    w.fc1_b, w.fc2_b, nw ? nw->n1s : nullptr,
-                                   nw ? nw->n1b : nullptr, next ? s->xn : nullptr, T, stream);
+                                   nw ? nw->n1b : nullptr, next ? s->xn : nullptr, T, stream,
+                                   next ? nullptr : stage_xh(s, st),
+                                   next ? nullptr : stage_stats(s, st));
             break;
         }
         default:
@@ -566,10 +565,11 @@ int block_ops(int st, int b, int *ops) {
     return n;
 }
 
-// Patch merge after stage 1 or 2 with its LayerNorm over 4C folded: the A
-// operand gathers the 2x2 tokens from xh, the statistics combine the tokens'
-// group partials, and the epilogue writes the next stage's x, xh and stats.
-// Tiles as linear_f16 picks for these (N, K); LW > 0 runs the tile on the
+// Patch merge after stage st with its LayerNorm over 4C folded: the A operand
+// gathers the 2x2 tokens from xh, the statistics combine the tokens' group
+// partials (groups of 64 channels, or the whole 96-channel token at stage 0),
+// and the epilogue writes the next stage's x, xh and stats.  Tiles as
+// linear_f16 picks for these (N, K); LW > 0 runs the tile on the
 // wave-specialised pipeline with LW loader waves (measured on MI355X for the
 // second merge, 1056 x 768 x 1536: 7.3 vs 8.9 us).
 template <int C, class T, int LW = 0>
@@ -578,15 +578,16 @@ void merge_folded(bf_cuda_swin *s, int st, hipStream_t stream) {
     const int T2 = B * s->h[st + 1] * s->w[st + 1];
     constexpr int kLoadThreads = LW > 0 ? LW * kWave : T::kThreads;
     DmaMergeRows<T::BM, T::BK, kLoadThreads, C> al{};
-    al.base = s->xh[st & 1];
+    al.base = stage_xh(s, st);
     al.batches = B;
     al.H = H;
     al.W = W;
     DmaRowsBf16<T::BN, T::BK, kLoadThreads> bl{s->merge_w[st], 4 * C, 2 * C, 4 * C};
     const int nx = (st + 1) & 1;
-    using Src = LnMerge<C / kStatCols>;
+    constexpr bool kWhole = C % kStatCols != 0;  // one group per token
+    using Src = LnMerge<kWhole ? 1 : C / kStatCols, kWhole ? C : kStatCols>;
     EpiStatsRows<true, false, Src> epi{s->x,          s->xh[nx],     s->stats[nx],
-                                       s->merge_d[st], s->merge_c[st], Src{s->stats[st & 1], H, W},
+                                       s->merge_d[st], s->merge_c[st], Src{stage_stats(s, st), H, W},
                                        T2,            2 * C};
     if constexpr (LW > 0)
         launch_gemm_spec<T>(al, bl, epi, T2, 2 * C, 4 * C, stream);
@@ -595,19 +596,12 @@ void merge_folded(bf_cuda_swin *s, int st, hipStream_t stream) {
 }
 
 void merge_op(bf_cuda_swin *s, int st, hipStream_t stream) {
-    const int B = (int)s->batches, C = kC[st];
-    const int T2 = B * s->h[st + 1] * s->w[st + 1];
-    if (st == 0) {
-        launch_merge(C, s->x, s->xn, s->merge_s[st], s->merge_b[st], B, s->h[st], s->w[st], stream);
-        linear_f16(s->xn, s->merge_w[st], T2, 2 * C, 4 * C,
-                   EpiStatsRows<false, false>{s->x, s->xh[1], s->stats[1], nullptr, nullptr, {}, T2,
-                                              2 * C},
-                   stream);
-    } else if (st == 1) {
+    if (st == 0)
+        merge_folded<96, DmaTile<128, 64, 64, 2, 2, 2, true>>(s, st, stream);
+    else if (st == 1)
         merge_folded<192, DmaTile<64, 64, 64, 2, 2, 2, true>>(s, st, stream);
-    } else {
+    else
         merge_folded<384, DmaTile<64, 64, 128, 2, 2, 3, true>, 4>(s, st, stream);
-    }
 }
 
 }  // namespace

@@ -1,6 +1,6 @@
-// Swin-T building blocks on gfx950: the patch-merge gather with its LayerNorm,
-// the stage-output LayerNorm with NHWC->NCHW store, and batched shifted-
-// window attention on MFMA.  The Swin path's 16-bit operands (LayerNorm
+// Swin-T building blocks on gfx950: the stage-output LayerNorm with
+// NHWC->NCHW store and batched shifted-window attention on MFMA (the patch
+// merges run as LN-folded GEMMs, ln_fold.h).  The Swin path's 16-bit operands (LayerNorm
 // outputs, QKV, attention terms and output, MLP hidden, weights) are fp16
 // words held in the bf16 container type, multiplied on the fp16 MFMA with
 // fp32 accumulation.
@@ -30,56 +30,6 @@ __device__ __forceinline__ void store4(bf16 *p, float a, float b, float c, float
     bf16x4 v;  // fp16 words
     v[0] = to_half(a); v[1] = to_half(b); v[2] = to_half(c); v[3] = to_half(d);
     *reinterpret_cast<bf16x4 *>(p) = v;
-}
-
-// Patch merging: output row (n, oy, ox) is the 2x2 nn.Unfold of x[n,H,W,C]
-// with element order c*4 + ky*2 + kx (zero beyond odd edges; reference
-// swin_backbone.c:278-302, cuda_swin.cu:218-225), LayerNorm over 4C, fp16.
-template <int C>
-__global__ __launch_bounds__(256) void merge_ln_kernel(const float *x, bf16 *y, const float *g,
-                                                       const float *b, int batches, int H,
-                                                       int W) {
-    constexpr int LPR = (C % 64 == 0) ? 64 : 32;
-    constexpr int PER = C / LPR;  // channels per lane
-    constexpr int RPW = kWave / LPR;
-    const int lane = threadIdx.x & 63;
-    const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-    const int sub = lane / LPR, li = lane % LPR;
-    const int H2 = (H + 1) / 2, W2 = (W + 1) / 2, rows = batches * H2 * W2;
-    const int row = wave * RPW + sub;
-    const bool ok = row < rows;
-    const int rr = ok ? row : 0;
-    const int n = rr / (H2 * W2), p2 = rr - n * H2 * W2, oy = p2 / W2, ox = p2 - oy * W2;
-    float v[PER][4];
-    float s = 0.0f;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const int sy = 2 * oy + (q >> 1), sx = 2 * ox + (q & 1);
-        const bool in = ok && sy < H && sx < W;
-        const float *src = x + (((size_t)n * H + sy) * W + sx) * C;
-#pragma unroll
-        for (int p = 0; p < PER; ++p) {
-            v[p][q] = in ? src[li + p * LPR] : 0.0f;
-            s += v[p][q];
-        }
-    }
-    const float mean = group_sum<LPR>(s) * (1.0f / (4 * C));
-    float sq = 0.0f;
-#pragma unroll
-    for (int p = 0; p < PER; ++p)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) sq += (v[p][q] - mean) * (v[p][q] - mean);
-    const float rstd = rsqrtf(group_sum<LPR>(sq) * (1.0f / (4 * C)) + 1e-5f);
-    if (!ok) return;
-#pragma unroll
-    for (int p = 0; p < PER; ++p) {
-        const int e = (li + p * LPR) * 4;
-        const float4 gg = *reinterpret_cast<const float4 *>(g + e);
-        const float4 bb = *reinterpret_cast<const float4 *>(b + e);
-        store4(y + (size_t)row * 4 * C + e, (v[p][0] - mean) * rstd * gg.x + bb.x,
-               (v[p][1] - mean) * rstd * gg.y + bb.y, (v[p][2] - mean) * rstd * gg.z + bb.z,
-               (v[p][3] - mean) * rstd * gg.w + bb.w);
-    }
 }
 
 // Stage output: LayerNorm over C of tokens [n, HW, C], stored NCHW.  A block

@@ -2,6 +2,8 @@
 //   [x += proj(a) + b_proj]                      (PROJ: a = attention output)
 //   x += fc2(GELU(fc1(LN2(x)) + b1)) + b2
 //   xn = LN1'(x)                                  (optional: next block's LN1)
+//   or xh = fp16(x), stats = (mean, M2) of x      (optional: for a consumer
+//                                                  that folds its LayerNorm)
 // in one launch: x is read and written once, the 4C-wide hidden layer never
 // leaves the chip.
 //
@@ -112,7 +114,8 @@ __global__ __launch_bounds__(Cfg::kThreads) __attribute__((amdgpu_waves_per_eu(4
     float *__restrict__ x, const bf16 *attn, const bf16 *__restrict__ wproj,
     const float *__restrict__ bproj, const float *__restrict__ ln_g, const float *__restrict__ ln_b,
     const bf16 *__restrict__ wpk, const float *__restrict__ b1, const float *__restrict__ b2,
-    const float *__restrict__ next_g, const float *__restrict__ next_b, bf16 *xn, int T) {
+    const float *__restrict__ next_g, const float *__restrict__ next_b, bf16 *xn, int T,
+    bf16 *__restrict__ xh, float2 *__restrict__ stats) {
     // attn and xn may be the same buffer: each row is read (prologue) by the
     // lane group that later writes it (epilogue), so neither is __restrict__.
     constexpr int C = Cfg::C, TF = Cfg::TF, KS = Cfg::kKs, CF = Cfg::kCf;
@@ -282,7 +285,12 @@ __global__ __launch_bounds__(Cfg::kThreads) __attribute__((amdgpu_waves_per_eu(4
         }
     }
 
-    // Residual (+ LN1' of the next block): acc[j][i][e] is channel 16j + 4g + e.
+    // Residual, then one of (uniform for the whole launch):
+    //   xn = LN1'(x) of the next block, with x stored fp32;
+    //   xh = fp16 words of x and stats[t] = (mean, M2) over the row, for a
+    //   consumer that folds the next LayerNorm (the patch merge), x not stored;
+    //   x stored fp32 only.
+    // acc[j][i][e] is channel 16j + 4g + e.
 #pragma unroll
     for (int i = 0; i < TF; ++i) {
         const int t = tok0 + 16 * i + l16;
@@ -295,10 +303,10 @@ __global__ __launch_bounds__(Cfg::kThreads) __attribute__((amdgpu_waves_per_eu(4
             xr[i][j].y += acc[j][i][1];
             xr[i][j].z += acc[j][i][2];
             xr[i][j].w += acc[j][i][3];
-            if (ok) *reinterpret_cast<float4 *>(row + 16 * j) = xr[i][j];
+            if (ok && !xh) *reinterpret_cast<float4 *>(row + 16 * j) = xr[i][j];
             s += (xr[i][j].x + xr[i][j].y) + (xr[i][j].z + xr[i][j].w);
         }
-        if (!xn) continue;  // uniform: the next LayerNorm is fused or not for the whole launch
+        if (!xn && !xh) continue;
         s += __shfl_xor(s, 16);
         s += __shfl_xor(s, 32);
         const float mean = s * (1.0f / C);
@@ -311,6 +319,20 @@ __global__ __launch_bounds__(Cfg::kThreads) __attribute__((amdgpu_waves_per_eu(4
         }
         qs += __shfl_xor(qs, 16);
         qs += __shfl_xor(qs, 32);
+        if (xh) {
+            if (!ok) continue;
+            if (g == 0) stats[t] = make_float2(mean, qs);
+#pragma unroll
+            for (int j = 0; j < CF; ++j) {
+                bf16x4 o;
+                o[0] = to_half(xr[i][j].x);
+                o[1] = to_half(xr[i][j].y);
+                o[2] = to_half(xr[i][j].z);
+                o[3] = to_half(xr[i][j].w);
+                *reinterpret_cast<bf16x4 *>(xh + (size_t)t * C + 16 * j + 4 * g) = o;
+            }
+            continue;
+        }
         const float rstd = rsqrtf(qs * (1.0f / C) + 1e-5f);
         if (!ok) continue;
 #pragma unroll
@@ -328,14 +350,17 @@ __global__ __launch_bounds__(Cfg::kThreads) __attribute__((amdgpu_waves_per_eu(4
     }
 }
 
+// xn (with next_g / next_b) or xh (with stats) selects the epilogue above;
+// at most one of them is set.
 template <class Cfg>
 inline void launch_swin_mlp(float *x, const bf16 *attn, const bf16 *wproj, const float *bproj,
                             const float *ln_g, const float *ln_b, const bf16 *wpk,
                             const float *b1, const float *b2, const float *next_g,
-                            const float *next_b, bf16 *xn, int T, hipStream_t s) {
+                            const float *next_b, bf16 *xn, int T, hipStream_t s,
+                            bf16 *xh = nullptr, float2 *stats = nullptr) {
     hipLaunchKernelGGL((swin_mlp_kernel<Cfg>), dim3((T + Cfg::kTokens - 1) / Cfg::kTokens),
                        dim3(Cfg::kThreads), 0, s, x, attn, wproj, bproj, ln_g, ln_b, wpk, b1, b2,
-                       next_g, next_b, xn, T);
+                       next_g, next_b, xn, T, xh, stats);
 }
 
 }  // namespace bfhip
