@@ -10,8 +10,10 @@
 // per-wave tiles: 64 x 64 is the default, K = 96 layers run three 32-deep
 // steps and the N = 768, K >= 768 reductions one more stage of 128.  Where a
 // wider tile measured faster it is listed by (N, K): 128 x 64 for stage-1
-// qkv / fc2 and the first merge (M = 16896), 64 x 128 for stage-1 fc1,
-// stage-2 qkv and stage-3 fc1.  (N, K)
+// qkv / fc2 and the first merge (M = 16896), 64 x 128 for stage-2 qkv and
+// stage-3 fc1; stage-1 fc1 (1584 tiles of 64 x 128) as 32-deep k-steps in
+// three stages, whose 36 KiB of LDS let four workgroups share a CU (1.55
+// rounds instead of 2.06 at three: 18.9 vs 19.7 us).  (N, K)
 // identifies the layer, so the table holds for any camera count; other shapes
 // take the 64-deep default.
 //
@@ -48,14 +50,14 @@ inline void linear_spec(const bf16 *x, const bf16 *w, int M, int N, int K, const
     launch_gemm_spec<T>(al, bl, epi, M, N, K, s);
 }
 
-enum LinearTile { kK32, kK64, kK128, kTall, kWide, kSpecBig, kSpec64, kSpec128 };
+enum LinearTile { kK32, kK64, kK128, kTall, kWide, kWide32, kSpecBig, kSpec64, kSpec128 };
 
 inline LinearTile pick_linear_tile(int N, int K) {
     struct Entry { int n, k; LinearTile t; };
     static const Entry table[] = {
         {768, 3072, kSpec128}, {384, 1536, kSpec64}, {768, 768, kSpec128}, {768, 1536, kK128},
         {576, 192, kTall}, {192, 768, kTall},  {192, 384, kTall},
-        {768, 192, kWide}, {1152, 384, kWide}, {3072, 768, kWide},
+        {768, 192, kWide32}, {1152, 384, kWide}, {3072, 768, kWide},
         {1536, 384, kSpecBig},
     };
     for (const Entry &e : table)
@@ -80,6 +82,7 @@ inline void linear_f16(const bf16 *x, const bf16 *w, int M, int N, int K, const 
         case kK128: linear_tile<DmaTile<64, 64, 128, 2, 2, 3, true>>(x, w, M, N, K, epi, s); break;
         case kTall: linear_tile<DmaTile<128, 64, 64, 2, 2, 2, true>>(x, w, M, N, K, epi, s); break;
         case kWide: linear_tile<DmaTile<64, 128, 64, 2, 2, 2, true>>(x, w, M, N, K, epi, s); break;
+        case kWide32: linear_tile<DmaTile<64, 128, 32, 2, 2, 3, true>>(x, w, M, N, K, epi, s); break;
         case kSpecBig: linear_spec<DmaTile<128, 128, 64, 2, 4, 2, true>, 4>(x, w, M, N, K, epi, s); break;
         case kSpec64: linear_spec<DmaTile<64, 64, 64, 2, 2, 4, true>, 4>(x, w, M, N, K, epi, s); break;
         case kSpec128: linear_spec<DmaTile<64, 64, 128, 2, 2, 3, true>, 4>(x, w, M, N, K, epi, s); break;
