@@ -7,21 +7,9 @@
 #pragma once
 
 #include "hip_common.h"
+#include "ln_fold.h"
 
 namespace bfhip {
-
-// ------------------------------------------------------------ LayerNorm rows
-// Row layout of a C-channel LayerNorm across a wave: LPR lanes per row
-// (largest power of two <= 64 dividing C/4), PER float4 per lane.
-template <int C>
-struct RowLayout {
-    static constexpr int V4 = C / 4;
-    static constexpr int LPR = (V4 % 64 == 0) ? 64 : (V4 % 32 == 0) ? 32 : (V4 % 16 == 0) ? 16
-                             : (V4 % 8 == 0) ? 8 : (V4 % 4 == 0) ? 4 : (V4 % 2 == 0) ? 2 : 1;
-    static constexpr int PER = V4 / LPR;
-    static constexpr int RPW = kWave / LPR;
-    static_assert(C % 4 == 0, "channels must be a multiple of 4");
-};
 
 __device__ __forceinline__ void store4(float *p, float a, float b, float c, float d) {
     *reinterpret_cast<float4 *>(p) = make_float4(a, b, c, d);
@@ -32,57 +20,72 @@ __device__ __forceinline__ void store4(bf16 *p, float a, float b, float c, float
     *reinterpret_cast<bf16x4 *>(p) = v;
 }
 
-// Stage output: LayerNorm over C of tokens [n, HW, C], stored NCHW.  A block
-// normalises kRows consecutive tokens into LDS, then writes kRows-token runs
-// of each channel plane (reference store_output, swin_backbone.c:265-276).
-// kRows is chosen per stage so the grid has several hundred blocks.
-template <int C, int kRows>
-__global__ __launch_bounds__(256) void out_ln_kernel(const float *x, float *out, const float *g,
-                                                     const float *b, int rows, int hw) {
-    using L = RowLayout<C>;
-    __shared__ float tile[C * (kRows + 1)];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int sub = lane / L::LPR, li = lane % L::LPR;
-    const int row0 = blockIdx.x * kRows;
-    // `base` is uniform across the wave, so every lane group runs the same
-    // number of iterations and its shuffles see only active lanes.
-    for (int base = wave * L::RPW; base < kRows; base += 4 * L::RPW) {
-        const int r = base + sub, row = row0 + r;
-        const bool ok = row < rows && r < kRows;
-        float4 v[L::PER];
-        float s = 0.0f;
+// Stage output: LayerNorm over C = 64 G channels of tokens [n, hw, C], stored
+// NCHW (reference store_output, swin_backbone.c:265-276).  The row statistics
+// are the (mean, M2) partials per 64-channel group that the stage's last
+// residual writer left in `stats` (row r: stats[r * G + g]), so a block can
+// own a kR-token x 64-channel tile: it reads the tile as 256-byte row
+// segments, normalises it into LDS transposed, and writes kR-token runs of
+// each of its 64 channel planes, as float4 when `vec` (hw % 4 == 0 and out
+// 16-byte aligned: four tokens from a multiple of 4 never straddle two
+// images), else per element.  Grid (ceil(rows / kR), G), 256 threads.
+template <int G, int kR>
+__global__ __launch_bounds__(256) void out_ln_kernel(const float *x, const float2 *stats,
+                                                     float *out, const float *g, const float *b,
+                                                     int rows, int hw, bool vec) {
+    constexpr int C = G * kStatCols;
+    static_assert(kR % 16 == 0 && kR <= 256, "tile rows");
+    __shared__ float tile[kStatCols][kR + 1];
+    __shared__ float2 norm[kR];
+    const int tid = threadIdx.x;
+    const int row0 = blockIdx.x * kR, c0 = blockIdx.y * kStatCols;
+    // The x tile and the statistics are loaded together, then combined.
+    constexpr int kPer = kR / 16;  // rows per thread: tid / 16, + 16, ...
+    const int q = 4 * (tid & 15), r0 = tid >> 4;
+    float4 v[kPer];
 #pragma unroll
-        for (int p = 0; p < L::PER; ++p) {
-            v[p] = ok ? reinterpret_cast<const float4 *>(x + (size_t)row * C)[li + p * L::LPR]
-                      : make_float4(0.f, 0.f, 0.f, 0.f);
-            s += (v[p].x + v[p].y) + (v[p].z + v[p].w);
-        }
-        const float mean = group_sum<L::LPR>(s) * (1.0f / C);
-        float q = 0.0f;
+    for (int i = 0; i < kPer; ++i) {
+        const int row = row0 + r0 + 16 * i;
+        v[i] = row < rows ? *reinterpret_cast<const float4 *>(x + (size_t)row * C + c0 + q)
+                          : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    if (tid < kR) {
+        const int row = row0 + tid;
+        float2 p[G];
 #pragma unroll
-        for (int p = 0; p < L::PER; ++p) {
-            const float a = v[p].x - mean, bb = v[p].y - mean, c = v[p].z - mean,
-                        d = v[p].w - mean;
-            q += (a * a + bb * bb) + (c * c + d * d);
-        }
-        const float rstd = rsqrtf(group_sum<L::LPR>(q) * (1.0f / C) + 1e-5f);
-        if (r < kRows) {
+        for (int k = 0; k < G; ++k)
+            p[k] = row < rows ? stats[(size_t)row * G + k] : make_float2(0.0f, 0.0f);
+        norm[tid] = ln_combine<G>(p);
+    }
+    const float4 gv = *reinterpret_cast<const float4 *>(g + c0 + q);
+    const float4 bv = *reinterpret_cast<const float4 *>(b + c0 + q);
+    __syncthreads();
 #pragma unroll
-            for (int p = 0; p < L::PER; ++p) {
-                const int c4 = (li + p * L::LPR) * 4;
-                tile[(c4 + 0) * (kRows + 1) + r] = (v[p].x - mean) * rstd * g[c4 + 0] + b[c4 + 0];
-                tile[(c4 + 1) * (kRows + 1) + r] = (v[p].y - mean) * rstd * g[c4 + 1] + b[c4 + 1];
-                tile[(c4 + 2) * (kRows + 1) + r] = (v[p].z - mean) * rstd * g[c4 + 2] + b[c4 + 2];
-                tile[(c4 + 3) * (kRows + 1) + r] = (v[p].w - mean) * rstd * g[c4 + 3] + b[c4 + 3];
-            }
-        }
+    for (int i = 0; i < kPer; ++i) {
+        const int r = r0 + 16 * i;
+        const float2 m = norm[r];
+        tile[q + 0][r] = (v[i].x - m.x) * m.y * gv.x + bv.x;
+        tile[q + 1][r] = (v[i].y - m.x) * m.y * gv.y + bv.y;
+        tile[q + 2][r] = (v[i].z - m.x) * m.y * gv.z + bv.z;
+        tile[q + 3][r] = (v[i].w - m.x) * m.y * gv.w + bv.w;
     }
     __syncthreads();
-    for (int e = threadIdx.x; e < C * kRows; e += blockDim.x) {
-        const int c = e / kRows, r = e - c * kRows, row = row0 + r;
-        if (row >= rows) continue;
-        const int n = row / hw, p = row - n * hw;
-        out[((size_t)n * C + c) * hw + p] = tile[c * (kRows + 1) + r];
+    if (vec) {
+        constexpr int kQ = kR / 4;
+        for (int e = tid; e < kStatCols * kQ; e += 256) {
+            const int c = e / kQ, r = 4 * (e - c * kQ), row = row0 + r;
+            if (row >= rows) continue;
+            const int n = row / hw, p = row - n * hw;
+            *reinterpret_cast<float4 *>(out + ((size_t)n * C + c0 + c) * hw + p) =
+                make_float4(tile[c][r], tile[c][r + 1], tile[c][r + 2], tile[c][r + 3]);
+        }
+    } else {
+        for (int e = tid; e < kStatCols * kR; e += 256) {
+            const int c = e / kR, r = e - c * kR, row = row0 + r;
+            if (row >= rows) continue;
+            const int n = row / hw, p = row - n * hw;
+            out[((size_t)n * C + c0 + c) * hw + p] = tile[c][r];
+        }
     }
 }
 
