@@ -427,7 +427,7 @@ void patch_embed(bf_cuda_swin *s, const float *images, hipStream_t stream) {
     // 4x4/s4 conv 3->96 straight from NCHW images into NHWC tokens; the
     // epilogue holds whole rows and applies the patch norm (-> x) and block
     // 0's LN1 (-> xn).
-    using T = Tile<128, 96, 32, 2, 2, true>;
+    using T = Tile<64, 96, 32, 1, 2, true>;
     const int B = (int)s->batches;
     ConvGeom g{};
     g.N = B; g.Ci = 3; g.IH = (int)s->input_h; g.IW = (int)s->input_w;
