@@ -316,29 +316,46 @@ static __global__ __launch_bounds__(256) void window_attention_kernel(
 #pragma unroll
     for (int c = 0; c < 8; ++c) add[c] = *reinterpret_cast<const bf16x8 *>(tp + c * 512);
 
+    // Every slot's q / k / v and the bias row are loaded unconditionally (a
+    // slot without a token reads token row 0), so all of them are in flight
+    // together; the selects below pick the token row, the qkv bias for a
+    // zero-padded source, or zeros for the MFMA padding rows.
     int tok[4];
+    bf16x8 qr[4], kr[4], vr[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        tok[b] = window_token(16 * b + l16, n, wy, wx, H, W, Hp, Wp, shift);
+        const bf16 *src = qkv + (size_t)(tok[b] < 0 ? 0 : tok[b]) * ld + h * 32 + 8 * g;
+        qr[b] = *reinterpret_cast<const bf16x8 *>(src);
+        kr[b] = *reinterpret_cast<const bf16x8 *>(src + C);
+        vr[b] = *reinterpret_cast<const bf16x8 *>(src + 2 * C);
+    }
+    bf16x8 qb, kb, vb;
+    {
+        const float *bq = qkv_bias + h * 32 + 8 * g;
+        float fq[8], fk[8], fv[8];
+#pragma unroll
+        for (int e = 0; e < 8; e += 4) {
+            *reinterpret_cast<float4 *>(fq + e) = *reinterpret_cast<const float4 *>(bq + e);
+            *reinterpret_cast<float4 *>(fk + e) = *reinterpret_cast<const float4 *>(bq + C + e);
+            *reinterpret_cast<float4 *>(fv + e) = *reinterpret_cast<const float4 *>(bq + 2 * C + e);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            qb[e] = to_half(fq[e]);
+            kb[e] = to_half(fk[e]);
+            vb[e] = to_half(fv[e]);
+        }
+    }
     bf16x8 qf[4], kf[4];
     bf16 *Vt = sV[wave];
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
-        tok[b] = window_token(16 * b + l16, n, wy, wx, H, W, Hp, Wp, shift);
-        bf16x8 q = {}, k = {}, v = {};
-        if (tok[b] >= 0) {
-            const bf16 *src = qkv + (size_t)tok[b] * ld + h * 32 + 8 * g;
-            q = *reinterpret_cast<const bf16x8 *>(src);
-            k = *reinterpret_cast<const bf16x8 *>(src + C);
-            v = *reinterpret_cast<const bf16x8 *>(src + 2 * C);
-        } else if (tok[b] == -1) {  // zero-padded source: q/k/v are the qkv bias
-            const float *bq = qkv_bias + h * 32 + 8 * g;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                q[e] = to_half(bq[e]);
-                k[e] = to_half(bq[C + e]);
-                v[e] = to_half(bq[2 * C + e]);
-            }
-        }
-        qf[b] = q;
-        kf[b] = k;
+        const bf16x8 zero = {};
+        const bool real = tok[b] >= 0, pad = tok[b] == -1;
+        qf[b] = real ? qr[b] : pad ? qb : zero;
+        kf[b] = real ? kr[b] : pad ? kb : zero;
+        const bf16x8 v = real ? vr[b] : pad ? vb : zero;
 #pragma unroll
         for (int e = 0; e < 8; ++e) Vt[(8 * g + e) * VS + 16 * b + l16] = v[e];
     }

@@ -19,6 +19,7 @@
  *       qkv fp16 [tokens, 3C] (token-major, tokens = batches*height*width),
  *       qkv_bias fp32 [3C], bias_mat fp32 [heads, 49, 49] (relative-position
  *       bias already gathered), out fp16 [tokens, C].  C = 32 * heads.
+ *       qkv, qkv_bias and out must be 16-byte aligned.
  *       (fp16 is the Swin path's operand format.)
  *
  *   bfhip_debug_window_attention_noalloc
