@@ -395,13 +395,24 @@ __global__ __launch_bounds__(64 * (C / 32)) __attribute__((amdgpu_waves_per_eu(C
     const int Hp = wy_n * 7, Wp = wx_n * 7;
     const int l16 = lane & 15, g = lane >> 4;
 
-    // The window's rows, 16 bytes per thread and step.
-    for (int c = threadIdx.x; c < 64 * (C / 8); c += 64 * HEADS) {
-        const int r = c / (C / 8), q = c - r * (C / 8);
-        const int t = window_token(r, n, wy, wx, H, W, Hp, Wp, shift);
-        bf16x8 v = {};
-        if (t >= 0) v = *reinterpret_cast<const bf16x8 *>(xn + (size_t)t * C + 8 * q);
-        *reinterpret_cast<bf16x8 *>(sX + r * XS + 8 * q) = v;
+    // The window's rows, 16 bytes per thread and step: all four steps' loads
+    // are issued before any is stored (a slot without a token reads row 0
+    // and stores zeros), so their latencies overlap.
+    constexpr int kSteps = 64 * (C / 8) / (64 * HEADS);
+    static_assert(kSteps * 64 * HEADS == 64 * (C / 8), "whole steps");
+    bf16x8 xv[kSteps];
+    int xt[kSteps];
+#pragma unroll
+    for (int i = 0; i < kSteps; ++i) {
+        const int c = threadIdx.x + i * 64 * HEADS, r = c / (C / 8), q = c - r * (C / 8);
+        xt[i] = window_token(r, n, wy, wx, H, W, Hp, Wp, shift);
+        xv[i] = *reinterpret_cast<const bf16x8 *>(xn + (size_t)(xt[i] < 0 ? 0 : xt[i]) * C + 8 * q);
+    }
+#pragma unroll
+    for (int i = 0; i < kSteps; ++i) {
+        const int c = threadIdx.x + i * 64 * HEADS, r = c / (C / 8), q = c - r * (C / 8);
+        const bf16x8 zero = {};
+        *reinterpret_cast<bf16x8 *>(sX + r * XS + 8 * q) = xt[i] >= 0 ? xv[i] : zero;
     }
 
     int tok[4];
