@@ -602,11 +602,18 @@ __device__ __forceinline__ void pack_nhwc_block(const float *x, bf16 *y, int C, 
                                                 int ld, int n, int c0, int p0, float (&tile)[64][65]) {
     const int t = threadIdx.x;
     const float *src = x + (size_t)n * C * HW;
+    // All 16 reads are issued before the first LDS store (an element outside
+    // the map reads element 0 and stores 0), so their latencies overlap.
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int c = c0 + (t >> 6) + 4 * i, p = p0 + (t & 63);
+        v[i] = src[(c < C && p < HW) ? (size_t)c * HW + p : 0];
+    }
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         const int cl = (t >> 6) + 4 * i, pl = t & 63;
-        const int c = c0 + cl, p = p0 + pl;
-        tile[cl][pl] = (c < C && p < HW) ? src[(size_t)c * HW + p] : 0.0f;
+        tile[cl][pl] = (c0 + cl < C && p0 + pl < HW) ? v[i] : 0.0f;
     }
     __syncthreads();
     bf16 *dst = y + (size_t)n * HW * ld;
