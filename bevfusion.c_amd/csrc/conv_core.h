@@ -307,10 +307,12 @@ struct SrcNHWC {
     const bf16 *x;
     int C, H, W;
     struct Row {};
+    using Raw = bf16x8;
     __device__ Row row(int, int, int) const { return {}; }
-    __device__ bf16x8 load(const Row &, int n, int iy, int ix, int c0) const {
+    __device__ Raw fetch(const Row &, int n, int iy, int ix, int c0) const {
         return *reinterpret_cast<const bf16x8 *>(x + (((size_t)n * H + iy) * W + ix) * C + c0);
     }
+    __device__ bf16x8 finish(const Raw &r) const { return r; }
 };
 
 // Channel concat of two NHWC maps of the same size: [0,C0) from a, rest from b.
@@ -318,12 +320,14 @@ struct SrcNHWCConcat {
     const bf16 *a, *b;
     int C0, C1, H, W;
     struct Row {};
+    using Raw = bf16x8;
     __device__ Row row(int, int, int) const { return {}; }
-    __device__ bf16x8 load(const Row &, int n, int iy, int ix, int c0) const {
+    __device__ Raw fetch(const Row &, int n, int iy, int ix, int c0) const {
         const size_t pix = ((size_t)n * H + iy) * W + ix;
         return c0 < C0 ? *reinterpret_cast<const bf16x8 *>(a + pix * C0 + c0)
                        : *reinterpret_cast<const bf16x8 *>(b + pix * C1 + (c0 - C0));
     }
+    __device__ bf16x8 finish(const Raw &r) const { return r; }
 };
 
 // dtransform.0 fused into dtransform.3's gather: the 8 virtual channels of tap
@@ -335,9 +339,12 @@ struct SrcNHWCDepthAffine {
     const float *w, *b;
     int H, W;
     struct Row {};
+    using Raw = float;
     __device__ Row row(int, int, int) const { return {}; }
-    __device__ bf16x8 load(const Row &, int n, int iy, int ix, int) const {
-        const float d = depth[((size_t)n * H + iy) * W + ix];
+    __device__ Raw fetch(const Row &, int n, int iy, int ix, int) const {
+        return depth[((size_t)n * H + iy) * W + ix];
+    }
+    __device__ bf16x8 finish(const Raw &d) const {
         bf16x8 o;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -361,7 +368,8 @@ struct LoadConvNHWC {
     int n[kPer], iy0[kPer], ix0[kPer];
     bool ok[kPer];
     typename Src::Row rs[kPer];
-    bf16x8 st[kPer];
+    typename Src::Raw raw[kPer];  // fetched by load(), finished by store()
+    bool val[kPer];
 
     __device__ void setup(int m0, int t) {
         tid = t;
@@ -384,19 +392,23 @@ struct LoadConvNHWC {
         const bool kin = k < g.K;
         const int tap = kin ? k / g.Ci : 0, c0 = k - tap * g.Ci;
         const int ky = tap / KW, kx = tap - ky * KW;
+        // Every chunk's read is issued (a zero tap reads pixel (n, 0, 0)
+        // channel 0); store() applies the source's transform and the zeros,
+        // so no read waits inside load().
 #pragma unroll
         for (int p = 0; p < kPer; ++p) {
             const int iy = iy0[p] + ky, ix = ix0[p] + kx;
-            bf16x8 v = {};
-            if (kin && ok[p] && (unsigned)iy < (unsigned)g.IH && (unsigned)ix < (unsigned)g.IW)
-                v = src.load(rs[p], n[p], iy, ix, c0);
-            st[p] = v;
+            val[p] = kin && ok[p] && (unsigned)iy < (unsigned)g.IH && (unsigned)ix < (unsigned)g.IW;
+            raw[p] = src.fetch(rs[p], n[p], val[p] ? iy : 0, val[p] ? ix : 0, val[p] ? c0 : 0);
         }
     }
     __device__ void store(bf16 *lds) const {
 #pragma unroll
-        for (int p = 0; p < kPer; ++p)
-            *reinterpret_cast<bf16x8 *>(lds + (tid / kPerRow + p * kRowStep) * (BK + 8) + cc * 8) = st[p];
+        for (int p = 0; p < kPer; ++p) {
+            const bf16x8 zero = {};
+            *reinterpret_cast<bf16x8 *>(lds + (tid / kPerRow + p * kRowStep) * (BK + 8) + cc * 8) =
+                val[p] ? src.finish(raw[p]) : zero;
+        }
     }
 };
 
