@@ -132,7 +132,8 @@ struct LoadPatch4x4 {
     int row, kg;
     const float *pix;  // image n, row 4*oy, column 4*ox, channel 0
     bool ok;
-    bf16 st[kPer];
+    float4 raw[kPer / 4];  // fetched by load(), converted by store()
+    bool val[kPer / 4];
 
     __device__ void setup(int m0, int tid) {
         row = tid % BM;
@@ -142,16 +143,17 @@ struct LoadPatch4x4 {
         const int mm = ok ? m : 0, n = mm / ohw, p = mm - n * ohw, oy = p / g.OW, ox = p - oy * g.OW;
         pix = x + (((size_t)n * g.Ci) * g.IH + 4 * oy) * g.IW + 4 * ox;
     }
+    // Every float4 is read (an element past K or past the last row reads the
+    // pixel's channel-0 run) before any is used; store() converts and zeroes,
+    // so the reads stay in flight across the caller's MFMAs.
     __device__ void load(int k0) {
         const int k = k0 + kg * kPer;
 #pragma unroll
         for (int q = 0; q < kPer; q += 4) {
             const int kk = k + q, ci = kk >> 4, ky = (kk >> 2) & 3;
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (ok && kk < g.K)
-                v = *reinterpret_cast<const float4 *>(pix + ((size_t)ci * g.IH + ky) * g.IW);
-            st[q] = to_word(v.x, F16); st[q + 1] = to_word(v.y, F16);
-            st[q + 2] = to_word(v.z, F16); st[q + 3] = to_word(v.w, F16);
+            val[q / 4] = ok && kk < g.K;
+            raw[q / 4] = *reinterpret_cast<const float4 *>(
+                pix + (val[q / 4] ? ((size_t)ci * g.IH + ky) * g.IW : 0));
         }
     }
     __device__ void store(bf16 *lds) const {
@@ -160,7 +162,11 @@ struct LoadPatch4x4 {
         for (int c = 0; c < kPer; c += 8) {
             bf16x8 v;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) v[e] = st[c + e];
+            for (int h = 0; h < 2; ++h) {
+                const float4 f = val[c / 4 + h] ? raw[c / 4 + h] : make_float4(0.f, 0.f, 0.f, 0.f);
+                v[4 * h + 0] = to_word(f.x, F16); v[4 * h + 1] = to_word(f.y, F16);
+                v[4 * h + 2] = to_word(f.z, F16); v[4 * h + 3] = to_word(f.w, F16);
+            }
             *reinterpret_cast<bf16x8 *>(dst + c) = v;
         }
     }
