@@ -670,13 +670,13 @@ int window_attention_items(const void *qkv, const float *qkv_bias, const float *
     if (!qkv || !qkv_bias || !bias_mat || !out || batches <= 0 || height <= 0 || width <= 0 ||
         heads <= 0 || channels != 32 * heads || shift < 0 || shift >= 7)
         return fail(error, cap, "invalid window-attention probe");
-    if ((reinterpret_cast<uintptr_t>(qkv) | reinterpret_cast<uintptr_t>(qkv_bias) |
-         reinterpret_cast<uintptr_t>(out)) & 15)
-        return fail(error, cap, "window-attention probe buffers must be 16-byte aligned");
     const long long wy_n = (height + 6) / 7, wx_n = (width + 6) / 7;
     const long long items = (long long)batches * wy_n * wx_n * heads;
     if (items > INT_MAX || (long long)batches * height * width * 3 * channels > INT_MAX)
         return fail(error, cap, "window-attention probe is too large");
+    if ((reinterpret_cast<uintptr_t>(qkv) | reinterpret_cast<uintptr_t>(qkv_bias) |
+         reinterpret_cast<uintptr_t>(out)) & 15)
+        return fail(error, cap, "window-attention probe buffers must be 16-byte aligned");
     return (int)items;
 }
 

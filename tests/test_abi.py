@@ -115,6 +115,8 @@ def test_index_probes_reject_invalid():
     assert lib.bfhip_debug_window_attention(s, s, s, s, 70000, 7000, 7000, 96, 3, 3, None, e,
                                             256) == 0
     assert b"too large" in e.value
+    assert lib.bfhip_debug_window_attention(s, s, s, s, 1, 7, 7, 96, 3, 3, None, e, 256) == 0
+    assert b"16-byte aligned" in e.value
     # The no-allocation variant shares the contract and bounds the head count
     # by its static array; both are checked before any HIP call.
     noalloc = lib.bfhip_debug_window_attention_noalloc
@@ -122,7 +124,8 @@ def test_index_probes_reject_invalid():
     assert b"invalid" in e.value
     assert noalloc(s, s, s, s, 70000, 7000, 7000, 96, 3, 3, None, e, 256) == 0
     assert b"too large" in e.value
-    assert noalloc(s, s, s, s, 1, 7, 7, 32 * 33, 33, 3, None, e, 256) == 0
+    aligned = C.c_void_p(256)
+    assert noalloc(aligned, aligned, aligned, aligned, 1, 7, 7, 32 * 33, 33, 3, None, e, 256) == 0
     assert b"at most 32 heads" in e.value
 
 
