@@ -427,6 +427,15 @@ __global__ __launch_bounds__(64 * (C / 32)) __attribute__((amdgpu_waves_per_eu(C
         for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
             for (int b = 0; b < 4; ++b) acc[cb][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+        // All of this matrix's weight fragments are read before the first
+        // MFMA, so the L2 reads overlap.
+        bf16x8 wa[KS][2];
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb)
+                wa[s][cb] = *reinterpret_cast<const bf16x8 *>(
+                    wqkv + (size_t)(m * C + h * 32 + 16 * cb + l16) * C + 32 * s + 8 * g);
 #pragma unroll
         for (int s = 0; s < KS; ++s) {
             bf16x8 xb[4];
@@ -434,12 +443,9 @@ __global__ __launch_bounds__(64 * (C / 32)) __attribute__((amdgpu_waves_per_eu(C
             for (int b = 0; b < 4; ++b)
                 xb[b] = *reinterpret_cast<const bf16x8 *>(sX + (16 * b + l16) * XS + 32 * s + 8 * g);
 #pragma unroll
-            for (int cb = 0; cb < 2; ++cb) {
-                const bf16x8 wa = *reinterpret_cast<const bf16x8 *>(
-                    wqkv + (size_t)(m * C + h * 32 + 16 * cb + l16) * C + 32 * s + 8 * g);
+            for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
-                for (int b = 0; b < 4; ++b) acc[cb][b] = mfma16_f16(wa, xb[b], acc[cb][b]);
-            }
+                for (int b = 0; b < 4; ++b) acc[cb][b] = mfma16_f16(wa[s][cb], xb[b], acc[cb][b]);
         }
     };
     // fp16 words of Y^T + bias in k-slot order: e < 4 -> channel 4g + e,
