@@ -131,6 +131,9 @@ SIGNATURES = {
     "bfhip_camera_profile_layer_io": (_i, [_vp, _i, _vp, _vp, _vp, _vp, C.c_char_p, _sz]),
     "bfhip_calibrate": (_i, [_i, _i, _i, _vp, _vp, _sz, _vp, C.c_char_p, _sz]),
     "bfhip_debug_runtime_fail_next": (_i, [_vp, C.c_char_p, _sz]),
+    "bfhip_debug_camera_gather": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, C.c_char_p, _sz]),
+    "bfhip_debug_fpn_upsample": (_i, [_vp, _i, _vp, _vp, _vp, C.c_char_p, _sz]),
+    "bfhip_debug_swin_merge_gather": (_i, [_vp, _i, _vp, _vp, _vp, C.c_char_p, _sz]),
     "bfhip_debug_window_map": (_i, [_i, _i, _i, _i, _vp, _vp, _vp, C.c_char_p, _sz]),
     "bfhip_debug_window_attention": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp,
                                           C.c_char_p, _sz]),
@@ -406,6 +409,75 @@ def window_attention(qkv, qkv_bias, bias_mat, batches, height, width, heads, shi
     _check(getattr(hip_lib(), name)(
         _vp(qkv.data_ptr()), _ptr(qkv_bias), _ptr(bias_mat), _vp(out.data_ptr()), batches,
         height, width, c, heads, shift, _stream(stream), err, 512), err, name)
+    return out
+
+
+def camera_gather(neck, layer, src0, src1=None, affine=None, stream=None):
+    """A-operand gather of camera-neck conv `layer` over identity weights
+    (bfhip_debug_camera_gather, include/bfhip_debug.h): returns fp32 [M, K],
+    the gathered operand of the production loader instance."""
+    torch = _torch()
+    layers = {1: (3, 1, 1), 3: (3, 1, 1), 4: (5, 4, 2), 5: (5, 2, 2), 6: (3, 1, 1),
+              7: (3, 1, 1), 8: (1, 1, 0), 9: (3, 1, 1), 10: (3, 2, 1), 11: (3, 1, 1)}
+    if layer not in layers:
+        raise BfHipError(f"no gather probe for camera layer {layer}")
+    k, st, pad = layers[layer]
+    if layer == 4:
+        if src0.dtype != torch.float32 or src0.dim() != 3 or affine is None:
+            raise BfHipError("dtransform.3 takes fp32 depth [B, H, W] and a 16-float affine")
+        n, ih, iw = src0.shape
+        ci = 8
+    else:
+        if src0.dtype != torch.float16 or src0.dim() != 4:
+            raise BfHipError("src0 must be fp16 [B, H, W, C]")
+        n, ih, iw, ci = src0.shape
+        if layer == 6:
+            if src1 is None or src1.dtype != torch.float16 or tuple(src1.shape[:3]) != (n, ih, iw):
+                raise BfHipError("depthnet.0 takes src1 fp16 [B, H, W, 256]")
+            ci += src1.shape[3]
+    for t in (src0, src1, affine):
+        if t is not None and not t.is_contiguous():
+            raise BfHipError("probe inputs must be contiguous")
+    oh, ow = (ih + 2 * pad - k) // st + 1, (iw + 2 * pad - k) // st + 1
+    out = torch.empty((n * oh * ow, k * k * ci), dtype=torch.float32, device=src0.device)
+    err = _err()
+    _check(hip_lib().bfhip_debug_camera_gather(
+        neck.handle, layer, _vp(src0.data_ptr()), _vp(src1.data_ptr() if src1 is not None else None),
+        _vp(affine.data_ptr() if affine is not None else None), _vp(out.data_ptr()),
+        _stream(stream), err, 512), err, "bfhip_debug_camera_gather")
+    return out
+
+
+def fpn_upsample(neck, level, up, stream=None):
+    """Lateral-conv epilogue over a zero product (bfhip_debug_fpn_upsample):
+    up fp32 [B, h, w, 256] -> fp16 [B, H, W, 256] = fp16(relu(bilinear(up)))."""
+    torch = _torch()
+    if up.dtype != torch.float32 or up.dim() != 4 or up.shape[3] != 256 or not up.is_contiguous():
+        raise BfHipError("up must be a contiguous fp32 [B, h, w, 256] tensor")
+    big = (neck.h, neck.w)
+    mid = (-(-neck.h // 2), -(-neck.w // 2))
+    H, W = big if level == 0 else mid
+    out = torch.empty((up.shape[0], H, W, 256), dtype=torch.float16, device=up.device)
+    err = _err()
+    _check(hip_lib().bfhip_debug_fpn_upsample(neck.handle, level, _ptr(up), _vp(out.data_ptr()),
+                                              _stream(stream), err, 512),
+           err, "bfhip_debug_fpn_upsample")
+    return out
+
+
+def swin_merge_gather(swin, stage, xh, stream=None):
+    """Patch-merge gather of stage `stage` over permuted identity weights
+    (bfhip_debug_swin_merge_gather): xh fp16 [B, H, W, C] -> fp32
+    [B*H2*W2, 4C] in the reference's unfold column order."""
+    torch = _torch()
+    if xh.dtype != torch.float16 or xh.dim() != 4 or not xh.is_contiguous():
+        raise BfHipError("xh must be a contiguous fp16 [B, H, W, C] tensor")
+    b, h, w, c = xh.shape
+    out = torch.empty((b * -(-h // 2) * -(-w // 2), 4 * c), dtype=torch.float32, device=xh.device)
+    err = _err()
+    _check(hip_lib().bfhip_debug_swin_merge_gather(swin.handle, stage, _vp(xh.data_ptr()),
+                                                   _vp(out.data_ptr()), _stream(stream), err, 512),
+           err, "bfhip_debug_swin_merge_gather")
     return out
 
 

@@ -11,8 +11,10 @@ Test infrastructure (built by the same call, never linked by the products):
 from __future__ import annotations
 
 import concurrent.futures as cf
+import json
 import os
 import pathlib
+import re
 import shutil
 import subprocess
 import sys
@@ -54,11 +56,34 @@ def build_model_lib() -> pathlib.Path:
     return out
 
 
-def _compile_hip(src: pathlib.Path) -> pathlib.Path:
+_REMARK = re.compile(r"remark: +(Function Name|TotalSGPRs|VGPRs|AGPRs|ScratchSize \[bytes/lane\]|"
+                     r"Occupancy \[waves/SIMD\]|SGPRs Spill|VGPRs Spill|LDS Size \[bytes/block\]): "
+                     r"(\S+) \[-Rpass-analysis=kernel-resource-usage\]")
+_RESOURCE_KEYS = {"TotalSGPRs": "sgprs", "VGPRs": "vgprs", "AGPRs": "agprs",
+                  "ScratchSize [bytes/lane]": "scratch", "Occupancy [waves/SIMD]": "occupancy",
+                  "SGPRs Spill": "sgpr_spill", "VGPRs Spill": "vgpr_spill",
+                  "LDS Size [bytes/block]": "lds"}
+
+
+def _kernel_resources(text: str) -> dict:
+    """Per-kernel resource usage from the compiler's kernel-resource-usage
+    remarks: {mangled name: {sgprs, vgprs, agprs, scratch, occupancy,
+    sgpr_spill, vgpr_spill, lds}}."""
+    out, cur = {}, None
+    for key, value in _REMARK.findall(text):
+        if key == "Function Name":
+            cur = out.setdefault(value, {})
+        elif cur is not None:
+            cur[_RESOURCE_KEYS[key]] = int(value)
+    return out
+
+
+def _compile_hip(src: pathlib.Path):
     OBJ.mkdir(exist_ok=True)
     obj = OBJ / (src.stem + ".o")
-    _run([HIPCC, *HIP_FLAGS, "-c", str(src), "-o", str(obj)])
-    return obj
+    text = _run([HIPCC, *HIP_FLAGS, "-Rpass-analysis=kernel-resource-usage", "-c", str(src),
+                 "-o", str(obj)])
+    return obj, _kernel_resources(text)
 
 
 def build_hip_lib(jobs: int | None = None) -> pathlib.Path:
@@ -66,7 +91,12 @@ def build_hip_lib(jobs: int | None = None) -> pathlib.Path:
     sources = sorted(CSRC.glob("*.hip"))
     jobs = jobs or min(len(sources), max(1, (os.cpu_count() or 2) // 2))
     with cf.ThreadPoolExecutor(max_workers=jobs) as pool:
-        objs = list(pool.map(_compile_hip, sources))
+        built = list(pool.map(_compile_hip, sources))
+    objs = [o for o, _ in built]
+    # Kernel resource report (registers, scratch, occupancy, LDS) of every
+    # kernel in the library, read by tests/test_kernel_resources.py.
+    report = {src.name: res for src, (_, res) in zip(sources, built)}
+    (OBJ / "kernel_resources.json").write_text(json.dumps(report, indent=1, sort_keys=True))
     out = LIB / "libbfhip.so"
     tmp = LIB / "libbfhip.so.tmp"
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs),

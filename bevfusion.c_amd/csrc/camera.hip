@@ -16,6 +16,7 @@
 //   depthnet.6 stores logits / context from its epilogue;
 //   the last downsample conv stores the x/y-transposed map.
 #include "bf_cuda_camera.h"
+#include "bfhip_debug.h"
 #include "bfhip_profile.h"
 #include "conv_layers.h"
 
@@ -96,27 +97,66 @@ using DDs0 = DmaTile<160, 80, 32, 5, 1, 3, true>;   // downsample.0 at the full 
 using DDs1 = DmaTile<160, 80, 32, 5, 1, 4, true>;   // downsample.1 / .2 at half resolution
 constexpr int kDsLoaders = 5;
 
-// FPN output conv: channels-last only, or also NCHW fp32 for the boundary.
-template <class T>
-void fpn_conv(const ConvLayer &l, const bf16 *in, bf16 *nhwc, float *nchw, hipStream_t s) {
-    if constexpr (std::is_same_v<T, S64>) {
-        if (nchw)
-            run_conv_spec<T, 3, kS64Loaders>(l, in, 256, nullptr, 0, out_to(l, nhwc, nchw, 1, true), s);
-        else
-            run_conv_spec<T, 3, kS64Loaders>(l, in, 256, nullptr, 0, nhwc_to(l, nhwc, true), s);
-        return;
-    }
-    if (use_s256(l)) {
-        if (nchw)
-            run_conv_spec<S256, 3, kS256Loaders>(l, in, 256, nullptr, 0, out_to(l, nhwc, nchw, 1, true), s);
-        else
-            run_conv_spec<S256, 3, kS256Loaders>(l, in, 256, nullptr, 0, nhwc_to(l, nhwc, true), s);
-        return;
-    }
-    if (nchw)
-        run_conv_dma<T, 3>(l, in, 256, nullptr, 0, out_to(l, nhwc, nchw, 1, true), s);
+// The A-operand gather of each conv layer, with the tile, pipeline and loader
+// instance the forward runs; `epi` consumes the product.  The forward passes
+// its epilogues; bfhip_debug_camera_gather passes a row-major fp32 store over
+// identity weights, which makes the product the gathered operand itself.
+// 3x3 256 -> 256 convs over one map (a) or over concat(a, b).
+template <class Epi>
+void conv_256(const ConvLayer &l, const bf16 *a, int c0, const bf16 *b, int c1, const Epi &epi,
+              hipStream_t s) {
+    if (use_s256(l))
+        run_conv_spec<S256, 3, kS256Loaders>(l, a, c0, b, c1, epi, s);
     else
-        run_conv_dma<T, 3>(l, in, 256, nullptr, 0, nhwc_to(l, nhwc, true), s);
+        run_conv_dma<D256, 3>(l, a, c0, b, c1, epi, s);
+}
+template <class Epi>
+void conv_fpn1(const ConvLayer &l, const bf16 *in, const Epi &epi, hipStream_t s) {
+    run_conv_spec<S64, 3, kS64Loaders>(l, in, 256, nullptr, 0, epi, s);
+}
+template <class Epi>
+void conv_dt1(const ConvLayer &l, const float *depth, const float *aw, const float *ab,
+              const Epi &epi, hipStream_t s) {
+    run_conv<T32, 5, 5>(l, SrcNHWCDepthAffine<true>{depth, aw, ab, l.ih, l.iw}, epi, s);
+}
+template <class Epi>
+void conv_dt2(const ConvLayer &l, const bf16 *in, const Epi &epi, hipStream_t s) {
+    run_conv_spec<S32, 5>(l, in, 32, nullptr, 0, epi, s);
+}
+template <class Epi>
+void conv_dn6(const ConvLayer &l, const bf16 *in, const Epi &epi, hipStream_t s) {
+    run_conv_dma<D256, 1>(l, in, 256, nullptr, 0, epi, s);
+}
+template <class Epi>
+void conv_ds0(const ConvLayer &l, const bf16 *in, const Epi &epi, hipStream_t s) {
+    run_conv_spec<DDs0, 3, kDsLoaders>(l, in, kDsPad, nullptr, 0, epi, s);
+}
+template <class Epi>
+void conv_ds1(const ConvLayer &l, const bf16 *in, const Epi &epi, hipStream_t s) {
+    run_conv_spec<DDs1, 3, kDsLoaders>(l, in, kDsPad, nullptr, 0, epi, s);
+}
+// The checkpoint's x/y permute out[c][x][y] = y(c, y, x) (reference
+// transpose_xy_kernel, cuda_camera.cu:265-271; lss_downsample.c:142-146):
+// with the GEMM rows in x-major pixel order (YFAST) the transposed NCHW
+// output is plain channel planes along the rows.
+template <class Epi>
+void conv_ds2(const ConvLayer &l, const bf16 *in, const Epi &epi, hipStream_t s) {
+    run_conv_spec<DDs1, 3, kDsLoaders, true>(l, in, kDsPad, nullptr, 0, epi, s);
+}
+
+// FPN output conv: channels-last only, or also NCHW fp32 for the boundary.
+template <class Epi>
+void fpn_conv_epi(int layer, const ConvLayer &l, const bf16 *in, const Epi &epi, hipStream_t s) {
+    if (layer == kFpn1)
+        conv_fpn1(l, in, epi, s);
+    else
+        conv_256(l, in, 256, nullptr, 0, epi, s);
+}
+void fpn_conv(int layer, const ConvLayer &l, const bf16 *in, bf16 *nhwc, float *nchw, hipStream_t s) {
+    if (nchw)
+        fpn_conv_epi(layer, l, in, out_to(l, nhwc, nchw, 1, true), s);
+    else
+        fpn_conv_epi(layer, l, in, nhwc_to(l, nhwc, true), s);
 }
 
 // Lateral 1x1 conv `layer` over concat(lower [B][H][W][Cl], up(upper
@@ -130,6 +170,15 @@ void fpn_conv(const ConvLayer &l, const bf16 *in, bf16 *nhwc, float *nchw, hipSt
 using DLatUp = DmaTile<32, 64, 64, 1, 2, 3, true>;     // upper products (M = B*h*w)
 using SLatUpDeep = DmaTile<32, 32, 64, 1, 1, 4, true>;  // upper products with Cu >= 512
 using DLat = DmaTile<64, 64, 64, 2, 2, 2, true>;       // lower halves
+// The lower half: out = relu(W[:, :Cl] . lower + bias + bilinear(up)), with
+// the upsampling in the epilogue (EpiUpAddNHWC); w rows hold ldw columns.
+void lateral_lower(const bf16 *lower, int Cl, const bf16 *w, int ldw, const float *bias,
+                   const float *up, bf16 *out, int M, int H, int W, int h, int wd, hipStream_t s) {
+    using T = DLat;
+    DmaRowsBf16<T::BM, T::BK, T::kThreads> al{lower, Cl, M, Cl};
+    DmaRowsBf16<T::BN, T::BK, T::kThreads> bl{w, ldw, 256, Cl};
+    launch_gemm_dma<T>(al, bl, EpiUpAddNHWC{out, bias, up, M, 256, H, W, h, wd, 1}, M, 256, Cl, s);
+}
 void lateral(const ConvLayer &l, const bf16 *lower, int Cl, int H, int W, const bf16 *upper, int Cu,
              int h, int w, float *up, bf16 *out, hipStream_t s) {
     const int B = l.n, Mu = B * h * w, M = B * H * W, ci = Cl + Cu;
@@ -144,12 +193,7 @@ void lateral(const ConvLayer &l, const bf16 *lower, int Cl, int H, int W, const 
         DmaRowsBf16<T::BN, T::BK, T::kThreads> bl{l.w + Cl, ci, 256, Cu};
         launch_gemm_dma<T>(al, bl, EpiRowsF32{up, nullptr, 256, Mu, 256, 0}, Mu, 256, Cu, s);
     }
-    {
-        using T = DLat;
-        DmaRowsBf16<T::BM, T::BK, T::kThreads> al{lower, Cl, M, Cl};
-        DmaRowsBf16<T::BN, T::BK, T::kThreads> bl{l.w, ci, 256, Cl};
-        launch_gemm_dma<T>(al, bl, EpiUpAddNHWC{out, l.b, up, M, 256, H, W, h, w, 1}, M, 256, Cl, s);
-    }
+    lateral_lower(lower, Cl, l.w, ci, l.b, up, out, M, H, W, h, w, s);
 }
 
 void lateral1(bf_cuda_camera_neck *n, hipStream_t s) {
@@ -171,9 +215,9 @@ void fpn_impl(bf_cuda_camera_neck *n, const float *s0, const float *s1, const fl
     pack_nhwc_many(PackJobs<3>{{{s0, n->p0, 192, hw}, {s1, n->p1, 384, hw1}, {s2, n->p2, 768, hw2}}}, B,
                    s, true);
     lateral1(n, s);
-    fpn_conv<S64>(n->L[kFpn1], n->t1, n->f1, out1, s);
+    fpn_conv(kFpn1, n->L[kFpn1], n->t1, n->f1, out1, s);
     lateral0(n, s);
-    fpn_conv<D256>(n->L[kFpn0], n->t0, n->f0, out0, s);
+    fpn_conv(kFpn0, n->L[kFpn0], n->t0, n->f0, out0, s);
 }
 
 // One layer of the depth head (dtransform.3 .. depthnet.6); the forward and
@@ -183,26 +227,12 @@ void depth_layer(bf_cuda_camera_neck *n, int layer, const float *depth, float *l
     const int h = (int)n->h, w = (int)n->w;
     const ConvLayer &l = n->L[layer];
     switch (layer) {
-        case kDt1:
-            run_conv<T32, 5, 5>(l, SrcNHWCDepthAffine<true>{depth, n->dt0_w, n->dt0_b, 8 * h, 8 * w},
-                                nhwc_to(l, n->e1, true), s);
-            break;
-        case kDt2: run_conv_spec<S32, 5>(l, n->e1, 32, nullptr, 0, nhwc_to(l, n->e2, true), s); break;
-        case kDn0:
-            if (use_s256(l))
-                run_conv_spec<S256, 3, kS256Loaders>(l, n->e2, 64, n->f0, 256, nhwc_to(l, n->d0, true), s);
-            else
-                run_conv_dma<D256, 3>(l, n->e2, 64, n->f0, 256, nhwc_to(l, n->d0, true), s);
-            break;
-        case kDn3:
-            if (use_s256(l))
-                run_conv_spec<S256, 3, kS256Loaders>(l, n->d0, 256, nullptr, 0, nhwc_to(l, n->d1, true), s);
-            else
-                run_conv_dma<D256, 3>(l, n->d0, 256, nullptr, 0, nhwc_to(l, n->d1, true), s);
-            break;
+        case kDt1: conv_dt1(l, depth, n->dt0_w, n->dt0_b, nhwc_to(l, n->e1, true), s); break;
+        case kDt2: conv_dt2(l, n->e1, nhwc_to(l, n->e2, true), s); break;
+        case kDn0: conv_256(l, n->e2, 64, n->f0, 256, nhwc_to(l, n->d0, true), s); break;
+        case kDn3: conv_256(l, n->d0, 256, nullptr, 0, nhwc_to(l, n->d1, true), s); break;
         case kDn6:
-            run_conv_dma<D256, 1>(l, n->d1, 256, nullptr, 0,
-                                  EpiSplitDepth{logits, context, l.b, l.n * h * w, h * w, 118, 80}, s);
+            conv_dn6(l, n->d1, EpiSplitDepth{logits, context, l.b, l.n * h * w, h * w, 118, 80}, s);
             break;
         default: break;
     }
@@ -211,27 +241,11 @@ void depth_layer(bf_cuda_camera_neck *n, int layer, const float *depth, float *l
 // One layer of the post-LSS downsample from the packed BEV in n->bp; the last
 // one stores the x/y-transposed NCHW output.
 void downsample_layer(bf_cuda_camera_neck *n, int layer, float *output, hipStream_t s) {
-    const int bh = (int)n->bev_h, bw = (int)n->bev_w;
     const ConvLayer &l = n->L[layer];
     switch (layer) {
-        case kDs0:
-            run_conv_spec<DDs0, 3, kDsLoaders>(l, n->bp, kDsPad, nullptr, 0,
-                                               nhwc_to(l, n->b0, true, kDsPad), s);
-            break;
-        case kDs1:
-            run_conv_spec<DDs1, 3, kDsLoaders>(l, n->b0, kDsPad, nullptr, 0,
-                                               nhwc_to(l, n->b1, true, kDsPad), s);
-            break;
-        case kDs2:
-            // The checkpoint's x/y permute out[c][x][y] = y(c, y, x) (reference
-            // transpose_xy_kernel, cuda_camera.cu:265-271; lss_downsample.c:
-            // 142-146): with the GEMM rows in x-major pixel order the
-            // transposed NCHW output is plain channel planes along the rows.
-            run_conv_spec<DDs1, 3, kDsLoaders, true>(l, n->b1, kDsPad, nullptr, 0,
-                                                     EpiPlanesNCHW{output, l.b, l.oh * l.ow, 80,
-                                                                   l.oh * l.ow},
-                                                     s);
-            break;
+        case kDs0: conv_ds0(l, n->bp, nhwc_to(l, n->b0, true, kDsPad), s); break;
+        case kDs1: conv_ds1(l, n->b0, nhwc_to(l, n->b1, true, kDsPad), s); break;
+        case kDs2: conv_ds2(l, n->b1, EpiPlanesNCHW{output, l.b, l.oh * l.ow, 80, l.oh * l.ow}, s); break;
         default: break;
     }
 }
@@ -430,9 +444,9 @@ extern "C" int bfhip_camera_profile_layer(bf_cuda_camera_neck *n, int layer, voi
     // Same kernels and shapes as the forward entry points, on context buffers.
     switch (layer) {
         case kLat1: lateral1(n, s); break;
-        case kFpn1: fpn_conv<S64>(l, n->t1, n->f1, nullptr, s); break;
+        case kFpn1: fpn_conv(layer, l, n->t1, n->f1, nullptr, s); break;
         case kLat0: lateral0(n, s); break;
-        case kFpn0: fpn_conv<D256>(l, n->t0, n->f0, nullptr, s); break;
+        case kFpn0: fpn_conv(layer, l, n->t0, n->f0, nullptr, s); break;
         case kDt2: case kDn0: case kDn3: depth_layer(n, layer, nullptr, nullptr, nullptr, s); break;
         case kDs0: case kDs1: downsample_layer(n, layer, nullptr, s); break;
         case kDs2:
@@ -455,4 +469,91 @@ extern "C" int bfhip_camera_profile_layer_io(bf_cuda_camera_neck *n, int layer, 
     else
         depth_layer(n, layer, input, out0, out1, s);
     return launch_ok(error, cap, "launch HIP camera layer profiling");
+}
+
+// ---- Index probes (include/bfhip_debug.h) ----------------------------------
+namespace {
+
+// Device allocations of a probe, released on every return path.
+struct ProbeBuffers {
+    std::vector<void *> held;
+    ProbeBuffers() = default;
+    ProbeBuffers(const ProbeBuffers &) = delete;
+    ProbeBuffers &operator=(const ProbeBuffers &) = delete;
+    ~ProbeBuffers() {
+        for (void *p : held) (void)hipFree(p);
+    }
+    void *upload(const void *host, size_t bytes, char *error, size_t cap) {
+        void *p = nullptr;
+        if (!hip_ok(hipMalloc(&p, bytes), error, cap, "allocate probe buffer")) return nullptr;
+        held.push_back(p);
+        if (!hip_ok(hipMemcpy(p, host, bytes, hipMemcpyHostToDevice), error, cap, "upload probe buffer"))
+            return nullptr;
+        return p;
+    }
+};
+
+}  // namespace
+
+extern "C" int bfhip_debug_camera_gather(bf_cuda_camera_neck *n, int layer, const void *src0,
+                                         const void *src1, const float *affine, float *out,
+                                         void *stream, char *error, size_t cap) {
+    const bool conv = layer == kFpn1 || layer == kFpn0 || (layer >= kDt1 && layer <= kDs2);
+    if (!n || !conv || !src0 || !out || (layer == kDn0 && !src1) || (layer == kDt1 && !affine))
+        return fail(error, cap, "invalid camera gather probe");
+    ConvLayer l = n->L[layer];
+    const int K = l.ci * l.k * l.k, M = l.n * l.oh * l.ow;
+    if ((long long)M * K > INT_MAX) return fail(error, cap, "camera gather probe is too large");
+    // Identity weights (fp16 1.0 = 0x3C00 on the diagonal, K output columns)
+    // and a zero bias: the product is the gathered operand, exactly.
+    std::vector<uint16_t> ident((size_t)K * K, 0);
+    for (int k = 0; k < K; ++k) ident[(size_t)k * K + k] = 0x3C00;
+    const std::vector<float> zero(K, 0.0f);
+    ProbeBuffers buf;
+    l.w = static_cast<const bf16 *>(buf.upload(ident.data(), ident.size() * 2, error, cap));
+    l.b = static_cast<const float *>(buf.upload(zero.data(), zero.size() * 4, error, cap));
+    if (!l.w || !l.b) return 0;
+    l.co = K;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const EpiRowsF32 epi{out, nullptr, K, M, K, 0};
+    const bf16 *a = static_cast<const bf16 *>(src0), *b = static_cast<const bf16 *>(src1);
+    switch (layer) {
+        case kFpn1: case kFpn0: fpn_conv_epi(layer, l, a, epi, s); break;
+        case kDt1: conv_dt1(l, static_cast<const float *>(src0), affine, affine + 8, epi, s); break;
+        case kDt2: conv_dt2(l, a, epi, s); break;
+        case kDn0: conv_256(l, a, 64, b, 256, epi, s); break;
+        case kDn3: conv_256(l, a, 256, nullptr, 0, epi, s); break;
+        case kDn6: conv_dn6(l, a, epi, s); break;
+        case kDs0: conv_ds0(l, a, epi, s); break;
+        case kDs1: conv_ds1(l, a, epi, s); break;
+        case kDs2: conv_ds2(l, a, epi, s); break;
+        default: break;
+    }
+    return launch_ok(error, cap, "launch camera gather probe") &&
+           hip_ok(hipStreamSynchronize(s), error, cap, "camera gather probe");
+}
+
+extern "C" int bfhip_debug_fpn_upsample(bf_cuda_camera_neck *n, int level, const float *up,
+                                        void *out, void *stream, char *error, size_t cap) {
+    if (!n || (level != 0 && level != 1) || !up || !out)
+        return fail(error, cap, "invalid FPN upsample probe");
+    const ConvLayer &l = n->L[level == 0 ? kLat0 : kLat1];
+    const int Cl = level == 0 ? 192 : 384;
+    const int H = level == 0 ? (int)n->h : (int)n->h1, W = level == 0 ? (int)n->w : (int)n->w1;
+    const int h = level == 0 ? (int)n->h1 : (int)n->h2, w = level == 0 ? (int)n->w1 : (int)n->w2;
+    const int M = l.n * H * W;
+    // Zero lower map, weights and bias: the epilogue adds the bilinear
+    // upsampling of `up` to an exact zero.
+    const std::vector<uint16_t> lower((size_t)M * Cl, 0), weights((size_t)256 * Cl, 0);
+    const std::vector<float> bias(256, 0.0f);
+    ProbeBuffers buf;
+    const void *dl = buf.upload(lower.data(), lower.size() * 2, error, cap);
+    const void *dw = buf.upload(weights.data(), weights.size() * 2, error, cap);
+    const void *db = buf.upload(bias.data(), bias.size() * 4, error, cap);
+    if (!dl || !dw || !db) return 0;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    lateral_lower(static_cast<const bf16 *>(dl), Cl, static_cast<const bf16 *>(dw), Cl,
+                  static_cast<const float *>(db), up, static_cast<bf16 *>(out), M, H, W, h, w, s);
+    return launch_ok(error, cap, "launch FPN upsample probe") &&
+           hip_ok(hipStreamSynchronize(s), error, cap, "FPN upsample probe");
 }

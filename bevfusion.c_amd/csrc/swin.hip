@@ -116,6 +116,17 @@ struct FoldedLinear {
     std::vector<float> c, d;
 };
 
+// Column order of the patch-merge reduction weights: folded column q*C + ch
+// reads the reference's unfold column ch*4 + q (nn.Unfold order, channel then
+// tap q = 2 ky + kx; swin_backbone.c:287-296), the tap-major order in which
+// DmaMergeRows gathers the 2x2 tokens.
+std::vector<int> merge_tap_order(int C) {
+    std::vector<int> perm(4 * (size_t)C);
+    for (int q = 0; q < 4; ++q)
+        for (int ch = 0; ch < C; ++ch) perm[(size_t)q * C + ch] = ch * 4 + q;
+    return perm;
+}
+
 FoldedLinear fold_ln(const float *W, const float *b, const float *g, const float *beta, int N,
                      int K, const std::vector<int> *perm) {
     FoldedLinear f;
@@ -293,10 +304,7 @@ static int swin_build(bf_cuda_swin *s, const bf_model *model, size_t batches, si
         std::snprintf(name, sizeof(name), "image_backbone.norm%d.bias", st + 1);
         const float *ob = bind_f32(model, name, {(uint32_t)kC[st + 1]}, error, cap);
         if (!ms || !mb || !mw || !os || !ob) return 0;
-        // Folded column q*C + ch reads unfold column ch*4 + q (DmaMergeRows).
-        std::vector<int> perm(4 * c);
-        for (uint32_t q = 0; q < 4; ++q)
-            for (uint32_t ch = 0; ch < c; ++ch) perm[q * c + ch] = (int)(ch * 4 + q);
+        const std::vector<int> perm = merge_tap_order((int)c);
         const FoldedLinear fm = fold_ln(mw, nullptr, ms, mb, 2 * c, 4 * c, &perm);
         o_mw[st] = arena.add(fm.w.data(), fm.w.size() * 2);
         o_mc[st] = arena.add_f32(fm.c);
@@ -570,37 +578,51 @@ int block_ops(int st, int b, int *ops) {
 // and the epilogue writes the next stage's x, xh and stats.  Tiles as
 // linear_f16 picks for these (N, K); LW > 0 runs the tile on the
 // wave-specialised pipeline with LW loader waves (measured on MI355X for the
-// second merge, 1056 x 768 x 1536: 7.3 vs 8.9 us).
+// second merge, 1056 x 768 x 1536: 7.3 vs 8.9 us).  The gather and its tile
+// are merge_gemm's, which bfhip_debug_swin_merge_gather also runs.
+template <int C, class T, int LW, class Epi>
+void merge_gemm(const bf16 *xh, int B, int H, int W, const bf16 *w, int N, const Epi &epi,
+                hipStream_t stream) {
+    const int T2 = B * ((H + 1) / 2) * ((W + 1) / 2);
+    constexpr int kLoadThreads = LW > 0 ? LW * kWave : T::kThreads;
+    DmaMergeRows<T::BM, T::BK, kLoadThreads, C> al{};
+    al.base = xh;
+    al.batches = B;
+    al.H = H;
+    al.W = W;
+    DmaRowsBf16<T::BN, T::BK, kLoadThreads> bl{w, 4 * C, N, 4 * C};
+    if constexpr (LW > 0)
+        launch_gemm_spec<T>(al, bl, epi, T2, N, 4 * C, stream);
+    else
+        launch_gemm_dma<T>(al, bl, epi, T2, N, 4 * C, stream);
+}
+
 template <int C, class T, int LW = 0>
 void merge_folded(bf_cuda_swin *s, int st, hipStream_t stream) {
     const int B = (int)s->batches, H = s->h[st], W = s->w[st];
     const int T2 = B * s->h[st + 1] * s->w[st + 1];
-    constexpr int kLoadThreads = LW > 0 ? LW * kWave : T::kThreads;
-    DmaMergeRows<T::BM, T::BK, kLoadThreads, C> al{};
-    al.base = stage_xh(s, st);
-    al.batches = B;
-    al.H = H;
-    al.W = W;
-    DmaRowsBf16<T::BN, T::BK, kLoadThreads> bl{s->merge_w[st], 4 * C, 2 * C, 4 * C};
     const int nx = (st + 1) & 1;
     constexpr bool kWhole = C % kStatCols != 0;  // one group per token
     using Src = LnMerge<kWhole ? 1 : C / kStatCols, kWhole ? C : kStatCols>;
     EpiStatsRows<true, false, Src> epi{s->x,          s->xh[nx],     s->stats[nx],
                                        s->merge_d[st], s->merge_c[st], Src{stage_stats(s, st), H, W},
                                        T2,            2 * C};
-    if constexpr (LW > 0)
-        launch_gemm_spec<T>(al, bl, epi, T2, 2 * C, 4 * C, stream);
-    else
-        launch_gemm_dma<T>(al, bl, epi, T2, 2 * C, 4 * C, stream);
+    merge_gemm<C, T, LW>(stage_xh(s, st), B, H, W, s->merge_w[st], 2 * C, epi, stream);
 }
+
+// The merge tiles per stage.
+using MergeT0 = DmaTile<128, 64, 64, 2, 2, 2, true>;
+using MergeT1 = DmaTile<64, 64, 64, 2, 2, 2, true>;
+using MergeT2 = DmaTile<64, 64, 128, 2, 2, 3, true>;
+constexpr int kMergeLoaders2 = 4;
 
 void merge_op(bf_cuda_swin *s, int st, hipStream_t stream) {
     if (st == 0)
-        merge_folded<96, DmaTile<128, 64, 64, 2, 2, 2, true>>(s, st, stream);
+        merge_folded<96, MergeT0>(s, st, stream);
     else if (st == 1)
-        merge_folded<192, DmaTile<64, 64, 64, 2, 2, 2, true>>(s, st, stream);
+        merge_folded<192, MergeT1>(s, st, stream);
     else
-        merge_folded<384, DmaTile<64, 64, 128, 2, 2, 3, true>, 4>(s, st, stream);
+        merge_folded<384, MergeT2, kMergeLoaders2>(s, st, stream);
 }
 
 }  // namespace
@@ -789,4 +811,42 @@ extern "C" int bfhip_debug_window_attention_noalloc(const void *qkv, const float
     window_attention_launch(qkv, qkv_bias, bias_mat, out, term, height, width, channels, heads,
                             shift, items, s);
     return launch_ok(error, cap, "launch window attention without allocation");
+}
+
+// ---- Patch-merge gather probe (include/bfhip_debug.h) ----------------------
+// The merge of stage `stage` on the caller's fp16 tokens xh [B, H, W, C] with
+// identity reduction weights whose columns go through merge_tap_order (as the
+// folded weights do at create) and a plain fp32 store: the output row m is
+// then the reference's unfold row, out[m][c*4 + q] = xh[token q of m][c].
+extern "C" int bfhip_debug_swin_merge_gather(bf_cuda_swin *s, int stage, const void *xh, float *out,
+                                             void *stream, char *error, size_t cap) {
+    if (!s || stage < 0 || stage > 2 || !xh || !out) return fail(error, cap, "invalid merge gather probe");
+    if (((uintptr_t)xh & 15) || ((uintptr_t)out & 15))
+        return fail(error, cap, "merge gather probe buffers must be 16-byte aligned");
+    const int C = kC[stage], B = (int)s->batches, H = s->h[stage], W = s->w[stage];
+    const int T2 = B * s->h[stage + 1] * s->w[stage + 1];
+    const std::vector<int> perm = merge_tap_order(C);
+    std::vector<uint16_t> wt((size_t)4 * C * 4 * C, 0);  // [4C outputs][4C columns]
+    for (int kk = 0; kk < 4 * C; ++kk) wt[(size_t)perm[kk] * 4 * C + kk] = 0x3C00;  // fp16 1.0
+    bf16 *w = nullptr;
+    if (!hip_ok(hipMalloc(&w, wt.size() * 2), error, cap, "allocate merge probe weights")) return 0;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    int ok = hip_ok(hipMemcpy(w, wt.data(), wt.size() * 2, hipMemcpyHostToDevice), error, cap,
+                    "upload merge probe weights");
+    if (ok) {
+        const EpiRowsF32 epi{out, nullptr, 4 * C, T2, 4 * C, 0};
+        const bf16 *x = static_cast<const bf16 *>(xh);
+        // Same (C, tile, loader waves) per stage as merge_op; the reduction
+        // runs over 4C outputs here instead of 2C.
+        if (stage == 0)
+            merge_gemm<96, MergeT0, 0>(x, B, H, W, w, 4 * C, epi, st);
+        else if (stage == 1)
+            merge_gemm<192, MergeT1, 0>(x, B, H, W, w, 4 * C, epi, st);
+        else
+            merge_gemm<384, MergeT2, kMergeLoaders2>(x, B, H, W, w, 4 * C, epi, st);
+        ok = launch_ok(error, cap, "launch merge gather probe") &&
+             hip_ok(hipStreamSynchronize(st), error, cap, "merge gather probe");
+    }
+    (void)hipFree(w);
+    return ok;
 }

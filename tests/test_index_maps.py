@@ -102,3 +102,87 @@ def test_im2col_times_weights_is_the_oracle_conv(case):
     got = got.transpose(0, 3, 1, 2)
     assert ref.shape == got.shape
     np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-5)
+
+
+# Channels-last gather map: the camera neck's geometries (batch 2) plus odd
+# sizes, strides and the x-major row order.
+NHWC_GEOMS = [
+    # (ci, ih, iw, k, stride, pad)
+    (16, 16, 44, 3, 1, 1), (8, 64, 176, 5, 4, 2), (32, 64, 176, 5, 2, 2), (24, 32, 88, 1, 1, 0),
+    (16, 36, 36, 3, 2, 1), (8, 5, 7, 3, 1, 1), (8, 7, 5, 5, 2, 2),
+]
+
+
+@pytest.mark.parametrize("geom", NHWC_GEOMS)
+@pytest.mark.parametrize("yfast", [False, True])
+def test_conv_im2col_nhwc_is_the_nchw_map_relaid(geom, yfast):
+    ci, ih, iw, k, s, p = geom
+    b = 2
+    oh, ow = (ih + 2 * p - k) // s + 1, (iw + 2 * p - k) // s + 1
+    nchw = index_maps.conv_im2col(b, ci, ih, iw, k, k, s, s, p, p, oh, ow, False)
+    nhwc = index_maps.conv_im2col_nhwc(b, ci, ih, iw, k, k, s, s, p, p, oh, ow, yfast)
+    # NCHW flat -> (n, c, iy, ix) -> NHWC flat; reduction c*KK + tap -> tap*Ci + c.
+    n = nchw // (ci * ih * iw)
+    r = nchw % (ci * ih * iw)
+    c, iy, ix = r // (ih * iw), (r // iw) % ih, r % iw
+    relaid = np.where(nchw >= 0, ((n * ih + iy) * iw + ix) * ci + c, -1)
+    kk = k * k
+    col = np.arange(kk * ci)
+    relaid = relaid[:, (col % ci) * kk + col // ci]
+    if yfast:  # GEMM row n*OH*OW + ox*OH + oy holds NCHW row n*OH*OW + oy*OW + ox
+        rows = np.arange(b * oh * ow)
+        nn, pos = rows // (oh * ow), rows % (oh * ow)
+        relaid = relaid[nn * oh * ow + (pos % oh) * ow + pos // oh]
+    np.testing.assert_array_equal(nhwc, relaid)
+    part = index_maps.conv_im2col_nhwc(b, ci, ih, iw, k, k, s, s, p, p, oh, ow, yfast,
+                                       rows=range(5, 17))
+    np.testing.assert_array_equal(part, nhwc[5:17])
+
+
+@pytest.mark.parametrize("geom", NHWC_GEOMS[:4])
+def test_conv_im2col_nhwc_gathers_torch_conv(geom):
+    """The gathered rows times channels-last weights are torch's conv2d."""
+    import torch
+    import torch.nn.functional as F
+    ci, ih, iw, k, s, p = geom
+    b, co = 2, 5
+    oh, ow = (ih + 2 * p - k) // s + 1, (iw + 2 * p - k) // s + 1
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((b, ih, iw, ci))
+    w = rng.standard_normal((co, ci, k, k))
+    idx = index_maps.conv_im2col_nhwc(b, ci, ih, iw, k, k, s, s, p, p, oh, ow)
+    flat = np.concatenate([x.ravel(), [0.0]])
+    a = flat[np.where(idx >= 0, idx, flat.size - 1)]
+    got = a @ w.transpose(0, 2, 3, 1).reshape(co, -1).T
+    ref = F.conv2d(torch.from_numpy(x).permute(0, 3, 1, 2), torch.from_numpy(w), stride=s,
+                   padding=p).permute(0, 2, 3, 1).reshape(-1, co).numpy()
+    np.testing.assert_allclose(got, ref, rtol=1e-10, atol=1e-10)
+
+
+@pytest.mark.parametrize("shape", [(2, 8, 22, 3), (1, 7, 14, 4), (2, 5, 7, 2), (1, 1, 1, 8),
+                                   (1, 64, 176, 2)])
+def test_merge_unfold_matches_pad_unfold(shape):
+    import torch
+    import torch.nn.functional as F
+    b, h, w, c = shape
+    ids = np.arange(b * h * w * c, dtype=np.float64).reshape(b, h, w, c) + 1
+    t = torch.from_numpy(ids).permute(0, 3, 1, 2)
+    t = F.pad(t, (0, w % 2, 0, h % 2))
+    u = F.unfold(t, kernel_size=2, stride=2)  # [b, 4c, L], rows c*4 + ky*2 + kx
+    expect = u.permute(0, 2, 1).reshape(-1, 4 * c).numpy().astype(np.int64) - 1
+    np.testing.assert_array_equal(index_maps.merge_unfold(b, h, w, c), expect)
+
+
+@pytest.mark.parametrize("sizes", [(16, 44, 32, 88), (8, 22, 16, 44), (3, 4, 5, 7), (2, 2, 3, 4),
+                                   (5, 3, 9, 6), (1, 1, 2, 2)])
+def test_bilinear_onehot_matches_interpolate(sizes):
+    import torch
+    import torch.nn.functional as F
+    ih, iw, oh, ow = sizes
+    sel = np.arange(ih * iw)
+    got = index_maps.bilinear_onehot(ih, iw, oh, ow, sel)
+    eye = torch.eye(ih * iw, dtype=torch.float64).reshape(ih * iw, 1, ih, iw)
+    ref = F.interpolate(eye, size=(oh, ow), mode="bilinear", align_corners=False)[:, 0].numpy()
+    np.testing.assert_allclose(got, ref, rtol=0, atol=2e-7)
+    if oh == 2 * ih and ow == 2 * iw:  # dyadic weights: exact in float32
+        np.testing.assert_array_equal(got, ref.astype(np.float32))
