@@ -152,17 +152,23 @@ class _Init:
     so that a wrong branch cannot hide under the residual stream.
     """
 
-    def __init__(self, seed: int, mode: str = "baseline", gain: float = 1.0):
+    def __init__(self, seed: int, mode: str = "baseline", gain: float = 1.0, offset: float = 0.0):
         if mode not in ("baseline", "fan_in"):
             raise ValueError(mode)
-        self.seed, self.mode, self.gain = seed, mode, gain
+        self.seed, self.mode, self.gain, self.offset = seed, mode, gain, offset
 
     def weight(self, name, shape, fan_in):
         std = 0.02 if self.mode == "baseline" else self.gain / np.sqrt(fan_in)
         return randn(self.seed, name, shape, std)
 
     def bias(self, name, shape):
-        return randn(self.seed, name, shape, 0.02)
+        b = randn(self.seed, name, shape, 0.02)
+        # ``offset``: the residual branches' output biases (attention proj and
+        # fc2) add a common offset to every channel, so the residual rows the
+        # LayerNorms see carry a mean far larger than their spread.
+        if self.offset and name.endswith(("attn.w_msa.proj.bias", "ffn.layers.1.bias")):
+            b = (b + self.offset).astype(np.float32)
+        return b
 
     def norm(self, prefix, c):
         return [(prefix + ".weight", randn(self.seed, prefix + ".weight", (c,), 0.02, 1.0)),
@@ -236,14 +242,16 @@ def neck_tensors(init: _Init):
     return out
 
 
-def camera_branch_tensors(seed: int = 0, mode: str = "baseline", gain: float = 1.0):
-    init = _Init(seed, mode, gain)
+def camera_branch_tensors(seed: int = 0, mode: str = "baseline", gain: float = 1.0,
+                          offset: float = 0.0):
+    init = _Init(seed, mode, gain, offset)
     return swin_tensors(init) + neck_tensors(init)
 
 
-def write_camera_branch(path, seed: int = 0, mode: str = "baseline", gain: float = 1.0) -> pathlib.Path:
+def write_camera_branch(path, seed: int = 0, mode: str = "baseline", gain: float = 1.0,
+                        offset: float = 0.0) -> pathlib.Path:
     path = pathlib.Path(path)
-    write_bfw(camera_branch_tensors(seed, mode, gain), path)
+    write_bfw(camera_branch_tensors(seed, mode, gain, offset), path)
     return path
 
 

@@ -136,10 +136,10 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 // ------------------------------------------------------------------ epilogue
-// Optional epilogue traits: kRowStat epilogues need one float2 per output row
+// Optional epilogue traits: kRowStat epilogues need one Stat per output row
 // (e.g. LayerNorm statistics): thread t < BM fetches row m0 + t's inputs at
 // kernel start (Pre stat_load(row), so the loads overlap the main loop),
-// reduces them after it (float2 stat_finish(pre)) into LDS, and rows() gets
+// reduces them after it (Stat stat_finish(pre)) into LDS, and rows() gets
 // them; kFullRow epilogues take the whole staged fp32 tile
 // (tile<T>(sC, stride, m0, n0, tid)) to reduce across full rows or to store it
 // in another order.
@@ -149,18 +149,61 @@ template <class E>
 struct EpiRowStat<E, std::void_t<decltype(E::kRowStat)>> : std::bool_constant<E::kRowStat> {};
 struct NoRowStat {};
 template <class E, bool = EpiRowStat<E>::value>
-struct EpiPre { using type = NoRowStat; };
+struct EpiPre { using type = NoRowStat; using stat = float2; };
 template <class E>
-struct EpiPre<E, true> { using type = typename E::Pre; };
+struct EpiPre<E, true> { using type = typename E::Pre; using stat = typename E::Stat; };
+
+// kCorrSteps > 0 (row-statistics epilogues only): before staging, every
+// accumulator gets a rank-limited correction added on the matrix cores,
+// acc[row][col] += sum over kCorrSteps 32-deep k-steps of A[row][k] B[col][k].
+// A carries per-row values split into two fp16 words each: k-slots 2t and
+// 2t + 1 hold hi = fp16(u_t) and lo = fp16(u_t - hi), u_4q..u_4q+3 coming
+// from the row's Stat as epi.corr_u4(stat, q); B is the epilogue's fp16
+// table (epi.corr_col(col, k0) -> 8 words at k0..k0+7), fetched at kernel
+// start.  The LayerNorm-folded linears use it for their centring correction
+// (ln_fold.h).
+template <class E, class = void>
+struct EpiCorr { static constexpr int value = 0; };
+template <class E>
+struct EpiCorr<E, std::void_t<decltype(E::kCorrSteps)>> { static constexpr int value = E::kCorrSteps; };
+
+template <class T, class Epi, int KC = EpiCorr<Epi>::value>
+struct EpiPrefetch {
+    typename EpiPre<Epi>::type pre;
+    bf16x8 cb[T::kFragN][KC];  // correction B fragments of the wave's columns
+};
+template <class T, class Epi>
+struct EpiPrefetch<T, Epi, 0> {
+    typename EpiPre<Epi>::type pre;
+};
 
 template <class T, class Epi>
-__device__ __forceinline__ typename EpiPre<Epi>::type epi_prefetch(const Epi &epi, int m0, int tid) {
+__device__ __forceinline__ EpiPrefetch<T, Epi> epi_prefetch(const Epi &epi, int m0, int n0, int tid) {
     static_assert(!EpiRowStat<Epi>::value || T::BM <= T::kThreads, "one thread per tile row");
-    typename EpiPre<Epi>::type pre{};
+    static_assert(EpiCorr<Epi>::value == 0 || (EpiRowStat<Epi>::value && Epi::kRowVector),
+                  "the correction reads the staged row statistics");
+    EpiPrefetch<T, Epi> pf{};
     if constexpr (EpiRowStat<Epi>::value)
-        if (tid < T::BM) pre = epi.stat_load(m0 + tid);
-    return pre;
+        if (tid < T::BM) pf.pre = epi.stat_load(m0 + tid);
+    if constexpr (EpiCorr<Epi>::value > 0) {
+        const int lane = tid & 63, wn = (tid >> 6) % T::WN;
+#pragma unroll
+        for (int j = 0; j < T::kFragN; ++j)
+#pragma unroll
+            for (int c = 0; c < EpiCorr<Epi>::value; ++c)
+                pf.cb[j][c] = epi.corr_col(n0 + wn * T::kWaveCols + j * 16 + (lane & 15),
+                                           32 * c + 8 * (lane >> 4));
+    }
+    return pf;
 }
+// kQuadRows epilogues reduce across the 16 lanes that hold one 64-column
+// group (row16_sum): they need the whole-quad path below, in which every
+// thread owns one column quad for the whole tile and control flow is uniform
+// over each row of 16 lanes.
+template <class E, class = void>
+struct EpiQuadRows : std::false_type {};
+template <class E>
+struct EpiQuadRows<E, std::void_t<decltype(E::kQuadRows)>> : std::bool_constant<E::kQuadRows> {};
 template <class E, class = void>
 struct EpiFullRow : std::false_type {};
 template <class E>
@@ -171,16 +214,40 @@ struct EpiFullRow<E, std::void_t<decltype(E::kFullRow)>> : std::bool_constant<E:
 // arena) so that whole rows leave as 16-byte vectors; column-fragment
 // epilogues take the four rows of each MFMA fragment directly.
 template <class T, class Epi>
-__device__ __forceinline__ void store_tile(const f32x4 (&acc)[T::kFragM][T::kFragN], const Epi &epi,
+__device__ __forceinline__ void store_tile(f32x4 (&acc)[T::kFragM][T::kFragN], const Epi &epi,
                                            unsigned char *smem, int m0, int n0, int tid,
-                                           const typename EpiPre<Epi>::type &pre = {}) {
+                                           const EpiPrefetch<T, Epi> &pf) {
     const int lane = tid & 63, wave = tid >> 6;
     const int wm = wave / T::WN, wn = wave % T::WN;
     if constexpr (Epi::kRowVector) {
         constexpr int kCStride = T::BN + 4;  // floats; staggers rows across banks
         float *sC = reinterpret_cast<float *>(smem);
-        float2 *sStat = reinterpret_cast<float2 *>(smem + (size_t)T::BM * kCStride * sizeof(float));
+        using Stat = typename EpiPre<Epi>::stat;
+        Stat *sStat = reinterpret_cast<Stat *>(smem + (size_t)T::BM * kCStride * sizeof(float));
         const int r0 = wm * T::kWaveRows + 4 * (lane >> 4), c0 = wn * T::kWaveCols + (lane & 15);
+        if constexpr (EpiCorr<Epi>::value > 0) {
+            // Row statistics first (the correction's A operand), then the
+            // correction on the matrix cores, then the staging below.
+            if (tid < T::BM) sStat[tid] = epi.stat_finish(pf.pre);
+            lds_barrier();
+#pragma unroll
+            for (int i = 0; i < T::kFragM; ++i) {
+                const Stat &st = sStat[wm * T::kWaveRows + i * 16 + (lane & 15)];
+#pragma unroll
+                for (int c = 0; c < EpiCorr<Epi>::value; ++c) {
+                    const float4 u4 = epi.corr_u4(st, 4 * c + (lane >> 4));
+                    const float u[4] = {u4.x, u4.y, u4.z, u4.w};
+                    bf16x8 a;
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        a[2 * t] = to_half(u[t]);
+                        a[2 * t + 1] = to_half(u[t] - half_to_f32(a[2 * t]));
+                    }
+#pragma unroll
+                    for (int j = 0; j < T::kFragN; ++j) acc[i][j] = mfma16_as<T::kF16>(a, pf.cb[j][c], acc[i][j]);
+                }
+            }
+        }
 #pragma unroll
         for (int i = 0; i < T::kFragM; ++i)
 #pragma unroll
@@ -188,13 +255,13 @@ __device__ __forceinline__ void store_tile(const f32x4 (&acc)[T::kFragM][T::kFra
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
                     sC[(r0 + i * 16 + r) * kCStride + c0 + j * 16] = acc[i][j][r];
-        if constexpr (EpiRowStat<Epi>::value)
-            if (tid < T::BM) sStat[tid] = epi.stat_finish(pre);
+        if constexpr (EpiRowStat<Epi>::value && EpiCorr<Epi>::value == 0)
+            if (tid < T::BM) sStat[tid] = epi.stat_finish(pf.pre);
         lds_barrier();  // LDS only: prefetches in flight stay in flight
         constexpr int kQuads = T::BN / 4;
-        static_assert(!EpiRowStat<Epi>::value ||
+        static_assert(!(EpiRowStat<Epi>::value || EpiQuadRows<Epi>::value) ||
                           (T::kThreads % kQuads == 0 && T::BM % (T::kThreads / kQuads) == 0),
-                      "row-statistics epilogues need whole column quads per thread");
+                      "row-statistics and 64-column-group epilogues need whole column quads per thread");
         if constexpr (EpiFullRow<Epi>::value) {
             epi.template tile<T>(sC, kCStride, m0, n0, tid);
         } else if constexpr (T::kThreads % kQuads == 0 && T::BM % (T::kThreads / kQuads) == 0) {
@@ -232,7 +299,7 @@ __device__ __forceinline__ void store_tile(const f32x4 (&acc)[T::kFragM][T::kFra
 template <class T, class Epi>
 constexpr size_t epilogue_bytes() {
     return Epi::kRowVector ? (size_t)T::BM * (T::BN + 4) * sizeof(float) +
-                                 (EpiRowStat<Epi>::value ? (size_t)T::BM * sizeof(float2) : 0)
+                                 (EpiRowStat<Epi>::value ? (size_t)T::BM * sizeof(typename EpiPre<Epi>::stat) : 0)
                            : 0;
 }
 
@@ -256,7 +323,7 @@ __global__ __launch_bounds__(T::kThreads) void gemm_kernel(ALoad al, BLoad bl, E
 
     al.setup(m0, tid);
     bl.setup(n0, tid);
-    const auto pre = epi_prefetch<T>(epi, m0, tid);
+    const auto pre = epi_prefetch<T>(epi, m0, n0, tid);
 
     f32x4 acc[T::kFragM][T::kFragN];
 #pragma unroll
@@ -451,7 +518,7 @@ __global__ __launch_bounds__(T::kThreads) void gemm_dma_kernel(ALoad al, BLoad b
 
     al.setup(m0, tid);
     bl.setup(n0, tid);
-    const auto pre = epi_prefetch<T>(epi, m0, tid);
+    const auto pre = epi_prefetch<T>(epi, m0, n0, tid);
 
     f32x4 acc[T::kFragM][T::kFragN];
 #pragma unroll
@@ -575,12 +642,13 @@ __global__ __launch_bounds__(T::kThreads + ALoad::kWaves * kWave) void gemm_spec
             }
         }
         __syncthreads();  // the compute waves' end-of-loop barrier
+        if constexpr (EpiCorr<Epi>::value > 0) __syncthreads();  // store_tile's statistics barrier
         if constexpr (Epi::kRowVector) __syncthreads();  // store_tile's staging barrier
         return;
     }
 
     const int wm = wave / T::WN, wn = wave % T::WN;
-    const auto pre = epi_prefetch<T>(epi, m0, tid);
+    const auto pre = epi_prefetch<T>(epi, m0, n0, tid);
     f32x4 acc[T::kFragM][T::kFragN];
 #pragma unroll
     for (int i = 0; i < T::kFragM; ++i)

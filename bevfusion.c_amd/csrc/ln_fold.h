@@ -4,12 +4,20 @@
 //   y_j = sum_k ((x_k - mu) r g_k + beta_k) W_jk + b_j
 //       = r (sum_k x_k W'_jk - mu c_j) + d_j,
 //   W'_jk = g_k W_jk,  c_j = sum_k W'_jk,  d_j = b_j + sum_k beta_k W_jk,
-// with mu and r = 1/sqrt(var + 1e-5) the row's statistics.  W' (fp16), c and
-// d are built once at create; c sums the fp16-rounded W' the matrix cores
-// actually multiply, so mu c_j cancels the mean that fp16(x) carries into the
-// product.  The GEMM therefore runs on the residual stream itself, held as an
-// fp16 copy xh next to the fp32 x, and the LayerNorm becomes two fp32 terms in
-// the epilogue: no normalisation pass over x and no launch for it.
+// with mu and r = 1/sqrt(var + 1e-5) the row's statistics.  W' (fp16) and d
+// are built once at create.  The GEMM runs on the residual stream itself,
+// held as an fp16 copy xh next to the fp32 x, and the LayerNorm becomes fp32
+// terms in the epilogue: no normalisation pass over x and no launch for it.
+//
+// The fp16 copy is centred per statistics group: the writer stores
+// xh_k = fp16(x_k - m_g) with m_g the mean of the group g (64 channels) that
+// holds k, so its rounding error scales with the group's spread, not with a
+// common offset the row may carry (a row whose mean is 50x its standard
+// deviation would otherwise lose ~50x the precision of fp16(LN(x))).  The
+// consumer adds the group means back through per-group column sums:
+//   sum_k x_k W'_jk - mu c_j = sum_k xh_k W'_jk + sum_g (m_g - mu) c_jg,
+//   c_jg = sum over k in group g of W'_jk,
+// with c_jg summed from the fp16-rounded W' the matrix cores multiply.
 //
 // The statistics come from the epilogue that writes x (the residual adds of
 // proj and fc2, the patch-merge reduction): every 64-column group of a row
@@ -28,24 +36,37 @@ namespace bfhip {
 
 constexpr int kStatCols = 64;  // columns per statistics group
 
+// One row's LayerNorm terms for a consumer over N statistics groups: the
+// mean mu, r = 1/sqrt(var + 1e-5) and u_g = m_g - mu, the group means
+// relative to the row mean (the centring correction above).
+template <int N>
+struct RowLn {
+    static constexpr int kPad = (N + 3) / 4 * 4;  // u in whole 16-byte blocks
+    float u[kPad];                                // zero past N
+    float mean, r, unused[2];
+};
+
 // Combines equal-count (mean, M2) group partials of COLS columns each in
-// index order into (mean, 1/sqrt(var + 1e-5)); absent groups are passed as
-// (0, 0).
+// index order into the row's RowLn; absent groups are passed as (0, 0).
 template <int N, int COLS = kStatCols>
-__device__ __forceinline__ float2 ln_combine(const float2 (&p)[N]) {
+__device__ __forceinline__ RowLn<N> ln_combine(const float2 (&p)[N]) {
     float s = 0.0f;
 #pragma unroll
     for (int g = 0; g < N; ++g) s += p[g].x;
     const float mean = s * (1.0f / N);
     float m2 = 0.0f, dev = 0.0f;
+    RowLn<N> out{};
 #pragma unroll
     for (int g = 0; g < N; ++g) {
         const float d = p[g].x - mean;
         m2 += p[g].y;
         dev += d * d;
+        out.u[g] = d;
     }
     const float var = (m2 + (float)COLS * dev) * (1.0f / (COLS * N));
-    return make_float2(mean, rsqrtf(var + 1e-5f));
+    out.mean = mean;
+    out.r = rsqrtf(var + 1e-5f);
+    return out;
 }
 
 // Statistics sources.  load(row) fetches a row's partials (issued at kernel
@@ -55,6 +76,7 @@ template <int G>
 struct LnRows {
     static constexpr int kGroups = G;
     struct Pre { float2 p[G]; };
+    using Stat = RowLn<G>;
     const float2 *stats;
     __device__ Pre load(int row) const {
         Pre r;
@@ -63,17 +85,19 @@ struct LnRows {
         for (int g = 0; g < G; ++g) r.p[g] = p[g];
         return r;
     }
-    __device__ float2 finish(const Pre &r) const { return ln_combine(r.p); }
+    __device__ Stat finish(const Pre &r) const { return ln_combine(r.p); }
 };
 
 // Patch-merge row (n, oy, ox): its 2x2 source tokens of the previous stage
 // ([B, H, W] tokens, G groups of COLS columns each), taps q = 2 dy + dx in
 // order; a tap past an odd edge is a token of zeros (mean 0, M2 0), as the
 // zero padding before the reference's unfold (swin_backbone.c:278-302).
+// Group q * G + g covers folded columns q * C + g * COLS .. + COLS - 1.
 template <int G, int COLS = kStatCols>
 struct LnMerge {
-    static constexpr int kGroups = G;
+    static constexpr int kGroups = 4 * G;
     struct Pre { float2 p[4 * G]; };
+    using Stat = RowLn<4 * G>;
     const float2 *stats;
     int H, W;
     __device__ Pre load(int m) const {
@@ -90,13 +114,15 @@ struct LnMerge {
         }
         return r;
     }
-    __device__ float2 finish(const Pre &r) const { return ln_combine<4 * G, COLS>(r.p); }
+    __device__ Stat finish(const Pre &r) const { return ln_combine<4 * G, COLS>(r.p); }
 };
 
 struct LnNone {  // producers that take no LayerNorm on their input
+    static constexpr int kGroups = 1;
     struct Pre {};
+    using Stat = RowLn<1>;
     __device__ Pre load(int) const { return Pre{}; }
-    __device__ float2 finish(const Pre &) const { return make_float2(0.0f, 0.0f); }
+    __device__ Stat finish(const Pre &) const { return Stat{}; }
 };
 
 // Sum over each DPP row of 16 lanes, returned to every lane of the row:
@@ -115,15 +141,42 @@ __device__ __forceinline__ float row16_sum(float v) {
     return v;
 }
 
-struct LnCol {
-    int col;
-    float4 d, c;  // shift (bias or folded d) and folded column sums
+// The centring correction on the matrix cores (the GEMM core's kCorrSteps):
+// k-slots 2g and 2g + 1 of a row hold u_g split into two fp16 words
+// (hi = fp16(u_g), lo = fp16(u_g - hi), so hi + lo carries u_g to ~22 bits;
+// the core builds them from corr_u4), and both slots of column j hold
+// fp16(c_jg); the table `corr` is [N][steps * 32] fp16 words, zero past 2 NG.
+// The product is added to the accumulators before the epilogue, which then
+// applies r acc + d.
+template <int NG>
+struct LnCorr {
+    static constexpr int kSteps = (2 * NG + 31) / 32;
 };
 
-__device__ __forceinline__ float4 ln_apply(float4 v, float2 st, const LnCol &c) {
-    // r (acc - mu c) + d
-    return make_float4(st.y * (v.x - st.x * c.c.x) + c.d.x, st.y * (v.y - st.x * c.c.y) + c.d.y,
-                       st.y * (v.z - st.x * c.c.z) + c.d.z, st.y * (v.w - st.x * c.c.w) + c.d.w);
+// u of groups 4q .. 4q + 3 (zero past NG): the groups behind k-slots
+// 8q .. 8q + 7 of the correction operand.
+template <int NG>
+__device__ __forceinline__ float4 ln_corr_u4(const RowLn<NG> &st, int q) {
+    constexpr int kBlocks = RowLn<NG>::kPad / 4;
+    const float4 v = reinterpret_cast<const float4 *>(st.u)[q < kBlocks ? q : kBlocks - 1];
+    return q < kBlocks ? v : make_float4(0.f, 0.f, 0.f, 0.f);
+}
+
+__device__ __forceinline__ bf16x8 ln_corr_col(const bf16 *corr, int steps, int col, int N, int k0) {
+    return col < N ? *reinterpret_cast<const bf16x8 *>(corr + (size_t)col * steps * 32 + k0) : bf16x8{};
+}
+
+// A column quad's shift (bias or folded d).
+struct LnCol {
+    int col;
+    float4 d;
+};
+
+// r acc + d: acc already holds the centring correction.
+template <int NG>
+__device__ __forceinline__ float4 ln_apply(float4 v, const RowLn<NG> &st, const LnCol &c) {
+    return make_float4(fmaf(st.r, v.x, c.d.x), fmaf(st.r, v.y, c.d.y), fmaf(st.r, v.z, c.d.z),
+                       fmaf(st.r, v.w, c.d.w));
 }
 
 __device__ __forceinline__ void store_half4(bf16 *p, float4 y) {
@@ -133,31 +186,37 @@ __device__ __forceinline__ void store_half4(bf16 *p, float4 y) {
 }
 
 // Writer of the residual stream: y = [LN-folded] acc + shift [+ x], stored as
-// fp32 x, fp16 xh, and per-64-column (mean, M2) of y.  x, xh: [M, N]
-// row-major; stats: [M, N / 64].  N % 64 == 0 and 16-byte aligned buffers
-// (host-checked); a tile's column quads of one 64-column group are 16
-// consecutive lanes, which reduce the group with cross-lane sums.
+// fp32 x, the centred fp16 copy xh = fp16(y - m_g), and per-64-column
+// (m_g, M2_g) of y.  x, xh: [M, N] row-major; stats: [M, N / 64].  N % 64 ==
+// 0 and 16-byte aligned buffers (host-checked); a tile's column quads of one
+// 64-column group are 16 consecutive lanes, which reduce the group with
+// cross-lane sums.
 template <bool kLnIn, bool kResidual, class Src = LnNone>
 struct EpiStatsRows {
     static constexpr bool kRowVector = true;
     static constexpr bool kRowStat = kLnIn;
+    static constexpr bool kQuadRows = true;  // row16_sum over each 64-column group
+    static constexpr int NG = Src::kGroups;
+    static constexpr int kCorrSteps = kLnIn ? LnCorr<NG>::kSteps : 0;
     float *x;
     bf16 *xh;
     float2 *stats;
     const float *shift;  // bias (may be null), or the folded d with kLnIn
-    const float *csum;   // folded column sums c (kLnIn)
+    const bf16 *corr;    // centring-correction table (kLnIn; LnCorr)
     Src src;             // row statistics of the LayerNorm input (kLnIn)
     int M, N;
-    __device__ LnCol column(int col) const {
-        return LnCol{col, load_quad(shift, col, N),
-                     kLnIn ? load_quad(csum, col, N) : make_float4(0.f, 0.f, 0.f, 0.f)};
-    }
+    __device__ LnCol column(int col) const { return LnCol{col, load_quad(shift, col, N)}; }
     using Pre = typename Src::Pre;
+    using Stat = typename Src::Stat;
     __device__ Pre stat_load(int row) const { return row < M ? src.load(row) : Pre{}; }
-    __device__ float2 stat_finish(const Pre &p) const { return src.finish(p); }
+    __device__ Stat stat_finish(const Pre &p) const { return src.finish(p); }
+    __device__ float4 corr_u4(const Stat &st, int q) const { return ln_corr_u4(st, q); }
+    __device__ bf16x8 corr_col(int col, int k0) const {
+        return ln_corr_col(corr, LnCorr<NG>::kSteps, col, N, k0);
+    }
     template <int R>
     __device__ void rows(int row0, int step, const LnCol &c, const float4 (&v)[R],
-                         const float2 *st = nullptr) const {
+                         const Stat *st = nullptr) const {
         if (c.col >= N) return;  // whole 64-column groups: uniform over the 16 lanes
         float4 y[R];
         if constexpr (kResidual) {
@@ -181,7 +240,7 @@ struct EpiStatsRows {
             const float m2 = row16_sum((a * a + b * b) + (cc * cc + d * d));
             if (row < M) {
                 *reinterpret_cast<float4 *>(x + (size_t)row * N + c.col) = y[i];
-                store_half4(xh + (size_t)row * N + c.col, y[i]);
+                store_half4(xh + (size_t)row * N + c.col, make_float4(a, b, cc, d));
                 if ((c.col & (kStatCols - 1)) == 0)
                     stats[(size_t)row * (N / kStatCols) + c.col / kStatCols] = make_float2(mean, m2);
             }
@@ -189,25 +248,32 @@ struct EpiStatsRows {
     }
 };
 
-// Reader of LN(x): out = fp16(act(r (acc - mu c) + d)) for the QKV (no
-// activation) and fc1 (GELU) linears.  ld % 4 == 0, N % 4 == 0.
+// Reader of LN(x): out = fp16(act(r (acc + sum_g u_g c_jg) + d)) for the QKV
+// (no activation) and fc1 (GELU) linears over the centred copy, the sum added
+// on the matrix cores (kCorrSteps).  ld % 4 == 0, N % 4 == 0.
 template <bool GELU, class Src>
 struct EpiLnF16 {
     static constexpr bool kRowVector = true;
     static constexpr bool kRowStat = true;
+    static constexpr int NG = Src::kGroups;
+    static constexpr int kCorrSteps = LnCorr<NG>::kSteps;
     bf16 *out;
-    const float *shift, *csum;
+    const float *shift;
+    const bf16 *corr;  // centring-correction table (LnCorr)
     Src src;
     int ld, M, N;
-    __device__ LnCol column(int col) const {
-        return LnCol{col, load_quad(shift, col, N), load_quad(csum, col, N)};
-    }
+    __device__ LnCol column(int col) const { return LnCol{col, load_quad(shift, col, N)}; }
     using Pre = typename Src::Pre;
+    using Stat = typename Src::Stat;
     __device__ Pre stat_load(int row) const { return row < M ? src.load(row) : Pre{}; }
-    __device__ float2 stat_finish(const Pre &p) const { return src.finish(p); }
+    __device__ Stat stat_finish(const Pre &p) const { return src.finish(p); }
+    __device__ float4 corr_u4(const Stat &st, int q) const { return ln_corr_u4(st, q); }
+    __device__ bf16x8 corr_col(int col, int k0) const {
+        return ln_corr_col(corr, LnCorr<NG>::kSteps, col, N, k0);
+    }
     template <int R>
     __device__ void rows(int row0, int step, const LnCol &c, const float4 (&v)[R],
-                         const float2 *st) const {
+                         const Stat *st) const {
         if (c.col >= N) return;
 #pragma unroll
         for (int i = 0; i < R; ++i) {

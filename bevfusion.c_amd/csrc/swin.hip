@@ -73,8 +73,10 @@ constexpr bool kFusedWmsa[4] = {true, false, false, false};
 struct BlockW {
     const float *n1s, *n1b, *n2s, *n2b, *qkv_b, *proj_b, *fc1_b, *fc2_b, *bias_mat;
     // Stages 1-3: qkv_w and fc1_w hold the LN-folded weights W' (ln_fold.h),
-    // with their column sums c and shifts d.
-    const float *qkv_c, *qkv_d, *fc1_c, *fc1_d;
+    // with their centring-correction tables (per-group column sums) and
+    // shifts d.
+    const bf16 *qkv_corr, *fc1_corr;
+    const float *qkv_d, *fc1_d;
     const bf16 *qkv_w, *proj_w, *fc1_w, *fc2_w;
     const bf16 *mlp_w;      // fc1/fc2 packed for the fused MLP (fused stages only)
     const bf16 *mlp_proj;   // proj packed for the fused MLP (fused stages only)
@@ -83,7 +85,7 @@ struct BlockW {
 
 struct BlockOff {
     size_t n1s, n1b, n2s, n2b, qkv_b, proj_b, fc1_b, fc2_b, bias_mat, qkv_w, proj_w, fc1_w, fc2_w;
-    size_t qkv_c, qkv_d, fc1_c, fc1_d;
+    size_t qkv_corr, qkv_d, fc1_corr, fc1_d;
     size_t mlp_w, mlp_proj, attn_term;
 };
 
@@ -98,7 +100,8 @@ struct bf_cuda_swin {
     BlockW blocks[4][6];
     const float *out_s[3], *out_b[3];
     const bf16 *merge_w[3];           // LN-folded, columns in tap-major order
-    const float *merge_c[3], *merge_d[3];
+    const bf16 *merge_corr[3];        // centring-correction tables (ln_fold.h)
+    const float *merge_d[3];
     float *x;
     bf16 *xn, *big;
     bf16 *xh[2];
@@ -109,11 +112,24 @@ namespace {
 
 // A linear fed by a LayerNorm, folded (ln_fold.h): W'[j][kk] =
 // fp16(g[k] W[j][k]) with k = perm(kk) (identity when perm is null),
-// c_j = sum of the fp16 W' row, d_j = b_j + sum_k beta_k W[j][k] (b may be
-// null); sums in double.
+// c[q][j] = sum of the fp16 W' row over the folded columns of statistics
+// group q (group_cols columns each), d_j = b_j + sum_k beta_k W[j][k] (b may
+// be null); sums in double.
 struct FoldedLinear {
     std::vector<uint16_t> w;
-    std::vector<float> c, d;
+    std::vector<float> c, d;  // c: [K / group_cols][N]
+    // c as the GEMM epilogue's centring-correction table (ln_fold.h,
+    // LnCorr): per column, fp16(c[q][j]) at k-slots 2q and 2q + 1, zero up to
+    // the next multiple of 32 slots.
+    std::vector<uint16_t> corr() const {
+        const size_t N = d.size(), groups = c.size() / N;
+        const size_t slots = (2 * groups + 31) / 32 * 32;
+        std::vector<uint16_t> t(N * slots, 0);
+        for (size_t j = 0; j < N; ++j)
+            for (size_t q = 0; q < groups; ++q)
+                t[j * slots + 2 * q] = t[j * slots + 2 * q + 1] = f16_bits(c[q * N + j]);
+        return t;
+    }
 };
 
 // Column order of the patch-merge reduction weights: folded column q*C + ch
@@ -128,22 +144,26 @@ std::vector<int> merge_tap_order(int C) {
 }
 
 FoldedLinear fold_ln(const float *W, const float *b, const float *g, const float *beta, int N,
-                     int K, const std::vector<int> *perm) {
+                     int K, const std::vector<int> *perm, int group_cols) {
     FoldedLinear f;
+    const int groups = K / group_cols;
     f.w.resize((size_t)N * K);
-    f.c.resize(N);
+    f.c.resize((size_t)groups * N);
     f.d.resize(N);
     for (int j = 0; j < N; ++j) {
         const float *row = W + (size_t)j * K;
-        double cs = 0.0, ds = b ? (double)b[j] : 0.0;
-        for (int kk = 0; kk < K; ++kk) {
-            const int k = perm ? (*perm)[kk] : kk;
-            const uint16_t h = f16_bits(g[k] * row[k]);
-            f.w[(size_t)j * K + kk] = h;
-            cs += (double)f16_value(h);
-            ds += (double)beta[k] * (double)row[k];
+        double ds = b ? (double)b[j] : 0.0;
+        for (int q = 0; q < groups; ++q) {
+            double cs = 0.0;
+            for (int kk = q * group_cols; kk < (q + 1) * group_cols; ++kk) {
+                const int k = perm ? (*perm)[kk] : kk;
+                const uint16_t h = f16_bits(g[k] * row[k]);
+                f.w[(size_t)j * K + kk] = h;
+                cs += (double)f16_value(h);
+                ds += (double)beta[k] * (double)row[k];
+            }
+            f.c[(size_t)q * N + j] = (float)cs;
         }
-        f.c[j] = (float)cs;
         f.d[j] = (float)ds;
     }
     return f;
@@ -266,18 +286,19 @@ static int swin_build(bf_cuda_swin *s, const bf_model *model, size_t batches, si
             o.attn_term = arena.add(nullptr, attn_term_elems((int)hd, (b & 1) ? 3 : 0) * 2);
             o.proj_w = arena.add_f16(proj_w, (size_t)c * c);
             o.fc2_w = arena.add_f16(fc2_w, (size_t)4 * c * c);
-            o.qkv_c = o.qkv_d = o.fc1_c = o.fc1_d = 0;
+            o.qkv_corr = o.qkv_d = o.fc1_corr = o.fc1_d = 0;
             if (st == 0) {  // fused window MSA and MLP: LayerNorm kept explicit
                 o.qkv_w = arena.add_f16(qkv_w, (size_t)3 * c * c);
                 o.fc1_w = arena.add_f16(fc1_w, (size_t)4 * c * c);
             } else {
-                const FoldedLinear fq = fold_ln(qkv_w, qkv_b, n1s, n1b, 3 * c, c, nullptr);
-                const FoldedLinear f1 = fold_ln(fc1_w, fc1_b, n2s, n2b, 4 * c, c, nullptr);
+                const FoldedLinear fq = fold_ln(qkv_w, qkv_b, n1s, n1b, 3 * c, c, nullptr, kStatCols);
+                const FoldedLinear f1 = fold_ln(fc1_w, fc1_b, n2s, n2b, 4 * c, c, nullptr, kStatCols);
                 o.qkv_w = arena.add(fq.w.data(), fq.w.size() * 2);
-                o.qkv_c = arena.add_f32(fq.c);
+                const std::vector<uint16_t> qc = fq.corr(), fc = f1.corr();
+                o.qkv_corr = arena.add(qc.data(), qc.size() * 2);
                 o.qkv_d = arena.add_f32(fq.d);
                 o.fc1_w = arena.add(f1.w.data(), f1.w.size() * 2);
-                o.fc1_c = arena.add_f32(f1.c);
+                o.fc1_corr = arena.add(fc.data(), fc.size() * 2);
                 o.fc1_d = arena.add_f32(f1.d);
             }
             o.mlp_w = o.mlp_proj = 0;
@@ -305,9 +326,13 @@ static int swin_build(bf_cuda_swin *s, const bf_model *model, size_t batches, si
         const float *ob = bind_f32(model, name, {(uint32_t)kC[st + 1]}, error, cap);
         if (!ms || !mb || !mw || !os || !ob) return 0;
         const std::vector<int> perm = merge_tap_order((int)c);
-        const FoldedLinear fm = fold_ln(mw, nullptr, ms, mb, 2 * c, 4 * c, &perm);
+        // Statistics groups of the merge input: 64 channels of each of the
+        // four tokens, or each whole 96-channel token at stage 0.
+        const int gcols = c % kStatCols ? (int)c : kStatCols;
+        const FoldedLinear fm = fold_ln(mw, nullptr, ms, mb, 2 * c, 4 * c, &perm, gcols);
         o_mw[st] = arena.add(fm.w.data(), fm.w.size() * 2);
-        o_mc[st] = arena.add_f32(fm.c);
+        const std::vector<uint16_t> mc = fm.corr();
+        o_mc[st] = arena.add(mc.data(), mc.size() * 2);
         o_md[st] = arena.add_f32(fm.d);
         o_os[st] = arena.add_f32(os, kC[st + 1]);
         o_ob[st] = arena.add_f32(ob, kC[st + 1]);
@@ -332,15 +357,15 @@ static int swin_build(bf_cuda_swin *s, const bf_model *model, size_t batches, si
                 w.fc2_b = F(o.fc2_b); w.bias_mat = F(o.bias_mat);
                 w.qkv_w = H(o.qkv_w); w.proj_w = H(o.proj_w); w.fc1_w = H(o.fc1_w);
                 w.fc2_w = H(o.fc2_w);
-                w.qkv_c = st ? F(o.qkv_c) : nullptr; w.qkv_d = st ? F(o.qkv_d) : nullptr;
-                w.fc1_c = st ? F(o.fc1_c) : nullptr; w.fc1_d = st ? F(o.fc1_d) : nullptr;
+                w.qkv_corr = st ? H(o.qkv_corr) : nullptr; w.qkv_d = st ? F(o.qkv_d) : nullptr;
+                w.fc1_corr = st ? H(o.fc1_corr) : nullptr; w.fc1_d = st ? F(o.fc1_d) : nullptr;
                 w.mlp_w = kFusedMlp[st] ? H(o.mlp_w) : nullptr;
                 w.mlp_proj = kFusedMlp[st] ? H(o.mlp_proj) : nullptr;
                 w.attn_term = H(o.attn_term);
             }
         for (int st = 0; st < 3; ++st) {
             s->merge_w[st] = H(o_mw[st]); s->out_s[st] = F(o_os[st]); s->out_b[st] = F(o_ob[st]);
-            s->merge_c[st] = F(o_mc[st]);
+            s->merge_corr[st] = H(o_mc[st]);
             s->merge_d[st] = F(o_md[st]);
         }
         // Attention score terms (relative bias + shift mask, in the kernel's
@@ -489,7 +514,7 @@ void block_op(bf_cuda_swin *s, int st, int b, int op, hipStream_t stream) {
             with_groups(C, [&](auto g) {
                 using Src = LnRows<decltype(g)::value>;
                 linear_f16(xh, w.qkv_w, T, 3 * C, C,
-                           EpiLnF16<false, Src>{s->big, w.qkv_d, w.qkv_c, Src{stats}, 3 * C, T, 3 * C},
+                           EpiLnF16<false, Src>{s->big, w.qkv_d, w.qkv_corr, Src{stats}, 3 * C, T, 3 * C},
                            stream);
             });
             break;
@@ -520,7 +545,7 @@ void block_op(bf_cuda_swin *s, int st, int b, int op, hipStream_t stream) {
             with_groups(C, [&](auto g) {
                 using Src = LnRows<decltype(g)::value>;
                 linear_f16(xh, w.fc1_w, T, 4 * C, C,
-                           EpiLnF16<true, Src>{s->big, w.fc1_d, w.fc1_c, Src{stats}, 4 * C, T, 4 * C},
+                           EpiLnF16<true, Src>{s->big, w.fc1_d, w.fc1_corr, Src{stats}, 4 * C, T, 4 * C},
                            stream);
             });
             break;
@@ -605,7 +630,7 @@ void merge_folded(bf_cuda_swin *s, int st, hipStream_t stream) {
     constexpr bool kWhole = C % kStatCols != 0;  // one group per token
     using Src = LnMerge<kWhole ? 1 : C / kStatCols, kWhole ? C : kStatCols>;
     EpiStatsRows<true, false, Src> epi{s->x,          s->xh[nx],     s->stats[nx],
-                                       s->merge_d[st], s->merge_c[st], Src{stage_stats(s, st), H, W},
+                                       s->merge_d[st], s->merge_corr[st], Src{stage_stats(s, st), H, W},
                                        T2,            2 * C};
     merge_gemm<C, T, LW>(stage_xh(s, st), B, H, W, s->merge_w[st], 2 * C, epi, stream);
 }

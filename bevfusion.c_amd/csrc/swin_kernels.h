@@ -55,7 +55,8 @@ __global__ __launch_bounds__(256) void out_ln_kernel(const float *x, const float
 #pragma unroll
         for (int k = 0; k < G; ++k)
             p[k] = row < rows ? stats[(size_t)row * G + k] : make_float2(0.0f, 0.0f);
-        norm[tid] = ln_combine<G>(p);
+        const RowLn<G> l = ln_combine<G>(p);
+        norm[tid] = make_float2(l.mean, l.r);
     }
     const float4 gv = *reinterpret_cast<const float4 *>(g + c0 + q);
     const float4 bv = *reinterpret_cast<const float4 *>(b + c0 + q);

@@ -2,8 +2,9 @@
 //   [x += proj(a) + b_proj]                      (PROJ: a = attention output)
 //   x += fc2(GELU(fc1(LN2(x)) + b1)) + b2
 //   xn = LN1'(x)                                  (optional: next block's LN1)
-//   or xh = fp16(x), stats = (mean, M2) of x      (optional: for a consumer
-//                                                  that folds its LayerNorm)
+//   or xh = fp16(x - mean), stats = (mean, M2) of x (optional: for a
+//                                                  consumer that folds its
+//                                                  LayerNorm)
 // in one launch: x is read and written once, the 4C-wide hidden layer never
 // leaves the chip.
 //
@@ -115,9 +116,11 @@ __global__ __launch_bounds__(Cfg::kThreads) __attribute__((amdgpu_waves_per_eu(4
     const float *__restrict__ bproj, const float *__restrict__ ln_g, const float *__restrict__ ln_b,
     const bf16 *__restrict__ wpk, const float *__restrict__ b1, const float *__restrict__ b2,
     const float *__restrict__ next_g, const float *__restrict__ next_b, bf16 *xn, int T,
-    bf16 *__restrict__ xh, float2 *__restrict__ stats) {
-    // attn and xn may be the same buffer: each row is read (prologue) by the
-    // lane group that later writes it (epilogue), so neither is __restrict__.
+    bf16 *xh, float2 *__restrict__ stats) {
+    // attn may be the same buffer as xn (the next block's LN1 overwrites the
+    // attention rows) or as xh (the stage's last block writes the fp16 copy
+    // over them): each row is read (prologue) by the lane group that later
+    // writes it (epilogue), so none of the three is __restrict__.
     constexpr int C = Cfg::C, TF = Cfg::TF, KS = Cfg::kKs, CF = Cfg::kCf;
     constexpr int NB = Cfg::kBufs, P = Cfg::kPerWave;
     // The chunk buffers are the kernel's only LDS object: a second __shared__
@@ -287,8 +290,9 @@ __global__ __launch_bounds__(Cfg::kThreads) __attribute__((amdgpu_waves_per_eu(4
 
     // Residual, then one of (uniform for the whole launch):
     //   xn = LN1'(x) of the next block, with x stored fp32;
-    //   xh = fp16 words of x and stats[t] = (mean, M2) over the row, for a
-    //   consumer that folds the next LayerNorm (the patch merge), x not stored;
+    //   xh = fp16 words of x - mean and stats[t] = (mean, M2) over the row, for
+    //   a consumer that folds the next LayerNorm (the patch merge), x not
+    //   stored;
     //   x stored fp32 only.
     // acc[j][i][e] is channel 16j + 4g + e.
 #pragma unroll
@@ -322,13 +326,14 @@ __global__ __launch_bounds__(Cfg::kThreads) __attribute__((amdgpu_waves_per_eu(4
         if (xh) {
             if (!ok) continue;
             if (g == 0) stats[t] = make_float2(mean, qs);
+            // The copy is centred on the token mean (ln_fold.h).
 #pragma unroll
             for (int j = 0; j < CF; ++j) {
                 bf16x4 o;
-                o[0] = to_half(xr[i][j].x);
-                o[1] = to_half(xr[i][j].y);
-                o[2] = to_half(xr[i][j].z);
-                o[3] = to_half(xr[i][j].w);
+                o[0] = to_half(xr[i][j].x - mean);
+                o[1] = to_half(xr[i][j].y - mean);
+                o[2] = to_half(xr[i][j].z - mean);
+                o[3] = to_half(xr[i][j].w - mean);
                 *reinterpret_cast<bf16x4 *>(xh + (size_t)t * C + 16 * j + 4 * g) = o;
             }
             continue;

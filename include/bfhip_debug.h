@@ -31,7 +31,10 @@
  *       heads (larger counts return 0 with a message); the stream must belong
  *       to the current device.  Every call on a device shares that device's
  *       array, so calls that overlap in time on one device (other streams or
- *       host threads) race; calls queued on one stream do not.
+ *       host threads) race; calls queued on one stream do not.  The array's
+ *       device address is resolved on the first call on each device and kept:
+ *       like every other object of the library, it does not survive
+ *       hipDeviceReset.
  *
  *   bfhip_debug_camera_gather
  *       Runs the A-operand gather of camera-neck conv `layer` (the layer

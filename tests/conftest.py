@@ -35,10 +35,10 @@ def tmp_models(tmp_path_factory):
     base = tmp_path_factory.mktemp("models")
     cache = {}
 
-    def get(mode="fan_in", seed=1, gain=1.0):
-        key = (mode, seed, gain)
+    def get(mode="fan_in", seed=1, gain=1.0, offset=0.0):
+        key = (mode, seed, gain, offset)
         if key not in cache:
-            cache[key] = bfw.write_camera_branch(base / f"cam_{mode}_{seed}_{gain}.bfw",
-                                                 seed=seed, mode=mode, gain=gain)
+            cache[key] = bfw.write_camera_branch(base / f"cam_{mode}_{seed}_{gain}_{offset}.bfw",
+                                                 seed=seed, mode=mode, gain=gain, offset=offset)
         return cache[key]
     return get

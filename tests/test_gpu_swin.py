@@ -111,3 +111,30 @@ def test_swin_unaligned_images_match_aligned(device, tmp_models):
     for oa, ob in zip(a, b):
         assert torch.equal(oa, ob), "unaligned images change the result"
     ctx.close()
+
+
+@pytest.mark.parametrize("offset", [10.0, 30.0])
+def test_swin_offset_rows_match_oracle(device, tmp_models, offset):
+    """Residual rows with a large common offset.  The attention-proj and fc2
+    biases of every block carry +offset, so the rows entering the LayerNorms
+    of stages 1-3 have |mean| up to 50x (offset 10) and 150x (offset 30)
+    their spread (median over rows, measured with the float64 restatement and
+    asserted here).  Those LayerNorms are folded into the linears that
+    consume them: the fp16 copy of the residual stream carries the offset
+    into the matrix product, the reason this case is tested on its own."""
+    import torchref
+    from bfhip import bfw
+    path = tmp_models("fan_in", 1, 1.0, offset)
+    images = bfw.synthetic_images(7, 1, 64, 96)
+    ratios = []
+    torchref.swin_backbone(dict(bfw.camera_branch_tensors(1, "fan_in", 1.0, offset)), images,
+                           ratios)
+    assert max(ratios) >= 4.5 * offset and sorted(ratios)[len(ratios) // 2] >= 2 * offset, ratios
+    got = _run_swin(path, images, device)
+    ref = _oracle_swin(path, images)
+    for i, (g, r) in enumerate(zip(got, ref)):
+        assert np.isfinite(g).all()
+        rel = float(np.linalg.norm(g - r) / np.linalg.norm(r))
+        mx = float(np.abs(g - r).max() / np.sqrt(np.mean(r * r)))
+        print(f"offset {offset} output{i}: rel-L2 {rel:.3e}, max-abs {mx:.3e} x RMS", flush=True)
+        assert_close(g, r, f"swin offset {offset} output{i}")

@@ -63,3 +63,35 @@ def test_noalloc_window_attention_rejects_too_many_heads(device):
     with pytest.raises(bfhip.BfHipError, match="at most 32 heads"):
         bfhip.window_attention(*args, 1, 7, 7, 33, 0, noalloc=True)
     torch.cuda.synchronize()
+
+
+def test_noalloc_window_attention_under_graph_capture(device):
+    """Two no-allocation calls captured in one HIP graph (torch.cuda.graph),
+    the second on a smaller problem; every replay, with eager work and
+    synchronisation between replays, must equal the allocating probe bit for
+    bit.  The captured kernels write the score terms into the static array at
+    replay time, so nothing is allocated inside or after the capture."""
+    import bfhip
+    import torch
+    shapes = CASES[0]
+    inputs = [_inputs(31 + i, s, device) for i, s in enumerate(shapes)]
+    want = [bfhip.window_attention(*args, *s) for s, args in zip(shapes, inputs)]
+    outs = [torch.zeros_like(w) for w in want]
+    # One eager call first: resolves the device's array before the capture.
+    bfhip.window_attention(*inputs[1], *shapes[1], out=outs[1], noalloc=True)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for s, args, o in zip(shapes, inputs, outs):
+            bfhip.window_attention(*args, *s, out=o, noalloc=True)
+    for rep in range(4):
+        print(f"[case] graph replay {rep}", flush=True)
+        for o in outs:
+            o.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        for s, o, w in zip(shapes, outs, want):
+            assert torch.equal(o, w), f"replay {rep} {s}: differs from the allocating probe"
+        # eager work between replays (the same entry point on another problem)
+        bfhip.window_attention(*inputs[0], *shapes[0], noalloc=True)
+        torch.cuda.synchronize()

@@ -102,10 +102,21 @@ def _bn(x, p, prefix, eps=1e-5):
                         eps=eps)
 
 
-def swin_backbone(p, images):
+def _offset_ratio(x, sink):
+    """Median over rows of |row mean| / row std of a LayerNorm input."""
+    if sink is not None:
+        mu = x.mean(-1)
+        sd = x.std(-1, unbiased=False)
+        sink.append(float((mu.abs() / sd).median()))
+
+
+def swin_backbone(p, images, ln_offsets=None):
     """Swin-T (mmdet SwinTransformer, out_indices 1..3) in float64.
 
-    ``p`` maps tensor names to arrays (the synthetic checkpoint)."""
+    ``p`` maps tensor names to arrays (the synthetic checkpoint).  With
+    ``ln_offsets`` a list, the median |mean| / std of the rows entering each
+    LayerNorm of stages 1-3 (norm1, norm2, the stage-output norm) is appended
+    to it."""
     pre = "image_backbone."
     x = F.conv2d(_t(images), _t(p[pre + "patch_embed.projection.weight"]),
                  _t(p[pre + "patch_embed.projection.bias"]), stride=4)
@@ -118,6 +129,7 @@ def swin_backbone(p, images):
                                               (2, 2, 6, 2))):
         for k in range(depth):
             q = f"{pre}stages.{s}.blocks.{k}."
+            _offset_ratio(x, ln_offsets if s > 0 else None)
             y = F.layer_norm(x, (c,), _t(p[q + "norm1.weight"]), _t(p[q + "norm1.bias"]), 1e-5)
             y = torch.from_numpy(shifted_window_msa(
                 y.numpy(), p[q + "attn.w_msa.qkv.weight"], p[q + "attn.w_msa.qkv.bias"],
@@ -125,11 +137,13 @@ def swin_backbone(p, images):
                 p[q + "attn.w_msa.relative_position_index"], p[q + "attn.w_msa.proj.weight"],
                 p[q + "attn.w_msa.proj.bias"], heads, 7, 3 if k % 2 else 0))
             x = x + y
+            _offset_ratio(x, ln_offsets if s > 0 else None)
             y = F.layer_norm(x, (c,), _t(p[q + "norm2.weight"]), _t(p[q + "norm2.bias"]), 1e-5)
             y = F.gelu(F.linear(y, _t(p[q + "ffn.layers.0.0.weight"]),
                                 _t(p[q + "ffn.layers.0.0.bias"])))
             x = x + F.linear(y, _t(p[q + "ffn.layers.1.weight"]), _t(p[q + "ffn.layers.1.bias"]))
         if s > 0:
+            _offset_ratio(x, ln_offsets)
             o = F.layer_norm(x, (c,), _t(p[f"{pre}norm{s}.weight"]), _t(p[f"{pre}norm{s}.bias"]),
                              1e-5)
             outs.append(o.permute(0, 3, 1, 2).contiguous().numpy())
