@@ -179,6 +179,27 @@ def swin_op_cost(stage, op, b=6):
     raise ValueError(op)
 
 
+def patch_embed_cost(b=6):
+    """4x4/s4 conv 3 -> 96 + patch norm + LN1: fp32 images read, x (fp32) and
+    xn (fp16) written."""
+    t = b * 64 * 176
+    return 2.0 * t * 96 * 48, b * 3 * 256 * 704 * 4 + t * 96 * (4 + 2) + 96 * 48 * 2
+
+
+def out_norm_cost(stage, b=6):
+    """Stage-output LayerNorm: x (fp32) and its (mean, M2) per 64 channels read,
+    the NCHW fp32 output written."""
+    h, w, c = SWIN_STAGES[stage][:3]
+    t = b * h * w
+    return 8.0 * t * c, t * c * 4 * 2 + t * (c // 64) * 8
+
+
+def pack_cost(b=6):
+    """Three Swin levels, NCHW fp32 read, channels-last fp16 written."""
+    el = b * (192 * 32 * 88 + 384 * 16 * 44 + 768 * 8 * 22)
+    return 0.0, el * (4 + 2)
+
+
 def neck_layer_cost(layer):
     if layer in LATERALS:  # executed work of the two GEMMs (fp32 upper product written and read)
         m, cl, mu, cu = LATERALS[layer]
@@ -189,14 +210,18 @@ def neck_layer_cost(layer):
 
 
 def neck_io(dev):
-    """Caller buffers the IO layers read or write: dense depth, logits,
-    context and the downsample output."""
+    """Caller buffers the IO ops read or write: dense depth, logits, context,
+    the downsample output, images (patch embedding) and the three Swin
+    levels (output norms, level pack)."""
     import torch
     g = torch.Generator(device="cpu").manual_seed(0)
     return {"depth": torch.rand((6, 1, 256, 704), generator=g).to(dev),
             "logits": torch.empty((6, 118, 32, 88), device=dev),
             "ctx": torch.empty((6, 80, 32, 88), device=dev),
-            "down": torch.empty((1, 80, DOWN_IN_HW // 2, DOWN_IN_HW // 2), device=dev)}
+            "down": torch.empty((1, 80, DOWN_IN_HW // 2, DOWN_IN_HW // 2), device=dev),
+            "images": torch.rand((6, 3, 256, 704), generator=g).to(dev),
+            "levels": [torch.rand((6, c, h, w), generator=g).to(dev)
+                       for c, h, w in ((192, 32, 88), (384, 16, 44), (768, 8, 22))]}
 
 
 def roofline_entry(name, avg_s, per_frame, flops, nbytes):
@@ -250,6 +275,14 @@ def op_table(swin, neck, stream, io):
         if st < 3:
             table[f"swin.s{st}.merge"] = (lambda st=st: swin.profile_op(st, 0, "merge", stream),
                                           1, swin_op_cost(st, "merge"))
+    # The Swin launches outside the blocks and the neck's level pack.
+    table["swin.patch_embed"] = (lambda: swin.profile_io("patch_embed", 0, images=io["images"],
+                                                         stream=stream), 1, patch_embed_cost())
+    for st in (1, 2, 3):
+        table[f"swin.s{st}.out_norm"] = (
+            lambda st=st: swin.profile_io("out_norm", st, out=io["levels"][st - 1], stream=stream),
+            1, out_norm_cost(st))
+    table["neck.pack"] = (lambda: neck.profile_pack(*io["levels"], stream=stream), 1, pack_cost())
     for layer, (name, *_rest) in NECK_LAYERS.items():
         if layer == 4:
             fn = lambda: neck.profile_layer_io(4, inp=io["depth"], stream=stream)

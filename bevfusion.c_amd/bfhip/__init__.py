@@ -127,6 +127,8 @@ SIGNATURES = {
                                          C.c_char_p, _sz]),
     "bf_cuda_camera_downsample_forward": (_i, [_vp, _vp, _vp, _vp, C.c_char_p, _sz]),
     "bfhip_swin_profile_op": (_i, [_vp, _i, _i, _i, _vp, C.c_char_p, _sz]),
+    "bfhip_swin_profile_io": (_i, [_vp, _i, _i, _vp, _vp, _vp, C.c_char_p, _sz]),
+    "bfhip_camera_profile_pack": (_i, [_vp, _vp, _vp, _vp, _vp, C.c_char_p, _sz]),
     "bfhip_camera_profile_layer": (_i, [_vp, _i, _vp, C.c_char_p, _sz]),
     "bfhip_camera_profile_layer_io": (_i, [_vp, _i, _vp, _vp, _vp, _vp, C.c_char_p, _sz]),
     "bfhip_calibrate": (_i, [_i, _i, _i, _vp, _vp, _sz, _vp, C.c_char_p, _sz]),
@@ -517,6 +519,18 @@ class Swin:
                                               _stream(stream), err, 512), err,
                "bfhip_swin_profile_op")
 
+    def profile_io(self, op, stage=0, images=None, out=None, stream=None):
+        """Patch embedding ("patch_embed", reads images) or the output norm of
+        stage 1..3 ("out_norm", writes out) on caller buffers
+        (bfhip_swin_profile_io)."""
+        err = _err()
+        code = {"patch_embed": 10, "out_norm": 11}[op]
+        _check(self.lib.bfhip_swin_profile_io(self.handle, stage, code,
+                                              _vp(images.data_ptr() if images is not None else None),
+                                              _vp(out.data_ptr() if out is not None else None),
+                                              _stream(stream), err, 512), err,
+               "bfhip_swin_profile_io")
+
     def close(self):
         if self.handle:
             self.lib.bf_cuda_swin_destroy(self.handle)
@@ -604,6 +618,14 @@ class CameraNeck:
         _check(self.lib.bfhip_camera_profile_layer_io(self.handle, layer, _ptr(inp), _ptr(out0),
                                                       _ptr(out1), _stream(stream), err, 512),
                err, "bfhip_camera_profile_layer_io")
+
+    def profile_pack(self, s0, s1, s2, stream=None):
+        """Enqueue the pack of the three Swin levels to channels-last fp16
+        (bfhip_camera_profile_pack)."""
+        err = _err()
+        _check(self.lib.bfhip_camera_profile_pack(self.handle, _ptr(s0), _ptr(s1), _ptr(s2),
+                                                  _stream(stream), err, 512),
+               err, "bfhip_camera_profile_pack")
 
     def close(self):
         if self.handle:

@@ -206,14 +206,20 @@ void lateral0(bf_cuda_camera_neck *n, hipStream_t s) {
             n->t0, s);
 }
 
-// FPN from NCHW fp32 Swin levels; FPN levels land channels-last in f0/f1 and,
-// when requested, also NCHW fp32 in out0/out1.
-void fpn_impl(bf_cuda_camera_neck *n, const float *s0, const float *s1, const float *s2,
-              float *out0, float *out1, hipStream_t s) {
+// The three Swin levels to channels-last fp16 in one launch.
+void pack_levels(bf_cuda_camera_neck *n, const float *s0, const float *s1, const float *s2,
+                 hipStream_t s) {
     const int B = (int)n->batches;
     const int hw = (int)(n->h * n->w), hw1 = (int)(n->h1 * n->w1), hw2 = (int)(n->h2 * n->w2);
     pack_nhwc_many(PackJobs<3>{{{s0, n->p0, 192, hw}, {s1, n->p1, 384, hw1}, {s2, n->p2, 768, hw2}}}, B,
                    s, true);
+}
+
+// FPN from NCHW fp32 Swin levels; FPN levels land channels-last in f0/f1 and,
+// when requested, also NCHW fp32 in out0/out1.
+void fpn_impl(bf_cuda_camera_neck *n, const float *s0, const float *s1, const float *s2,
+              float *out0, float *out1, hipStream_t s) {
+    pack_levels(n, s0, s1, s2, s);
     lateral1(n, s);
     fpn_conv(kFpn1, n->L[kFpn1], n->t1, n->f1, out1, s);
     lateral0(n, s);
@@ -469,6 +475,13 @@ extern "C" int bfhip_camera_profile_layer_io(bf_cuda_camera_neck *n, int layer, 
     else
         depth_layer(n, layer, input, out0, out1, s);
     return launch_ok(error, cap, "launch HIP camera layer profiling");
+}
+
+extern "C" int bfhip_camera_profile_pack(bf_cuda_camera_neck *n, const float *s0, const float *s1,
+                                         const float *s2, void *stream, char *error, size_t cap) {
+    if (!n || !s0 || !s1 || !s2) return fail(error, cap, "invalid HIP camera pack profiling call");
+    pack_levels(n, s0, s1, s2, reinterpret_cast<hipStream_t>(stream));
+    return launch_ok(error, cap, "launch HIP camera pack profiling");
 }
 
 // ---- Index probes (include/bfhip_debug.h) ----------------------------------

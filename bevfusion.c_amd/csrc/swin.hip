@@ -693,6 +693,21 @@ extern "C" int bfhip_swin_profile_op(bf_cuda_swin *s, int stage, int block, int 
     return launch_ok(error, cap, "launch HIP Swin profiling op");
 }
 
+extern "C" int bfhip_swin_profile_io(bf_cuda_swin *s, int stage, int op, const float *images,
+                                     float *out, void *stream, char *error, size_t cap) {
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (s && op == BFHIP_SWIN_PATCH_EMBED && stage == 0 && images) {
+        patch_embed(s, images, st);
+    } else if (s && op == BFHIP_SWIN_OUT_NORM && stage >= 1 && stage <= 3 && out) {
+        const int T = (int)s->batches * s->h[stage] * s->w[stage];
+        launch_out_ln(kC[stage], s->x, stage_stats(s, stage), out, s->out_s[stage - 1],
+                      s->out_b[stage - 1], T, s->h[stage] * s->w[stage], st);
+    } else {
+        return fail(error, cap, "invalid HIP Swin profiling io call");
+    }
+    return launch_ok(error, cap, "launch HIP Swin profiling io op");
+}
+
 extern "C" int bfhip_debug_window_map(int batches, int height, int width, int shift, int *token,
                                       int *label, void *stream, char *error, size_t cap) {
     if (!token || !label || batches <= 0 || height <= 0 || width <= 0 || shift < 0 || shift >= 7)

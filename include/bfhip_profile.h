@@ -48,6 +48,21 @@ enum {
 int bfhip_swin_profile_op(bf_cuda_swin *swin, int stage, int block, int op,
                           void *stream, char *error, size_t error_cap);
 
+/* The Swin launches outside the blocks, on caller device buffers, at the
+ * forward's shape and kernel instance:
+ *   BFHIP_SWIN_PATCH_EMBED  the patch embedding (4x4/s4 conv + patch norm +
+ *                           block 0's LN1): reads `images` [B,3,H,W];
+ *                           `stage` must be 0;
+ *   BFHIP_SWIN_OUT_NORM     the output LayerNorm of stage `stage` (1..3):
+ *                           writes `out`, the stage's NCHW output. */
+enum {
+    BFHIP_SWIN_PATCH_EMBED = 10,
+    BFHIP_SWIN_OUT_NORM = 11
+};
+
+int bfhip_swin_profile_io(bf_cuda_swin *swin, int stage, int op, const float *images, float *out,
+                          void *stream, char *error, size_t error_cap);
+
 /* Camera-neck convolution `layer` in the context's layer table: 0 lateral 1,
  * 1 fpn 1, 2 lateral 0, 3 fpn 0, 5 dtransform.6, 6 depthnet.0, 7 depthnet.3,
  * 9-11 downsample.  Layers 4 (dtransform.3, reads the caller's dense depth)
@@ -70,6 +85,12 @@ int bfhip_camera_profile_layer(bf_cuda_camera_neck *neck, int layer, void *strea
 int bfhip_camera_profile_layer_io(bf_cuda_camera_neck *neck, int layer, const float *input,
                                   float *out0, float *out1, void *stream, char *error,
                                   size_t error_cap);
+
+/* The neck's pack of the three Swin levels (NCHW fp32 [B,192,h,w],
+ * [B,384,h1,w1], [B,768,h2,w2] -> channels-last fp16), one launch, as the
+ * FPN forward runs it. */
+int bfhip_camera_profile_pack(bf_cuda_camera_neck *neck, const float *s0, const float *s1,
+                              const float *s2, void *stream, char *error, size_t error_cap);
 
 /* Calibration kernels (machine rates for the roofline discussion).  Each
  * enqueues one launch of `grid` workgroups on `stream`:

@@ -139,7 +139,8 @@ def test_gemm_config1_matches_oracle(device):
 
 
 @pytest.mark.parametrize("shape", [(1, 1, 1), (7, 5, 4), (300, 96, 96), (129, 130, 131),
-                                   (1000, 384, 1536), (64, 3072, 768), (513, 8, 33)])
+                                   (1000, 384, 1536), (64, 3072, 768), (513, 8, 33),
+                                   (200, 96, 145), (77, 31, 250), (33, 64, 288)])
 def test_gemm_shapes(device, shape):
     import bfhip
     m, k, n = shape
