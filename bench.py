@@ -68,6 +68,8 @@ def parse():
     p.add_argument("--no-downsample", action="store_true", help="skip the downsample leg")
     p.add_argument("--no-config1", action="store_true", help="skip the config-1 linear leg")
     p.add_argument("--no-calibrate", action="store_true", help="skip the machine calibration leg")
+    p.add_argument("--no-library", action="store_true",
+                   help="skip the library-GEMM comparison leg (hipBLASLt on the Swin shapes)")
     p.add_argument("--pmc-child", default="",
                    help=argparse.SUPPRESS)  # internal: the program rocprofv3 profiles
     p.add_argument("--no-lss", action="store_true", help="skip the LSS pooling leg")
@@ -694,16 +696,19 @@ def calibrate_leg(dev):
         # CU; 64 x 64 wave tiles with random or constant fp16 operands, and
         # 32 x 32 wave tiles (LDS-heavy) for the fragment-read bandwidth.
         mgrid, miters = 1024, 2000
-        for kind, fm, key in (("mfma_lds", 4, "mfma16_lds_random_tflops"),
-                              ("mfma_lds_flat", 4, "mfma16_lds_constant_tflops"),
-                              ("mfma_lds_narrow", 2, "mfma16_lds_random_32x32_tflops")):
+        for kind, fm, key, lds_key in (
+                ("mfma_lds", 4, "mfma16_lds_random_tflops", None),
+                ("mfma_lds_flat", 4, "mfma16_lds_constant_tflops", None),
+                ("mfma_lds_narrow", 2, "mfma16_lds_random_32x32_tflops", "lds_fragment_read"),
+                ("mfma_lds_narrow_flat", 2, "mfma16_lds_constant_32x32_tflops",
+                 "lds_fragment_read_constant")):
             t = timed(lambda kind=kind: bfhip.calibrate(kind, mgrid, miters, dst=sink, stream=stream), 5)
             waves = mgrid * 8 * miters
             out[key] = round(waves * 2 * fm * fm * 16384 / t / 1e12, 1)
-            if fm == 2:
+            if lds_key:
                 lds_f = waves * 2 * (2 * fm) * 1024 / t
-                out["lds_fragment_read_tb_s"] = round(lds_f / 1e12, 1)
-                out["lds_fragment_read_b_per_clk_per_cu_at_2_4ghz"] = round(lds_f / 256 / 2.4e9, 1)
+                out[lds_key + "_tb_s"] = round(lds_f / 1e12, 1)
+                out[lds_key + "_b_per_clk_per_cu_at_2_4ghz"] = round(lds_f / 256 / 2.4e9, 1)
         src = torch.zeros(256 << 20, device=dev)  # 1 GiB
         dst = torch.empty_like(src)
         t = timed(lambda: bfhip.calibrate("copy", 4096, src=src, dst=dst, stream=stream), 5)
@@ -716,6 +721,63 @@ def calibrate_leg(dev):
                    "GEMM cores do (random operands draw more power, hence a lower clock, than "
                    "constant ones); copy: 1 GiB float4, read + write bytes")
     return out
+
+
+def library_gemm_leg(dev, kernels, reps=50):
+    """The Swin-T linear shapes at 6x256x704 as plain library GEMMs, for
+    comparison with this library's ops: torch.nn.functional.linear in bf16
+    (X [M, K] and W [N, K] row-major, no bias, no epilogue), which ROCm's
+    PyTorch hands to hipBLASLt when that is the preferred BLAS library.  Each
+    shape runs `reps` times in one captured HIP graph, timed with HIP events
+    on the capture stream.  Beside each shape: this library's op of the same
+    stage and shape from the roofline leg (fused epilogue included: folded
+    LayerNorm, bias, GELU, residual add and row statistics), where the
+    forward launches it as a separate op."""
+    import torch
+    import torch.nn.functional as F
+    ours = {e["kernel"]: e["avg_us"] for e in kernels}
+    try:
+        torch.backends.cuda.preferred_blas_library("hipblaslt")
+    except (RuntimeError, AttributeError):
+        pass
+    # torch names the Lt backend after CUDA's; on ROCm it is hipBLASLt.
+    backend = str(torch.backends.cuda.preferred_blas_library()).split(".")[-1]
+    library = {"Cublaslt": "hipBLASLt", "Cublas": "rocBLAS", "Ck": "composable_kernel"}.get(
+        backend, backend)
+    stream = torch.cuda.Stream()
+    ev = lambda: torch.cuda.Event(enable_timing=True)
+    rows = []
+    with torch.cuda.stream(stream):
+        for st, (h, w, c, _heads, _depth) in enumerate(SWIN_STAGES):
+            m = 6 * h * w
+            for op, n, k in (("qkv", 3 * c, c), ("proj", c, c), ("fc1", 4 * c, c),
+                             ("fc2", c, 4 * c)):
+                gen = torch.Generator(device=dev).manual_seed(1000 * st + n + k)
+                x = torch.randn(m, k, device=dev, dtype=torch.bfloat16, generator=gen)
+                wt = (0.02 * torch.randn(n, k, device=dev, generator=gen)).to(torch.bfloat16)
+                y = F.linear(x, wt)
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g, stream=stream):
+                    for _ in range(reps):
+                        y = F.linear(x, wt)
+                g.replay()
+                start, stop = ev(), ev()
+                start.record(stream)
+                for _ in range(3):
+                    g.replay()
+                stop.record(stream)
+                stop.synchronize()
+                us = start.elapsed_time(stop) * 1e3 / (3 * reps)
+                name = f"swin.s{st}.{op}"
+                row = {"op": name, "m": m, "n": n, "k": k, "library_us": round(us, 2),
+                       "library_tflops": round(2.0 * m * n * k / us / 1e6, 1)}
+                if name in ours:
+                    row["ours_us"] = ours[name]
+                rows.append(row)
+                del g, x, wt, y
+    return {"library": library, "dtype": "bf16", "reps_per_graph": reps, "rows": rows,
+            "note": "library: torch.nn.functional.linear, no epilogue; ours: the op's own "
+                    "kernel from the roofline leg, with its fused epilogue"}
 
 
 LSS_OP = "lss_forward"
@@ -1432,6 +1494,8 @@ def main():
         result["config1"] = config1_leg(dev, 50, not args.no_cpu)
     if not args.no_calibrate:
         result["calibration"] = calibrate_leg(dev)
+    if not args.no_library:
+        result["library_gemm"] = library_gemm_leg(dev, kernels)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(model_path, args.cpu_cameras)
     if not args.no_lss:

@@ -322,7 +322,7 @@ def gemm_f32(x, w, b=None, relu=False, out=None, stream=None):
 
 
 CALIB_KINDS = ("empty", "mfma16", "mfma32", "lds", "copy", "mfma_lds", "mfma_lds_flat",
-               "mfma_lds_narrow")
+               "mfma_lds_narrow", "mfma_lds_narrow_flat")
 
 
 def calibrate(kind, grid, iters=0, src=None, dst=None, stream=None):

@@ -192,7 +192,8 @@ extern "C" int bfhip_calibrate(int kind, int grid, int iters, const void *src, v
         }
         case BFHIP_CALIB_MFMA_LDS:
         case BFHIP_CALIB_MFMA_LDS_FLAT:
-        case BFHIP_CALIB_MFMA_LDS_NARROW: {
+        case BFHIP_CALIB_MFMA_LDS_NARROW:
+        case BFHIP_CALIB_MFMA_LDS_NARROW_FLAT: {
             const size_t need = (size_t)grid * 512 * sizeof(float);
             const int flag = sink && bytes >= need ? 1 : 0;
             if (kind == BFHIP_CALIB_MFMA_LDS)
@@ -201,8 +202,11 @@ extern "C" int bfhip_calibrate(int kind, int grid, int iters, const void *src, v
             else if (kind == BFHIP_CALIB_MFMA_LDS_FLAT)
                 hipLaunchKernelGGL((calib_lds_mfma_kernel<4, 4, 8, false>), dim3(grid), dim3(512), 0, s,
                                    iters, sink, flag);
-            else
+            else if (kind == BFHIP_CALIB_MFMA_LDS_NARROW)
                 hipLaunchKernelGGL((calib_lds_mfma_kernel<2, 2, 8, true>), dim3(grid), dim3(512), 0, s,
+                                   iters, sink, flag);
+            else
+                hipLaunchKernelGGL((calib_lds_mfma_kernel<2, 2, 8, false>), dim3(grid), dim3(512), 0, s,
                                    iters, sink, flag);
             break;
         }

@@ -257,11 +257,13 @@ __global__ __launch_bounds__(Cfg::kThreads) __attribute__((amdgpu_waves_per_eu(4
         issue(q + NB - 1);
         const bf16 *wb = sw[q % NB] + lane * 8;
 
+        // The fc1 accumulators start at the bias (one VALU add per hidden
+        // element saved; the GELU below is VALU-bound).
         f32x4 h[2][TF];
 #pragma unroll
         for (int f = 0; f < 2; ++f)
 #pragma unroll
-            for (int i = 0; i < TF; ++i) h[f][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int i = 0; i < TF; ++i) h[f][i] = f32x4{bq[f].x, bq[f].y, bq[f].z, bq[f].w};
 #pragma unroll
         for (int k = 0; k < KS; ++k)
 #pragma unroll
@@ -275,11 +277,7 @@ __global__ __launch_bounds__(Cfg::kThreads) __attribute__((amdgpu_waves_per_eu(4
 #pragma unroll
         for (int i = 0; i < TF; ++i)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float4 b = bq[e >> 2];
-                const float bias = (e & 3) == 0 ? b.x : (e & 3) == 1 ? b.y : (e & 3) == 2 ? b.z : b.w;
-                hb[i][e] = to_half(gelu(h[e >> 2][i][e & 3] + bias));
-            }
+            for (int e = 0; e < 8; ++e) hb[i][e] = to_half(gelu(h[e >> 2][i][e & 3]));
 #pragma unroll
         for (int j = 0; j < CF; ++j) {
             const bf16x8 a = *reinterpret_cast<const bf16x8 *>(wb + (2 * KS + j) * 512);

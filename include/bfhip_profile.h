@@ -107,7 +107,8 @@ int bfhip_camera_profile_pack(bf_cuda_camera_neck *neck, const float *s0, const 
  *                    random fp16 values in [-1, 1);
  *   MFMA_LDS_FLAT    the same with constant small-integer operands;
  *   MFMA_LDS_NARROW  the same as MFMA_LDS on 32 x 32 tiles: per iteration
- *                    4 KiB of LDS reads and 8 MFMAs per wave (LDS-heavy).
+ *                    4 KiB of LDS reads and 8 MFMAs per wave (LDS-heavy);
+ *   MFMA_LDS_NARROW_FLAT  MFMA_LDS_NARROW with constant operands.
  * For the compute kinds, dst may receive one float per thread when `bytes`
  * covers grid * threads floats (it keeps the work observable); otherwise
  * nothing is stored. */
@@ -119,7 +120,8 @@ enum {
     BFHIP_CALIB_COPY = 4,
     BFHIP_CALIB_MFMA_LDS = 5,
     BFHIP_CALIB_MFMA_LDS_FLAT = 6,
-    BFHIP_CALIB_MFMA_LDS_NARROW = 7
+    BFHIP_CALIB_MFMA_LDS_NARROW = 7,
+    BFHIP_CALIB_MFMA_LDS_NARROW_FLAT = 8
 };
 
 int bfhip_calibrate(int kind, int grid, int iters, const void *src, void *dst, size_t bytes,
