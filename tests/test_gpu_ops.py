@@ -176,3 +176,46 @@ def test_repeat_is_bit_exact(device):
     a = bfhip.gemm_f32(x, w).cpu().numpy()
     b = bfhip.gemm_f32(x, w).cpu().numpy()
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+# (rows, in, out, relu, bias, inject Inf/NaN): shapes the short-reduction
+# panel kernel takes (K <= 128, K % 4 == 0, 144 < N <= 288, N % 4 == 0):
+# ragged row panels, N not a multiple of 16, K not a multiple of 8 or 32,
+# one to four 32-deep k-steps, ReLU, no bias, and Inf/NaN operands.
+PANEL_CASES = [(1001, 100, 148, True, True, False), (64, 4, 160, False, False, False),
+               (5, 128, 200, False, True, False), (130, 32, 288, True, True, True),
+               (11264, 96, 288, False, True, False), (65, 60, 252, False, True, False)]
+
+
+@pytest.mark.parametrize("case", PANEL_CASES)
+def test_gemm_panel_equals_tiled_core(device, case):
+    """The panel kernel (aligned operands) against the tiled core, reached by
+    handing the library an output that is not 16-byte aligned: same bf16
+    operand rounding, same 32-deep k order and bias after the accumulation,
+    so the two must agree bit for bit; and both within 1e-5 of the float64
+    sum over bf16-rounded operands."""
+    import bfhip
+    import torch
+    m, k, n, relu, with_bias, special = case
+    print(f"[case] panel gemm {m}x{k}->{n} relu={relu} bias={with_bias} special={special}",
+          flush=True)
+    rng = np.random.default_rng(m + 3 * k + 7 * n)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    w = (rng.standard_normal((n, k)) / np.sqrt(k)).astype(np.float32)
+    b = rng.standard_normal(n).astype(np.float32) if with_bias else None
+    if special:
+        x[0, 0] = np.inf
+        x[-1, -1] = np.nan
+    xt, wt = _t(x, device), _t(w, device)
+    bt = _t(b, device) if with_bias else None
+    panel = bfhip.gemm_f32(xt, wt, bt, relu=relu)
+    buf = torch.empty(m * n + 1, device=device)
+    tiled_out = buf[1:].view(m, n)
+    bfhip.gemm_f32(xt, wt, bt, relu=relu, out=tiled_out)
+    torch.cuda.synchronize()
+    a, t = panel.cpu().numpy(), tiled_out.cpu().numpy()
+    assert np.array_equal(a.view(np.uint32), t.view(np.uint32)), "panel and tiled core differ"
+    want = convref.gemm_abi(x, w, b, relu, round_inputs=bf16_round)
+    if special:
+        assert np.array_equal(np.isnan(a), np.isnan(want)) and np.array_equal(np.isinf(a), np.isinf(want))
+    _tight(a, want, f"panel gemm {case}")
