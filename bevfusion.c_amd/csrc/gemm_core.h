@@ -296,6 +296,24 @@ __device__ __forceinline__ void store_tile(f32x4 (&acc)[T::kFragM][T::kFragN], c
     }
 }
 
+// Barriers inside a kFullRow epilogue's tile() (E::kTileBarriers, default 0).
+template <class E, class = void>
+struct EpiTileBarriers { static constexpr int value = 0; };
+template <class E>
+struct EpiTileBarriers<E, std::void_t<decltype(E::kTileBarriers)>> {
+    static constexpr int value = E::kTileBarriers;
+};
+
+// Barriers store_tile executes, tile() included (the spec kernel's loader
+// waves pass as many).
+template <class Epi>
+constexpr int store_tile_barriers() {
+    if constexpr (!Epi::kRowVector) return 0;
+    else
+        return 1 + (EpiCorr<Epi>::value > 0 ? 1 : 0) +
+               (EpiFullRow<Epi>::value ? EpiTileBarriers<Epi>::value : 0);
+}
+
 template <class T, class Epi>
 constexpr size_t epilogue_bytes() {
     return Epi::kRowVector ? (size_t)T::BM * (T::BN + 4) * sizeof(float) +
@@ -642,8 +660,8 @@ __global__ __launch_bounds__(T::kThreads + ALoad::kWaves * kWave) void gemm_spec
             }
         }
         __syncthreads();  // the compute waves' end-of-loop barrier
-        if constexpr (EpiCorr<Epi>::value > 0) __syncthreads();  // store_tile's statistics barrier
-        if constexpr (Epi::kRowVector) __syncthreads();  // store_tile's staging barrier
+#pragma unroll
+        for (int k = 0; k < store_tile_barriers<Epi>(); ++k) __syncthreads();  // store_tile's
         return;
     }
 

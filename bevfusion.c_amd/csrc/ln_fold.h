@@ -300,6 +300,7 @@ struct EpiPatchNorms {
     bf16 *xn;
     const float *bias, *g0, *b0, *g1, *b1;
     int M;
+    static constexpr int kTileBarriers = 3;  // tile() synchronises three times
     template <class T>
     __device__ void tile(float *sC, int stride, int m0, int, int tid) const {
         static_assert(T::BN == C && T::kThreads == 2 * T::BM, "two threads per 96-channel row");
