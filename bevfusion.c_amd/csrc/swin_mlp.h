@@ -239,27 +239,19 @@ __global__ __launch_bounds__(Cfg::kThreads) __attribute__((amdgpu_waves_per_eu(4
         for (int i = 0; i < TF; ++i) acc[j][i] = f32x4{bj.x, bj.y, bj.z, bj.w};
     }
 
-    for (int q = 0; q < Cfg::kChunks; ++q) {
-        // NB - 2 chunk loads were issued after chunk q: wait for q only.
-        DmaWait<NB - 2>::template stages<P>(NB - 2);
-        // Every wave's part of chunk q landed, and buffer (q - 1) % NB is no
-        // longer read by anyone.
-        if (q == 0) __syncthreads(); else lds_barrier();
-        // fc1 bias of hidden rows 32q + 16f + 4g + r, from the chunk's bias
-        // block.  Read before the next chunk's DMA is issued: the compiler
-        // makes this read wait for every chunk DMA in flight, which here is
-        // only the chunk issued an iteration ago.
-        float4 bq[2];
+    // fc1 bias of hidden rows 32q + 16f + 4g + r, from chunk q's bias block.
+    // Read before the next chunk's DMA is issued: the compiler makes this read
+    // wait for every chunk DMA in flight.
+    auto bias_of = [&](int q, float4 (&bq)[2]) {
 #pragma unroll
         for (int f = 0; f < 2; ++f)
             bq[f] = __builtin_bit_cast(
                 float4, *reinterpret_cast<const bf16x8 *>(sw[q % NB] + (Cfg::kFrags * 1024 + g * 32 + f * 16) / 2));
-        issue(q + NB - 1);
+    };
+    // fc1 of chunk q; the accumulators start at the bias (one VALU add per
+    // hidden element saved).
+    auto fc1_of = [&](int q, const float4 (&bq)[2], f32x4 (&h)[2][TF]) {
         const bf16 *wb = sw[q % NB] + lane * 8;
-
-        // The fc1 accumulators start at the bias (one VALU add per hidden
-        // element saved; the GELU below is VALU-bound).
-        f32x4 h[2][TF];
 #pragma unroll
         for (int f = 0; f < 2; ++f)
 #pragma unroll
@@ -272,7 +264,10 @@ __global__ __launch_bounds__(Cfg::kThreads) __attribute__((amdgpu_waves_per_eu(4
 #pragma unroll
                 for (int i = 0; i < TF; ++i) h[f][i] = mfma16_f16(a, xf[i][k], h[f][i]);
             }
-        // GELU(H + b1) -> fc2 B operands (k-slot order).
+    };
+    // GELU(H + b1) of chunk q -> fc2 B operands (k-slot order), then fc2.
+    auto gelu_fc2 = [&](int q, const f32x4 (&h)[2][TF]) {
+        const bf16 *wb = sw[q % NB] + lane * 8;
         bf16x8 hb[TF];
 #pragma unroll
         for (int i = 0; i < TF; ++i)
@@ -283,6 +278,42 @@ __global__ __launch_bounds__(Cfg::kThreads) __attribute__((amdgpu_waves_per_eu(4
             const bf16x8 a = *reinterpret_cast<const bf16x8 *>(wb + (2 * KS + j) * 512);
 #pragma unroll
             for (int i = 0; i < TF; ++i) acc[j][i] = mfma16_f16(a, hb[i], acc[j][i]);
+        }
+    };
+
+    // Software pipeline over the chunks: iteration q runs fc1 of chunk q + 1
+    // before GELU and fc2 of chunk q, so the matrix cores have independent
+    // work while the GELU runs.  Chunk q + NB - 1 is issued at iteration q
+    // into the buffer of chunk q - 1, whose last reader (fc2, iteration
+    // q - 1) every wave has passed at the iteration's barrier; chunk q + 1,
+    // issued NB - 2 iterations earlier, must have landed by then.
+    static_assert(NB >= 3, "fc1 runs one chunk ahead");
+    DmaWait<NB - 2>::template stages<P>(NB - 2);  // chunk 0 (chunks 1 .. NB - 2 in flight)
+    __syncthreads();
+    f32x4 h[2][TF];
+    {
+        float4 bq[2];
+        bias_of(0, bq);
+        fc1_of(0, bq, h);
+    }
+    for (int q = 0; q < Cfg::kChunks; ++q) {
+        const bool more = q + 1 < Cfg::kChunks;
+        f32x4 hn[2][TF];
+        if (more) {
+            // Chunks 0 .. q + NB - 2 were issued: NB - 3 after chunk q + 1.
+            DmaWait<NB - 3>::template stages<P>(NB - 3);
+            lds_barrier();
+            float4 bq[2];
+            bias_of(q + 1, bq);
+            issue(q + NB - 1);
+            fc1_of(q + 1, bq, hn);
+        }
+        gelu_fc2(q, h);
+        if (more) {
+#pragma unroll
+            for (int f = 0; f < 2; ++f)
+#pragma unroll
+                for (int i = 0; i < TF; ++i) h[f][i] = hn[f][i];
         }
     }
 
