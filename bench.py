@@ -274,16 +274,23 @@ def op_table(swin, neck, stream, io):
             per_frame = 1 if (op == "ln1" and st in fused) else depth
             table[f"swin.s{st}.{op}"] = (lambda st=st, op=op: swin.profile_op(st, 0, op, stream),
                                          per_frame, swin_op_cost(st, op))
-        if st < 3:
+        if st == 0:
             table[f"swin.s{st}.merge"] = (lambda st=st: swin.profile_op(st, 0, "merge", stream),
                                           1, swin_op_cost(st, "merge"))
+        elif st < 3:
+            # The forward runs the merges after stages 1 and 2 in one launch
+            # with that stage's output LayerNorm.
+            mf, mb = swin_op_cost(st, "merge")
+            lf, lb = out_norm_cost(st)
+            table[f"swin.s{st}.merge_out_norm"] = (
+                lambda st=st: swin.profile_io("merge_out_norm", st, out=io["levels"][st - 1],
+                                              stream=stream), 1, (mf + lf, mb + lb))
     # The Swin launches outside the blocks and the neck's level pack.
     table["swin.patch_embed"] = (lambda: swin.profile_io("patch_embed", 0, images=io["images"],
                                                          stream=stream), 1, patch_embed_cost())
-    for st in (1, 2, 3):
-        table[f"swin.s{st}.out_norm"] = (
-            lambda st=st: swin.profile_io("out_norm", st, out=io["levels"][st - 1], stream=stream),
-            1, out_norm_cost(st))
+    table["swin.s3.out_norm"] = (
+        lambda: swin.profile_io("out_norm", 3, out=io["levels"][2], stream=stream), 1,
+        out_norm_cost(3))
     table["neck.pack"] = (lambda: neck.profile_pack(*io["levels"], stream=stream), 1, pack_cost())
     for layer, (name, *_rest) in NECK_LAYERS.items():
         if layer == 4:

@@ -520,11 +520,12 @@ class Swin:
                "bfhip_swin_profile_op")
 
     def profile_io(self, op, stage=0, images=None, out=None, stream=None):
-        """Patch embedding ("patch_embed", reads images) or the output norm of
-        stage 1..3 ("out_norm", writes out) on caller buffers
-        (bfhip_swin_profile_io)."""
+        """Patch embedding ("patch_embed", reads images), the output norm of
+        stage 1..3 alone ("out_norm", writes out), or the merge after stage
+        1..2 with that stage's output norm in one launch ("merge_out_norm",
+        writes out) on caller buffers (bfhip_swin_profile_io)."""
         err = _err()
-        code = {"patch_embed": 10, "out_norm": 11}[op]
+        code = {"patch_embed": 10, "out_norm": 11, "merge_out_norm": 12}[op]
         _check(self.lib.bfhip_swin_profile_io(self.handle, stage, code,
                                               _vp(images.data_ptr() if images is not None else None),
                                               _vp(out.data_ptr() if out is not None else None),

@@ -518,18 +518,39 @@ struct DmaWait {
     }
 };
 
+// LDS of one LDS-DMA / wave-specialised workgroup: stages, or the epilogue's
+// staging tile if larger.
+template <class T, class Epi>
+constexpr size_t dma_smem_bytes() {
+    constexpr size_t kAB = (size_t)T::kStages * (T::BM + T::BN) * T::BK * sizeof(bf16);
+    constexpr size_t kC = epilogue_bytes<T, Epi>();
+    return kAB > kC ? kAB : kC;
+}
+template <class T, class ALoad, class BLoad, class Epi>
+__device__ __forceinline__ void gemm_dma_block(ALoad &al, BLoad &bl, const Epi &epi, int M, int N,
+                                               int K, int tiles_n, int pid, unsigned char *smem);
+template <class T, class ALoad, class BLoad, class Epi>
+__device__ __forceinline__ void gemm_spec_block(ALoad &al, BLoad &bl, const Epi &epi, int M, int N,
+                                                int K, int tiles_n, int pid, unsigned char *smem);
+
 template <class T, class ALoad, class BLoad, class Epi>
 __global__ __launch_bounds__(T::kThreads) void gemm_dma_kernel(ALoad al, BLoad bl, Epi epi,
                                                                int M, int N, int K, int tiles_n) {
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[dma_smem_bytes<T, Epi>()];
+    gemm_dma_block<T>(al, bl, epi, M, N, K, tiles_n, xcd_swizzle((int)blockIdx.x, (int)gridDim.x), smem);
+}
+
+// Tile `pid` of the LDS-DMA core on the workgroup's `smem` (dma_smem_bytes);
+// gemm_dma_kernel is one such tile per workgroup, and a kernel that fuses
+// other work into the same launch can call it for part of its grid.
+template <class T, class ALoad, class BLoad, class Epi>
+__device__ __forceinline__ void gemm_dma_block(ALoad &al, BLoad &bl, const Epi &epi, int M, int N,
+                                               int K, int tiles_n, int pid, unsigned char *smem) {
     constexpr int S = T::kStages;
     constexpr int kA = T::BM * T::BK, kB = T::BN * T::BK;  // elements per stage
-    constexpr size_t kABBytes = (size_t)S * (kA + kB) * sizeof(bf16);
-    constexpr size_t kCBytes = epilogue_bytes<T, Epi>();
-    __shared__ __attribute__((aligned(1024))) unsigned char smem[kABBytes > kCBytes ? kABBytes : kCBytes];
     bf16 *sA = reinterpret_cast<bf16 *>(smem);
     bf16 *sB = sA + S * kA;
 
-    const int pid = xcd_swizzle((int)blockIdx.x, (int)gridDim.x);
     const int m0 = (pid / tiles_n) * T::BM, n0 = (pid % tiles_n) * T::BN;
     const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / T::WN, wn = wave % T::WN;
@@ -626,15 +647,20 @@ inline void launch_gemm_dma(const ALoad &al, const BLoad &bl, const Epi &epi, in
 template <class T, class ALoad, class BLoad, class Epi>
 __global__ __launch_bounds__(T::kThreads + ALoad::kWaves * kWave) void gemm_spec_kernel(
     ALoad al, BLoad bl, Epi epi, int M, int N, int K, int tiles_n) {
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[dma_smem_bytes<T, Epi>()];
+    gemm_spec_block<T>(al, bl, epi, M, N, K, tiles_n, xcd_swizzle((int)blockIdx.x, (int)gridDim.x), smem);
+}
+
+// Tile `pid` of the wave-specialised pipeline on the workgroup's `smem`
+// (dma_smem_bytes), as gemm_dma_block.
+template <class T, class ALoad, class BLoad, class Epi>
+__device__ __forceinline__ void gemm_spec_block(ALoad &al, BLoad &bl, const Epi &epi, int M, int N,
+                                                int K, int tiles_n, int pid, unsigned char *smem) {
     constexpr int S = T::kStages;
     constexpr int kA = T::BM * T::BK, kB = T::BN * T::BK;  // elements per stage
-    constexpr size_t kABBytes = (size_t)S * (kA + kB) * sizeof(bf16);
-    constexpr size_t kCBytes = epilogue_bytes<T, Epi>();
-    __shared__ __attribute__((aligned(1024))) unsigned char smem[kABBytes > kCBytes ? kABBytes : kCBytes];
     bf16 *sA = reinterpret_cast<bf16 *>(smem);
     bf16 *sB = sA + S * kA;
 
-    const int pid = xcd_swizzle((int)blockIdx.x, (int)gridDim.x);
     const int m0 = (pid / tiles_n) * T::BM, n0 = (pid % tiles_n) * T::BN;
     const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nk = (K + T::BK - 1) / T::BK;

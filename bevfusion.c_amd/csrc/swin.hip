@@ -102,13 +102,19 @@ struct bf_cuda_swin {
     const bf16 *merge_w[3];           // LN-folded, columns in tap-major order
     const bf16 *merge_corr[3];        // centring-correction tables (ln_fold.h)
     const float *merge_d[3];
-    float *x;
+    float *x;      // the fp32 residual stream (stage 2's at x + x2_off, the others at x)
+    size_t x2_off;
     bf16 *xn, *big;
     bf16 *xh[2];
     float2 *stats[2];
 };
 
 namespace {
+
+// Stage st's fp32 residual stream.  Stage 2's lies after stage 1's, so the
+// merges after stages 1 and 2 never write over the rows that the same
+// launch's output LayerNorm reads (merge_out_ln_kernel).
+float *stage_x(bf_cuda_swin *s, int st) { return st == 2 ? s->x + s->x2_off : s->x; }
 
 // A linear fed by a LayerNorm, folded (ln_fold.h): W'[j][kk] =
 // fp16(g[k] W[j][k]) with k = perm(kk) (identity when perm is null),
@@ -176,18 +182,16 @@ FoldedLinear fold_ln(const float *W, const float *b, const float *g, const float
 void launch_out_ln(int C, const float *x, const float2 *stats, float *out, const float *g,
                    const float *b, int rows, int hw, hipStream_t s) {
     const bool vec = hw % 4 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0;
+    const OutLnArgs a{x, stats, out, g, b, rows, hw, vec};
     switch (C) {
         case 192:
-            hipLaunchKernelGGL((out_ln_kernel<3, 64>), dim3((rows + 63) / 64, 3), dim3(256), 0, s, x,
-                               stats, out, g, b, rows, hw, vec);
+            hipLaunchKernelGGL((out_ln_kernel<3, 64>), dim3((rows + 63) / 64, 3), dim3(256), 0, s, a);
             break;
         case 384:
-            hipLaunchKernelGGL((out_ln_kernel<6, 64>), dim3((rows + 63) / 64, 6), dim3(256), 0, s, x,
-                               stats, out, g, b, rows, hw, vec);
+            hipLaunchKernelGGL((out_ln_kernel<6, 64>), dim3((rows + 63) / 64, 6), dim3(256), 0, s, a);
             break;
         case 768:
-            hipLaunchKernelGGL((out_ln_kernel<12, 32>), dim3((rows + 31) / 32, 12), dim3(256), 0, s,
-                               x, stats, out, g, b, rows, hw, vec);
+            hipLaunchKernelGGL((out_ln_kernel<12, 32>), dim3((rows + 31) / 32, 12), dim3(256), 0, s, a);
             break;
         default: break;
     }
@@ -385,6 +389,10 @@ static int swin_build(bf_cuda_swin *s, const bf_model *model, size_t batches, si
     }
     {
         size_t x_elems = 0, xn_elems = 0, big_elems = 0, xh_elems = 0, stat_elems = 0;
+        const size_t tok1 = batches * (size_t)s->h[1] * s->w[1];
+        const size_t tok2 = batches * (size_t)s->h[2] * s->w[2];
+        s->x2_off = (tok1 * kC[1] + 63) & ~size_t(63);  // 256-byte aligned
+        x_elems = s->x2_off + tok2 * kC[2];
         for (int st = 0; st < 4; ++st) {
             const size_t t = batches * (size_t)s->h[st] * s->w[st];
             x_elems = std::max(x_elems, t * kC[st]);
@@ -401,7 +409,6 @@ static int swin_build(bf_cuda_swin *s, const bf_model *model, size_t batches, si
             if (st < 3) {
                 const size_t t2 = batches * (size_t)s->h[st + 1] * s->w[st + 1];
                 xn_elems = std::max(xn_elems, t2 * 4 * kC[st]);
-                x_elems = std::max(x_elems, t2 * 2 * kC[st]);
             }
         }
         // The linears address their 16-bit operands through 32-bit buffer offsets.
@@ -469,7 +476,7 @@ void patch_embed(bf_cuda_swin *s, const float *images, hipStream_t stream) {
     g.M = B * s->h[0] * s->w[0]; g.K = 48;
     LoadRowsBf16<T::BN, T::BK, T::kThreads> bl{s->patch_w, 48, 96, 48};
     const BlockW &b0 = s->blocks[0][0];
-    EpiPatchNorms epi{s->x, s->xn, s->patch_b, s->patch_ns, s->patch_nb, b0.n1s, b0.n1b, g.M};
+    EpiPatchNorms epi{stage_x(s, 0), s->xn, s->patch_b, s->patch_ns, s->patch_nb, b0.n1s, b0.n1b, g.M};
     if (((uintptr_t)images & 15) == 0) {  // IW % 4 == 0 by contract: float4 patch rows
         LoadPatch4x4<T::BM, T::BK, T::kThreads, true> al{images, g};
         launch_gemm<T>(al, bl, epi, g.M, 96, 48, stream);
@@ -538,7 +545,7 @@ void block_op(bf_cuda_swin *s, int st, int b, int op, hipStream_t stream) {
             break;
         case BFHIP_SWIN_PROJ:
             linear_f16(s->xn, w.proj_w, T, C, C,
-                       EpiStatsRows<false, true>{s->x, xh, stats, w.proj_b, nullptr, {}, T, C},
+                       EpiStatsRows<false, true>{stage_x(s, st), xh, stats, w.proj_b, nullptr, {}, T, C},
                        stream);
             break;
         case BFHIP_SWIN_FC1:  // LN2 folded
@@ -553,7 +560,7 @@ void block_op(bf_cuda_swin *s, int st, int b, int op, hipStream_t stream) {
             // The last block of a stage leaves x and its row statistics for
             // the stage-output norm (and, before stage 3, the patch merge).
             linear_f16(s->big, w.fc2_w, T, C, 4 * C,
-                       EpiStatsRows<false, true>{s->x, xh, stats, w.fc2_b, nullptr, {}, T, C},
+                       EpiStatsRows<false, true>{stage_x(s, st), xh, stats, w.fc2_b, nullptr, {}, T, C},
                        stream);
             break;
         case BFHIP_SWIN_MLP: {
@@ -563,7 +570,7 @@ void block_op(bf_cuda_swin *s, int st, int b, int op, hipStream_t stream) {
             const bool next = b + 1 < kDepth[st];
             const BlockW *nw = next ? &s->blocks[st][b + 1] : nullptr;
             // proj reads the attention output in xn; LN1' overwrites it row by row.
-            launch_swin_mlp<MlpS0>(s->x, s->xn, w.mlp_proj, w.proj_b, w.n2s, w.n2b, w.mlp_w,
+            launch_swin_mlp<MlpS0>(stage_x(s, st), s->xn, w.mlp_proj, w.proj_b, w.n2s, w.n2b, w.mlp_w,
                                    w.fc1_b, w.fc2_b, nw ? nw->n1s : nullptr,
                                    nw ? nw->n1b : nullptr, next ? s->xn : nullptr, T, stream,
                                    next ? nullptr : stage_xh(s, st),
@@ -597,6 +604,34 @@ int block_ops(int st, int b, int *ops) {
     return n;
 }
 
+// A patch merge and the stage-output LayerNorm of the same stage in one
+// launch: workgroups [0, tiles) are the merge's tiles (the first ids, so
+// their XCD mapping is the standalone launch's), the rest the LayerNorm's
+// 64-token x 64-channel tiles (OutLn).  Both read stage st's activations;
+// the merge writes stage st + 1's residual into the other parity buffer, so
+// the two are independent, and the LayerNorm's HBM-bound tiles fill the CU
+// slots the merge leaves free instead of running after it.  The branch is
+// uniform per workgroup.
+template <bool SPEC, class T, class ALoad, class BLoad, class Epi, int G, int THREADS>
+__global__ __launch_bounds__(THREADS) void merge_out_ln_kernel(ALoad al, BLoad bl, Epi epi, int M,
+                                                               int N, int K, int tiles_n,
+                                                               int tiles, OutLnArgs o) {
+    using LN = OutLn<G, 64, THREADS>;
+    constexpr size_t kM = dma_smem_bytes<T, Epi>();
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[kM > LN::kSmem ? kM : LN::kSmem];
+    const int bid = (int)blockIdx.x;
+    if (bid < tiles) {
+        const int pid = xcd_swizzle(bid, tiles);
+        if constexpr (SPEC)
+            gemm_spec_block<T>(al, bl, epi, M, N, K, tiles_n, pid, smem);
+        else
+            gemm_dma_block<T>(al, bl, epi, M, N, K, tiles_n, pid, smem);
+        return;
+    }
+    const int r = bid - tiles;
+    LN::block(o, r / G, r % G, smem);
+}
+
 // Patch merge after stage st with its LayerNorm over 4C folded: the A operand
 // gathers the 2x2 tokens from xh, the statistics combine the tokens' group
 // partials (groups of 64 channels, or the whole 96-channel token at stage 0),
@@ -604,10 +639,12 @@ int block_ops(int st, int b, int *ops) {
 // linear_f16 picks for these (N, K); LW > 0 runs the tile on the
 // wave-specialised pipeline with LW loader waves (measured on MI355X for the
 // second merge, 1056 x 768 x 1536: 7.3 vs 8.9 us).  The gather and its tile
-// are merge_gemm's, which bfhip_debug_swin_merge_gather also runs.
+// are merge_gemm's, which bfhip_debug_swin_merge_gather also runs.  With
+// `ln` (stages 1 and 2), stage st's output LayerNorm runs in the same launch
+// (merge_out_ln_kernel, G = C / 64 statistics groups).
 template <int C, class T, int LW, class Epi>
 void merge_gemm(const bf16 *xh, int B, int H, int W, const bf16 *w, int N, const Epi &epi,
-                hipStream_t stream) {
+                hipStream_t stream, const OutLnArgs *ln = nullptr) {
     const int T2 = B * ((H + 1) / 2) * ((W + 1) / 2);
     constexpr int kLoadThreads = LW > 0 ? LW * kWave : T::kThreads;
     DmaMergeRows<T::BM, T::BK, kLoadThreads, C> al{};
@@ -616,6 +653,18 @@ void merge_gemm(const bf16 *xh, int B, int H, int W, const bf16 *w, int N, const
     al.H = H;
     al.W = W;
     DmaRowsBf16<T::BN, T::BK, kLoadThreads> bl{w, 4 * C, N, 4 * C};
+    if constexpr (C % kStatCols == 0) {
+        if (ln) {
+            constexpr int G = C / kStatCols, kThreads = T::kThreads + (LW > 0 ? LW * kWave : 0);
+            const int tiles_n = (N + T::BN - 1) / T::BN;
+            const int tiles = (T2 + T::BM - 1) / T::BM * tiles_n;
+            const int ln_blocks = (ln->rows + 63) / 64 * G;
+            hipLaunchKernelGGL((merge_out_ln_kernel<(LW > 0), T, decltype(al), decltype(bl), Epi, G, kThreads>),
+                               dim3(tiles + ln_blocks), dim3(kThreads), 0, stream, al, bl, epi, T2, N,
+                               4 * C, tiles_n, tiles, *ln);
+            return;
+        }
+    }
     if constexpr (LW > 0)
         launch_gemm_spec<T>(al, bl, epi, T2, N, 4 * C, stream);
     else
@@ -623,16 +672,16 @@ void merge_gemm(const bf16 *xh, int B, int H, int W, const bf16 *w, int N, const
 }
 
 template <int C, class T, int LW = 0>
-void merge_folded(bf_cuda_swin *s, int st, hipStream_t stream) {
+void merge_folded(bf_cuda_swin *s, int st, hipStream_t stream, const OutLnArgs *ln = nullptr) {
     const int B = (int)s->batches, H = s->h[st], W = s->w[st];
     const int T2 = B * s->h[st + 1] * s->w[st + 1];
     const int nx = (st + 1) & 1;
     constexpr bool kWhole = C % kStatCols != 0;  // one group per token
     using Src = LnMerge<kWhole ? 1 : C / kStatCols, kWhole ? C : kStatCols>;
-    EpiStatsRows<true, false, Src> epi{s->x,          s->xh[nx],     s->stats[nx],
+    EpiStatsRows<true, false, Src> epi{stage_x(s, st + 1), s->xh[nx],     s->stats[nx],
                                        s->merge_d[st], s->merge_corr[st], Src{stage_stats(s, st), H, W},
                                        T2,            2 * C};
-    merge_gemm<C, T, LW>(stage_xh(s, st), B, H, W, s->merge_w[st], 2 * C, epi, stream);
+    merge_gemm<C, T, LW>(stage_xh(s, st), B, H, W, s->merge_w[st], 2 * C, epi, stream, ln);
 }
 
 // The merge tiles per stage.
@@ -641,13 +690,22 @@ using MergeT1 = DmaTile<64, 64, 64, 2, 2, 2, true>;
 using MergeT2 = DmaTile<64, 64, 128, 2, 2, 3, true>;
 constexpr int kMergeLoaders2 = 4;
 
-void merge_op(bf_cuda_swin *s, int st, hipStream_t stream) {
+// The merge after stage st; with `ln`, stage st's output LayerNorm in the
+// same launch (stages 1 and 2).
+void merge_op(bf_cuda_swin *s, int st, hipStream_t stream, const OutLnArgs *ln = nullptr) {
     if (st == 0)
         merge_folded<96, MergeT0>(s, st, stream);
     else if (st == 1)
-        merge_folded<192, MergeT1>(s, st, stream);
+        merge_folded<192, MergeT1>(s, st, stream, ln);
     else
-        merge_folded<384, MergeT2, kMergeLoaders2>(s, st, stream);
+        merge_folded<384, MergeT2, kMergeLoaders2>(s, st, stream, ln);
+}
+
+// Stage st's output LayerNorm into `out` (NCHW fp32).
+OutLnArgs out_ln_args(bf_cuda_swin *s, int st, float *out) {
+    const int T = (int)s->batches * s->h[st] * s->w[st], hw = s->h[st] * s->w[st];
+    return OutLnArgs{stage_x(s, st), stage_stats(s, st), out, s->out_s[st - 1], s->out_b[st - 1], T,
+                     hw, hw % 4 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0};
 }
 
 }  // namespace
@@ -666,11 +724,17 @@ extern "C" int bf_cuda_swin_forward(bf_cuda_swin *s, const float *images, float 
             const int n = block_ops(st, b, ops);
             for (int i = 0; i < n; ++i) block_op(s, st, b, ops[i], stream);
         }
-        const int T = (int)s->batches * s->h[st] * s->w[st];
-        if (st > 0)
-            launch_out_ln(kC[st], s->x, stage_stats(s, st), outputs[st - 1], s->out_s[st - 1],
+        // Stage outputs: stage 3's alone, stages 1 and 2 in the merge's launch.
+        if (st == 3) {
+            const int T = (int)s->batches * s->h[st] * s->w[st];
+            launch_out_ln(kC[st], stage_x(s, st), stage_stats(s, st), outputs[st - 1], s->out_s[st - 1],
                           s->out_b[st - 1], T, s->h[st] * s->w[st], stream);
-        if (st < 3) merge_op(s, st, stream);
+        } else if (st > 0) {
+            const OutLnArgs ln = out_ln_args(s, st, outputs[st - 1]);
+            merge_op(s, st, stream, &ln);
+        } else {
+            merge_op(s, st, stream);
+        }
     }
     return launch_ok(error, cap, "launch HIP Swin graph");
 }
@@ -700,8 +764,11 @@ extern "C" int bfhip_swin_profile_io(bf_cuda_swin *s, int stage, int op, const f
         patch_embed(s, images, st);
     } else if (s && op == BFHIP_SWIN_OUT_NORM && stage >= 1 && stage <= 3 && out) {
         const int T = (int)s->batches * s->h[stage] * s->w[stage];
-        launch_out_ln(kC[stage], s->x, stage_stats(s, stage), out, s->out_s[stage - 1],
+        launch_out_ln(kC[stage], stage_x(s, stage), stage_stats(s, stage), out, s->out_s[stage - 1],
                       s->out_b[stage - 1], T, s->h[stage] * s->w[stage], st);
+    } else if (s && op == BFHIP_SWIN_MERGE_OUT_NORM && stage >= 1 && stage <= 2 && out) {
+        const OutLnArgs ln = out_ln_args(s, stage, out);
+        merge_op(s, stage, st, &ln);
     } else {
         return fail(error, cap, "invalid HIP Swin profiling io call");
     }

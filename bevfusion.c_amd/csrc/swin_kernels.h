@@ -28,66 +28,89 @@ __device__ __forceinline__ void store4(bf16 *p, float a, float b, float c, float
 // segments, normalises it into LDS transposed, and writes kR-token runs of
 // each of its 64 channel planes, as float4 when `vec` (hw % 4 == 0 and out
 // 16-byte aligned: four tokens from a multiple of 4 never straddle two
-// images), else per element.  Grid (ceil(rows / kR), G), 256 threads.
+// images), else per element.  block() is tile (bx, by) with THREADS threads
+// on `smem` (kSmem bytes); out_ln_kernel runs grid (ceil(rows / kR), G) of
+// them with 256 threads, and a kernel that fuses it with other work calls
+// block() for part of its grid.
+struct OutLnArgs {
+    const float *x;
+    const float2 *stats;
+    float *out;
+    const float *g, *b;
+    int rows, hw;
+    bool vec;
+};
+
+template <int G, int kR, int THREADS>
+struct OutLn {
+    static constexpr int C = G * kStatCols;
+    static constexpr int kPass = THREADS / 16;  // rows per pass of the tile load
+    static_assert(kR % 16 == 0 && kR <= THREADS && kR % kPass == 0, "tile rows");
+    static constexpr size_t kTileBytes = (size_t)kStatCols * (kR + 1) * sizeof(float);
+    static constexpr size_t kSmem = kTileBytes + (size_t)kR * sizeof(float2);
+
+    __device__ __forceinline__ static void block(const OutLnArgs &a, int bx, int by, unsigned char *smem) {
+        float(*tile)[kR + 1] = reinterpret_cast<float(*)[kR + 1]>(smem);
+        float2 *norm = reinterpret_cast<float2 *>(smem + kTileBytes);
+        const int tid = threadIdx.x;
+        const int row0 = bx * kR, c0 = by * kStatCols;
+        // The x tile and the statistics are loaded together, then combined.
+        constexpr int kPer = kR / kPass;  // rows per thread: tid / 16, + kPass, ...
+        const int q = 4 * (tid & 15), r0 = tid >> 4;
+        float4 v[kPer];
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int row = row0 + r0 + kPass * i;
+            v[i] = row < a.rows ? *reinterpret_cast<const float4 *>(a.x + (size_t)row * C + c0 + q)
+                                : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        if (tid < kR) {
+            const int row = row0 + tid;
+            float2 p[G];
+#pragma unroll
+            for (int k = 0; k < G; ++k)
+                p[k] = row < a.rows ? a.stats[(size_t)row * G + k] : make_float2(0.0f, 0.0f);
+            const RowLn<G> l = ln_combine<G>(p);
+            norm[tid] = make_float2(l.mean, l.r);
+        }
+        const float4 gv = *reinterpret_cast<const float4 *>(a.g + c0 + q);
+        const float4 bv = *reinterpret_cast<const float4 *>(a.b + c0 + q);
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int r = r0 + kPass * i;
+            const float2 m = norm[r];
+            tile[q + 0][r] = (v[i].x - m.x) * m.y * gv.x + bv.x;
+            tile[q + 1][r] = (v[i].y - m.x) * m.y * gv.y + bv.y;
+            tile[q + 2][r] = (v[i].z - m.x) * m.y * gv.z + bv.z;
+            tile[q + 3][r] = (v[i].w - m.x) * m.y * gv.w + bv.w;
+        }
+        __syncthreads();
+        if (a.vec) {
+            constexpr int kQ = kR / 4;
+            for (int e = tid; e < kStatCols * kQ; e += THREADS) {
+                const int c = e / kQ, r = 4 * (e - c * kQ), row = row0 + r;
+                if (row >= a.rows) continue;
+                const int n = row / a.hw, p = row - n * a.hw;
+                *reinterpret_cast<float4 *>(a.out + ((size_t)n * C + c0 + c) * a.hw + p) =
+                    make_float4(tile[c][r], tile[c][r + 1], tile[c][r + 2], tile[c][r + 3]);
+            }
+        } else {
+            for (int e = tid; e < kStatCols * kR; e += THREADS) {
+                const int c = e / kR, r = e - c * kR, row = row0 + r;
+                if (row >= a.rows) continue;
+                const int n = row / a.hw, p = row - n * a.hw;
+                a.out[((size_t)n * C + c0 + c) * a.hw + p] = tile[c][r];
+            }
+        }
+    }
+};
+
 template <int G, int kR>
-__global__ __launch_bounds__(256) void out_ln_kernel(const float *x, const float2 *stats,
-                                                     float *out, const float *g, const float *b,
-                                                     int rows, int hw, bool vec) {
-    constexpr int C = G * kStatCols;
-    static_assert(kR % 16 == 0 && kR <= 256, "tile rows");
-    __shared__ float tile[kStatCols][kR + 1];
-    __shared__ float2 norm[kR];
-    const int tid = threadIdx.x;
-    const int row0 = blockIdx.x * kR, c0 = blockIdx.y * kStatCols;
-    // The x tile and the statistics are loaded together, then combined.
-    constexpr int kPer = kR / 16;  // rows per thread: tid / 16, + 16, ...
-    const int q = 4 * (tid & 15), r0 = tid >> 4;
-    float4 v[kPer];
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-        const int row = row0 + r0 + 16 * i;
-        v[i] = row < rows ? *reinterpret_cast<const float4 *>(x + (size_t)row * C + c0 + q)
-                          : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-    if (tid < kR) {
-        const int row = row0 + tid;
-        float2 p[G];
-#pragma unroll
-        for (int k = 0; k < G; ++k)
-            p[k] = row < rows ? stats[(size_t)row * G + k] : make_float2(0.0f, 0.0f);
-        const RowLn<G> l = ln_combine<G>(p);
-        norm[tid] = make_float2(l.mean, l.r);
-    }
-    const float4 gv = *reinterpret_cast<const float4 *>(g + c0 + q);
-    const float4 bv = *reinterpret_cast<const float4 *>(b + c0 + q);
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-        const int r = r0 + 16 * i;
-        const float2 m = norm[r];
-        tile[q + 0][r] = (v[i].x - m.x) * m.y * gv.x + bv.x;
-        tile[q + 1][r] = (v[i].y - m.x) * m.y * gv.y + bv.y;
-        tile[q + 2][r] = (v[i].z - m.x) * m.y * gv.z + bv.z;
-        tile[q + 3][r] = (v[i].w - m.x) * m.y * gv.w + bv.w;
-    }
-    __syncthreads();
-    if (vec) {
-        constexpr int kQ = kR / 4;
-        for (int e = tid; e < kStatCols * kQ; e += 256) {
-            const int c = e / kQ, r = 4 * (e - c * kQ), row = row0 + r;
-            if (row >= rows) continue;
-            const int n = row / hw, p = row - n * hw;
-            *reinterpret_cast<float4 *>(out + ((size_t)n * C + c0 + c) * hw + p) =
-                make_float4(tile[c][r], tile[c][r + 1], tile[c][r + 2], tile[c][r + 3]);
-        }
-    } else {
-        for (int e = tid; e < kStatCols * kR; e += 256) {
-            const int c = e / kR, r = e - c * kR, row = row0 + r;
-            if (row >= rows) continue;
-            const int n = row / hw, p = row - n * hw;
-            out[((size_t)n * C + c0 + c) * hw + p] = tile[c][r];
-        }
-    }
+__global__ __launch_bounds__(256) void out_ln_kernel(OutLnArgs a) {
+    using LN = OutLn<G, kR, 256>;
+    __shared__ __attribute__((aligned(16))) unsigned char smem[LN::kSmem];
+    LN::block(a, (int)blockIdx.x, (int)blockIdx.y, smem);
 }
 
 // ------------------------------------------------------- window attention

@@ -53,11 +53,16 @@ int bfhip_swin_profile_op(bf_cuda_swin *swin, int stage, int block, int op,
  *   BFHIP_SWIN_PATCH_EMBED  the patch embedding (4x4/s4 conv + patch norm +
  *                           block 0's LN1): reads `images` [B,3,H,W];
  *                           `stage` must be 0;
- *   BFHIP_SWIN_OUT_NORM     the output LayerNorm of stage `stage` (1..3):
- *                           writes `out`, the stage's NCHW output. */
+ *   BFHIP_SWIN_OUT_NORM     the output LayerNorm of stage `stage` (1..3),
+ *                           alone: writes `out`, the stage's NCHW output
+ *                           (the forward runs it alone at stage 3);
+ *   BFHIP_SWIN_MERGE_OUT_NORM  the patch merge after stage `stage` (1..2)
+ *                           and that stage's output LayerNorm into `out`, in
+ *                           one launch, as the forward runs them. */
 enum {
     BFHIP_SWIN_PATCH_EMBED = 10,
-    BFHIP_SWIN_OUT_NORM = 11
+    BFHIP_SWIN_OUT_NORM = 11,
+    BFHIP_SWIN_MERGE_OUT_NORM = 12
 };
 
 int bfhip_swin_profile_io(bf_cuda_swin *swin, int stage, int op, const float *images, float *out,

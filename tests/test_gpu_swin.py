@@ -138,3 +138,40 @@ def test_swin_offset_rows_match_oracle(device, tmp_models, offset):
         mx = float(np.abs(g - r).max() / np.sqrt(np.mean(r * r)))
         print(f"offset {offset} output{i}: rel-L2 {rel:.3e}, max-abs {mx:.3e} x RMS", flush=True)
         assert_close(g, r, f"swin offset {offset} output{i}")
+
+
+@pytest.mark.parametrize("shape", [(2, 56, 112), (6, 256, 704)])
+def test_swin_fused_merge_out_norm_matches_forward(device, tmp_models, shape):
+    """The forward runs the merges after stages 1 and 2 in one launch with
+    that stage's output LayerNorm (merge_out_ln_kernel).  After a forward the
+    context still holds stage 2's residual, row statistics and fp16 copy
+    (stage 3's live elsewhere), so the profiling hook that runs the same
+    fused launch for stage 2 (include/bfhip_profile.h,
+    BFHIP_SWIN_MERGE_OUT_NORM) and the standalone stage-2 LayerNorm must both
+    reproduce the forward's second output bit for bit; and stage 3's
+    standalone LayerNorm, run before them, the third."""
+    import bfhip
+    import torch
+    from bfhip import bfw
+    b, h, w = shape
+    print(f"[case] fused merge + output norm, {shape}", flush=True)
+    path = tmp_models("fan_in", 1)
+    images = bfw.synthetic_images(7, b, h, w)
+    x = torch.from_numpy(images).to(device)
+    with bfhip.Model(path) as m:
+        ctx = bfhip.Swin(m, b, h, w)
+    outs = ctx.forward(x)
+    torch.cuda.synchronize()
+    fused = torch.full_like(outs[1], float("nan"))
+    alone = torch.full_like(outs[1], float("nan"))
+    last = torch.full_like(outs[2], float("nan"))
+    # Stage 3's norm first: the merge in the fused launch rewrites stage 3's
+    # residual (with the merge output, before stage 3's blocks).
+    ctx.profile_io("out_norm", 3, out=last)
+    ctx.profile_io("merge_out_norm", 2, out=fused)
+    ctx.profile_io("out_norm", 2, out=alone)
+    torch.cuda.synchronize()
+    assert torch.equal(fused, outs[1]), "fused launch's output norm differs from the forward's"
+    assert torch.equal(alone, outs[1]), "standalone output norm differs from the fused one"
+    assert torch.equal(last, outs[2])
+    ctx.close()
