@@ -6,13 +6,15 @@
 //             last); a stable radix sort of (key, sample index) pairs
 //             (rocPRIM, AMD's device primitives) lists each cell's samples in
 //             ascending sample order; a lower bound per cell gives each
-//             cell's run; each sample's list slot and each slot's context row
-//             are stored.
-//   forward:  depth softmax per pixel, each probability stored at its
-//             sample's list slot; context NCHW -> rows [B*N*H*W][C]; per BEV
-//             cell a group of lanes sums prob * row over the cell's run in
-//             list order, and each workgroup stores 64 consecutive cells of
-//             every channel plane as coalesced rows.
+//             cell's run, padded to whole quads; the list of {context row,
+//             sample} and the pool schedule are stored.
+//   forward:  one prologue launch computes the per-pixel softmax statistics
+//             {max, 1 / sum} and turns the context NCHW into rows
+//             [B*N*H*W][C]; per BEV cell a group of lanes sums
+//             expf(l - max) * inv * row over the cell's run in list order,
+//             and each workgroup stores 64 consecutive cells of every channel
+//             plane as coalesced rows; cells cut by a slice bound are added
+//             up by a last pass.
 // Stateless routes: the reference's atomic accumulation (one wave per pixel,
 // softmax on the wave, atomicAdd per (channel, depth) sample).
 //
@@ -277,26 +279,26 @@ __global__ __launch_bounds__(256) void list_padding_kernel(const int *__restrict
 
 // Pool schedule.  The BEV output is cut into tiles of kTileCells consecutive
 // cells of one batch; a tile whose lists hold more than kSliceEntries entries
-// is cut into equal slices, each pooled by its own workgroup into a partial
-// tile that a second pass adds up in slice order.
+// is cut into equal slices, each pooled by its own workgroup.  A slice stores
+// the cells whose lists begin inside it; a cell that runs on into the next
+// slice leaves partial rows (the owner's and each later slice's share) that a
+// second pass adds up in slice order.
 constexpr int kTileCells = 64;
 constexpr int kSliceEntries = 2048;
 constexpr int kScheduleThreads = 1024;
 
 // One workgroup: per tile, slice count; exclusive scans give each tile's
-// first work item, its first scratch slot (multi-slice tiles only) and its
-// index among multi-slice tiles.  sched layout: slices[tiles],
-// slice_base[tiles + 1], scratch_base[tiles], multi_base[tiles + 1].
+// first work item and its index among multi-slice tiles.  sched layout:
+// slices[tiles], slice_base[tiles + 1], multi_base[tiles + 1].
 __global__ __launch_bounds__(kScheduleThreads) void schedule_kernel(const int *__restrict__ starts,
                                                                    int *__restrict__ sched,
                                                                    int tiles, int tiles_per_batch,
                                                                    int cells) {
-    __shared__ int part[3][kScheduleThreads];
-    int *slices = sched, *slice_base = sched + tiles, *scratch_base = slice_base + tiles + 1,
-        *multi_base = scratch_base + tiles;
+    __shared__ int part[2][kScheduleThreads];
+    int *slices = sched, *slice_base = sched + tiles, *multi_base = slice_base + tiles + 1;
     const int t = threadIdx.x, per = (tiles + kScheduleThreads - 1) / kScheduleThreads;
     const int lo = min(tiles, t * per), hi = min(tiles, lo + per);
-    int sum[3] = {0, 0, 0};
+    int sum[2] = {0, 0};
     for (int i = lo; i < hi; ++i) {
         const int b = i / tiles_per_batch, j0 = (i - b * tiles_per_batch) * kTileCells;
         const int first = b * cells + j0, last = b * cells + min(cells, j0 + kTileCells);
@@ -304,32 +306,29 @@ __global__ __launch_bounds__(kScheduleThreads) void schedule_kernel(const int *_
         const int ns = max(1, (entries + kSliceEntries - 1) / kSliceEntries);
         slices[i] = ns;
         sum[0] += ns;
-        sum[1] += ns > 1 ? ns : 0;
-        sum[2] += ns > 1;
+        sum[1] += ns > 1;
     }
-    for (int q = 0; q < 3; ++q) part[q][t] = sum[q];
+    for (int q = 0; q < 2; ++q) part[q][t] = sum[q];
     __syncthreads();
     for (int off = 1; off < kScheduleThreads; off <<= 1) {  // inclusive scans
-        int v[3];
-        for (int q = 0; q < 3; ++q) v[q] = t >= off ? part[q][t - off] : 0;
+        int v[2];
+        for (int q = 0; q < 2; ++q) v[q] = t >= off ? part[q][t - off] : 0;
         __syncthreads();
-        for (int q = 0; q < 3; ++q) part[q][t] += v[q];
+        for (int q = 0; q < 2; ++q) part[q][t] += v[q];
         __syncthreads();
     }
-    int run[3];
-    for (int q = 0; q < 3; ++q) run[q] = part[q][t] - sum[q];
+    int run[2];
+    for (int q = 0; q < 2; ++q) run[q] = part[q][t] - sum[q];
     for (int i = lo; i < hi; ++i) {
         const int ns = slices[i];
         slice_base[i] = run[0];
-        scratch_base[i] = run[1];
-        multi_base[i] = run[2];
+        multi_base[i] = run[1];
         run[0] += ns;
-        run[1] += ns > 1 ? ns : 0;
-        run[2] += ns > 1;
+        run[1] += ns > 1;
     }
     if (t == kScheduleThreads - 1) {
         slice_base[tiles] = part[0][t];
-        multi_base[tiles] = part[2][t];
+        multi_base[tiles] = part[1][t];
     }
 }
 
@@ -340,24 +339,40 @@ __global__ __launch_bounds__(256) void work_list_kernel(const int *__restrict__ 
                                                        int *__restrict__ multi, int tiles) {
     const int t = blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= tiles) return;
-    const int *slices = sched, *slice_base = sched + tiles, *multi_base = slice_base + 2 * tiles + 1;
+    const int *slices = sched, *slice_base = sched + tiles, *multi_base = slice_base + tiles + 1;
     const int ns = slices[t];
     for (int k = 0; k < ns; ++k) work[slice_base[t] + k] = make_int2(t, k);
     if (ns > 1) multi[multi_base[t]] = t;
 }
 
-// Per-pixel depth softmax statistics {max, 1 / sum exp(l - max)} (reference
-// lss.c:144-158 operation order: float max, double sum of expf(l - max), the
-// inverse rounded to float); a sample's probability is then
-// expf(l - max) * inv.  Workgroup = 32 pixels x 8 depth slices of kSlice bins.
+// Entry bound k of a tile's ns slices: whole quads of [start, end).
+__device__ __forceinline__ int slice_bound(int start, int end, int k, int ns) {
+    const int Q0 = start / kQuad, Qn = end / kQuad - Q0;
+    return kQuad * (Q0 + (int)((long long)Qn * k / ns));
+}
+
+// Forward prologue, one launch: workgroups [0, softmax_blocks) compute the
+// per-pixel depth softmax statistics, the rest turn the context NCHW into
+// rows.
+//
+// Statistics {max, 1 / sum exp(l - max)} (reference lss.c:144-158 operation
+// order: float max, double sum of expf(l - max), the inverse rounded to
+// float); a sample's probability is then expf(l - max) * inv.  Workgroup =
+// 32 pixels x 8 depth slices of kSlice bins.
 constexpr int kSoftmaxPixels = 32, kSlices = 8, kSlice = kMaxDepth / kSlices;
-__global__ __launch_bounds__(256) void softmax_stats_kernel(const float *__restrict__ logits,
-                                                           float2 *__restrict__ stats, int pixels,
-                                                           int depths, int hw) {
-    __shared__ float part_max[kSlices][kSoftmaxPixels];
-    __shared__ double part_sum[kSlices][kSoftmaxPixels];
+// Context rows: workgroup = 64 pixels of one camera; channels in chunks of
+// up to kRowChunk through an LDS tile [channel][pixel] (65-float pitch), so
+// both the plane reads and the row writes are contiguous runs.
+constexpr int kRowPixels = 64, kRowChunk = 128, kRowPitch = kRowPixels + 1;
+
+__device__ __forceinline__ void softmax_stats_block(const float *__restrict__ logits,
+                                                    float2 *__restrict__ stats, int pixels,
+                                                    int depths, int hw, int block, float *smem) {
+    float(*part_max)[kSoftmaxPixels] = reinterpret_cast<float(*)[kSoftmaxPixels]>(smem);
+    double(*part_sum)[kSoftmaxPixels] =
+        reinterpret_cast<double(*)[kSoftmaxPixels]>(smem + kSlices * kSoftmaxPixels);
     const int lane = threadIdx.x & (kSoftmaxPixels - 1), slice = threadIdx.x / kSoftmaxPixels;
-    const int px = blockIdx.x * kSoftmaxPixels + lane;
+    const int px = block * kSoftmaxPixels + lane;
     const bool live = px < pixels;
     const int cam = live ? px / hw : 0, p = live ? px - cam * hw : 0;
     const size_t base = (size_t)cam * depths * hw + p;
@@ -388,23 +403,47 @@ __global__ __launch_bounds__(256) void softmax_stats_kernel(const float *__restr
     stats[px] = make_float2(m, (float)(1.0 / total));
 }
 
-// Context [cams][C][hw] -> [cams * hw][C] through a 64 x 64 LDS tile.
-__global__ __launch_bounds__(256) void context_rows_kernel(const float *__restrict__ ctx,
-                                                           float *__restrict__ rows, int C,
-                                                           int hw) {
-    __shared__ float tile[64][65];
-    const int cam = blockIdx.z, c0 = blockIdx.y * 64, p0 = blockIdx.x * 64, t = threadIdx.x;
-    const float *src = ctx + (size_t)cam * C * hw;
-    for (int i = 0; i < 16; ++i) {
-        const int cl = (t >> 6) + 4 * i, pl = t & 63, c = c0 + cl, p = p0 + pl;
-        tile[cl][pl] = (c < C && p < hw) ? src[(size_t)c * hw + p] : 0.0f;
+__device__ __forceinline__ void context_rows_block(const float *__restrict__ ctx,
+                                                   float *__restrict__ rows, int C, int hw,
+                                                   int groups, int block, float *tile) {
+    const int cam = block / groups, p0 = (block - cam * groups) * kRowPixels;
+    const int np = min(kRowPixels, hw - p0), t = threadIdx.x;
+    const float *src = ctx + (size_t)cam * C * hw + p0;
+    float *dst = rows + ((size_t)cam * hw + p0) * C;
+    for (int c0 = 0; c0 < C; c0 += kRowChunk) {
+        const int cc = min(kRowChunk, C - c0);
+        constexpr int kLoads = kRowChunk * kRowPixels / 256;
+        float v[kLoads];
+        const int pl = t & (kRowPixels - 1), cl = t / kRowPixels;
+#pragma unroll
+        for (int i = 0; i < kLoads; ++i) {
+            const int c = cl + 4 * i;
+            v[i] = (c < cc && pl < np) ? src[(size_t)(c0 + c) * hw + pl] : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < kLoads; ++i)
+            if (cl + 4 * i < cc) tile[(cl + 4 * i) * kRowPitch + pl] = v[i];
+        __syncthreads();
+        // row-major [np][cc] run of the output (contiguous when cc == C)
+        for (int o = t; o < np * cc; o += 256) {
+            const int p = o / cc, c = o - p * cc;
+            dst[(size_t)p * C + c0 + c] = tile[c * kRowPitch + p];
+        }
+        __syncthreads();
     }
-    __syncthreads();
-    float *dst = rows + (size_t)cam * hw * C;
-    for (int i = 0; i < 16; ++i) {
-        const int pl = (t >> 6) + 4 * i, cl = t & 63, c = c0 + cl, p = p0 + pl;
-        if (c < C && p < hw) dst[(size_t)p * C + c] = tile[cl][pl];
-    }
+}
+
+__global__ __launch_bounds__(256) void forward_prologue_kernel(
+    const float *__restrict__ logits, float2 *__restrict__ stats, const float *__restrict__ ctx,
+    float *__restrict__ rows, int pixels, int depths, int hw, int C, int softmax_blocks,
+    int row_groups) {
+    __shared__ __align__(16) float smem[kRowChunk * kRowPitch];
+    static_assert(kSlices * kSoftmaxPixels * (sizeof(float) + sizeof(double)) <= sizeof(smem),
+                  "softmax partials fit the tile");
+    if ((int)blockIdx.x < softmax_blocks)
+        softmax_stats_block(logits, stats, pixels, depths, hw, blockIdx.x, smem);
+    else
+        context_rows_block(ctx, rows, C, hw, row_groups, blockIdx.x - softmax_blocks, smem);
 }
 
 // ------------------------------------------------------------------ pooling
@@ -430,7 +469,7 @@ struct PoolArgs {
     const int *starts;         // padded list start per cell [cell_count + 1]
     const int *sched;          // schedule_kernel layout
     const int2 *work;          // (tile, slice)
-    float *scratch;            // partial tiles: [slot][pass][chunk_max][64]
+    float *scratch;            // partial rows of multi-slice tiles: [work item][2][C]
     float *bev;
     int cells, tiles, tiles_per_batch, C, passes, chunk_max, zero_row;
     unsigned row_bytes, rows_bytes;  // C * 4; (B*N*H*W + 1) * C * 4 < 2^32
@@ -470,9 +509,8 @@ __global__ __launch_bounds__(256) void pool_kernel(PoolArgs a) {
     if ((int)threadIdx.x <= tile_cells) s_start[threadIdx.x] = a.starts[oc0 + threadIdx.x];
     __syncthreads();
     const int ns = slices[tile_id];
-    const int Q0 = s_start[0] / kQuad, Qn = s_start[tile_cells] / kQuad - Q0;
-    const int e0 = kQuad * (Q0 + (int)((long long)Qn * k / ns));
-    const int e1 = kQuad * (Q0 + (int)((long long)Qn * (k + 1) / ns));
+    const int e0 = slice_bound(s_start[0], s_start[tile_cells], k, ns);
+    const int e1 = slice_bound(s_start[0], s_start[tile_cells], k + 1, ns);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     for (int pass = 0; pass < a.passes; ++pass) {
         const int c0 = pass * a.chunk_max, chunk = min(a.chunk_max, a.C - c0);
@@ -575,41 +613,56 @@ __global__ __launch_bounds__(256) void pool_kernel(PoolArgs a) {
             }
         }
         __syncthreads();
+        // Cells whose lists begin in [e0, e1) (the last slice: every cell from
+        // e0 on) are this slice's; one that runs past e1 is stored as its
+        // partial row 1, and a cell begun before e0 that runs into the slice
+        // as its partial row 0, for the combine pass.
         const int j = threadIdx.x & 63;
-        if (ns == 1) {
-            float *out = a.bev + ((size_t)b * a.C + c0) * a.cells + j0;
-            for (int c = threadIdx.x >> 6; c < chunk; c += 4)
-                if (j < tile_cells) out[(size_t)c * a.cells + j] = tile[c * kTileCells + (j ^ (c & 63))];
-        } else {
-            const int slot = a.sched[2 * a.tiles + 1 + tile_id] + k;  // scratch_base[tile] + k
-            float *part = a.scratch + ((size_t)slot * a.passes + pass) * a.chunk_max * kTileCells;
-            for (int c = threadIdx.x >> 6; c < chunk; c += 4)
-                part[c * kTileCells + j] = tile[c * kTileCells + (j ^ (c & 63))];
+        const int st = j < tile_cells ? s_start[j] : 0, en = j < tile_cells ? s_start[j + 1] : 0;
+        const bool owned = j < tile_cells && st >= e0 && (k == ns - 1 || st < e1);
+        const bool tail = owned && en > e1, head = !owned && st < e0 && en > e0;
+        float *out = a.bev + ((size_t)b * a.C + c0) * a.cells + j0;
+        const size_t row = (size_t)(slice_base[tile_id] + k) * 2 + (tail ? 1 : 0);
+        float *part = a.scratch + row * a.C + c0;
+        for (int c = threadIdx.x >> 6; c < chunk; c += 4) {
+            const float v = tile[c * kTileCells + (j ^ (c & 63))];
+            if (tail || head) part[c] = v;
+            else if (owned) out[(size_t)c * a.cells + j] = v;
         }
         __syncthreads();
     }
 }
 
-// Sum of a multi-slice tile's partial tiles in slice order.
+// The cells of multi-slice tiles that run across a slice bound: the owner's
+// partial row plus each later slice's, in slice order.
 __global__ __launch_bounds__(256) void combine_kernel(PoolArgs a, const int *__restrict__ multi) {
     const int *slices = a.sched, *slice_base = a.sched + a.tiles;
-    const int *scratch_base = slice_base + a.tiles + 1, *multi_base = scratch_base + a.tiles;
+    const int *multi_base = slice_base + a.tiles + 1;
     if ((int)blockIdx.x >= multi_base[a.tiles]) return;
-    const int tile_id = multi[blockIdx.x], ns = slices[tile_id], slot0 = scratch_base[tile_id];
+    const int tile_id = multi[blockIdx.x], ns = slices[tile_id], w0 = slice_base[tile_id];
     const int b = tile_id / a.tiles_per_batch, j0 = (tile_id - b * a.tiles_per_batch) * kTileCells;
     const int tile_cells = min(kTileCells, a.cells - j0);
-    const int j = threadIdx.x & 63;
-    if (j >= tile_cells) return;
-    for (int pass = 0; pass < a.passes; ++pass) {
-        const int c0 = pass * a.chunk_max, chunk = min(a.chunk_max, a.C - c0);
-        float *out = a.bev + ((size_t)b * a.C + c0) * a.cells + j0;
-        for (int c = threadIdx.x >> 6; c < chunk; c += 4) {
-            const size_t e = (size_t)c * kTileCells + j;
-            const size_t stride = (size_t)a.passes * a.chunk_max * kTileCells;
-            const float *p = a.scratch + ((size_t)slot0 * a.passes + pass) * a.chunk_max * kTileCells + e;
-            float sum = p[0];
-            for (int q = 1; q < ns; ++q) sum += p[q * stride];
-            out[(size_t)c * a.cells + j] = sum;
+    const int *start = a.starts + (size_t)b * a.cells + j0;
+    const int first = start[0], last = start[tile_cells];
+    for (int k = 0; k + 1 < ns; ++k) {
+        const int e0 = slice_bound(first, last, k, ns), e1 = slice_bound(first, last, k + 1, ns);
+        // the cell holding entry e1 - 1: last t with start[t] <= e1 - 1
+        int lo = 0, hi = tile_cells;
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (start[mid] <= e1 - 1) lo = mid;
+            else hi = mid;
+        }
+        const int t = lo, end = start[t + 1];
+        if (start[t] < e0 || end <= e1) continue;  // not slice k's, or ends at the bound
+        float *out = a.bev + (size_t)b * a.C * a.cells + j0 + t;
+        for (int c = threadIdx.x; c < a.C; c += 256) {
+            float sum = a.scratch[((size_t)(w0 + k) * 2 + 1) * a.C + c];
+            for (int m = k + 1; m < ns; ++m) {
+                sum += a.scratch[(size_t)(w0 + m) * 2 * a.C + c];
+                if (end <= slice_bound(first, last, m + 1, ns)) break;
+            }
+            out[(size_t)c * a.cells] = sum;
         }
     }
 }
@@ -793,13 +846,13 @@ extern "C" int bf_cuda_lss_plan_create(const bf_lss_desc *d, bf_cuda_lss_plan **
     p->round = (last_chunk + p->vw - 1) / p->vw >= kRoundWide ? kRoundWide : kQuad;
     // keys + sorted keys, order [samples]; starts, padded starts [cells + 1];
     // padded list; softmax stats [pixels]; context rows + one zero row;
-    // calibration; schedule; work list; multi-slice tiles; partial tiles;
+    // calibration; schedule; work list; multi-slice tiles; partial rows;
     // rocPRIM scratch.
-    const size_t scratch_floats = (size_t)2 * p->max_multi * p->passes * p->chunk_max * kTileCells;
+    const size_t scratch_floats = (size_t)2 * p->max_work * d->channels;
     const size_t parts[13] = {z.samples * 8, z.samples * 4, (z.cell_count + 1) * 4,
                               (z.cell_count + 1) * 4, p->list_capacity * 8, z.pixels * 8,
                               (z.context_count + d->channels) * 4, z.cams * kCalib * 4,
-                              ((size_t)4 * p->tiles + 2) * 4, (size_t)p->max_work * 8,
+                              ((size_t)3 * p->tiles + 2) * 4, (size_t)p->max_work * 8,
                               (size_t)p->max_multi * 4, scratch_floats * 4, p->tmp_bytes};
     size_t offs[13], total = 0;
     for (int i = 0; i < 13; ++i) {
@@ -933,10 +986,12 @@ extern "C" int bf_cuda_lss_plan_forward_f32(bf_cuda_lss_plan *plan, const float 
     const Sizes &z = plan->z;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int hw = (int)(d->feature_height * d->feature_width), C = (int)d->channels;
-    hipLaunchKernelGGL(softmax_stats_kernel, dim3(blocks_for(z.pixels, kSoftmaxPixels)), dim3(256),
-                       0, s, logits, plan->stats, (int)z.pixels, (int)d->depth_bins, hw);
-    hipLaunchKernelGGL(context_rows_kernel, dim3((hw + 63) / 64, (C + 63) / 64, (unsigned)z.cams),
-                       dim3(256), 0, s, context, plan->rows, C, hw);
+    const int softmax_blocks = (int)blocks_for(z.pixels, kSoftmaxPixels);
+    const int row_groups = (hw + kRowPixels - 1) / kRowPixels;
+    hipLaunchKernelGGL(forward_prologue_kernel,
+                       dim3((unsigned)(softmax_blocks + row_groups * (int)z.cams)), dim3(256), 0, s,
+                       logits, plan->stats, context, plan->rows, (int)z.pixels,
+                       (int)d->depth_bins, hw, C, softmax_blocks, row_groups);
     PoolArgs args;
     args.list = plan->list;
     args.logits = logits;
