@@ -3,11 +3,11 @@
 // Plan route (deterministic, no floating-point atomics):
 //   prepare:  every sample (b, n, d, y, x) -> BEV cell key (rank + b * cells;
 //             samples outside the grid get the key B * cells, which sorts
-//             last); a stable radix sort of (key, sample index) pairs
-//             (rocPRIM, AMD's device primitives) lists each cell's samples in
-//             ascending sample order; a lower bound per cell gives each
-//             cell's run, padded to whole quads; the list of {context row,
-//             sample} and the pool schedule are stored.
+//             last); a stable LSD radix sort of (key, sample index) pairs
+//             lists each cell's samples in ascending sample order; a lower
+//             bound per cell gives each cell's run, padded to whole quads;
+//             the list of {context row, sample} and the pool schedule are
+//             stored.
 //   forward:  one prologue launch computes the per-pixel softmax statistics
 //             {max, 1 / sum} and turns the context NCHW into rows
 //             [B*N*H*W][C]; per BEV cell a group of lanes sums
@@ -25,7 +25,6 @@
 #include "bf_cuda.h"
 #include "hip_common.h"
 
-#include <rocprim/device/device_radix_sort.hpp>
 #include <rocprim/device/device_scan.hpp>
 #include <rocprim/iterator/counting_iterator.hpp>
 #include <rocprim/iterator/transform_iterator.hpp>
@@ -114,17 +113,15 @@ __device__ __forceinline__ int point_rank(const float p[3], const Grid &g) {
     return (c[2] * g.cells[0] + c[0]) * g.cells[1] + c[1];
 }
 
-// Stateless ranks (within a batch, -1 outside) or plan keys (rank + batch *
-// cells, `invalid` outside).
+// Stateless ranks: the cell within the sample's batch, -1 outside.
 __global__ __launch_bounds__(256) void geometry_rank_kernel(const float *__restrict__ geometry,
                                                             int *__restrict__ out, int samples,
-                                                            int per_batch, int cells, Grid g,
-                                                            int with_batch, int invalid) {
+                                                            Grid g) {
     const int s = blockIdx.x * blockDim.x + threadIdx.x;
     if (s >= samples) return;
-    const float p[3] = {geometry[3 * (size_t)s], geometry[3 * (size_t)s + 1], geometry[3 * (size_t)s + 2]};
-    const int r = point_rank(p, g);
-    out[s] = r < 0 ? invalid : (with_batch ? r + (s / per_batch) * cells : r);
+    const float p[3] = {geometry[3 * (size_t)s], geometry[3 * (size_t)s + 1],
+                        geometry[3 * (size_t)s + 2]};
+    out[s] = point_rank(p, g);
 }
 
 // Per-camera transform coefficients, 40 floats: [0,9) post-rotation^-1,
@@ -188,17 +185,12 @@ __global__ void calibration_kernel(const float *__restrict__ cam_rot,
     o[38] = extra_trans ? 1.0f : 0.0f;
 }
 
-__global__ __launch_bounds__(256) void calibration_rank_kernel(const float *__restrict__ frustum,
-                                                               const float *__restrict__ calib,
-                                                               int *__restrict__ keys, int samples,
-                                                               int depth_hw, int cams_per_batch,
-                                                               int cells, Grid g, int invalid) {
+// Key of frustum point `local` seen by camera `cam` with coefficient row o.
+__device__ __forceinline__ int calibration_key(const float *__restrict__ frustum, const float *o,
+                                               int local, int cam, int cams_per_batch, int cells,
+                                               const Grid &g, int invalid) {
 #pragma clang fp contract(off)
-    const int s = blockIdx.x * blockDim.x + threadIdx.x;
-    if (s >= samples) return;
-    const int cam = s / depth_hw, local = s - cam * depth_hw;
-    const float *o = calib + (size_t)cam * kCalib;
-    if (o[36] == 0.0f) { keys[s] = invalid; return; }
+    if (o[36] == 0.0f) return invalid;
     const float *f = frustum + 3 * (size_t)local;
     const float p[3] = {f[0] - o[21], f[1] - o[22], f[2] - o[23]};
     float u[3], q[3], l[3], r[3];
@@ -213,7 +205,7 @@ __global__ __launch_bounds__(256) void calibration_rank_kernel(const float *__re
     if (o[38] != 0.0f)
         for (int i = 0; i < 3; ++i) r[i] += o[33 + i];
     const int rank = point_rank(r, g);
-    keys[s] = rank >= 0 ? rank + (cam / cams_per_batch) * cells : invalid;
+    return rank >= 0 ? rank + (cam / cams_per_batch) * cells : invalid;
 }
 
 __global__ __launch_bounds__(256) void fill_float_kernel(float *p, int n) {
@@ -250,7 +242,8 @@ struct PaddedCount {
     }
 };
 
-// Sorted position i of a valid sample -> its padded slot: {pixel, sample}.
+// Sorted position i of a valid sample -> its padded slot: {pixel, sample};
+// the last sample of a cell also writes the cell's padding entries.
 __global__ __launch_bounds__(256) void list_entries_kernel(const int *__restrict__ order,
                                                           const int *__restrict__ sorted_keys,
                                                           const int *__restrict__ starts,
@@ -262,19 +255,312 @@ __global__ __launch_bounds__(256) void list_entries_kernel(const int *__restrict
     const int key = sorted_keys[i];
     if (key >= cell_count) return;
     const int s = order[i];
-    const int cam = s / depth_hw;
-    list[padded_starts[key] + (i - starts[key])] =
-        make_int2(cam * hw + (s - cam * depth_hw) % hw, s);
+    const int cam = s / depth_hw, first = starts[key], slot = padded_starts[key] + (i - first);
+    list[slot] = make_int2(cam * hw + (s - cam * depth_hw) % hw, s);
+    if (i + 1 == starts[key + 1])
+        for (int k = slot + 1; k < padded_starts[key + 1]; ++k) list[k] = make_int2(0, -1);
 }
 
-__global__ __launch_bounds__(256) void list_padding_kernel(const int *__restrict__ starts,
-                                                          const int *__restrict__ padded_starts,
-                                                          int2 *__restrict__ list,
-                                                          int cell_count) {
-    const int c = blockIdx.x * blockDim.x + threadIdx.x;
-    if (c >= cell_count) return;
-    const int first = padded_starts[c] + (starts[c + 1] - starts[c]);
-    for (int k = first; k < padded_starts[c + 1]; ++k) list[k] = make_int2(0, -1);
+// Stable LSD radix sort of the (key, sample) pairs, keys < 2^end_bit, in
+// passes of up to kDigitBits bits; pass 0 reads the samples as 0..n-1.  One
+// pass, over tiles of kSortTile consecutive pairs:
+//   digit_count_kernel    each tile's count of every digit -> counts[digit][tile];
+//   digit_offsets_kernel  per digit, the exclusive scan of its counts over the
+//                         tiles, and the digit's total;
+//   digit_scatter_kernel  per tile, a stable sort by digit in LDS (splits on
+//                         three digit bits at a time), then each pair goes to
+//                         (pairs of smaller digits) + (its digit's pairs in
+//                         earlier tiles) + (its rank among them in the tile).
+// Every pass keeps equal digits in input order, so equal keys end in
+// ascending sample order.  Integer counts only: the result is the unique
+// stable order, the same on every run.
+constexpr int kDigitBits = 9, kDigits = 1 << kDigitBits, kSplitBits = 3;
+constexpr int kSortThreads = 256, kSortItems = 16, kSortTile = kSortThreads * kSortItems;
+static_assert(kSplitBits == 3 && kSortTile < 65536, "eight 16-bit bucket counts in four words");
+// LDS index of tile position i: one pad word per kSortItems, so the blocked
+// reads (thread t, items t*kSortItems + j) fall in distinct banks.
+__device__ __forceinline__ int sort_slot(int i) { return i + i / kSortItems; }
+constexpr int kSortSlots = kSortTile + kSortTile / kSortItems;
+
+__device__ __forceinline__ int digit_of(int key, int shift) {
+    return (int)(((unsigned)key >> shift) & (kDigits - 1));
+}
+
+__global__ __launch_bounds__(kSortThreads) void digit_count_kernel(const int *__restrict__ keys,
+                                                                  int n, int shift, int tiles,
+                                                                  int *__restrict__ counts) {
+    __shared__ int hist[kDigits];
+    for (int d = threadIdx.x; d < kDigits; d += kSortThreads) hist[d] = 0;
+    __syncthreads();
+    const int base = blockIdx.x * kSortTile;
+#pragma unroll
+    for (int j = 0; j < kSortItems; ++j) {
+        const int i = base + j * kSortThreads + (int)threadIdx.x;
+        if (i < n) atomicAdd(&hist[digit_of(keys[i], shift)], 1);
+    }
+    __syncthreads();
+    for (int d = threadIdx.x; d < kDigits; d += kSortThreads)
+        counts[(size_t)d * tiles + blockIdx.x] = hist[d];
+}
+
+// Inclusive scan of one int per thread over the workgroup (kSortThreads);
+// `total` receives the sum.  Ends with the workgroup synchronised.
+__device__ __forceinline__ int block_inclusive_scan(int v, int *wave_sums, int *total) {
+    constexpr int kWaves = kSortThreads / kWave;
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+        const int u = __shfl_up(v, o);
+        if (lane >= o) v += u;
+    }
+    if (lane == kWave - 1) wave_sums[wave] = v;
+    __syncthreads();
+    int before = 0, all = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+        const int x = wave_sums[w];
+        before += w < wave ? x : 0;
+        all += x;
+    }
+    *total = all;
+    __syncthreads();  // wave_sums may be reused
+    return v + before;
+}
+
+// Inclusive scan of four words per thread over the workgroup (out[w]) and
+// the four totals.  Ends with the workgroup synchronised.
+__device__ __forceinline__ void block_scan4(const unsigned (&in)[4], unsigned (*wave_sums)[4],
+                                            unsigned (&out)[4], unsigned (&total)[4]) {
+    constexpr int kWaves = kSortThreads / kWave;
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) out[w] = in[w];
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const unsigned u = __shfl_up(out[w], o);
+            if (lane >= o) out[w] += u;
+        }
+    }
+    if (lane == kWave - 1)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) wave_sums[wave][w] = out[w];
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        unsigned before = 0, all = 0;
+#pragma unroll
+        for (int q = 0; q < kWaves; ++q) {
+            const unsigned x = wave_sums[q][w];
+            before += q < wave ? x : 0u;
+            all += x;
+        }
+        out[w] += before;
+        total[w] = all;
+    }
+    __syncthreads();  // wave_sums may be reused
+}
+
+__global__ __launch_bounds__(kSortThreads) void digit_offsets_kernel(const int *__restrict__ counts,
+                                                                    int tiles,
+                                                                    int *__restrict__ offs,
+                                                                    int *__restrict__ totals) {
+    __shared__ int wave_sums[kSortThreads / kWave];
+    const int d = blockIdx.x;
+    const int *c = counts + (size_t)d * tiles;
+    int *o = offs + (size_t)d * tiles;
+    const int per = (tiles + kSortThreads - 1) / kSortThreads;
+    const int lo = min(tiles, (int)threadIdx.x * per), hi = min(tiles, lo + per);
+    int sum = 0;
+    for (int i = lo; i < hi; ++i) sum += c[i];
+    int total;
+    int run = block_inclusive_scan(sum, wave_sums, &total) - sum;
+    for (int i = lo; i < hi; ++i) {
+        o[i] = run;
+        run += c[i];
+    }
+    if (threadIdx.x == 0) totals[d] = total;
+}
+
+// vals_in == nullptr: the sample of pair i is i.
+__global__ __launch_bounds__(kSortThreads) void digit_scatter_kernel(
+    const int *__restrict__ keys_in, const int *__restrict__ vals_in, int n, int shift, int bits,
+    int tiles, const int *__restrict__ offs, const int *__restrict__ totals,
+    int *__restrict__ keys_out, int *__restrict__ vals_out) {
+    __shared__ int K[kSortSlots], V[kSortSlots];
+    __shared__ int first[kDigits];  // output position of the tile's first pair of each digit
+    __shared__ int start[kDigits];  // tile position of that pair
+    __shared__ int wave_sums[kSortThreads / kWave];
+    __shared__ unsigned wave_sums4[kSortThreads / kWave][4];
+    const int t = threadIdx.x, base = blockIdx.x * kSortTile, valid = min(kSortTile, n - base);
+
+    // The tile in position order (coalesced loads, issued first so that they
+    // overlap the offsets below); past n, key -1 (digit kDigits - 1, after
+    // every real pair of the tile in a stable sort).
+    int k[kSortItems], v[kSortItems];
+#pragma unroll
+    for (int j = 0; j < kSortItems; ++j) {
+        const int i = j * kSortThreads + t;
+        const bool live = i < valid;
+        k[j] = live ? keys_in[base + i] : -1;
+        v[j] = live ? (vals_in ? vals_in[base + i] : base + i) : 0;
+    }
+    // Pairs of smaller digits (exclusive scan of the totals, two digits per
+    // thread) plus this digit's pairs in earlier tiles.
+    {
+        static_assert(kDigits == 2 * kSortThreads, "two digits per thread");
+        const int a = totals[2 * t], b = totals[2 * t + 1];
+        const int oa = offs[(size_t)(2 * t) * tiles + blockIdx.x];
+        const int ob = offs[(size_t)(2 * t + 1) * tiles + blockIdx.x];
+        int total;
+        const int incl = block_inclusive_scan(a + b, wave_sums, &total);
+        first[2 * t] = incl - a - b + oa;
+        first[2 * t + 1] = incl - b + ob;
+    }
+#pragma unroll
+    for (int j = 0; j < kSortItems; ++j) {
+        const int i = j * kSortThreads + t;
+        K[sort_slot(i)] = k[j];
+        V[sort_slot(i)] = v[j];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kSortItems; ++j) {
+        k[j] = K[sort_slot(t * kSortItems + j)];
+        v[j] = V[sort_slot(t * kSortItems + j)];
+    }
+    // Stable splits on kSplitBits digit bits at a time: a pair's new tile
+    // position is (pairs of smaller buckets) + (its bucket's pairs in earlier
+    // threads) + (in this thread, before it).  The eight per-bucket counts
+    // travel as 16-bit fields, two per 32-bit word (a tile has < 2^16 pairs,
+    // so no field carries into the next).
+    for (int b0 = 0; b0 < bits; b0 += kSplitBits) {
+        const int mask = (1 << min(kSplitBits, bits - b0)) - 1;
+        unsigned c[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < kSortItems; ++j) {
+            const int bk = (digit_of(k[j], shift) >> b0) & mask;
+            const unsigned one = 1u << (16 * (bk & 1));
+#pragma unroll
+            for (int w = 0; w < 4; ++w) c[w] += (bk >> 1) == w ? one : 0u;
+        }
+        // (the scan's barriers also order the previous split's LDS reads
+        // before the stores below)
+        unsigned tot[4], r[4];
+        block_scan4(c, wave_sums4, r, tot);  // r: inclusive prefix per word
+        // bucket bases: exclusive scan of the eight totals
+        unsigned base = 0, packed[4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const unsigned lo = tot[w] & 0xffffu, hi = tot[w] >> 16;
+            packed[w] = base | ((base + lo) << 16);
+            base += lo + hi;
+        }
+#pragma unroll
+        for (int w = 0; w < 4; ++w) r[w] = packed[w] + (r[w] - c[w]);
+#pragma unroll
+        for (int j = 0; j < kSortItems; ++j) {
+            const int bk = (digit_of(k[j], shift) >> b0) & mask, sh = 16 * (bk & 1), wd = bk >> 1;
+            unsigned word = r[0];
+#pragma unroll
+            for (int w = 1; w < 4; ++w) word = wd == w ? r[w] : word;
+            const int pos = (int)((word >> sh) & 0xffffu);
+#pragma unroll
+            for (int w = 0; w < 4; ++w) r[w] += wd == w ? 1u << sh : 0u;
+            K[sort_slot(pos)] = k[j];
+            V[sort_slot(pos)] = v[j];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < kSortItems; ++j) {
+            k[j] = K[sort_slot(t * kSortItems + j)];
+            v[j] = V[sort_slot(t * kSortItems + j)];
+        }
+    }
+    // K / V hold the tile sorted by digit.  Each digit's first tile position,
+    // then every real pair to its output slot (consecutive threads take
+    // consecutive positions, so a digit's run is stored contiguously).
+#pragma unroll
+    for (int j = 0; j < kSortItems; ++j) {
+        const int p = j * kSortThreads + t;
+        const int d = digit_of(K[sort_slot(p)], shift);
+        if (p < valid && (p == 0 || digit_of(K[sort_slot(p - 1)], shift) != d)) start[d] = p;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kSortItems; ++j) {
+        const int p = j * kSortThreads + t;
+        if (p >= valid) continue;
+        const int key = K[sort_slot(p)], d = digit_of(key, shift);
+        const int dst = first[d] + (p - start[d]);
+        if ((unsigned)dst >= (unsigned)n) continue;  // unreachable for a sorted tile
+        keys_out[dst] = key;
+        vals_out[dst] = V[sort_slot(p)];
+    }
+}
+
+// Plan keys, one workgroup of kKeyThreads per sort tile, with the tile's
+// count of each first-pass digit (the sort's first count pass, fused).
+constexpr int kKeyThreads = 1024, kKeyItems = kSortTile / kKeyThreads;
+template <class KeyOf>
+__device__ __forceinline__ void keys_tile(const KeyOf &key_of, int *__restrict__ keys, int samples,
+                                          int tiles, int *__restrict__ counts, int *hist) {
+    for (int d = threadIdx.x; d < kDigits; d += kKeyThreads) hist[d] = 0;
+    __syncthreads();
+    const int base = blockIdx.x * kSortTile;
+    int key[kKeyItems];
+#pragma unroll
+    for (int j = 0; j < kKeyItems; ++j) {
+        const int i = base + j * kKeyThreads + (int)threadIdx.x;
+        key[j] = i < samples ? key_of(i) : 0;
+    }
+#pragma unroll
+    for (int j = 0; j < kKeyItems; ++j) {
+        const int i = base + j * kKeyThreads + (int)threadIdx.x;
+        if (i < samples) {
+            keys[i] = key[j];
+            atomicAdd(&hist[digit_of(key[j], 0)], 1);
+        }
+    }
+    __syncthreads();
+    for (int d = threadIdx.x; d < kDigits; d += kKeyThreads)
+        counts[(size_t)d * tiles + blockIdx.x] = hist[d];
+}
+
+__global__ __launch_bounds__(kKeyThreads) void geometry_keys_kernel(
+    const float *__restrict__ geometry, int *__restrict__ keys, int samples, int per_batch,
+    int cells, Grid g, int invalid, int tiles, int *__restrict__ counts) {
+    __shared__ int hist[kDigits];
+    keys_tile([&](int s) {
+        const float p[3] = {geometry[3 * (size_t)s], geometry[3 * (size_t)s + 1],
+                            geometry[3 * (size_t)s + 2]};
+        const int r = point_rank(p, g);
+        return r < 0 ? invalid : r + (s / per_batch) * cells;
+    }, keys, samples, tiles, counts, hist);
+}
+
+// The calibration of the first kStageCams cameras the tile touches is read
+// from LDS (a tile spans two cameras at production sizes); any further ones
+// from global memory.
+constexpr int kStageCams = 8;
+__global__ __launch_bounds__(kKeyThreads) void calibration_keys_kernel(
+    const float *__restrict__ frustum, const float *__restrict__ calib, int *__restrict__ keys,
+    int samples, int cams, int depth_hw, int cams_per_batch, int cells, Grid g, int invalid,
+    int tiles, int *__restrict__ counts) {
+    __shared__ int hist[kDigits];
+    __shared__ float stage[kStageCams * kCalib];
+    const int cam0 = blockIdx.x * kSortTile / depth_hw, staged = min(kStageCams, cams - cam0);
+    for (int i = threadIdx.x; i < staged * kCalib; i += kKeyThreads)
+        stage[i] = calib[(size_t)cam0 * kCalib + i];
+    // (keys_tile's first barrier publishes the stage)
+    keys_tile([&](int s) {
+        const int cam = s / depth_hw;
+        const float *o = cam - cam0 < staged ? stage + (cam - cam0) * kCalib
+                                             : calib + (size_t)cam * kCalib;
+        return calibration_key(frustum, o, s - cam * depth_hw, cam, cams_per_batch, cells, g,
+                               invalid);
+    }, keys, samples, tiles, counts, hist);
 }
 
 // Pool schedule.  The BEV output is cut into tiles of kTileCells consecutive
@@ -289,9 +575,13 @@ constexpr int kScheduleThreads = 1024;
 
 // One workgroup: per tile, slice count; exclusive scans give each tile's
 // first work item and its index among multi-slice tiles.  sched layout:
-// slices[tiles], slice_base[tiles + 1], multi_base[tiles + 1].
+// slices[tiles], slice_base[tiles + 1], multi_base[tiles + 1].  Work list:
+// item slice_base[t] + k = (tile t, slice k); multi-slice tiles listed in
+// tile order.
 __global__ __launch_bounds__(kScheduleThreads) void schedule_kernel(const int *__restrict__ starts,
                                                                    int *__restrict__ sched,
+                                                                   int2 *__restrict__ work,
+                                                                   int *__restrict__ multi,
                                                                    int tiles, int tiles_per_batch,
                                                                    int cells) {
     __shared__ int part[2][kScheduleThreads];
@@ -323,6 +613,8 @@ __global__ __launch_bounds__(kScheduleThreads) void schedule_kernel(const int *_
         const int ns = slices[i];
         slice_base[i] = run[0];
         multi_base[i] = run[1];
+        for (int k = 0; k < ns; ++k) work[run[0] + k] = make_int2(i, k);
+        if (ns > 1) multi[run[1]] = i;
         run[0] += ns;
         run[1] += ns > 1;
     }
@@ -330,19 +622,6 @@ __global__ __launch_bounds__(kScheduleThreads) void schedule_kernel(const int *_
         slice_base[tiles] = part[0][t];
         multi_base[tiles] = part[1][t];
     }
-}
-
-// Work list: item slice_base[t] + k = (tile t, slice k); multi-slice tiles
-// listed in tile order.
-__global__ __launch_bounds__(256) void work_list_kernel(const int *__restrict__ sched,
-                                                       int2 *__restrict__ work,
-                                                       int *__restrict__ multi, int tiles) {
-    const int t = blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= tiles) return;
-    const int *slices = sched, *slice_base = sched + tiles, *multi_base = slice_base + tiles + 1;
-    const int ns = slices[t];
-    for (int k = 0; k < ns; ++k) work[slice_base[t] + k] = make_int2(t, k);
-    if (ns > 1) multi[multi_base[t]] = t;
 }
 
 // Entry bound k of a tile's ns slices: whole quads of [start, end).
@@ -719,6 +998,13 @@ __global__ __launch_bounds__(64) void lift_pool_atomic_kernel(
 
 inline unsigned blocks_for(size_t n, int per = 256) { return (unsigned)((n + per - 1) / per); }
 
+// Scratch of the pair sort: the ping-pong keys and samples, the per-tile
+// digit counts and offsets, the digit totals.
+size_t sort_tmp_bytes(size_t n) {
+    const size_t tiles = (n + kSortTile - 1) / kSortTile;
+    return (2 * n + 2 * (size_t)kDigits * tiles + kDigits) * sizeof(int);
+}
+
 int fail_contract(char *error, size_t cap, const char *what) { return fail(error, cap, "%s", what); }
 
 int stateless_pool(const float *logits, const float *ctx, const float *geometry, const int *ranks,
@@ -782,7 +1068,7 @@ extern "C" int bf_cuda_lss_geometry_to_ranks_f32(const float *geometry, int *ran
     if (!sizes_of(d, &z)) return fail(error, cap, "HIP LSS rank size overflow");
     hipLaunchKernelGGL(geometry_rank_kernel, dim3(blocks_for(z.samples)), dim3(256), 0,
                        reinterpret_cast<hipStream_t>(stream), geometry, ranks, (int)z.samples,
-                       (int)(z.samples / d->batches), (int)z.cells, grid_of(d), 0, -1);
+                       grid_of(d));
     return launch_ok(error, cap, "HIP LSS rank launch");
 }
 
@@ -820,20 +1106,16 @@ extern "C" int bf_cuda_lss_plan_create(const bf_lss_desc *d, bf_cuda_lss_plan **
         bf_cuda_lss_plan_destroy(p);
         return fail(error, cap, "HIP LSS plan size overflow");
     }
-    size_t sort_bytes = 0, scan_bytes = 0;
+    size_t scan_bytes = 0;
     const auto padded = rocprim::make_transform_iterator(rocprim::counting_iterator<int>(0),
                                                          PaddedCount{nullptr});
-    if (!hip_ok(rocprim::radix_sort_pairs(nullptr, sort_bytes, (const unsigned *)nullptr,
-                                          (unsigned *)nullptr, rocprim::counting_iterator<int>(0),
-                                          (int *)nullptr, (unsigned)z.samples, 0u, p->end_bit),
-                error, cap, "size HIP LSS plan sort") ||
-        !hip_ok(rocprim::exclusive_scan(nullptr, scan_bytes, padded, (int *)nullptr, 0,
+    if (!hip_ok(rocprim::exclusive_scan(nullptr, scan_bytes, padded, (int *)nullptr, 0,
                                         z.cell_count + 1, rocprim::plus<int>()),
                 error, cap, "size HIP LSS plan scan")) {
         bf_cuda_lss_plan_destroy(p);
         return 0;
     }
-    p->tmp_bytes = std::max(sort_bytes, scan_bytes);
+    p->tmp_bytes = std::max(sort_tmp_bytes(z.samples), scan_bytes);
     p->tiles_per_batch = (int)((z.cells + kTileCells - 1) / kTileCells);
     p->tiles = p->tiles_per_batch * (int)d->batches;
     p->max_multi = (int)std::max<size_t>(1, (p->list_capacity + kSliceEntries - 1) / kSliceEntries);
@@ -896,6 +1178,50 @@ extern "C" size_t bf_cuda_lss_plan_resident_bytes(const bf_cuda_lss_plan *plan) 
 
 namespace {
 
+// The pair sort's scratch in the plan's tmp region.
+struct SortScratch {
+    int tiles;
+    int *alt_k, *alt_v;   // ping-pong pairs
+    int *counts, *offs;   // [digit][tile]
+    int *totals;          // [digit]
+};
+SortScratch sort_scratch(const bf_cuda_lss_plan *p) {
+    SortScratch w;
+    const int n = (int)p->z.samples;
+    w.tiles = (n + kSortTile - 1) / kSortTile;
+    w.alt_k = reinterpret_cast<int *>(p->tmp);
+    w.alt_v = w.alt_k + n;
+    w.counts = w.alt_v + n;
+    w.offs = w.counts + (size_t)kDigits * w.tiles;
+    w.totals = w.offs + (size_t)kDigits * w.tiles;
+    return w;
+}
+
+// The stable sort of (plan->keys, sample index) into sorted_keys / order:
+// ceil(end_bit / kDigitBits) digit passes, ping-ponging through the plan's
+// scratch so that the last pass writes the outputs.  The key kernels leave
+// the first pass's digit counts.
+void sort_pairs(bf_cuda_lss_plan *p, hipStream_t s) {
+    const int n = (int)p->z.samples;
+    const SortScratch w = sort_scratch(p);
+    const int passes = ((int)p->end_bit + kDigitBits - 1) / kDigitBits;
+    const int *in_k = p->keys, *in_v = nullptr;
+    for (int q = 0; q < passes; ++q) {
+        const bool last = (passes - 1 - q) % 2 == 0;
+        int *out_k = last ? p->sorted_keys : w.alt_k, *out_v = last ? p->order : w.alt_v;
+        const int shift = q * kDigitBits, bits = std::min(kDigitBits, (int)p->end_bit - shift);
+        if (q > 0)
+            hipLaunchKernelGGL(digit_count_kernel, dim3(w.tiles), dim3(kSortThreads), 0, s, in_k,
+                               n, shift, w.tiles, w.counts);
+        hipLaunchKernelGGL(digit_offsets_kernel, dim3(kDigits), dim3(kSortThreads), 0, s,
+                           w.counts, w.tiles, w.offs, w.totals);
+        hipLaunchKernelGGL(digit_scatter_kernel, dim3(w.tiles), dim3(kSortThreads), 0, s, in_k,
+                           in_v, n, shift, bits, w.tiles, w.offs, w.totals, out_k, out_v);
+        in_k = out_k;
+        in_v = out_v;
+    }
+}
+
 // Cell lists from the keys in plan->keys: the stable sort of (key, sample)
 // pairs orders every cell's samples by sample index (out-of-grid samples sort
 // after the last cell); a lower bound per cell locates each cell's run; runs
@@ -905,13 +1231,7 @@ int build_lists(bf_cuda_lss_plan *p, hipStream_t s, char *error, size_t cap) {
     const bf_lss_desc *d = &p->desc;
     const int n = (int)p->z.samples, cell_count = (int)p->z.cell_count;
     const int hw = (int)(d->feature_height * d->feature_width);
-    if (!hip_ok(rocprim::radix_sort_pairs(p->tmp, p->tmp_bytes,
-                                          reinterpret_cast<const unsigned *>(p->keys),
-                                          reinterpret_cast<unsigned *>(p->sorted_keys),
-                                          rocprim::counting_iterator<int>(0), p->order,
-                                          (unsigned)n, 0u, p->end_bit, s),
-                error, cap, "HIP LSS plan sort"))
-        return 0;
+    sort_pairs(p, s);
     hipLaunchKernelGGL(cell_starts_kernel, dim3(blocks_for((size_t)cell_count + 1)), dim3(256), 0, s,
                        p->sorted_keys, n, p->starts, cell_count);
     // padded counts of cells [0, cell_count) and 0 for the end marker
@@ -925,12 +1245,8 @@ int build_lists(bf_cuda_lss_plan *p, hipStream_t s, char *error, size_t cap) {
     hipLaunchKernelGGL(list_entries_kernel, dim3(blocks_for(n)), dim3(256), 0, s, p->order,
                        p->sorted_keys, p->starts, p->padded_starts, p->list, n, cell_count,
                        (int)d->depth_bins * hw, hw);
-    hipLaunchKernelGGL(list_padding_kernel, dim3(blocks_for(cell_count)), dim3(256), 0, s,
-                       p->starts, p->padded_starts, p->list, cell_count);
     hipLaunchKernelGGL(schedule_kernel, dim3(1), dim3(kScheduleThreads), 0, s, p->padded_starts,
-                       p->sched, p->tiles, p->tiles_per_batch, (int)p->z.cells);
-    hipLaunchKernelGGL(work_list_kernel, dim3(blocks_for(p->tiles)), dim3(256), 0, s, p->sched,
-                       p->work, p->multi, p->tiles);
+                       p->sched, p->work, p->multi, p->tiles, p->tiles_per_batch, (int)p->z.cells);
     if (!launch_ok(error, cap, "HIP LSS plan list build")) return 0;
     p->prepared = 1;
     return 1;
@@ -945,10 +1261,10 @@ extern "C" int bf_cuda_lss_plan_prepare_geometry_f32(bf_cuda_lss_plan *plan,
     const bf_lss_desc *d = &plan->desc;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     plan->prepared = 0;
-    hipLaunchKernelGGL(geometry_rank_kernel, dim3(blocks_for(plan->z.samples)), dim3(256), 0, s,
-                       geometry, plan->keys, (int)plan->z.samples,
-                       (int)(plan->z.samples / d->batches), (int)plan->z.cells, grid_of(d), 1,
-                       (int)plan->z.cell_count);
+    const SortScratch w = sort_scratch(plan);
+    hipLaunchKernelGGL(geometry_keys_kernel, dim3(w.tiles), dim3(kKeyThreads), 0, s, geometry,
+                       plan->keys, (int)plan->z.samples, (int)(plan->z.samples / d->batches),
+                       (int)plan->z.cells, grid_of(d), (int)plan->z.cell_count, w.tiles, w.counts);
     if (!launch_ok(error, cap, "HIP LSS plan rank launch")) return 0;
     return build_lists(plan, s, error, cap);
 }
@@ -970,9 +1286,11 @@ extern "C" int bf_cuda_lss_plan_prepare_calibration_f32(
                        post_translation, extra_rotation, extra_translation, plan->calib,
                        (int)d->cameras, cams);
     const int depth_hw = (int)(d->depth_bins * d->feature_height * d->feature_width);
-    hipLaunchKernelGGL(calibration_rank_kernel, dim3(blocks_for(plan->z.samples)), dim3(256), 0, s,
-                       frustum, plan->calib, plan->keys, (int)plan->z.samples, depth_hw,
-                       (int)d->cameras, (int)plan->z.cells, grid_of(d), (int)plan->z.cell_count);
+    const SortScratch w = sort_scratch(plan);
+    hipLaunchKernelGGL(calibration_keys_kernel, dim3(w.tiles), dim3(kKeyThreads), 0, s, frustum,
+                       plan->calib, plan->keys, (int)plan->z.samples, cams, depth_hw,
+                       (int)d->cameras, (int)plan->z.cells, grid_of(d), (int)plan->z.cell_count,
+                       w.tiles, w.counts);
     if (!launch_ok(error, cap, "HIP LSS calibration rank launch")) return 0;
     return build_lists(plan, s, error, cap);
 }
