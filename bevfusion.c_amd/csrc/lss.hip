@@ -25,9 +25,6 @@
 #include "bf_cuda.h"
 #include "hip_common.h"
 
-#include <rocprim/device/device_scan.hpp>
-#include <rocprim/iterator/counting_iterator.hpp>
-#include <rocprim/iterator/transform_iterator.hpp>
 
 #include <algorithm>
 #include <cfloat>
@@ -215,32 +212,99 @@ __global__ __launch_bounds__(256) void fill_float_kernel(float *p, int n) {
 
 // starts[c] = first sorted position whose key is >= c (c in [0, cell_count]):
 // a lower bound over the sorted keys, so empty cells get empty runs.
-__global__ __launch_bounds__(256) void cell_starts_kernel(const int *__restrict__ sorted_keys,
-                                                         int samples, int *__restrict__ starts,
-                                                         int cell_count) {
-    const int c = blockIdx.x * blockDim.x + threadIdx.x;
-    if (c > cell_count) return;
+// Padded cell lists.  Every cell's run is padded to a multiple of 4 entries
+// (kQuad) so that cell boundaries fall on quad boundaries; padding entries
+// carry sample -1 (weight 0 on an all-zero context row).
+constexpr int kQuad = 4;
+constexpr int kStartThreads = 256;
+
+__device__ __forceinline__ int lower_bound_key(const int *__restrict__ sorted_keys, int samples,
+                                               int c) {
     int lo = 0, hi = samples;
     while (lo < hi) {
         const int mid = (lo + hi) >> 1;
         if (sorted_keys[mid] < c) lo = mid + 1;
         else hi = mid;
     }
-    starts[c] = lo;
+    return lo;
 }
 
-// Padded cell lists.  Every cell's run is padded to a multiple of 4 entries
-// (kQuad) so that cell boundaries fall on quad boundaries; padding entries
-// carry sample -1 (weight 0 on an all-zero context row).
-constexpr int kQuad = 4;
-
-struct PaddedCount {
-    const int *starts;
-    __host__ __device__ int operator()(int c) const {
-        const int n = starts[c + 1] - starts[c];
-        return (n + kQuad - 1) & ~(kQuad - 1);
+// Run start of every cell c <= cell_count (the last is the end of the valid
+// samples) by lower bound in the sorted keys, and per workgroup of
+// kStartThreads cells the sum of their padded run lengths.
+__global__ __launch_bounds__(kStartThreads) void cell_starts_kernel(const int *__restrict__ sorted_keys,
+                                                                   int samples,
+                                                                   int *__restrict__ starts,
+                                                                   int *__restrict__ block_sums,
+                                                                   int cell_count) {
+    __shared__ int s_start[kStartThreads + 1];
+    __shared__ int wave_sums[kStartThreads / kWave];
+    const int c0 = blockIdx.x * kStartThreads, t = threadIdx.x, c = c0 + t;
+    const int st = lower_bound_key(sorted_keys, samples, min(c, cell_count));
+    if (c <= cell_count) starts[c] = st;
+    s_start[t] = st;
+    if (t == kStartThreads - 1)
+        s_start[kStartThreads] = lower_bound_key(sorted_keys, samples, min(c + 1, cell_count));
+    __syncthreads();
+    const int len = c < cell_count ? s_start[t + 1] - s_start[t] : 0;
+    int v = (len + kQuad - 1) & ~(kQuad - 1);
+    const int lane = t & (kWave - 1), wave = t / kWave;
+#pragma unroll
+    for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    if (lane == 0) wave_sums[wave] = v;
+    __syncthreads();
+    if (t == 0) {
+        int sum = 0;
+#pragma unroll
+        for (int w = 0; w < kStartThreads / kWave; ++w) sum += wave_sums[w];
+        block_sums[blockIdx.x] = sum;
     }
-};
+}
+
+// Exclusive scan of the block sums in place (one workgroup).
+__global__ __launch_bounds__(1024) void block_sums_scan_kernel(int *__restrict__ block_sums,
+                                                               int blocks) {
+    __shared__ int part[1024];
+    int carry = 0;
+    for (int b0 = 0; b0 < blocks; b0 += 1024) {
+        const int b = b0 + (int)threadIdx.x;
+        const int v = b < blocks ? block_sums[b] : 0;
+        part[threadIdx.x] = v;
+        __syncthreads();
+        for (int off = 1; off < 1024; off <<= 1) {
+            const int u = threadIdx.x >= (unsigned)off ? part[threadIdx.x - off] : 0;
+            __syncthreads();
+            part[threadIdx.x] += u;
+            __syncthreads();
+        }
+        if (b < blocks) block_sums[b] = carry + part[threadIdx.x] - v;
+        carry += part[1023];
+        __syncthreads();
+    }
+}
+
+// padded_starts[c] = sum of the padded run lengths of the cells before c.
+__global__ __launch_bounds__(kStartThreads) void padded_starts_kernel(
+    const int *__restrict__ starts, const int *__restrict__ block_prefix,
+    int *__restrict__ padded_starts, int cell_count) {
+    __shared__ int wave_sums[kStartThreads / kWave];
+    const int c = blockIdx.x * kStartThreads + threadIdx.x;
+    const int len = c < cell_count ? starts[c + 1] - starts[c] : 0;
+    const int v = (len + kQuad - 1) & ~(kQuad - 1);
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    int incl = v;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+        const int u = __shfl_up(incl, o);
+        if (lane >= o) incl += u;
+    }
+    if (lane == kWave - 1) wave_sums[wave] = incl;
+    __syncthreads();
+    int before = block_prefix[blockIdx.x];
+#pragma unroll
+    for (int w = 0; w < kStartThreads / kWave; ++w) before += w < wave ? wave_sums[w] : 0;
+    if (c <= cell_count) padded_starts[c] = before + incl - v;
+}
 
 // Sorted position i of a valid sample -> its padded slot: {pixel, sample};
 // the last sample of a cell also writes the cell's padding entries.
@@ -1036,7 +1100,7 @@ struct bf_cuda_lss_plan {
     int2 *list, *work;
     float2 *stats;
     float *rows, *calib, *scratch;
-    void *tmp;  // rocPRIM sort / scan scratch
+    void *tmp;  // pair-sort scratch, then the padded-start block sums
     size_t tmp_bytes;
     void *arena;
     size_t resident_bytes;
@@ -1106,16 +1170,9 @@ extern "C" int bf_cuda_lss_plan_create(const bf_lss_desc *d, bf_cuda_lss_plan **
         bf_cuda_lss_plan_destroy(p);
         return fail(error, cap, "HIP LSS plan size overflow");
     }
-    size_t scan_bytes = 0;
-    const auto padded = rocprim::make_transform_iterator(rocprim::counting_iterator<int>(0),
-                                                         PaddedCount{nullptr});
-    if (!hip_ok(rocprim::exclusive_scan(nullptr, scan_bytes, padded, (int *)nullptr, 0,
-                                        z.cell_count + 1, rocprim::plus<int>()),
-                error, cap, "size HIP LSS plan scan")) {
-        bf_cuda_lss_plan_destroy(p);
-        return 0;
-    }
-    p->tmp_bytes = std::max(sort_tmp_bytes(z.samples), scan_bytes);
+    // the sort's scratch, then (reused) the block sums of the padded starts
+    const size_t start_blocks = (z.cell_count + kStartThreads) / kStartThreads;
+    p->tmp_bytes = std::max(sort_tmp_bytes(z.samples), start_blocks * sizeof(int));
     p->tiles_per_batch = (int)((z.cells + kTileCells - 1) / kTileCells);
     p->tiles = p->tiles_per_batch * (int)d->batches;
     p->max_multi = (int)std::max<size_t>(1, (p->list_capacity + kSliceEntries - 1) / kSliceEntries);
@@ -1129,7 +1186,7 @@ extern "C" int bf_cuda_lss_plan_create(const bf_lss_desc *d, bf_cuda_lss_plan **
     // keys + sorted keys, order [samples]; starts, padded starts [cells + 1];
     // padded list; softmax stats [pixels]; context rows + one zero row;
     // calibration; schedule; work list; multi-slice tiles; partial rows;
-    // rocPRIM scratch.
+    // sort / scan scratch.
     const size_t scratch_floats = (size_t)2 * p->max_work * d->channels;
     const size_t parts[13] = {z.samples * 8, z.samples * 4, (z.cell_count + 1) * 4,
                               (z.cell_count + 1) * 4, p->list_capacity * 8, z.pixels * 8,
@@ -1232,16 +1289,16 @@ int build_lists(bf_cuda_lss_plan *p, hipStream_t s, char *error, size_t cap) {
     const int n = (int)p->z.samples, cell_count = (int)p->z.cell_count;
     const int hw = (int)(d->feature_height * d->feature_width);
     sort_pairs(p, s);
-    hipLaunchKernelGGL(cell_starts_kernel, dim3(blocks_for((size_t)cell_count + 1)), dim3(256), 0, s,
-                       p->sorted_keys, n, p->starts, cell_count);
-    // padded counts of cells [0, cell_count) and 0 for the end marker
-    const auto padded = rocprim::make_transform_iterator(rocprim::counting_iterator<int>(0),
-                                                         PaddedCount{p->starts});
-    if (!launch_ok(error, cap, "HIP LSS plan starts") ||
-        !hip_ok(rocprim::exclusive_scan(p->tmp, p->tmp_bytes, padded, p->padded_starts, 0,
-                                        (size_t)cell_count + 1, rocprim::plus<int>(), s),
-                error, cap, "HIP LSS plan scan"))
-        return 0;
+    // run starts, then the padded starts: per-block sums, their scan, and
+    // each block's scan on top
+    const int start_blocks = cell_count / kStartThreads + 1;  // cells 0..cell_count
+    int *block_sums = reinterpret_cast<int *>(p->tmp);
+    hipLaunchKernelGGL(cell_starts_kernel, dim3(start_blocks), dim3(kStartThreads), 0, s,
+                       p->sorted_keys, n, p->starts, block_sums, cell_count);
+    hipLaunchKernelGGL(block_sums_scan_kernel, dim3(1), dim3(1024), 0, s, block_sums,
+                       start_blocks);
+    hipLaunchKernelGGL(padded_starts_kernel, dim3(start_blocks), dim3(kStartThreads), 0, s,
+                       p->starts, block_sums, p->padded_starts, cell_count);
     hipLaunchKernelGGL(list_entries_kernel, dim3(blocks_for(n)), dim3(256), 0, s, p->order,
                        p->sorted_keys, p->starts, p->padded_starts, p->list, n, cell_count,
                        (int)d->depth_bins * hw, hw);

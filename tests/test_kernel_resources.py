@@ -2,13 +2,12 @@
 compiler's kernel-resource-usage remarks that build() records in
 bevfusion.c_amd/_build/kernel_resources.json.
 
-Every kernel written for this library runs without scratch memory and without
-vector-register spills (SGPR spills go to VGPR lanes, not memory): a kernel that uses scratch pays for it on every dispatch (a
-by-value struct kernel argument read through a reference was once copied to
-scratch and cost about 20 us per camera frame over the frame's GEMMs).  Only
-rocPRIM's radix-sort kernels (a library dependency of the LSS plan) may use
-scratch.  The GEMM cores and the fused Swin kernels also keep their LDS
-within the 160 KiB of a CU.
+Every kernel of the library runs without scratch memory and without
+vector-register spills (SGPR spills go to VGPR lanes, not memory): a kernel
+that uses scratch pays for it on every dispatch (a by-value struct kernel
+argument read through a reference was once copied to scratch and cost about
+20 us per camera frame over the frame's GEMMs).  The GEMM cores and the fused
+Swin kernels also keep their LDS within the 160 KiB of a CU.
 """
 
 import json
@@ -29,14 +28,14 @@ def report():
 
 def test_every_source_reports_its_kernels(report):
     assert {"swin.hip", "camera.hip", "ops.hip", "bev.hip", "lss.hip"} <= set(report)
-    assert sum(len(v) for v in report.values()) > 300
+    assert sum(len(v) for v in report.values()) > 200
     gemm = [k for v in report.values() for k in v if "gemm_" in k]
     assert len(gemm) > 60
 
 
-def test_no_scratch_or_vgpr_spills_outside_rocprim(report):
+def test_no_scratch_or_vgpr_spills(report):
     bad = [(src, name, r) for src, kernels in report.items() for name, r in kernels.items()
-           if (r.get("scratch", 0) or r.get("vgpr_spill", 0)) and "rocprim" not in name]
+           if r.get("scratch", 0) or r.get("vgpr_spill", 0)]
     assert not bad, bad[:5]
 
 
