@@ -42,30 +42,53 @@ enum {
     kConvs
 };
 
-// ConvTranspose2d 2x2 stride 2 as a GEMM over input pixels: column
-// n = (dy * 2 + dx) * Co + co of input pixel (y, x) is output pixel
-// (2y + dy, 2x + dx), channel co.  BN-folded bias + ReLU; stores NHWC fp16
-// and NCHW fp32.
+// ConvTranspose2d 2x2 stride 2 as a GEMM over input pixels m = y * IW + x:
+// column n = (dy * Co + co) * 2 + dx is output pixel (2y + dy, 2x + dx),
+// channel co, so a tile's column pair (dx = 0, 1) holds two adjacent outputs.
+// BN-folded bias + ReLU (passing NaN).  The staged tile is stored as NCHW
+// fp32 runs (one float2 per input pixel and channel, consecutive threads on
+// consecutive pixels) and NHWC fp16 rows (eight channels of one output pixel
+// per 16-byte store).
 struct EpiDeconv2x2 {
-    static constexpr bool kRowVector = false;
+    static constexpr bool kRowVector = true;
+    static constexpr bool kFullRow = true;
     bf16 *nhwc;
     float *nchw;
     const float *bias;
     int M, IW, Co, OW, ohw;
-    __device__ void operator()(int row, int col, f32x4 v) const {
-        if (col >= 4 * Co) return;
-        const int tap = col / Co, co = col - tap * Co, dy = tap >> 1, dx = tap & 1;
-        const float b = bias[co];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int m = row + r;
-            if (m >= M) break;
-            const int y = m / IW, x = m - y * IW;
+    template <class T>
+    __device__ void tile(float *sC, int stride, int m0, int n0, int tid) const {
+        static_assert(T::BN % 16 == 0, "whole chunks of eight column pairs");
+        constexpr int kPairs = T::BN / 2, kChunks = kPairs / 8;
+        for (int item = tid; item < kPairs * T::BM; item += T::kThreads) {
+            const int j = item / T::BM, r = item - j * T::BM, m = m0 + r, n = n0 + 2 * j;
+            if (m >= M || n >= 4 * Co) continue;
+            const int dy = (n >> 1) / Co, co = (n >> 1) - dy * Co, y = m / IW, x = m - y * IW;
+            const float b = bias[co];
+            const float y0 = sC[r * stride + 2 * j] + b, y1 = sC[r * stride + 2 * j + 1] + b;
+            const float v0 = y0 < 0.0f ? 0.0f : y0, v1 = y1 < 0.0f ? 0.0f : y1;
+            float *dst = nchw + (size_t)co * ohw + (size_t)(2 * y + dy) * OW + 2 * x;
+            if (((uintptr_t)dst & 7) == 0) {
+                *reinterpret_cast<float2 *>(dst) = make_float2(v0, v1);
+            } else {
+                dst[0] = v0;
+                dst[1] = v1;
+            }
+        }
+        for (int item = tid; item < T::BM * 2 * kChunks; item += T::kThreads) {
+            const int r = item / (2 * kChunks), rest = item - r * (2 * kChunks);
+            const int dx = rest / kChunks, ch = rest - dx * kChunks, m = m0 + r;
+            const int n = n0 + 16 * ch;  // the chunk's first column (Co % 8 == 0: one dy)
+            if (m >= M || n >= 4 * Co) continue;
+            const int dy = (n >> 1) / Co, co = (n >> 1) - dy * Co, y = m / IW, x = m - y * IW;
             const int p = (2 * y + dy) * OW + 2 * x + dx;
-            float val = v[r] + b;
-            val = val < 0.0f ? 0.0f : val;
-            nhwc[(size_t)p * Co + co] = to_word(val, true);
-            nchw[(size_t)co * ohw + p] = val;
+            bf16x8 o;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float y = sC[r * stride + 16 * ch + 2 * e + dx] + bias[co + e];
+                o[e] = to_word(y < 0.0f ? 0.0f : y, true);
+            }
+            *reinterpret_cast<bf16x8 *>(nhwc + (size_t)p * Co + co) = o;
         }
     }
 };
@@ -101,7 +124,7 @@ struct bf_cuda_bev_stage {
     size_t h, w, resident_bytes;
     unsigned char *params, *acts;
     ConvLayer L[kConvs];
-    const bf16 *deconv_w;  // [4 * 256][256]: row (dy * 2 + dx) * 256 + co, column ci
+    const bf16 *deconv_w;  // [4 * 256][256]: row (dy * 256 + co) * 2 + dx, column ci
     const float *deconv_b;
     // Channels-last fp16 maps: packed input (336 in rows of 384), ping-pong (<= 256),
     // deblock outputs (256 each, read together by the shared conv), shared.
@@ -111,7 +134,7 @@ struct bf_cuda_bev_stage {
 namespace {
 
 // Folds the transposed deblock's BN into its [in][out][2][2] weights and
-// stores them as the GEMM's [tap * Co + co][ci] operand.
+// stores them as the GEMM's [(dy * Co + co) * 2 + dx][ci] operand.
 int fold_deconv(const bf_model *m, std::vector<float> &w, std::vector<float> &b, char *error,
                 size_t cap) {
     const float *src = bind_f32(m, "backbone_2d.deblocks.1.0.weight", {256u, 256u, 2u, 2u},
@@ -130,8 +153,9 @@ int fold_deconv(const bf_model *m, std::vector<float> &w, std::vector<float> &b,
         const float f = p[0][co] / std::sqrt(p[3][co] + kBevBnEps);
         b[co] = (0.0f - p[2][co]) * f + p[1][co];
         for (int ci = 0; ci < 256; ++ci)
-            for (int t = 0; t < 4; ++t)
-                w[((size_t)t * 256 + co) * 256 + ci] = src[((size_t)ci * 256 + co) * 4 + t] * f;
+            for (int t = 0; t < 4; ++t)  // t = dy * 2 + dx
+                w[(((size_t)(t >> 1) * 256 + co) * 2 + (t & 1)) * 256 + ci] =
+                    src[((size_t)ci * 256 + co) * 4 + t] * f;
     }
     return 1;
 }
