@@ -226,6 +226,34 @@ def test_plan_dense_cells_bit_exact(channels, cells, device):
     assert np.array_equal(bfhip.lss_lift_pool(logits, ctx, geo, bd).cpu().numpy(), want)
 
 
+@pytest.mark.parametrize("cells,batches", [((600, 600, 1), 1), ((400, 360, 2), 2)])
+def test_plan_keys_of_three_digit_passes(cells, batches, device):
+    """Grids whose keys need more than 18 bits take three 9-bit passes of the
+    pair sort (360 000 and 576 000 cells, keys up to 2^19 / 2^20): the plan
+    must still list every cell's samples in sample order, so the integer
+    sums of the exact inputs equal the oracle bit for bit, and the general
+    inputs meet the tolerance."""
+    sc = lss_scene.rig(seed=9, height=8, width=22, depth_bins=60, channels=8)
+    if batches == 2:
+        b = lss_scene.rig(seed=10, height=8, width=22, depth_bins=60, channels=8)
+        b["extra_rotation"] = lss_scene._rot_z(0.7).reshape(1, 3, 3)
+        sc = dict(sc, **{k: np.concatenate([sc[k], b[k]]) for k in
+                         ("depth_logits", "context", *lss_scene.CALIBRATION_KEYS)})
+    sc["desc"] = dict(sc["desc"], batches=batches, minimum=(-60.0, -60.0, -5.0),
+                      step=(120.0 / cells[0], 120.0 / cells[1], 10.0 / cells[2]), cells=cells)
+    bd, od = _descs(sc["desc"])
+    g = _frustum_geometry(sc)
+    assert batches * cells[0] * cells[1] * cells[2] > 1 << 18
+    with bfhip.LssPlan(bd) as plan:
+        plan.prepare_geometry(_dev(g, device))
+        got = plan.forward(_dev(sc["depth_logits"], device), _dev(sc["context"], device))
+        _check(got.cpu().numpy(), sc["depth_logits"], sc["context"], g, od,
+               f"lss plan {cells} x {batches}")
+        logits_h, ctx_h = _exact_inputs(sc, 3)
+        exact = plan.forward(_dev(logits_h, device), _dev(ctx_h, device)).cpu().numpy()
+    assert np.array_equal(exact, ORACLE.lss_lift_pool(logits_h, ctx_h, g, od))
+
+
 def test_all_samples_outside_or_non_finite(device):
     sc = SCENES["compact"]
     bd, od = _descs(sc["desc"])
