@@ -67,7 +67,11 @@ constexpr bool kFusedMlp[4] = {true, false, false, false};
 // per window, window_msa_kernel).  Measured at 6x256x704: stage 0 26.5 us
 // fused vs 32.8 us for QKV GEMM + attention (the 39 MB of q, k, v stay on
 // chip); stage 1 25.5 us vs 23.1 us (six waves of ~226 VGPRs per window and
-// 390 windows), so it keeps the separate kernels.
+// 390 windows), so it keeps the separate kernels.  At stage 2 a variant with
+// LayerNorm-1 applied on load (six of a window's twelve heads per workgroup,
+// weight fragments streamed from L2 four k-steps ahead) took 21.9 us vs 19.0
+// us for QKV GEMM + attention: one workgroup per CU at 234 VGPRs, each wave
+// waiting on its weight chunks.
 constexpr bool kFusedWmsa[4] = {true, false, false, false};
 
 struct BlockW {
