@@ -864,36 +864,25 @@ namespace {
 constexpr int kScratchHeads = 32;
 constexpr size_t kScratchElems = (size_t)4 * kScratchHeads * 8 * 64 * 8;
 static_assert(kScratchElems >= attn_term_elems(kScratchHeads, 1), "scratch covers the largest term");
-constexpr int kScratchDevices = 64;
 }  // namespace
 
 static __device__ __align__(256) bf16 scratch[kScratchElems];
 
 namespace {
-std::mutex g_scratch_mutex;
-void *g_scratch_address[kScratchDevices];  // per device; guarded by g_scratch_mutex
-
 // This device's copy of `scratch`: the host-side name of the array is not a
-// device address, so it is resolved once per device (with that device
-// current) and only the resolved pointer is ever passed to a kernel.
+// device address, so it is resolved with the device current, on every call (a
+// host-side lookup that allocates nothing; nothing cached can go stale after a
+// device reset or a reload of the code object), and only the resolved pointer
+// is ever passed to a kernel.
 bf16 *scratch_on(int device, char *error, size_t cap) {
-    if (device < 0 || device >= kScratchDevices) {
-        fail(error, cap, "window attention without allocation supports HIP devices 0..%d (got %d)",
-             kScratchDevices - 1, device);
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+        fail(error, cap, "resolve the window-attention scratch array on HIP device %d: %s", device,
+             e != hipSuccess ? hipGetErrorString(e) : "null address");
         return nullptr;
     }
-    std::lock_guard<std::mutex> lock(g_scratch_mutex);
-    if (!g_scratch_address[device]) {
-        void *p = nullptr;
-        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-        if (e != hipSuccess || !p) {
-            fail(error, cap, "resolve the window-attention scratch array: %s",
-                 e != hipSuccess ? hipGetErrorString(e) : "null address");
-            return nullptr;
-        }
-        g_scratch_address[device] = p;
-    }
-    return static_cast<bf16 *>(g_scratch_address[device]);
+    return static_cast<bf16 *>(p);
 }
 }  // namespace
 
