@@ -426,6 +426,34 @@ struct DmaTile {
     static_assert(kStages >= 2 && kStages <= 8, "2 to 8 stages");
 };
 
+// Tile order of the DMA and wave-specialised kernels.  By default
+// xcd_swizzle keeps consecutive row-major tiles on one XCD, so each XCD sweeps
+// whole row panels and fetches all of B: right when A is the larger operand.
+// A tile type derived as XcdBlocks<T, GM> deals the grid as GM row groups x
+// 8 / GM column groups instead (xcd_block_tile), for layers whose B (the
+// weights) is as large as A or larger; the choice is compile-time, so other
+// layers' kernels carry no decode.
+template <class T, class = void>
+struct TileXcdRowGroups { static constexpr int value = 0; };
+template <class T>
+struct TileXcdRowGroups<T, std::void_t<decltype(T::kXcdRowGroups)>> {
+    static constexpr int value = T::kXcdRowGroups;
+};
+template <class T, int GM>
+struct XcdBlocks : T {
+    static_assert(GM == 1 || GM == 2 || GM == 4 || GM == 8, "row groups must divide the 8 XCDs");
+    static constexpr int kXcdRowGroups = GM;
+};
+
+template <class T>
+__device__ __forceinline__ int tile_pid(int tiles_n) {
+    const int bid = (int)blockIdx.x, count = (int)gridDim.x;
+    if constexpr (TileXcdRowGroups<T>::value == 0)
+        return xcd_swizzle(bid, count);
+    else
+        return xcd_block_tile(bid, count / tiles_n, tiles_n, TileXcdRowGroups<T>::value);
+}
+
 template <int BK>
 __device__ __forceinline__ int dma_swizzle(int r) {
     return BK == 32 ? (r >> 1) & 3 : r & 7;
@@ -537,7 +565,7 @@ template <class T, class ALoad, class BLoad, class Epi>
 __global__ __launch_bounds__(T::kThreads) void gemm_dma_kernel(ALoad al, BLoad bl, Epi epi,
                                                                int M, int N, int K, int tiles_n) {
     __shared__ __attribute__((aligned(1024))) unsigned char smem[dma_smem_bytes<T, Epi>()];
-    gemm_dma_block<T>(al, bl, epi, M, N, K, tiles_n, xcd_swizzle((int)blockIdx.x, (int)gridDim.x), smem);
+    gemm_dma_block<T>(al, bl, epi, M, N, K, tiles_n, tile_pid<T>(tiles_n), smem);
 }
 
 // Tile `pid` of the LDS-DMA core on the workgroup's `smem` (dma_smem_bytes);
@@ -648,7 +676,7 @@ template <class T, class ALoad, class BLoad, class Epi>
 __global__ __launch_bounds__(T::kThreads + ALoad::kWaves * kWave) void gemm_spec_kernel(
     ALoad al, BLoad bl, Epi epi, int M, int N, int K, int tiles_n) {
     __shared__ __attribute__((aligned(1024))) unsigned char smem[dma_smem_bytes<T, Epi>()];
-    gemm_spec_block<T>(al, bl, epi, M, N, K, tiles_n, xcd_swizzle((int)blockIdx.x, (int)gridDim.x), smem);
+    gemm_spec_block<T>(al, bl, epi, M, N, K, tiles_n, tile_pid<T>(tiles_n), smem);
 }
 
 // Tile `pid` of the wave-specialised pipeline on the workgroup's `smem`

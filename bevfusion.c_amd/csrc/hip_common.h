@@ -123,7 +123,7 @@ __device__ __forceinline__ float group_max(float v) {
 
 // Map a linear workgroup id so that consecutive logical tiles stay on one XCD
 // (workgroups are dealt round-robin over the 8 XCDs; each XCD owns an L2).
-__device__ __forceinline__ int xcd_swizzle(int pid, int count) {
+__host__ __device__ __forceinline__ int xcd_swizzle(int pid, int count) {
     constexpr int kXcd = 8;
     if (count < kXcd * 2) return pid;
     const int per = count / kXcd, extra = count % kXcd;
@@ -131,6 +131,51 @@ __device__ __forceinline__ int xcd_swizzle(int pid, int count) {
     // The first `extra` XCDs receive per+1 tiles.
     const int base = xcd < extra ? xcd * (per + 1) : extra * (per + 1) + (xcd - extra) * per;
     return base + local;
+}
+
+// Row-major tile index of workgroup `bid` when a tiles_m x tiles_n grid is
+// dealt to the 8 XCDs as rectangular blocks: XCD x (the one that runs the
+// workgroups with bid % 8 == x) owns the tiles of row group x / (8 / gm) and
+// column group x % (8 / gm), so it fetches 1/gm of A's rows and gm/8 of B's
+// columns instead of, for a grid of whole row panels, all of B.  The blocks
+// hold floor/ceil shares of the rows and columns and an XCD's workgroup count
+// is fixed by the round-robin deal, so a block can hold more tiles than its
+// XCD has workgroups: those tiles go, in XCD order, to the workgroups that
+// XCDs with smaller blocks have left over.  Every bid in [0, tiles_m * tiles_n)
+// maps to a distinct tile (tests/tile_order_check.hip checks this on the
+// host).  Uniform per workgroup (scalar arithmetic).
+__host__ __device__ __forceinline__ int xcd_block_tile(int bid, int tiles_m, int tiles_n, int gm) {
+    constexpr int kXcd = 8;
+    const int gn = kXcd / gm, count = tiles_m * tiles_n;
+    if (count < kXcd * 2 || tiles_m < gm || tiles_n < gn) return xcd_swizzle(bid, count);
+    struct Block { int r0, c0, cols, tiles, slots; };
+    auto block = [&](int x) {
+        const int yr = x / gn, yc = x % gn;
+        const int r0 = yr * tiles_m / gm, r1 = (yr + 1) * tiles_m / gm;
+        const int c0 = yc * tiles_n / gn, c1 = (yc + 1) * tiles_n / gn;
+        return Block{r0, c0, c1 - c0, (r1 - r0) * (c1 - c0), count / kXcd + (x < count % kXcd)};
+    };
+    const int x = bid % kXcd, l = bid / kXcd;
+    Block b = block(x);
+    if (l < b.tiles) return (b.r0 + l / b.cols) * tiles_n + b.c0 + l % b.cols;
+    // A workgroup this XCD has left over: the j-th tile, in XCD order, of the
+    // blocks larger than their XCD's share.
+    int j = l - b.tiles;
+    for (int y = 0; y < x; ++y) {
+        const Block o = block(y);
+        if (o.slots > o.tiles) j += o.slots - o.tiles;
+    }
+    for (int y = 0; y < kXcd; ++y) {
+        b = block(y);
+        const int extra = b.tiles - b.slots;
+        if (extra <= 0) continue;
+        if (j < extra) {
+            const int t = b.slots + j;
+            return (b.r0 + t / b.cols) * tiles_n + b.c0 + t % b.cols;
+        }
+        j -= extra;
+    }
+    return 0;  // not reached: the left-over workgroups and tiles are equal in number
 }
 
 }  // namespace bfhip

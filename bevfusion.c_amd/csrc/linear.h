@@ -26,6 +26,14 @@
 // 11.5 vs 11.9 us with one loader wave), stage-3 fc2 (64 x 64 x 128, three
 // stages: 12.8 vs 14.2 us with one loader wave, 16.3 us plain) and stage-3
 // proj (64 x 64 x 128, three stages: 5.6 vs 6.4 us as 32 x 64 with one).
+//
+// Stage-3 fc1 (M = 1056 tokens at six cameras, W 3072 x 768) deals its tiles
+// to the XCDs as 2 row groups x 4 column groups (XcdBlocks): each XCD's L2
+// then fetches a quarter of W instead of all of it (plain fp16 stores: 11.7
+// -> 10.3 us).  The same order measured no faster, or slower by up to 1 us,
+// for the other stage-3 linears and the stage-2 -> 3 merge: their repeated
+// weight reads are served by the memory-side cache, and the per-CU fetch
+// rate, not the HBM, bounds them.
 #pragma once
 
 #include <cstdint>
@@ -50,14 +58,14 @@ inline void linear_spec(const bf16 *x, const bf16 *w, int M, int N, int K, const
     launch_gemm_spec<T>(al, bl, epi, M, N, K, s);
 }
 
-enum LinearTile { kK32, kK64, kK128, kTall, kWide, kWide32, kSpecBig, kSpec64, kSpec128 };
+enum LinearTile { kK32, kK64, kK128, kTall, kWide, kWideXcd2, kWide32, kSpecBig, kSpec64, kSpec128 };
 
 inline LinearTile pick_linear_tile(int N, int K) {
     struct Entry { int n, k; LinearTile t; };
     static const Entry table[] = {
         {768, 3072, kSpec128}, {384, 1536, kSpec64}, {768, 768, kSpec128}, {768, 1536, kK128},
         {576, 192, kTall}, {192, 768, kTall},  {192, 384, kTall},
-        {768, 192, kWide32}, {1152, 384, kWide}, {3072, 768, kWide},
+        {768, 192, kWide32}, {1152, 384, kWide}, {3072, 768, kWideXcd2},
         {1536, 384, kSpecBig},
     };
     for (const Entry &e : table)
@@ -82,6 +90,9 @@ inline void linear_f16(const bf16 *x, const bf16 *w, int M, int N, int K, const 
         case kK128: linear_tile<DmaTile<64, 64, 128, 2, 2, 3, true>>(x, w, M, N, K, epi, s); break;
         case kTall: linear_tile<DmaTile<128, 64, 64, 2, 2, 2, true>>(x, w, M, N, K, epi, s); break;
         case kWide: linear_tile<DmaTile<64, 128, 64, 2, 2, 2, true>>(x, w, M, N, K, epi, s); break;
+        case kWideXcd2:
+            linear_tile<XcdBlocks<DmaTile<64, 128, 64, 2, 2, 2, true>, 2>>(x, w, M, N, K, epi, s);
+            break;
         case kWide32: linear_tile<DmaTile<64, 128, 32, 2, 2, 3, true>>(x, w, M, N, K, epi, s); break;
         case kSpecBig: linear_spec<DmaTile<128, 128, 64, 2, 4, 2, true>, 4>(x, w, M, N, K, epi, s); break;
         case kSpec64: linear_spec<DmaTile<64, 64, 64, 2, 2, 4, true>, 4>(x, w, M, N, K, epi, s); break;
