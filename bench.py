@@ -139,8 +139,12 @@ NECK_LAYERS = {
 IO_LAYERS = (4, 8, 11)  # timed on caller buffers (bfhip_camera_profile_layer_io)
 # The lateral 1x1 convs over concat(lower, bilinear-up(upper)) run as two
 # GEMMs (W_lower . lower, and W_upper . upper at the upper resolution, added
-# upsampled in the first one's epilogue): layer -> (M, Cl, M_upper, Cu).
+# upsampled in the first one's epilogue): layer -> (M, Cl, M_upper, Cu).  The
+# forward runs the lower GEMM in one launch with a depth-encoder conv, so the
+# op table times three launches: the upper products (hooks 0 and 2), and
+# dtransform.3 / .6 each with its lateral's lower half (hooks 4 and 5).
 LATERALS = {0: (6 * 16 * 44, 384, 6 * 8 * 22, 768), 2: (6 * 32 * 88, 192, 6 * 16 * 44, 256)}
+PAIRED_LATERAL = {4: 0, 5: 2}  # depth-encoder layer -> the lateral whose lower half it shares a launch with
 
 
 def swin_op_cost(stage, op, b=6):
@@ -202,13 +206,27 @@ def pack_cost(b=6):
     return 0.0, el * (4 + 2)
 
 
+def lateral_cost(layer, part):
+    """The upper-level product ("upper": reads upper and W_upper, writes the
+    fp32 product) or the lower half ("lower": reads lower, W_lower and the
+    fp32 product, writes the output) of lateral `layer`."""
+    m, cl, mu, cu = LATERALS[layer]
+    if part == "upper":
+        return 2.0 * 256 * mu * cu, mu * cu * 2 + 256 * cu * 2 + mu * 256 * 4
+    return 2.0 * 256 * m * cl, m * cl * 2 + 256 * cl * 2 + mu * 256 * 4 + m * 256 * 2
+
+
 def neck_layer_cost(layer):
-    if layer in LATERALS:  # executed work of the two GEMMs (fp32 upper product written and read)
-        m, cl, mu, cu = LATERALS[layer]
-        return (2.0 * 256 * (m * cl + mu * cu),
-                m * cl * 2 + mu * cu * 2 + 256 * (cl + cu) * 2 + 2 * mu * 256 * 4 + m * 256 * 2)
+    """Algorithmic FLOPs and HBM bytes of the launch(es) the op-table entry of
+    neck `layer` runs (see PAIRED_LATERAL)."""
+    if layer in LATERALS:
+        return lateral_cost(layer, "upper")
     name, m, ci, co, k, in_bytes, out_el = NECK_LAYERS[layer]
-    return 2.0 * m * co * ci * k * k, in_bytes + co * ci * k * k * 2 + m * co * out_el
+    flops, nbytes = 2.0 * m * co * ci * k * k, in_bytes + co * ci * k * k * 2 + m * co * out_el
+    if layer in PAIRED_LATERAL:
+        lf, lb = lateral_cost(PAIRED_LATERAL[layer], "lower")
+        flops, nbytes = flops + lf, nbytes + lb
+    return flops, nbytes
 
 
 def neck_io(dev):
@@ -301,6 +319,10 @@ def op_table(swin, neck, stream, io):
             fn = lambda: neck.profile_layer_io(11, out0=io["down"], stream=stream)
         else:
             fn = lambda layer=layer: neck.profile_layer(layer, stream)
+        if layer in LATERALS:
+            name += "_upper"
+        elif layer in PAIRED_LATERAL:
+            name += "+" + NECK_LAYERS[PAIRED_LATERAL[layer]][0] + "_lower"
         table[f"neck.{name}"] = (fn, 1, neck_layer_cost(layer))
     return table
 

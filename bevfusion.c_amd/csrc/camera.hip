@@ -114,14 +114,27 @@ template <class Epi>
 void conv_fpn1(const ConvLayer &l, const bf16 *in, const Epi &epi, hipStream_t s) {
     run_conv_spec<S64, 3, kS64Loaders>(l, in, 256, nullptr, 0, epi, s);
 }
+// dtransform.3 and .6 as jobs: the forward runs each in one launch with a
+// lateral's lower half (neck_impl), the other entry points and the probes
+// alone, with the same tile, loaders and epilogue.  dtransform.6 takes two
+// loader waves so that its workgroup matches the lateral's four waves.
+constexpr int kS32Loaders = 2;
+template <class Epi>
+auto dt1_job(const ConvLayer &l, const float *depth, const float *aw, const float *ab, const Epi &epi) {
+    return conv_job<T32, 5, 5>(l, SrcNHWCDepthAffine<true>{depth, aw, ab, l.ih, l.iw}, epi);
+}
+template <class Epi>
+auto dt2_job(const ConvLayer &l, const bf16 *in, const Epi &epi) {
+    return conv_job_spec<S32, 5, kS32Loaders>(l, in, 32, nullptr, 0, epi);
+}
 template <class Epi>
 void conv_dt1(const ConvLayer &l, const float *depth, const float *aw, const float *ab,
               const Epi &epi, hipStream_t s) {
-    run_conv<T32, 5, 5>(l, SrcNHWCDepthAffine<true>{depth, aw, ab, l.ih, l.iw}, epi, s);
+    launch_gemm_job(dt1_job(l, depth, aw, ab, epi), s);
 }
 template <class Epi>
 void conv_dt2(const ConvLayer &l, const bf16 *in, const Epi &epi, hipStream_t s) {
-    run_conv_spec<S32, 5>(l, in, 32, nullptr, 0, epi, s);
+    launch_gemm_job(dt2_job(l, in, epi), s);
 }
 template <class Epi>
 void conv_dn6(const ConvLayer &l, const bf16 *in, const Epi &epi, hipStream_t s) {
@@ -172,16 +185,18 @@ using SLatUpDeep = DmaTile<32, 32, 64, 1, 1, 4, true>;  // upper products with C
 using DLat = DmaTile<64, 64, 64, 2, 2, 2, true>;       // lower halves
 // The lower half: out = relu(W[:, :Cl] . lower + bias + bilinear(up)), with
 // the upsampling in the epilogue (EpiUpAddNHWC); w rows hold ldw columns.
-void lateral_lower(const bf16 *lower, int Cl, const bf16 *w, int ldw, const float *bias,
-                   const float *up, bf16 *out, int M, int H, int W, int h, int wd, hipStream_t s) {
+auto lateral_lower_job(const bf16 *lower, int Cl, const bf16 *w, int ldw, const float *bias,
+                       const float *up, bf16 *out, int M, int H, int W, int h, int wd) {
     using T = DLat;
     DmaRowsBf16<T::BM, T::BK, T::kThreads> al{lower, Cl, M, Cl};
     DmaRowsBf16<T::BN, T::BK, T::kThreads> bl{w, ldw, 256, Cl};
-    launch_gemm_dma<T>(al, bl, EpiUpAddNHWC{out, bias, up, M, 256, H, W, h, wd, 1}, M, 256, Cl, s);
+    return gemm_job<GemmCore::kDma, T>(al, bl, EpiUpAddNHWC{out, bias, up, M, 256, H, W, h, wd, 1},
+                                       M, 256, Cl);
 }
-void lateral(const ConvLayer &l, const bf16 *lower, int Cl, int H, int W, const bf16 *upper, int Cu,
-             int h, int w, float *up, bf16 *out, hipStream_t s) {
-    const int B = l.n, Mu = B * h * w, M = B * H * W, ci = Cl + Cu;
+// The upper product W[:, Cl:] . upper into `up` (fp32).
+void lateral_upper(const ConvLayer &l, int Cl, const bf16 *upper, int Cu, int h, int w, float *up,
+                   hipStream_t s) {
+    const int Mu = l.n * h * w, ci = Cl + Cu;
     if (Cu >= 512) {
         using T = SLatUpDeep;
         DmaRowsBf16<T::BM, T::BK, kWave> al{upper, Cu, Mu, Cu};
@@ -193,7 +208,11 @@ void lateral(const ConvLayer &l, const bf16 *lower, int Cl, int H, int W, const 
         DmaRowsBf16<T::BN, T::BK, T::kThreads> bl{l.w + Cl, ci, 256, Cu};
         launch_gemm_dma<T>(al, bl, EpiRowsF32{up, nullptr, 256, Mu, 256, 0}, Mu, 256, Cu, s);
     }
-    lateral_lower(lower, Cl, l.w, ci, l.b, up, out, M, H, W, h, w, s);
+}
+void lateral(const ConvLayer &l, const bf16 *lower, int Cl, int H, int W, const bf16 *upper, int Cu,
+             int h, int w, float *up, bf16 *out, hipStream_t s) {
+    lateral_upper(l, Cl, upper, Cu, h, w, up, s);
+    launch_gemm_job(lateral_lower_job(lower, Cl, l.w, Cl + Cu, l.b, up, out, l.n * H * W, H, W, h, w), s);
 }
 
 void lateral1(bf_cuda_camera_neck *n, hipStream_t s) {
@@ -260,6 +279,41 @@ void downsample_layer(bf_cuda_camera_neck *n, int layer, float *output, hipStrea
 void depth_impl(bf_cuda_camera_neck *n, const float *depth, float *logits, float *context,
                 hipStream_t s) {
     for (int layer : {kDt1, kDt2, kDn0, kDn3, kDn6}) depth_layer(n, layer, depth, logits, context, s);
+}
+
+// The depth encoder's two convs (dtransform.3 / .6) read only the dense depth,
+// so the forward runs each in one launch with one of the FPN's lateral lower
+// halves (gemm_pair_kernel): both grids are a few hundred latency-bound tiles
+// (132 + 264, and 528 + 1056), and paired they fill the CUs the other leaves
+// idle (frame -14 us measured on MI355X).
+void dt1_lateral1(bf_cuda_camera_neck *n, const float *depth, hipStream_t s) {
+    const ConvLayer &d = n->L[kDt1], &l = n->L[kLat1];
+    const int h1 = (int)n->h1, w1 = (int)n->w1, h2 = (int)n->h2, w2 = (int)n->w2;
+    launch_gemm_pair(dt1_job(d, depth, n->dt0_w, n->dt0_b, nhwc_to(d, n->e1, true)),
+                     lateral_lower_job(n->p1, 384, l.w, 384 + 768, l.b, n->u1, n->t1, l.n * h1 * w1,
+                                       h1, w1, h2, w2),
+                     s);
+}
+void dt2_lateral0(bf_cuda_camera_neck *n, hipStream_t s) {
+    const ConvLayer &d = n->L[kDt2], &l = n->L[kLat0];
+    const int h = (int)n->h, w = (int)n->w, h1 = (int)n->h1, w1 = (int)n->w1;
+    launch_gemm_pair(dt2_job(d, n->e1, nhwc_to(d, n->e2, true)),
+                     lateral_lower_job(n->p0, 192, l.w, 192 + 256, l.b, n->u0, n->t0, l.n * h * w, h,
+                                       w, h1, w1),
+                     s);
+}
+
+// The whole neck: FPN and depth head with the two pairs above.
+void neck_impl(bf_cuda_camera_neck *n, const float *s0, const float *s1, const float *s2,
+               const float *depth, float *logits, float *context, hipStream_t s) {
+    pack_levels(n, s0, s1, s2, s);
+    lateral_upper(n->L[kLat1], 384, n->p2, 768, (int)n->h2, (int)n->w2, n->u1, s);
+    dt1_lateral1(n, depth, s);
+    fpn_conv(kFpn1, n->L[kFpn1], n->t1, n->f1, nullptr, s);
+    lateral_upper(n->L[kLat0], 192, n->f1, 256, (int)n->h1, (int)n->w1, n->u0, s);
+    dt2_lateral0(n, s);
+    fpn_conv(kFpn0, n->L[kFpn0], n->t0, n->f0, nullptr, s);
+    for (int layer : {kDn0, kDn3, kDn6}) depth_layer(n, layer, depth, logits, context, s);
 }
 
 int build(bf_cuda_camera_neck *n, const bf_model *model, char *error, size_t cap) {
@@ -422,8 +476,7 @@ extern "C" int bf_cuda_camera_neck_forward(bf_cuda_camera_neck *n, const float *
     if (!n || !s0 || !s1 || !s2 || !depth || !logits || !context)
         return fail(error, cap, "invalid HIP camera-neck buffers");
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    fpn_impl(n, s0, s1, s2, nullptr, nullptr, s);
-    depth_impl(n, depth, logits, context, s);
+    neck_impl(n, s0, s1, s2, depth, logits, context, s);
     return launch_ok(error, cap, "HIP camera-neck launch");
 }
 
@@ -449,11 +502,12 @@ extern "C" int bfhip_camera_profile_layer(bf_cuda_camera_neck *n, int layer, voi
     const ConvLayer &l = n->L[layer];
     // Same kernels and shapes as the forward entry points, on context buffers.
     switch (layer) {
-        case kLat1: lateral1(n, s); break;
+        case kLat1: lateral_upper(l, 384, n->p2, 768, h2, w2, n->u1, s); break;
         case kFpn1: fpn_conv(layer, l, n->t1, n->f1, nullptr, s); break;
-        case kLat0: lateral0(n, s); break;
+        case kLat0: lateral_upper(l, 192, n->f1, 256, h1, w1, n->u0, s); break;
         case kFpn0: fpn_conv(layer, l, n->t0, n->f0, nullptr, s); break;
-        case kDt2: case kDn0: case kDn3: depth_layer(n, layer, nullptr, nullptr, nullptr, s); break;
+        case kDt2: dt2_lateral0(n, s); break;
+        case kDn0: case kDn3: depth_layer(n, layer, nullptr, nullptr, nullptr, s); break;
         case kDs0: case kDs1: downsample_layer(n, layer, nullptr, s); break;
         case kDs2:
             run_conv_dma<DDs1, 3>(l, n->b1, kDsPad, nullptr, 0, nhwc_to(l, n->b0, true, kDsPad), s);
@@ -472,6 +526,8 @@ extern "C" int bfhip_camera_profile_layer_io(bf_cuda_camera_neck *n, int layer, 
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     if (layer == kDs2)
         downsample_layer(n, layer, out0, s);
+    else if (layer == kDt1)
+        dt1_lateral1(n, input, s);
     else
         depth_layer(n, layer, input, out0, out1, s);
     return launch_ok(error, cap, "launch HIP camera layer profiling");
@@ -565,8 +621,10 @@ extern "C" int bfhip_debug_fpn_upsample(bf_cuda_camera_neck *n, int level, const
     const void *db = buf.upload(bias.data(), bias.size() * 4, error, cap);
     if (!dl || !dw || !db) return 0;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    lateral_lower(static_cast<const bf16 *>(dl), Cl, static_cast<const bf16 *>(dw), Cl,
-                  static_cast<const float *>(db), up, static_cast<bf16 *>(out), M, H, W, h, w, s);
+    launch_gemm_job(lateral_lower_job(static_cast<const bf16 *>(dl), Cl, static_cast<const bf16 *>(dw),
+                                      Cl, static_cast<const float *>(db), up, static_cast<bf16 *>(out),
+                                      M, H, W, h, w),
+                    s);
     return launch_ok(error, cap, "launch FPN upsample probe") &&
            hip_ok(hipStreamSynchronize(s), error, cap, "FPN upsample probe");
 }

@@ -102,6 +102,25 @@ void run_conv_spec(const ConvLayer &l, const bf16 *a, int c0, const bf16 *b, int
     launch_gemm_spec<T>(al, bl, epi, g.M, l.co, g.K, s);
 }
 
+// The same convs as jobs of gemm_pair_kernel (gemm_core.h), for a launch
+// shared with an independent layer.
+template <class T, int KH, int KW, class Src, class Epi>
+auto conv_job(const ConvLayer &l, const Src &src, const Epi &epi) {
+    const ConvGeom g = geom_of(l);
+    LoadConvNHWC<T::BM, T::BK, T::kThreads, KH, KW, Src> al{};
+    al.src = src;
+    al.g = g;
+    LoadRowsBf16<T::BN, T::BK, T::kThreads> bl{l.w, g.K, l.co, g.K};
+    return gemm_job<GemmCore::kReg, T>(al, bl, epi, g.M, l.co, g.K);
+}
+template <class T, int K, int LW, class Epi>
+auto conv_job_spec(const ConvLayer &l, const bf16 *a, int c0, const bf16 *b, int c1, const Epi &epi) {
+    const ConvGeom g = geom_of(l);
+    DmaConvNHWC<T::BM, T::BK, LW * kWave, K, K, false> al{a, b, c0, c1, g};
+    DmaRowsBf16<T::BN, T::BK, LW * kWave> bl{l.w, g.K, l.co, g.K};
+    return gemm_job<GemmCore::kSpec, T>(al, bl, epi, g.M, l.co, g.K);
+}
+
 inline EpiConvOut out_to(const ConvLayer &l, bf16 *nhwc, float *nchw = nullptr, int relu = 1,
                          bool f16 = false) {
     return EpiConvOut{nhwc, nchw, l.b, l.n * l.oh * l.ow, l.co, l.oh * l.ow, relu, (int)f16};

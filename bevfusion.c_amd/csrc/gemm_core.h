@@ -322,19 +322,34 @@ constexpr size_t epilogue_bytes() {
 }
 
 // ------------------------------------------------------------------ main loop
+// One LDS arena: double-buffered A/B tiles in the main loop, then (for
+// row-vector epilogues) the fp32 output tile.
+template <class T, class Epi>
+constexpr size_t reg_smem_bytes() {
+    constexpr size_t kABBytes = (size_t)2 * (T::BM + T::BN) * T::kStride * sizeof(bf16);
+    constexpr size_t kCBytes = epilogue_bytes<T, Epi>();
+    return kABBytes > kCBytes ? kABBytes : kCBytes;
+}
+template <class T, class ALoad, class BLoad, class Epi>
+__device__ __forceinline__ void gemm_reg_block(ALoad &al, BLoad &bl, const Epi &epi, int M, int N,
+                                               int K, int tiles_n, int pid, unsigned char *smem);
+
 template <class T, class ALoad, class BLoad, class Epi>
 __global__ __launch_bounds__(T::kThreads) void gemm_kernel(ALoad al, BLoad bl, Epi epi,
                                                            int M, int N, int K, int tiles_n) {
-    // One LDS arena: double-buffered A/B tiles in the main loop, then (for
-    // row-vector epilogues) the fp32 output tile.
-    constexpr size_t kABBytes = (size_t)2 * (T::BM + T::BN) * T::kStride * sizeof(bf16);
-    constexpr size_t kCBytes = epilogue_bytes<T, Epi>();
-    __shared__ __attribute__((aligned(16))) unsigned char smem[kABBytes > kCBytes ? kABBytes : kCBytes];
+    __shared__ __attribute__((aligned(16))) unsigned char smem[reg_smem_bytes<T, Epi>()];
+    gemm_reg_block<T>(al, bl, epi, M, N, K, tiles_n, xcd_swizzle((int)blockIdx.x, (int)gridDim.x), smem);
+}
+
+// Tile `pid` of the register-fed core on the workgroup's `smem`
+// (reg_smem_bytes); gemm_kernel is one such tile per workgroup.
+template <class T, class ALoad, class BLoad, class Epi>
+__device__ __forceinline__ void gemm_reg_block(ALoad &al, BLoad &bl, const Epi &epi, int M, int N,
+                                               int K, int tiles_n, int pid, unsigned char *smem) {
     bf16(*sA)[T::BM * T::kStride] = reinterpret_cast<bf16(*)[T::BM * T::kStride]>(smem);
     bf16(*sB)[T::BN * T::kStride] =
         reinterpret_cast<bf16(*)[T::BN * T::kStride]>(smem + (size_t)2 * T::BM * T::kStride * sizeof(bf16));
 
-    const int pid = xcd_swizzle((int)blockIdx.x, (int)gridDim.x);
     const int m0 = (pid / tiles_n) * T::BM, n0 = (pid % tiles_n) * T::BN;
     const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / T::WN, wn = wave % T::WN;
@@ -768,6 +783,88 @@ inline void launch_gemm_spec(const ALoad &al, const BLoad &bl, const Epi &epi, i
     hipLaunchKernelGGL((gemm_spec_kernel<T, ALoad, BLoad, Epi>), dim3(tiles_m * tiles_n),
                        dim3(T::kThreads + ALoad::kWaves * kWave), 0, stream, al, bl, epi, M, N,
                        K, tiles_n);
+}
+
+// ============================================ two independent GEMMs, one launch
+// A GEMM (or implicit-GEMM conv) as a job of gemm_pair_kernel: the tile
+// instance, its loaders and epilogue, on one of the three cores.
+enum class GemmCore { kReg, kDma, kSpec };
+template <GemmCore C, class T, class Epi>
+constexpr size_t job_smem_bytes() {
+    if constexpr (C == GemmCore::kReg) return reg_smem_bytes<T, Epi>();
+    else return dma_smem_bytes<T, Epi>();
+}
+template <GemmCore C, class T, class ALoad>
+constexpr int job_threads() {
+    if constexpr (C == GemmCore::kSpec) return T::kThreads + ALoad::kWaves * kWave;
+    else return T::kThreads;
+}
+template <GemmCore C, class T, class ALoad, class BLoad, class Epi>
+struct GemmJob {
+    static_assert(TileXcdRowGroups<T>::value == 0, "jobs use the default tile order");
+    static constexpr size_t kSmem = job_smem_bytes<C, T, Epi>();
+    static constexpr int kThreads = job_threads<C, T, ALoad>();
+    ALoad al;
+    BLoad bl;
+    Epi epi;
+    int M, N, K, tiles_n, tiles;
+    // Tile `local` of this job (0 <= local < tiles), XCD-swizzled within it.
+    __device__ void run(int local, unsigned char *smem) {
+        const int pid = xcd_swizzle(local, tiles);
+        if constexpr (C == GemmCore::kReg)
+            gemm_reg_block<T>(al, bl, epi, M, N, K, tiles_n, pid, smem);
+        else if constexpr (C == GemmCore::kDma)
+            gemm_dma_block<T>(al, bl, epi, M, N, K, tiles_n, pid, smem);
+        else
+            gemm_spec_block<T>(al, bl, epi, M, N, K, tiles_n, pid, smem);
+    }
+};
+template <GemmCore C, class T, class ALoad, class BLoad, class Epi>
+GemmJob<C, T, ALoad, BLoad, Epi> gemm_job(const ALoad &al, const BLoad &bl, const Epi &epi, int M,
+                                          int N, int K) {
+    if constexpr (C == GemmCore::kSpec)
+        static_assert(ALoad::kWaves == BLoad::kWaves, "both loaders span the same loader waves");
+    const int tiles_n = (N + T::BN - 1) / T::BN;
+    return GemmJob<C, T, ALoad, BLoad, Epi>{al, bl, epi, M, N, K, tiles_n,
+                                            (M + T::BM - 1) / T::BM * tiles_n};
+}
+
+// Two GEMMs with no data dependence between them in one launch: workgroups
+// [0, slots_a) run job A's tiles (slots_a is A's tile count rounded up to the
+// 8 XCDs, so that B's tiles keep their XCD swizzle), the rest job B's.  Layers
+// whose grids each leave most CUs idle for most of their time (a few hundred
+// latency-bound tiles) then share the machine instead of running one after the
+// other, and one launch boundary goes.  Both jobs run the same workgroup size;
+// the branch is uniform per workgroup, and each job's barriers are its own.
+template <class JA, class JB>
+__global__ __launch_bounds__(JA::kThreads) void gemm_pair_kernel(JA a, JB b, int slots_a) {
+    static_assert(JA::kThreads == JB::kThreads, "paired jobs run the same workgroup size");
+    constexpr size_t kSmem = JA::kSmem > JB::kSmem ? JA::kSmem : JB::kSmem;
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[kSmem];
+    const int bid = (int)blockIdx.x;
+    if (bid < slots_a) {
+        if (bid < a.tiles) a.run(bid, smem);
+        return;
+    }
+    b.run(bid - slots_a, smem);
+}
+
+// One job alone, on its core's own kernel.
+template <GemmCore C, class T, class ALoad, class BLoad, class Epi>
+inline void launch_gemm_job(const GemmJob<C, T, ALoad, BLoad, Epi> &j, hipStream_t stream) {
+    if constexpr (C == GemmCore::kReg)
+        launch_gemm<T>(j.al, j.bl, j.epi, j.M, j.N, j.K, stream);
+    else if constexpr (C == GemmCore::kDma)
+        launch_gemm_dma<T>(j.al, j.bl, j.epi, j.M, j.N, j.K, stream);
+    else
+        launch_gemm_spec<T>(j.al, j.bl, j.epi, j.M, j.N, j.K, stream);
+}
+
+template <class JA, class JB>
+inline void launch_gemm_pair(const JA &a, const JB &b, hipStream_t stream) {
+    const int slots_a = (a.tiles + 7) / 8 * 8;
+    hipLaunchKernelGGL((gemm_pair_kernel<JA, JB>), dim3(slots_a + b.tiles), dim3(JA::kThreads), 0,
+                       stream, a, b, slots_a);
 }
 
 // ---------------------------------------------------------------- epilogues

@@ -70,10 +70,15 @@ int bfhip_swin_profile_io(bf_cuda_swin *swin, int stage, int op, const float *im
 
 /* Camera-neck convolution `layer` in the context's layer table: 0 lateral 1,
  * 1 fpn 1, 2 lateral 0, 3 fpn 0, 5 dtransform.6, 6 depthnet.0, 7 depthnet.3,
- * 9-11 downsample.  Layers 4 (dtransform.3, reads the caller's dense depth)
- * and 8 (depthnet.6, writes the caller's logits/context) are refused here;
- * bfhip_camera_profile_layer_io runs them on caller buffers.  Layer 11 here
- * stores channels-last into context scratch instead of the transposed
+ * 9-11 downsample.  The forward runs each lateral as two launches: the
+ * upper-level product, and the lower half (which adds the upsampled product)
+ * in one launch with a depth-encoder conv.  So layers 0 and 2 here run the
+ * upper-level product alone, and layer 5 runs dtransform.6 together with
+ * lateral 0's lower half (the forward's launch).  Layers 4 (dtransform.3,
+ * reads the caller's dense depth; shares its launch with lateral 1's lower
+ * half) and 8 (depthnet.6, writes the caller's logits/context) are refused
+ * here; bfhip_camera_profile_layer_io runs them on caller buffers.  Layer 11
+ * here stores channels-last into context scratch instead of the transposed
  * caller output (bfhip_camera_profile_layer_io runs the forward's kernel). */
 int bfhip_camera_profile_layer(bf_cuda_camera_neck *neck, int layer, void *stream,
                                char *error, size_t error_cap);
@@ -81,7 +86,7 @@ int bfhip_camera_profile_layer(bf_cuda_camera_neck *neck, int layer, void *strea
 /* The layers whose forward launch reads or writes caller buffers, on caller
  * device buffers, at the forward's shape and kernel instance:
  *   4   dtransform.0 fused into dtransform.3: reads `input`, the dense depth
- *       [B,1,8h,8w];
+ *       [B,1,8h,8w]; runs in one launch with lateral 1's lower half;
  *   8   depthnet.6: writes `out0` (logits [B,118,h,w]) and `out1` (context
  *       [B,80,h,w]);
  *   11  the last downsample conv: writes `out0`, the x/y-transposed
