@@ -866,7 +866,9 @@ constexpr size_t kScratchElems = (size_t)4 * kScratchHeads * 8 * 64 * 8;
 static_assert(kScratchElems >= attn_term_elems(kScratchHeads, 1), "scratch covers the largest term");
 }  // namespace
 
-static __device__ __align__(256) bf16 scratch[kScratchElems];
+// The score terms are fp16 words; the attention kernel takes them through the
+// library's 16-bit word pointer type (bf16 *), which carries either format.
+static __device__ __align__(256) uint16_t scratch[kScratchElems];
 
 namespace {
 // This device's copy of `scratch`: the host-side name of the array is not a
@@ -882,7 +884,7 @@ bf16 *scratch_on(int device, char *error, size_t cap) {
              e != hipSuccess ? hipGetErrorString(e) : "null address");
         return nullptr;
     }
-    return static_cast<bf16 *>(p);
+    return static_cast<bf16 *>(p);  // fp16 words (see `scratch`)
 }
 }  // namespace
 
