@@ -32,9 +32,8 @@
  *       to the current device.  Every call on a device shares that device's
  *       array, so calls that overlap in time on one device (other streams or
  *       host threads) race; calls queued on one stream do not.  The array's
- *       device address is resolved on the first call on each device and kept:
- *       like every other object of the library, it does not survive
- *       hipDeviceReset.
+ *       device address is looked up on every call (a host-side lookup that
+ *       allocates nothing), with the stream's device current.
  *
  *   bfhip_debug_camera_gather
  *       Runs the A-operand gather of camera-neck conv `layer` (the layer
